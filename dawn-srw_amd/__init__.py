@@ -1,0 +1,22 @@
+"""dawn-srw_amd: MI355X-native Select-Read-Write (SRW) unit-pool layer.
+
+The hot path of madst0614/DAWN-SRW (the fused gate + SRW function of
+models/dawn_spatial_v41_exp.py:352-909 and its inference twin :1713-1738)
+rebuilt as hand-written gfx950 HIP kernels behind a C ABI
+(include/srw_amd.h, lib/libsrw_amd.so).  This package is the Python host
+side: a ctypes binding, a tensor-level wrapper and a drop-in mirror of the
+reference factories.
+
+The directory name is not a Python identifier; load the package with
+``__graft_entry__.load_package()``, which registers it as ``dawn_srw_amd``.
+"""
+
+from ._capi import SrwError, SrwLibraryError, load_library  # noqa: F401
+from .layer import GateConfig, srw_forward  # noqa: F401
+from .srw import (chunk_plan, make_sharded_srw, make_sharded_srw_paired,  # noqa: F401
+                  srw_inference)
+from . import inputs  # noqa: F401
+
+__all__ = ["SrwError", "SrwLibraryError", "load_library", "GateConfig",
+           "srw_forward", "chunk_plan", "make_sharded_srw",
+           "make_sharded_srw_paired", "srw_inference", "inputs"]

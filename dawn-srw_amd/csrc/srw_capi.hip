@@ -1,0 +1,142 @@
+// srw_capi.hip -- the extern "C" boundary of libsrw_amd.so.
+//
+// Validates a call, sizes the workspace, picks a kernel family and enqueues
+// it on the caller's stream.  No allocation, no global state beyond the
+// per-thread name of the last path taken.
+
+#include <math.h>
+#include <string.h>
+
+#include "srw_internal.hpp"
+
+namespace {
+
+thread_local const char* g_last_path = "none";
+
+srw_status_t validate(const srw_desc_t* d) {
+  if (!d) return SRW_EINVAL;
+  if (d->T < 0 || d->d_model < 1 || d->d_route < 1 || d->n_units < 1) return SRW_EINVAL;
+  if (d->n_routes != 1 && d->n_routes != 2) return SRW_EINVAL;
+  if (d->dtype != SRW_F32 && d->dtype != SRW_BF16) return SRW_EINVAL;
+  if (d->gate != SRW_GATE_V41 && d->gate != SRW_GATE_GELU_V401) return SRW_EINVAL;
+  if (d->stats_mode != SRW_STATS_ONEPASS && d->stats_mode != SRW_STATS_CENTERED &&
+      d->stats_mode != SRW_STATS_GRAM)
+    return SRW_EINVAL;
+  if (d->chunk_size < 0) return SRW_EINVAL;
+  if (!isfinite(d->sharpness) || !isfinite(d->act_threshold) || !isfinite(d->act_cutoff) ||
+      !isfinite(d->epsilon) || !isfinite(d->max_intensity) || !isfinite(d->scale))
+    return SRW_EINVAL;
+  if (d->flags & ~(SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_SPARSE_SKIP | SRW_FLAG_NO_FAST)) return SRW_EINVAL;
+  return SRW_OK;
+}
+
+// Which family serves this descriptor: 1 = MFMA, 0 = generic, -1 = none.
+int choose(const srw_desc_t& d) {
+  const bool force_generic = (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST)) != 0;
+  if (!force_generic && srw::mfma_supports(d)) return 1;
+  if (d.stats_mode == SRW_STATS_GRAM) return -1;  // only the MFMA family implements it
+  if (d.flags & SRW_FLAG_SPARSE_SKIP) return -1;
+  if (srw::generic_supports(d)) return 0;
+  return -1;
+}
+
+size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+}  // namespace
+
+extern "C" {
+
+int32_t srw_abi_version(void) { return SRW_AMD_ABI_VERSION; }
+
+const char* srw_status_string(srw_status_t s) {
+  switch (s) {
+    case SRW_OK: return "SRW_OK";
+    case SRW_EINVAL: return "SRW_EINVAL: invalid argument";
+    case SRW_EUNSUPPORTED: return "SRW_EUNSUPPORTED: configuration not implemented";
+    case SRW_EHIP: return "SRW_EHIP: HIP runtime error";
+    case SRW_EWORKSPACE: return "SRW_EWORKSPACE: workspace missing or too small";
+  }
+  return "SRW_?: unknown status";
+}
+
+srw_status_t srw_desc_init(srw_desc_t* d) {
+  if (!d) return SRW_EINVAL;
+  memset(d, 0, sizeof(*d));
+  d->n_routes = 1;
+  d->dtype = SRW_BF16;
+  d->gate = SRW_GATE_V41;
+  d->stats_mode = SRW_STATS_ONEPASS;
+  d->sharpness = 500.0f;       // v41:297
+  d->act_threshold = 0.5f;     // v41:298
+  d->act_cutoff = 0.01f;       // v41:299
+  d->epsilon = 1e-4f;          // v41:300
+  d->max_intensity = 10.0f;    // v41:301
+  d->dead_threshold = 0.01f;   // v41:352
+  d->scale = 1.0f;
+  d->chunk_size = 0;
+  d->flags = 0;
+  return SRW_OK;
+}
+
+srw_status_t srw_workspace_size(const srw_desc_t* d, size_t* bytes) {
+  srw_status_t st = validate(d);
+  if (st != SRW_OK) return st;
+  if (!bytes) return SRW_EINVAL;
+  const int which = choose(*d);
+  if (which < 0) return SRW_EUNSUPPORTED;
+  *bytes = align256(which == 1 ? srw::mfma_workspace_bytes(*d) : srw::generic_workspace_bytes(*d));
+  return SRW_OK;
+}
+
+srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw_outputs_t* o, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  srw_status_t st = validate(d);
+  if (st != SRW_OK) return st;
+  if (!in || !o) return SRW_EINVAL;
+  const int which = choose(*d);
+  if (which < 0) return SRW_EUNSUPPORTED;
+  if (d->T == 0) {  // nothing to compute; empty tensors may carry null pointers
+    g_last_path = "empty";
+    return SRW_OK;
+  }
+  if (!in->x || !in->h || !in->emb || !in->tau_offset || !in->read || !in->write || !o->out) return SRW_EINVAL;
+  if (in->h == in->x && !(d->n_routes == 1 && d->d_route == d->d_model)) return SRW_EINVAL;
+  const size_t need = align256(which == 1 ? srw::mfma_workspace_bytes(*d) : srw::generic_workspace_bytes(*d));
+  if (need > 0 && (!workspace || workspace_bytes < need)) return SRW_EWORKSPACE;
+
+  srw::LaunchArgs a{};
+  a.d = *d;
+  a.in = *in;
+  a.o = *o;
+  if (!(d->flags & SRW_FLAG_DIAG)) {
+    a.o.token_diag = nullptr;
+    a.o.unit_diag = nullptr;
+  }
+  a.gp.sharp = d->sharpness;
+  a.gp.thr = d->act_threshold;
+  a.gp.cut = d->act_cutoff;
+  a.gp.eps = d->epsilon;
+  a.gp.maxi = d->max_intensity;
+  a.gp.cap_thresh = (d->epsilon + d->max_intensity) - 1e-3f;  // v41:487 in float32
+  a.words = (d->n_units + 63) / 64;
+  a.chunk = (d->chunk_size > 0 && d->chunk_size < d->n_units) ? d->chunk_size : d->n_units;
+  a.ws = static_cast<char*>(workspace);
+  a.ws_bytes = workspace_bytes;
+  a.stream = static_cast<hipStream_t>(stream);
+
+  (void)hipGetLastError();  // start from a clean error state
+  hipError_t e;
+  if (which == 1) {
+    const char* name = "mfma";
+    e = srw::mfma_forward(a, &name);
+    g_last_path = name;
+  } else {
+    e = srw::generic_forward(a);
+    g_last_path = "generic";
+  }
+  return e == hipSuccess ? SRW_OK : SRW_EHIP;
+}
+
+const char* srw_last_path(void) { return g_last_path; }
+
+}  // extern "C"

@@ -1,0 +1,41 @@
+// srw_internal.hpp -- host-side launch interface between the C ABI layer
+// (srw_capi.hip) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "srw_amd.h"
+#include "srw_common.hpp"
+
+namespace srw {
+
+// Everything a kernel family needs for one srw_forward call, with pointers
+// already offset and validated by the ABI layer.
+struct LaunchArgs {
+  srw_desc_t d;
+  srw_tensors_t in;
+  srw_outputs_t o;
+  GateParams gp;
+  int64_t words;     // ceil(N / 64): pass_mask words per (token, route)
+  int64_t chunk;     // N-chunk size of the reference plan (emulation); N if none
+  char* ws;          // workspace base (may be null when none is needed)
+  size_t ws_bytes;
+  hipStream_t stream;
+};
+
+// Generic kernels: one workgroup per (token, route), scalar FMA, faithful
+// to every reference rounding point.  Any shape with D <= 4096.
+size_t generic_workspace_bytes(const srw_desc_t& d);
+bool generic_supports(const srw_desc_t& d);
+hipError_t generic_forward(const LaunchArgs& a);
+
+// Fill kernel (graph-safe replacement for hipMemsetAsync).
+hipError_t fill_f32(float* p, int64_t n, float v, hipStream_t s);
+
+// MFMA kernels (bf16 / f32 matrix cores), see srw_mfma.hip.
+size_t mfma_workspace_bytes(const srw_desc_t& d);
+bool mfma_supports(const srw_desc_t& d);
+hipError_t mfma_forward(const LaunchArgs& a, const char** path_name);
+
+}  // namespace srw

@@ -1,0 +1,184 @@
+"""Drop-in mirror of the reference SRW operator interface.
+
+Reference (madst0614/DAWN-SRW, models/dawn_spatial_v41_exp.py):
+
+* ``make_sharded_srw(mesh, max_chunk_size=2048, dead_threshold=0.01,
+  sharpness=..., activation_threshold=..., activation_cutoff=...,
+  epsilon=..., max_intensity=...)`` (:352-637) returns
+  ``fused_gate_srw(x, h, emb, tau_offset, read, write)`` -> 22-tuple.
+* ``make_sharded_srw_paired(...)`` (:640-909) returns the paired QK form
+  (h [B,S,2,dr], tau_offset [B,S,2,1], out [B,S,2,D]).
+* ``_srw_inference(x, h, emb_norm, tau_offset, w_read, w_write)``
+  (:1713-1738) -> out (dtype-preserving, two-pass centred std).
+
+The factories return functions with the same positional signature and the
+same 22-tuple order, so they slot into ``sharded_fns = (fused_single,
+fused_paired)`` (consumed at :1034 and :1164).  The mesh is one device: a
+``mesh`` whose ``shape`` has data or model axes larger than 1 is refused
+(one GPU; the cross-device psums of the reference are identities there).
+
+Inputs are torch tensors on a HIP device.  Like the reference, the fused
+functions cast x, h, emb, read and write to bf16 (:423-430) and return
+``out`` as float32 holding bf16-rounded values (:586, :630).  The kernel
+computes every per-token and per-unit reduction; this module only turns
+those [T]- and [N]-sized vectors into the reference's scalars (:588-635).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .layer import GateConfig, srw_forward
+from . import _capi as C
+
+__all__ = ["make_sharded_srw", "make_sharded_srw_paired", "srw_inference",
+           "chunk_plan", "GateConfig"]
+
+_TD = C.TDIAG_INDEX
+
+
+def chunk_plan(n_local: int, max_chunk_size: int):
+    """(nc, cs) chunk plan of the N axis (v41:416-420)."""
+    nc = max(1, n_local // max_chunk_size)
+    while n_local % nc != 0 and nc < n_local:
+        nc += 1
+    return nc, n_local // nc
+
+
+def _check_mesh(mesh):
+    if mesh is None:
+        return
+    shape = getattr(mesh, "shape", None)
+    if shape is None:
+        raise TypeError("mesh must be None or expose a .shape mapping")
+    for ax in ("data", "model"):
+        if int(shape.get(ax, 1)) != 1:
+            raise NotImplementedError(
+                f"mesh axis '{ax}' = {shape[ax]}: this build runs the SRW layer on one GPU")
+
+
+def _diag_tuple(res, N, B, S, R, dead_threshold):
+    """The reference's diagnostics (v41:588-635 single, :862-907 paired).
+
+    res: kernel outputs with token_diag [T,R,14] and unit_diag [N,2].
+    Per-token outputs keep the reference's [B,S,1] shape (route-averaged
+    when R == 2, :864-871).
+    """
+    td = res["token_diag"]
+    g = res["gate_sum"]                         # [T,R]
+    na = res["n_active"].to(torch.float32)      # [T,R]
+    col = lambda k: td[..., _TD[k]]             # noqa: E731
+    s_mean, s_std, tau = col("s_mean"), col("s_std"), col("tau")
+    n_tot = float(N)
+
+    def per_token(v):                           # [T,R] -> [B,S,1]
+        return v.mean(dim=1).reshape(B, S, 1) if R == 2 else v.reshape(B, S, 1)
+
+    active_frac = per_token(na / n_tot)                            # :589 / :863-864
+    gate_max = per_token(col("gate_max"))                          # :583 / :871
+    strong_frac = per_token(col("n_strong") / n_tot)               # :590
+    boundary_frac = per_token(col("n_boundary") / n_tot)           # :592
+    z_mean_active = per_token(g / (na + 1e-8))                     # :594 / :869
+    active_denom = torch.clamp_min(na, 1.0)                        # :599
+    z_lt_075 = (col("n_band075") / active_denom).mean()            # :600-601
+    z_lt_030 = (col("n_band030") / active_denom).mean()
+    # moments -> skew / kurtosis (:466-474)
+    cube_mean = col("sum_s3") / n_tot
+    quad_mean = col("sum_s4") / n_tot
+    central_third = cube_mean - 3.0 * s_mean * (s_std ** 2) - s_mean ** 3
+    skew = (central_third / (s_std ** 3 + 1e-8)).mean()
+    central_fourth = (quad_mean - 4.0 * s_mean * cube_mean
+                      + 6.0 * (s_mean ** 2) * (s_std ** 2) + 3.0 * s_mean ** 4)
+    kurt = (central_fourth / (s_std ** 4 + 1e-8)).mean()
+    # per-unit stats: score LB (:445-447, :476-483), dead units (:543-552)
+    ud = res["unit_diag"]
+    per_neuron = ud[:, 0] / float(B * S * R)
+    mean_score = per_neuron.sum() / n_tot
+    var_score = (per_neuron ** 2).sum() / n_tot - mean_score ** 2
+    score_lb = var_score / (mean_score ** 2 + var_score + 1e-2)
+    dead = (ud[:, 1] < dead_threshold).to(torch.float32)
+    dead_penalty = (torch.relu(-per_neuron) * dead).sum()
+    dead_count = dead.sum()
+    # entropy (:611-618)
+    gse = torch.clamp_min(g, 1e-6)
+    safe = torch.where(g > 1e-6, col("g_log_g"), torch.zeros_like(g))
+    ent = -safe / gse + torch.log(gse)
+    ent = torch.where(torch.isfinite(ent), ent, torch.zeros_like(ent))
+    return (active_frac, gate_max, score_lb, s_std.mean(), g.mean(), na.mean(),
+            strong_frac, boundary_frac, z_mean_active, tau.mean(), z_lt_075,
+            z_lt_030, skew, na.std(correction=0), ent.mean(),
+            col("int_sum").mean(), kurt, dead_penalty, dead_count,
+            col("int_max").max(), col("n_int_cap").sum() / float(B * S * R * N))
+
+
+def _make(routes: int, mesh, max_chunk_size, dead_threshold, sharpness,
+          activation_threshold, activation_cutoff, epsilon, max_intensity):
+    _check_mesh(mesh)
+    consts = GateConfig(float(sharpness), float(activation_threshold),
+                        float(activation_cutoff), float(epsilon),
+                        float(max_intensity), float(dead_threshold))
+
+    def fused(x, h, emb, tau_offset, read, write):
+        B, S, D = x.shape
+        N = emb.shape[0]
+        _, cs = chunk_plan(N, max_chunk_size)
+        bf = torch.bfloat16
+        xb = x.reshape(B * S, D).to(bf).contiguous()
+        if routes == 1:
+            hb = h.reshape(B * S, 1, h.shape[-1]).to(bf).contiguous()
+            tau = tau_offset.reshape(B * S, 1).to(torch.float32).contiguous()
+        else:
+            hb = h.reshape(B * S, 2, h.shape[-1]).to(bf).contiguous()
+            tau = tau_offset.reshape(B * S, 2).to(torch.float32).contiguous()
+        res = srw_forward(xb, hb, emb.to(bf).contiguous(), tau,
+                          read.to(bf).contiguous(), write.to(bf).contiguous(),
+                          stats="onepass", consts=consts, chunk_size=cs,
+                          diag=True, want_mask=False)
+        if routes == 1:
+            out = res["out"].reshape(B, S, D).to(torch.float32)
+        else:
+            out = res["out"].reshape(B, S, 2, D).to(torch.float32)
+        return (out,) + _diag_tuple(res, N, B, S, routes, dead_threshold)
+
+    fused.__name__ = "fused_gate_srw" if routes == 1 else "fused_gate_srw_paired"
+    return fused
+
+
+def make_sharded_srw(mesh=None, max_chunk_size=2048, dead_threshold=0.01,
+                     sharpness=500.0, activation_threshold=0.5,
+                     activation_cutoff=0.01, epsilon=1e-4, max_intensity=10.0):
+    """Single-route fused gate + SRW (v41:352-637); see the module docstring."""
+    return _make(1, mesh, max_chunk_size, dead_threshold, sharpness,
+                 activation_threshold, activation_cutoff, epsilon, max_intensity)
+
+
+def make_sharded_srw_paired(mesh=None, max_chunk_size=2048, dead_threshold=0.01,
+                            sharpness=500.0, activation_threshold=0.5,
+                            activation_cutoff=0.01, epsilon=1e-4,
+                            max_intensity=10.0):
+    """Paired QK fused gate + SRW sharing one x.R^T (v41:640-909)."""
+    return _make(2, mesh, max_chunk_size, dead_threshold, sharpness,
+                 activation_threshold, activation_cutoff, epsilon, max_intensity)
+
+
+def srw_inference(x, h, emb_norm, tau_offset, w_read, w_write, *,
+                  consts: GateConfig = GateConfig(), gate: str = "v41"):
+    """``_srw_inference`` (v41:1713-1738; v4.0.1 form v401:1443-1463 with
+    gate="gelu_v401").
+
+    Keeps the input dtype (float32 end to end for float32 inputs) and uses
+    the two-pass centred std.  x [..., D], h [..., dr], tau_offset [..., 1].
+    Returns float32 out [..., D].
+    """
+    lead = x.shape[:-1]
+    D = x.shape[-1]
+    T = 1
+    for s in lead:
+        T *= int(s)
+    xx = x.reshape(T, D).contiguous()
+    hh = h.reshape(T, 1, h.shape[-1]).to(x.dtype).contiguous()
+    tau = tau_offset.reshape(T, 1).to(torch.float32).contiguous()
+    res = srw_forward(xx, hh, emb_norm.to(x.dtype).contiguous(), tau,
+                      w_read.to(x.dtype).contiguous(), w_write.to(x.dtype).contiguous(),
+                      gate=gate, stats="centered", consts=consts, want_mask=False)
+    return res["out"].reshape(*lead, D).to(torch.float32)

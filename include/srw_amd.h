@@ -1,0 +1,192 @@
+/*
+ * srw_amd.h -- C ABI of the MI355X-native Select-Read-Write (SRW) unit-pool
+ * layer (DAWN-SRW v4.1 / v4.0.1 gate), built for gfx950.
+ *
+ * One call computes, for every token t and route r of a pool of N rank-1
+ * units with rows e_n (routing, d_route), r_n (read, d_model) and w_n
+ * (write, d_model):
+ *
+ *   s[t,n]   = h[t,r,:] . e_n                         (score)
+ *   tau[t]   = mean_n s + tau_offset[t,r] * (std_n s + 1e-8)
+ *   gate     = sigmoid(k (s - tau - a)) * (eps + min(max(s - tau - a - c, 0), M))   (v4.1)
+ *            | z Phi(z), z = (s - tau)/std, 0 for z <= 0                          (v4.0.1)
+ *   out[t,r] = scale * sum_n gate * (x[t,:] . r_n) * w_n / max(den, 1)
+ *   den      = sum_n intensity (v4.1) | sum_n gate (v4.0.1)
+ *
+ * Reference interfaces replaced (paths relative to madst0614/DAWN-SRW):
+ *   srw_forward, n_routes = 1, SRW_STATS_ONEPASS
+ *       -> make_sharded_srw(...) -> fused_gate_srw(x, h, emb, tau_offset,
+ *          read, write)                models/dawn_spatial_v41_exp.py:352-637
+ *   srw_forward, n_routes = 2, SRW_STATS_ONEPASS
+ *       -> make_sharded_srw_paired(...) -> fused_gate_srw_paired(...)
+ *                                         models/dawn_spatial_v41_exp.py:640-909
+ *   srw_forward, n_routes = 1, SRW_STATS_CENTERED, dtype = SRW_F32
+ *       -> _srw_inference(x, h, emb_norm, tau_offset, w_read, w_write)
+ *                                         models/dawn_spatial_v41_exp.py:1713-1738
+ *   gate = SRW_GATE_GELU_V401
+ *       -> fused_gate_srw / _srw_inference of
+ *          models/legacy/dawn_spatial_v401_exp.py:229-355, 1443-1463
+ *   the closure constants of the factories (v41:297-301, 352-383) travel in
+ *   srw_desc_t; srw_desc_init() fills the reference defaults.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer owned by the caller; row-major,
+ *     contiguous.  The library allocates nothing: scratch memory is the
+ *     caller's workspace (size from srw_workspace_size).
+ *   - x, h, emb, read, write and out share desc->dtype (SRW_BF16 or SRW_F32).
+ *     tau_offset and every per-token / per-unit statistic are float32.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
+ *     is asynchronous.  The library keeps no state between calls and is
+ *     thread-safe; calls that share a workspace must not overlap.
+ *   - Errors are status codes; no C++ exception crosses the ABI.  NaN / Inf
+ *     inputs propagate as in the reference (no extra clamping).
+ */
+#ifndef SRW_AMD_H
+#define SRW_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SRW_AMD_ABI_VERSION 1
+
+typedef enum srw_status {
+  SRW_OK = 0,
+  SRW_EINVAL = 1,       /* bad shape, pointer or constant */
+  SRW_EUNSUPPORTED = 2, /* valid request the library does not implement */
+  SRW_EHIP = 3,         /* a HIP runtime call failed (launch, device query) */
+  SRW_EWORKSPACE = 4    /* workspace missing or smaller than required */
+} srw_status_t;
+
+typedef enum srw_dtype {
+  SRW_F32 = 0,
+  SRW_BF16 = 1
+} srw_dtype_t;
+
+typedef enum srw_gate {
+  SRW_GATE_V41 = 0,       /* activation x intensity (v41:505-511) */
+  SRW_GATE_GELU_V401 = 1  /* z Phi(z), R/W rows forward-normalised (v401:294-310) */
+} srw_gate_t;
+
+typedef enum srw_stats_mode {
+  /* One-pass moments of the dtype-rounded scores: s_std = sqrt(E[s^2] -
+   * mean^2) + 1e-8 (fused_gate_srw pass 1, v41:433-464). */
+  SRW_STATS_ONEPASS = 0,
+  /* Two-pass centred variance: s_std = sqrt(E[(s-mean)^2]) + 1e-8
+   * (_srw_inference, v41:1717-1722). */
+  SRW_STATS_CENTERED = 1,
+  /* Closed form: sum s = h.(sum e), sum s^2 = h^T (E^T E) h.  Skips the
+   * score pre-pass; moments come from unrounded scores. */
+  SRW_STATS_GRAM = 2
+} srw_stats_mode_t;
+
+/* desc->flags */
+#define SRW_FLAG_DIAG 0x1u        /* fill token_diag / unit_diag (training diagnostics) */
+#define SRW_FLAG_EMULATE 0x2u     /* reference rounding emulation (per-chunk bf16 rounding
+                                     of the partial write GEMM, v41:518); selects the
+                                     bit-faithful scalar kernels */
+#define SRW_FLAG_SPARSE_SKIP 0x4u /* skip read/write rows of units no token of a tile passes
+                                     (exact for the v4.0.1 gate; bounded error for v4.1) */
+#define SRW_FLAG_NO_FAST 0x8u     /* force the generic kernels (testing) */
+
+typedef struct srw_desc {
+  int64_t T;          /* tokens (B*S) */
+  int64_t d_model;    /* D: x, read, write, out rows */
+  int64_t d_route;    /* dr: h, emb rows */
+  int64_t n_units;    /* N: pool rows */
+  int32_t n_routes;   /* 1 = single route, 2 = paired (QK) sharing one x.R^T */
+  int32_t dtype;      /* srw_dtype_t */
+  int32_t gate;       /* srw_gate_t */
+  int32_t stats_mode; /* srw_stats_mode_t */
+  float sharpness;        /* v4.1 SHARPNESS            (default 500)  */
+  float act_threshold;    /* v4.1 ACTIVATION_THRESHOLD (default 0.5)  */
+  float act_cutoff;       /* v4.1 ACTIVATION_CUTOFF    (default 0.01) */
+  float epsilon;          /* v4.1 EPSILON              (default 1e-4) */
+  float max_intensity;    /* v4.1 MAX_INTENSITY        (default 10)   */
+  float dead_threshold;   /* dead-unit threshold for unit_diag consumers (0.01) */
+  float scale;            /* multiplies out after the den division (1 = reference fn) */
+  int32_t chunk_size;     /* N-chunk of the reference plan (v41:416-420); used by
+                             SRW_FLAG_EMULATE only; 0 = one chunk */
+  uint32_t flags;         /* SRW_FLAG_* */
+  int32_t reserved[3];
+} srw_desc_t;
+
+/* Per-token diagnostics, token_diag[(t * n_routes + r) * SRW_TDIAG_COUNT + k]. */
+enum {
+  SRW_TDIAG_S_MEAN = 0,   /* mean_n s */
+  SRW_TDIAG_S_STD,        /* std_n s + 1e-8 */
+  SRW_TDIAG_TAU,          /* tau */
+  SRW_TDIAG_SUM_S3,       /* sum_n s^3 (ONEPASS mode; 0 otherwise) */
+  SRW_TDIAG_SUM_S4,       /* sum_n s^4 (ONEPASS mode; 0 otherwise) */
+  SRW_TDIAG_GATE_MAX,     /* max_n gate */
+  SRW_TDIAG_INT_SUM,      /* sum_n intensity (v4.1) | sum_n z+ (v4.0.1), before the floor */
+  SRW_TDIAG_N_STRONG,     /* #act > 0.9  (v4.0.1: #gate > 0.5) */
+  SRW_TDIAG_N_BOUNDARY,   /* #0.1 < act < 0.9 (v4.0.1: #phi > .95 or phi < .05) */
+  SRW_TDIAG_N_BAND075,    /* #0.05 < act < 0.95 (v4.0.1: #0 < z < 0.75) */
+  SRW_TDIAG_N_BAND030,    /* #0.2 < act < 0.8 (v4.0.1: #0 < z < 0.30) */
+  SRW_TDIAG_G_LOG_G,      /* sum_n gate * log(gate + 1e-8) */
+  SRW_TDIAG_INT_MAX,      /* max_n intensity */
+  SRW_TDIAG_N_INT_CAP,    /* #intensity >= eps + max_intensity - 1e-3 */
+  SRW_TDIAG_COUNT
+};
+
+/* Per-unit diagnostics, unit_diag[n * SRW_UDIAG_COUNT + k]; reduced over all
+ * tokens and routes of the call (v41:543-552, 445-447). */
+enum {
+  SRW_UDIAG_SCORE_SUM = 0, /* sum_{t,r} s[t,r,n] */
+  SRW_UDIAG_GATE_MAX,      /* max_{t,r} gate[t,r,n] */
+  SRW_UDIAG_COUNT
+};
+
+typedef struct srw_tensors {
+  const void* x;           /* [T, D] */
+  const void* h;           /* [T, n_routes, dr]; may alias x when n_routes == 1, dr == D */
+  const void* emb;         /* [N, dr] */
+  const float* tau_offset; /* [T, n_routes] */
+  const void* read;        /* [N, D] */
+  const void* write;       /* [N, D] */
+} srw_tensors_t;
+
+typedef struct srw_outputs {
+  void* out;               /* [T, n_routes, D] (required) */
+  float* gate_sum;         /* [T, n_routes]   sum_n gate            (optional) */
+  float* den;              /* [T, n_routes]   max(den, 1)           (optional) */
+  int32_t* n_active;       /* [T, n_routes]   #units with act > 0.5 (optional) */
+  uint64_t* pass_mask;     /* [T, n_routes, ceil(N/64)] bit n%64 of word n/64 set
+                              iff unit n passes (act > 0.5)        (optional) */
+  float* token_diag;       /* [T, n_routes, SRW_TDIAG_COUNT]  needs SRW_FLAG_DIAG */
+  float* unit_diag;        /* [N, SRW_UDIAG_COUNT]            needs SRW_FLAG_DIAG */
+} srw_outputs_t;
+
+/* ABI version of the loaded library (SRW_AMD_ABI_VERSION). */
+int32_t srw_abi_version(void);
+
+/* Human-readable name of a status code (static storage). */
+const char* srw_status_string(srw_status_t status);
+
+/* Fill *desc with the v4.1 reference defaults (v41:297-301, 352; scale 1,
+ * SRW_BF16, SRW_GATE_V41, SRW_STATS_ONEPASS, n_routes 1, chunk_size 0) and
+ * zero shapes. */
+srw_status_t srw_desc_init(srw_desc_t* desc);
+
+/* Validate *desc and report the workspace (device bytes) srw_forward needs. */
+srw_status_t srw_workspace_size(const srw_desc_t* desc, size_t* bytes);
+
+/* Enqueue one SRW layer forward on `stream`.  Replaces fused_gate_srw /
+ * fused_gate_srw_paired / _srw_inference (see the table at the top). */
+srw_status_t srw_forward(const srw_desc_t* desc, const srw_tensors_t* in,
+                         const srw_outputs_t* outs, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* Name of the kernel family the last srw_forward on this thread used
+ * ("generic", "mfma_bf16", ...), for tests and benchmarks. */
+const char* srw_last_path(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SRW_AMD_H */

@@ -1,0 +1,58 @@
+"""Parity helpers shared by the GPU tests: tolerances and the tie band.
+
+Tolerances (from the hot path's contract):
+  * float32 path vs the float32 restatement: relative Frobenius error of out
+    <= 1e-5;
+  * bf16 path vs the bf16 restatement: relative Frobenius error of out
+    <= 2e-2 (and, per token row, <= 5e-2 of that row's norm);
+  * passing set: identical outside a tie band |margin| <= delta, where
+    delta covers one bf16 ulp of the score plus the tau difference (bf16),
+    or 1e-5 * max(1, s_std) (float32).
+"""
+
+from __future__ import annotations
+
+import torch
+
+REL_F32 = 1e-5
+REL_BF16 = 2e-2
+ROW_REL_BF16 = 5e-2
+
+
+def rel_fro(got: torch.Tensor, ref: torch.Tensor) -> float:
+    got = got.double()
+    ref = ref.double()
+    return float((got - ref).norm() / ref.norm().clamp_min(1e-30))
+
+
+def row_rel_max(got: torch.Tensor, ref: torch.Tensor) -> float:
+    got = got.double().reshape(-1, got.shape[-1])
+    ref = ref.double().reshape(-1, ref.shape[-1])
+    num = (got - ref).norm(dim=-1)
+    den = ref.norm(dim=-1).clamp_min(1e-30)
+    return float((num / den).max())
+
+
+def unpack_mask(words: torch.Tensor, N: int) -> torch.Tensor:
+    """[..., W] int64 words -> [..., N] bool (bit n % 64 of word n // 64)."""
+    w = words.cpu().to(torch.int64)
+    bits = torch.arange(64, dtype=torch.int64)
+    b = ((w.unsqueeze(-1) >> bits) & 1).bool()
+    return b.reshape(*w.shape[:-1], -1)[..., :N]
+
+
+def bf16_ulp(v: torch.Tensor) -> torch.Tensor:
+    """One bf16 ulp at |v| (2^(e-7) for v in [2^e, 2^(e+1)))."""
+    a = v.abs().clamp_min(2.0 ** -126)
+    e = torch.floor(torch.log2(a))
+    return torch.pow(2.0, e - 7)
+
+
+def check_pass_set(mask_got: torch.Tensor, margin_ref: torch.Tensor, delta: torch.Tensor):
+    """Mismatches of the passing set must lie inside |margin_ref| <= delta.
+
+    Returns (n_mismatch, n_outside_band)."""
+    ref = margin_ref > 0
+    mism = mask_got != ref
+    outside = mism & (margin_ref.abs() > delta)
+    return int(mism.sum()), int(outside.sum())

@@ -1,0 +1,132 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol the
+header declares, its struct layouts match the ctypes mirror (checked with a
+gcc-compiled probe of include/srw_amd.h), and argument validation returns
+the documented status codes without touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "srw_amd.h")
+
+
+@pytest.fixture(scope="module")
+def C(pkg):
+    from dawn_srw_amd import _capi
+    _capi.load_library()
+    return _capi
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(srw_\w+)\s*\(", text, flags=re.M))
+
+
+def test_library_exports_every_header_symbol(C):
+    declared = _header_functions()
+    assert declared == set(C.EXPORTED_SYMBOLS)
+    lib = C.load_library()
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.srw_abi_version() == C.ABI_VERSION
+
+
+def test_struct_layout_matches_header(C, tmp_path):
+    fields = [f[0] for f in C.SrwDesc._fields_]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "srw_amd.h"', "int main(void){",
+             'printf("%zu %zu %zu %d %d\\n", sizeof(srw_desc_t), sizeof(srw_tensors_t), '
+             'sizeof(srw_outputs_t), (int)SRW_TDIAG_COUNT, (int)SRW_UDIAG_COUNT);']
+    for f in fields:
+        lines.append(f'printf("{f} %zu\\n", offsetof(srw_desc_t, {f}));')
+    lines.append("return 0;}")
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER),
+                    str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    sizes = [int(v) for v in out[0].split()]
+    assert sizes == [ctypes.sizeof(C.SrwDesc), ctypes.sizeof(C.SrwTensors),
+                     ctypes.sizeof(C.SrwOutputs), len(C.TDIAG), len(C.UDIAG)]
+    for line in out[1:]:
+        if line:
+            name, off = line.split()
+            assert getattr(C.SrwDesc, name).offset == int(off), name
+
+
+def test_desc_init_reference_defaults(C):
+    d = C.desc_init()
+    # models/dawn_spatial_v41_exp.py:297-301, :352
+    assert (d.sharpness, d.act_threshold, d.epsilon, d.max_intensity) == (500.0, 0.5,
+                                                                           ctypes.c_float(1e-4).value, 10.0)
+    assert d.act_cutoff == ctypes.c_float(0.01).value
+    assert d.dead_threshold == ctypes.c_float(0.01).value
+    assert (d.n_routes, d.dtype, d.gate, d.stats_mode, d.scale) == (1, C.SRW_BF16, C.SRW_GATE_V41,
+                                                                    C.SRW_STATS_ONEPASS, 1.0)
+
+
+def _desc(C, **kw):
+    d = C.desc_init()
+    d.T, d.d_model, d.d_route, d.n_units = 16, 64, 32, 100
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+@pytest.mark.parametrize("bad", [dict(T=-1), dict(d_model=0), dict(n_units=0), dict(n_routes=3),
+                                 dict(dtype=7), dict(gate=9), dict(stats_mode=5),
+                                 dict(chunk_size=-2), dict(flags=0x100),
+                                 dict(sharpness=float("nan"))])
+def test_invalid_descriptors_rejected(C, bad):
+    d = _desc(C, **bad)
+    n = ctypes.c_size_t(0)
+    assert C.load_library().srw_workspace_size(ctypes.byref(d), ctypes.byref(n)) == C.SRW_EINVAL
+    t, o = C.SrwTensors(), C.SrwOutputs()
+    st = C.load_library().srw_forward(ctypes.byref(d), ctypes.byref(t), ctypes.byref(o), None, 0, None)
+    assert st == C.SRW_EINVAL
+
+
+def test_null_pointers_rejected_before_any_launch(C):
+    d = _desc(C)
+    t, o = C.SrwTensors(), C.SrwOutputs()
+    st = C.load_library().srw_forward(ctypes.byref(d), ctypes.byref(t), ctypes.byref(o), None, 0, None)
+    assert st == C.SRW_EINVAL
+    assert C.load_library().srw_forward(ctypes.byref(d), None, None, None, 0, None) == C.SRW_EINVAL
+
+
+def test_workspace_sizes(C):
+    assert C.workspace_size(_desc(C)) == 0
+    d = _desc(C, gate=C.SRW_GATE_GELU_V401)      # forward-normalised R and W copies (bf16)
+    assert C.workspace_size(d) == 2 * 100 * 64 * 2
+    d = _desc(C, gate=C.SRW_GATE_GELU_V401, dtype=C.SRW_F32)
+    assert C.workspace_size(d) == 2 * 100 * 64 * 4
+
+
+def test_status_strings(C):
+    lib = C.load_library()
+    for s in range(5):
+        assert lib.srw_status_string(s).decode().startswith("SRW_")
+    with pytest.raises(C.SrwError):
+        C.check(C.SRW_EINVAL)
+
+
+def test_wrapper_refuses_cpu_tensors(pkg):
+    import torch
+    x = torch.zeros(4, 8)
+    with pytest.raises(ValueError):
+        pkg.srw_forward(x, x, torch.zeros(3, 8), torch.zeros(4, 1), torch.zeros(3, 8), torch.zeros(3, 8))
+
+
+def test_mesh_larger_than_one_device_refused(pkg):
+    class Mesh:
+        shape = {"data": 1, "model": 2}
+    with pytest.raises(NotImplementedError):
+        pkg.make_sharded_srw(Mesh())
+    pkg.make_sharded_srw(None)
