@@ -1,0 +1,217 @@
+"""Benchmark of the MI355X SRW layer (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload know]
+
+A step is one SRW layer forward (``srw_forward`` through the C ABI) over the
+workload's synthetic batch, inputs already resident in HBM.  The default
+workload is the 40M Know pool named by the headline metric: T = 4096 tokens
+(batch 8 x seq 512), d_model = 384, N = 25 200 units, score = x.E^T
+(d_route = d_model), bf16, the reference's fused_gate_srw semantics
+(models/dawn_spatial_v41_exp.py:415-635: one-pass moments of the bf16
+scores, v4.1 gate, N chunked at 12 500 -> 2 chunks of 12 600).
+
+Prints ONE JSON line (rank 0, N = 1) with the throughput, the roofline of
+the dominant kernel (timed alone with HIP events that the library records
+around it on the call's stream) and a CPU baseline: the oracle's
+restatement of the same function timed on this host on a bounded sample of
+the same workload.  Progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "SRW layer tokens/sec on 1 MI355X (40M Know pool); % bf16 MFMA / HBM peak"
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+
+# HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc
+# FETCH_SIZE / WRITE_SIZE runs scaled by a copy kernel of known size; None
+# until measured for the kernel this build ships.
+MEASURED_TRAFFIC = {}
+
+WORKLOADS = {
+    # name: (inputs.CONFIGS key, reference max_chunk_size, note)
+    "know": ("know", 12500, "configs[0] Know pool at bf16 (the headline metric's 40M Know pool)"),
+    "v": ("v", 12500, "configs[1] V pool"),
+    "qk": ("qk", 12500, "configs[1] QK pool, paired routes sharing one x.R^T"),
+    "decode_know": ("decode_know", 12500, "configs[3] decode-shaped Know pool, T=64, 3% pass"),
+    "scaled": ("scaled", 12500, "configs[4] scaled Know pool d=1024 N=100000 T=16384, 2% pass"),
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float) -> dict:
+    """The oracle's fused_gate_srw (bf16 emulation) on a token sample of the
+    same pool, timed on the host cores (test infrastructure as the timed CPU
+    restatement; never part of the GPU path)."""
+    import torch
+    from oracle import srw_ref
+
+    threads = torch.get_num_threads()
+    T_s = min(shape.T, 1024)
+    x = inp["x"][:T_s]
+    tau = torch.full((T_s, shape.routes), tau_value)
+    if shape.routes == 1:
+        h = x if shape.h_is_x else inp["h"][:T_s, 0]
+        fn = lambda: srw_ref.fused_gate_srw(  # noqa: E731
+            x[None], h[None], inp["emb"], tau[None], inp["read"], inp["write"],
+            max_chunk_size=chunk)
+    else:
+        h = inp["h"][:T_s]
+        fn = lambda: srw_ref.fused_gate_srw_paired(  # noqa: E731
+            x[None], h[None], inp["emb"], tau.reshape(1, T_s, 2, 1), inp["read"],
+            inp["write"], max_chunk_size=chunk)
+    fn()  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    log(f"cpu baseline: T_sample={T_s} runs={len(times)} median={med * 1e3:.1f} ms "
+        f"threads={threads}")
+    return {"value": T_s / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle fused_gate_srw bf16 emulation, first {T_s} of the "
+                       f"{shape.T} tokens, full pool N={shape.N}, median of {len(times)} "
+                       f"runs; {cpu_model()}")}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="know", choices=sorted(WORKLOADS))
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--stats", default="onepass", choices=["onepass", "centered", "gram"])
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="time budget of the CPU baseline (0 skips it)")
+    ap.add_argument("--force-generic", action="store_true",
+                    help="time the generic (scalar) kernels instead of the MFMA path")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs the SRW layer on one GPU only; "
+              "--gpus above 1 is not supported (token-sharding design is documented, "
+              "not built)", file=sys.stderr)
+        return 2
+
+    import torch
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    from dawn_srw_amd import _capi as C
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    key, max_chunk, note = WORKLOADS[args.workload]
+    shape = pkg.inputs.CONFIGS[key]
+    _, cs = pkg.chunk_plan(shape.N, max_chunk)
+    log(f"workload {args.workload}: T={shape.T} D={shape.D} dr={shape.dr} N={shape.N} "
+        f"R={shape.routes} chunk={cs}")
+
+    inp = pkg.inputs.make_pool_inputs(shape, seed=args.seed)
+    tau_value = -0.5
+    if shape.pass_target is not None:
+        tau_value = pkg.inputs.calibrate_tau_offset(inp, shape.pass_target)
+        inp["tau_offset"].fill_(tau_value)
+    bf = torch.bfloat16
+    x = inp["x"].to(bf).to(dev)
+    h = x if shape.h_is_x else inp["h"].to(bf).to(dev)
+    plan = pkg.SrwPlan(x, h, inp["emb"].to(bf).to(dev), inp["tau_offset"].to(dev),
+                       inp["read"].to(bf).to(dev), inp["write"].to(bf).to(dev),
+                       stats=args.stats, chunk_size=cs, want_mask=True,
+                       force_generic=args.force_generic)
+    stream = torch.cuda.current_stream(dev)
+
+    for _ in range(args.warmup):
+        plan.launch(stream)
+    torch.cuda.synchronize()
+    log(f"warm-up done, path={plan.path}, mean active/token="
+        f"{plan.n_active.float().mean().item():.1f}")
+
+    K = args.steps
+    ev_k = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(K)]
+    for a, b in ev_k:      # materialise the HIP events on this stream
+        a.record(stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    t_begin = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_begin.record(stream)
+    for i in range(K):
+        C.set_kernel_events(ev_k[i][0].cuda_event, ev_k[i][1].cuda_event)
+        plan.launch(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    C.set_kernel_events(None, None)
+    step_ms = t_begin.elapsed_time(t_end) / K
+    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev_k)
+    log(f"timed {K} steps: {step_ms:.4f} ms/step (events), wall {wall / K * 1e3:.4f} ms/step, "
+        f"dominant kernel {kern_ms:.4f} ms")
+
+    T, D, dr, N, R = shape.T, shape.D, shape.dr, shape.N, shape.routes
+    flops = 2.0 * T * N * (R * dr + D + R * D)          # score + read (once) + write
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    traffic = MEASURED_TRAFFIC.get((args.workload, plan.path))
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "traffic": traffic, "kernel": plan.path,
+                "kernel_ms": round(kern_ms, 5), "algorithmic_flop": flops}
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        torch.set_num_threads(min(os.cpu_count() or 1, 16))
+        cpu = cpu_baseline(pkg, shape, inp, tau_value, max_chunk, args.cpu_seconds)
+
+    value = T / (step_ms * 1e-3)
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": K, "warmup": args.warmup, "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1) x RMS-normalised; E ~ N(0,1/dr); "
+                                  "R, W L2-normalised rows)",
+        "config": {"workload": args.workload, "note": note, "T": T, "d_model": D,
+                   "d_route": dr, "n_units": N, "routes": R, "chunk": cs,
+                   "stats": args.stats, "tau_offset": round(tau_value, 4),
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

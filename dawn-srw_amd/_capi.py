@@ -48,6 +48,7 @@ UDIAG = ("score_sum", "gate_max")
 EXPORTED_SYMBOLS = (
     "srw_abi_version", "srw_status_string", "srw_desc_init",
     "srw_workspace_size", "srw_forward", "srw_last_path",
+    "srw_set_kernel_events",
 )
 
 
@@ -117,6 +118,8 @@ def load_library() -> ctypes.CDLL:
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.srw_last_path.restype = ctypes.c_char_p
         lib.srw_last_path.argtypes = []
+        lib.srw_set_kernel_events.restype = ctypes.c_int
+        lib.srw_set_kernel_events.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         got = lib.srw_abi_version()
         if got != ABI_VERSION:
             raise SrwLibraryError(f"libsrw_amd.so ABI {got} != binding ABI {ABI_VERSION}")
@@ -144,3 +147,10 @@ def workspace_size(desc: SrwDesc) -> int:
 
 def last_path() -> str:
     return load_library().srw_last_path().decode()
+
+
+def set_kernel_events(start, stop) -> None:
+    """Install (or, with None, None, clear) the hipEvent_t handles that
+    srw_forward records around its dominant kernel on this thread."""
+    check(load_library().srw_set_kernel_events(
+        ctypes.c_void_p(start or 0), ctypes.c_void_p(stop or 0)))

@@ -12,6 +12,8 @@
 namespace {
 
 thread_local const char* g_last_path = "none";
+thread_local hipEvent_t g_ev_start = nullptr;
+thread_local hipEvent_t g_ev_stop = nullptr;
 
 srw_status_t validate(const srw_desc_t* d) {
   if (!d) return SRW_EINVAL;
@@ -43,6 +45,15 @@ int choose(const srw_desc_t& d) {
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
 }  // namespace
+
+namespace srw {
+void dominant_kernel_begin(hipStream_t s) {
+  if (g_ev_start && g_ev_stop) (void)hipEventRecord(g_ev_start, s);
+}
+void dominant_kernel_end(hipStream_t s) {
+  if (g_ev_start && g_ev_stop) (void)hipEventRecord(g_ev_stop, s);
+}
+}  // namespace srw
 
 extern "C" {
 
@@ -138,5 +149,12 @@ srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw
 }
 
 const char* srw_last_path(void) { return g_last_path; }
+
+srw_status_t srw_set_kernel_events(void* start, void* stop) {
+  if ((start == nullptr) != (stop == nullptr)) return SRW_EINVAL;
+  g_ev_start = static_cast<hipEvent_t>(start);
+  g_ev_stop = static_cast<hipEvent_t>(stop);
+  return SRW_OK;
+}
 
 }  // extern "C"

@@ -266,8 +266,10 @@ __global__ void fill_kernel(float* p, int64_t n, float v) {
 
 template <typename E, bool V401, bool EMU, bool DIAG>
 hipError_t launch_generic(const GenericParams& p, int64_t blocks, size_t smem, hipStream_t s) {
+  dominant_kernel_begin(s);
   hipLaunchKernelGGL((srw_generic_kernel<E, V401, EMU, DIAG>), dim3(static_cast<unsigned>(blocks)), dim3(kGT),
                      smem, s, p);
+  dominant_kernel_end(s);
   return hipGetLastError();
 }
 

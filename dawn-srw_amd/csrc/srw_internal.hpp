@@ -30,6 +30,11 @@ size_t generic_workspace_bytes(const srw_desc_t& d);
 bool generic_supports(const srw_desc_t& d);
 hipError_t generic_forward(const LaunchArgs& a);
 
+// Profiling hook (srw_set_kernel_events): brackets the dominant kernel of a
+// call with the caller's events, when the calling thread installed them.
+void dominant_kernel_begin(hipStream_t s);
+void dominant_kernel_end(hipStream_t s);
+
 // Fill kernel (graph-safe replacement for hipMemsetAsync).
 hipError_t fill_f32(float* p, int64_t n, float v, hipStream_t s);
 

@@ -1,6 +1,7 @@
 """Host wrapper of ``srw_forward``: torch tensors in, torch tensors out.
 
-This is the single place where tensors cross into libsrw_amd.so.  It checks
+This is the single place where tensors cross into libsrw_amd.so
+(``SrwPlan``; ``srw_forward`` is a one-shot plan).  It checks
 shapes, dtypes and devices, allocates the outputs and the workspace with
 torch's caching allocator, and enqueues the call on torch's current stream.
 Every computation runs in the library's HIP kernels; there is no CPU or
@@ -50,6 +51,110 @@ def _check_dev(name, t, dev, dtype=None, shape=None):
         raise ValueError(f"{name} must be contiguous")
 
 
+class SrwPlan:
+    """One bound ``srw_forward`` call: inputs checked, outputs and workspace
+    allocated, and the C descriptor structs built once, so that ``launch()``
+    is a single C call (benchmarks, loops over the same buffers).
+
+    The arguments are those of :func:`srw_forward`.  The input tensors are
+    held by reference; overwrite them in place to feed new data.
+    """
+
+    def __init__(self, x, h, emb, tau_offset, read, write, *, gate: str = "v41",
+                 stats: str = "onepass", consts: GateConfig = GateConfig(),
+                 scale: float = 1.0, chunk_size: int = 0, diag: bool = False,
+                 want_mask: bool = True, emulate: bool = False,
+                 sparse_skip: bool = False, force_generic: bool = False):
+        if x.dim() != 2:
+            raise ValueError("x must be [T, D]")
+        T, D = x.shape
+        dev = x.device
+        if dev.type != "cuda":
+            raise ValueError("srw_forward runs on a HIP device; got " + str(dev))
+        dt = x.dtype
+        if dt not in _DTYPES:
+            raise TypeError(f"unsupported dtype {dt}")
+        h_is_x = h is x
+        if h_is_x:
+            R, dr = 1, D
+        else:
+            if h.dim() != 3:
+                raise ValueError("h must be [T, R, d_route]")
+            R, dr = h.shape[1], h.shape[2]
+            _check_dev("h", h, dev, dt, (T, R, dr))
+        N = emb.shape[0]
+        _check_dev("x", x, dev, dt)
+        _check_dev("emb", emb, dev, dt, (N, dr))
+        _check_dev("tau_offset", tau_offset, dev, torch.float32, (T, R))
+        _check_dev("read", read, dev, dt, (N, D))
+        _check_dev("write", write, dev, dt, (N, D))
+        if gate not in _GATES:
+            raise ValueError(f"gate must be one of {sorted(_GATES)}")
+        if stats not in _STATS:
+            raise ValueError(f"stats must be one of {sorted(_STATS)}")
+
+        desc = C.desc_init()
+        desc.T, desc.d_model, desc.d_route, desc.n_units = T, D, dr, N
+        desc.n_routes = R
+        desc.dtype = _DTYPES[dt]
+        desc.gate = _GATES[gate]
+        desc.stats_mode = _STATS[stats]
+        desc.sharpness = consts.sharpness
+        desc.act_threshold = consts.activation_threshold
+        desc.act_cutoff = consts.activation_cutoff
+        desc.epsilon = consts.epsilon
+        desc.max_intensity = consts.max_intensity
+        desc.dead_threshold = consts.dead_threshold
+        desc.scale = scale
+        desc.chunk_size = int(chunk_size)
+        desc.flags = ((C.SRW_FLAG_DIAG if diag else 0) | (C.SRW_FLAG_EMULATE if emulate else 0)
+                      | (C.SRW_FLAG_SPARSE_SKIP if sparse_skip else 0)
+                      | (C.SRW_FLAG_NO_FAST if force_generic else 0))
+
+        words = (N + 63) // 64
+        self.out = torch.empty((T, R, D), dtype=dt, device=dev)
+        self.gate_sum = torch.empty((T, R), dtype=torch.float32, device=dev)
+        self.den = torch.empty((T, R), dtype=torch.float32, device=dev)
+        self.n_active = torch.empty((T, R), dtype=torch.int32, device=dev)
+        self.pass_mask = (torch.empty((T, R, words), dtype=torch.int64, device=dev)
+                          if want_mask else None)
+        self.token_diag = (torch.empty((T, R, len(C.TDIAG)), dtype=torch.float32, device=dev)
+                           if diag else None)
+        self.unit_diag = (torch.empty((N, len(C.UDIAG)), dtype=torch.float32, device=dev)
+                          if diag else None)
+        self.ws_bytes = C.workspace_size(desc)
+        self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
+
+        self.inputs = (x, h, emb, tau_offset, read, write)
+        self.device = dev
+        self.shape = dict(T=T, D=D, dr=dr, N=N, R=R)
+        self._desc = desc
+        self._tens = C.SrwTensors(_ptr(x), _ptr(x if h_is_x else h), _ptr(emb),
+                                  _ptr(tau_offset), _ptr(read), _ptr(write))
+        self._outs = C.SrwOutputs(_ptr(self.out), _ptr(self.gate_sum), _ptr(self.den),
+                                  _ptr(self.n_active), _ptr(self.pass_mask),
+                                  _ptr(self.token_diag), _ptr(self.unit_diag))
+        self._lib = C.load_library()
+        self.path = None
+
+    def launch(self, stream=None) -> None:
+        """Enqueue the call on ``stream`` (default: torch's current stream)."""
+        if stream is None:
+            with torch.cuda.device(self.device):
+                stream = torch.cuda.current_stream(self.device)
+        C.check(self._lib.srw_forward(
+            ctypes.byref(self._desc), ctypes.byref(self._tens), ctypes.byref(self._outs),
+            _ptr(self.workspace), ctypes.c_size_t(self.ws_bytes),
+            ctypes.c_void_p(stream.cuda_stream)))
+        self.path = C.last_path()
+
+    def results(self) -> dict:
+        return dict(out=self.out, gate_sum=self.gate_sum, den=self.den,
+                    n_active=self.n_active, pass_mask=self.pass_mask,
+                    token_diag=self.token_diag, unit_diag=self.unit_diag,
+                    path=self.path, workspace=self.workspace)
+
+
 def srw_forward(x, h, emb, tau_offset, read, write, *, gate: str = "v41",
                 stats: str = "onepass", consts: GateConfig = GateConfig(),
                 scale: float = 1.0, chunk_size: int = 0, diag: bool = False,
@@ -62,74 +167,20 @@ def srw_forward(x, h, emb, tau_offset, read, write, *, gate: str = "v41",
     x, h, emb, read and write share one dtype (float32 or bfloat16), all on
     one CUDA (HIP) device, contiguous.
 
+    Options: ``gate`` "v41" | "gelu_v401"; ``stats`` "onepass" (moments of
+    the rounded scores, fused_gate_srw) | "centered" (two-pass,
+    _srw_inference) | "gram" (closed form from E^T E); ``chunk_size`` the
+    reference's N-chunk (its partial write GEMMs are rounded to bf16 per
+    chunk); ``scale`` multiplies out after the den division.
+
     Returns a dict: out [T, R, D] (input dtype), gate_sum / den [T, R] f32,
     n_active [T, R] int32, pass_mask [T, R, ceil(N/64)] int64 (bit n % 64 of
     word n // 64) or None, token_diag [T, R, 14] / unit_diag [N, 2] f32 when
     ``diag``, and ``path`` (the kernel family used).
     """
-    if x.dim() != 2:
-        raise ValueError("x must be [T, D]")
-    T, D = x.shape
-    dev = x.device
-    if dev.type != "cuda":
-        raise ValueError("srw_forward runs on a HIP device; got " + str(dev))
-    dt = x.dtype
-    if dt not in _DTYPES:
-        raise TypeError(f"unsupported dtype {dt}")
-    h_is_x = h is x
-    if h_is_x:
-        R, dr = 1, D
-    else:
-        if h.dim() != 3:
-            raise ValueError("h must be [T, R, d_route]")
-        R, dr = h.shape[1], h.shape[2]
-        _check_dev("h", h, dev, dt, (T, R, dr))
-    N = emb.shape[0]
-    _check_dev("x", x, dev, dt)
-    _check_dev("emb", emb, dev, dt, (N, dr))
-    _check_dev("tau_offset", tau_offset, dev, torch.float32, (T, R))
-    _check_dev("read", read, dev, dt, (N, D))
-    _check_dev("write", write, dev, dt, (N, D))
-
-    desc = C.desc_init()
-    desc.T, desc.d_model, desc.d_route, desc.n_units = T, D, dr, N
-    desc.n_routes = R
-    desc.dtype = _DTYPES[dt]
-    desc.gate = _GATES[gate]
-    desc.stats_mode = _STATS[stats]
-    desc.sharpness = consts.sharpness
-    desc.act_threshold = consts.activation_threshold
-    desc.act_cutoff = consts.activation_cutoff
-    desc.epsilon = consts.epsilon
-    desc.max_intensity = consts.max_intensity
-    desc.dead_threshold = consts.dead_threshold
-    desc.scale = scale
-    desc.chunk_size = int(chunk_size)
-    desc.flags = ((C.SRW_FLAG_DIAG if diag else 0) | (C.SRW_FLAG_EMULATE if emulate else 0)
-                  | (C.SRW_FLAG_SPARSE_SKIP if sparse_skip else 0)
-                  | (C.SRW_FLAG_NO_FAST if force_generic else 0))
-
-    words = (N + 63) // 64
-    out = torch.empty((T, R, D), dtype=dt, device=dev)
-    gate_sum = torch.empty((T, R), dtype=torch.float32, device=dev)
-    den = torch.empty((T, R), dtype=torch.float32, device=dev)
-    n_active = torch.empty((T, R), dtype=torch.int32, device=dev)
-    mask = torch.empty((T, R, words), dtype=torch.int64, device=dev) if want_mask else None
-    tdiag = torch.empty((T, R, len(C.TDIAG)), dtype=torch.float32, device=dev) if diag else None
-    udiag = torch.empty((N, len(C.UDIAG)), dtype=torch.float32, device=dev) if diag else None
-
-    ws_bytes = C.workspace_size(desc)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-
-    tens = C.SrwTensors(_ptr(x), _ptr(x if h_is_x else h), _ptr(emb), _ptr(tau_offset),
-                        _ptr(read), _ptr(write))
-    outs = C.SrwOutputs(_ptr(out), _ptr(gate_sum), _ptr(den), _ptr(n_active), _ptr(mask),
-                        _ptr(tdiag), _ptr(udiag))
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        C.check(C.load_library().srw_forward(
-            ctypes.byref(desc), ctypes.byref(tens), ctypes.byref(outs),
-            _ptr(ws), ctypes.c_size_t(ws_bytes), ctypes.c_void_p(stream)))
-    return dict(out=out, gate_sum=gate_sum, den=den, n_active=n_active,
-                pass_mask=mask, token_diag=tdiag, unit_diag=udiag,
-                path=C.last_path(), workspace=ws)
+    plan = SrwPlan(x, h, emb, tau_offset, read, write, gate=gate, stats=stats,
+                   consts=consts, scale=scale, chunk_size=chunk_size, diag=diag,
+                   want_mask=want_mask, emulate=emulate, sparse_skip=sparse_skip,
+                   force_generic=force_generic)
+    plan.launch()
+    return plan.results()

@@ -185,6 +185,14 @@ srw_status_t srw_forward(const srw_desc_t* desc, const srw_tensors_t* in,
  * ("generic", "mfma_bf16", ...), for tests and benchmarks. */
 const char* srw_last_path(void);
 
+/* Profiling hook; no counterpart in the reference (its timing is host-side
+ * time.time() around whole calls, scripts/train_jax.py:2469-2481).  When
+ * both are non-NULL, every later srw_forward on this thread records the
+ * hipEvent_t `start` on the call's stream right before its dominant kernel
+ * (the fused score/read/gate/write kernel) and `stop` right after it, so a
+ * benchmark can time that kernel alone.  NULL, NULL switches it off. */
+srw_status_t srw_set_kernel_events(void* start, void* stop);
+
 #ifdef __cplusplus
 }
 #endif
