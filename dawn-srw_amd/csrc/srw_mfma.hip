@@ -1,13 +1,740 @@
-// srw_mfma.hip -- MFMA kernel family (placeholder until the tiled kernels land).
+// srw_mfma.hip -- bf16 matrix-core SRW forward for gfx950.
+//
+// Replaces the two chunk scans of fused_gate_srw (models/dawn_spatial_v41_exp.py
+// :433-577) with four kernels on the caller's stream:
+//
+//   pack      W [N, D] -> W^T fragments: the write GEMM contracts over units,
+//             which are the strided axis of W, so W is re-laid once per call in
+//             the order the matrix core's B operand wants (unit-contiguous, in
+//             the unit permutation the gate registers come out in).
+//   stats     S = H.E^T on the matrix cores, rounded to bf16 (v41:439), and the
+//             per-token power sums sum s, sum s^2 per N-split (v41:441-442).
+//   main      per (token tile, N-split): tau from the moments (v41:461-464),
+//             then for every 32-unit tile: S^T = E_t.H^T and XR^T = R_t.X^T
+//             (MFMA), the v4.1 gate in registers (v41:506-511), P = bf16(bf16(g)
+//             * bf16(xr)) (v41:516-518) fed straight back as the A operand of
+//             OUT += P.W_t (MFMA) -- the [T, N] gate never leaves the registers.
+//             Emits fp32 partial OUT, per-token partial sum gate / sum
+//             intensity / active count, and the pass bitmask.
+//   finalize  sums the N-split partials, rounds each reference chunk's write
+//             GEMM to bf16 (v41:518, chunk plan v41:416-420), den =
+//             max(sum intensity, 1), out = bf16(raw / den) (v41:584-586).
+//
+// Matrix-core layout facts used throughout (v_mfma_f32_32x32x16_bf16, wave64):
+//   A operand: lane l holds A[l % 32][8 (l / 32) + i], i = 0..7
+//   B operand: lane l holds B[8 (l / 32) + i][l % 32]
+//   C/D:       acc[v] of lane l is C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32]
+// so the gate values a lane holds after the score GEMM (one token, 16 units)
+// are already an A operand of the write GEMM, under the unit permutation
+// unit_of_k() below; the packed W^T uses the same permutation.
+//
+// Workgroup: 4 waves, 32 tokens per wave (token tile 128); X (and H) live in
+// VGPRs for the whole kernel, the fp32 OUT tile [32 x D] per wave in the
+// accumulator registers.  E, R and W^T tiles stream through LDS in a double
+// buffer filled by direct global->LDS loads, laid out fragment-major so every
+// LDS read is one conflict-free 16-byte row per lane.
+
+#include <type_traits>
+
 #include "srw_internal.hpp"
 
 namespace srw {
 
-size_t mfma_workspace_bytes(const srw_desc_t&) { return 0; }
-bool mfma_supports(const srw_desc_t&) { return false; }
-hipError_t mfma_forward(const LaunchArgs&, const char** path_name) {
-  *path_name = "mfma";
-  return hipErrorNotSupported;
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;     // 4 waves
+constexpr int kTokTile = 128;     // tokens per workgroup
+constexpr int kUnitTile = 32;     // units per tile
+constexpr int kFragBytes = 1024;  // one MFMA operand fragment: 64 lanes x 16 B
+constexpr int kTargetBlocks = 256;
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ inline f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Two floats -> two bf16 (round to nearest even, v_cvt_pk_bf16_f32), low = first.
+__device__ inline uint32_t pack_bf16(float lo, float hi) {
+  f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+__device__ inline float lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ inline float hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
+// One 16-byte direct global->LDS load per lane; the LDS destination of the
+// wave is `lds` (wave-uniform) + 16 * lane.
+__device__ inline void g2lds16(const void* g, char* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 0);
+}
+
+__device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// Unit (within a 32-unit tile) carried by k index 8*half + i of k-step j of
+// the write GEMM: the accumulator row of score-GEMM register v = 8 j + i.
+__host__ __device__ inline int unit_of_k(int j, int half, int i) {
+  return 16 * j + 8 * (i >> 2) + 4 * half + (i & 3);
+}
+// Unit (within the tile) of score-accumulator register v in lane-half `half`.
+__device__ inline int unit_of_acc(int v, int half) { return 8 * (v >> 2) + 4 * half + (v & 3); }
+
+struct Geometry {
+  int64_t T, N, cs;      // tokens, units, reference chunk size (N if unchunked)
+  int nc;                // reference chunks
+  int spc;               // N-splits per chunk
+  int S;                 // N-splits in total (nc * spc)
+  int TT;                // token tiles
+  int ntiles;            // ceil(N / 32): global 32-unit tiles
+};
+
+// Tile range [ta, tb) and unit bounds [lo, hi) of N-split `split`.  Splits
+// never cross a reference chunk; tiles are globally 32-aligned, so a tile
+// that holds a chunk boundary is shared by two splits (each masks the other's
+// units).
+__device__ inline void split_range(const Geometry& g, int split, int& ta, int& tb, int64_t& lo,
+                                   int64_t& hi) {
+  const int c = split / g.spc, sub = split % g.spc;
+  const int64_t c_lo = c * g.cs;
+  const int64_t c_hi = (c + 1) * g.cs < g.N ? (c + 1) * g.cs : g.N;
+  const int t_lo = static_cast<int>(c_lo / kUnitTile);
+  const int t_hi = static_cast<int>((c_hi + kUnitTile - 1) / kUnitTile);
+  const int64_t nt = t_hi - t_lo;
+  ta = t_lo + static_cast<int>(nt * sub / g.spc);
+  tb = t_lo + static_cast<int>(nt * (sub + 1) / g.spc);
+  lo = static_cast<int64_t>(ta) * kUnitTile > c_lo ? static_cast<int64_t>(ta) * kUnitTile : c_lo;
+  hi = static_cast<int64_t>(tb) * kUnitTile < c_hi ? static_cast<int64_t>(tb) * kUnitTile : c_hi;
+}
+
+// ---------------------------------------------------------------------------
+// pack: Wp[tile][db][j][lane][i] = W[32 tile + unit_of_k(j, lane/32, i)][32 db + lane%32]
+// (zero beyond N).  One thread per 16-byte output fragment row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pack_w_kernel(const uint16_t* __restrict__ W, uint16_t* __restrict__ Wp,
+                                                     int64_t N, int D, int64_t n_rows) {
+  const int DB = D / 32;
+  for (int64_t r = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; r < n_rows;
+       r += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int lane = static_cast<int>(r & 63);
+    const int64_t frag = r >> 6;                 // tile * (2 DB) + db * 2 + j
+    const int j = static_cast<int>(frag & 1);
+    const int db = static_cast<int>((frag >> 1) % DB);
+    const int64_t tile = (frag >> 1) / DB;
+    const int d = 32 * db + (lane & 31);
+    const int half = lane >> 5;
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t pair = 0;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int64_t u = tile * kUnitTile + unit_of_k(j, half, 2 * q + e);
+        const uint32_t b = u < N ? W[u * D + d] : 0u;
+        pair |= b << (16 * e);
+      }
+      w[q] = pair;
+    }
+    *reinterpret_cast<u32x4_t*>(Wp + r * 8) = u32x4_t{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// ---------------------------------------------------------------------------
+// stats: per (token tile, split) the bf16-score power sums sum s, sum s^2.
+// ---------------------------------------------------------------------------
+struct StatsParams {
+  const uint16_t* h;   // [T, dr]
+  const uint16_t* emb; // [N, dr]
+  float* mom;          // [S][T][2]
+  uint32_t* mask32;    // pass bitmask as uint32 words [T][mask_words32] (may be null)
+  int64_t mask_words32;
+  Geometry g;
+};
+
+template <int KH>
+__global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  constexpr int STAGE = KH * kFragBytes;
+  constexpr int DR = KH * 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int split = blockIdx.x % p.g.S;
+  const int ttile = blockIdx.x / p.g.S;
+  const int64_t t = static_cast<int64_t>(ttile) * kTokTile + 32 * wave + col;
+  const int64_t tl = t < p.g.T ? t : p.g.T - 1;
+  int ta, tb;
+  int64_t lo, hi;
+  split_range(p.g, split, ta, tb, lo, hi);
+
+  // Zero the mask words that two splits share (chunk boundaries inside a
+  // tile) and the unused upper half of the last 64-bit word; the main kernel
+  // ORs into the former and never writes the latter.
+  if (p.mask32 && split == 0) {
+    for (int c = 1; c < p.g.nc; ++c) {
+      const int64_t b = c * p.g.cs;
+      if (b % kUnitTile && half == 0 && t < p.g.T) p.mask32[t * p.mask_words32 + b / kUnitTile] = 0u;
+    }
+    if ((p.g.ntiles & 1) && half == 0 && t < p.g.T) p.mask32[t * p.mask_words32 + p.g.ntiles] = 0u;
+  }
+
+  u32x4_t hq[KH];
+#pragma unroll
+  for (int ks = 0; ks < KH; ++ks)
+    hq[ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl * DR + 16 * ks + 8 * half);
+
+  auto issue = [&](int tile, int stage) {
+    const int64_t u = static_cast<int64_t>(tile) * kUnitTile + col;
+    const int64_t row = u < p.g.N ? u : p.g.N - 1;
+    for (int f = wave; f < KH; f += 4)
+      g2lds16(p.emb + row * DR + 16 * f + 8 * half, lds + stage * STAGE + f * kFragBytes);
+  };
+
+  float s1 = 0.f, s2 = 0.f;
+  if (ta < tb) {
+    issue(ta, 0);
+    wait_vm0();
+    __syncthreads();
+  }
+  for (int tile = ta; tile < tb; ++tile) {
+    const int st = (tile - ta) & 1;
+    if (tile + 1 < tb) issue(tile + 1, st ^ 1);
+    f32x16_t acc = {};
+    const char* base = lds + st * STAGE + lane * 16;
+#pragma unroll
+    for (int ks = 0; ks < KH; ++ks)
+      acc = mfma(*reinterpret_cast<const u32x4_t*>(base + ks * kFragBytes), hq[ks], acc);
+    const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
+    const bool full = u0 >= lo && u0 + kUnitTile <= hi;
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      const uint32_t sp = pack_bf16(acc[v], acc[v + 1]);
+      float a = lo_f32(sp), b = hi_f32(sp);
+      if (!full) {
+        const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
+        if (!(ua >= lo && ua < hi)) a = 0.f;
+        if (!(ub >= lo && ub < hi)) b = 0.f;
+      }
+      s1 += a;
+      s2 += __fmul_rn(a, a);
+      s1 += b;
+      s2 += __fmul_rn(b, b);
+    }
+    wait_vm0();
+    __syncthreads();
+  }
+  s1 += __shfl_xor(s1, 32);
+  s2 += __shfl_xor(s2, 32);
+  if (half == 0 && t < p.g.T) {
+    float* m = p.mom + (static_cast<int64_t>(split) * p.g.T + t) * 2;
+    m[0] = s1;
+    m[1] = s2;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// main: fused score / read / gate / write for one (token tile, N-split).
+// ---------------------------------------------------------------------------
+struct MainParams {
+  const uint16_t* x;     // [T, D]
+  const uint16_t* h;     // [T, dr] (== x when HX)
+  const uint16_t* emb;   // [N, dr]
+  const uint16_t* read;  // [N, D]
+  const uint16_t* wp;    // packed W^T fragments
+  const float* tau_off;  // [T]
+  const float* mom;      // [S][T][2]
+  float* out_part;       // [S][T][D]
+  float* tok_part;       // [S][T][4]: sum gate, sum intensity, active count, -
+  uint32_t* mask32;      // [T][mask_words32] or null
+  int64_t mask_words32;
+  Geometry g;
+  GateParams gp;
+  float exp_scale;       // -sharpness * log2(e)
+};
+
+template <int DB, int KH, bool HX>
+__global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  constexpr int D = DB * 32;
+  constexpr int DR = KH * 16;
+  constexpr int KX = D / 16;
+  constexpr int F_E = KH, F_R = KX, F_W = 2 * DB;
+  constexpr int F = F_E + F_R + F_W;
+  constexpr int STAGE = F * kFragBytes;
+  static_assert(!HX || KH == KX, "h aliases x only when d_route == d_model");
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int split = blockIdx.x % p.g.S;
+  const int ttile = blockIdx.x / p.g.S;
+  const int64_t tw = static_cast<int64_t>(ttile) * kTokTile + 32 * wave;  // wave's first token
+  const int64_t t = tw + col;
+  const int64_t tl = t < p.g.T ? t : p.g.T - 1;
+  int ta, tb;
+  int64_t lo, hi;
+  split_range(p.g, split, ta, tb, lo, hi);
+
+  // token operands, resident for the whole kernel
+  u32x4_t xq[KX];
+#pragma unroll
+  for (int ks = 0; ks < KX; ++ks)
+    xq[ks] = *reinterpret_cast<const u32x4_t*>(p.x + tl * D + 16 * ks + 8 * half);
+  u32x4_t hq[HX ? 1 : KH];
+  if constexpr (!HX) {
+#pragma unroll
+    for (int ks = 0; ks < KH; ++ks)
+      hq[ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl * DR + 16 * ks + 8 * half);
+  }
+
+  // tau = mean + tau_offset * (sqrt(E[s^2] - mean^2) + 1e-8)   (v41:461-464)
+  float tau;
+  {
+    float a = 0.f, b = 0.f;
+    for (int s = 0; s < p.g.S; ++s) {
+      const float* m = p.mom + (static_cast<int64_t>(s) * p.g.T + tl) * 2;
+      a += m[0];
+      b += m[1];
+    }
+    const float fN = static_cast<float>(p.g.N);
+    const float mean = a / fN;
+    const float sd = sqrtf(b / fN - __fmul_rn(mean, mean)) + 1e-8f;
+    tau = mean + __fmul_rn(p.tau_off[tl], sd);
+  }
+  const GateParams gp = p.gp;
+
+  f32x16_t oacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
+  float gsum = 0.f, isum = 0.f;
+  uint32_t nact = 0;
+
+  // Direct global->LDS loads of one tile: wave w issues fragments w, w+4, ...
+  // of each of the E, R and W^T groups.
+  auto issue = [&](int tile, int stage) {
+    char* sb = lds + stage * STAGE;
+    const int64_t u = static_cast<int64_t>(tile) * kUnitTile + col;
+    const int64_t row = u < p.g.N ? u : p.g.N - 1;
+    const uint16_t* esrc = p.emb + row * DR + 8 * half;
+    const uint16_t* rsrc = p.read + row * D + 8 * half;
+    const uint16_t* wsrc = p.wp + static_cast<int64_t>(tile) * F_W * 512 + lane * 8;
+#pragma unroll
+    for (int q = 0; q < (F_E + 3) / 4; ++q) {
+      const int f = wave + 4 * q;
+      if (f < F_E) g2lds16(esrc + 16 * f, sb + f * kFragBytes);
+    }
+#pragma unroll
+    for (int q = 0; q < (F_R + 3) / 4; ++q) {
+      const int f = wave + 4 * q;
+      if (f < F_R) g2lds16(rsrc + 16 * f, sb + (F_E + f) * kFragBytes);
+    }
+#pragma unroll
+    for (int q = 0; q < (F_W + 3) / 4; ++q) {
+      const int f = wave + 4 * q;
+      if (f < F_W) g2lds16(wsrc + f * 512, sb + (F_E + F_R + f) * kFragBytes);
+    }
+  };
+
+  // gate epilogue (v41:503-518) for one tile: the lane holds token `col` and
+  // the 16 units unit_of_acc(v, half); returns the bf16 products packed as the
+  // write GEMM's A operand and the pass bits (element v at bit 15 - v).
+  auto epilogue = [&](auto full_tag, const f32x16_t& sacc, const f32x16_t& racc, int64_t u0,
+                      uint32_t* pk) -> uint32_t {
+    constexpr bool FULL = decltype(full_tag)::value;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      const uint32_t sp = pack_bf16(sacc[v], sacc[v + 1]);   // bf16 scores (v41:503)
+      const uint32_t xp = pack_bf16(racc[v], racc[v + 1]);   // bf16 x.r (v41:517)
+      float g2[2], in2[2];
+      bool on2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float s = e ? hi_f32(sp) : lo_f32(sp);
+        const float raw = s - tau;
+        const float margin = raw - gp.thr;
+        const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(margin * p.exp_scale));
+        const float am = fmaxf(margin - gp.cut, 0.0f);
+        float inten = gp.eps + fminf(am, gp.maxi);
+        float g = act * inten;
+        bool on = act > 0.5f;
+        if constexpr (!FULL) {
+          const int64_t u = u0 + unit_of_acc(v + e, half);
+          const bool ok = u >= lo && u < hi;
+          g = ok ? g : 0.f;
+          inten = ok ? inten : 0.f;
+          on = on && ok;
+        }
+        g2[e] = g;
+        in2[e] = inten;
+        on2[e] = on;
+      }
+      gsum += g2[0];
+      gsum += g2[1];
+      isum += in2[0];
+      isum += in2[1];
+      bits = (bits << 2) | (on2[0] ? 2u : 0u) | (on2[1] ? 1u : 0u);
+      const uint32_t gq = pack_bf16(g2[0], g2[1]);             // gate_bf (v41:516)
+      pk[v >> 1] = pack_bf16(lo_f32(gq) * lo_f32(xp), hi_f32(gq) * hi_f32(xp));  // (v41:518)
+    }
+    return bits;
+  };
+
+  constexpr int G = 4;  // fragments read from LDS ahead of their MFMAs
+  if (ta < tb) {
+    issue(ta, 0);
+    wait_vm0();
+    __syncthreads();
+  }
+  for (int tile = ta; tile < tb; ++tile) {
+    const int st = (tile - ta) & 1;
+    if (tile + 1 < tb) issue(tile + 1, st ^ 1);
+    const char* base = lds + st * STAGE + lane * 16;
+
+    // score and read GEMMs, transposed: rows = units, columns = tokens
+    f32x16_t sacc = {}, racc = {};
+    if constexpr (HX) {
+#pragma unroll
+      for (int k0 = 0; k0 < KX; k0 += G) {
+        u32x4_t ef[G], rf[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          ef[g] = *reinterpret_cast<const u32x4_t*>(base + (k0 + g) * kFragBytes);
+          rf[g] = *reinterpret_cast<const u32x4_t*>(base + (F_E + k0 + g) * kFragBytes);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          sacc = mfma(ef[g], xq[k0 + g], sacc);
+          racc = mfma(rf[g], xq[k0 + g], racc);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k0 = 0; k0 < KH; k0 += G) {
+        u32x4_t ef[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          if (k0 + g < KH) ef[g] = *reinterpret_cast<const u32x4_t*>(base + (k0 + g) * kFragBytes);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          if (k0 + g < KH) sacc = mfma(ef[g], hq[HX ? 0 : k0 + g], sacc);
+      }
+#pragma unroll
+      for (int k0 = 0; k0 < KX; k0 += G) {
+        u32x4_t rf[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          rf[g] = *reinterpret_cast<const u32x4_t*>(base + (F_E + k0 + g) * kFragBytes);
+#pragma unroll
+        for (int g = 0; g < G; ++g) racc = mfma(rf[g], xq[k0 + g], racc);
+      }
+    }
+
+    const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
+    uint32_t pk[8];
+    uint32_t bits;
+    if (u0 >= lo && u0 + kUnitTile <= hi)
+      bits = epilogue(std::integral_constant<bool, true>{}, sacc, racc, u0, pk);
+    else
+      bits = epilogue(std::integral_constant<bool, false>{}, sacc, racc, u0, pk);
+
+    // write GEMM: OUT[32 tok x D] += P[32 tok x 32 units] . W_t[32 units x D]
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x4_t a = {pk[4 * j], pk[4 * j + 1], pk[4 * j + 2], pk[4 * j + 3]};
+#pragma unroll
+      for (int d0 = 0; d0 < DB; d0 += G) {
+        u32x4_t wf[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          if (d0 + g < DB)
+            wf[g] = *reinterpret_cast<const u32x4_t*>(base + (F_E + F_R + 2 * (d0 + g) + j) * kFragBytes);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+          if (d0 + g < DB) oacc[d0 + g] = mfma(a, wf[g], oacc[d0 + g]);
+      }
+    }
+
+    // pass bitmask
+    {
+      const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
+      uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
+      m <<= 4 * half;
+      nact += __builtin_popcount(m);
+      m |= __shfl_xor(m, 32);
+      if (p.mask32 && half == 0 && t < p.g.T) {
+        uint32_t* dst = p.mask32 + t * p.mask_words32 + tile;
+        const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
+        if (shared) atomicOr(dst, m);
+        else *dst = m;
+      }
+    }
+    wait_vm0();
+    __syncthreads();
+  }
+
+  // partial outputs of this split
+  gsum += __shfl_xor(gsum, 32);
+  isum += __shfl_xor(isum, 32);
+  nact += __shfl_xor(nact, 32);
+  if (half == 0 && t < p.g.T) {
+    float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * 4;
+    tp[0] = gsum;
+    tp[1] = isum;
+    tp[2] = static_cast<float>(nact);
+  }
+  float* op = p.out_part + static_cast<int64_t>(split) * p.g.T * D;
+  if (tw + 32 <= p.g.T) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) op[(tw + unit_of_acc(v, half)) * D + 32 * db + col] = oacc[db][v];
+  } else {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t tt = tw + unit_of_acc(v, half);
+        if (tt < p.g.T) op[tt * D + 32 * db + col] = oacc[db][v];
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// finalize: reduce the N-splits, bf16-round each reference chunk's write GEMM,
+// divide by den, round, scale.
+// ---------------------------------------------------------------------------
+struct FinalParams {
+  const float* out_part;
+  const float* tok_part;
+  uint16_t* out;         // [T, D] bf16
+  float* gate_sum;
+  float* den;
+  int32_t* n_active;
+  int64_t T;
+  int D, S, spc;
+  float scale;
+};
+
+__global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
+  const int64_t total = p.T * p.D;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t t = i / p.D;
+    const int d = static_cast<int>(i - t * p.D);
+    float isum = 0.f;
+    for (int s = 0; s < p.S; ++s) isum += p.tok_part[(s * p.T + t) * 4 + 1];
+    const float den = fmaxf(isum, 1.0f);                    // v41:584
+    float raw = 0.f;
+    for (int s0 = 0; s0 < p.S; s0 += p.spc) {                // one reference chunk
+      float c = 0.f;
+      for (int s = s0; s < s0 + p.spc; ++s) c += p.out_part[(s * p.T + t) * p.D + d];
+      raw += round_bf16(c);                                  // bf16 dot output (v41:518)
+    }
+    const float o = round_bf16(raw / den);                  // v41:585-586
+    p.out[i] = f32_to_bf16_bits(o * p.scale);
+    if (d == 0) {
+      float gs = 0.f, na = 0.f;
+      for (int s = 0; s < p.S; ++s) {
+        gs += p.tok_part[(s * p.T + t) * 4 + 0];
+        na += p.tok_part[(s * p.T + t) * 4 + 2];
+      }
+      if (p.gate_sum) p.gate_sum[t] = gs;
+      if (p.den) p.den[t] = den;
+      if (p.n_active) p.n_active[t] = static_cast<int32_t>(na);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct Kernels {
+  void (*stats)(StatsParams);
+  void (*main)(MainParams);
+};
+
+template <int DB, int KH, bool HX>
+Kernels kernels_of() {
+  return Kernels{srw_stats_kernel<KH>, srw_main_kernel<DB, KH, HX>};
+}
+
+// Instantiated shapes (d_model, d_route); for d_route == d_model there is a
+// variant whose score operand is the x registers themselves (h aliases x).
+bool pick(int64_t D, int64_t dr, bool hx, Kernels* k) {
+  if (hx && D == dr) {
+    if (D == 384) { *k = kernels_of<12, 24, true>(); return true; }
+    if (D == 128) { *k = kernels_of<4, 8, true>(); return true; }
+    if (D == 64) { *k = kernels_of<2, 4, true>(); return true; }
+  }
+  if (D == 384 && dr == 384) { *k = kernels_of<12, 24, false>(); return true; }
+  if (D == 384 && dr == 128) { *k = kernels_of<12, 8, false>(); return true; }
+  if (D == 128 && dr == 128) { *k = kernels_of<4, 8, false>(); return true; }
+  if (D == 128 && dr == 64) { *k = kernels_of<4, 4, false>(); return true; }
+  if (D == 64 && dr == 64) { *k = kernels_of<2, 4, false>(); return true; }
+  if (D == 64 && dr == 32) { *k = kernels_of<2, 2, false>(); return true; }
+  return false;
+}
+
+Geometry geometry(const srw_desc_t& d, int64_t chunk) {
+  Geometry g{};
+  g.T = d.T;
+  g.N = d.n_units;
+  g.cs = chunk > 0 && chunk < d.n_units ? chunk : d.n_units;
+  g.nc = static_cast<int>((g.N + g.cs - 1) / g.cs);
+  g.TT = static_cast<int>((d.T + kTokTile - 1) / kTokTile);
+  g.ntiles = static_cast<int>((g.N + kUnitTile - 1) / kUnitTile);
+  // every split needs >= 1 tile: a chunk of L units spans >= L / 32 tiles
+  const int64_t last = g.N - (g.nc - 1) * g.cs;
+  const int64_t min_tiles = (last < g.cs ? last : g.cs) / kUnitTile;
+  int spc = static_cast<int>((kTargetBlocks + g.TT * g.nc - 1) / (g.TT * g.nc));
+  if (spc < 1) spc = 1;
+  if (spc > min_tiles) spc = static_cast<int>(min_tiles > 0 ? min_tiles : 1);
+  g.spc = spc;
+  g.S = g.nc * spc;
+  return g;
+}
+
+struct WsLayout {
+  size_t wp, mom, out_part, tok_part, total;
+};
+
+size_t al(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+WsLayout ws_layout(const srw_desc_t& d, const Geometry& g) {
+  WsLayout w{};
+  size_t off = 0;
+  w.wp = off;
+  off += al(static_cast<size_t>(g.ntiles) * kUnitTile * d.d_model * 2);
+  w.mom = off;
+  off += al(static_cast<size_t>(g.S) * d.T * 2 * 4);
+  w.out_part = off;
+  off += al(static_cast<size_t>(g.S) * d.T * d.d_model * 4);
+  w.tok_part = off;
+  off += al(static_cast<size_t>(g.S) * d.T * 4 * 4);
+  w.total = off;
+  return w;
+}
+
+int64_t chunk_of(const srw_desc_t& d) {
+  return d.chunk_size > 0 && d.chunk_size < d.n_units ? d.chunk_size : d.n_units;
+}
+
+}  // namespace
+
+bool mfma_supports(const srw_desc_t& d) {
+  if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41 || d.stats_mode != SRW_STATS_ONEPASS) return false;
+  if (d.n_routes != 1) return false;
+  if (d.flags & (SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
+  Kernels k;
+  if (!pick(d.d_model, d.d_route, false, &k)) return false;  // the aliasing variant is optional
+  // every reference chunk must hold at least one whole 32-unit tile
+  const int64_t cs = chunk_of(d);
+  const int64_t last = d.n_units - ((d.n_units + cs - 1) / cs - 1) * cs;
+  return (last < cs ? last : cs) >= kUnitTile;
+}
+
+size_t mfma_workspace_bytes(const srw_desc_t& d) {
+  const Geometry g = geometry(d, chunk_of(d));
+  return ws_layout(d, g).total;
+}
+
+hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
+  const srw_desc_t& d = a.d;
+  *path_name = "mfma_bf16";
+  const bool hx = a.in.h == a.in.x;
+  Kernels k;
+  if (!pick(d.d_model, d.d_route, hx, &k)) return hipErrorNotSupported;
+  const Geometry g = geometry(d, a.chunk);
+  const WsLayout L = ws_layout(d, g);
+  if (a.ws_bytes < L.total) return hipErrorInvalidValue;
+  uint16_t* wp = reinterpret_cast<uint16_t*>(a.ws + L.wp);
+  float* mom = reinterpret_cast<float*>(a.ws + L.mom);
+  float* out_part = reinterpret_cast<float*>(a.ws + L.out_part);
+  float* tok_part = reinterpret_cast<float*>(a.ws + L.tok_part);
+  const int D = static_cast<int>(d.d_model);
+  const int KH = static_cast<int>(d.d_route / 16);
+  const int KX = D / 16;
+  const int DB = D / 32;
+  uint32_t* mask32 = reinterpret_cast<uint32_t*>(a.o.pass_mask);
+  const int64_t mw32 = 2 * a.words;
+  hipError_t e;
+
+  // pack W^T
+  {
+    const int64_t rows = static_cast<int64_t>(g.ntiles) * 2 * DB * 64;
+    int64_t blocks = (rows + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(pack_w_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, a.stream,
+                       static_cast<const uint16_t*>(a.in.write), wp, d.n_units, D, rows);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  const unsigned grid = static_cast<unsigned>(g.TT * g.S);
+  // stats
+  {
+    StatsParams sp{};
+    sp.h = static_cast<const uint16_t*>(a.in.h);
+    sp.emb = static_cast<const uint16_t*>(a.in.emb);
+    sp.mom = mom;
+    sp.mask32 = mask32;
+    sp.mask_words32 = mw32;
+    sp.g = g;
+    const size_t smem = static_cast<size_t>(2 * KH) * kFragBytes;
+    if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(k.stats),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem))) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(k.stats, dim3(grid), dim3(kThreads), smem, a.stream, sp);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  // main
+  {
+    MainParams mp{};
+    mp.x = static_cast<const uint16_t*>(a.in.x);
+    mp.h = static_cast<const uint16_t*>(a.in.h);
+    mp.emb = static_cast<const uint16_t*>(a.in.emb);
+    mp.read = static_cast<const uint16_t*>(a.in.read);
+    mp.wp = wp;
+    mp.tau_off = a.in.tau_offset;
+    mp.mom = mom;
+    mp.out_part = out_part;
+    mp.tok_part = tok_part;
+    mp.mask32 = mask32;
+    mp.mask_words32 = mw32;
+    mp.g = g;
+    mp.gp = a.gp;
+    mp.exp_scale = -d.sharpness * 1.4426950408889634f;
+    const size_t smem = static_cast<size_t>(2 * (KH + KX + 2 * DB)) * kFragBytes;
+    if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(k.main),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem))) != hipSuccess)
+      return e;
+    dominant_kernel_begin(a.stream);
+    hipLaunchKernelGGL(k.main, dim3(grid), dim3(kThreads), smem, a.stream, mp);
+    dominant_kernel_end(a.stream);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  // finalize
+  {
+    FinalParams fp{};
+    fp.out_part = out_part;
+    fp.tok_part = tok_part;
+    fp.out = static_cast<uint16_t*>(a.o.out);
+    fp.gate_sum = a.o.gate_sum;
+    fp.den = a.o.den;
+    fp.n_active = a.o.n_active;
+    fp.T = d.T;
+    fp.D = D;
+    fp.S = g.S;
+    fp.spc = g.spc;
+    fp.scale = d.scale;
+    int64_t blocks = (d.T * D + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(srw_finalize_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, a.stream, fp);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace srw

@@ -1,0 +1,149 @@
+"""GPU parity of the matrix-core path (libsrw_amd.so "mfma_bf16" kernels,
+through the C ABI) against the CPU oracle's restatement of fused_gate_srw
+(models/dawn_spatial_v41_exp.py:415-635).
+
+Shapes cover: d_route == d_model with h aliasing x (the Know-pool form of
+the benchmark), a separate router h with d_route = 128, ragged N (not a
+multiple of the 32-unit tile), ragged T (not a multiple of the 128-token
+tile), reference chunk boundaries that fall inside a unit tile, the den
+floor, and the full configs[0] size.
+
+Tolerances: out within 2e-2 relative (Frobenius) of the bf16 restatement,
+and the passing set identical outside a tie band of one bf16 score ulp plus
+the tau slack -- the score GEMM's fp32 accumulation order differs from the
+CPU matmul, so a score can round to the neighbouring bf16 value.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import srw_ref
+from tests.parity import (REL_BF16, bf16_ulp, check_pass_set, rel_fro, row_rel_max,
+                          unpack_mask)
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+
+
+def _inputs(pkg, T, D, dr, N, h_is_x, seed, tau=-0.5):
+    shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=1, h_is_x=h_is_x)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=seed)
+    inp["tau_offset"].fill_(tau)
+    return inp
+
+
+def _gpu(pkg, dev, inp, chunk_size, **kw):
+    x = inp["x"].to(BF).to(dev)
+    h = x if "h" not in inp else inp["h"].to(BF).to(dev)
+    res = pkg.srw_forward(x, h, inp["emb"].to(BF).to(dev), inp["tau_offset"].to(dev),
+                          inp["read"].to(BF).to(dev), inp["write"].to(BF).to(dev),
+                          chunk_size=chunk_size, **kw)
+    torch.cuda.synchronize()
+    return {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in res.items()}
+
+
+def _oracle(inp, max_chunk):
+    x = inp["x"][None]
+    h = x if "h" not in inp else inp["h"][:, 0][None]
+    return srw_ref.fused_gate_srw(x, h, inp["emb"], inp["tau_offset"][None], inp["read"],
+                                  inp["write"], max_chunk_size=max_chunk, return_trace=True)
+
+
+def _check(got, ref, tr, T, N, D, out_tol=REL_BF16):
+    out_ref = ref[0].reshape(T, D)
+    out = got["out"][:, 0].float()
+    err = rel_fro(out, out_ref)
+    print(f"  out rel err {err:.3e}, worst row {row_rel_max(out, out_ref):.3e}", flush=True)
+    assert err <= out_tol
+    assert row_rel_max(out, out_ref) <= 5e-2
+    den_ref = tr["den"].reshape(T)
+    assert torch.allclose(got["den"][:, 0], den_ref, rtol=2e-4, atol=0)
+    assert torch.allclose(got["gate_sum"][:, 0], tr["gate_sum"].reshape(T), rtol=2e-3, atol=1e-5)
+    margin = tr["margin"].reshape(T, N)
+    score = margin + tr["tau"].reshape(T, 1) + 0.5
+    delta = 2 * bf16_ulp(score) + 1e-4 * tr["s_std"].reshape(T, 1)
+    mask = unpack_mask(got["pass_mask"][:, 0], N)
+    n_mis, n_out = check_pass_set(mask, margin, delta)
+    print(f"  pass-set mismatches {n_mis} (outside tie band {n_out})", flush=True)
+    assert n_out == 0
+    # bits beyond N in the last word are zero
+    words = got["pass_mask"][:, 0]
+    full = unpack_mask(words, words.shape[-1] * 64)
+    assert not bool(full[:, N:].any())
+    # n_active is the popcount of the mask
+    assert torch.equal(got["n_active"][:, 0].long(), mask.sum(dim=1))
+
+
+CASES = [
+    # T, D, dr, N, h_is_x, max_chunk (reference), seed
+    (256, 384, 384, 2600, True, 1300, 1),     # chunk boundary 1300 inside a tile
+    (200, 384, 128, 1580, False, 12500, 2),   # ragged T and N, router h
+    (77, 128, 64, 777, False, 300, 3),        # three chunks of 259 units
+    (33, 64, 64, 100, True, 2048, 4),         # tiny pool, one chunk
+    (130, 128, 128, 70, True, 2048, 5),       # odd tile count: upper half of last word unused
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "T{}D{}dr{}N{}{}c{}".format(
+    c[0], c[1], c[2], c[3], "x" if c[4] else "", c[5]))
+def test_mfma_matches_fused_oracle(pkg, dev, case):
+    T, D, dr, N, hx, max_chunk, seed = case
+    print(f"[gpu] mfma bf16 {case}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, hx, seed)
+    _, cs = srw_ref.chunk_plan(N, max_chunk)
+    got = _gpu(pkg, dev, inp, cs)
+    assert got["path"] == "mfma_bf16"
+    ref, tr = _oracle(inp, max_chunk)
+    _check(got, ref, tr, T, N, D)
+
+
+def test_mfma_den_floor(pkg, dev):
+    """A high tau_offset on a V-sized pool: sum intensity < 1, den floors at 1."""
+    T, D, dr, N = 64, 384, 384, 2600
+    print(f"[gpu] mfma den floor T{T} N{N}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, True, seed=21, tau=3.0)
+    got = _gpu(pkg, dev, inp, 0)
+    assert got["path"] == "mfma_bf16"
+    ref, tr = _oracle(inp, 12500)
+    assert (tr["intensity_sum"] < 1).any()
+    assert torch.equal(got["den"][:, 0] == 1.0, tr["den"].reshape(T) == 1.0)
+    _check(got, ref, tr, T, N, D)
+
+
+def test_mfma_matches_generic_kernel(pkg, dev):
+    """The matrix-core path against the bit-faithful scalar kernels on the GPU."""
+    T, D, dr, N = 512, 384, 384, 6000
+    print(f"[gpu] mfma vs generic T{T} N{N}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, True, seed=7)
+    _, cs = srw_ref.chunk_plan(N, 2500)
+    fast = _gpu(pkg, dev, inp, cs)
+    slow = _gpu(pkg, dev, inp, cs, emulate=True)
+    assert fast["path"] == "mfma_bf16" and slow["path"] == "generic"
+    assert rel_fro(fast["out"].float(), slow["out"].float()) <= 5e-3
+    assert torch.allclose(fast["den"], slow["den"], rtol=2e-4)
+
+
+def test_mfma_full_know_config(pkg, dev):
+    """configs[0] at full size: T=4096, D=384, N=25200, two reference chunks."""
+    shape = pkg.inputs.CONFIGS["know"]
+    print(f"[gpu] mfma full Know config {shape}", flush=True)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=0)
+    _, cs = srw_ref.chunk_plan(shape.N, 12500)
+    got = _gpu(pkg, dev, inp, cs)
+    assert got["path"] == "mfma_bf16"
+    # the oracle on a token subset (rows are independent across tokens)
+    Ts = 512
+    sub = dict(inp, x=inp["x"][:Ts], tau_offset=inp["tau_offset"][:Ts])
+    ref, tr = _oracle(sub, 12500)
+    got_s = {k: (v[:Ts] if isinstance(v, torch.Tensor) and v.shape[0] == shape.T else v)
+             for k, v in got.items()}
+    _check(got_s, ref, tr, Ts, shape.N, shape.D)
+    # whole-batch properties: about half the units pass (tau_offset = -0.5),
+    # den = N eps + sum_{margin > cutoff} min(margin - cutoff, 10) >= N eps
+    frac = got["n_active"].float().mean().item() / shape.N
+    assert 0.45 < frac < 0.55, frac
+    assert bool((got["den"] >= shape.N * 1e-4).all())
+    assert bool(torch.isfinite(got["out"].float()).all())
