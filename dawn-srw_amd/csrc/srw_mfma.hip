@@ -85,11 +85,20 @@ __host__ __device__ inline int unit_of_k(int j, int half, int i) {
 // Unit (within the tile) of score-accumulator register v in lane-half `half`.
 __device__ inline int unit_of_acc(int v, int half) { return 8 * (v >> 2) + 4 * half + (v & 3); }
 
+// The gate epilogue of a tile as 48 micro-steps (type * 16 + element):
+// type 0 = bf16 score, margin, exp; 1 = sigmoid, intensity, gate; 2 = sums,
+// pass bit, bf16 product.  Element v's three steps are spread two entries
+// apart so each result has an MFMA's duration to land before it is used.
+__device__ constexpr uint8_t kEpiStep[48] = {
+    0, 1, 16, 2, 17, 32, 3, 18, 33, 4, 19, 34, 5, 20, 35, 6, 21, 36, 7, 22, 37, 8, 23, 38,
+    9, 24, 39, 10, 25, 40, 11, 26, 41, 12, 27, 42, 13, 28, 43, 14, 29, 44, 15, 30, 45, 31, 46, 47};
+
 struct Geometry {
   int64_t T, N, cs;      // tokens, units, reference chunk size (N if unchunked)
   int nc;                // reference chunks
-  int spc;               // N-splits per chunk
+  int spc;               // N-splits per chunk of the main kernel
   int S;                 // N-splits in total (nc * spc)
+  int spc_st, S_st;      // the same for the moments kernel (finer: two workgroups per CU)
   int TT;                // token tiles
   int ntiles;            // ceil(N / 32): global 32-unit tiles
 };
@@ -98,16 +107,16 @@ struct Geometry {
 // never cross a reference chunk; tiles are globally 32-aligned, so a tile
 // that holds a chunk boundary is shared by two splits (each masks the other's
 // units).
-__device__ inline void split_range(const Geometry& g, int split, int& ta, int& tb, int64_t& lo,
+__device__ inline void split_range(const Geometry& g, int spc, int split, int& ta, int& tb, int64_t& lo,
                                    int64_t& hi) {
-  const int c = split / g.spc, sub = split % g.spc;
+  const int c = split / spc, sub = split % spc;
   const int64_t c_lo = c * g.cs;
   const int64_t c_hi = (c + 1) * g.cs < g.N ? (c + 1) * g.cs : g.N;
   const int t_lo = static_cast<int>(c_lo / kUnitTile);
   const int t_hi = static_cast<int>((c_hi + kUnitTile - 1) / kUnitTile);
   const int64_t nt = t_hi - t_lo;
-  ta = t_lo + static_cast<int>(nt * sub / g.spc);
-  tb = t_lo + static_cast<int>(nt * (sub + 1) / g.spc);
+  ta = t_lo + static_cast<int>(nt * sub / spc);
+  tb = t_lo + static_cast<int>(nt * (sub + 1) / spc);
   lo = static_cast<int64_t>(ta) * kUnitTile > c_lo ? static_cast<int64_t>(ta) * kUnitTile : c_lo;
   hi = static_cast<int64_t>(tb) * kUnitTile < c_hi ? static_cast<int64_t>(tb) * kUnitTile : c_hi;
 }
@@ -163,13 +172,13 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
   constexpr int DR = KH * 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const int split = blockIdx.x % p.g.S;
-  const int ttile = blockIdx.x / p.g.S;
+  const int split = blockIdx.x % p.g.S_st;
+  const int ttile = blockIdx.x / p.g.S_st;
   const int64_t t = static_cast<int64_t>(ttile) * kTokTile + 32 * wave + col;
   const int64_t tl = t < p.g.T ? t : p.g.T - 1;
   int ta, tb;
   int64_t lo, hi;
-  split_range(p.g, split, ta, tb, lo, hi);
+  split_range(p.g, p.g.spc_st, split, ta, tb, lo, hi);
 
   // Zero the mask words that two splits share (chunk boundaries inside a
   // tile) and the unused upper half of the last 64-bit word; the main kernel
@@ -205,9 +214,17 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
     if (tile + 1 < tb) issue(tile + 1, st ^ 1);
     f32x16_t acc = {};
     const char* base = lds + st * STAGE + lane * 16;
+    constexpr int PF = 4;
+    u32x4_t ef[PF];
 #pragma unroll
-    for (int ks = 0; ks < KH; ++ks)
-      acc = mfma(*reinterpret_cast<const u32x4_t*>(base + ks * kFragBytes), hq[ks], acc);
+    for (int g = 0; g < PF; ++g)
+      if (g < KH) ef[g] = *reinterpret_cast<const u32x4_t*>(base + g * kFragBytes);
+#pragma unroll
+    for (int ks = 0; ks < KH; ++ks) {
+      const u32x4_t e = ef[ks % PF];
+      if (ks + PF < KH) ef[ks % PF] = *reinterpret_cast<const u32x4_t*>(base + (ks + PF) * kFragBytes);
+      acc = mfma(e, hq[ks], acc);
+    }
     const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
     const bool full = u0 >= lo && u0 + kUnitTile <= hi;
 #pragma unroll
@@ -256,6 +273,12 @@ struct MainParams {
   float exp_scale;       // -sharpness * log2(e)
 };
 
+// Software pipeline over the split's 32-unit tiles.  Iteration i runs the
+// score/read GEMMs of tile i+1 interleaved (sched_group_barrier) with the gate
+// epilogue of tile i -- matrix-core and vector-ALU work of one wave overlap --
+// then the write GEMM of tile i.  LDS holds two E/R stages (tile i+1 being read,
+// tile i+2 being loaded) and two W^T stages (tile i being read, tile i+1
+// being loaded): 2 x 48 KB + 2 x 24 KB at d_model = d_route = 384.
 template <int DB, int KH, bool HX>
 __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
@@ -263,8 +286,8 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
   constexpr int DR = KH * 16;
   constexpr int KX = D / 16;
   constexpr int F_E = KH, F_R = KX, F_W = 2 * DB;
-  constexpr int F = F_E + F_R + F_W;
-  constexpr int STAGE = F * kFragBytes;
+  constexpr int ER_STAGE = (F_E + F_R) * kFragBytes;
+  constexpr int W_STAGE = F_W * kFragBytes;
   static_assert(!HX || KH == KX, "h aliases x only when d_route == d_model");
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -276,7 +299,7 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
   const int64_t tl = t < p.g.T ? t : p.g.T - 1;
   int ta, tb;
   int64_t lo, hi;
-  split_range(p.g, split, ta, tb, lo, hi);
+  split_range(p.g, p.g.spc, split, ta, tb, lo, hi);
 
   // token operands, resident for the whole kernel
   u32x4_t xq[KX];
@@ -294,7 +317,7 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
   float tau;
   {
     float a = 0.f, b = 0.f;
-    for (int s = 0; s < p.g.S; ++s) {
+    for (int s = 0; s < p.g.S_st; ++s) {
       const float* m = p.mom + (static_cast<int64_t>(s) * p.g.T + tl) * 2;
       a += m[0];
       b += m[1];
@@ -312,15 +335,16 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
   float gsum = 0.f, isum = 0.f;
   uint32_t nact = 0;
 
-  // Direct global->LDS loads of one tile: wave w issues fragments w, w+4, ...
-  // of each of the E, R and W^T groups.
-  auto issue = [&](int tile, int stage) {
-    char* sb = lds + stage * STAGE;
+  char* const er_base = lds;
+  char* const w_base = lds + 2 * ER_STAGE;
+
+  // Direct global->LDS loads: wave w issues fragments w, w+4, ... of a group.
+  auto issue_er = [&](int tile, int stage) {
+    char* sb = er_base + stage * ER_STAGE;
     const int64_t u = static_cast<int64_t>(tile) * kUnitTile + col;
     const int64_t row = u < p.g.N ? u : p.g.N - 1;
     const uint16_t* esrc = p.emb + row * DR + 8 * half;
     const uint16_t* rsrc = p.read + row * D + 8 * half;
-    const uint16_t* wsrc = p.wp + static_cast<int64_t>(tile) * F_W * 512 + lane * 8;
 #pragma unroll
     for (int q = 0; q < (F_E + 3) / 4; ++q) {
       const int f = wave + 4 * q;
@@ -331,16 +355,40 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
       const int f = wave + 4 * q;
       if (f < F_R) g2lds16(rsrc + 16 * f, sb + (F_E + f) * kFragBytes);
     }
+  };
+  auto issue_w = [&](int tile, int stage) {
+    char* sb = w_base + stage * W_STAGE;
+    const uint16_t* wsrc = p.wp + static_cast<int64_t>(tile) * F_W * 512 + lane * 8;
 #pragma unroll
     for (int q = 0; q < (F_W + 3) / 4; ++q) {
       const int f = wave + 4 * q;
-      if (f < F_W) g2lds16(wsrc + f * 512, sb + (F_E + F_R + f) * kFragBytes);
+      if (f < F_W) g2lds16(wsrc + f * 512, sb + f * kFragBytes);
     }
   };
 
-  // gate epilogue (v41:503-518) for one tile: the lane holds token `col` and
-  // the 16 units unit_of_acc(v, half); returns the bf16 products packed as the
-  // write GEMM's A operand and the pass bits (element v at bit 15 - v).
+  // score and read GEMMs of one tile, transposed: rows = units, columns = tokens
+  auto phase_a = [&](int stage, f32x16_t& sacc, f32x16_t& racc) {
+    const char* base = er_base + stage * ER_STAGE + lane * 16;
+    auto frag = [&](int f) { return *reinterpret_cast<const u32x4_t*>(base + f * kFragBytes); };
+    sacc = f32x16_t{};
+    racc = f32x16_t{};
+    if constexpr (HX) {
+#pragma unroll
+      for (int ks = 0; ks < KX; ++ks) {
+        sacc = mfma(frag(ks), xq[ks], sacc);
+        racc = mfma(frag(F_E + ks), xq[ks], racc);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KH; ++ks) sacc = mfma(frag(ks), hq[HX ? 0 : ks], sacc);
+#pragma unroll
+      for (int ks = 0; ks < KX; ++ks) racc = mfma(frag(F_E + ks), xq[ks], racc);
+    }
+  };
+
+  // gate epilogue (v41:503-518): the lane holds token `col` and the 16 units
+  // unit_of_acc(v, half); writes the bf16 products packed as the write GEMM's
+  // A operand and returns the pass bits (element v at bit 15 - v).
   auto epilogue = [&](auto full_tag, const f32x16_t& sacc, const f32x16_t& racc, int64_t u0,
                       uint32_t* pk) -> uint32_t {
     constexpr bool FULL = decltype(full_tag)::value;
@@ -383,97 +431,144 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
     return bits;
   };
 
-  constexpr int G = 4;  // fragments read from LDS ahead of their MFMAs
+  // write GEMM: OUT[32 tok x D] += P[32 tok x 32 units] . W_t[32 units x D],
+  // W^T fragments read from LDS PF MFMAs ahead
+  auto phase_c = [&](int stage, const uint32_t* pk) {
+    const char* base = w_base + stage * W_STAGE + lane * 16;
+    constexpr int NC = 2 * DB, PF = 4;
+    auto frag = [&](int k) {  // MFMA k: j = k / DB, db = k % DB
+      return *reinterpret_cast<const u32x4_t*>(base + (2 * (k % DB) + k / DB) * kFragBytes);
+    };
+    u32x4_t fr[PF];
+#pragma unroll
+    for (int k = 0; k < PF; ++k) fr[k] = frag(k);
+    const u32x4_t a0 = {pk[0], pk[1], pk[2], pk[3]}, a1 = {pk[4], pk[5], pk[6], pk[7]};
+#pragma unroll
+    for (int k = 0; k < NC; ++k) {
+      const u32x4_t b = fr[k % PF];
+      if (k + PF < NC) fr[k % PF] = frag(k + PF);
+      oacc[k % DB] = mfma(k < DB ? a0 : a1, b, oacc[k % DB]);
+    }
+  };
+
+  // pass bitmask and active count of one tile
+  auto emit_mask = [&](int tile, uint32_t bits) {
+    const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
+    const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
+    uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
+    m <<= 4 * half;
+    nact += __builtin_popcount(m);
+    m |= __shfl_xor(m, 32);
+    if (p.mask32 && half == 0 && t < p.g.T) {
+      uint32_t* dst = p.mask32 + t * p.mask_words32 + tile;
+      const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
+      if (shared) atomicOr(dst, m);
+      else *dst = m;
+    }
+  };
+
+  // Steady state of the pipeline: the score/read GEMMs of the next tile
+  // (NM MFMAs, operands read from LDS PF steps ahead) with the 48 epilogue
+  // micro-steps of this tile spread over them; sched_barrier(0) fences each
+  // MFMA with its slice so that the wave issues vector work while the matrix
+  // core runs.
+  auto fused_step = [&](int stage, f32x16_t& sn, f32x16_t& rn, const f32x16_t& sacc,
+                        const f32x16_t& racc, uint32_t* pk) -> uint32_t {
+    constexpr int NM = KH + KX;
+    constexpr int PF = 4;
+    const char* base = er_base + stage * ER_STAGE + lane * 16;
+    // MFMA k: HX interleaves score (even k) and read (odd k) steps; otherwise
+    // all score steps, then all read steps.
+    auto frag_of = [](int k) constexpr { return HX ? ((k & 1) ? F_E + (k >> 1) : (k >> 1)) : (k < KH ? k : F_E + (k - KH)); };
+    u32x4_t fr[PF];
+#pragma unroll
+    for (int k = 0; k < PF; ++k) fr[k] = *reinterpret_cast<const u32x4_t*>(base + frag_of(k) * kFragBytes);
+    sn = f32x16_t{};
+    rn = f32x16_t{};
+    uint32_t sp[8], xp[8], gpk[8];
+    float mg[16], ex[16], gv[16], iv[16];
+    bool on[16];
+    uint32_t bits = 0;
+#pragma unroll
+    for (int k = 0; k < NM; ++k) {
+      const u32x4_t a = fr[k % PF];
+      if (k + PF < NM) fr[k % PF] = *reinterpret_cast<const u32x4_t*>(base + frag_of(k + PF) * kFragBytes);
+      const bool is_score = HX ? !(k & 1) : (k < KH);
+      const int ks = HX ? (k >> 1) : (k < KH ? k : k - KH);
+      if (is_score) sn = mfma(a, HX ? xq[ks] : hq[HX ? 0 : ks], sn);
+      else rn = mfma(a, xq[ks], rn);
+#pragma unroll
+      for (int st = (k * 48) / NM; st < ((k + 1) * 48) / NM; ++st) {
+        const int typ = kEpiStep[st] >> 4, v = kEpiStep[st] & 15;
+        if (typ == 0) {
+          if (!(v & 1)) {
+            sp[v >> 1] = pack_bf16(sacc[v], sacc[v + 1]);   // bf16 scores (v41:503)
+            xp[v >> 1] = pack_bf16(racc[v], racc[v + 1]);   // bf16 x.r (v41:517)
+          }
+          const float sv = (v & 1) ? hi_f32(sp[v >> 1]) : lo_f32(sp[v >> 1]);
+          const float raw = sv - tau;
+          mg[v] = raw - gp.thr;
+          ex[v] = __builtin_amdgcn_exp2f(mg[v] * p.exp_scale);
+        } else if (typ == 1) {
+          const float act = __builtin_amdgcn_rcpf(1.0f + ex[v]);
+          const float am = fmaxf(mg[v] - gp.cut, 0.0f);
+          iv[v] = gp.eps + fminf(am, gp.maxi);
+          gv[v] = act * iv[v];
+          on[v] = act > 0.5f;
+        } else {
+          gsum += gv[v];
+          isum += iv[v];
+          bits = (bits << 1) | (on[v] ? 1u : 0u);
+          if (v & 1) {
+            gpk[v >> 1] = pack_bf16(gv[v - 1], gv[v]);       // gate_bf (v41:516)
+            pk[v >> 1] = pack_bf16(lo_f32(gpk[v >> 1]) * lo_f32(xp[v >> 1]),
+                                   hi_f32(gpk[v >> 1]) * hi_f32(xp[v >> 1]));  // (v41:518)
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return bits;
+  };
+
+  // two accumulator pairs alternate between "phase-A results of the tile
+  // being finished" and "phase A of the next tile"
+  f32x16_t s0 = {}, r0 = {}, s1 = {}, r1 = {};
   if (ta < tb) {
-    issue(ta, 0);
+    issue_er(ta, ta & 1);
+    issue_w(ta, ta & 1);
+    if (ta + 1 < tb) issue_er(ta + 1, (ta + 1) & 1);
     wait_vm0();
+    __syncthreads();
+    phase_a(ta & 1, s0, r0);
     __syncthreads();
   }
-  for (int tile = ta; tile < tb; ++tile) {
-    const int st = (tile - ta) & 1;
-    if (tile + 1 < tb) issue(tile + 1, st ^ 1);
-    const char* base = lds + st * STAGE + lane * 16;
-
-    // score and read GEMMs, transposed: rows = units, columns = tokens
-    f32x16_t sacc = {}, racc = {};
-    if constexpr (HX) {
-#pragma unroll
-      for (int k0 = 0; k0 < KX; k0 += G) {
-        u32x4_t ef[G], rf[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          ef[g] = *reinterpret_cast<const u32x4_t*>(base + (k0 + g) * kFragBytes);
-          rf[g] = *reinterpret_cast<const u32x4_t*>(base + (F_E + k0 + g) * kFragBytes);
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          sacc = mfma(ef[g], xq[k0 + g], sacc);
-          racc = mfma(rf[g], xq[k0 + g], racc);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int k0 = 0; k0 < KH; k0 += G) {
-        u32x4_t ef[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-          if (k0 + g < KH) ef[g] = *reinterpret_cast<const u32x4_t*>(base + (k0 + g) * kFragBytes);
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-          if (k0 + g < KH) sacc = mfma(ef[g], hq[HX ? 0 : k0 + g], sacc);
-      }
-#pragma unroll
-      for (int k0 = 0; k0 < KX; k0 += G) {
-        u32x4_t rf[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-          rf[g] = *reinterpret_cast<const u32x4_t*>(base + (F_E + k0 + g) * kFragBytes);
-#pragma unroll
-        for (int g = 0; g < G; ++g) racc = mfma(rf[g], xq[k0 + g], racc);
-      }
-    }
-
-    const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
+  // one pipeline iteration: finish tile i (its phase-A results in sc/rc)
+  // while the next tile's phase A accumulates into sn/rn
+  auto iteration = [&](int i, f32x16_t& sc, f32x16_t& rc, f32x16_t& sn, f32x16_t& rn) {
+    if (i + 2 < tb) issue_er(i + 2, i & 1);
+    if (i + 1 < tb) issue_w(i + 1, (i + 1) & 1);
+    const int64_t u0 = static_cast<int64_t>(i) * kUnitTile;
+    const bool full = u0 >= lo && u0 + kUnitTile <= hi;
     uint32_t pk[8];
     uint32_t bits;
-    if (u0 >= lo && u0 + kUnitTile <= hi)
-      bits = epilogue(std::integral_constant<bool, true>{}, sacc, racc, u0, pk);
-    else
-      bits = epilogue(std::integral_constant<bool, false>{}, sacc, racc, u0, pk);
-
-    // write GEMM: OUT[32 tok x D] += P[32 tok x 32 units] . W_t[32 units x D]
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const u32x4_t a = {pk[4 * j], pk[4 * j + 1], pk[4 * j + 2], pk[4 * j + 3]};
-#pragma unroll
-      for (int d0 = 0; d0 < DB; d0 += G) {
-        u32x4_t wf[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-          if (d0 + g < DB)
-            wf[g] = *reinterpret_cast<const u32x4_t*>(base + (F_E + F_R + 2 * (d0 + g) + j) * kFragBytes);
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-          if (d0 + g < DB) oacc[d0 + g] = mfma(a, wf[g], oacc[d0 + g]);
-      }
+    if (i + 1 < tb && full) {
+      // steady state: next tile's GEMMs overlap this tile's gate epilogue
+      bits = fused_step((i + 1) & 1, sn, rn, sc, rc, pk);
+    } else {
+      if (full) bits = epilogue(std::integral_constant<bool, true>{}, sc, rc, u0, pk);
+      else bits = epilogue(std::integral_constant<bool, false>{}, sc, rc, u0, pk);
+      if (i + 1 < tb) phase_a((i + 1) & 1, sn, rn);
     }
-
-    // pass bitmask
-    {
-      const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
-      uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
-      m <<= 4 * half;
-      nact += __builtin_popcount(m);
-      m |= __shfl_xor(m, 32);
-      if (p.mask32 && half == 0 && t < p.g.T) {
-        uint32_t* dst = p.mask32 + t * p.mask_words32 + tile;
-        const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
-        if (shared) atomicOr(dst, m);
-        else *dst = m;
-      }
-    }
+    phase_c(i & 1, pk);
+    emit_mask(i, bits);
     wait_vm0();
     __syncthreads();
+  };
+  for (int i = ta; i < tb; ++i) {
+    iteration(i, s0, r0, s1, r1);
+    s0 = s1;
+    r0 = r1;
   }
 
   // partial outputs of this split
@@ -500,6 +595,264 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
         const int64_t tt = tw + unit_of_acc(v, half);
         if (tt < p.g.T) op[tt * D + 32 * db + col] = oacc[db][v];
       }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// main, warp-specialised: 8 waves, two per SIMD.  Waves 0-3 (producers) own 32
+// tokens each with X (and H) in VGPRs: the score/read GEMMs of tile i and its
+// gate epilogue, handing the bf16 products P to LDS.  Waves 4-7 (consumers)
+// own the same 32-token blocks with the fp32 OUT accumulators: the write GEMM
+// of tile i - 1 from LDS P and W^T.  One workgroup barrier per tile; both
+// roles issue global->LDS loads (producers E/R of the next tile, consumers W^T
+// of this one), because per-CU load throughput grows with the number of
+// issuing waves.  The two waves on a SIMD overlap one's vector-ALU epilogue with the
+// other's matrix-core work, and each role fits the 256 registers a wave may
+// hold at two waves per SIMD.  LDS = 2 E/R + 2 W^T + 2 P stages.
+// ---------------------------------------------------------------------------
+constexpr int kWsThreads = 512;
+
+template <int DB, int KH, bool HX>
+__global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  constexpr int D = DB * 32;
+  constexpr int DR = KH * 16;
+  constexpr int KX = D / 16;
+  constexpr int F_E = KH, F_R = KX, F_W = 2 * DB;
+  constexpr int ER_STAGE = (F_E + F_R) * kFragBytes;
+  constexpr int W_STAGE = F_W * kFragBytes;
+  constexpr int P_STAGE = 4 * 2 * kFragBytes;  // 4 token blocks x 2 k-steps
+  static_assert(!HX || KH == KX, "h aliases x only when d_route == d_model");
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool producer = wave < 4;
+  const int blk = wave & 3;                 // token block of this wave
+  const int half = lane >> 5, col = lane & 31;
+  const int split = blockIdx.x % p.g.S;
+  const int ttile = blockIdx.x / p.g.S;
+  const int64_t tw = static_cast<int64_t>(ttile) * kTokTile + 32 * blk;
+  const int64_t t = tw + col;
+  const int64_t tl = t < p.g.T ? t : p.g.T - 1;
+  int ta, tb;
+  int64_t lo, hi;
+  split_range(p.g, p.g.spc, split, ta, tb, lo, hi);
+  const int n = tb - ta;
+
+  char* const er_base = lds;
+  char* const w_base = lds + 2 * ER_STAGE;
+  char* const p_base = w_base + 2 * W_STAGE;
+
+  // Tile loads, direct global->LDS: producers fetch E/R of the next tile,
+  // consumers W^T of the current one, each wave a contiguous fragment run.
+  auto issue_er = [&](int tile, int stage) {
+    char* sb = er_base + stage * ER_STAGE;
+    const int64_t u = static_cast<int64_t>(tile) * kUnitTile + col;
+    const int64_t row = u < p.g.N ? u : p.g.N - 1;
+    constexpr int PE = (F_E + 3) / 4, PR = (F_R + 3) / 4;
+    const uint16_t* eb = p.emb + row * DR + 8 * half + 16 * PE * blk;
+    const uint16_t* rb = p.read + row * D + 8 * half + 16 * PR * blk;
+#pragma unroll
+    for (int q = 0; q < PE; ++q)
+      if (PE * blk + q < F_E) g2lds16(eb + 16 * q, sb + (PE * blk + q) * kFragBytes);
+#pragma unroll
+    for (int q = 0; q < PR; ++q)
+      if (PR * blk + q < F_R) g2lds16(rb + 16 * q, sb + (F_E + PR * blk + q) * kFragBytes);
+  };
+  auto issue_w = [&](int tile, int stage) {
+    char* sb = w_base + stage * W_STAGE;
+    constexpr int PW = (F_W + 3) / 4;
+    const uint16_t* wb = p.wp + (static_cast<int64_t>(tile) * F_W + PW * blk) * 512 + lane * 8;
+#pragma unroll
+    for (int q = 0; q < PW; ++q)
+      if (PW * blk + q < F_W) g2lds16(wb + q * 512, sb + (PW * blk + q) * kFragBytes);
+  };
+
+  // prologue: E/R of the first tile
+  if (n > 0 && producer) issue_er(ta, 0);
+  wait_vm0();
+  __syncthreads();
+
+  if (producer) {
+    // ---------------- producer: score / read GEMMs and the gate ----------------
+    u32x4_t xq[KX];
+#pragma unroll
+    for (int ks = 0; ks < KX; ++ks)
+      xq[ks] = *reinterpret_cast<const u32x4_t*>(p.x + tl * D + 16 * ks + 8 * half);
+    u32x4_t hq[HX ? 1 : KH];
+    if constexpr (!HX) {
+#pragma unroll
+      for (int ks = 0; ks < KH; ++ks)
+        hq[ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl * DR + 16 * ks + 8 * half);
+    }
+    // tau = mean + tau_offset * (sqrt(E[s^2] - mean^2) + 1e-8)   (v41:461-464),
+    // folded with the gate's constant offsets:
+    //   margin = s - tau - thr,  exp argument = margin * c  (c = -sharpness log2 e)
+    float k_exp, tau_cut;
+    {
+      float a = 0.f, b = 0.f;
+      for (int s = 0; s < p.g.S_st; ++s) {
+        const float* m = p.mom + (static_cast<int64_t>(s) * p.g.T + tl) * 2;
+        a += m[0];
+        b += m[1];
+      }
+      const float fN = static_cast<float>(p.g.N);
+      const float mean = a / fN;
+      const float sd = sqrtf(b / fN - __fmul_rn(mean, mean)) + 1e-8f;
+      const float tau = mean + __fmul_rn(p.tau_off[tl], sd);
+      const float tau_thr = tau + p.gp.thr;
+      k_exp = -tau_thr * p.exp_scale;
+      tau_cut = tau_thr + p.gp.cut;
+    }
+    const float c_exp = p.exp_scale, eps = p.gp.eps, maxi = p.gp.maxi;
+    float gsum = 0.f, isum = 0.f;
+    uint32_t nact = 0;
+
+    // gate epilogue (v41:503-518) of one tile; P goes to LDS as the consumer's
+    // A operand (k-step j at [blk][j][lane]); returns pass bits (v at 15 - v)
+    auto gate_tile = [&](auto full_tag, const f32x16_t& sacc, const f32x16_t& racc, int64_t u0,
+                         char* pdst) -> uint32_t {
+      constexpr bool FULL = decltype(full_tag)::value;
+      uint32_t bits = 0;
+      uint32_t pk[8];
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const uint32_t sp = pack_bf16(sacc[v], sacc[v + 1]);   // bf16 scores (v41:503)
+        const uint32_t xp = pack_bf16(racc[v], racc[v + 1]);   // bf16 x.r (v41:517)
+        float g2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float sv = e ? hi_f32(sp) : lo_f32(sp);
+          // sigmoid(sharpness * margin) = 1 / (1 + 2^(margin * c)); active <=> margin > 0 <=> arg < 0
+          const float arg = fmaf(sv, c_exp, k_exp);
+          const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(arg));
+          // intensity = eps + min(max(margin - cutoff, 0), max_intensity)
+          float inten = eps + __builtin_amdgcn_fmed3f(sv - tau_cut, 0.0f, maxi);
+          float g = act * inten;
+          uint32_t sign = __float_as_uint(arg);
+          if constexpr (!FULL) {
+            const int64_t u = u0 + unit_of_acc(v + e, half);
+            const bool ok = u >= lo && u < hi;
+            g = ok ? g : 0.f;
+            inten = ok ? inten : 0.f;
+            sign = ok ? sign : 0u;
+          }
+          gsum += g;
+          isum += inten;
+          bits = __builtin_amdgcn_alignbit(bits, sign, 31);     // bits << 1 | active
+          g2[e] = g;
+        }
+        const uint32_t gq = pack_bf16(g2[0], g2[1]);             // gate_bf (v41:516)
+        pk[v >> 1] = pack_bf16(lo_f32(gq) * lo_f32(xp), hi_f32(gq) * hi_f32(xp));  // (v41:518)
+      }
+      *reinterpret_cast<u32x4_t*>(pdst + lane * 16) = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
+      *reinterpret_cast<u32x4_t*>(pdst + kFragBytes + lane * 16) = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
+      return bits;
+    };
+
+    for (int it = 0; it <= n; ++it) {
+      if (it + 1 < n) issue_er(ta + it + 1, (it + 1) & 1);
+      if (it < n) {
+        // score and read GEMMs, LDS operands read PF MFMAs ahead
+        const char* base = er_base + (it & 1) * ER_STAGE + lane * 16;
+        constexpr int NM = KH + KX, PF = 8;
+        auto frag_of = [](int k) constexpr {
+          return HX ? ((k & 1) ? F_E + (k >> 1) : (k >> 1)) : (k < KH ? k : F_E + (k - KH));
+        };
+        u32x4_t fr[PF];
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+          if (k < NM) fr[k] = *reinterpret_cast<const u32x4_t*>(base + frag_of(k) * kFragBytes);
+        f32x16_t sacc = {}, racc = {};
+#pragma unroll
+        for (int k = 0; k < NM; ++k) {
+          const u32x4_t a = fr[k % PF];
+          if (k + PF < NM) fr[k % PF] = *reinterpret_cast<const u32x4_t*>(base + frag_of(k + PF) * kFragBytes);
+          const bool is_score = HX ? !(k & 1) : (k < KH);
+          const int ks = HX ? (k >> 1) : (k < KH ? k : k - KH);
+          if (is_score) sacc = mfma(a, HX ? xq[ks] : hq[HX ? 0 : ks], sacc);
+          else racc = mfma(a, xq[ks], racc);
+          __builtin_amdgcn_sched_barrier(0);  // keep the reads PF steps ahead
+        }
+        // gate epilogue, P to LDS, pass bitmask
+        const int tile = ta + it;
+        const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
+        char* pdst = p_base + (it & 1) * P_STAGE + blk * 2 * kFragBytes;
+        uint32_t bits;
+        if (u0 >= lo && u0 + kUnitTile <= hi)
+          bits = gate_tile(std::integral_constant<bool, true>{}, sacc, racc, u0, pdst);
+        else
+          bits = gate_tile(std::integral_constant<bool, false>{}, sacc, racc, u0, pdst);
+        const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
+        uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
+        m <<= 4 * half;
+        nact += __builtin_popcount(m);
+        m |= __shfl_xor(m, 32);
+        if (p.mask32 && half == 0 && t < p.g.T) {
+          uint32_t* dst = p.mask32 + t * p.mask_words32 + tile;
+          const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
+          if (shared) atomicOr(dst, m);
+          else *dst = m;
+        }
+      }
+      wait_vm0();
+      __syncthreads();
+    }
+    gsum += __shfl_xor(gsum, 32);
+    isum += __shfl_xor(isum, 32);
+    nact += __shfl_xor(nact, 32);
+    if (half == 0 && t < p.g.T) {
+      float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * 4;
+      tp[0] = gsum;
+      tp[1] = isum;
+      tp[2] = static_cast<float>(nact);
+    }
+  } else {
+    // ---------------- consumer: the write GEMM, one tile behind ----------------
+    f32x16_t oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
+    for (int it = 0; it <= n; ++it) {
+      if (it < n) issue_w(ta + it, it & 1);
+      if (it >= 1) {
+        const int st = (it - 1) & 1;
+        const char* wb = w_base + st * W_STAGE + lane * 16;
+        const char* pb = p_base + st * P_STAGE + blk * 2 * kFragBytes + lane * 16;
+        const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(pb);
+        const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(pb + kFragBytes);
+        constexpr int NC = 2 * DB, PF = 6;
+        auto frag = [&](int k) {  // MFMA k: j = k / DB, db = k % DB
+          return *reinterpret_cast<const u32x4_t*>(wb + (2 * (k % DB) + k / DB) * kFragBytes);
+        };
+        u32x4_t fr[PF];
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+          if (k < NC) fr[k] = frag(k);
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+          const u32x4_t bq = fr[k % PF];
+          if (k + PF < NC) fr[k % PF] = frag(k + PF);
+          oacc[k % DB] = mfma(k < DB ? a0 : a1, bq, oacc[k % DB]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      wait_vm0();
+      __syncthreads();
+    }
+    float* op = p.out_part + static_cast<int64_t>(split) * p.g.T * D;
+    if (tw + 32 <= p.g.T) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) op[(tw + unit_of_acc(v, half)) * D + 32 * db + col] = oacc[db][v];
+    } else {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t tt = tw + unit_of_acc(v, half);
+          if (tt < p.g.T) op[tt * D + 32 * db + col] = oacc[db][v];
+        }
+    }
   }
 }
 
@@ -555,27 +908,35 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
 struct Kernels {
   void (*stats)(StatsParams);
   void (*main)(MainParams);
+  int main_threads;
+  int main_lds;  // bytes
 };
 
-template <int DB, int KH, bool HX>
+// WS: the warp-specialised main kernel (when both roles fit 256 registers)
+template <int DB, int KH, bool HX, bool WS>
 Kernels kernels_of() {
-  return Kernels{srw_stats_kernel<KH>, srw_main_kernel<DB, KH, HX>};
+  if constexpr (WS)
+    return Kernels{srw_stats_kernel<KH>, srw_main_ws_kernel<DB, KH, HX>, kWsThreads,
+                   (2 * (KH + 2 * DB) + 2 * 2 * DB + 2 * 8) * kFragBytes};
+  else
+    return Kernels{srw_stats_kernel<KH>, srw_main_kernel<DB, KH, HX>, kThreads,
+                   2 * (KH + 2 * DB + 2 * DB) * kFragBytes};
 }
 
 // Instantiated shapes (d_model, d_route); for d_route == d_model there is a
 // variant whose score operand is the x registers themselves (h aliases x).
 bool pick(int64_t D, int64_t dr, bool hx, Kernels* k) {
   if (hx && D == dr) {
-    if (D == 384) { *k = kernels_of<12, 24, true>(); return true; }
-    if (D == 128) { *k = kernels_of<4, 8, true>(); return true; }
-    if (D == 64) { *k = kernels_of<2, 4, true>(); return true; }
+    if (D == 384) { *k = kernels_of<12, 24, true, true>(); return true; }
+    if (D == 128) { *k = kernels_of<4, 8, true, true>(); return true; }
+    if (D == 64) { *k = kernels_of<2, 4, true, true>(); return true; }
   }
-  if (D == 384 && dr == 384) { *k = kernels_of<12, 24, false>(); return true; }
-  if (D == 384 && dr == 128) { *k = kernels_of<12, 8, false>(); return true; }
-  if (D == 128 && dr == 128) { *k = kernels_of<4, 8, false>(); return true; }
-  if (D == 128 && dr == 64) { *k = kernels_of<4, 4, false>(); return true; }
-  if (D == 64 && dr == 64) { *k = kernels_of<2, 4, false>(); return true; }
-  if (D == 64 && dr == 32) { *k = kernels_of<2, 2, false>(); return true; }
+  if (D == 384 && dr == 384) { *k = kernels_of<12, 24, false, false>(); return true; }
+  if (D == 384 && dr == 128) { *k = kernels_of<12, 8, false, true>(); return true; }
+  if (D == 128 && dr == 128) { *k = kernels_of<4, 8, false, true>(); return true; }
+  if (D == 128 && dr == 64) { *k = kernels_of<4, 4, false, true>(); return true; }
+  if (D == 64 && dr == 64) { *k = kernels_of<2, 4, false, true>(); return true; }
+  if (D == 64 && dr == 32) { *k = kernels_of<2, 2, false, true>(); return true; }
   return false;
 }
 
@@ -595,6 +956,11 @@ Geometry geometry(const srw_desc_t& d, int64_t chunk) {
   if (spc > min_tiles) spc = static_cast<int>(min_tiles > 0 ? min_tiles : 1);
   g.spc = spc;
   g.S = g.nc * spc;
+  int spc_st = static_cast<int>((2 * kTargetBlocks + g.TT * g.nc - 1) / (g.TT * g.nc));
+  if (spc_st < 1) spc_st = 1;
+  if (spc_st > min_tiles) spc_st = static_cast<int>(min_tiles > 0 ? min_tiles : 1);
+  g.spc_st = spc_st;
+  g.S_st = g.nc * spc_st;
   return g;
 }
 
@@ -610,7 +976,7 @@ WsLayout ws_layout(const srw_desc_t& d, const Geometry& g) {
   w.wp = off;
   off += al(static_cast<size_t>(g.ntiles) * kUnitTile * d.d_model * 2);
   w.mom = off;
-  off += al(static_cast<size_t>(g.S) * d.T * 2 * 4);
+  off += al(static_cast<size_t>(g.S_st) * d.T * 2 * 4);
   w.out_part = off;
   off += al(static_cast<size_t>(g.S) * d.T * d.d_model * 4);
   w.tok_part = off;
@@ -673,6 +1039,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   const unsigned grid = static_cast<unsigned>(g.TT * g.S);
+  const unsigned grid_st = static_cast<unsigned>(g.TT * g.S_st);
   // stats
   {
     StatsParams sp{};
@@ -686,7 +1053,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(k.stats),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem))) != hipSuccess)
       return e;
-    hipLaunchKernelGGL(k.stats, dim3(grid), dim3(kThreads), smem, a.stream, sp);
+    hipLaunchKernelGGL(k.stats, dim3(grid_st), dim3(kThreads), smem, a.stream, sp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   // main
@@ -706,12 +1073,12 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     mp.g = g;
     mp.gp = a.gp;
     mp.exp_scale = -d.sharpness * 1.4426950408889634f;
-    const size_t smem = static_cast<size_t>(2 * (KH + KX + 2 * DB)) * kFragBytes;
+    const size_t smem = static_cast<size_t>(k.main_lds);
     if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(k.main),
                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem))) != hipSuccess)
       return e;
     dominant_kernel_begin(a.stream);
-    hipLaunchKernelGGL(k.main, dim3(grid), dim3(kThreads), smem, a.stream, mp);
+    hipLaunchKernelGGL(k.main, dim3(grid), dim3(k.main_threads), smem, a.stream, mp);
     dominant_kernel_end(a.stream);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
