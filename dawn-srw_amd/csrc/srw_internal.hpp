@@ -38,6 +38,20 @@ void dominant_kernel_end(hipStream_t s);
 // Fill kernel (graph-safe replacement for hipMemsetAsync).
 hipError_t fill_f32(float* p, int64_t n, float v, hipStream_t s);
 
+// Pack a bf16 [N, D] matrix unit-contiguous in matrix-core fragment order
+// (32-unit tiles; tail units zero), see srw_mfma.hip.
+hipError_t pack_unit_major(const uint16_t* src, uint16_t* dst, int64_t N, int D, hipStream_t s);
+
+// Gram statistics (SRW_STATS_GRAM), see srw_gram.hip: writes the per-token
+// moment partials mom[gram_moment_parts(dr)][T][2] = (sum s, sum s^2).
+bool gram_supports(int64_t dr);
+int gram_moment_parts(int64_t dr);
+size_t gram_workspace_bytes(int64_t N, int64_t dr);
+// Also zeroes the pass-mask words that two N-splits share (chunk boundaries
+// inside a 32-unit tile of chunk size cs) and the unused half of the last word.
+hipError_t gram_moments(const uint16_t* emb, const uint16_t* h, int64_t T, int64_t N, int64_t dr, float* mom,
+                        char* ws, hipStream_t s, uint32_t* mask32, int64_t words32, int64_t cs, int nc);
+
 // MFMA kernels (bf16 / f32 matrix cores), see srw_mfma.hip.
 size_t mfma_workspace_bytes(const srw_desc_t& d);
 bool mfma_supports(const srw_desc_t& d);

@@ -961,11 +961,12 @@ Geometry geometry(const srw_desc_t& d, int64_t chunk) {
   if (spc_st > min_tiles) spc_st = static_cast<int>(min_tiles > 0 ? min_tiles : 1);
   g.spc_st = spc_st;
   g.S_st = g.nc * spc_st;
+  if (d.stats_mode == SRW_STATS_GRAM) g.S_st = gram_moment_parts(d.d_route);  // moments from the Gram kernels
   return g;
 }
 
 struct WsLayout {
-  size_t wp, mom, out_part, tok_part, total;
+  size_t wp, mom, gram, out_part, tok_part, total;
 };
 
 size_t al(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
@@ -977,6 +978,8 @@ WsLayout ws_layout(const srw_desc_t& d, const Geometry& g) {
   off += al(static_cast<size_t>(g.ntiles) * kUnitTile * d.d_model * 2);
   w.mom = off;
   off += al(static_cast<size_t>(g.S_st) * d.T * 2 * 4);
+  w.gram = off;
+  if (d.stats_mode == SRW_STATS_GRAM) off += al(gram_workspace_bytes(d.n_units, d.d_route));
   w.out_part = off;
   off += al(static_cast<size_t>(g.S) * d.T * d.d_model * 4);
   w.tok_part = off;
@@ -991,8 +994,18 @@ int64_t chunk_of(const srw_desc_t& d) {
 
 }  // namespace
 
+hipError_t pack_unit_major(const uint16_t* src, uint16_t* dst, int64_t N, int D, hipStream_t s) {
+  const int64_t ntiles = (N + kUnitTile - 1) / kUnitTile;
+  const int64_t rows = ntiles * 2 * (D / 32) * 64;
+  int64_t blocks = (rows + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(pack_w_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, src, dst, N, D, rows);
+  return hipGetLastError();
+}
+
 bool mfma_supports(const srw_desc_t& d) {
-  if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41 || d.stats_mode != SRW_STATS_ONEPASS) return false;
+  if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41) return false;
+  if (d.stats_mode != SRW_STATS_ONEPASS && !(d.stats_mode == SRW_STATS_GRAM && gram_supports(d.d_route))) return false;
   if (d.n_routes != 1) return false;
   if (d.flags & (SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
   Kernels k;
@@ -1023,7 +1036,6 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   float* tok_part = reinterpret_cast<float*>(a.ws + L.tok_part);
   const int D = static_cast<int>(d.d_model);
   const int KH = static_cast<int>(d.d_route / 16);
-  const int KX = D / 16;
   const int DB = D / 32;
   uint32_t* mask32 = reinterpret_cast<uint32_t*>(a.o.pass_mask);
   const int64_t mw32 = 2 * a.words;
@@ -1040,8 +1052,11 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   }
   const unsigned grid = static_cast<unsigned>(g.TT * g.S);
   const unsigned grid_st = static_cast<unsigned>(g.TT * g.S_st);
-  // stats
-  {
+  if (d.stats_mode == SRW_STATS_GRAM) {
+    if ((e = gram_moments(static_cast<const uint16_t*>(a.in.emb), static_cast<const uint16_t*>(a.in.h), d.T,
+                          d.n_units, d.d_route, mom, a.ws + L.gram, a.stream, mask32, mw32, g.cs, g.nc)) != hipSuccess)
+      return e;
+  } else {
     StatsParams sp{};
     sp.h = static_cast<const uint16_t*>(a.in.h);
     sp.emb = static_cast<const uint16_t*>(a.in.emb);

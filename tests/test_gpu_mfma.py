@@ -52,7 +52,7 @@ def _oracle(inp, max_chunk):
                                   inp["write"], max_chunk_size=max_chunk, return_trace=True)
 
 
-def _check(got, ref, tr, T, N, D, out_tol=REL_BF16):
+def _check(got, ref, tr, T, N, D, out_tol=REL_BF16, extra_delta=None):
     out_ref = ref[0].reshape(T, D)
     out = got["out"][:, 0].float()
     err = rel_fro(out, out_ref)
@@ -60,11 +60,17 @@ def _check(got, ref, tr, T, N, D, out_tol=REL_BF16):
     assert err <= out_tol
     assert row_rel_max(out, out_ref) <= 5e-2
     den_ref = tr["den"].reshape(T)
-    assert torch.allclose(got["den"][:, 0], den_ref, rtol=2e-4, atol=0)
+    den_tol = 2e-4 * den_ref
+    if extra_delta is not None:
+        # a tau shift moves every active unit's intensity by the same amount
+        den_tol = den_tol + tr["n_active"].reshape(T) * extra_delta.reshape(T)
+    assert bool(((got["den"][:, 0] - den_ref).abs() <= den_tol).all())
     assert torch.allclose(got["gate_sum"][:, 0], tr["gate_sum"].reshape(T), rtol=2e-3, atol=1e-5)
     margin = tr["margin"].reshape(T, N)
     score = margin + tr["tau"].reshape(T, 1) + 0.5
     delta = 2 * bf16_ulp(score) + 1e-4 * tr["s_std"].reshape(T, 1)
+    if extra_delta is not None:
+        delta = delta + extra_delta.reshape(T, 1)
     mask = unpack_mask(got["pass_mask"][:, 0], N)
     n_mis, n_out = check_pass_set(mask, margin, delta)
     print(f"  pass-set mismatches {n_mis} (outside tie band {n_out})", flush=True)
@@ -98,6 +104,52 @@ def test_mfma_matches_fused_oracle(pkg, dev, case):
     assert got["path"] == "mfma_bf16"
     ref, tr = _oracle(inp, max_chunk)
     _check(got, ref, tr, T, N, D)
+
+
+GRAM_CASES = [
+    (256, 384, 384, 2600, True, 1300, 11),
+    (200, 384, 128, 1580, False, 12500, 12),
+    (77, 128, 64, 777, False, 300, 13),
+    (64, 64, 32, 100, False, 2048, 14),
+]
+
+
+@pytest.mark.parametrize("case", GRAM_CASES, ids=lambda c: "T{}D{}dr{}N{}{}c{}".format(
+    c[0], c[1], c[2], c[3], "x" if c[4] else "", c[5]))
+def test_mfma_gram_stats_matches_fused_oracle(pkg, dev, case):
+    """Moments from G = E^T E and sum e (SRW_STATS_GRAM) instead of the score
+    pre-pass: same output and passing-set bar as the one-pass path."""
+    T, D, dr, N, hx, max_chunk, seed = case
+    print(f"[gpu] mfma bf16 gram {case}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, hx, seed)
+    _, cs = srw_ref.chunk_plan(N, max_chunk)
+    got = _gpu(pkg, dev, inp, cs, stats="gram")
+    assert got["path"] == "mfma_bf16"
+    ref, tr = _oracle(inp, max_chunk)
+    # Gram moments are those of the unrounded scores: the tie band widens by
+    # |tau(unrounded scores) - tau(bf16 scores)|, computed here in fp64.
+    h = inp["x"] if "h" not in inp else inp["h"][:, 0]
+    s64 = h.to(torch.bfloat16).double() @ inp["emb"].to(torch.bfloat16).double().T
+    mean = s64.mean(dim=1)
+    std = torch.sqrt((s64 * s64).mean(dim=1) - mean * mean) + 1e-8
+    tau_g = mean + inp["tau_offset"][:, 0].double() * std
+    dtau = (tau_g - tr["tau"].reshape(T).double()).abs().float()
+    print(f"  max |tau_gram - tau_ref| = {float(dtau.max()):.2e}", flush=True)
+    _check(got, ref, tr, T, N, D, extra_delta=2 * dtau + 1e-6)
+
+
+def test_mfma_gram_equals_onepass_closely(pkg, dev):
+    """Gram moments vs the bf16-score pre-pass on the same inputs: den and the
+    outputs agree to well inside the bf16 tolerance."""
+    T, D, dr, N = 512, 384, 384, 6000
+    print(f"[gpu] gram vs onepass T{T} N{N}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, True, seed=17)
+    a = _gpu(pkg, dev, inp, 0, stats="onepass")
+    b = _gpu(pkg, dev, inp, 0, stats="gram")
+    assert rel_fro(b["out"].float(), a["out"].float()) <= 2e-3
+    assert torch.allclose(b["den"], a["den"], rtol=1e-3)  # n_active * |d tau| / den ~ 1e-4
+    mism = (unpack_mask(a["pass_mask"][:, 0], N) != unpack_mask(b["pass_mask"][:, 0], N)).sum()
+    assert int(mism) <= T * N * 1e-4
 
 
 def test_mfma_den_floor(pkg, dev):
