@@ -34,10 +34,13 @@ METRIC = "SRW layer tokens/sec on 1 MI355X (40M Know pool); % bf16 MFMA / HBM pe
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 
-# HBM bytes per launch of the dominant kernel, from rocprofv3 --pmc
-# FETCH_SIZE / WRITE_SIZE runs scaled by a copy kernel of known size; None
-# until measured for the kernel this build ships.
-MEASURED_TRAFFIC = {}
+# HBM bytes per launch of the dominant kernel: rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE (KiB per dispatch) scaled by what the same counters read for a
+# 256 MiB copy (--calibrate-copy 256): FETCH x 2.00, WRITE x 1.00.  Keyed by
+# (workload, stats mode); profiles/know_T4096_N25200_traffic.md has the runs.
+MEASURED_TRAFFIC = {
+    ("know", "onepass"): (42938 * 2.0 + 63612 * 1.0) * 1024,
+}
 
 WORKLOADS = {
     # name: (inputs.CONFIGS key, reference max_chunk_size, note)
@@ -114,6 +117,9 @@ def main() -> int:
                     help="time budget of the CPU baseline (0 skips it)")
     ap.add_argument("--force-generic", action="store_true",
                     help="time the generic (scalar) kernels instead of the MFMA path")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                    help="first run one device-to-device copy of MB MiB (a known-size "
+                         "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -136,6 +142,17 @@ def main() -> int:
     _, cs = pkg.chunk_plan(shape.N, max_chunk)
     log(f"workload {args.workload}: T={shape.T} D={shape.D} dr={shape.dr} N={shape.N} "
         f"R={shape.routes} chunk={cs}")
+
+    if args.calibrate_copy > 0:
+        n = args.calibrate_copy * (1 << 20) // 4
+        # a source no kernel has written, so that its reads come from HBM
+        src = torch.empty(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {args.calibrate_copy} MiB read + {args.calibrate_copy} MiB written")
+        del src, dst
 
     inp = pkg.inputs.make_pool_inputs(shape, seed=args.seed)
     tau_value = -0.5
@@ -184,7 +201,7 @@ def main() -> int:
     T, D, dr, N, R = shape.T, shape.D, shape.dr, shape.N, shape.routes
     flops = 2.0 * T * N * (R * dr + D + R * D)          # score + read (once) + write
     achieved = flops / (kern_ms * 1e-3) / 1e12
-    traffic = MEASURED_TRAFFIC.get((args.workload, plan.path))
+    traffic = MEASURED_TRAFFIC.get((args.workload, args.stats)) if plan.path == "mfma_bf16" else None
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                 "traffic": traffic, "kernel": plan.path,
