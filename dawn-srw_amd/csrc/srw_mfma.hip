@@ -256,9 +256,13 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
 // ---------------------------------------------------------------------------
 // main: fused score / read / gate / write for one (token tile, N-split).
 // ---------------------------------------------------------------------------
+// Rows of the main kernel are "virtual tokens" v = t * routes + r: h, tau,
+// outputs and every partial are indexed by v, x by v / routes (paired QK runs
+// as 2T rows sharing each x row).
 struct MainParams {
-  const uint16_t* x;     // [T, D]
+  const uint16_t* x;     // [T / routes, D]
   const uint16_t* h;     // [T, dr] (== x when HX)
+  int routes;
   const uint16_t* emb;   // [N, dr]
   const uint16_t* read;  // [N, D]
   const uint16_t* wp;    // packed W^T fragments
@@ -305,7 +309,7 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
   u32x4_t xq[KX];
 #pragma unroll
   for (int ks = 0; ks < KX; ++ks)
-    xq[ks] = *reinterpret_cast<const u32x4_t*>(p.x + tl * D + 16 * ks + 8 * half);
+    xq[ks] = *reinterpret_cast<const u32x4_t*>(p.x + (tl / p.routes) * D + 16 * ks + 8 * half);
   u32x4_t hq[HX ? 1 : KH];
   if constexpr (!HX) {
 #pragma unroll
@@ -677,7 +681,7 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
     u32x4_t xq[KX];
 #pragma unroll
     for (int ks = 0; ks < KX; ++ks)
-      xq[ks] = *reinterpret_cast<const u32x4_t*>(p.x + tl * D + 16 * ks + 8 * half);
+      xq[ks] = *reinterpret_cast<const u32x4_t*>(p.x + (tl / p.routes) * D + 16 * ks + 8 * half);
     u32x4_t hq[HX ? 1 : KH];
     if constexpr (!HX) {
 #pragma unroll
@@ -942,11 +946,11 @@ bool pick(int64_t D, int64_t dr, bool hx, Kernels* k) {
 
 Geometry geometry(const srw_desc_t& d, int64_t chunk) {
   Geometry g{};
-  g.T = d.T;
+  g.T = d.T * d.n_routes;  // virtual tokens (token, route)
   g.N = d.n_units;
   g.cs = chunk > 0 && chunk < d.n_units ? chunk : d.n_units;
   g.nc = static_cast<int>((g.N + g.cs - 1) / g.cs);
-  g.TT = static_cast<int>((d.T + kTokTile - 1) / kTokTile);
+  g.TT = static_cast<int>((g.T + kTokTile - 1) / kTokTile);
   g.ntiles = static_cast<int>((g.N + kUnitTile - 1) / kUnitTile);
   // every split needs >= 1 tile: a chunk of L units spans >= L / 32 tiles
   const int64_t last = g.N - (g.nc - 1) * g.cs;
@@ -977,13 +981,13 @@ WsLayout ws_layout(const srw_desc_t& d, const Geometry& g) {
   w.wp = off;
   off += al(static_cast<size_t>(g.ntiles) * kUnitTile * d.d_model * 2);
   w.mom = off;
-  off += al(static_cast<size_t>(g.S_st) * d.T * 2 * 4);
+  off += al(static_cast<size_t>(g.S_st) * g.T * 2 * 4);
   w.gram = off;
   if (d.stats_mode == SRW_STATS_GRAM) off += al(gram_workspace_bytes(d.n_units, d.d_route));
   w.out_part = off;
-  off += al(static_cast<size_t>(g.S) * d.T * d.d_model * 4);
+  off += al(static_cast<size_t>(g.S) * g.T * d.d_model * 4);
   w.tok_part = off;
-  off += al(static_cast<size_t>(g.S) * d.T * 4 * 4);
+  off += al(static_cast<size_t>(g.S) * g.T * 4 * 4);
   w.total = off;
   return w;
 }
@@ -1006,7 +1010,7 @@ hipError_t pack_unit_major(const uint16_t* src, uint16_t* dst, int64_t N, int D,
 bool mfma_supports(const srw_desc_t& d) {
   if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41) return false;
   if (d.stats_mode != SRW_STATS_ONEPASS && !(d.stats_mode == SRW_STATS_GRAM && gram_supports(d.d_route))) return false;
-  if (d.n_routes != 1) return false;
+  if (d.n_routes != 1 && d.n_routes != 2) return false;  // paired QK: 2 rows per token
   if (d.flags & (SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
   Kernels k;
   if (!pick(d.d_model, d.d_route, false, &k)) return false;  // the aliasing variant is optional
@@ -1053,7 +1057,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   const unsigned grid = static_cast<unsigned>(g.TT * g.S);
   const unsigned grid_st = static_cast<unsigned>(g.TT * g.S_st);
   if (d.stats_mode == SRW_STATS_GRAM) {
-    if ((e = gram_moments(static_cast<const uint16_t*>(a.in.emb), static_cast<const uint16_t*>(a.in.h), d.T,
+    if ((e = gram_moments(static_cast<const uint16_t*>(a.in.emb), static_cast<const uint16_t*>(a.in.h), g.T,
                           d.n_units, d.d_route, mom, a.ws + L.gram, a.stream, mask32, mw32, g.cs, g.nc)) != hipSuccess)
       return e;
   } else {
@@ -1075,6 +1079,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   {
     MainParams mp{};
     mp.x = static_cast<const uint16_t*>(a.in.x);
+    mp.routes = d.n_routes;
     mp.h = static_cast<const uint16_t*>(a.in.h);
     mp.emb = static_cast<const uint16_t*>(a.in.emb);
     mp.read = static_cast<const uint16_t*>(a.in.read);
@@ -1106,12 +1111,12 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     fp.gate_sum = a.o.gate_sum;
     fp.den = a.o.den;
     fp.n_active = a.o.n_active;
-    fp.T = d.T;
+    fp.T = g.T;
     fp.D = D;
     fp.S = g.S;
     fp.spc = g.spc;
     fp.scale = d.scale;
-    int64_t blocks = (d.T * D + 255) / 256;
+    int64_t blocks = (g.T * D + 255) / 256;
     if (blocks > 16384) blocks = 16384;
     hipLaunchKernelGGL(srw_finalize_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, a.stream, fp);
     if ((e = hipGetLastError()) != hipSuccess) return e;

@@ -152,6 +152,58 @@ def test_mfma_gram_equals_onepass_closely(pkg, dev):
     assert int(mism) <= T * N * 1e-4
 
 
+PAIRED_CASES = [
+    # T, D, dr, N, max_chunk, seed
+    (128, 384, 128, 1580, 12500, 21),   # the 40M QK pool with the router's d_route
+    (100, 384, 384, 700, 12500, 22),    # configs[1] d_route = d_model, ragged T and N
+    (70, 128, 64, 777, 300, 23),        # three reference chunks
+]
+
+
+@pytest.mark.parametrize("case", PAIRED_CASES, ids=lambda c: "T{}D{}dr{}N{}c{}".format(*c[:5]))
+def test_mfma_paired_matches_fused_paired_oracle(pkg, dev, case):
+    """Paired QK routes (fused_gate_srw_paired, v41:640-909) on the matrix cores."""
+    T, D, dr, N, max_chunk, seed = case
+    print(f"[gpu] mfma bf16 paired {case}", flush=True)
+    shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=2)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=seed)
+    _, cs = srw_ref.chunk_plan(N, max_chunk)
+    got = _gpu(pkg, dev, inp, cs)
+    assert got["path"] == "mfma_bf16"
+    ref, tr = srw_ref.fused_gate_srw_paired(
+        inp["x"][None], inp["h"][None], inp["emb"], inp["tau_offset"].reshape(1, T, 2, 1),
+        inp["read"], inp["write"], max_chunk_size=max_chunk, return_trace=True)
+    # rows are (token, route) pairs: check them as 2T single-route rows
+    flat = dict(margin=tr["margin"].reshape(2 * T, N), tau=tr["tau"].reshape(2 * T, 1),
+                s_std=tr["s_std"].reshape(2 * T, 1), den=tr["den"].reshape(2 * T),
+                gate_sum=tr["gate_sum"].reshape(2 * T), n_active=tr["n_active"].reshape(2 * T))
+    got2 = {k: (v.reshape(2 * T, *v.shape[2:]) if isinstance(v, torch.Tensor) and v.dim() >= 2
+                and v.shape[:2] == (T, 2) else v) for k, v in got.items()}
+    got2 = {k: (v[:, None] if isinstance(v, torch.Tensor) and k in ("out", "gate_sum", "den",
+                                                                     "n_active", "pass_mask") else v)
+            for k, v in got2.items()}
+    _check(got2, (ref[0].reshape(2 * T, D),), flat, 2 * T, N, D)
+
+
+def test_mfma_paired_equals_two_singles(pkg, dev):
+    """paired(Q, K) == (single(Q), single(K)) on the same pool (v41:796-797)."""
+    T, D, dr, N = 96, 384, 128, 1580
+    print(f"[gpu] paired vs two singles T{T} N{N}", flush=True)
+    shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=2)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=31)
+    both = _gpu(pkg, dev, inp, 0)
+    for r in range(2):
+        one = dict(inp, h=inp["h"][:, r:r + 1].contiguous(), tau_offset=inp["tau_offset"][:, r:r + 1].contiguous())
+        single = _gpu(pkg, dev, one, 0)
+        assert single["path"] == "mfma_bf16"
+        assert rel_fro(both["out"][:, r].float(), single["out"][:, 0].float()) <= 1e-3
+        # different N-split geometry -> fp32 summation order differs; only
+        # units within rounding of the threshold may flip
+        mism = (unpack_mask(both["pass_mask"][:, r], N) != unpack_mask(single["pass_mask"][:, 0], N)).sum()
+        assert int(mism) <= 4
+        assert torch.allclose(both["den"][:, r], single["den"][:, 0], rtol=1e-5)
+
+
 def test_mfma_den_floor(pkg, dev):
     """A high tau_offset on a V-sized pool: sum intensity < 1, den floors at 1."""
     T, D, dr, N = 64, 384, 384, 2600
