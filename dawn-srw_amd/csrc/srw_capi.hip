@@ -28,7 +28,8 @@ srw_status_t validate(const srw_desc_t* d) {
   if (!isfinite(d->sharpness) || !isfinite(d->act_threshold) || !isfinite(d->act_cutoff) ||
       !isfinite(d->epsilon) || !isfinite(d->max_intensity) || !isfinite(d->scale))
     return SRW_EINVAL;
-  if (d->flags & ~(SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_SPARSE_SKIP | SRW_FLAG_NO_FAST)) return SRW_EINVAL;
+  if (d->flags & ~(SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_SPARSE_SKIP | SRW_FLAG_NO_FAST | SRW_FLAG_POOL_CACHED))
+    return SRW_EINVAL;
   return SRW_OK;
 }
 

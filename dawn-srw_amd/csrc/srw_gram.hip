@@ -283,7 +283,8 @@ size_t gram_workspace_bytes(int64_t N, int64_t dr) {
 }
 
 hipError_t gram_moments(const uint16_t* emb, const uint16_t* h, int64_t T, int64_t N, int64_t dr, float* mom,
-                        char* ws, hipStream_t s, uint32_t* mask32, int64_t words32, int64_t cs, int nc) {
+                        char* ws, hipStream_t s, uint32_t* mask32, int64_t words32, int64_t cs, int nc,
+                        bool pool_cached) {
   const int64_t ntiles = (N + 31) / 32;
   const int DBr = static_cast<int>(dr / 32);
   char* p = ws;
@@ -297,31 +298,33 @@ hipError_t gram_moments(const uint16_t* emb, const uint16_t* h, int64_t T, int64
   p += al(static_cast<size_t>(dr) * dr * 2 * 2);
   float* esum = reinterpret_cast<float*>(p);
   hipError_t e;
-  if ((e = pack_unit_major(emb, ep, N, static_cast<int>(dr), s)) != hipSuccess) return e;
+  GramMaskPrep mp{mask32, words32, cs, nc, static_cast<int>(ntiles)};
+  if (!pool_cached) {  // else G and esum of this pool are already in the workspace
+    if ((e = pack_unit_major(emb, ep, N, static_cast<int>(dr), s)) != hipSuccess) return e;
 
-  GramParams gpp{};
-  gpp.ep = ep;
-  gpp.gpart = gpart;
-  gpp.epart = epart;
-  gpp.ntiles = static_cast<int>(ntiles);
-  gpp.DBr = DBr;
-  gpp.RB = DBr >= 4 ? 4 : DBr;
-  gpp.KS = kGramSplits;
-  const int NR = DBr / gpp.RB, NU = NR * (NR + 1) / 2;
-  const size_t smem = static_cast<size_t>(2 * 4 * gpp.RB) * kFragBytes;
-  if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(gram_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               static_cast<int>(smem))) != hipSuccess)
-    return e;
-  hipLaunchKernelGGL(gram_kernel, dim3(static_cast<unsigned>(NU * kGramSplits)), dim3(256), smem, s, gpp);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+    GramParams gpp{};
+    gpp.ep = ep;
+    gpp.gpart = gpart;
+    gpp.epart = epart;
+    gpp.ntiles = static_cast<int>(ntiles);
+    gpp.DBr = DBr;
+    gpp.RB = DBr >= 4 ? 4 : DBr;
+    gpp.KS = kGramSplits;
+    const int NR = DBr / gpp.RB, NU = NR * (NR + 1) / 2;
+    const size_t smem = static_cast<size_t>(2 * 4 * gpp.RB) * kFragBytes;
+    if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(gram_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 static_cast<int>(smem))) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(gram_kernel, dim3(static_cast<unsigned>(NU * kGramSplits)), dim3(256), smem, s, gpp);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
 
-  int64_t blocks = (dr * dr + 255) / 256;
-  hipLaunchKernelGGL(gram_reduce_kernel<kGramSplits>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, gpart,
-                     epart, gp, esum, static_cast<int>(dr), gpp.RB);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+    int64_t blocks = (dr * dr + 255) / 256;
+    hipLaunchKernelGGL(gram_reduce_kernel<kGramSplits>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, gpart,
+                       epart, gp, esum, static_cast<int>(dr), gpp.RB);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
 
   const unsigned mblocks = static_cast<unsigned>(((T + 127) / 128) * DBr);
-  GramMaskPrep mp{mask32, words32, cs, nc, static_cast<int>(ntiles)};
   switch (dr) {
     case 384: hipLaunchKernelGGL(gram_mom_kernel<24>, dim3(mblocks), dim3(256), 0, s, h, gp, esum, mom, T, mp); break;
     case 128: hipLaunchKernelGGL(gram_mom_kernel<8>, dim3(mblocks), dim3(256), 0, s, h, gp, esum, mom, T, mp); break;

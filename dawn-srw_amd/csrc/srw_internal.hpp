@@ -49,8 +49,10 @@ int gram_moment_parts(int64_t dr);
 size_t gram_workspace_bytes(int64_t N, int64_t dr);
 // Also zeroes the pass-mask words that two N-splits share (chunk boundaries
 // inside a 32-unit tile of chunk size cs) and the unused half of the last word.
+// pool_cached: G and esum of this pool are already in `ws` from an earlier call.
 hipError_t gram_moments(const uint16_t* emb, const uint16_t* h, int64_t T, int64_t N, int64_t dr, float* mom,
-                        char* ws, hipStream_t s, uint32_t* mask32, int64_t words32, int64_t cs, int nc);
+                        char* ws, hipStream_t s, uint32_t* mask32, int64_t words32, int64_t cs, int nc,
+                        bool pool_cached);
 
 // MFMA kernels (bf16 / f32 matrix cores), see srw_mfma.hip.
 size_t mfma_workspace_bytes(const srw_desc_t& d);

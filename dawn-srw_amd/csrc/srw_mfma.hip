@@ -266,8 +266,7 @@ struct MainParams {
   const uint16_t* emb;   // [N, dr]
   const uint16_t* read;  // [N, D]
   const uint16_t* wp;    // packed W^T fragments
-  const float* tau_off;  // [T]
-  const float* mom;      // [S][T][2]
+  const float* tau;      // [T] thresholds (srw_tau_kernel)
   float* out_part;       // [S][T][D]
   float* tok_part;       // [S][T][4]: sum gate, sum intensity, active count, -
   uint32_t* mask32;      // [T][mask_words32] or null
@@ -317,20 +316,7 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
       hq[ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl * DR + 16 * ks + 8 * half);
   }
 
-  // tau = mean + tau_offset * (sqrt(E[s^2] - mean^2) + 1e-8)   (v41:461-464)
-  float tau;
-  {
-    float a = 0.f, b = 0.f;
-    for (int s = 0; s < p.g.S_st; ++s) {
-      const float* m = p.mom + (static_cast<int64_t>(s) * p.g.T + tl) * 2;
-      a += m[0];
-      b += m[1];
-    }
-    const float fN = static_cast<float>(p.g.N);
-    const float mean = a / fN;
-    const float sd = sqrtf(b / fN - __fmul_rn(mean, mean)) + 1e-8f;
-    tau = mean + __fmul_rn(p.tau_off[tl], sd);
-  }
+  const float tau = p.tau[tl];  // srw_tau_kernel (v41:461-464)
   const GateParams gp = p.gp;
 
   f32x16_t oacc[DB];
@@ -693,23 +679,17 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
     //   margin = s - tau - thr,  exp argument = margin * c  (c = -sharpness log2 e)
     float k_exp, tau_cut;
     {
-      float a = 0.f, b = 0.f;
-      for (int s = 0; s < p.g.S_st; ++s) {
-        const float* m = p.mom + (static_cast<int64_t>(s) * p.g.T + tl) * 2;
-        a += m[0];
-        b += m[1];
-      }
-      const float fN = static_cast<float>(p.g.N);
-      const float mean = a / fN;
-      const float sd = sqrtf(b / fN - __fmul_rn(mean, mean)) + 1e-8f;
-      const float tau = mean + __fmul_rn(p.tau_off[tl], sd);
-      const float tau_thr = tau + p.gp.thr;
+      const float tau_thr = p.tau[tl] + p.gp.thr;
       k_exp = -tau_thr * p.exp_scale;
       tau_cut = tau_thr + p.gp.cut;
     }
     const float c_exp = p.exp_scale, eps = p.gp.eps, maxi = p.gp.maxi;
     float gsum = 0.f, isum = 0.f;
     uint32_t nact = 0;
+    // Drain the x / h / tau loads here: left pending into the tile loop, they
+    // make the compiler wait for every load in flight (the next tile's LDS
+    // prefetch included) at the top of each iteration.
+    wait_vm0();
 
     // gate epilogue (v41:503-518) of one tile; P goes to LDS as the consumer's
     // A operand (k-step j at [blk][j][lane]); returns pass bits (v at 15 - v)
@@ -861,8 +841,35 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
 }
 
 // ---------------------------------------------------------------------------
+// tau: per row, the moment partials -> tau = mean + tau_offset * (sqrt(E[s^2]
+// - mean^2) + 1e-8) (v41:461-464).  One wave per row; lanes split the partials.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void srw_tau_kernel(const float* __restrict__ mom, const float* __restrict__ tau_off,
+                                                      float* __restrict__ tau, int64_t T, int S_st, int64_t N) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float a = 0.f, b = 0.f;
+  for (int s = lane; s < S_st; s += 64) {
+    const float* m = mom + (static_cast<int64_t>(s) * T + t) * 2;
+    a += m[0];
+    b += m[1];
+  }
+  a = wave_sum(a);
+  b = wave_sum(b);
+  if (lane == 0) {
+    const float fN = static_cast<float>(N);
+    const float mean = a / fN;
+    const float sd = sqrtf(b / fN - __fmul_rn(mean, mean)) + 1e-8f;
+    tau[t] = mean + __fmul_rn(tau_off[t], sd);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // finalize: reduce the N-splits, bf16-round each reference chunk's write GEMM,
-// divide by den, round, scale.
+// divide by den, round, scale.  One workgroup per row: the per-token partials
+// are reduced once, then each thread sums its columns over the splits with
+// eight independent loads in flight.
 // ---------------------------------------------------------------------------
 struct FinalParams {
   const float* out_part;
@@ -877,32 +884,51 @@ struct FinalParams {
 };
 
 __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
-  const int64_t total = p.T * p.D;
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t t = i / p.D;
-    const int d = static_cast<int>(i - t * p.D);
-    float isum = 0.f;
-    for (int s = 0; s < p.S; ++s) isum += p.tok_part[(s * p.T + t) * 4 + 1];
-    const float den = fmaxf(isum, 1.0f);                    // v41:584
+  __shared__ float red[3][4];
+  const int64_t t = blockIdx.x;
+  const int tid = threadIdx.x;
+  float gs = 0.f, is = 0.f, na = 0.f;
+  for (int s = tid; s < p.S; s += 256) {
+    const float* tp = p.tok_part + (static_cast<int64_t>(s) * p.T + t) * 4;
+    gs += tp[0];
+    is += tp[1];
+    na += tp[2];
+  }
+  gs = wave_sum(gs);
+  is = wave_sum(is);
+  na = wave_sum(na);
+  if ((tid & 63) == 0) {
+    red[0][tid >> 6] = gs;
+    red[1][tid >> 6] = is;
+    red[2][tid >> 6] = na;
+  }
+  __syncthreads();
+  const float G = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+  const float I = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  const float NA = red[2][0] + red[2][1] + red[2][2] + red[2][3];
+  const float den = fmaxf(I, 1.0f);                          // v41:584
+  const int64_t stride = p.T * p.D;
+  for (int d = tid; d < p.D; d += 256) {
+    const float* col = p.out_part + t * p.D + d;
     float raw = 0.f;
     for (int s0 = 0; s0 < p.S; s0 += p.spc) {                // one reference chunk
-      float c = 0.f;
-      for (int s = s0; s < s0 + p.spc; ++s) c += p.out_part[(s * p.T + t) * p.D + d];
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      int s = s0;
+      for (; s + 8 <= s0 + p.spc; s += 8) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += col[(s + j) * stride];
+      }
+      for (; s < s0 + p.spc; ++s) acc[0] += col[s * stride];
+      const float c = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
       raw += round_bf16(c);                                  // bf16 dot output (v41:518)
     }
     const float o = round_bf16(raw / den);                  // v41:585-586
-    p.out[i] = f32_to_bf16_bits(o * p.scale);
-    if (d == 0) {
-      float gs = 0.f, na = 0.f;
-      for (int s = 0; s < p.S; ++s) {
-        gs += p.tok_part[(s * p.T + t) * 4 + 0];
-        na += p.tok_part[(s * p.T + t) * 4 + 2];
-      }
-      if (p.gate_sum) p.gate_sum[t] = gs;
-      if (p.den) p.den[t] = den;
-      if (p.n_active) p.n_active[t] = static_cast<int32_t>(na);
-    }
+    p.out[t * p.D + d] = f32_to_bf16_bits(o * p.scale);
+  }
+  if (tid == 0) {
+    if (p.gate_sum) p.gate_sum[t] = G;
+    if (p.den) p.den[t] = den;
+    if (p.n_active) p.n_active[t] = static_cast<int32_t>(NA);
   }
 }
 
@@ -970,7 +996,7 @@ Geometry geometry(const srw_desc_t& d, int64_t chunk) {
 }
 
 struct WsLayout {
-  size_t wp, mom, gram, out_part, tok_part, total;
+  size_t wp, mom, tau, gram, out_part, tok_part, total;
 };
 
 size_t al(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
@@ -982,6 +1008,8 @@ WsLayout ws_layout(const srw_desc_t& d, const Geometry& g) {
   off += al(static_cast<size_t>(g.ntiles) * kUnitTile * d.d_model * 2);
   w.mom = off;
   off += al(static_cast<size_t>(g.S_st) * g.T * 2 * 4);
+  w.tau = off;
+  off += al(static_cast<size_t>(g.T) * 4);
   w.gram = off;
   if (d.stats_mode == SRW_STATS_GRAM) off += al(gram_workspace_bytes(d.n_units, d.d_route));
   w.out_part = off;
@@ -1045,8 +1073,11 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   const int64_t mw32 = 2 * a.words;
   hipError_t e;
 
-  // pack W^T
-  {
+  float* tau = reinterpret_cast<float*>(a.ws + L.tau);
+  const bool cached = (d.flags & SRW_FLAG_POOL_CACHED) != 0;
+
+  // pack W^T (kept in the workspace across calls that declare the pool cached)
+  if (!cached) {
     const int64_t rows = static_cast<int64_t>(g.ntiles) * 2 * DB * 64;
     int64_t blocks = (rows + 255) / 256;
     if (blocks > 8192) blocks = 8192;
@@ -1058,7 +1089,8 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   const unsigned grid_st = static_cast<unsigned>(g.TT * g.S_st);
   if (d.stats_mode == SRW_STATS_GRAM) {
     if ((e = gram_moments(static_cast<const uint16_t*>(a.in.emb), static_cast<const uint16_t*>(a.in.h), g.T,
-                          d.n_units, d.d_route, mom, a.ws + L.gram, a.stream, mask32, mw32, g.cs, g.nc)) != hipSuccess)
+                          d.n_units, d.d_route, mom, a.ws + L.gram, a.stream, mask32, mw32, g.cs, g.nc,
+                          cached)) != hipSuccess)
       return e;
   } else {
     StatsParams sp{};
@@ -1075,6 +1107,10 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     hipLaunchKernelGGL(k.stats, dim3(grid_st), dim3(kThreads), smem, a.stream, sp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
+  // tau per row from the moment partials
+  hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((g.T + 3) / 4)), dim3(256), 0, a.stream, mom,
+                     a.in.tau_offset, tau, g.T, g.S_st, g.N);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
   // main
   {
     MainParams mp{};
@@ -1084,8 +1120,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     mp.emb = static_cast<const uint16_t*>(a.in.emb);
     mp.read = static_cast<const uint16_t*>(a.in.read);
     mp.wp = wp;
-    mp.tau_off = a.in.tau_offset;
-    mp.mom = mom;
+    mp.tau = tau;
     mp.out_part = out_part;
     mp.tok_part = tok_part;
     mp.mask32 = mask32;
@@ -1116,9 +1151,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     fp.S = g.S;
     fp.spc = g.spc;
     fp.scale = d.scale;
-    int64_t blocks = (g.T * D + 255) / 256;
-    if (blocks > 16384) blocks = 16384;
-    hipLaunchKernelGGL(srw_finalize_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, a.stream, fp);
+    hipLaunchKernelGGL(srw_finalize_kernel, dim3(static_cast<unsigned>(g.T)), dim3(256), 0, a.stream, fp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return hipSuccess;

@@ -137,15 +137,29 @@ class SrwPlan:
         self._lib = C.load_library()
         self.path = None
 
-    def launch(self, stream=None) -> None:
-        """Enqueue the call on ``stream`` (default: torch's current stream)."""
+    def launch(self, stream=None, pool_cached: bool = False) -> None:
+        """Enqueue the call on ``stream`` (default: torch's current stream).
+
+        ``pool_cached=True`` declares that ``emb``, ``read`` and ``write`` are
+        unchanged since this plan's previous launch (decode steps over one
+        pool): the pool-derived data kept in the workspace (packed W^T, Gram
+        statistics) is reused instead of rebuilt.
+        """
         if stream is None:
             with torch.cuda.device(self.device):
                 stream = torch.cuda.current_stream(self.device)
-        C.check(self._lib.srw_forward(
-            ctypes.byref(self._desc), ctypes.byref(self._tens), ctypes.byref(self._outs),
-            _ptr(self.workspace), ctypes.c_size_t(self.ws_bytes),
-            ctypes.c_void_p(stream.cuda_stream)))
+        if pool_cached and self.path is None:
+            raise ValueError("pool_cached needs an earlier launch of this plan")
+        base = self._desc.flags
+        if pool_cached:
+            self._desc.flags = base | C.SRW_FLAG_POOL_CACHED
+        try:
+            C.check(self._lib.srw_forward(
+                ctypes.byref(self._desc), ctypes.byref(self._tens), ctypes.byref(self._outs),
+                _ptr(self.workspace), ctypes.c_size_t(self.ws_bytes),
+                ctypes.c_void_p(stream.cuda_stream)))
+        finally:
+            self._desc.flags = base
         self.path = C.last_path()
 
     def results(self) -> dict:

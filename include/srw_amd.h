@@ -91,6 +91,12 @@ typedef enum srw_stats_mode {
 #define SRW_FLAG_SPARSE_SKIP 0x4u /* skip read/write rows of units no token of a tile passes
                                      (exact for the v4.0.1 gate; bounded error for v4.1) */
 #define SRW_FLAG_NO_FAST 0x8u     /* force the generic kernels (testing) */
+#define SRW_FLAG_POOL_CACHED 0x10u /* emb, read and write are unchanged since the last call
+                                      that used this workspace with the same descriptor:
+                                      reuse the packed W^T and Gram statistics kept in the
+                                      workspace (decode steps, layers sharing one pool).
+                                      No counterpart in the reference, which recasts its
+                                      pools on every call (v41:423-430). */
 
 typedef struct srw_desc {
   int64_t T;          /* tokens (B*S) */

@@ -105,11 +105,13 @@ def test_workspace_sizes(C):
     # generic kernels: no workspace for the v4.1 gate
     assert C.workspace_size(_desc(C, flags=C.SRW_FLAG_NO_FAST)) == 0
     # matrix-core path (T=16, D=64, dr=32, N=100): packed W^T of ceil(N/32)
-    # tiles, and per-N-split moments / partial out / per-token partials for
-    # S = 3 splits (one 128-token tile, a split per 32-unit tile, 3 whole tiles)
+    # tiles, per-N-split moments, per-token tau, and partial out / per-token
+    # partials for S = 3 splits (one 128-token tile, a split per 32-unit tile,
+    # 3 whole tiles)
     al = lambda b: (b + 255) // 256 * 256  # noqa: E731
     S, T, D = 3, 16, 64
-    want = al(4 * 32 * D * 2) + al(S * T * 2 * 4) + al(S * T * D * 4) + al(S * T * 4 * 4)
+    want = (al(4 * 32 * D * 2) + al(S * T * 2 * 4) + al(T * 4) + al(S * T * D * 4)
+            + al(S * T * 4 * 4))
     assert C.workspace_size(_desc(C)) == want
     d = _desc(C, gate=C.SRW_GATE_GELU_V401)      # forward-normalised R and W copies (bf16)
     assert C.workspace_size(d) == 2 * 100 * 64 * 2

@@ -52,6 +52,20 @@ def _oracle(inp, max_chunk):
                                   inp["write"], max_chunk_size=max_chunk, return_trace=True)
 
 
+def _gram_delta(inp, tr):
+    """Gram moments are those of the unrounded scores: the tie band widens by
+    |tau(unrounded scores) - tau(bf16 scores)|, computed here in fp64."""
+    T = inp["x"].shape[0]
+    h = inp["x"] if "h" not in inp else inp["h"][:, 0]
+    s64 = h.to(torch.bfloat16).double() @ inp["emb"].to(torch.bfloat16).double().T
+    mean = s64.mean(dim=1)
+    std = torch.sqrt((s64 * s64).mean(dim=1) - mean * mean) + 1e-8
+    tau_g = mean + inp["tau_offset"][:, 0].double() * std
+    dtau = (tau_g - tr["tau"].reshape(T).double()).abs().float()
+    print(f"  max |tau_gram - tau_ref| = {float(dtau.max()):.2e}", flush=True)
+    return 2 * dtau + 1e-6
+
+
 def _check(got, ref, tr, T, N, D, out_tol=REL_BF16, extra_delta=None):
     out_ref = ref[0].reshape(T, D)
     out = got["out"][:, 0].float()
@@ -126,16 +140,7 @@ def test_mfma_gram_stats_matches_fused_oracle(pkg, dev, case):
     got = _gpu(pkg, dev, inp, cs, stats="gram")
     assert got["path"] == "mfma_bf16"
     ref, tr = _oracle(inp, max_chunk)
-    # Gram moments are those of the unrounded scores: the tie band widens by
-    # |tau(unrounded scores) - tau(bf16 scores)|, computed here in fp64.
-    h = inp["x"] if "h" not in inp else inp["h"][:, 0]
-    s64 = h.to(torch.bfloat16).double() @ inp["emb"].to(torch.bfloat16).double().T
-    mean = s64.mean(dim=1)
-    std = torch.sqrt((s64 * s64).mean(dim=1) - mean * mean) + 1e-8
-    tau_g = mean + inp["tau_offset"][:, 0].double() * std
-    dtau = (tau_g - tr["tau"].reshape(T).double()).abs().float()
-    print(f"  max |tau_gram - tau_ref| = {float(dtau.max()):.2e}", flush=True)
-    _check(got, ref, tr, T, N, D, extra_delta=2 * dtau + 1e-6)
+    _check(got, ref, tr, T, N, D, extra_delta=_gram_delta(inp, tr))
 
 
 def test_mfma_gram_equals_onepass_closely(pkg, dev):
@@ -251,3 +256,36 @@ def test_mfma_full_know_config(pkg, dev):
     assert 0.45 < frac < 0.55, frac
     assert bool((got["den"] >= shape.N * 1e-4).all())
     assert bool(torch.isfinite(got["out"].float()).all())
+
+
+@pytest.mark.parametrize("stats", ["onepass", "gram"])
+def test_mfma_pool_cached_reuses_pool_data(pkg, dev, stats):
+    """Decode-style steps over one pool: a plan launched once, then fed new
+    tokens in place and launched with pool_cached=True (packed W^T and Gram
+    statistics reused from the workspace), gives exactly what a fresh call
+    on the new tokens gives."""
+    T, D, dr, N = 64, 384, 384, 6100
+    print(f"[gpu] mfma pool cached {stats} T{T} N{N}", flush=True)
+    _, cs = srw_ref.chunk_plan(N, 2500)
+    a = _inputs(pkg, T, D, dr, N, True, seed=31)
+    b = _inputs(pkg, T, D, dr, N, True, seed=32)
+    b.update(emb=a["emb"], read=a["read"], write=a["write"])
+    b["tau_offset"].uniform_(-0.8, 0.2)
+    x = a["x"].to(BF).to(dev)
+    plan = pkg.SrwPlan(x, x, a["emb"].to(BF).to(dev), a["tau_offset"].to(dev),
+                       a["read"].to(BF).to(dev), a["write"].to(BF).to(dev), stats=stats,
+                       chunk_size=cs)
+    plan.launch()
+    first = plan.out.clone()
+    plan.inputs[0].copy_(b["x"].to(BF))
+    plan.inputs[3].copy_(b["tau_offset"])
+    plan.launch(pool_cached=True)
+    torch.cuda.synchronize()
+    assert plan.path == "mfma_bf16"
+    fresh = _gpu(pkg, dev, b, cs, stats=stats)
+    assert torch.equal(plan.out.cpu(), fresh["out"])
+    assert torch.equal(plan.den.cpu(), fresh["den"])
+    assert torch.equal(plan.pass_mask.cpu(), fresh["pass_mask"])
+    assert not torch.equal(first.cpu(), fresh["out"])
+    ref, tr = _oracle(b, 2500)
+    _check(fresh, ref, tr, T, N, D, extra_delta=_gram_delta(b, tr) if stats == "gram" else None)
