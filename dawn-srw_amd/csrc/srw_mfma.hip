@@ -77,6 +77,36 @@ __device__ inline void g2lds16(const void* g, char* lds) {
 
 __device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
+// A 32-row tile of a row-major bf16 [rows, K] array (E or R), staged in LDS
+// as K / 16 one-KB blocks.  Load block j moves whole 128-byte lines (8 rows x
+// 128 B; 16 rows x 64 B when K = 32): a wave load that touches 32 B of each of
+// 32 rows costs the texture path four times the line requests and halves the
+// global->LDS rate.  The 16-byte pieces of each row are XOR-swizzled by row,
+// so that the MFMA fragment reads (32 rows x 32 B) are free of bank conflicts.
+template <int KF>  // K / 16: MFMA k-steps per row
+struct RowTile {
+  static constexpr int K = KF * 16;
+  static constexpr int PPR = KF * 2 < 8 ? KF * 2 : 8;  // 16-B pieces of a row per block
+  static constexpr int RPI = 64 / PPR;                 // rows per block
+  static constexpr int RG = 32 / RPI;                  // row groups
+  static constexpr int NM = PPR / 2;                   // k-steps per block row
+  __device__ static int swz(int r) { return (r / (8 / PPR)) % PPR; }
+  // load block j of the tile whose first row is row0 (rows past `rows` read the last one)
+  __device__ static void load(const uint16_t* a, int64_t row0, int64_t rows, int j, int lane, char* tile) {
+    const int r = RPI * (j % RG) + lane / PPR;
+    const int c = 8 * ((j / RG) * PPR + ((lane % PPR) ^ swz(r)));
+    const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
+    g2lds16(a + row * K + c, tile + j * kFragBytes);
+  }
+  // LDS byte offset of the 16 B that `lane` feeds to MFMA k-step ks:
+  // lane_off(lane, ks % NM) + step_off(ks)
+  __device__ static int lane_off(int lane, int m) {
+    const int u = lane & 31, h = lane >> 5;
+    return (u / RPI) * kFragBytes + (PPR * (u % RPI) + ((2 * m + h) ^ swz(u))) * 16;
+  }
+  static constexpr int step_off(int ks) { return (ks / NM) * RG * kFragBytes; }
+};
+
 // Unit (within a 32-unit tile) carried by k index 8*half + i of k-step j of
 // the write GEMM: the accumulator row of score-GEMM register v = 8 j + i.
 __host__ __device__ inline int unit_of_k(int j, int half, int i) {
@@ -196,12 +226,14 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
   for (int ks = 0; ks < KH; ++ks)
     hq[ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl * DR + 16 * ks + 8 * half);
 
+  using TileE = RowTile<KH>;
   auto issue = [&](int tile, int stage) {
-    const int64_t u = static_cast<int64_t>(tile) * kUnitTile + col;
-    const int64_t row = u < p.g.N ? u : p.g.N - 1;
-    for (int f = wave; f < KH; f += 4)
-      g2lds16(p.emb + row * DR + 16 * f + 8 * half, lds + stage * STAGE + f * kFragBytes);
+    for (int j = wave; j < KH; j += 4)
+      TileE::load(p.emb, static_cast<int64_t>(tile) * kUnitTile, p.g.N, j, lane, lds + stage * STAGE);
   };
+  int le[TileE::NM];
+#pragma unroll
+  for (int m = 0; m < TileE::NM; ++m) le[m] = TileE::lane_off(lane, m);
 
   float s1 = 0.f, s2 = 0.f;
   if (ta < tb) {
@@ -213,16 +245,19 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
     const int st = (tile - ta) & 1;
     if (tile + 1 < tb) issue(tile + 1, st ^ 1);
     f32x16_t acc = {};
-    const char* base = lds + st * STAGE + lane * 16;
+    const char* base = lds + st * STAGE;
+    auto frag = [&](int ks) {
+      return *reinterpret_cast<const u32x4_t*>(base + le[ks % TileE::NM] + TileE::step_off(ks));
+    };
     constexpr int PF = 4;
     u32x4_t ef[PF];
 #pragma unroll
     for (int g = 0; g < PF; ++g)
-      if (g < KH) ef[g] = *reinterpret_cast<const u32x4_t*>(base + g * kFragBytes);
+      if (g < KH) ef[g] = frag(g);
 #pragma unroll
     for (int ks = 0; ks < KH; ++ks) {
       const u32x4_t e = ef[ks % PF];
-      if (ks + PF < KH) ef[ks % PF] = *reinterpret_cast<const u32x4_t*>(base + (ks + PF) * kFragBytes);
+      if (ks + PF < KH) ef[ks % PF] = frag(ks + PF);
       acc = mfma(e, hq[ks], acc);
     }
     const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
@@ -328,23 +363,36 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
   char* const er_base = lds;
   char* const w_base = lds + 2 * ER_STAGE;
 
-  // Direct global->LDS loads: wave w issues fragments w, w+4, ... of a group.
+  // Direct global->LDS loads: wave w issues blocks w, w+4, ... of a group.
+  using TileE = RowTile<KH>;
+  using TileR = RowTile<KX>;
   auto issue_er = [&](int tile, int stage) {
     char* sb = er_base + stage * ER_STAGE;
-    const int64_t u = static_cast<int64_t>(tile) * kUnitTile + col;
-    const int64_t row = u < p.g.N ? u : p.g.N - 1;
-    const uint16_t* esrc = p.emb + row * DR + 8 * half;
-    const uint16_t* rsrc = p.read + row * D + 8 * half;
+    const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
 #pragma unroll
     for (int q = 0; q < (F_E + 3) / 4; ++q) {
       const int f = wave + 4 * q;
-      if (f < F_E) g2lds16(esrc + 16 * f, sb + f * kFragBytes);
+      if (f < F_E) TileE::load(p.emb, u0, p.g.N, f, lane, sb);
     }
 #pragma unroll
     for (int q = 0; q < (F_R + 3) / 4; ++q) {
       const int f = wave + 4 * q;
-      if (f < F_R) g2lds16(rsrc + 16 * f, sb + (F_E + f) * kFragBytes);
+      if (f < F_R) TileR::load(p.read, u0, p.g.N, f, lane, sb + F_E * kFragBytes);
     }
+  };
+  // LDS offsets of this lane's E / R fragment pieces (see RowTile)
+  int le[TileE::NM], lr[TileR::NM];
+#pragma unroll
+  for (int m = 0; m < TileE::NM; ++m) le[m] = TileE::lane_off(lane, m);
+#pragma unroll
+  for (int m = 0; m < TileR::NM; ++m) lr[m] = F_E * kFragBytes + TileR::lane_off(lane, m);
+  // operand of MFMA k of phase A: HX interleaves score (even k) and read (odd
+  // k) steps; otherwise all score steps, then all read steps
+  auto er_frag = [&](const char* sbase, int k) {
+    const bool is_score = HX ? !(k & 1) : (k < KH);
+    const int ks = HX ? (k >> 1) : (k < KH ? k : k - KH);
+    const int off = is_score ? le[ks % TileE::NM] + TileE::step_off(ks) : lr[ks % TileR::NM] + TileR::step_off(ks);
+    return *reinterpret_cast<const u32x4_t*>(sbase + off);
   };
   auto issue_w = [&](int tile, int stage) {
     char* sb = w_base + stage * W_STAGE;
@@ -358,21 +406,16 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
 
   // score and read GEMMs of one tile, transposed: rows = units, columns = tokens
   auto phase_a = [&](int stage, f32x16_t& sacc, f32x16_t& racc) {
-    const char* base = er_base + stage * ER_STAGE + lane * 16;
-    auto frag = [&](int f) { return *reinterpret_cast<const u32x4_t*>(base + f * kFragBytes); };
+    const char* base = er_base + stage * ER_STAGE;
     sacc = f32x16_t{};
     racc = f32x16_t{};
-    if constexpr (HX) {
+    constexpr int NM = KH + KX;
 #pragma unroll
-      for (int ks = 0; ks < KX; ++ks) {
-        sacc = mfma(frag(ks), xq[ks], sacc);
-        racc = mfma(frag(F_E + ks), xq[ks], racc);
-      }
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < KH; ++ks) sacc = mfma(frag(ks), hq[HX ? 0 : ks], sacc);
-#pragma unroll
-      for (int ks = 0; ks < KX; ++ks) racc = mfma(frag(F_E + ks), xq[ks], racc);
+    for (int k = 0; k < NM; ++k) {
+      const bool is_score = HX ? !(k & 1) : (k < KH);
+      const int ks = HX ? (k >> 1) : (k < KH ? k : k - KH);
+      if (is_score) sacc = mfma(er_frag(base, k), HX ? xq[ks] : hq[HX ? 0 : ks], sacc);
+      else racc = mfma(er_frag(base, k), xq[ks], racc);
     }
   };
 
@@ -466,13 +509,10 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
                         const f32x16_t& racc, uint32_t* pk) -> uint32_t {
     constexpr int NM = KH + KX;
     constexpr int PF = 4;
-    const char* base = er_base + stage * ER_STAGE + lane * 16;
-    // MFMA k: HX interleaves score (even k) and read (odd k) steps; otherwise
-    // all score steps, then all read steps.
-    auto frag_of = [](int k) constexpr { return HX ? ((k & 1) ? F_E + (k >> 1) : (k >> 1)) : (k < KH ? k : F_E + (k - KH)); };
+    const char* base = er_base + stage * ER_STAGE;
     u32x4_t fr[PF];
 #pragma unroll
-    for (int k = 0; k < PF; ++k) fr[k] = *reinterpret_cast<const u32x4_t*>(base + frag_of(k) * kFragBytes);
+    for (int k = 0; k < PF; ++k) fr[k] = er_frag(base, k);
     sn = f32x16_t{};
     rn = f32x16_t{};
     uint32_t sp[8], xp[8], gpk[8];
@@ -482,7 +522,7 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
 #pragma unroll
     for (int k = 0; k < NM; ++k) {
       const u32x4_t a = fr[k % PF];
-      if (k + PF < NM) fr[k % PF] = *reinterpret_cast<const u32x4_t*>(base + frag_of(k + PF) * kFragBytes);
+      if (k + PF < NM) fr[k % PF] = er_frag(base, k + PF);
       const bool is_score = HX ? !(k & 1) : (k < KH);
       const int ks = HX ? (k >> 1) : (k < KH ? k : k - KH);
       if (is_score) sn = mfma(a, HX ? xq[ks] : hq[HX ? 0 : ks], sn);
@@ -590,15 +630,19 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
 
 // ---------------------------------------------------------------------------
 // main, warp-specialised: 8 waves, two per SIMD.  Waves 0-3 (producers) own 32
-// tokens each with X (and H) in VGPRs: the score/read GEMMs of tile i and its
-// gate epilogue, handing the bf16 products P to LDS.  Waves 4-7 (consumers)
-// own the same 32-token blocks with the fp32 OUT accumulators: the write GEMM
-// of tile i - 1 from LDS P and W^T.  One workgroup barrier per tile; both
-// roles issue global->LDS loads (producers E/R of the next tile, consumers W^T
-// of this one), because per-CU load throughput grows with the number of
-// issuing waves.  The two waves on a SIMD overlap one's vector-ALU epilogue with the
-// other's matrix-core work, and each role fits the 256 registers a wave may
-// hold at two waves per SIMD.  LDS = 2 E/R + 2 W^T + 2 P stages.
+// tokens each with X (and H) in VGPRs and run the score/read GEMMs of tile i,
+// handing the bf16-rounded scores and x.r products (the values the reference
+// rounds, v41:503, 517) to LDS.  Waves 4-7 (consumers) own the same 32-token
+// blocks: the gate epilogue of tile i - 1 (gate, P, pass bits, sums) in
+// registers, then its write GEMM into the fp32 OUT accumulators.  A producer's
+// MFMAs thus run back to back while the consumer on the same SIMD issues the
+// vector-ALU epilogue beside them.
+//
+// Per tile two workgroup barriers: the first (mid) lets producers overwrite
+// the single score stage S once consumers have read it; the second (end)
+// publishes S and the next tile's E/R and W^T.  Both roles issue global->LDS
+// loads (producers E/R of the next tile, consumers W^T of this one), spread
+// over their compute.  LDS = 2 E/R + 2 W^T stages + S.
 // ---------------------------------------------------------------------------
 constexpr int kWsThreads = 512;
 
@@ -611,10 +655,11 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
   constexpr int F_E = KH, F_R = KX, F_W = 2 * DB;
   constexpr int ER_STAGE = (F_E + F_R) * kFragBytes;
   constexpr int W_STAGE = F_W * kFragBytes;
-  constexpr int P_STAGE = 4 * 2 * kFragBytes;  // 4 token blocks x 2 k-steps
+  constexpr int S_BLK = 4 * kFragBytes;  // per token block: bf16 scores (2 KB), bf16 x.r (2 KB)
   static_assert(!HX || KH == KX, "h aliases x only when d_route == d_model");
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool producer = wave < 4;
   const int blk = wave & 3;                 // token block of this wave
   const int half = lane >> 5, col = lane & 31;
@@ -630,40 +675,43 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
 
   char* const er_base = lds;
   char* const w_base = lds + 2 * ER_STAGE;
-  char* const p_base = w_base + 2 * W_STAGE;
+  char* const s_blk = w_base + 2 * W_STAGE + blk * S_BLK + lane * 16;
 
-  // Tile loads, direct global->LDS: producers fetch E/R of the next tile,
-  // consumers W^T of the current one, each wave a contiguous fragment run.
-  auto issue_er = [&](int tile, int stage) {
+  // Tile loads, direct global->LDS: each wave a contiguous run of blocks.  A
+  // wave's loads are spread over its compute: issued back to back they stall
+  // the wave at in-order issue until the memory pipeline drains.
+  constexpr int PE = (F_E + 3) / 4, PR = (F_R + 3) / 4, NL_ER = PE + PR;
+  constexpr int PW = (F_W + 3) / 4;
+  using TileE = RowTile<KH>;
+  using TileR = RowTile<KX>;
+  auto er_load = [&](int tile, int stage, int q) {
     char* sb = er_base + stage * ER_STAGE;
-    const int64_t u = static_cast<int64_t>(tile) * kUnitTile + col;
-    const int64_t row = u < p.g.N ? u : p.g.N - 1;
-    constexpr int PE = (F_E + 3) / 4, PR = (F_R + 3) / 4;
-    const uint16_t* eb = p.emb + row * DR + 8 * half + 16 * PE * blk;
-    const uint16_t* rb = p.read + row * D + 8 * half + 16 * PR * blk;
-#pragma unroll
-    for (int q = 0; q < PE; ++q)
-      if (PE * blk + q < F_E) g2lds16(eb + 16 * q, sb + (PE * blk + q) * kFragBytes);
-#pragma unroll
-    for (int q = 0; q < PR; ++q)
-      if (PR * blk + q < F_R) g2lds16(rb + 16 * q, sb + (F_E + PR * blk + q) * kFragBytes);
+    const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
+    if (q < PE) {
+      if (PE * blk + q < F_E) TileE::load(p.emb, u0, p.g.N, PE * blk + q, lane, sb);
+    } else {
+      const int r = q - PE;
+      if (PR * blk + r < F_R) TileR::load(p.read, u0, p.g.N, PR * blk + r, lane, sb + F_E * kFragBytes);
+    }
   };
-  auto issue_w = [&](int tile, int stage) {
-    char* sb = w_base + stage * W_STAGE;
-    constexpr int PW = (F_W + 3) / 4;
-    const uint16_t* wb = p.wp + (static_cast<int64_t>(tile) * F_W + PW * blk) * 512 + lane * 8;
-#pragma unroll
-    for (int q = 0; q < PW; ++q)
-      if (PW * blk + q < F_W) g2lds16(wb + q * 512, sb + (PW * blk + q) * kFragBytes);
+  // W^T: wave-uniform tile base + 32-bit lane offset
+  const uint32_t w_voff = static_cast<uint32_t>(PW * blk * kFragBytes + lane * 16);
+  auto w_load = [&](int tile, int stage, int q) {
+    if (PW * blk + q < F_W)
+      g2lds16(reinterpret_cast<const char*>(p.wp) + static_cast<int64_t>(tile) * W_STAGE + (w_voff + q * kFragBytes),
+              w_base + stage * W_STAGE + (PW * blk + q) * kFragBytes);
   };
 
   // prologue: E/R of the first tile
-  if (n > 0 && producer) issue_er(ta, 0);
+  if (n > 0 && producer) {
+#pragma unroll
+    for (int q = 0; q < NL_ER; ++q) er_load(ta, 0, q);
+  }
   wait_vm0();
   __syncthreads();
 
   if (producer) {
-    // ---------------- producer: score / read GEMMs and the gate ----------------
+    // ---------------- producer: score / read GEMMs ----------------
     u32x4_t xq[KX];
 #pragma unroll
     for (int ks = 0; ks < KX; ++ks)
@@ -674,8 +722,74 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
       for (int ks = 0; ks < KH; ++ks)
         hq[ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl * DR + 16 * ks + 8 * half);
     }
-    // tau = mean + tau_offset * (sqrt(E[s^2] - mean^2) + 1e-8)   (v41:461-464),
-    // folded with the gate's constant offsets:
+    int le[TileE::NM], lr[TileR::NM];  // LDS offsets of this lane's E / R pieces (RowTile)
+#pragma unroll
+    for (int m = 0; m < TileE::NM; ++m) le[m] = TileE::lane_off(lane, m);
+#pragma unroll
+    for (int m = 0; m < TileR::NM; ++m) lr[m] = F_E * kFragBytes + TileR::lane_off(lane, m);
+    // Drain the x / h loads here: left pending into the tile loop, they make
+    // the compiler wait for every load in flight (the next tile's LDS
+    // prefetch included) at the top of each iteration.
+    wait_vm0();
+
+    for (int it = 0; it <= n; ++it) {
+      const bool pre = it + 1 < n;  // the next tile's E/R go out during this one's MFMAs
+      // S piece q (16 B per lane) = bf16 scores and x.r of elements 4q..4q+3:
+      // {s[4q], s[4q+1]}, {s[4q+2], s[4q+3]}, {xr[4q], xr[4q+1]}, {xr[4q+2], xr[4q+3]}
+      uint32_t sx[16];
+      if (it < n) {
+        // MFMA k: HX interleaves score (even k) and read (odd k) steps,
+        // otherwise all score steps, then all read steps; LDS operands are
+        // read PF MFMAs ahead
+        const char* base = er_base + (it & 1) * ER_STAGE;
+        constexpr int NM = KH + KX, PF = 8;
+        auto frag = [&](int k) {
+          const bool is_score = HX ? !(k & 1) : (k < KH);
+          const int ks = HX ? (k >> 1) : (k < KH ? k : k - KH);
+          const int off = is_score ? le[ks % TileE::NM] + TileE::step_off(ks)
+                                   : lr[ks % TileR::NM] + TileR::step_off(ks);
+          return *reinterpret_cast<const u32x4_t*>(base + off);
+        };
+        u32x4_t fr[PF];
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+          if (k < NM) fr[k] = frag(k);
+        f32x16_t sacc = {}, racc = {};
+#pragma unroll
+        for (int k = 0; k < NM; ++k) {
+#pragma unroll
+          for (int q = 0; q < NL_ER; ++q)
+            if (k == q * NM / (2 * NL_ER) && pre) er_load(ta + it + 1, (it + 1) & 1, q);  // first half
+          const u32x4_t a = fr[k % PF];
+          if (k + PF < NM) fr[k % PF] = frag(k + PF);
+          const bool is_score = HX ? !(k & 1) : (k < KH);
+          const int ks = HX ? (k >> 1) : (k < KH ? k : k - KH);
+          if (is_score) sacc = mfma(a, HX ? xq[ks] : hq[HX ? 0 : ks], sacc);
+          else racc = mfma(a, xq[ks], racc);
+          __builtin_amdgcn_sched_barrier(0);  // keep the reads PF steps ahead
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          sx[4 * q] = pack_bf16(sacc[4 * q], sacc[4 * q + 1]);          // bf16 scores (v41:503)
+          sx[4 * q + 1] = pack_bf16(sacc[4 * q + 2], sacc[4 * q + 3]);
+          sx[4 * q + 2] = pack_bf16(racc[4 * q], racc[4 * q + 1]);      // bf16 x.r (v41:517)
+          sx[4 * q + 3] = pack_bf16(racc[4 * q + 2], racc[4 * q + 3]);
+        }
+      }
+      __syncthreads();  // mid: consumers have read S (tile it - 1)
+      if (it < n) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<u32x4_t*>(s_blk + q * kFragBytes) =
+              u32x4_t{sx[4 * q], sx[4 * q + 1], sx[4 * q + 2], sx[4 * q + 3]};
+      }
+      wait_vm0();
+      __syncthreads();  // end: S, next E/R and W^T visible
+    }
+  } else {
+    // ---------------- consumer: gate epilogue and write GEMM, one tile behind ----------------
+    // tau = mean + tau_offset * (sqrt(E[s^2] - mean^2) + 1e-8) (v41:461-464,
+    // srw_tau_kernel), folded with the gate's constant offsets:
     //   margin = s - tau - thr,  exp argument = margin * c  (c = -sharpness log2 e)
     float k_exp, tau_cut;
     {
@@ -686,22 +800,24 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
     const float c_exp = p.exp_scale, eps = p.gp.eps, maxi = p.gp.maxi;
     float gsum = 0.f, isum = 0.f;
     uint32_t nact = 0;
-    // Drain the x / h / tau loads here: left pending into the tile loop, they
-    // make the compiler wait for every load in flight (the next tile's LDS
-    // prefetch included) at the top of each iteration.
+    f32x16_t oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
     wait_vm0();
 
-    // gate epilogue (v41:503-518) of one tile; P goes to LDS as the consumer's
-    // A operand (k-step j at [blk][j][lane]); returns pass bits (v at 15 - v)
-    auto gate_tile = [&](auto full_tag, const f32x16_t& sacc, const f32x16_t& racc, int64_t u0,
-                         char* pdst) -> uint32_t {
+    // gate epilogue (v41:503-518) of one tile from the bf16 scores / x.r:
+    // P (the write GEMM's A operand, k-step j in pk[4j..4j+3]) and the pass
+    // bits (element v at bit 15 - v); W^T loads of the tile go out between
+    // element pairs
+    auto gate_tile = [&](auto full_tag, int64_t u0, uint32_t* pk, int wtile, int wstage) -> uint32_t {
       constexpr bool FULL = decltype(full_tag)::value;
       uint32_t bits = 0;
-      uint32_t pk[8];
+      u32x4_t sq;
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
-        const uint32_t sp = pack_bf16(sacc[v], sacc[v + 1]);   // bf16 scores (v41:503)
-        const uint32_t xp = pack_bf16(racc[v], racc[v + 1]);   // bf16 x.r (v41:517)
+        if ((v & 3) == 0) sq = *reinterpret_cast<const u32x4_t*>(s_blk + (v >> 2) * kFragBytes);
+        if ((v >> 1) < PW && wtile >= 0) w_load(wtile, wstage, v >> 1);
+        const uint32_t sp = sq[(v >> 1) & 1], xp = sq[2 + ((v >> 1) & 1)];
         float g2[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -728,81 +844,45 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
         const uint32_t gq = pack_bf16(g2[0], g2[1]);             // gate_bf (v41:516)
         pk[v >> 1] = pack_bf16(lo_f32(gq) * lo_f32(xp), hi_f32(gq) * hi_f32(xp));  // (v41:518)
       }
-      *reinterpret_cast<u32x4_t*>(pdst + lane * 16) = u32x4_t{pk[0], pk[1], pk[2], pk[3]};
-      *reinterpret_cast<u32x4_t*>(pdst + kFragBytes + lane * 16) = u32x4_t{pk[4], pk[5], pk[6], pk[7]};
       return bits;
     };
 
     for (int it = 0; it <= n; ++it) {
-      if (it + 1 < n) issue_er(ta + it + 1, (it + 1) & 1);
-      if (it < n) {
-        // score and read GEMMs, LDS operands read PF MFMAs ahead
-        const char* base = er_base + (it & 1) * ER_STAGE + lane * 16;
-        constexpr int NM = KH + KX, PF = 8;
-        auto frag_of = [](int k) constexpr {
-          return HX ? ((k & 1) ? F_E + (k >> 1) : (k >> 1)) : (k < KH ? k : F_E + (k - KH));
-        };
-        u32x4_t fr[PF];
+      const bool cur = it < n;  // this tile's W^T goes out during the previous tile's epilogue
+      if (it == 0) {
+        if (cur) {
 #pragma unroll
-        for (int k = 0; k < PF; ++k)
-          if (k < NM) fr[k] = *reinterpret_cast<const u32x4_t*>(base + frag_of(k) * kFragBytes);
-        f32x16_t sacc = {}, racc = {};
-#pragma unroll
-        for (int k = 0; k < NM; ++k) {
-          const u32x4_t a = fr[k % PF];
-          if (k + PF < NM) fr[k % PF] = *reinterpret_cast<const u32x4_t*>(base + frag_of(k + PF) * kFragBytes);
-          const bool is_score = HX ? !(k & 1) : (k < KH);
-          const int ks = HX ? (k >> 1) : (k < KH ? k : k - KH);
-          if (is_score) sacc = mfma(a, HX ? xq[ks] : hq[HX ? 0 : ks], sacc);
-          else racc = mfma(a, xq[ks], racc);
-          __builtin_amdgcn_sched_barrier(0);  // keep the reads PF steps ahead
+          for (int q = 0; q < PW; ++q) w_load(ta, 0, q);
         }
-        // gate epilogue, P to LDS, pass bitmask
-        const int tile = ta + it;
+        __syncthreads();  // mid
+      } else {
+        const int tile = ta + it - 1;
         const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
-        char* pdst = p_base + (it & 1) * P_STAGE + blk * 2 * kFragBytes;
+        uint32_t pk[8];
         uint32_t bits;
+        const int wtile = cur ? ta + it : -1;
         if (u0 >= lo && u0 + kUnitTile <= hi)
-          bits = gate_tile(std::integral_constant<bool, true>{}, sacc, racc, u0, pdst);
+          bits = gate_tile(std::integral_constant<bool, true>{}, u0, pk, wtile, it & 1);
         else
-          bits = gate_tile(std::integral_constant<bool, false>{}, sacc, racc, u0, pdst);
-        const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
-        uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
-        m <<= 4 * half;
-        nact += __builtin_popcount(m);
-        m |= __shfl_xor(m, 32);
-        if (p.mask32 && half == 0 && t < p.g.T) {
-          uint32_t* dst = p.mask32 + t * p.mask_words32 + tile;
-          const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
-          if (shared) atomicOr(dst, m);
-          else *dst = m;
+          bits = gate_tile(std::integral_constant<bool, false>{}, u0, pk, wtile, it & 1);
+        // pass bitmask of the tile
+        {
+          const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
+          uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
+          m <<= 4 * half;
+          nact += __builtin_popcount(m);
+          m |= __shfl_xor(m, 32);
+          if (p.mask32 && half == 0 && t < p.g.T) {
+            uint32_t* dst = p.mask32 + t * p.mask_words32 + tile;
+            const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
+            if (shared) atomicOr(dst, m);
+            else *dst = m;
+          }
         }
-      }
-      wait_vm0();
-      __syncthreads();
-    }
-    gsum += __shfl_xor(gsum, 32);
-    isum += __shfl_xor(isum, 32);
-    nact += __shfl_xor(nact, 32);
-    if (half == 0 && t < p.g.T) {
-      float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * 4;
-      tp[0] = gsum;
-      tp[1] = isum;
-      tp[2] = static_cast<float>(nact);
-    }
-  } else {
-    // ---------------- consumer: the write GEMM, one tile behind ----------------
-    f32x16_t oacc[DB];
-#pragma unroll
-    for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
-    for (int it = 0; it <= n; ++it) {
-      if (it < n) issue_w(ta + it, it & 1);
-      if (it >= 1) {
-        const int st = (it - 1) & 1;
-        const char* wb = w_base + st * W_STAGE + lane * 16;
-        const char* pb = p_base + st * P_STAGE + blk * 2 * kFragBytes + lane * 16;
-        const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(pb);
-        const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(pb + kFragBytes);
+        __builtin_amdgcn_sched_barrier(0);
+        // write GEMM: OUT[32 tok x D] += P[32 tok x 32 units] . W_t[32 units x D]
+        const char* wb = w_base + ((it - 1) & 1) * W_STAGE + lane * 16;
+        const u32x4_t a0 = {pk[0], pk[1], pk[2], pk[3]}, a1 = {pk[4], pk[5], pk[6], pk[7]};
         constexpr int NC = 2 * DB, PF = 6;
         auto frag = [&](int k) {  // MFMA k: j = k / DB, db = k % DB
           return *reinterpret_cast<const u32x4_t*>(wb + (2 * (k % DB) + k / DB) * kFragBytes);
@@ -818,9 +898,19 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
           oacc[k % DB] = mfma(k < DB ? a0 : a1, bq, oacc[k % DB]);
           __builtin_amdgcn_sched_barrier(0);
         }
+        __syncthreads();  // mid
       }
       wait_vm0();
-      __syncthreads();
+      __syncthreads();  // end
+    }
+    gsum += __shfl_xor(gsum, 32);
+    isum += __shfl_xor(isum, 32);
+    nact += __shfl_xor(nact, 32);
+    if (half == 0 && t < p.g.T) {
+      float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * 4;
+      tp[0] = gsum;
+      tp[1] = isum;
+      tp[2] = static_cast<float>(nact);
     }
     float* op = p.out_part + static_cast<int64_t>(split) * p.g.T * D;
     if (tw + 32 <= p.g.T) {
@@ -947,7 +1037,7 @@ template <int DB, int KH, bool HX, bool WS>
 Kernels kernels_of() {
   if constexpr (WS)
     return Kernels{srw_stats_kernel<KH>, srw_main_ws_kernel<DB, KH, HX>, kWsThreads,
-                   (2 * (KH + 2 * DB) + 2 * 2 * DB + 2 * 8) * kFragBytes};
+                   (2 * (KH + 2 * DB) + 2 * 2 * DB + 16) * kFragBytes};  // 2 E/R, 2 W^T, S
   else
     return Kernels{srw_stats_kernel<KH>, srw_main_kernel<DB, KH, HX>, kThreads,
                    2 * (KH + 2 * DB + 2 * DB) * kFragBytes};
