@@ -77,12 +77,27 @@ __device__ inline void g2lds16(const void* g, char* lds) {
 
 __device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
+// Workgroup barrier that waits only for this wave's LDS operations.
+// __syncthreads() is a workgroup-scope release/acquire, for which the
+// compiler also drains every global load in flight (vmcnt(0)) -- including
+// the global->LDS prefetch of later tiles.  Here global->LDS loads stay in
+// flight; a caller that publishes them waits for them first.  The
+// compiler-only fences keep memory accesses on their side of the barrier.
+__device__ inline void barrier_lds() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // A 32-row tile of a row-major bf16 [rows, K] array (E or R), staged in LDS
 // as K / 16 one-KB blocks.  Load block j moves whole 128-byte lines (8 rows x
 // 128 B; 16 rows x 64 B when K = 32): a wave load that touches 32 B of each of
 // 32 rows costs the texture path four times the line requests and halves the
 // global->LDS rate.  The 16-byte pieces of each row are XOR-swizzled by row,
-// so that the MFMA fragment reads (32 rows x 32 B) are free of bank conflicts.
+// so that the MFMA fragment reads (32 rows x 32 B) are free of bank conflicts:
+// the LDS serves a ds_read_b128 16 lanes (256 B) at a time, and each group of
+// 16 lanes hits 16 distinct 16-byte slots.
 template <int KF>  // K / 16: MFMA k-steps per row
 struct RowTile {
   static constexpr int K = KF * 16;
@@ -90,13 +105,32 @@ struct RowTile {
   static constexpr int RPI = 64 / PPR;                 // rows per block
   static constexpr int RG = 32 / RPI;                  // row groups
   static constexpr int NM = PPR / 2;                   // k-steps per block row
-  __device__ static int swz(int r) { return (r / (8 / PPR)) % PPR; }
-  // load block j of the tile whose first row is row0 (rows past `rows` read the last one)
-  __device__ static void load(const uint16_t* a, int64_t row0, int64_t rows, int j, int lane, char* tile) {
-    const int r = RPI * (j % RG) + lane / PPR;
-    const int c = 8 * ((j / RG) * PPR + ((lane % PPR) ^ swz(r)));
-    const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
-    g2lds16(a + row * K + c, tile + j * kFragBytes);
+  __host__ __device__ static constexpr int swz(int r) {
+    return PPR == 8 ? (r % 8) ^ ((r / 8) & 1) : (r / 4) % 4;
+  }
+  // Byte offset, within block j's rows, of the 16 B `lane` loads: swz depends
+  // on the row group of block j only through its parity (PPR = 8), so each
+  // lane keeps two offsets; block j adds the wave-uniform block_off(j).
+  __device__ static uint32_t lane_src(int lane, int parity) {
+    const int r = lane / PPR;
+    const int sw = PPR == 8 ? swz(r) ^ parity : swz(r);
+    return static_cast<uint32_t>((r * K + 8 * ((lane % PPR) ^ sw)) * 2);
+  }
+  static constexpr int block_off(int j) { return (RPI * (j % RG) * K + 8 * (j / RG) * PPR) * 2; }
+  // load block j of the tile whose first row is row0 (rows past `rows` read the last one);
+  // lsrc = {lane_src(lane, 0), lane_src(lane, 1)}.  Whole tiles use a
+  // wave-uniform base plus the lane offset.
+  __device__ static void load(const uint16_t* a, int64_t row0, int64_t rows, int j, int lane, const uint32_t* lsrc,
+                              char* tile) {
+    if (row0 + 32 <= rows) {
+      g2lds16(reinterpret_cast<const char*>(a) + (row0 * K * 2 + block_off(j)) + lsrc[(j % RG) & 1],
+              tile + j * kFragBytes);
+    } else {
+      const int r = RPI * (j % RG) + lane / PPR;
+      const int c = 8 * ((j / RG) * PPR + ((lane % PPR) ^ swz(r)));
+      const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
+      g2lds16(a + row * K + c, tile + j * kFragBytes);
+    }
   }
   // LDS byte offset of the 16 B that `lane` feeds to MFMA k-step ks:
   // lane_off(lane, ks % NM) + step_off(ks)
@@ -128,8 +162,9 @@ struct Geometry {
   int nc;                // reference chunks
   int spc;               // N-splits per chunk of the main kernel
   int S;                 // N-splits in total (nc * spc)
-  int spc_st, S_st;      // the same for the moments kernel (finer: two workgroups per CU)
-  int TT;                // token tiles
+  int spc_st, S_st;      // the same for the moments kernel
+  int TT;                // token tiles of the main kernel
+  int TT_st;             // token tiles of the moments kernel
   int ntiles;            // ceil(N / 32): global 32-unit tiles
 };
 
@@ -200,7 +235,8 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int STAGE = KH * kFragBytes;
   constexpr int DR = KH * 16;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = lane >> 5, col = lane & 31;
   const int split = blockIdx.x % p.g.S_st;
   const int ttile = blockIdx.x / p.g.S_st;
@@ -227,9 +263,10 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
     hq[ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl * DR + 16 * ks + 8 * half);
 
   using TileE = RowTile<KH>;
+  const uint32_t lsrc[2] = {TileE::lane_src(lane, 0), TileE::lane_src(lane, 1)};
   auto issue = [&](int tile, int stage) {
     for (int j = wave; j < KH; j += 4)
-      TileE::load(p.emb, static_cast<int64_t>(tile) * kUnitTile, p.g.N, j, lane, lds + stage * STAGE);
+      TileE::load(p.emb, static_cast<int64_t>(tile) * kUnitTile, p.g.N, j, lane, lsrc, lds + stage * STAGE);
   };
   int le[TileE::NM];
 #pragma unroll
@@ -243,7 +280,7 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
   }
   for (int tile = ta; tile < tb; ++tile) {
     const int st = (tile - ta) & 1;
-    if (tile + 1 < tb) issue(tile + 1, st ^ 1);
+    const bool pre = tile + 1 < tb;  // the next tile's loads go out between this one's MFMAs
     f32x16_t acc = {};
     const char* base = lds + st * STAGE;
     auto frag = [&](int ks) {
@@ -258,7 +295,11 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
     for (int ks = 0; ks < KH; ++ks) {
       const u32x4_t e = ef[ks % PF];
       if (ks + PF < KH) ef[ks % PF] = frag(ks + PF);
+      if (pre && (ks % 4) == 0 && wave + ks < KH)  // block wave + ks: this wave's share, every 4th MFMA
+        TileE::load(p.emb, static_cast<int64_t>(tile + 1) * kUnitTile, p.g.N, wave + ks, lane, lsrc,
+                    lds + (st ^ 1) * STAGE);
       acc = mfma(e, hq[ks], acc);
+      __builtin_amdgcn_sched_barrier(0);
     }
     const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
     const bool full = u0 >= lo && u0 + kUnitTile <= hi;
@@ -328,7 +369,8 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
   constexpr int W_STAGE = F_W * kFragBytes;
   static_assert(!HX || KH == KX, "h aliases x only when d_route == d_model");
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = lane >> 5, col = lane & 31;
   const int split = blockIdx.x % p.g.S;
   const int ttile = blockIdx.x / p.g.S;
@@ -366,18 +408,20 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
   // Direct global->LDS loads: wave w issues blocks w, w+4, ... of a group.
   using TileE = RowTile<KH>;
   using TileR = RowTile<KX>;
+  const uint32_t lsrc_e[2] = {TileE::lane_src(lane, 0), TileE::lane_src(lane, 1)};
+  const uint32_t lsrc_r[2] = {TileR::lane_src(lane, 0), TileR::lane_src(lane, 1)};
   auto issue_er = [&](int tile, int stage) {
     char* sb = er_base + stage * ER_STAGE;
     const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
 #pragma unroll
     for (int q = 0; q < (F_E + 3) / 4; ++q) {
       const int f = wave + 4 * q;
-      if (f < F_E) TileE::load(p.emb, u0, p.g.N, f, lane, sb);
+      if (f < F_E) TileE::load(p.emb, u0, p.g.N, f, lane, lsrc_e, sb);
     }
 #pragma unroll
     for (int q = 0; q < (F_R + 3) / 4; ++q) {
       const int f = wave + 4 * q;
-      if (f < F_R) TileR::load(p.read, u0, p.g.N, f, lane, sb + F_E * kFragBytes);
+      if (f < F_R) TileR::load(p.read, u0, p.g.N, f, lane, lsrc_r, sb + F_E * kFragBytes);
     }
   };
   // LDS offsets of this lane's E / R fragment pieces (see RowTile)
@@ -684,14 +728,16 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
   constexpr int PW = (F_W + 3) / 4;
   using TileE = RowTile<KH>;
   using TileR = RowTile<KX>;
+  const uint32_t lsrc_e[2] = {TileE::lane_src(lane, 0), TileE::lane_src(lane, 1)};
+  const uint32_t lsrc_r[2] = {TileR::lane_src(lane, 0), TileR::lane_src(lane, 1)};
   auto er_load = [&](int tile, int stage, int q) {
     char* sb = er_base + stage * ER_STAGE;
     const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
     if (q < PE) {
-      if (PE * blk + q < F_E) TileE::load(p.emb, u0, p.g.N, PE * blk + q, lane, sb);
+      if (PE * blk + q < F_E) TileE::load(p.emb, u0, p.g.N, PE * blk + q, lane, lsrc_e, sb);
     } else {
       const int r = q - PE;
-      if (PR * blk + r < F_R) TileR::load(p.read, u0, p.g.N, PR * blk + r, lane, sb + F_E * kFragBytes);
+      if (PR * blk + r < F_R) TileR::load(p.read, u0, p.g.N, PR * blk + r, lane, lsrc_r, sb + F_E * kFragBytes);
     }
   };
   // W^T: wave-uniform tile base + 32-bit lane offset
@@ -776,7 +822,7 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
           sx[4 * q + 3] = pack_bf16(racc[4 * q + 2], racc[4 * q + 3]);
         }
       }
-      __syncthreads();  // mid: consumers have read S (tile it - 1)
+      barrier_lds();  // mid: consumers have read S (tile it - 1)
       if (it < n) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -784,7 +830,7 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
               u32x4_t{sx[4 * q], sx[4 * q + 1], sx[4 * q + 2], sx[4 * q + 3]};
       }
       wait_vm0();
-      __syncthreads();  // end: S, next E/R and W^T visible
+      barrier_lds();  // end: S, next E/R and W^T visible
     }
   } else {
     // ---------------- consumer: gate epilogue and write GEMM, one tile behind ----------------
@@ -854,7 +900,7 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
 #pragma unroll
           for (int q = 0; q < PW; ++q) w_load(ta, 0, q);
         }
-        __syncthreads();  // mid
+        barrier_lds();  // mid
       } else {
         const int tile = ta + it - 1;
         const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
@@ -898,10 +944,10 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
           oacc[k % DB] = mfma(k < DB ? a0 : a1, bq, oacc[k % DB]);
           __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();  // mid
+        barrier_lds();  // mid
       }
       wait_vm0();
-      __syncthreads();  // end
+      barrier_lds();  // end
     }
     gsum += __shfl_xor(gsum, 32);
     isum += __shfl_xor(isum, 32);
@@ -1076,7 +1122,8 @@ Geometry geometry(const srw_desc_t& d, int64_t chunk) {
   if (spc > min_tiles) spc = static_cast<int>(min_tiles > 0 ? min_tiles : 1);
   g.spc = spc;
   g.S = g.nc * spc;
-  int spc_st = static_cast<int>((2 * kTargetBlocks + g.TT * g.nc - 1) / (g.TT * g.nc));
+  g.TT_st = g.TT;  // the moments kernel uses the main kernel's token tiles, two workgroups per CU
+  int spc_st = static_cast<int>((2 * kTargetBlocks + g.TT_st * g.nc - 1) / (g.TT_st * g.nc));
   if (spc_st < 1) spc_st = 1;
   if (spc_st > min_tiles) spc_st = static_cast<int>(min_tiles > 0 ? min_tiles : 1);
   g.spc_st = spc_st;
@@ -1176,7 +1223,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   const unsigned grid = static_cast<unsigned>(g.TT * g.S);
-  const unsigned grid_st = static_cast<unsigned>(g.TT * g.S_st);
+  const unsigned grid_st = static_cast<unsigned>(g.TT_st * g.S_st);
   if (d.stats_mode == SRW_STATS_GRAM) {
     if ((e = gram_moments(static_cast<const uint16_t*>(a.in.emb), static_cast<const uint16_t*>(a.in.h), g.T,
                           d.n_units, d.d_route, mom, a.ws + L.gram, a.stream, mask32, mw32, g.cs, g.nc,
