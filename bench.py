@@ -117,6 +117,9 @@ def main() -> int:
                     help="time budget of the CPU baseline (0 skips it)")
     ap.add_argument("--force-generic", action="store_true",
                     help="time the generic (scalar) kernels instead of the MFMA path")
+    ap.add_argument("--diag", action="store_true",
+                    help="also compute the training diagnostics (SRW_FLAG_DIAG: the 22-tuple "
+                         "path of the drop-in fused_gate_srw)")
     ap.add_argument("--pool-cached", action="store_true",
                     help="steps after the first reuse the pool data kept in the workspace "
                          "(SRW_FLAG_POOL_CACHED: decode steps / layers sharing one pool)")
@@ -167,7 +170,7 @@ def main() -> int:
     h = x if shape.h_is_x else inp["h"].to(bf).to(dev)
     plan = pkg.SrwPlan(x, h, inp["emb"].to(bf).to(dev), inp["tau_offset"].to(dev),
                        inp["read"].to(bf).to(dev), inp["write"].to(bf).to(dev),
-                       stats=args.stats, chunk_size=cs, want_mask=True,
+                       stats=args.stats, chunk_size=cs, want_mask=True, diag=args.diag,
                        force_generic=args.force_generic)
     stream = torch.cuda.current_stream(dev)
 
@@ -225,7 +228,7 @@ def main() -> int:
                                   "R, W L2-normalised rows)",
         "config": {"workload": args.workload, "note": note, "T": T, "d_model": D,
                    "d_route": dr, "n_units": N, "routes": R, "chunk": cs,
-                   "stats": args.stats, "pool_cached": args.pool_cached,
+                   "stats": args.stats, "diag": args.diag, "pool_cached": args.pool_cached,
                    "tau_offset": round(tau_value, 4),
                    "parallelism": "single GPU"},
         "roofline": roofline,

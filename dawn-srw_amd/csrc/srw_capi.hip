@@ -34,9 +34,10 @@ srw_status_t validate(const srw_desc_t* d) {
 }
 
 // Which family serves this descriptor: 1 = MFMA, 0 = generic, -1 = none.
-int choose(const srw_desc_t& d) {
+// h_is_x: h aliases x (known to srw_forward from the pointers).
+int choose(const srw_desc_t& d, bool h_is_x) {
   const bool force_generic = (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST)) != 0;
-  if (!force_generic && srw::mfma_supports(d)) return 1;
+  if (!force_generic && srw::mfma_supports(d, h_is_x)) return 1;
   if (d.stats_mode == SRW_STATS_GRAM) return -1;  // only the MFMA family implements it
   if (d.flags & SRW_FLAG_SPARSE_SKIP) return -1;
   if (srw::generic_supports(d)) return 0;
@@ -94,9 +95,19 @@ srw_status_t srw_workspace_size(const srw_desc_t* d, size_t* bytes) {
   srw_status_t st = validate(d);
   if (st != SRW_OK) return st;
   if (!bytes) return SRW_EINVAL;
-  const int which = choose(*d);
-  if (which < 0) return SRW_EUNSUPPORTED;
-  *bytes = align256(which == 1 ? srw::mfma_workspace_bytes(*d) : srw::generic_workspace_bytes(*d));
+  // the largest need over the paths a call may take: h aliasing x (possible
+  // when d_route == d_model with one route) can select the MFMA family
+  const bool can_alias = d->n_routes == 1 && d->d_route == d->d_model;
+  const int which = choose(*d, false);
+  const int which_alias = can_alias ? choose(*d, true) : which;
+  if (which < 0 && which_alias < 0) return SRW_EUNSUPPORTED;
+  size_t need = 0;
+  for (int w : {which, which_alias}) {
+    if (w < 0) continue;
+    const size_t n = align256(w == 1 ? srw::mfma_workspace_bytes(*d) : srw::generic_workspace_bytes(*d));
+    need = n > need ? n : need;
+  }
+  *bytes = need;
   return SRW_OK;
 }
 
@@ -105,7 +116,7 @@ srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw
   srw_status_t st = validate(d);
   if (st != SRW_OK) return st;
   if (!in || !o) return SRW_EINVAL;
-  const int which = choose(*d);
+  const int which = choose(*d, in->h != nullptr && in->h == in->x);
   if (which < 0) return SRW_EUNSUPPORTED;
   if (d->T == 0) {  // nothing to compute; empty tensors may carry null pointers
     g_last_path = "empty";

@@ -56,7 +56,8 @@ hipError_t gram_moments(const uint16_t* emb, const uint16_t* h, int64_t T, int64
 
 // MFMA kernels (bf16 / f32 matrix cores), see srw_mfma.hip.
 size_t mfma_workspace_bytes(const srw_desc_t& d);
-bool mfma_supports(const srw_desc_t& d);
+// h_is_x: h aliases x (d_route == d_model, one route), which some shapes need
+bool mfma_supports(const srw_desc_t& d, bool h_is_x);
 hipError_t mfma_forward(const LaunchArgs& a, const char** path_name);
 
 }  // namespace srw

@@ -77,6 +77,48 @@ __device__ inline void g2lds16(const void* g, char* lds) {
 
 __device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
+// Lane exchanges within 32-lane halves, on the vector ALU (DPP and the gfx950
+// row swap) rather than the LDS crossbar: the value of lane (lane ^ m).
+__device__ inline float as_f(int v) { return __builtin_bit_cast(float, v); }
+__device__ inline int as_i(float v) { return __builtin_bit_cast(int, v); }
+template <int M>
+__device__ inline float lane_xor(float v, int lane) {
+  if constexpr (M == 1) return as_f(__builtin_amdgcn_mov_dpp(as_i(v), 0xB1, 0xF, 0xF, true));  // quad_perm [1,0,3,2]
+  if constexpr (M == 2) return as_f(__builtin_amdgcn_mov_dpp(as_i(v), 0x4E, 0xF, 0xF, true));  // quad_perm [2,3,0,1]
+  if constexpr (M == 4) {
+    const float up = as_f(__builtin_amdgcn_mov_dpp(as_i(v), 0x104, 0xF, 0xF, true));  // row_shl:4
+    const float dn = as_f(__builtin_amdgcn_mov_dpp(as_i(v), 0x114, 0xF, 0xF, true));  // row_shr:4
+    return (lane & 4) ? dn : up;
+  }
+  if constexpr (M == 8) return as_f(__builtin_amdgcn_mov_dpp(as_i(v), 0x128, 0xF, 0xF, true));  // row_ror:8
+  if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(as_i(v), as_i(v), false, false);
+    return as_f((lane & 16) ? r[0] : r[1]);
+  }
+}
+
+// Reduce-scatter of 16 values per lane over the 32 lanes of each half: on
+// return a[0] of lane l holds the reduction, over the half's 32 lanes, of
+// element k = 8 (l & 1) + 4 (l >> 1 & 1) + 2 (l >> 2 & 1) + (l >> 3 & 1).
+template <class Op>
+__device__ inline void reduce_scatter16(float (&a)[16], int lane, Op op) {
+  auto step = [&](auto mtag, int cnt) {
+    constexpr int M = decltype(mtag)::value;
+    const bool up = lane & M;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k >= cnt / 2) break;
+      const float send = up ? a[k] : a[k + cnt / 2], keep = up ? a[k + cnt / 2] : a[k];
+      a[k] = op(keep, lane_xor<M>(send, lane));
+    }
+  };
+  step(std::integral_constant<int, 1>{}, 16);
+  step(std::integral_constant<int, 2>{}, 8);
+  step(std::integral_constant<int, 4>{}, 4);
+  step(std::integral_constant<int, 8>{}, 2);
+  a[0] = op(a[0], lane_xor<16>(a[0], lane));
+}
+
 // Workgroup barrier that waits only for this wave's LDS operations.
 // __syncthreads() is a workgroup-scope release/acquire, for which the
 // compiler also drains every global load in flight (vmcnt(0)) -- including
@@ -230,8 +272,10 @@ struct StatsParams {
   Geometry g;
 };
 
-template <int KH>
+// DG: also sum s^3, s^4 (training diagnostics, v41:442-444); mom stride 4
+template <int KH, bool DG>
 __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
+  constexpr int MS = DG ? 4 : 2;
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int STAGE = KH * kFragBytes;
   constexpr int DR = KH * 16;
@@ -272,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
 #pragma unroll
   for (int m = 0; m < TileE::NM; ++m) le[m] = TileE::lane_off(lane, m);
 
-  float s1 = 0.f, s2 = 0.f;
+  float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
   if (ta < tb) {
     issue(ta, 0);
     wait_vm0();
@@ -312,26 +356,46 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
         if (!(ua >= lo && ua < hi)) a = 0.f;
         if (!(ub >= lo && ub < hi)) b = 0.f;
       }
+      const float a2 = __fmul_rn(a, a), b2 = __fmul_rn(b, b);
       s1 += a;
-      s2 += __fmul_rn(a, a);
+      s2 += a2;
       s1 += b;
-      s2 += __fmul_rn(b, b);
+      s2 += b2;
+      if constexpr (DG) {
+        s3 += __fmul_rn(a2, a);
+        s4 += __fmul_rn(a2, a2);
+        s3 += __fmul_rn(b2, b);
+        s4 += __fmul_rn(b2, b2);
+      }
     }
     wait_vm0();
     __syncthreads();
   }
   s1 += __shfl_xor(s1, 32);
   s2 += __shfl_xor(s2, 32);
+  if constexpr (DG) {
+    s3 += __shfl_xor(s3, 32);
+    s4 += __shfl_xor(s4, 32);
+  }
   if (half == 0 && t < p.g.T) {
-    float* m = p.mom + (static_cast<int64_t>(split) * p.g.T + t) * 2;
+    float* m = p.mom + (static_cast<int64_t>(split) * p.g.T + t) * MS;
     m[0] = s1;
     m[1] = s2;
+    if constexpr (DG) {
+      m[2] = s3;
+      m[3] = s4;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
 // main: fused score / read / gate / write for one (token tile, N-split).
 // ---------------------------------------------------------------------------
+// Per-token partial slots of the main kernel with diagnostics (kTokPartDiag
+// floats per (split, row)); slots 0-2 are sum gate, sum intensity, active count.
+constexpr int kTokPartDiag = 12;
+enum { TP_SMAX = 4, TP_STRONG, TP_BOUND, TP_075, TP_030, TP_CAP, TP_GLOGG };
+
 // Rows of the main kernel are "virtual tokens" v = t * routes + r: h, tau,
 // outputs and every partial are indexed by v, x by v / routes (paired QK runs
 // as 2T rows sharing each x row).
@@ -344,13 +408,22 @@ struct MainParams {
   const uint16_t* wp;    // packed W^T fragments
   const float* tau;      // [T] thresholds (srw_tau_kernel)
   float* out_part;       // [S][T][D]
-  float* tok_part;       // [S][T][4]: sum gate, sum intensity, active count, -
+  float* tok_part;       // [S][T][TPS]: sum gate, sum intensity, active count, - [, diagnostics]
+  float* unit_diag;      // [N][SRW_UDIAG_COUNT] (diagnostics) or null
   uint32_t* mask32;      // [T][mask_words32] or null
   int64_t mask_words32;
   Geometry g;
   GateParams gp;
   float exp_scale;       // -sharpness * log2(e)
 };
+
+// v4.1 gate of a margin m = s - tau - thr (v41:503-511), with the kernels' operations
+__device__ inline float gate_of_margin(float m, const GateParams& gp, float exp_scale) {
+  const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(m * exp_scale));
+  const float inten = gp.eps + __builtin_amdgcn_fmed3f(m - gp.cut, 0.0f, gp.maxi);
+  return act * inten;
+}
+__device__ inline float gate_of_margin(float m, const MainParams& p) { return gate_of_margin(m, p.gp, p.exp_scale); }
 
 // Software pipeline over the split's 32-unit tiles.  Iteration i runs the
 // score/read GEMMs of tile i+1 interleaved (sched_group_barrier) with the gate
@@ -690,9 +763,12 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
 // ---------------------------------------------------------------------------
 constexpr int kWsThreads = 512;
 
-template <int DB, int KH, bool HX>
+// DG: training diagnostics -- per-token extras in tok_part (TPS = 12), per-unit
+// score sums and gate maxima into unit_diag (atomics)
+template <int DB, int KH, bool HX, bool DG>
 __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
+  constexpr int TPS = DG ? kTokPartDiag : 4;
   constexpr int D = DB * 32;
   constexpr int DR = KH * 16;
   constexpr int KX = D / 16;
@@ -773,6 +849,13 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
     for (int m = 0; m < TileE::NM; ++m) le[m] = TileE::lane_off(lane, m);
 #pragma unroll
     for (int m = 0; m < TileR::NM; ++m) lr[m] = F_E * kFragBytes + TileR::lane_off(lane, m);
+    // diagnostics (v41:519-534): the row's max score, act-band counts as
+    // thresholds on the exp argument (act > 0.9 <=> arg < -log2 9; 0.1 < act <
+    // 0.9 <=> |arg| < log2 9; 0.05 / 0.95: log2 19; 0.2 / 0.8: 2), capped
+    // intensities (s >= tau + thr + cut + max_intensity - 1e-3)
+    const float tau_t = DG ? p.tau[tl] : 0.f;
+    float smax = -INFINITY, isum = 0.f;
+    uint32_t n_strong = 0, n_bound = 0, n_075 = 0, n_030 = 0, n_cap = 0, nact = 0;
     // Drain the x / h loads here: left pending into the tile loop, they make
     // the compiler wait for every load in flight (the next tile's LDS
     // prefetch included) at the top of each iteration.
@@ -788,7 +871,7 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
         // otherwise all score steps, then all read steps; LDS operands are
         // read PF MFMAs ahead
         const char* base = er_base + (it & 1) * ER_STAGE;
-        constexpr int NM = KH + KX, PF = 8;
+        constexpr int NM = KH + KX, PF = DG ? 4 : 8;
         auto frag = [&](int k) {
           const bool is_score = HX ? !(k & 1) : (k < KH);
           const int ks = HX ? (k >> 1) : (k < KH ? k : k - KH);
@@ -821,6 +904,65 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
           sx[4 * q + 2] = pack_bf16(racc[4 * q], racc[4 * q + 1]);      // bf16 x.r (v41:517)
           sx[4 * q + 3] = pack_bf16(racc[4 * q + 2], racc[4 * q + 3]);
         }
+        if constexpr (DG) {
+          // per-unit sum of scores and max of (score - tau) over this wave's 32
+          // tokens (v41:445-447, 543-552): butterfly over the lanes of each half
+          const int64_t u0 = static_cast<int64_t>(ta + it) * kUnitTile;
+          const float tau_thr = tau_t + p.gp.thr;
+          const float k_exp = -tau_thr * p.exp_scale;
+          const float tau_cut = tau_thr + p.gp.cut;
+          const float cap_s = tau_cut + (p.gp.maxi - 1e-3f);
+          const bool full = u0 >= lo && u0 + kUnitTile <= hi;
+          uint32_t bits = 0;
+          float su[16], mx[16];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const uint32_t pr = sx[4 * (v >> 2) + ((v & 3) >> 1)];
+            const float sv = (v & 1) ? hi_f32(pr) : lo_f32(pr);
+            const int64_t u = u0 + unit_of_acc(v, half);
+            const bool uok = full || (u >= lo && u < hi);
+            const bool ok = t < p.g.T && uok;
+            su[v] = ok ? sv : 0.f;
+            mx[v] = ok ? sv - tau_t : -INFINITY;
+            const float arg = fmaf(sv, p.exp_scale, k_exp);
+            const float aa = fabsf(arg);
+            smax = fmaxf(smax, uok ? sv : -INFINITY);
+            n_strong += (uok && arg < -3.169925001442312f) ? 1u : 0u;
+            n_bound += (uok && aa < 3.169925001442312f) ? 1u : 0u;
+            n_075 += (uok && aa < 4.247927513443585f) ? 1u : 0u;
+            n_030 += (uok && aa < 2.0f) ? 1u : 0u;
+            n_cap += (uok && sv >= cap_s) ? 1u : 0u;
+            // intensity sum and pass bits (v41:503-511, 528) as in the gate epilogue
+            const float inten = p.gp.eps + __builtin_amdgcn_fmed3f(sv - tau_cut, 0.0f, p.gp.maxi);
+            isum += uok ? inten : 0.f;
+            bits = __builtin_amdgcn_alignbit(bits, uok ? __float_as_uint(arg) : 0u, 31);
+          }
+          {
+            const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
+            uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
+            m <<= 4 * half;
+            nact += __builtin_popcount(m);
+            m |= __shfl_xor(m, 32);
+            if (p.mask32 && half == 0 && t < p.g.T) {
+              uint32_t* dst = p.mask32 + t * p.mask_words32 + (ta + it);
+              const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
+              if (shared) atomicOr(dst, m);
+              else *dst = m;
+            }
+          }
+          reduce_scatter16(su, lane, [](float x, float y) { return x + y; });
+          reduce_scatter16(mx, lane, [](float x, float y) { return fmaxf(x, y); });
+          const int k = 8 * (lane & 1) + 4 * ((lane >> 1) & 1) + 2 * ((lane >> 2) & 1) + ((lane >> 3) & 1);
+          const int64_t u = u0 + unit_of_acc(k, half);
+          if (p.unit_diag && !(lane & 16) && u >= lo && u < hi) {
+            atomicAdd(p.unit_diag + u * SRW_UDIAG_COUNT + SRW_UDIAG_SCORE_SUM, su[0]);
+            if (mx[0] > -INFINITY) {
+              const float g = gate_of_margin(mx[0] - p.gp.thr, p);
+              atomicMax(reinterpret_cast<unsigned int*>(p.unit_diag + u * SRW_UDIAG_COUNT + SRW_UDIAG_GATE_MAX),
+                        __float_as_uint(g));
+            }
+          }
+        }
       }
       barrier_lds();  // mid: consumers have read S (tile it - 1)
       if (it < n) {
@@ -831,6 +973,27 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
       }
       wait_vm0();
       barrier_lds();  // end: S, next E/R and W^T visible
+    }
+    if constexpr (DG) {
+      smax = fmaxf(smax, __shfl_xor(smax, 32));
+      n_strong += __shfl_xor(n_strong, 32);
+      n_bound += __shfl_xor(n_bound, 32);
+      n_075 += __shfl_xor(n_075, 32);
+      n_030 += __shfl_xor(n_030, 32);
+      n_cap += __shfl_xor(n_cap, 32);
+      isum += __shfl_xor(isum, 32);
+      nact += __shfl_xor(nact, 32);
+      if (half == 0 && t < p.g.T) {
+        float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * TPS;
+        tp[1] = isum;
+        tp[2] = static_cast<float>(nact);
+        tp[TP_SMAX] = smax;
+        tp[TP_STRONG] = static_cast<float>(n_strong);
+        tp[TP_BOUND] = static_cast<float>(n_bound);
+        tp[TP_075] = static_cast<float>(n_075);
+        tp[TP_030] = static_cast<float>(n_030);
+        tp[TP_CAP] = static_cast<float>(n_cap);
+      }
     }
   } else {
     // ---------------- consumer: gate epilogue and write GEMM, one tile behind ----------------
@@ -846,6 +1009,7 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
     const float c_exp = p.exp_scale, eps = p.gp.eps, maxi = p.gp.maxi;
     float gsum = 0.f, isum = 0.f;
     uint32_t nact = 0;
+    float glogg = 0.f;  // diagnostics: sum gate * log2(gate + 1e-8) (v41:533-534)
     f32x16_t oacc[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
@@ -883,8 +1047,12 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
             sign = ok ? sign : 0u;
           }
           gsum += g;
-          isum += inten;
-          bits = __builtin_amdgcn_alignbit(bits, sign, 31);     // bits << 1 | active
+          if constexpr (DG) {
+            glogg = fmaf(g, __builtin_amdgcn_logf(g + 1e-8f), glogg);
+          } else {
+            isum += inten;
+            bits = __builtin_amdgcn_alignbit(bits, sign, 31);   // bits << 1 | active
+          }
           g2[e] = g;
         }
         const uint32_t gq = pack_bf16(g2[0], g2[1]);             // gate_bf (v41:516)
@@ -911,8 +1079,8 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
           bits = gate_tile(std::integral_constant<bool, true>{}, u0, pk, wtile, it & 1);
         else
           bits = gate_tile(std::integral_constant<bool, false>{}, u0, pk, wtile, it & 1);
-        // pass bitmask of the tile
-        {
+        // pass bitmask of the tile (the producer emits it with diagnostics)
+        if constexpr (!DG) {
           const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
           uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
           m <<= 4 * half;
@@ -929,7 +1097,7 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
         // write GEMM: OUT[32 tok x D] += P[32 tok x 32 units] . W_t[32 units x D]
         const char* wb = w_base + ((it - 1) & 1) * W_STAGE + lane * 16;
         const u32x4_t a0 = {pk[0], pk[1], pk[2], pk[3]}, a1 = {pk[4], pk[5], pk[6], pk[7]};
-        constexpr int NC = 2 * DB, PF = 6;
+        constexpr int NC = 2 * DB, PF = DG ? 4 : 6;
         auto frag = [&](int k) {  // MFMA k: j = k / DB, db = k % DB
           return *reinterpret_cast<const u32x4_t*>(wb + (2 * (k % DB) + k / DB) * kFragBytes);
         };
@@ -952,11 +1120,16 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
     gsum += __shfl_xor(gsum, 32);
     isum += __shfl_xor(isum, 32);
     nact += __shfl_xor(nact, 32);
+    if constexpr (DG) glogg += __shfl_xor(glogg, 32);
     if (half == 0 && t < p.g.T) {
-      float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * 4;
+      float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * TPS;
       tp[0] = gsum;
-      tp[1] = isum;
-      tp[2] = static_cast<float>(nact);
+      if constexpr (DG) {
+        tp[TP_GLOGG] = glogg * 0.69314718055994531f;  // log2 -> ln
+      } else {
+        tp[1] = isum;
+        tp[2] = static_cast<float>(nact);
+      }
     }
     float* op = p.out_part + static_cast<int64_t>(split) * p.g.T * D;
     if (tw + 32 <= p.g.T) {
@@ -978,26 +1151,47 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
 
 // ---------------------------------------------------------------------------
 // tau: per row, the moment partials -> tau = mean + tau_offset * (sqrt(E[s^2]
-// - mean^2) + 1e-8) (v41:461-464).  One wave per row; lanes split the partials.
+// - mean^2) + 1e-8) (v41:461-464).  One wave per row; lanes split the
+// partials.  mom holds ms floats per (split, row): s, s^2 [, s^3, s^4].  With
+// token_diag, also the row's mean, std, tau and third / fourth power sums
+// (zero without them).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void srw_tau_kernel(const float* __restrict__ mom, const float* __restrict__ tau_off,
-                                                      float* __restrict__ tau, int64_t T, int S_st, int64_t N) {
+                                                      float* __restrict__ tau, int64_t T, int S_st, int64_t N, int ms,
+                                                      float* __restrict__ token_diag) {
   const int lane = threadIdx.x & 63;
   const int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  float a = 0.f, b = 0.f;
+  float a = 0.f, b = 0.f, c = 0.f, d = 0.f;
   for (int s = lane; s < S_st; s += 64) {
-    const float* m = mom + (static_cast<int64_t>(s) * T + t) * 2;
+    const float* m = mom + (static_cast<int64_t>(s) * T + t) * ms;
     a += m[0];
     b += m[1];
+    if (ms == 4) {
+      c += m[2];
+      d += m[3];
+    }
   }
   a = wave_sum(a);
   b = wave_sum(b);
+  if (token_diag && ms == 4) {
+    c = wave_sum(c);
+    d = wave_sum(d);
+  }
   if (lane == 0) {
     const float fN = static_cast<float>(N);
     const float mean = a / fN;
     const float sd = sqrtf(b / fN - __fmul_rn(mean, mean)) + 1e-8f;
-    tau[t] = mean + __fmul_rn(tau_off[t], sd);
+    const float tv = mean + __fmul_rn(tau_off[t], sd);
+    tau[t] = tv;
+    if (token_diag) {
+      float* td = token_diag + t * SRW_TDIAG_COUNT;
+      td[SRW_TDIAG_S_MEAN] = mean;
+      td[SRW_TDIAG_S_STD] = sd;
+      td[SRW_TDIAG_TAU] = tv;
+      td[SRW_TDIAG_SUM_S3] = c;
+      td[SRW_TDIAG_SUM_S4] = d;
+    }
   }
 }
 
@@ -1017,6 +1211,11 @@ struct FinalParams {
   int64_t T;
   int D, S, spc;
   float scale;
+  int tps;               // floats per (split, row) in tok_part: 4, or kTokPartDiag with diagnostics
+  const float* tau;      // [T] (diagnostics)
+  float* token_diag;     // [T][SRW_TDIAG_COUNT] or null
+  GateParams gp;
+  float exp_scale;
 };
 
 __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
@@ -1025,7 +1224,7 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
   const int tid = threadIdx.x;
   float gs = 0.f, is = 0.f, na = 0.f;
   for (int s = tid; s < p.S; s += 256) {
-    const float* tp = p.tok_part + (static_cast<int64_t>(s) * p.T + t) * 4;
+    const float* tp = p.tok_part + (static_cast<int64_t>(s) * p.T + t) * p.tps;
     gs += tp[0];
     is += tp[1];
     na += tp[2];
@@ -1066,6 +1265,36 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
     if (p.den) p.den[t] = den;
     if (p.n_active) p.n_active[t] = static_cast<int32_t>(NA);
   }
+  if (p.token_diag && tid < 64) {
+    // per-token diagnostics (v41:519-534); gate and intensity are
+    // non-decreasing in the score, so their maxima follow from the max score
+    float smax = -INFINITY, c[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = tid; s < p.S; s += 64) {
+      const float* tp = p.tok_part + (static_cast<int64_t>(s) * p.T + t) * p.tps;
+      smax = fmaxf(smax, tp[TP_SMAX]);
+#pragma unroll
+      for (int k = 0; k < 6; ++k) c[k] += tp[TP_STRONG + k];
+    }
+    smax = wave_max(smax);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) c[k] = wave_sum(c[k]);
+    if (tid == 0) {
+      const float tau_thr = p.tau[t] + p.gp.thr;
+      const float tau_cut = tau_thr + p.gp.cut;
+      const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(smax, p.exp_scale, -tau_thr * p.exp_scale)));
+      const float imax = p.gp.eps + __builtin_amdgcn_fmed3f(smax - tau_cut, 0.0f, p.gp.maxi);
+      float* td = p.token_diag + t * SRW_TDIAG_COUNT;
+      td[SRW_TDIAG_GATE_MAX] = act * imax;
+      td[SRW_TDIAG_INT_SUM] = I;
+      td[SRW_TDIAG_N_STRONG] = c[0];
+      td[SRW_TDIAG_N_BOUNDARY] = c[1];
+      td[SRW_TDIAG_N_BAND075] = c[2];
+      td[SRW_TDIAG_N_BAND030] = c[3];
+      td[SRW_TDIAG_N_INT_CAP] = c[4];
+      td[SRW_TDIAG_G_LOG_G] = c[5];
+      td[SRW_TDIAG_INT_MAX] = imax;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1078,33 +1307,44 @@ struct Kernels {
   int main_lds;  // bytes
 };
 
-// WS: the warp-specialised main kernel (when both roles fit 256 registers)
+// WS: the warp-specialised main kernel (when both roles fit 256 registers);
+// DG: with training diagnostics (warp-specialised kernels only)
 template <int DB, int KH, bool HX, bool WS>
-Kernels kernels_of() {
-  if constexpr (WS)
-    return Kernels{srw_stats_kernel<KH>, srw_main_ws_kernel<DB, KH, HX>, kWsThreads,
-                   (2 * (KH + 2 * DB) + 2 * 2 * DB + 16) * kFragBytes};  // 2 E/R, 2 W^T, S
-  else
-    return Kernels{srw_stats_kernel<KH>, srw_main_kernel<DB, KH, HX>, kThreads,
+Kernels kernels_of(bool dg) {
+  if constexpr (WS) {
+    constexpr int lds = (2 * (KH + 2 * DB) + 2 * 2 * DB + 16) * kFragBytes;  // 2 E/R, 2 W^T, S
+    if (dg) return Kernels{srw_stats_kernel<KH, true>, srw_main_ws_kernel<DB, KH, HX, true>, kWsThreads, lds};
+    return Kernels{srw_stats_kernel<KH, false>, srw_main_ws_kernel<DB, KH, HX, false>, kWsThreads, lds};
+  } else {
+    return Kernels{srw_stats_kernel<KH, false>, srw_main_kernel<DB, KH, HX>, kThreads,
                    2 * (KH + 2 * DB + 2 * DB) * kFragBytes};
+  }
 }
 
 // Instantiated shapes (d_model, d_route); for d_route == d_model there is a
 // variant whose score operand is the x registers themselves (h aliases x).
-bool pick(int64_t D, int64_t dr, bool hx, Kernels* k) {
+bool pick(int64_t D, int64_t dr, bool hx, bool dg, Kernels* k) {
   if (hx && D == dr) {
-    if (D == 384) { *k = kernels_of<12, 24, true, true>(); return true; }
-    if (D == 128) { *k = kernels_of<4, 8, true, true>(); return true; }
-    if (D == 64) { *k = kernels_of<2, 4, true, true>(); return true; }
+    if (D == 384) { *k = kernels_of<12, 24, true, true>(dg); return true; }
+    if (D == 128) { *k = kernels_of<4, 8, true, true>(dg); return true; }
+    if (D == 64) { *k = kernels_of<2, 4, true, true>(dg); return true; }
   }
-  if (D == 384 && dr == 384) { *k = kernels_of<12, 24, false, false>(); return true; }
-  if (D == 384 && dr == 128) { *k = kernels_of<12, 8, false, true>(); return true; }
-  if (D == 128 && dr == 128) { *k = kernels_of<4, 8, false, true>(); return true; }
-  if (D == 128 && dr == 64) { *k = kernels_of<4, 4, false, true>(); return true; }
-  if (D == 64 && dr == 64) { *k = kernels_of<2, 4, false, true>(); return true; }
-  if (D == 64 && dr == 32) { *k = kernels_of<2, 2, false, true>(); return true; }
+  if (D == 384 && dr == 384) {
+    if (dg) return false;  // the pipelined single-role kernel has no diagnostics variant
+    *k = kernels_of<12, 24, false, false>(false);
+    return true;
+  }
+  if (D == 384 && dr == 128) { *k = kernels_of<12, 8, false, true>(dg); return true; }
+  if (D == 128 && dr == 128) { *k = kernels_of<4, 8, false, true>(dg); return true; }
+  if (D == 128 && dr == 64) { *k = kernels_of<4, 4, false, true>(dg); return true; }
+  if (D == 64 && dr == 64) { *k = kernels_of<2, 4, false, true>(dg); return true; }
+  if (D == 64 && dr == 32) { *k = kernels_of<2, 2, false, true>(dg); return true; }
   return false;
 }
+
+bool with_diag(const srw_desc_t& d) { return (d.flags & SRW_FLAG_DIAG) != 0; }
+int mom_stride(const srw_desc_t& d) { return with_diag(d) && d.stats_mode == SRW_STATS_ONEPASS ? 4 : 2; }
+int tok_part_stride(const srw_desc_t& d) { return with_diag(d) ? kTokPartDiag : 4; }
 
 Geometry geometry(const srw_desc_t& d, int64_t chunk) {
   Geometry g{};
@@ -1144,7 +1384,7 @@ WsLayout ws_layout(const srw_desc_t& d, const Geometry& g) {
   w.wp = off;
   off += al(static_cast<size_t>(g.ntiles) * kUnitTile * d.d_model * 2);
   w.mom = off;
-  off += al(static_cast<size_t>(g.S_st) * g.T * 2 * 4);
+  off += al(static_cast<size_t>(g.S_st) * g.T * mom_stride(d) * 4);
   w.tau = off;
   off += al(static_cast<size_t>(g.T) * 4);
   w.gram = off;
@@ -1152,7 +1392,7 @@ WsLayout ws_layout(const srw_desc_t& d, const Geometry& g) {
   w.out_part = off;
   off += al(static_cast<size_t>(g.S) * g.T * d.d_model * 4);
   w.tok_part = off;
-  off += al(static_cast<size_t>(g.S) * g.T * 4 * 4);
+  off += al(static_cast<size_t>(g.S) * g.T * tok_part_stride(d) * 4);
   w.total = off;
   return w;
 }
@@ -1172,13 +1412,13 @@ hipError_t pack_unit_major(const uint16_t* src, uint16_t* dst, int64_t N, int D,
   return hipGetLastError();
 }
 
-bool mfma_supports(const srw_desc_t& d) {
+bool mfma_supports(const srw_desc_t& d, bool h_is_x) {
   if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41) return false;
   if (d.stats_mode != SRW_STATS_ONEPASS && !(d.stats_mode == SRW_STATS_GRAM && gram_supports(d.d_route))) return false;
   if (d.n_routes != 1 && d.n_routes != 2) return false;  // paired QK: 2 rows per token
-  if (d.flags & (SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
+  if (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
   Kernels k;
-  if (!pick(d.d_model, d.d_route, false, &k)) return false;  // the aliasing variant is optional
+  if (!pick(d.d_model, d.d_route, h_is_x, with_diag(d), &k)) return false;
   // every reference chunk must hold at least one whole 32-unit tile
   const int64_t cs = chunk_of(d);
   const int64_t last = d.n_units - ((d.n_units + cs - 1) / cs - 1) * cs;
@@ -1194,8 +1434,9 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   const srw_desc_t& d = a.d;
   *path_name = "mfma_bf16";
   const bool hx = a.in.h == a.in.x;
+  const bool dg = with_diag(d);
   Kernels k;
-  if (!pick(d.d_model, d.d_route, hx, &k)) return hipErrorNotSupported;
+  if (!pick(d.d_model, d.d_route, hx, dg, &k)) return hipErrorNotSupported;
   const Geometry g = geometry(d, a.chunk);
   const WsLayout L = ws_layout(d, g);
   if (a.ws_bytes < L.total) return hipErrorInvalidValue;
@@ -1212,6 +1453,9 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
 
   float* tau = reinterpret_cast<float*>(a.ws + L.tau);
   const bool cached = (d.flags & SRW_FLAG_POOL_CACHED) != 0;
+  float* token_diag = dg ? a.o.token_diag : nullptr;
+  float* unit_diag = dg ? a.o.unit_diag : nullptr;
+  if (unit_diag && (e = fill_f32(unit_diag, d.n_units * SRW_UDIAG_COUNT, 0.f, a.stream)) != hipSuccess) return e;
 
   // pack W^T (kept in the workspace across calls that declare the pool cached)
   if (!cached) {
@@ -1246,7 +1490,8 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   }
   // tau per row from the moment partials
   hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((g.T + 3) / 4)), dim3(256), 0, a.stream, mom,
-                     a.in.tau_offset, tau, g.T, g.S_st, g.N);
+                     a.in.tau_offset, tau, g.T, g.S_st, g.N, d.stats_mode == SRW_STATS_GRAM ? 2 : mom_stride(d),
+                     token_diag);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   // main
   {
@@ -1260,6 +1505,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     mp.tau = tau;
     mp.out_part = out_part;
     mp.tok_part = tok_part;
+    mp.unit_diag = unit_diag;
     mp.mask32 = mask32;
     mp.mask_words32 = mw32;
     mp.g = g;
@@ -1288,6 +1534,11 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     fp.S = g.S;
     fp.spc = g.spc;
     fp.scale = d.scale;
+    fp.tps = tok_part_stride(d);
+    fp.tau = tau;
+    fp.token_diag = token_diag;
+    fp.gp = a.gp;
+    fp.exp_scale = -d.sharpness * 1.4426950408889634f;
     hipLaunchKernelGGL(srw_finalize_kernel, dim3(static_cast<unsigned>(g.T)), dim3(256), 0, a.stream, fp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }

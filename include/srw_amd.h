@@ -178,7 +178,9 @@ const char* srw_status_string(srw_status_t status);
  * zero shapes. */
 srw_status_t srw_desc_init(srw_desc_t* desc);
 
-/* Validate *desc and report the workspace (device bytes) srw_forward needs. */
+/* Validate *desc and report the workspace (device bytes) srw_forward needs:
+ * the larger of the kernel families the call may take (with d_route ==
+ * d_model and one route, passing h == x can select a different family). */
 srw_status_t srw_workspace_size(const srw_desc_t* desc, size_t* bytes);
 
 /* Enqueue one SRW layer forward on `stream`.  Replaces fused_gate_srw /

@@ -289,3 +289,75 @@ def test_mfma_pool_cached_reuses_pool_data(pkg, dev, stats):
     assert not torch.equal(first.cpu(), fresh["out"])
     ref, tr = _oracle(b, 2500)
     _check(fresh, ref, tr, T, N, D, extra_delta=_gram_delta(b, tr) if stats == "gram" else None)
+
+
+def _diag_scores(inp, hx, R):
+    """bf16 scores [T, R, N] as the reference rounds them (v41:439)."""
+    T = inp["x"].shape[0]
+    h = inp["x"][:, None] if hx else inp["h"]
+    s = h.to(torch.bfloat16).float() @ inp["emb"].to(torch.bfloat16).float().T
+    return s.to(torch.bfloat16).float().reshape(T, R, -1)
+
+
+DIAG_CASES = [
+    # T, D, dr, N, h_is_x, routes, max_chunk, seed
+    (256, 384, 384, 6000, True, 1, 2500, 41),   # Know form, two reference chunks
+    (200, 384, 128, 1580, False, 2, 12500, 42),  # paired QK pool with the router's d_route
+    (130, 128, 64, 1000, False, 1, 300, 43),    # four chunks, ragged T
+]
+
+
+@pytest.mark.parametrize("case", DIAG_CASES, ids=lambda c: "T{}D{}dr{}N{}R{}".format(c[0], c[1], c[2], c[3], c[5]))
+def test_mfma_diagnostics_match_generic(pkg, dev, case):
+    """SRW_FLAG_DIAG on the matrix-core path: token_diag [T,R,14] and
+    unit_diag [N,2] against the reference-faithful scalar kernels
+    (v41:442-552).  Band counts use thresholds on the exp argument (the exact
+    inverse of the act thresholds), so elements within rounding of a band edge
+    may fall on the other side: counts agree to 2 + 1e-3 N."""
+    T, D, dr, N, hx, R, max_chunk, seed = case
+    print(f"[gpu] mfma diagnostics {case}", flush=True)
+    shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=R, h_is_x=hx)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=seed)
+    inp["tau_offset"].uniform_(-0.9, 0.3)
+    _, cs = srw_ref.chunk_plan(N, max_chunk)
+    x = inp["x"].to(BF).to(dev)
+    h = x if hx else inp["h"].to(BF).to(dev)
+    args = (x, h, inp["emb"].to(BF).to(dev), inp["tau_offset"].to(dev), inp["read"].to(BF).to(dev),
+            inp["write"].to(BF).to(dev))
+    fast = pkg.srw_forward(*args, chunk_size=cs, diag=True)
+    slow = pkg.srw_forward(*args, chunk_size=cs, diag=True, emulate=True)
+    torch.cuda.synchronize()
+    assert fast["path"] == "mfma_bf16" and slow["path"] == "generic"
+    f = {k: v.cpu() for k, v in fast.items() if isinstance(v, torch.Tensor)}
+    g = {k: v.cpu() for k, v in slow.items() if isinstance(v, torch.Tensor)}
+    assert rel_fro(f["out"].float(), g["out"].float()) <= 5e-3
+    assert torch.allclose(f["den"], g["den"], rtol=2e-4)
+    td_f, td_g = f["token_diag"], g["token_diag"]
+    names = ["s_mean", "s_std", "tau", "sum_s3", "sum_s4", "gate_max", "int_sum", "n_strong",
+             "n_boundary", "n_band075", "n_band030", "g_log_g", "int_max", "n_int_cap"]
+    col = {n: i for i, n in enumerate(names)}
+    for n in ("s_mean", "s_std", "tau"):
+        assert torch.allclose(td_f[..., col[n]], td_g[..., col[n]], rtol=1e-4, atol=1e-5), n
+    # power sums of the bf16 scores: the two paths accumulate each score in a
+    # different fp32 order, so a score can round to the neighbouring bf16
+    # value (about 1 in 10^3 near a rounding midpoint); bound the deviation by
+    # a fraction of sum_n k |s|^(k-1) ulp(s) computed from the oracle's scores
+    sc = _diag_scores(inp, hx, R)
+    for k, n in ((3, "sum_s3"), (4, "sum_s4")):
+        sens = (k * sc.abs() ** (k - 1) * bf16_ulp(sc)).sum(dim=-1).reshape(td_g[..., 0].shape)
+        d = (td_f[..., col[n]] - td_g[..., col[n]]).abs()
+        bound = 0.02 * sens + 1e-5 * (sc.abs() ** k).sum(dim=-1).reshape(d.shape)
+        print(f"  {n}: max |diff| {float(d.max()):.3e}, max diff/bound {float((d / bound).max()):.3f}", flush=True)
+        assert (d <= bound).all(), n
+    for n in ("gate_max", "int_max", "int_sum"):
+        assert torch.allclose(td_f[..., col[n]], td_g[..., col[n]], rtol=2e-3, atol=1e-6), n
+    assert torch.allclose(td_f[..., col["g_log_g"]], td_g[..., col["g_log_g"]], rtol=2e-3,
+                          atol=1e-3), "g_log_g"
+    for n in ("n_strong", "n_boundary", "n_band075", "n_band030", "n_int_cap"):
+        d = (td_f[..., col[n]] - td_g[..., col[n]]).abs()
+        print(f"  {n}: max |diff| {float(d.max())}", flush=True)
+        assert (d <= 2 + 1e-3 * N).all(), n
+    ud_f, ud_g = f["unit_diag"], g["unit_diag"]
+    assert torch.allclose(ud_f[:, 0], ud_g[:, 0], rtol=1e-3, atol=1e-3 * (T * R) ** 0.5), "score_sum"
+    assert torch.allclose(ud_f[:, 1], ud_g[:, 1], rtol=2e-3, atol=1e-6), "unit gate_max"
+    assert torch.equal(f["n_active"], g["n_active"]) or int((f["n_active"] - g["n_active"]).abs().max()) <= 2
