@@ -39,7 +39,7 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 # 256 MiB copy (--calibrate-copy 256): FETCH x 2.00, WRITE x 1.00.  Keyed by
 # (workload, stats mode); profiles/know_T4096_N25200_traffic.md has the runs.
 MEASURED_TRAFFIC = {
-    ("know", "onepass"): (42938 * 2.0 + 63612 * 1.0) * 1024,
+    ("know", "onepass"): (41148 * 2.0 + 64190 * 1.0) * 1024,
 }
 
 WORKLOADS = {
