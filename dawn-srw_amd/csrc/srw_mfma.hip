@@ -1218,10 +1218,19 @@ struct FinalParams {
   float exp_scale;
 };
 
+// NG: split groups per workgroup.  One workgroup per (row, block of 256 / NG
+// columns); thread (g, c) = (tid / CW, tid % CW) sums column c over splits
+// s = g, g + NG, ... of each chunk with eight loads in flight; the NG group
+// sums of a chunk combine in a fixed order, so the result is deterministic.
+// Few splits per chunk (large T) use NG = 1, many (decode) NG = 16.
+template <int NG>
 __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
+  constexpr int CW = 256 / NG;
   __shared__ float red[3][4];
+  __shared__ float part[NG > 1 ? NG : 1][CW];
   const int64_t t = blockIdx.x;
   const int tid = threadIdx.x;
+  const int g = tid / CW, c = tid % CW;
   float gs = 0.f, is = 0.f, na = 0.f;
   for (int s = tid; s < p.S; s += 256) {
     const float* tp = p.tok_part + (static_cast<int64_t>(s) * p.T + t) * p.tps;
@@ -1243,23 +1252,38 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
   const float NA = red[2][0] + red[2][1] + red[2][2] + red[2][3];
   const float den = fmaxf(I, 1.0f);                          // v41:584
   const int64_t stride = p.T * p.D;
-  for (int d = tid; d < p.D; d += 256) {
-    const float* col = p.out_part + t * p.D + d;
-    float raw = 0.f;
-    for (int s0 = 0; s0 < p.S; s0 += p.spc) {                // one reference chunk
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      int s = s0;
-      for (; s + 8 <= s0 + p.spc; s += 8) {
+  const int d = blockIdx.y * CW + c;
+  const bool dok = d < p.D;
+  const float* col = p.out_part + t * p.D + (dok ? d : 0);
+  float raw = 0.f;
+  for (int s0 = 0; s0 < p.S; s0 += p.spc) {                  // one reference chunk
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int s = s0 + g;
+    for (; s + 7 * NG < s0 + p.spc; s += 8 * NG) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] += col[(s + j) * stride];
-      }
-      for (; s < s0 + p.spc; ++s) acc[0] += col[s * stride];
-      const float c = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
-      raw += round_bf16(c);                                  // bf16 dot output (v41:518)
+      for (int j = 0; j < 8; ++j) acc[j] += col[(s + NG * j) * stride];
     }
+    for (; s < s0 + p.spc; s += NG) acc[0] += col[s * stride];
+    const float sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    if constexpr (NG == 1) {
+      raw += round_bf16(sum);                                // bf16 dot output (v41:518)
+    } else {
+      part[g][c] = sum;
+      __syncthreads();
+      if (g == 0) {
+        float q = part[0][c];
+#pragma unroll
+        for (int k = 1; k < NG; ++k) q += part[k][c];
+        raw += round_bf16(q);                                // bf16 dot output (v41:518)
+      }
+      __syncthreads();
+    }
+  }
+  if (g == 0 && dok) {
     const float o = round_bf16(raw / den);                  // v41:585-586
     p.out[t * p.D + d] = f32_to_bf16_bits(o * p.scale);
   }
+  if (blockIdx.y != 0) return;
   if (tid == 0) {
     if (p.gate_sum) p.gate_sum[t] = G;
     if (p.den) p.den[t] = den;
@@ -1539,7 +1563,12 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     fp.token_diag = token_diag;
     fp.gp = a.gp;
     fp.exp_scale = -d.sharpness * 1.4426950408889634f;
-    hipLaunchKernelGGL(srw_finalize_kernel, dim3(static_cast<unsigned>(g.T)), dim3(256), 0, a.stream, fp);
+    // split groups per workgroup from the splits per chunk
+    const int ng = g.spc >= 64 ? 16 : (g.spc >= 16 ? 4 : 1);
+    const dim3 grid_f(static_cast<unsigned>(g.T), static_cast<unsigned>((D + 256 / ng - 1) / (256 / ng)));
+    if (ng == 16) hipLaunchKernelGGL(srw_finalize_kernel<16>, grid_f, dim3(256), 0, a.stream, fp);
+    else if (ng == 4) hipLaunchKernelGGL(srw_finalize_kernel<4>, grid_f, dim3(256), 0, a.stream, fp);
+    else hipLaunchKernelGGL(srw_finalize_kernel<1>, grid_f, dim3(256), 0, a.stream, fp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return hipSuccess;
