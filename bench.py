@@ -123,6 +123,9 @@ def main() -> int:
     ap.add_argument("--pool-cached", action="store_true",
                     help="steps after the first reuse the pool data kept in the workspace "
                          "(SRW_FLAG_POOL_CACHED: decode steps / layers sharing one pool)")
+    ap.add_argument("--graph", action="store_true",
+                    help="capture one call in a HIP graph and time graph replays (launch-bound "
+                         "shapes such as decode)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="first run one device-to-device copy of MB MiB (a known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -181,6 +184,24 @@ def main() -> int:
     log(f"warm-up done, path={plan.path}, mean active/token="
         f"{plan.n_active.float().mean().item():.1f}")
 
+    graph = None
+    if args.graph:
+        # a side stream for capture, as torch requires; replays run on `stream`
+        cap = torch.cuda.Stream(dev)
+        cap.wait_stream(stream)
+        with torch.cuda.stream(cap):
+            plan.launch(cap, pool_cached=args.pool_cached)
+        stream.wait_stream(cap)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=cap):
+            plan.launch(cap, pool_cached=args.pool_cached)
+        torch.cuda.synchronize()
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        log("captured one call in a HIP graph")
+
     K = args.steps
     ev_k = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in range(K)]
@@ -194,6 +215,9 @@ def main() -> int:
     wall0 = time.perf_counter()
     t_begin.record(stream)
     for i in range(K):
+        if graph is not None:
+            graph.replay()
+            continue
         C.set_kernel_events(ev_k[i][0].cuda_event, ev_k[i][1].cuda_event)
         plan.launch(stream, pool_cached=args.pool_cached)
     t_end.record(stream)
@@ -201,6 +225,13 @@ def main() -> int:
     wall = time.perf_counter() - wall0
     C.set_kernel_events(None, None)
     step_ms = t_begin.elapsed_time(t_end) / K
+    if graph is not None:
+        # the dominant kernel's own events are not recorded inside a replay:
+        # time it eagerly once more
+        for a, b in ev_k:
+            C.set_kernel_events(a.cuda_event, b.cuda_event)
+            plan.launch(stream, pool_cached=args.pool_cached)
+        torch.cuda.synchronize()
     kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev_k)
     log(f"timed {K} steps: {step_ms:.4f} ms/step (events), wall {wall / K * 1e3:.4f} ms/step, "
         f"dominant kernel {kern_ms:.4f} ms")
@@ -229,6 +260,7 @@ def main() -> int:
         "config": {"workload": args.workload, "note": note, "T": T, "d_model": D,
                    "d_route": dr, "n_units": N, "routes": R, "chunk": cs,
                    "stats": args.stats, "diag": args.diag, "pool_cached": args.pool_cached,
+                   "graph": args.graph,
                    "tau_offset": round(tau_value, 4),
                    "parallelism": "single GPU"},
         "roofline": roofline,

@@ -361,3 +361,45 @@ def test_mfma_diagnostics_match_generic(pkg, dev, case):
     assert torch.allclose(ud_f[:, 0], ud_g[:, 0], rtol=1e-3, atol=1e-3 * (T * R) ** 0.5), "score_sum"
     assert torch.allclose(ud_f[:, 1], ud_g[:, 1], rtol=2e-3, atol=1e-6), "unit gate_max"
     assert torch.equal(f["n_active"], g["n_active"]) or int((f["n_active"] - g["n_active"]).abs().max()) <= 2
+
+
+def test_mfma_graph_replay_matches_eager(pkg, dev):
+    """One call captured in a HIP graph and replayed three times, with eager
+    work between the replays (new tokens copied in place): every replay
+    equals an eager call on the same inputs.  With diagnostics, so the
+    unit_diag clear (a fill kernel, no memset node) and its atomics replay
+    too; the atomic per-unit score sums may differ in the last bits."""
+    T, D, dr, N = 256, 384, 128, 3000
+    print(f"[gpu] mfma graph replay T{T} D{D} dr{dr} N{N}", flush=True)
+    shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=1, h_is_x=False)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=51)
+    bf = BF
+    plan = pkg.SrwPlan(inp["x"].to(bf).to(dev), inp["h"].to(bf).to(dev), inp["emb"].to(bf).to(dev),
+                       inp["tau_offset"].to(dev), inp["read"].to(bf).to(dev),
+                       inp["write"].to(bf).to(dev), chunk_size=1500, diag=True)
+    plan.launch()
+    torch.cuda.synchronize()
+    assert plan.path == "mfma_bf16"
+    cur = torch.cuda.current_stream(dev)
+    cap = torch.cuda.Stream(dev)
+    cap.wait_stream(cur)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        plan.launch(cap)
+    torch.cuda.synchronize()
+    gen = torch.Generator().manual_seed(52)
+    keys = ("out", "gate_sum", "den", "n_active", "pass_mask", "token_diag")
+    for rep in range(3):
+        plan.inputs[0].copy_(torch.randn(T, D, generator=gen).to(bf))
+        plan.inputs[1].copy_(torch.randn(T, 1, dr, generator=gen).to(bf))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = {k: plan.results()[k].clone() for k in keys + ("unit_diag",)}
+        plan.launch()
+        torch.cuda.synchronize()
+        ref = plan.results()
+        for k in keys:
+            assert torch.equal(got[k], ref[k]), (rep, k)
+        assert torch.equal(got["unit_diag"][:, 1], ref["unit_diag"][:, 1]), rep
+        assert torch.allclose(got["unit_diag"][:, 0], ref["unit_diag"][:, 0], rtol=1e-5, atol=1e-4), rep
