@@ -19,7 +19,7 @@ import threading
 import torch  # noqa: F401  (must precede loading the HIP library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libsrw_amd.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # srw_status_t
 SRW_OK, SRW_EINVAL, SRW_EUNSUPPORTED, SRW_EHIP, SRW_EWORKSPACE = range(5)
@@ -73,7 +73,7 @@ class SrwTensors(ctypes.Structure):
 
 class SrwOutputs(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
-        "out", "gate_sum", "den", "n_active", "pass_mask", "token_diag", "unit_diag")]
+        "out", "gate_sum", "den", "n_active", "pass_mask", "token_diag", "unit_diag", "gate")]
 
 
 class SrwError(RuntimeError):

@@ -116,7 +116,8 @@ srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw
   srw_status_t st = validate(d);
   if (st != SRW_OK) return st;
   if (!in || !o) return SRW_EINVAL;
-  const int which = choose(*d, in->h != nullptr && in->h == in->x);
+  int which = choose(*d, in->h != nullptr && in->h == in->x);
+  if (which == 1 && o->gate) which = srw::generic_supports(*d) ? 0 : -1;  // the dense gate: generic kernels
   if (which < 0) return SRW_EUNSUPPORTED;
   if (d->T == 0) {  // nothing to compute; empty tensors may carry null pointers
     g_last_path = "empty";

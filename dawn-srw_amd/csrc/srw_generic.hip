@@ -36,6 +36,7 @@ struct GenericParams {
   uint64_t* pass_mask;
   float* token_diag;
   float* unit_diag;
+  float* gate_out;     // [T, R, N] or null
   int64_t D, dr, N, words, chunk;
   int R;
   int stats;
@@ -163,6 +164,7 @@ __global__ __launch_bounds__(kGT) void srw_generic_kernel(GenericParams a) {
       }
       gsum += gate;
       nact += active ? 1.f : 0.f;
+      if (a.gate_out) a.gate_out[tr * N + n] = gate;   // gate_raw (v41:1760, 1769)
       if (DIAG) {
         gmax = fmaxf(gmax, gate);
         glogg += gate * logf(gate + 1e-8f);
@@ -293,6 +295,7 @@ hipError_t generic_forward_t(const LaunchArgs& a) {
   p.pass_mask = a.o.pass_mask;
   p.token_diag = a.o.token_diag;
   p.unit_diag = a.o.unit_diag;
+  p.gate_out = a.o.gate;
   p.D = d.d_model;
   p.dr = d.d_route;
   p.N = d.n_units;

@@ -64,7 +64,8 @@ class SrwPlan:
                  stats: str = "onepass", consts: GateConfig = GateConfig(),
                  scale: float = 1.0, chunk_size: int = 0, diag: bool = False,
                  want_mask: bool = True, emulate: bool = False,
-                 sparse_skip: bool = False, force_generic: bool = False):
+                 sparse_skip: bool = False, force_generic: bool = False,
+                 want_gate: bool = False):
         if x.dim() != 2:
             raise ValueError("x must be [T, D]")
         T, D = x.shape
@@ -122,6 +123,8 @@ class SrwPlan:
                            if diag else None)
         self.unit_diag = (torch.empty((N, len(C.UDIAG)), dtype=torch.float32, device=dev)
                           if diag else None)
+        self.gate = (torch.empty((T, R, N), dtype=torch.float32, device=dev)
+                     if want_gate else None)
         self.ws_bytes = C.workspace_size(desc)
         self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
 
@@ -133,7 +136,7 @@ class SrwPlan:
                                   _ptr(tau_offset), _ptr(read), _ptr(write))
         self._outs = C.SrwOutputs(_ptr(self.out), _ptr(self.gate_sum), _ptr(self.den),
                                   _ptr(self.n_active), _ptr(self.pass_mask),
-                                  _ptr(self.token_diag), _ptr(self.unit_diag))
+                                  _ptr(self.token_diag), _ptr(self.unit_diag), _ptr(self.gate))
         self._lib = C.load_library()
         self.path = None
 
@@ -165,7 +168,7 @@ class SrwPlan:
     def results(self) -> dict:
         return dict(out=self.out, gate_sum=self.gate_sum, den=self.den,
                     n_active=self.n_active, pass_mask=self.pass_mask,
-                    token_diag=self.token_diag, unit_diag=self.unit_diag,
+                    token_diag=self.token_diag, unit_diag=self.unit_diag, gate=self.gate,
                     path=self.path, workspace=self.workspace)
 
 
@@ -173,7 +176,8 @@ def srw_forward(x, h, emb, tau_offset, read, write, *, gate: str = "v41",
                 stats: str = "onepass", consts: GateConfig = GateConfig(),
                 scale: float = 1.0, chunk_size: int = 0, diag: bool = False,
                 want_mask: bool = True, emulate: bool = False,
-                sparse_skip: bool = False, force_generic: bool = False) -> dict:
+                sparse_skip: bool = False, force_generic: bool = False,
+                want_gate: bool = False) -> dict:
     """One SRW layer forward on the GPU.
 
     x [T, D]; h [T, R, dr] (R = 1 or 2) or the tensor ``x`` itself (R = 1,
@@ -190,11 +194,12 @@ def srw_forward(x, h, emb, tau_offset, read, write, *, gate: str = "v41",
     Returns a dict: out [T, R, D] (input dtype), gate_sum / den [T, R] f32,
     n_active [T, R] int32, pass_mask [T, R, ceil(N/64)] int64 (bit n % 64 of
     word n // 64) or None, token_diag [T, R, 14] / unit_diag [N, 2] f32 when
-    ``diag``, and ``path`` (the kernel family used).
+    ``diag``, gate [T, R, N] f32 when ``want_gate`` (every unit's gate; such a
+    call runs the generic kernels), and ``path`` (the kernel family used).
     """
     plan = SrwPlan(x, h, emb, tau_offset, read, write, gate=gate, stats=stats,
                    consts=consts, scale=scale, chunk_size=chunk_size, diag=diag,
                    want_mask=want_mask, emulate=emulate, sparse_skip=sparse_skip,
-                   force_generic=force_generic)
+                   force_generic=force_generic, want_gate=want_gate)
     plan.launch()
     return plan.results()

@@ -182,3 +182,28 @@ def srw_inference(x, h, emb_norm, tau_offset, w_read, w_write, *,
                       w_read.to(x.dtype).contiguous(), w_write.to(x.dtype).contiguous(),
                       gate=gate, stats="centered", consts=consts, want_mask=False)
     return res["out"].reshape(*lead, D).to(torch.float32)
+
+
+def srw_inference_with_gates(x, h, emb_norm, tau_offset, w_read, w_write, *,
+                             consts: GateConfig = GateConfig()):
+    """``_srw_inference_with_gates`` (v41:1741-1769): ``(out, gate_raw,
+    gate_norm)`` with out float32 [..., D] as :func:`srw_inference`, gate_raw
+    float32 [..., N] (activation x intensity of every unit) and
+    gate_norm = gate_raw / max(sum_n gate_raw, 1e-8) (:1760).  The dense
+    gate comes from the generic kernels.
+    """
+    lead = x.shape[:-1]
+    D = x.shape[-1]
+    T = 1
+    for s in lead:
+        T *= int(s)
+    N = emb_norm.shape[0]
+    xx = x.reshape(T, D).contiguous()
+    hh = h.reshape(T, 1, h.shape[-1]).to(x.dtype).contiguous()
+    tau = tau_offset.reshape(T, 1).to(torch.float32).contiguous()
+    res = srw_forward(xx, hh, emb_norm.to(x.dtype).contiguous(), tau,
+                      w_read.to(x.dtype).contiguous(), w_write.to(x.dtype).contiguous(),
+                      stats="centered", consts=consts, want_mask=False, want_gate=True)
+    gate_raw = res["gate"].reshape(*lead, N)
+    gate_norm = gate_raw / torch.clamp_min(gate_raw.sum(dim=-1, keepdim=True), 1e-8)  # :1760
+    return res["out"].reshape(*lead, D).to(torch.float32), gate_raw, gate_norm

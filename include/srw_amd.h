@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define SRW_AMD_ABI_VERSION 1
+#define SRW_AMD_ABI_VERSION 2
 
 typedef enum srw_status {
   SRW_OK = 0,
@@ -165,6 +165,10 @@ typedef struct srw_outputs {
                               iff unit n passes (act > 0.5)        (optional) */
   float* token_diag;       /* [T, n_routes, SRW_TDIAG_COUNT]  needs SRW_FLAG_DIAG */
   float* unit_diag;        /* [N, SRW_UDIAG_COUNT]            needs SRW_FLAG_DIAG */
+  float* gate;             /* [T, n_routes, N] gate (activation x intensity, fp32) of every
+                              unit: the gate_raw of _srw_inference_with_gates
+                              (models/dawn_spatial_v41_exp.py:1741-1769).  Optional; a
+                              call that sets it runs the generic kernels. */
 } srw_outputs_t;
 
 /* ABI version of the loaded library (SRW_AMD_ABI_VERSION). */

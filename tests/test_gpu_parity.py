@@ -216,3 +216,27 @@ def test_empty_tokens(pkg, dev):
     tau = torch.empty(0, 1, device=dev)
     res = pkg.srw_forward(x, h, e, tau, rw, rw)
     assert res["out"].shape == (0, 1, 64) and res["path"] == "empty"
+
+
+@pytest.mark.parametrize("dtype", [F32, BF])
+def test_dropin_srw_inference_with_gates(pkg, dev, dtype):
+    """_srw_inference_with_gates (v41:1741-1769): out, the dense gate of every
+    unit and its row-normalised form, against the oracle."""
+    B, S, D, dr, N = 2, 12, 96, 32, 700
+    print(f"[gpu] drop-in srw_inference_with_gates {dtype} B{B} S{S} N{N}", flush=True)
+    inp = _inputs(pkg, B * S, D, dr, N, seed=9)
+    x = inp["x"].reshape(B, S, D).to(dtype)
+    h = inp["h"].reshape(B, S, dr).to(dtype)
+    tau = inp["tau_offset"].reshape(B, S, 1)
+    emb, rd, wr = (inp[k].to(dtype) for k in ("emb", "read", "write"))
+    out, g, gn = pkg.srw_inference_with_gates(x.to(dev), h.to(dev), emb.to(dev), tau.to(dev),
+                                              rd.to(dev), wr.to(dev))
+    ro, rg, rgn = srw_ref.srw_inference_with_gates(x, h, emb, tau, rd, wr)
+    assert out.dtype == F32 and out.shape == (B, S, D)
+    assert g.shape == (B, S, N) and gn.shape == (B, S, N)
+    tol = REL_F32 if dtype == F32 else REL_BF16
+    assert rel_fro(out.cpu(), ro) <= tol
+    # the gate itself is fp32 in both dtypes (scores are rounded to the input dtype first)
+    assert torch.allclose(g.cpu(), rg.float(), rtol=1e-4, atol=1e-7)
+    assert torch.allclose(gn.cpu(), rgn.float(), rtol=1e-4, atol=1e-7)
+    assert torch.allclose(gn.sum(dim=-1).cpu(), torch.ones(B, S), atol=1e-4)
