@@ -266,15 +266,21 @@ __global__ __launch_bounds__(256) void pack_w_kernel(const uint16_t* __restrict_
 struct StatsParams {
   const uint16_t* h;   // [T, dr]
   const uint16_t* emb; // [N, dr]
-  float* mom;          // [S][T][2]
+  const float* mean;   // [T] row means (second pass of the centred moments) or null
+  float* mom;          // [S][T][2 or 4]
   uint32_t* mask32;    // pass bitmask as uint32 words [T][mask_words32] (may be null)
   int64_t mask_words32;
   Geometry g;
 };
 
-// DG: also sum s^3, s^4 (training diagnostics, v41:442-444); mom stride 4
-template <int KH, bool DG>
+// MODE kStatsPlain: sum s, sum s^2 (v41:441-442); kStatsDiag: also sum s^3,
+// s^4 (training diagnostics, v41:442-444; mom stride 4); kStatsCentered: sum
+// s, sum (s - mean)^2 with the row means of a first pass (_srw_inference's
+// two-pass std, v41:1719-1721).
+constexpr int kStatsPlain = 0, kStatsDiag = 1, kStatsCentered = 2;
+template <int KH, int MODE>
 __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
+  constexpr bool DG = MODE == kStatsDiag;
   constexpr int MS = DG ? 4 : 2;
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int STAGE = KH * kFragBytes;
@@ -305,6 +311,7 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
 #pragma unroll
   for (int ks = 0; ks < KH; ++ks)
     hq[ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl * DR + 16 * ks + 8 * half);
+  const float mu = MODE == kStatsCentered ? p.mean[tl] : 0.f;
 
   using TileE = RowTile<KH>;
   const uint32_t lsrc[2] = {TileE::lane_src(lane, 0), TileE::lane_src(lane, 1)};
@@ -351,12 +358,23 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
     for (int v = 0; v < 16; v += 2) {
       const uint32_t sp = pack_bf16(acc[v], acc[v + 1]);
       float a = lo_f32(sp), b = hi_f32(sp);
+      bool oka = true, okb = true;
       if (!full) {
         const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
-        if (!(ua >= lo && ua < hi)) a = 0.f;
-        if (!(ub >= lo && ub < hi)) b = 0.f;
+        oka = ua >= lo && ua < hi;
+        okb = ub >= lo && ub < hi;
+        if (!oka) a = 0.f;
+        if (!okb) b = 0.f;
       }
-      const float a2 = __fmul_rn(a, a), b2 = __fmul_rn(b, b);
+      float a2, b2;  // squares, or squared deviations from the row mean (centred)
+      if constexpr (MODE == kStatsCentered) {
+        const float da = oka ? a - mu : 0.f, db = okb ? b - mu : 0.f;
+        a2 = __fmul_rn(da, da);
+        b2 = __fmul_rn(db, db);
+      } else {
+        a2 = __fmul_rn(a, a);
+        b2 = __fmul_rn(b, b);
+      }
       s1 += a;
       s2 += a2;
       s1 += b;
@@ -1156,9 +1174,13 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
 // token_diag, also the row's mean, std, tau and third / fourth power sums
 // (zero without them).
 // ---------------------------------------------------------------------------
+// mode kTauOnePass: std = sqrt(E[s^2] - mean^2) + 1e-8; kTauMean: store the
+// row mean in tau[] (input of the centred second pass); kTauCentered: std =
+// sqrt(sum (s - mean)^2 / N) + 1e-8 (v41:1719-1721).
+constexpr int kTauOnePass = 0, kTauMean = 1, kTauCentered = 2;
 __global__ __launch_bounds__(256) void srw_tau_kernel(const float* __restrict__ mom, const float* __restrict__ tau_off,
                                                       float* __restrict__ tau, int64_t T, int S_st, int64_t N, int ms,
-                                                      float* __restrict__ token_diag) {
+                                                      float* __restrict__ token_diag, int mode) {
   const int lane = threadIdx.x & 63;
   const int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
@@ -1181,7 +1203,11 @@ __global__ __launch_bounds__(256) void srw_tau_kernel(const float* __restrict__ 
   if (lane == 0) {
     const float fN = static_cast<float>(N);
     const float mean = a / fN;
-    const float sd = sqrtf(b / fN - __fmul_rn(mean, mean)) + 1e-8f;
+    if (mode == kTauMean) {
+      tau[t] = mean;
+      return;
+    }
+    const float sd = (mode == kTauCentered ? sqrtf(b / fN) : sqrtf(b / fN - __fmul_rn(mean, mean))) + 1e-8f;
     const float tv = mean + __fmul_rn(tau_off[t], sd);
     tau[t] = tv;
     if (token_diag) {
@@ -1326,6 +1352,7 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
 // ---------------------------------------------------------------------------
 struct Kernels {
   void (*stats)(StatsParams);
+  void (*stats_centered)(StatsParams);  // second pass of the centred moments
   void (*main)(MainParams);
   int main_threads;
   int main_lds;  // bytes
@@ -1337,11 +1364,14 @@ template <int DB, int KH, bool HX, bool WS>
 Kernels kernels_of(bool dg) {
   if constexpr (WS) {
     constexpr int lds = (2 * (KH + 2 * DB) + 2 * 2 * DB + 16) * kFragBytes;  // 2 E/R, 2 W^T, S
-    if (dg) return Kernels{srw_stats_kernel<KH, true>, srw_main_ws_kernel<DB, KH, HX, true>, kWsThreads, lds};
-    return Kernels{srw_stats_kernel<KH, false>, srw_main_ws_kernel<DB, KH, HX, false>, kWsThreads, lds};
+    if (dg)
+      return Kernels{srw_stats_kernel<KH, kStatsDiag>, srw_stats_kernel<KH, kStatsCentered>,
+                     srw_main_ws_kernel<DB, KH, HX, true>, kWsThreads, lds};
+    return Kernels{srw_stats_kernel<KH, kStatsPlain>, srw_stats_kernel<KH, kStatsCentered>,
+                   srw_main_ws_kernel<DB, KH, HX, false>, kWsThreads, lds};
   } else {
-    return Kernels{srw_stats_kernel<KH, false>, srw_main_kernel<DB, KH, HX>, kThreads,
-                   2 * (KH + 2 * DB + 2 * DB) * kFragBytes};
+    return Kernels{srw_stats_kernel<KH, kStatsPlain>, srw_stats_kernel<KH, kStatsCentered>,
+                   srw_main_kernel<DB, KH, HX>, kThreads, 2 * (KH + 2 * DB + 2 * DB) * kFragBytes};
   }
 }
 
@@ -1438,7 +1468,10 @@ hipError_t pack_unit_major(const uint16_t* src, uint16_t* dst, int64_t N, int D,
 
 bool mfma_supports(const srw_desc_t& d, bool h_is_x) {
   if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41) return false;
-  if (d.stats_mode != SRW_STATS_ONEPASS && !(d.stats_mode == SRW_STATS_GRAM && gram_supports(d.d_route))) return false;
+  if (d.stats_mode != SRW_STATS_ONEPASS && d.stats_mode != SRW_STATS_CENTERED &&
+      !(d.stats_mode == SRW_STATS_GRAM && gram_supports(d.d_route)))
+    return false;
+  if (d.stats_mode == SRW_STATS_CENTERED && with_diag(d)) return false;  // diagnostics: one-pass moments only
   if (d.n_routes != 1 && d.n_routes != 2) return false;  // paired QK: 2 rows per token
   if (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
   Kernels k;
@@ -1506,16 +1539,27 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     sp.mask_words32 = mw32;
     sp.g = g;
     const size_t smem = static_cast<size_t>(2 * KH) * kFragBytes;
-    if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(k.stats),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem))) != hipSuccess)
-      return e;
+    for (auto fn : {k.stats, k.stats_centered})
+      if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   static_cast<int>(smem))) != hipSuccess)
+        return e;
     hipLaunchKernelGGL(k.stats, dim3(grid_st), dim3(kThreads), smem, a.stream, sp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (d.stats_mode == SRW_STATS_CENTERED) {
+      // row means, then the sums of squared deviations from them (two-pass std)
+      hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((g.T + 3) / 4)), dim3(256), 0, a.stream, mom,
+                         a.in.tau_offset, tau, g.T, g.S_st, g.N, 2, nullptr, kTauMean);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      sp.mean = tau;
+      sp.mask32 = nullptr;  // the first pass cleared the shared mask words
+      hipLaunchKernelGGL(k.stats_centered, dim3(grid_st), dim3(kThreads), smem, a.stream, sp);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
   }
   // tau per row from the moment partials
   hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((g.T + 3) / 4)), dim3(256), 0, a.stream, mom,
                      a.in.tau_offset, tau, g.T, g.S_st, g.N, d.stats_mode == SRW_STATS_GRAM ? 2 : mom_stride(d),
-                     token_diag);
+                     token_diag, d.stats_mode == SRW_STATS_CENTERED ? kTauCentered : kTauOnePass);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   // main
   {

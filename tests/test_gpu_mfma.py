@@ -157,6 +157,43 @@ def test_mfma_gram_equals_onepass_closely(pkg, dev):
     assert int(mism) <= T * N * 1e-4
 
 
+CENTERED_CASES = [
+    # T, D, dr, N, h_is_x, seed
+    (256, 384, 384, 2600, True, 31),    # Know-pool form, ragged N
+    (200, 384, 128, 1580, False, 32),   # router h, ragged T and N
+    (33, 64, 64, 100, True, 33),        # tiny pool
+    (130, 128, 128, 70, True, 34),      # a single partial tile per row
+]
+
+
+@pytest.mark.parametrize("case", CENTERED_CASES, ids=lambda c: "T{}D{}dr{}N{}{}".format(
+    c[0], c[1], c[2], c[3], "x" if c[4] else ""))
+def test_mfma_centered_matches_srw_inference_oracle(pkg, dev, case):
+    """bf16 _srw_inference (v41:1713-1738) on the matrix cores: the two-pass
+    centred std (:1719-1721) from a second moments pass over the same bf16
+    scores, one unchunked write GEMM rounded once.  Same bar as the fused
+    path: out, den, gate sum and the passing set against the oracle; a tail
+    tile that counted padded units as deviations of -mean would move den."""
+    T, D, dr, N, hx, seed = case
+    print(f"[gpu] mfma bf16 centered {case}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, hx, seed)
+    got = _gpu(pkg, dev, inp, 0, stats="centered")
+    assert got["path"] == "mfma_bf16"
+    x = inp["x"].to(BF)
+    h = x if "h" not in inp else inp["h"][:, 0].to(BF)
+    ref, tr = srw_ref.srw_inference(x, h, inp["emb"].to(BF), inp["tau_offset"], inp["read"].to(BF),
+                                    inp["write"].to(BF), return_trace=True)
+    raw = tr["scores"] - tr["tau"]
+    flat = dict(margin=raw - 0.5, tau=tr["tau"], s_std=tr["s_std"], den=tr["den"],
+                gate_sum=tr["gate"].sum(dim=-1), n_active=(tr["activation"] > 0.5).sum(dim=-1))
+    _check(got, (ref,), flat, T, N, D)
+    # the generic kernels' centred sweep: same fp32 two-pass sums in another order
+    gen = _gpu(pkg, dev, inp, 0, stats="centered", force_generic=True)
+    assert gen["path"] == "generic"
+    assert torch.allclose(got["den"], gen["den"], rtol=1e-4)
+    assert rel_fro(got["out"].float(), gen["out"].float()) <= 1e-2
+
+
 PAIRED_CASES = [
     # T, D, dr, N, max_chunk, seed
     (128, 384, 128, 1580, 12500, 21),   # the 40M QK pool with the router's d_route
