@@ -37,9 +37,10 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 # HBM bytes per launch of the dominant kernel: rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (KiB per dispatch) scaled by what the same counters read for a
 # 256 MiB copy (--calibrate-copy 256): FETCH x 2.00, WRITE x 1.00.  Keyed by
-# (workload, stats mode); profiles/know_T4096_N25200_traffic.md has the runs.
+# (workload, stats mode, kernel family); profiles/know_T4096_N25200_traffic.md
+# has the runs.
 MEASURED_TRAFFIC = {
-    ("know", "onepass"): (41148 * 2.0 + 64190 * 1.0) * 1024,
+    ("know", "onepass", "mfma_bf16"): (41148 * 2.0 + 64190 * 1.0) * 1024,
 }
 
 WORKLOADS = {
@@ -117,6 +118,9 @@ def main() -> int:
                     help="time budget of the CPU baseline (0 skips it)")
     ap.add_argument("--force-generic", action="store_true",
                     help="time the generic (scalar) kernels instead of the MFMA path")
+    ap.add_argument("--tiled", action="store_true",
+                    help="run the tiled-GEMM kernels (P materialised) where a fused kernel "
+                         "exists too (they serve d_model > 384 anyway)")
     ap.add_argument("--diag", action="store_true",
                     help="also compute the training diagnostics (SRW_FLAG_DIAG: the 22-tuple "
                          "path of the drop-in fused_gate_srw)")
@@ -174,7 +178,7 @@ def main() -> int:
     plan = pkg.SrwPlan(x, h, inp["emb"].to(bf).to(dev), inp["tau_offset"].to(dev),
                        inp["read"].to(bf).to(dev), inp["write"].to(bf).to(dev),
                        stats=args.stats, chunk_size=cs, want_mask=True, diag=args.diag,
-                       force_generic=args.force_generic)
+                       force_generic=args.force_generic, tiled=args.tiled)
     stream = torch.cuda.current_stream(dev)
 
     plan.launch(stream)
@@ -238,12 +242,19 @@ def main() -> int:
 
     T, D, dr, N, R = shape.T, shape.D, shape.dr, shape.N, shape.routes
     flops = 2.0 * T * N * (R * dr + D + R * D)          # score + read (once) + write
-    achieved = flops / (kern_ms * 1e-3) / 1e12
-    traffic = MEASURED_TRAFFIC.get((args.workload, args.stats)) if plan.path == "mfma_bf16" else None
+    if plan.path == "tiled_bf16":
+        # the dominant kernel of the tiled family is the gate GEMM pair (score
+        # + read); the write GEMM is a kernel of its own
+        kflops = 2.0 * T * N * (R * dr + D)
+    else:
+        kflops = flops
+    achieved = kflops / (kern_ms * 1e-3) / 1e12
+    traffic = MEASURED_TRAFFIC.get((args.workload, args.stats, plan.path))
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                 "traffic": traffic, "kernel": plan.path,
-                "kernel_ms": round(kern_ms, 5), "algorithmic_flop": flops}
+                "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops,
+                "step_tflops": round(flops / (step_ms * 1e-3) / 1e12, 2)}
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -260,6 +271,7 @@ def main() -> int:
         "config": {"workload": args.workload, "note": note, "T": T, "d_model": D,
                    "d_route": dr, "n_units": N, "routes": R, "chunk": cs,
                    "stats": args.stats, "diag": args.diag, "pool_cached": args.pool_cached,
+                   "tiled": args.tiled,
                    "graph": args.graph,
                    "tau_offset": round(tau_value, 4),
                    "parallelism": "single GPU"},

@@ -35,6 +35,7 @@ SRW_FLAG_EMULATE = 0x2
 SRW_FLAG_SPARSE_SKIP = 0x4
 SRW_FLAG_NO_FAST = 0x8
 SRW_FLAG_POOL_CACHED = 0x10
+SRW_FLAG_TILED = 0x20
 
 # token_diag columns (SRW_TDIAG_*) and unit_diag columns (SRW_UDIAG_*)
 TDIAG = (

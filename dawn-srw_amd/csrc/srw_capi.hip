@@ -28,16 +28,22 @@ srw_status_t validate(const srw_desc_t* d) {
   if (!isfinite(d->sharpness) || !isfinite(d->act_threshold) || !isfinite(d->act_cutoff) ||
       !isfinite(d->epsilon) || !isfinite(d->max_intensity) || !isfinite(d->scale))
     return SRW_EINVAL;
-  if (d->flags & ~(SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_SPARSE_SKIP | SRW_FLAG_NO_FAST | SRW_FLAG_POOL_CACHED))
+  if (d->flags & ~(SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_SPARSE_SKIP | SRW_FLAG_NO_FAST | SRW_FLAG_POOL_CACHED |
+                   SRW_FLAG_TILED))
     return SRW_EINVAL;
   return SRW_OK;
 }
 
-// Which family serves this descriptor: 1 = MFMA, 0 = generic, -1 = none.
-// h_is_x: h aliases x (known to srw_forward from the pointers).
+// Which family serves this descriptor: 1 = fused MFMA, 2 = tiled GEMMs,
+// 0 = generic, -1 = none.  h_is_x: h aliases x (known to srw_forward from
+// the pointers).
 int choose(const srw_desc_t& d, bool h_is_x) {
   const bool force_generic = (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST)) != 0;
-  if (!force_generic && srw::mfma_supports(d, h_is_x)) return 1;
+  if (!force_generic) {
+    if ((d.flags & SRW_FLAG_TILED) && srw::tiled_supports(d)) return 2;
+    if (srw::mfma_supports(d, h_is_x)) return 1;
+    if (srw::tiled_supports(d)) return 2;
+  }
   if (d.stats_mode == SRW_STATS_GRAM) return -1;  // only the MFMA family implements it
   if (d.flags & SRW_FLAG_SPARSE_SKIP) return -1;
   if (srw::generic_supports(d)) return 0;
@@ -45,6 +51,12 @@ int choose(const srw_desc_t& d, bool h_is_x) {
 }
 
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+size_t bytes_of(int which, const srw_desc_t& d) {
+  if (which == 1) return srw::mfma_workspace_bytes(d);
+  if (which == 2) return srw::tiled_workspace_bytes(d);
+  return srw::generic_workspace_bytes(d);
+}
 
 }  // namespace
 
@@ -104,7 +116,7 @@ srw_status_t srw_workspace_size(const srw_desc_t* d, size_t* bytes) {
   size_t need = 0;
   for (int w : {which, which_alias}) {
     if (w < 0) continue;
-    const size_t n = align256(w == 1 ? srw::mfma_workspace_bytes(*d) : srw::generic_workspace_bytes(*d));
+    const size_t n = align256(bytes_of(w, *d));
     need = n > need ? n : need;
   }
   *bytes = need;
@@ -117,7 +129,7 @@ srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw
   if (st != SRW_OK) return st;
   if (!in || !o) return SRW_EINVAL;
   int which = choose(*d, in->h != nullptr && in->h == in->x);
-  if (which == 1 && o->gate) which = srw::generic_supports(*d) ? 0 : -1;  // the dense gate: generic kernels
+  if (which > 0 && o->gate) which = srw::generic_supports(*d) ? 0 : -1;  // the dense gate: generic kernels
   if (which < 0) return SRW_EUNSUPPORTED;
   if (d->T == 0) {  // nothing to compute; empty tensors may carry null pointers
     g_last_path = "empty";
@@ -125,7 +137,7 @@ srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw
   }
   if (!in->x || !in->h || !in->emb || !in->tau_offset || !in->read || !in->write || !o->out) return SRW_EINVAL;
   if (in->h == in->x && !(d->n_routes == 1 && d->d_route == d->d_model)) return SRW_EINVAL;
-  const size_t need = align256(which == 1 ? srw::mfma_workspace_bytes(*d) : srw::generic_workspace_bytes(*d));
+  const size_t need = align256(bytes_of(which, *d));
   if (need > 0 && (!workspace || workspace_bytes < need)) return SRW_EWORKSPACE;
 
   srw::LaunchArgs a{};
@@ -154,6 +166,9 @@ srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw
     const char* name = "mfma";
     e = srw::mfma_forward(a, &name);
     g_last_path = name;
+  } else if (which == 2) {
+    e = srw::tiled_forward(a);
+    g_last_path = "tiled_bf16";
   } else {
     e = srw::generic_forward(a);
     g_last_path = "generic";

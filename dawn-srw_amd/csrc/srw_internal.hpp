@@ -54,6 +54,42 @@ hipError_t gram_moments(const uint16_t* emb, const uint16_t* h, int64_t T, int64
                         char* ws, hipStream_t s, uint32_t* mask32, int64_t words32, int64_t cs, int nc,
                         bool pool_cached);
 
+// Per-row tau from moment partials mom[S_st][T][ms] (srw_mfma.hip).
+// kTauOnePass: std = sqrt(E[s^2] - mean^2) + 1e-8 (v41:461-462); kTauMean:
+// stores the row mean in tau[] (input of a centred second pass);
+// kTauCentered: std = sqrt(sum (s - mean)^2 / N) + 1e-8 (v41:1719-1721).
+enum TauMode { kTauOnePass = 0, kTauMean = 1, kTauCentered = 2 };
+hipError_t launch_tau(const float* mom, const float* tau_off, float* tau, int64_t T, int S_st, int64_t N, int ms,
+                      float* token_diag, int mode, hipStream_t s);
+
+// Final reduction over N-splits (srw_mfma.hip): sums the fp32 partial outputs
+// out_part[S][T][D] split by split, rounds each reference chunk (spc
+// consecutive splits) to bf16, den = max(sum intensity, 1) from
+// tok_part[S_tok][T][tps] = (sum gate, sum intensity, active count, ...),
+// out = bf16(bf16(raw / den) * scale).
+struct FinalizeArgs {
+  const float* out_part;
+  const float* tok_part;
+  uint16_t* out;
+  float* gate_sum;
+  float* den;
+  int32_t* n_active;
+  int64_t T;
+  int D, S, spc, S_tok, tps;
+  float scale;
+  const float* tau;    // diagnostics only
+  float* token_diag;   // [T][SRW_TDIAG_COUNT] or null
+  GateParams gp;
+  float exp_scale;
+};
+hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s);
+
+// Tiled-GEMM kernels for wide layers (bf16), see srw_tiled.hip: P = gated
+// product materialised in HBM; d_model and d_route multiples of 64.
+bool tiled_supports(const srw_desc_t& d);
+size_t tiled_workspace_bytes(const srw_desc_t& d);
+hipError_t tiled_forward(const LaunchArgs& a);
+
 // MFMA kernels (bf16 / f32 matrix cores), see srw_mfma.hip.
 size_t mfma_workspace_bytes(const srw_desc_t& d);
 // h_is_x: h aliases x (d_route == d_model, one route), which some shapes need

@@ -37,45 +37,16 @@
 #include <type_traits>
 
 #include "srw_internal.hpp"
+#include "srw_mfma_util.hpp"
 
 namespace srw {
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
 constexpr int kThreads = 256;     // 4 waves
 constexpr int kTokTile = 128;     // tokens per workgroup
 constexpr int kUnitTile = 32;     // units per tile
-constexpr int kFragBytes = 1024;  // one MFMA operand fragment: 64 lanes x 16 B
 constexpr int kTargetBlocks = 256;
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-__device__ inline f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
-
-// Two floats -> two bf16 (round to nearest even, v_cvt_pk_bf16_f32), low = first.
-__device__ inline uint32_t pack_bf16(float lo, float hi) {
-  f32x2_t v = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-}
-__device__ inline float lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
-__device__ inline float hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
-
-// One 16-byte direct global->LDS load per lane; the LDS destination of the
-// wave is `lds` (wave-uniform) + 16 * lane.
-__device__ inline void g2lds16(const void* g, char* lds) {
-  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 0);
-}
-
-__device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
 // Lane exchanges within 32-lane halves, on the vector ALU (DPP and the gfx950
 // row swap) rather than the LDS crossbar: the value of lane (lane ^ m).
@@ -119,18 +90,6 @@ __device__ inline void reduce_scatter16(float (&a)[16], int lane, Op op) {
   a[0] = op(a[0], lane_xor<16>(a[0], lane));
 }
 
-// Workgroup barrier that waits only for this wave's LDS operations.
-// __syncthreads() is a workgroup-scope release/acquire, for which the
-// compiler also drains every global load in flight (vmcnt(0)) -- including
-// the global->LDS prefetch of later tiles.  Here global->LDS loads stay in
-// flight; a caller that publishes them waits for them first.  The
-// compiler-only fences keep memory accesses on their side of the barrier.
-__device__ inline void barrier_lds() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 // A 32-row tile of a row-major bf16 [rows, K] array (E or R), staged in LDS
 // as K / 16 one-KB blocks.  Load block j moves whole 128-byte lines (8 rows x
@@ -1177,7 +1136,6 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
 // mode kTauOnePass: std = sqrt(E[s^2] - mean^2) + 1e-8; kTauMean: store the
 // row mean in tau[] (input of the centred second pass); kTauCentered: std =
 // sqrt(sum (s - mean)^2 / N) + 1e-8 (v41:1719-1721).
-constexpr int kTauOnePass = 0, kTauMean = 1, kTauCentered = 2;
 __global__ __launch_bounds__(256) void srw_tau_kernel(const float* __restrict__ mom, const float* __restrict__ tau_off,
                                                       float* __restrict__ tau, int64_t T, int S_st, int64_t N, int ms,
                                                       float* __restrict__ token_diag, int mode) {
@@ -1236,6 +1194,7 @@ struct FinalParams {
   int32_t* n_active;
   int64_t T;
   int D, S, spc;
+  int S_tok;             // per-token partial slots in tok_part (S for the fused kernels)
   float scale;
   int tps;               // floats per (split, row) in tok_part: 4, or kTokPartDiag with diagnostics
   const float* tau;      // [T] (diagnostics)
@@ -1258,7 +1217,7 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
   const int tid = threadIdx.x;
   const int g = tid / CW, c = tid % CW;
   float gs = 0.f, is = 0.f, na = 0.f;
-  for (int s = tid; s < p.S; s += 256) {
+  for (int s = tid; s < p.S_tok; s += 256) {
     const float* tp = p.tok_part + (static_cast<int64_t>(s) * p.T + t) * p.tps;
     gs += tp[0];
     is += tp[1];
@@ -1282,7 +1241,19 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
   const bool dok = d < p.D;
   const float* col = p.out_part + t * p.D + (dok ? d : 0);
   float raw = 0.f;
-  for (int s0 = 0; s0 < p.S; s0 += p.spc) {                  // one reference chunk
+  if (NG == 1 && p.spc == 1) {
+    // one split per chunk: the chunks' loads go out eight at a time, the
+    // rounded chunk results add in chunk order
+    for (int s0 = 0; s0 < p.S; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = s0 + j < p.S ? col[(s0 + j) * stride] : 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < p.S) raw += round_bf16(v[j]);               // bf16 dot output (v41:518)
+    }
+  }
+  for (int s0 = 0; s0 < p.S && !(NG == 1 && p.spc == 1); s0 += p.spc) {  // one reference chunk
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     int s = s0 + g;
     for (; s + 7 * NG < s0 + p.spc; s += 8 * NG) {
@@ -1319,7 +1290,7 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
     // per-token diagnostics (v41:519-534); gate and intensity are
     // non-decreasing in the score, so their maxima follow from the max score
     float smax = -INFINITY, c[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s = tid; s < p.S; s += 64) {
+    for (int s = tid; s < p.S_tok; s += 64) {
       const float* tp = p.tok_part + (static_cast<int64_t>(s) * p.T + t) * p.tps;
       smax = fmaxf(smax, tp[TP_SMAX]);
 #pragma unroll
@@ -1547,9 +1518,8 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (d.stats_mode == SRW_STATS_CENTERED) {
       // row means, then the sums of squared deviations from them (two-pass std)
-      hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((g.T + 3) / 4)), dim3(256), 0, a.stream, mom,
-                         a.in.tau_offset, tau, g.T, g.S_st, g.N, 2, nullptr, kTauMean);
-      if ((e = hipGetLastError()) != hipSuccess) return e;
+      if ((e = launch_tau(mom, a.in.tau_offset, tau, g.T, g.S_st, g.N, 2, nullptr, kTauMean, a.stream)) != hipSuccess)
+        return e;
       sp.mean = tau;
       sp.mask32 = nullptr;  // the first pass cleared the shared mask words
       hipLaunchKernelGGL(k.stats_centered, dim3(grid_st), dim3(kThreads), smem, a.stream, sp);
@@ -1557,10 +1527,10 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     }
   }
   // tau per row from the moment partials
-  hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((g.T + 3) / 4)), dim3(256), 0, a.stream, mom,
-                     a.in.tau_offset, tau, g.T, g.S_st, g.N, d.stats_mode == SRW_STATS_GRAM ? 2 : mom_stride(d),
-                     token_diag, d.stats_mode == SRW_STATS_CENTERED ? kTauCentered : kTauOnePass);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = launch_tau(mom, a.in.tau_offset, tau, g.T, g.S_st, g.N, d.stats_mode == SRW_STATS_GRAM ? 2 : mom_stride(d),
+                      token_diag, d.stats_mode == SRW_STATS_CENTERED ? kTauCentered : kTauOnePass, a.stream)) !=
+      hipSuccess)
+    return e;
   // main
   {
     MainParams mp{};
@@ -1589,33 +1559,60 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   // finalize
-  {
-    FinalParams fp{};
-    fp.out_part = out_part;
-    fp.tok_part = tok_part;
-    fp.out = static_cast<uint16_t*>(a.o.out);
-    fp.gate_sum = a.o.gate_sum;
-    fp.den = a.o.den;
-    fp.n_active = a.o.n_active;
-    fp.T = g.T;
-    fp.D = D;
-    fp.S = g.S;
-    fp.spc = g.spc;
-    fp.scale = d.scale;
-    fp.tps = tok_part_stride(d);
-    fp.tau = tau;
-    fp.token_diag = token_diag;
-    fp.gp = a.gp;
-    fp.exp_scale = -d.sharpness * 1.4426950408889634f;
-    // split groups per workgroup from the splits per chunk
-    const int ng = g.spc >= 64 ? 16 : (g.spc >= 16 ? 4 : 1);
-    const dim3 grid_f(static_cast<unsigned>(g.T), static_cast<unsigned>((D + 256 / ng - 1) / (256 / ng)));
-    if (ng == 16) hipLaunchKernelGGL(srw_finalize_kernel<16>, grid_f, dim3(256), 0, a.stream, fp);
-    else if (ng == 4) hipLaunchKernelGGL(srw_finalize_kernel<4>, grid_f, dim3(256), 0, a.stream, fp);
-    else hipLaunchKernelGGL(srw_finalize_kernel<1>, grid_f, dim3(256), 0, a.stream, fp);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  return hipSuccess;
+  FinalizeArgs f{};
+  f.out_part = out_part;
+  f.tok_part = tok_part;
+  f.out = static_cast<uint16_t*>(a.o.out);
+  f.gate_sum = a.o.gate_sum;
+  f.den = a.o.den;
+  f.n_active = a.o.n_active;
+  f.T = g.T;
+  f.D = D;
+  f.S = g.S;
+  f.spc = g.spc;
+  f.S_tok = g.S;
+  f.tps = tok_part_stride(d);
+  f.scale = d.scale;
+  f.tau = tau;
+  f.token_diag = token_diag;
+  f.gp = a.gp;
+  f.exp_scale = -d.sharpness * 1.4426950408889634f;
+  return launch_finalize(f, a.stream);
+}
+
+hipError_t launch_tau(const float* mom, const float* tau_off, float* tau, int64_t T, int S_st, int64_t N, int ms,
+                      float* token_diag, int mode, hipStream_t s) {
+  hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, s, mom, tau_off, tau, T,
+                     S_st, N, ms, token_diag, mode);
+  return hipGetLastError();
+}
+
+hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
+  FinalParams fp{};
+  fp.out_part = f.out_part;
+  fp.tok_part = f.tok_part;
+  fp.out = f.out;
+  fp.gate_sum = f.gate_sum;
+  fp.den = f.den;
+  fp.n_active = f.n_active;
+  fp.T = f.T;
+  fp.D = f.D;
+  fp.S = f.S;
+  fp.spc = f.spc;
+  fp.S_tok = f.S_tok;
+  fp.scale = f.scale;
+  fp.tps = f.tps;
+  fp.tau = f.tau;
+  fp.token_diag = f.token_diag;
+  fp.gp = f.gp;
+  fp.exp_scale = f.exp_scale;
+  // split groups per workgroup from the splits per chunk
+  const int ng = f.spc >= 64 ? 16 : (f.spc >= 16 ? 4 : 1);
+  const dim3 grid_f(static_cast<unsigned>(f.T), static_cast<unsigned>((f.D + 256 / ng - 1) / (256 / ng)));
+  if (ng == 16) hipLaunchKernelGGL(srw_finalize_kernel<16>, grid_f, dim3(256), 0, s, fp);
+  else if (ng == 4) hipLaunchKernelGGL(srw_finalize_kernel<4>, grid_f, dim3(256), 0, s, fp);
+  else hipLaunchKernelGGL(srw_finalize_kernel<1>, grid_f, dim3(256), 0, s, fp);
+  return hipGetLastError();
 }
 
 }  // namespace srw

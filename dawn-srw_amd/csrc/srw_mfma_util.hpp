@@ -1,0 +1,59 @@
+// srw_mfma_util.hpp -- gfx950 matrix-core and LDS helpers shared by the
+// bf16 kernel families (srw_mfma.hip, srw_gemm.hip).
+//
+// v_mfma_f32_32x32x16_bf16 operand layout (wave64):
+//   A operand: lane l holds A[l % 32][8 (l / 32) + i], i = 0..7
+//   B operand: lane l holds B[8 (l / 32) + i][l % 32]
+//   C/D:       acc[v] of lane l is C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32]
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace srw {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kFragBytes = 1024;  // one MFMA operand fragment: 64 lanes x 16 B
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ inline f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Two floats -> two bf16 (round to nearest even, v_cvt_pk_bf16_f32), low = first.
+__device__ inline uint32_t pack_bf16(float lo, float hi) {
+  f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+__device__ inline float lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ inline float hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
+// One 16-byte direct global->LDS load per lane; the LDS destination of the
+// wave is `lds` (wave-uniform) + 16 * lane.
+__device__ inline void g2lds16(const void* g, char* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 0);
+}
+
+__device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// Workgroup barrier that waits only for this wave's LDS operations.
+// __syncthreads() is a workgroup-scope release/acquire, for which the
+// compiler also drains every global load in flight (vmcnt(0)) -- including
+// the global->LDS prefetch of later tiles.  Here global->LDS loads stay in
+// flight; a caller that publishes them waits for them first.  The
+// compiler-only fences keep memory accesses on their side of the barrier.
+__device__ inline void barrier_lds() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+}  // namespace srw

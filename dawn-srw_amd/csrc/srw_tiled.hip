@@ -1,0 +1,737 @@
+// srw_tiled.hip -- bf16 matrix-core SRW forward for wide layers: three tiled
+// GEMMs with the gated product P materialised in HBM.
+//
+// The fused kernels (srw_mfma.hip) keep a [128 tokens x D] fp32 output tile
+// in registers for the whole N scan.  At d_model = 1024 (the scaled Know
+// pool) that tile is 512 KB, the whole register file of a CU, and the 400M /
+// 1B models (D = 1280 / 2048) are larger still.  Here the layer runs as
+//
+//   pack   W [N, D] -> W^T [D, N64] (unit-contiguous rows, zero tail)
+//   stats  S = E.H^T per 256-unit x 256-token tile, rounded to bf16
+//          (v41:439) and stored as S [T, N64] bf16; per-token partials sum s
+//          and sum s^2 (v41:441-442)
+//   centre (_srw_inference only) sum (s - mean)^2 streamed from the stored S
+//          (v41:1719-1721)
+//   gate   per tile: XR = R.X^T, the v4.1 gate of the stored scores
+//          (v41:506-511) and P = bf16(bf16(g) * bf16(xr)) (v41:516-518),
+//          written over S in place; the pass bits and per-token sum gate /
+//          sum intensity / active count partials (v41:519-534)
+//   write  OUT_c = P[:, chunk c] . W[chunk c, :] per reference chunk c (K =
+//          the chunk's units), fp32 partials; the shared finalize rounds each
+//          chunk to bf16 and divides by den (v41:518, 584-586)
+//
+// The reference computes the score GEMM twice (pass 1 and pass 2); here it
+// runs once and the bf16 scores travel through HBM: 2 B written + 2 B read
+// per (token, unit), plus the same for P, against 2 (dr + 2 D) matrix-core
+// flops -- ~770 flop/B at D = 1024, well above the 310 flop/B balance point
+// of 2.5 PFLOP/s over 8 TB/s.
+//
+// All three GEMMs share one main loop: a 256 x 256 output tile per workgroup
+// (4 waves as 2 x 2, 128 x 128 = 16 accumulators of 32 x 32 each), operands
+// K-contiguous in memory, 64-wide k blocks staged in a double-buffered LDS
+// ring by direct global->LDS loads of whole 128-byte lines, 16-byte pieces
+// XOR-swizzled by row so the fragment reads are free of bank conflicts.
+
+#include <type_traits>
+
+#include "srw_internal.hpp"
+#include "srw_mfma_util.hpp"
+
+namespace srw {
+
+namespace {
+
+constexpr int kGThreads = 256;              // 4 waves
+constexpr int kGRows = 256;                 // rows per operand tile = output tile side
+constexpr int kGK = 64;                     // k per stage: one 128-byte line per row
+constexpr int kOpBytes = kGRows * kGK * 2;  // 32 KB
+constexpr int kStageBytes = 2 * kOpBytes;   // A and B tiles
+constexpr int kGemmLds = 2 * kStageBytes;   // two stages: 128 KB
+constexpr int kGroupBytes = 32 * kGK * 2;   // 32 rows: one MFMA operand's rows
+
+// An operand tile in LDS: 32-row groups of 4 KB; row u of a group at
+// (u / 8) * 1 KB + (u % 8) * 128 B, its 16-byte piece q in slot q ^ gswz(u).
+__device__ inline int gswz(int u) { return (u & 7) ^ ((u >> 3) & 1); }
+
+// The eight rows a wave loads per stage: rows 32 i + 8 wave + lane / 8 of the
+// tile (i = 0..7), 16 bytes each per lane.  Memory row of tile row r =
+// min(row0 + r, rows - 1) / div (div = 2 maps paired-route rows to x rows).
+struct Opnd {
+  const char* base;  // byte address of memory row row0 / div, k = 0 (uniform)
+  uint32_t off[8];   // per-lane byte offsets from base: row and swizzled piece
+};
+
+__device__ inline Opnd make_opnd(const uint16_t* p, int64_t ld, int64_t row0, int64_t rows, int div, int wave,
+                                 int lane) {
+  Opnd o;
+  const int64_t base_row = row0 / div;
+  o.base = reinterpret_cast<const char*>(p + base_row * ld);
+  const int r8 = lane >> 3;
+  const int piece = (lane & 7) ^ r8 ^ (wave & 1);  // gswz(8 wave + r8) = r8 ^ (wave & 1)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int64_t row = row0 + 32 * i + 8 * wave + r8;
+    row = row < rows ? row : rows - 1;
+    o.off[i] = static_cast<uint32_t>(((row / div - base_row) * ld + 8 * piece) * 2);
+  }
+  return o;
+}
+
+// acc[i][j] += A-tile rows (128 wa + 32 i ..) . B-tile rows (128 wb + 32 j ..)^T over
+// k in [k0, k0 + 64 nk), wave = 2 wa + wb.  hook(kb, stage) runs once block kb
+// has landed in LDS, before any wave reads it (all threads call it).
+//
+// Per 64-wide block: four k-steps of 16 MFMAs.  Operand fragments are double
+// buffered in registers: k-step m's MFMAs run while k-step m+1's eight
+// fragments are read (one read per two MFMAs, in the order they are used).
+// The block barrier sits before k-step 3, whose fragments are then in
+// registers: after it no wave reads block kb's stage, so block kb + 2's loads
+// go into it at once, one per MFMA of k-step 3 (about four k-steps before
+// they are needed), and k-step 3's MFMAs also cover the first fragment reads
+// of block kb + 1.  (Global->LDS loads interleaved with fragment reads make
+// the compiler wait for every LDS read, so they stay in k-step 3.)
+template <class Hook>
+__device__ inline void gemm_loop(f32x16_t (&acc)[4][4], const Opnd& A, const Opnd& B, int64_t k0, int nk, char* lds,
+                                 int wave, int lane, Hook&& hook) {
+  const int wa = wave >> 1, wb = wave & 1;
+  const int u = lane & 31, h = lane >> 5;
+  int le[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) le[m] = (u >> 3) * 1024 + (u & 7) * 128 + (((2 * m + h) ^ gswz(u)) * 16);
+  // block b's loads (blocks past the last reload the last one: in bounds, never used)
+  auto issue = [&](int q, int b, char* stage) {
+    const int64_t kbyte = (k0 + static_cast<int64_t>(b < nk ? b : nk - 1) * kGK) * 2;
+    if (q < 8)
+      g2lds16(A.base + kbyte + A.off[q], stage + q * kGroupBytes + wave * 1024);
+    else
+      g2lds16(B.base + kbyte + B.off[q - 8], stage + kOpBytes + (q - 8) * kGroupBytes + wave * 1024);
+  };
+  // fragment g of k-step m: g < 4 the A rows 128 wa + 32 g .., else the B rows 128 wb + 32 (g - 4) ..
+  auto frag = [&](const char* stage, int g, int m) {
+    const int off = g < 4 ? (4 * wa + g) * kGroupBytes : kOpBytes + (4 * wb + g - 4) * kGroupBytes;
+    return *reinterpret_cast<const u32x4_t*>(stage + off + le[m]);
+  };
+#pragma unroll
+  for (int q = 0; q < 16; ++q) issue(q, 0, lds);
+#pragma unroll
+  for (int q = 0; q < 16; ++q) issue(q, 1, lds + kStageBytes);
+  __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): block 0 has landed, block 1 is in flight
+  barrier_lds();
+  hook(0, lds);
+  u32x4_t f[2][8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) f[0][g] = frag(lds, g, 0);
+  for (int kb = 0; kb < nk; ++kb) {
+    char* st = lds + (kb & 1) * kStageBytes;
+    char* nxt = lds + ((kb & 1) ^ 1) * kStageBytes;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int cb = m & 1;
+      if (m == 3) {
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm0();
+        __syncthreads();  // block kb + 1 has landed; nobody reads block kb's stage any more
+        if (kb + 1 < nk) hook(kb + 1, nxt);
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        acc[q >> 2][q & 3] = mfma(f[cb][q >> 2], f[cb][4 + (q & 3)], acc[q >> 2][q & 3]);
+        if ((q & 1) == 0) {  // read order a0 b0 b1 b2 b3 a1 a2 a3: the order the next k-step uses them
+          constexpr int kOrder[8] = {0, 4, 5, 6, 7, 1, 2, 3};
+          const int g = kOrder[q >> 1];
+          f[cb ^ 1][g] = m < 3 ? frag(st, g, m + 1) : frag(nxt, g, 0);
+        }
+        if (m == 3) issue(q, kb + 2, st);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  wait_vm0();
+  __syncthreads();  // the trailing reloads have landed before LDS is reused
+}
+
+struct NoHook {
+  __device__ void operator()(int, char*) const {}
+};
+
+// Workgroup -> (row tile, column tile) with the column tile shared by the
+// workgroups of one XCD (blockIdx % 8 on MI355X): they walk the row tiles of
+// one column tile together, so its operand rows are fetched into that XCD's
+// L2 once.  Returns false for the padding workgroups of the last group.
+__device__ inline bool tile_of(int nrow, int ncol, int& rt, int& ct) {
+  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+  ct = (k / nrow) * 8 + x;
+  rt = k % nrow;
+  return ct < ncol;
+}
+
+// ---------------------------------------------------------------------------
+// pack: W [N, D] -> W^T [D, N64], zero for units >= N
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pack_wt_kernel(const uint16_t* __restrict__ W, uint16_t* __restrict__ WT,
+                                                      int64_t N, int64_t N64, int D) {
+  __shared__ uint16_t tile[64][66];
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int d0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t n = n0 + r;
+    const int d = d0 + tx;
+    tile[r][tx] = (n < N && d < D) ? W[n * D + d] : static_cast<uint16_t>(0);
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int d = d0 + r;
+    const int64_t n = n0 + tx;
+    if (d < D && n < N64) WT[static_cast<int64_t>(d) * N64 + n] = tile[tx][r];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// stats: per-token moment partials of the bf16 scores
+// ---------------------------------------------------------------------------
+struct TStatsParams {
+  const uint16_t* h;    // [Tv, dr]
+  const uint16_t* emb;  // [N, dr]
+  uint16_t* S;          // [Tv, N64] bf16 scores (zero for units >= N)
+  float* mom;           // [2 CT][Tv][2]
+  int64_t Tv, N, N64, dr;
+  int RT, CT;
+};
+
+__global__ __launch_bounds__(kGThreads) void tiled_stats_kernel(TStatsParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
+  int rt, ct;
+  if (!tile_of(p.RT, p.CT, rt, ct)) return;
+  const int64_t u0 = static_cast<int64_t>(ct) * kGRows, v0 = static_cast<int64_t>(rt) * kGRows;
+  const Opnd A = make_opnd(p.emb, p.dr, u0, p.N, 1, wave, lane);
+  const Opnd B = make_opnd(p.h, p.dr, v0, p.Tv, 1, wave, lane);
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+  gemm_loop(acc, A, B, 0, static_cast<int>(p.dr / kGK), lds, wave, lane, NoHook{});
+
+  const int64_t nleft = p.N - (u0 + 128 * wa + 4 * h);  // units of this wave-row left in the pool
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t t = v0 + 128 * wb + 32 * j + u;
+    uint16_t* srow = p.S + t * p.N64;
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int v = 0; v < 16; v += 4) {
+        uint32_t sq[2];
+#pragma unroll
+        for (int e2 = 0; e2 < 2; ++e2) {
+          const uint32_t sp = pack_bf16(acc[i][j][v + 2 * e2], acc[i][j][v + 2 * e2 + 1]);  // bf16 scores (v41:439)
+          float a = lo_f32(sp), b = hi_f32(sp);
+          const int r = 32 * i + 8 * (v >> 2) + 2 * e2;  // unit offset from u0 + 128 wa + 4 h
+          const bool oka = r < nleft, okb = r + 1 < nleft;
+          a = oka ? a : 0.f;
+          b = okb ? b : 0.f;
+          s1 += a;
+          s2 += __fmul_rn(a, a);
+          s1 += b;
+          s2 += __fmul_rn(b, b);
+          sq[e2] = pack_bf16(a, b);
+        }
+        const int64_t n0 = u0 + 128 * wa + 32 * i + 8 * (v >> 2) + 4 * h;
+        if (t < p.Tv && n0 < p.N64) {
+          typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<u32x2_t*>(srow + n0) = u32x2_t{sq[0], sq[1]};
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    s1 += __shfl_xor(s1, 32);
+    s2 += __shfl_xor(s2, 32);
+    if (h == 0 && t < p.Tv) {
+      float* m = p.mom + ((static_cast<int64_t>(2 * ct + wa)) * p.Tv + t) * 2;
+      m[0] = s1;
+      m[1] = s2;
+    }
+  }
+}
+
+// centred second moments of the stored scores: mom[t] = (sum s, sum (s - mean)^2)
+// over the N units of row t (v41:1719-1721); one wave per row
+__global__ __launch_bounds__(256) void tiled_centre_kernel(const uint16_t* __restrict__ S,
+                                                           const float* __restrict__ mean, float* __restrict__ mom,
+                                                           int64_t Tv, int64_t N, int64_t N64) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= Tv) return;
+  const float mu = mean[t];
+  const uint16_t* row = S + t * N64;
+  float s1 = 0.f, s2 = 0.f;
+  for (int64_t n0 = 8 * lane; n0 < N; n0 += 512) {
+    const u32x4_t q = *reinterpret_cast<const u32x4_t*>(row + n0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float s = (k & 1) ? hi_f32(q[k >> 1]) : lo_f32(q[k >> 1]);
+      const bool ok = n0 + k < N;
+      const float d = ok ? s - mu : 0.f;
+      s1 += ok ? s : 0.f;
+      s2 += __fmul_rn(d, d);
+    }
+  }
+  s1 = wave_sum(s1);
+  s2 = wave_sum(s2);
+  if (lane == 0) {
+    mom[2 * t] = s1;
+    mom[2 * t + 1] = s2;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gate: XR of one tile, the v4.1 gate of the stored scores, P over S in place
+// ---------------------------------------------------------------------------
+struct TGateParams {
+  const uint16_t* x;     // [T, D] (row v / routes)
+  const uint16_t* read;  // [N, D]
+  const float* tau;      // [Tv]
+  uint16_t* P;           // [Tv, N64]: the bf16 scores in, P out
+  float* tok_part;       // [2 CT][Tv][4]: sum gate, sum intensity, active count
+  uint32_t* mask32;      // [Tv][mask_words32] or null
+  int64_t mask_words32;
+  int64_t Tv, N, N64, D;
+  int routes, RT, CT;
+  GateParams gp;
+  float exp_scale;       // -sharpness * log2(e)
+};
+
+__global__ __launch_bounds__(kGThreads) void tiled_gate_kernel(TGateParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
+  int rt, ct;
+  if (!tile_of(p.RT, p.CT, rt, ct)) return;
+  const int64_t u0 = static_cast<int64_t>(ct) * kGRows, v0 = static_cast<int64_t>(rt) * kGRows;
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+  {
+    const Opnd A = make_opnd(p.read, p.D, u0, p.N, 1, wave, lane);
+    const Opnd B = make_opnd(p.x, p.D, v0, p.Tv, p.routes, wave, lane);
+    gemm_loop(acc, A, B, 0, static_cast<int>(p.D / kGK), lds, wave, lane, NoHook{});
+  }
+
+  // gate epilogue (v41:503-534): margin = s - tau - thr folded into
+  // arg = s * c + k (c = -sharpness log2 e), sigmoid = 1 / (1 + 2^arg),
+  // intensity = eps + min(max(s - tau - thr - cut, 0), maxi);
+  // P = bf16(bf16(g) * bf16(xr)), four consecutive units per load / store.
+  // FULL: every unit of the tile is in the pool (all but the last unit tile).
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  const int64_t nleft = p.N - (u0 + 128 * wa + 4 * h);  // units of this wave-row left in the pool
+  const float c_exp = p.exp_scale, eps = p.gp.eps, maxi = p.gp.maxi;
+  auto epilogue = [&](auto full_tag) {
+    constexpr bool FULL = decltype(full_tag)::value;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = v0 + 128 * wb + 32 * j + u;
+      const bool tok = t < p.Tv;
+      uint16_t* prow = p.P + (tok ? t : p.Tv - 1) * p.N64;
+      const float tau_thr = p.tau[tok ? t : p.Tv - 1] + p.gp.thr;
+      const float k_exp = -tau_thr * c_exp;
+      const float tau_cut = tau_thr + p.gp.cut;
+      float gs = 0.f, is = 0.f;
+      int na = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t nb = u0 + 128 * wa + 32 * i + 4 * h;
+        u32x2_t sv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)  // the last unit tile may reach past the row's N64 columns
+          sv[q] = FULL || nb + 8 * q < p.N64 ? *reinterpret_cast<const u32x2_t*>(prow + nb + 8 * q) : u32x2_t{0u, 0u};
+        uint32_t bits = 0;  // element v of the 16 at bit 15 - v: set <=> arg < 0 <=> act > 0.5
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) {
+          const uint32_t sp = sv[v >> 2][(v >> 1) & 1];  // bf16 scores of units v, v + 1
+          float g2[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float s = e ? hi_f32(sp) : lo_f32(sp);
+            const float arg = fmaf(s, c_exp, k_exp);
+            const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(arg));
+            float inten = eps + __builtin_amdgcn_fmed3f(s - tau_cut, 0.0f, maxi);
+            float g = act * inten;
+            uint32_t sign = __float_as_uint(arg);
+            if constexpr (!FULL) {  // units past N count for nothing
+              const bool ok = 32 * i + 8 * ((v + e) >> 2) + ((v + e) & 3) < nleft;
+              g = ok ? g : 0.f;
+              inten = ok ? inten : 0.f;
+              sign = ok ? sign : 0u;
+            }
+            gs += g;
+            is += inten;
+            bits = __builtin_amdgcn_alignbit(bits, sign, 31);  // bits << 1 | sign bit
+            g2[e] = g;
+          }
+          const uint32_t gq = pack_bf16(g2[0], g2[1]);                              // gate_bf (v41:516)
+          const uint32_t xq = pack_bf16(acc[i][j][v], acc[i][j][v + 1]);            // xr (v41:517)
+          sv[v >> 2][(v >> 1) & 1] = pack_bf16(lo_f32(gq) * lo_f32(xq), hi_f32(gq) * hi_f32(xq));  // (v41:518)
+        }
+        if (tok) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (FULL || nb + 8 * q < p.N64) *reinterpret_cast<u32x2_t*>(prow + nb + 8 * q) = sv[q];
+        }
+        // element v -> unit 8 (v / 4) + 4 h + v % 4 of the 32-unit block
+        const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
+        uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
+        m <<= 4 * h;
+        na += __builtin_popcount(m);
+        m |= __shfl_xor(m, 32);
+        const int64_t word = (u0 + 128 * wa + 32 * i) / 32;
+        if (p.mask32 && h == 0 && tok && word < p.mask_words32) p.mask32[t * p.mask_words32 + word] = m;
+        __builtin_amdgcn_sched_barrier(0);  // one accumulator at a time: keeps the live registers bounded
+      }
+      gs += __shfl_xor(gs, 32);
+      is += __shfl_xor(is, 32);
+      na += __shfl_xor(na, 32);
+      if (h == 0 && tok) {
+        float* tp = p.tok_part + (static_cast<int64_t>(2 * ct + wa) * p.Tv + t) * 4;
+        tp[0] = gs;
+        tp[1] = is;
+        tp[2] = static_cast<float>(na);
+        tp[3] = 0.f;
+      }
+    }
+  };
+  if (u0 + kGRows <= p.N)
+    epilogue(std::integral_constant<bool, true>{});
+  else
+    epilogue(std::integral_constant<bool, false>{});
+}
+
+// ---------------------------------------------------------------------------
+// write: OUT partial of one N-split = P[:, split units] . W^T[:, split units]^T
+// ---------------------------------------------------------------------------
+struct TWriteParams {
+  const uint16_t* P;   // [Tv, N64]
+  const uint16_t* wt;  // [D, N64]
+  float* out_part;     // [S][Tv][D]
+  int64_t Tv, N, N64, D, cs;
+  int nc, spc, S, RT, DT;
+};
+
+// zero the units outside [lo, hi) of the P tile of one k block (first unit kbase)
+__device__ inline void mask_units(char* tile, int64_t kbase, int64_t lo, int64_t hi) {
+  const int r = threadIdx.x, u = r & 31;
+  char* row = tile + (r >> 5) * kGroupBytes + (u >> 3) * 1024 + (u & 7) * 128;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    uint16_t* e = reinterpret_cast<uint16_t*>(row + ((q ^ gswz(u)) * 16));
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int64_t n = kbase + 8 * q + k;
+      if (n < lo || n >= hi) e[k] = 0;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kGThreads) void tiled_write_kernel(TWriteParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
+  // workgroups of one (token tile, split) on one XCD, consecutive: their D
+  // tiles share the P tile
+  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int dt = k % p.DT;
+  const int w = (k / p.DT) * 8 + x;
+  if (w >= p.RT * p.S) return;
+  const int rt = w % p.RT, split = w / p.RT;
+  // the split's k blocks: reference chunk c's blocks, divided evenly into spc
+  const int c = split / p.spc, sub = split % p.spc;
+  const int64_t lo = c * p.cs, hi = (c + 1) * p.cs < p.N ? (c + 1) * p.cs : p.N;
+  const int64_t b_lo = lo / kGK, b_hi = (hi + kGK - 1) / kGK, nb = b_hi - b_lo;
+  const int64_t kb0 = b_lo + nb * sub / p.spc, kb1 = b_lo + nb * (sub + 1) / p.spc;
+  const int64_t v0 = static_cast<int64_t>(rt) * kGRows, d0 = static_cast<int64_t>(dt) * kGRows;
+  const Opnd A = make_opnd(p.P, p.N64, v0, p.Tv, 1, wave, lane);
+  const Opnd B = make_opnd(p.wt, p.N64, d0, p.D, 1, wave, lane);
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+  auto hook = [&](int kb, char* stage) {
+    const int64_t kbase = (kb0 + kb) * kGK;
+    if (kbase < lo || kbase + kGK > hi) {  // a block shared with the neighbouring chunk
+      mask_units(stage, kbase, lo, hi);
+      __syncthreads();
+    }
+  };
+  gemm_loop(acc, A, B, kb0 * kGK, static_cast<int>(kb1 - kb0), lds, wave, lane, hook);
+
+  float* dst = p.out_part + static_cast<int64_t>(split) * p.Tv * p.D;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t t = v0 + 128 * wa + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (t >= p.Tv) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t d = d0 + 128 * wb + 32 * j + u;
+        if (d < p.D) dst[t * p.D + d] = acc[i][j][v];
+      }
+    }
+  }
+}
+
+// per-token sums of the gate kernel's partials, in a fixed order:
+// sum[t] = sum over s of part[s][t] (sum gate, sum intensity, active count).
+// 64 tokens per workgroup, four partial groups s = g mod 4 per token with
+// eight loads in flight each, combined in LDS.
+__global__ __launch_bounds__(256) void tiled_tok_sum_kernel(const float* __restrict__ part, float* __restrict__ sum,
+                                                            int64_t Tv, int S) {
+  __shared__ float4 red[4][64];
+  const int c = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 64 + c;
+  const int64_t tl = t < Tv ? t : Tv - 1;
+  float4 acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k] = float4{0.f, 0.f, 0.f, 0.f};
+  int s = grp;
+  for (; s + 28 < S; s += 32) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 q = *reinterpret_cast<const float4*>(part + (static_cast<int64_t>(s + 4 * k) * Tv + tl) * 4);
+      acc[k].x += q.x;
+      acc[k].y += q.y;
+      acc[k].z += q.z;
+    }
+  }
+  for (; s < S; s += 4) {
+    const float4 q = *reinterpret_cast<const float4*>(part + (static_cast<int64_t>(s) * Tv + tl) * 4);
+    acc[0].x += q.x;
+    acc[0].y += q.y;
+    acc[0].z += q.z;
+  }
+#pragma unroll
+  for (int k = 1; k < 8; ++k) {
+    acc[0].x += acc[k].x;
+    acc[0].y += acc[k].y;
+    acc[0].z += acc[k].z;
+  }
+  red[grp][c] = acc[0];
+  __syncthreads();
+  if (grp == 0 && t < Tv) {
+    float4 r = red[0][c];
+#pragma unroll
+    for (int g = 1; g < 4; ++g) {
+      r.x += red[g][c].x;
+      r.y += red[g][c].y;
+      r.z += red[g][c].z;
+    }
+    r.w = 0.f;
+    *reinterpret_cast<float4*>(sum + t * 4) = r;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct TGeo {
+  int64_t Tv, N, N64, cs;
+  int nc, RT, CT, DT, spc, S;
+};
+
+int64_t al256(int64_t b) { return (b + 255) & ~static_cast<int64_t>(255); }
+
+TGeo tgeo(const srw_desc_t& d) {
+  TGeo g{};
+  g.Tv = d.T * d.n_routes;
+  g.N = d.n_units;
+  g.N64 = (g.N + kGK - 1) / kGK * kGK;
+  g.cs = d.chunk_size > 0 && d.chunk_size < d.n_units ? d.chunk_size : d.n_units;
+  g.nc = static_cast<int>((g.N + g.cs - 1) / g.cs);
+  g.RT = static_cast<int>((g.Tv + kGRows - 1) / kGRows);
+  g.CT = static_cast<int>((g.N + kGRows - 1) / kGRows);
+  g.DT = static_cast<int>((d.d_model + kGRows - 1) / kGRows);
+  // splits per chunk of the write GEMM: enough workgroups for 256 CUs, every
+  // split at least one k block
+  int64_t min_blocks = INT64_MAX;
+  for (int c = 0; c < g.nc; ++c) {
+    const int64_t lo = c * g.cs, hi = (c + 1) * g.cs < g.N ? (c + 1) * g.cs : g.N;
+    const int64_t nb = (hi + kGK - 1) / kGK - lo / kGK;
+    min_blocks = nb < min_blocks ? nb : min_blocks;
+  }
+  const int64_t per_split = static_cast<int64_t>(g.RT) * g.DT * g.nc;
+  int64_t spc = (512 + per_split - 1) / per_split;
+  spc = spc < 1 ? 1 : spc;
+  spc = spc > min_blocks ? min_blocks : spc;
+  g.spc = static_cast<int>(spc);
+  g.S = g.nc * g.spc;
+  return g;
+}
+
+struct TLayout {
+  size_t wt, P, mom, tau, out_part, tok_part, tok_sum, total;
+};
+
+TLayout tlayout(const srw_desc_t& d, const TGeo& g) {
+  TLayout l{};
+  size_t off = 0;
+  l.wt = off;
+  off += al256(d.d_model * g.N64 * 2);
+  l.P = off;
+  off += al256(g.Tv * g.N64 * 2);
+  l.mom = off;
+  off += al256(static_cast<int64_t>(2 * g.CT) * g.Tv * 2 * 4);
+  l.tau = off;
+  off += al256(g.Tv * 4);
+  l.out_part = off;
+  off += al256(static_cast<int64_t>(g.S) * g.Tv * d.d_model * 4);
+  l.tok_part = off;
+  off += al256(static_cast<int64_t>(2 * g.CT) * g.Tv * 4 * 4);
+  l.tok_sum = off;
+  off += al256(g.Tv * 4 * 4);
+  l.total = off;
+  return l;
+}
+
+hipError_t set_lds(const void* fn) {
+  return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+}
+
+}  // namespace
+
+bool tiled_supports(const srw_desc_t& d) {
+  if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41) return false;
+  if (d.stats_mode != SRW_STATS_ONEPASS && d.stats_mode != SRW_STATS_CENTERED) return false;
+  if (d.flags & (SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
+  if (d.n_routes != 1 && d.n_routes != 2) return false;
+  if (d.d_model % kGK != 0 || d.d_route % kGK != 0) return false;
+  return true;
+}
+
+size_t tiled_workspace_bytes(const srw_desc_t& d) { return tlayout(d, tgeo(d)).total; }
+
+hipError_t tiled_forward(const LaunchArgs& a) {
+  const srw_desc_t& d = a.d;
+  const TGeo g = tgeo(d);
+  const TLayout l = tlayout(d, g);
+  uint16_t* wt = reinterpret_cast<uint16_t*>(a.ws + l.wt);
+  uint16_t* P = reinterpret_cast<uint16_t*>(a.ws + l.P);
+  float* mom = reinterpret_cast<float*>(a.ws + l.mom);
+  float* tau = reinterpret_cast<float*>(a.ws + l.tau);
+  float* out_part = reinterpret_cast<float*>(a.ws + l.out_part);
+  float* tok_part = reinterpret_cast<float*>(a.ws + l.tok_part);
+  float* tok_sum = reinterpret_cast<float*>(a.ws + l.tok_sum);
+  const int D = static_cast<int>(d.d_model);
+  hipError_t e;
+  static_assert(kGemmLds <= 160 * 1024, "LDS per workgroup");
+  for (const void* fn : {reinterpret_cast<const void*>(tiled_stats_kernel),
+                         reinterpret_cast<const void*>(tiled_gate_kernel),
+                         reinterpret_cast<const void*>(tiled_write_kernel)})
+    if ((e = set_lds(fn)) != hipSuccess) return e;
+
+  if (!(d.flags & SRW_FLAG_POOL_CACHED)) {
+    const dim3 grid_p(static_cast<unsigned>(g.N64 / 64), static_cast<unsigned>((D + 63) / 64));
+    hipLaunchKernelGGL(pack_wt_kernel, grid_p, dim3(256), 0, a.stream, static_cast<const uint16_t*>(a.in.write), wt,
+                       g.N, g.N64, D);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  const unsigned grid_rc = static_cast<unsigned>(8 * g.RT * ((g.CT + 7) / 8));
+  TStatsParams sp{};
+  sp.h = static_cast<const uint16_t*>(a.in.h);
+  sp.emb = static_cast<const uint16_t*>(a.in.emb);
+  sp.S = P;
+  sp.mom = mom;
+  sp.Tv = g.Tv;
+  sp.N = g.N;
+  sp.N64 = g.N64;
+  sp.dr = d.d_route;
+  sp.RT = g.RT;
+  sp.CT = g.CT;
+  hipLaunchKernelGGL(tiled_stats_kernel, dim3(grid_rc), dim3(kGThreads), kGemmLds, a.stream, sp);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  int S_st = 2 * g.CT;
+  if (d.stats_mode == SRW_STATS_CENTERED) {
+    // row means, then sum (s - mean)^2 over the stored scores into mom[0][t]
+    if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, S_st, g.N, 2, nullptr, kTauMean, a.stream)) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(tiled_centre_kernel, dim3(static_cast<unsigned>((g.Tv + 3) / 4)), dim3(256), 0, a.stream, P,
+                       tau, mom, g.Tv, g.N, g.N64);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    S_st = 1;
+  }
+  if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, S_st, g.N, 2, nullptr,
+                      d.stats_mode == SRW_STATS_CENTERED ? kTauCentered : kTauOnePass, a.stream)) != hipSuccess)
+    return e;
+
+  TGateParams gp{};
+  gp.x = static_cast<const uint16_t*>(a.in.x);
+  gp.read = static_cast<const uint16_t*>(a.in.read);
+  gp.tau = tau;
+  gp.P = P;
+  gp.tok_part = tok_part;
+  gp.mask32 = reinterpret_cast<uint32_t*>(a.o.pass_mask);
+  gp.mask_words32 = 2 * a.words;
+  gp.Tv = g.Tv;
+  gp.N = g.N;
+  gp.N64 = g.N64;
+  gp.D = D;
+  gp.routes = d.n_routes;
+  gp.RT = g.RT;
+  gp.CT = g.CT;
+  gp.gp = a.gp;
+  gp.exp_scale = -d.sharpness * 1.4426950408889634f;
+  dominant_kernel_begin(a.stream);
+  hipLaunchKernelGGL(tiled_gate_kernel, dim3(grid_rc), dim3(kGThreads), kGemmLds, a.stream, gp);
+  dominant_kernel_end(a.stream);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+
+  TWriteParams wp{};
+  wp.P = P;
+  wp.wt = wt;
+  wp.out_part = out_part;
+  wp.Tv = g.Tv;
+  wp.N = g.N;
+  wp.N64 = g.N64;
+  wp.D = D;
+  wp.cs = g.cs;
+  wp.nc = g.nc;
+  wp.spc = g.spc;
+  wp.S = g.S;
+  wp.RT = g.RT;
+  wp.DT = g.DT;
+  const unsigned grid_w = static_cast<unsigned>(8 * g.DT * ((static_cast<int64_t>(g.RT) * g.S + 7) / 8));
+  hipLaunchKernelGGL(tiled_write_kernel, dim3(grid_w), dim3(kGThreads), kGemmLds, a.stream, wp);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+
+  hipLaunchKernelGGL(tiled_tok_sum_kernel, dim3(static_cast<unsigned>((g.Tv + 63) / 64)), dim3(256), 0, a.stream,
+                     tok_part, tok_sum, g.Tv, 2 * g.CT);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+
+  FinalizeArgs f{};
+  f.out_part = out_part;
+  f.tok_part = tok_sum;
+  f.out = static_cast<uint16_t*>(a.o.out);
+  f.gate_sum = a.o.gate_sum;
+  f.den = a.o.den;
+  f.n_active = a.o.n_active;
+  f.T = g.Tv;
+  f.D = D;
+  f.S = g.S;
+  f.spc = g.spc;
+  f.S_tok = 1;
+  f.tps = 4;
+  f.scale = d.scale;
+  f.gp = a.gp;
+  f.exp_scale = -d.sharpness * 1.4426950408889634f;
+  return launch_finalize(f, a.stream);
+}
+
+}  // namespace srw

@@ -65,7 +65,7 @@ class SrwPlan:
                  scale: float = 1.0, chunk_size: int = 0, diag: bool = False,
                  want_mask: bool = True, emulate: bool = False,
                  sparse_skip: bool = False, force_generic: bool = False,
-                 want_gate: bool = False):
+                 want_gate: bool = False, tiled: bool = False):
         if x.dim() != 2:
             raise ValueError("x must be [T, D]")
         T, D = x.shape
@@ -110,7 +110,8 @@ class SrwPlan:
         desc.chunk_size = int(chunk_size)
         desc.flags = ((C.SRW_FLAG_DIAG if diag else 0) | (C.SRW_FLAG_EMULATE if emulate else 0)
                       | (C.SRW_FLAG_SPARSE_SKIP if sparse_skip else 0)
-                      | (C.SRW_FLAG_NO_FAST if force_generic else 0))
+                      | (C.SRW_FLAG_NO_FAST if force_generic else 0)
+                      | (C.SRW_FLAG_TILED if tiled else 0))
 
         words = (N + 63) // 64
         self.out = torch.empty((T, R, D), dtype=dt, device=dev)
@@ -177,7 +178,7 @@ def srw_forward(x, h, emb, tau_offset, read, write, *, gate: str = "v41",
                 scale: float = 1.0, chunk_size: int = 0, diag: bool = False,
                 want_mask: bool = True, emulate: bool = False,
                 sparse_skip: bool = False, force_generic: bool = False,
-                want_gate: bool = False) -> dict:
+                want_gate: bool = False, tiled: bool = False) -> dict:
     """One SRW layer forward on the GPU.
 
     x [T, D]; h [T, R, dr] (R = 1 or 2) or the tensor ``x`` itself (R = 1,
@@ -189,7 +190,9 @@ def srw_forward(x, h, emb, tau_offset, read, write, *, gate: str = "v41",
     the rounded scores, fused_gate_srw) | "centered" (two-pass,
     _srw_inference) | "gram" (closed form from E^T E); ``chunk_size`` the
     reference's N-chunk (its partial write GEMMs are rounded to bf16 per
-    chunk); ``scale`` multiplies out after the den division.
+    chunk); ``scale`` multiplies out after the den division; ``tiled`` runs
+    the tiled-GEMM kernels (the gated product materialised in the workspace)
+    even where a fused kernel exists -- they serve d_model > 384 anyway.
 
     Returns a dict: out [T, R, D] (input dtype), gate_sum / den [T, R] f32,
     n_active [T, R] int32, pass_mask [T, R, ceil(N/64)] int64 (bit n % 64 of
@@ -200,6 +203,6 @@ def srw_forward(x, h, emb, tau_offset, read, write, *, gate: str = "v41",
     plan = SrwPlan(x, h, emb, tau_offset, read, write, gate=gate, stats=stats,
                    consts=consts, scale=scale, chunk_size=chunk_size, diag=diag,
                    want_mask=want_mask, emulate=emulate, sparse_skip=sparse_skip,
-                   force_generic=force_generic, want_gate=want_gate)
+                   force_generic=force_generic, want_gate=want_gate, tiled=tiled)
     plan.launch()
     return plan.results()

@@ -97,6 +97,12 @@ typedef enum srw_stats_mode {
                                       workspace (decode steps, layers sharing one pool).
                                       No counterpart in the reference, which recasts its
                                       pools on every call (v41:423-430). */
+#define SRW_FLAG_TILED 0x20u      /* run the tiled-GEMM kernels (gated product P materialised
+                                     in the workspace as bf16) even where a fused kernel
+                                     exists; without the flag they serve bf16 shapes the
+                                     fused kernels do not (d_model > 384, e.g. 1024 / 1280 /
+                                     2048; both widths multiples of 64).  No counterpart in
+                                     the reference (a kernel-family choice). */
 
 typedef struct srw_desc {
   int64_t T;          /* tokens (B*S) */

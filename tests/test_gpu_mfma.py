@@ -1,6 +1,6 @@
-"""GPU parity of the matrix-core path (libsrw_amd.so "mfma_bf16" kernels,
-through the C ABI) against the CPU oracle's restatement of fused_gate_srw
-(models/dawn_spatial_v41_exp.py:415-635).
+"""GPU parity of the matrix-core paths (libsrw_amd.so's fused "mfma_bf16"
+kernels and the "tiled_bf16" GEMM family, through the C ABI) against the CPU
+oracle's restatement of fused_gate_srw (models/dawn_spatial_v41_exp.py:415-635).
 
 Shapes cover: d_route == d_model with h aliasing x (the Know-pool form of
 the benchmark), a separate router h with d_route = 128, ragged N (not a
@@ -33,6 +33,9 @@ def _inputs(pkg, T, D, dr, N, h_is_x, seed, tau=-0.5):
     inp = pkg.inputs.make_pool_inputs(shape, seed=seed)
     inp["tau_offset"].fill_(tau)
     return inp
+
+
+FAMILIES = {"fused": ("mfma_bf16", {}), "tiled": ("tiled_bf16", {"tiled": True})}
 
 
 def _gpu(pkg, dev, inp, chunk_size, **kw):
@@ -107,15 +110,17 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("family", sorted(FAMILIES))
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "T{}D{}dr{}N{}{}c{}".format(
     c[0], c[1], c[2], c[3], "x" if c[4] else "", c[5]))
-def test_mfma_matches_fused_oracle(pkg, dev, case):
+def test_mfma_matches_fused_oracle(pkg, dev, case, family):
     T, D, dr, N, hx, max_chunk, seed = case
-    print(f"[gpu] mfma bf16 {case}", flush=True)
+    print(f"[gpu] {family} bf16 {case}", flush=True)
     inp = _inputs(pkg, T, D, dr, N, hx, seed)
     _, cs = srw_ref.chunk_plan(N, max_chunk)
-    got = _gpu(pkg, dev, inp, cs)
-    assert got["path"] == "mfma_bf16"
+    path, kw = FAMILIES[family]
+    got = _gpu(pkg, dev, inp, cs, **kw)
+    assert got["path"] == path
     ref, tr = _oracle(inp, max_chunk)
     _check(got, ref, tr, T, N, D)
 
@@ -166,19 +171,21 @@ CENTERED_CASES = [
 ]
 
 
+@pytest.mark.parametrize("family", sorted(FAMILIES))
 @pytest.mark.parametrize("case", CENTERED_CASES, ids=lambda c: "T{}D{}dr{}N{}{}".format(
     c[0], c[1], c[2], c[3], "x" if c[4] else ""))
-def test_mfma_centered_matches_srw_inference_oracle(pkg, dev, case):
+def test_mfma_centered_matches_srw_inference_oracle(pkg, dev, case, family):
     """bf16 _srw_inference (v41:1713-1738) on the matrix cores: the two-pass
     centred std (:1719-1721) from a second moments pass over the same bf16
     scores, one unchunked write GEMM rounded once.  Same bar as the fused
     path: out, den, gate sum and the passing set against the oracle; a tail
     tile that counted padded units as deviations of -mean would move den."""
     T, D, dr, N, hx, seed = case
-    print(f"[gpu] mfma bf16 centered {case}", flush=True)
+    print(f"[gpu] {family} bf16 centered {case}", flush=True)
     inp = _inputs(pkg, T, D, dr, N, hx, seed)
-    got = _gpu(pkg, dev, inp, 0, stats="centered")
-    assert got["path"] == "mfma_bf16"
+    path, kw = FAMILIES[family]
+    got = _gpu(pkg, dev, inp, 0, stats="centered", **kw)
+    assert got["path"] == path
     x = inp["x"].to(BF)
     h = x if "h" not in inp else inp["h"][:, 0].to(BF)
     ref, tr = srw_ref.srw_inference(x, h, inp["emb"].to(BF), inp["tau_offset"], inp["read"].to(BF),
@@ -202,16 +209,18 @@ PAIRED_CASES = [
 ]
 
 
+@pytest.mark.parametrize("family", sorted(FAMILIES))
 @pytest.mark.parametrize("case", PAIRED_CASES, ids=lambda c: "T{}D{}dr{}N{}c{}".format(*c[:5]))
-def test_mfma_paired_matches_fused_paired_oracle(pkg, dev, case):
+def test_mfma_paired_matches_fused_paired_oracle(pkg, dev, case, family):
     """Paired QK routes (fused_gate_srw_paired, v41:640-909) on the matrix cores."""
     T, D, dr, N, max_chunk, seed = case
-    print(f"[gpu] mfma bf16 paired {case}", flush=True)
+    print(f"[gpu] {family} bf16 paired {case}", flush=True)
     shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=2)
     inp = pkg.inputs.make_pool_inputs(shape, seed=seed)
     _, cs = srw_ref.chunk_plan(N, max_chunk)
-    got = _gpu(pkg, dev, inp, cs)
-    assert got["path"] == "mfma_bf16"
+    path, kw = FAMILIES[family]
+    got = _gpu(pkg, dev, inp, cs, **kw)
+    assert got["path"] == path
     ref, tr = srw_ref.fused_gate_srw_paired(
         inp["x"][None], inp["h"][None], inp["emb"], inp["tau_offset"].reshape(1, T, 2, 1),
         inp["read"], inp["write"], max_chunk_size=max_chunk, return_trace=True)
@@ -355,7 +364,7 @@ def test_mfma_diagnostics_match_generic(pkg, dev, case):
     print(f"[gpu] mfma diagnostics {case}", flush=True)
     shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=R, h_is_x=hx)
     inp = pkg.inputs.make_pool_inputs(shape, seed=seed)
-    inp["tau_offset"].uniform_(-0.9, 0.3)
+    inp["tau_offset"].uniform_(-0.9, 0.3, generator=torch.Generator().manual_seed(seed))
     _, cs = srw_ref.chunk_plan(N, max_chunk)
     x = inp["x"].to(BF).to(dev)
     h = x if hx else inp["h"].to(BF).to(dev)
@@ -388,8 +397,16 @@ def test_mfma_diagnostics_match_generic(pkg, dev, case):
         assert (d <= bound).all(), n
     for n in ("gate_max", "int_max", "int_sum"):
         assert torch.allclose(td_f[..., col[n]], td_g[..., col[n]], rtol=2e-3, atol=1e-6), n
-    assert torch.allclose(td_f[..., col["g_log_g"]], td_g[..., col["g_log_g"]], rtol=2e-3,
-                          atol=1e-3), "g_log_g"
+    # sum g log g mixes positive (g > 1) and negative terms and may cancel:
+    # bound the difference by the sum of the terms' magnitudes (v4.1 gate of
+    # the oracle's bf16 scores and the generic kernel's tau)
+    m = sc - td_g[..., col["tau"]][..., None] - 0.5
+    gt = torch.sigmoid(500.0 * m) * (1e-4 + torch.clamp(m - 0.01, 0.0, 10.0))
+    mag = (gt * torch.log(gt + 1e-8)).abs().sum(dim=-1)
+    d = (td_f[..., col["g_log_g"]] - td_g[..., col["g_log_g"]]).abs()
+    bound = 1e-3 + 2e-3 * td_g[..., col["g_log_g"]].abs() + 1e-4 * mag
+    print(f"  g_log_g: max |diff| {float(d.max()):.3e}, max diff/bound {float((d / bound).max()):.3f}", flush=True)
+    assert (d <= bound).all(), "g_log_g"
     for n in ("n_strong", "n_boundary", "n_band075", "n_band030", "n_int_cap"):
         d = (td_f[..., col[n]] - td_g[..., col[n]]).abs()
         print(f"  {n}: max |diff| {float(d.max())}", flush=True)
