@@ -19,7 +19,7 @@ import threading
 import torch  # noqa: F401  (must precede loading the HIP library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libsrw_amd.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # srw_status_t
 SRW_OK, SRW_EINVAL, SRW_EUNSUPPORTED, SRW_EHIP, SRW_EWORKSPACE = range(5)
@@ -50,7 +50,7 @@ UDIAG = ("score_sum", "gate_max")
 EXPORTED_SYMBOLS = (
     "srw_abi_version", "srw_status_string", "srw_desc_init",
     "srw_workspace_size", "srw_forward", "srw_last_path",
-    "srw_set_kernel_events",
+    "srw_set_kernel_events", "srw_backward_workspace_size", "srw_backward",
 )
 
 
@@ -75,6 +75,16 @@ class SrwTensors(ctypes.Structure):
 class SrwOutputs(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "out", "gate_sum", "den", "n_active", "pass_mask", "token_diag", "unit_diag", "gate")]
+
+
+class SrwCotangents(ctypes.Structure):
+    _fields_ = [("d_out", ctypes.c_void_p), ("out", ctypes.c_void_p),
+                ("d_score_lb", ctypes.c_float), ("d_dead_penalty", ctypes.c_float)]
+
+
+class SrwGrads(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "dx", "dh", "demb", "dtau_offset", "dread", "dwrite")]
 
 
 class SrwError(RuntimeError):
@@ -122,6 +132,12 @@ def load_library() -> ctypes.CDLL:
         lib.srw_last_path.argtypes = []
         lib.srw_set_kernel_events.restype = ctypes.c_int
         lib.srw_set_kernel_events.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        lib.srw_backward_workspace_size.restype = ctypes.c_int
+        lib.srw_backward_workspace_size.argtypes = [ctypes.POINTER(SrwDesc), ctypes.POINTER(ctypes.c_size_t)]
+        lib.srw_backward.restype = ctypes.c_int
+        lib.srw_backward.argtypes = [
+            ctypes.POINTER(SrwDesc), ctypes.POINTER(SrwTensors), ctypes.POINTER(SrwCotangents),
+            ctypes.POINTER(SrwGrads), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         got = lib.srw_abi_version()
         if got != ABI_VERSION:
             raise SrwLibraryError(f"libsrw_amd.so ABI {got} != binding ABI {ABI_VERSION}")
@@ -144,6 +160,12 @@ def desc_init() -> SrwDesc:
 def workspace_size(desc: SrwDesc) -> int:
     n = ctypes.c_size_t(0)
     check(load_library().srw_workspace_size(ctypes.byref(desc), ctypes.byref(n)))
+    return int(n.value)
+
+
+def backward_workspace_size(desc: SrwDesc) -> int:
+    n = ctypes.c_size_t(0)
+    check(load_library().srw_backward_workspace_size(ctypes.byref(desc), ctypes.byref(n)))
     return int(n.value)
 
 

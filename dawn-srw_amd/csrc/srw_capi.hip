@@ -176,6 +176,52 @@ srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw
   return e == hipSuccess ? SRW_OK : SRW_EHIP;
 }
 
+srw_status_t srw_backward_workspace_size(const srw_desc_t* d, size_t* bytes) {
+  srw_status_t st = validate(d);
+  if (st != SRW_OK) return st;
+  if (!bytes) return SRW_EINVAL;
+  if (!srw::tiled_backward_supports(*d)) return SRW_EUNSUPPORTED;
+  *bytes = align256(srw::tiled_backward_workspace_bytes(*d));
+  return SRW_OK;
+}
+
+srw_status_t srw_backward(const srw_desc_t* d, const srw_tensors_t* in, const srw_cotangents_t* cot,
+                          const srw_grads_t* grads, void* workspace, size_t workspace_bytes, void* stream) {
+  srw_status_t st = validate(d);
+  if (st != SRW_OK) return st;
+  if (!in || !cot || !grads) return SRW_EINVAL;
+  if (!srw::tiled_backward_supports(*d)) return SRW_EUNSUPPORTED;
+  if (d->T == 0) {
+    g_last_path = "empty";
+    return SRW_OK;
+  }
+  if (!in->x || !in->h || !in->emb || !in->tau_offset || !in->read || !in->write) return SRW_EINVAL;
+  if (!cot->d_out || !cot->out) return SRW_EINVAL;
+  if (!grads->dx || !grads->dh || !grads->demb || !grads->dtau_offset || !grads->dread || !grads->dwrite)
+    return SRW_EINVAL;
+  if (!isfinite(cot->d_score_lb) || !isfinite(cot->d_dead_penalty)) return SRW_EINVAL;
+  const size_t need = align256(srw::tiled_backward_workspace_bytes(*d));
+  if (!workspace || workspace_bytes < need) return SRW_EWORKSPACE;
+  srw::BackwardArgs a{};
+  a.d = *d;
+  a.in = *in;
+  a.cot = *cot;
+  a.g = *grads;
+  a.gp.sharp = d->sharpness;
+  a.gp.thr = d->act_threshold;
+  a.gp.cut = d->act_cutoff;
+  a.gp.eps = d->epsilon;
+  a.gp.maxi = d->max_intensity;
+  a.gp.cap_thresh = (d->epsilon + d->max_intensity) - 1e-3f;
+  a.ws = static_cast<char*>(workspace);
+  a.ws_bytes = workspace_bytes;
+  a.stream = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  const hipError_t e = srw::tiled_backward(a);
+  g_last_path = "tiled_bwd_bf16";
+  return e == hipSuccess ? SRW_OK : SRW_EHIP;
+}
+
 const char* srw_last_path(void) { return g_last_path; }
 
 srw_status_t srw_set_kernel_events(void* start, void* stop) {

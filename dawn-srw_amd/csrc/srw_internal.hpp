@@ -84,6 +84,23 @@ struct FinalizeArgs {
 };
 hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s);
 
+// Everything the backward needs for one srw_backward call.
+struct BackwardArgs {
+  srw_desc_t d;
+  srw_tensors_t in;
+  srw_cotangents_t cot;
+  srw_grads_t g;
+  GateParams gp;
+  char* ws;
+  size_t ws_bytes;
+  hipStream_t stream;
+};
+
+// Backward (VJP) on the tiled MFMA kernels, see srw_tiled.hip.
+bool tiled_backward_supports(const srw_desc_t& d);
+size_t tiled_backward_workspace_bytes(const srw_desc_t& d);
+hipError_t tiled_backward(const BackwardArgs& a);
+
 // Tiled-GEMM kernels for wide layers (bf16), see srw_tiled.hip: P = gated
 // product materialised in HBM; d_model and d_route multiples of 64.
 bool tiled_supports(const srw_desc_t& d);

@@ -48,6 +48,7 @@ constexpr int kOpBytes = kGRows * kGK * 2;  // 32 KB
 constexpr int kStageBytes = 2 * kOpBytes;   // A and B tiles
 constexpr int kGemmLds = 2 * kStageBytes;   // two stages: 128 KB
 constexpr int kGroupBytes = 32 * kGK * 2;   // 32 rows: one MFMA operand's rows
+constexpr int kNAlign = 64;                 // padding of the stored [., N] / [., T] rows
 
 // An operand tile in LDS: 32-row groups of 4 KB; row u of a group at
 // (u / 8) * 1 KB + (u % 8) * 128 B, its 16-byte piece q in slot q ^ gswz(u).
@@ -296,7 +297,9 @@ struct TGateParams {
   const uint16_t* x;     // [T, D] (row v / routes)
   const uint16_t* read;  // [N, D]
   const float* tau;      // [Tv]
-  uint16_t* P;           // [Tv, N64]: the bf16 scores in, P out
+  uint16_t* P;           // [Tv, N64]: the bf16 scores in, P out (in place)
+  uint16_t* P_out;       // KEEP: P here instead, the scores stay in P
+  uint16_t* XR_out;      // KEEP: bf16 x.r [Tv, N64]
   float* tok_part;       // [2 CT][Tv][4]: sum gate, sum intensity, active count
   uint32_t* mask32;      // [Tv][mask_words32] or null
   int64_t mask_words32;
@@ -306,6 +309,9 @@ struct TGateParams {
   float exp_scale;       // -sharpness * log2(e)
 };
 
+// KEEP (the backward's recompute): P and x.r go to P_out / XR_out and the
+// stored scores stay.
+template <bool KEEP>
 __global__ __launch_bounds__(kGThreads) void tiled_gate_kernel(TGateParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
@@ -348,7 +354,7 @@ __global__ __launch_bounds__(kGThreads) void tiled_gate_kernel(TGateParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int64_t nb = u0 + 128 * wa + 32 * i + 4 * h;
-        u32x2_t sv[4];
+        u32x2_t sv[4], xv[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q)  // the last unit tile may reach past the row's N64 columns
           sv[q] = FULL || nb + 8 * q < p.N64 ? *reinterpret_cast<const u32x2_t*>(prow + nb + 8 * q) : u32x2_t{0u, 0u};
@@ -378,12 +384,20 @@ __global__ __launch_bounds__(kGThreads) void tiled_gate_kernel(TGateParams p) {
           }
           const uint32_t gq = pack_bf16(g2[0], g2[1]);                              // gate_bf (v41:516)
           const uint32_t xq = pack_bf16(acc[i][j][v], acc[i][j][v + 1]);            // xr (v41:517)
+          if constexpr (KEEP) xv[v >> 2][(v >> 1) & 1] = xq;
           sv[v >> 2][(v >> 1) & 1] = pack_bf16(lo_f32(gq) * lo_f32(xq), hi_f32(gq) * hi_f32(xq));  // (v41:518)
         }
         if (tok) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (FULL || nb + 8 * q < p.N64) *reinterpret_cast<u32x2_t*>(prow + nb + 8 * q) = sv[q];
+          for (int q = 0; q < 4; ++q) {
+            if (!(FULL || nb + 8 * q < p.N64)) continue;
+            if constexpr (KEEP) {
+              *reinterpret_cast<u32x2_t*>(p.P_out + t * p.N64 + nb + 8 * q) = sv[q];
+              *reinterpret_cast<u32x2_t*>(p.XR_out + t * p.N64 + nb + 8 * q) = xv[q];
+            } else {
+              *reinterpret_cast<u32x2_t*>(prow + nb + 8 * q) = sv[q];
+            }
+          }
         }
         // element v -> unit 8 (v / 4) + 4 h + v % 4 of the 32-unit block
         const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
@@ -553,7 +567,7 @@ TGeo tgeo(const srw_desc_t& d) {
   TGeo g{};
   g.Tv = d.T * d.n_routes;
   g.N = d.n_units;
-  g.N64 = (g.N + kGK - 1) / kGK * kGK;
+  g.N64 = (g.N + kNAlign - 1) / kNAlign * kNAlign;
   g.cs = d.chunk_size > 0 && d.chunk_size < d.n_units ? d.chunk_size : d.n_units;
   g.nc = static_cast<int>((g.N + g.cs - 1) / g.cs);
   g.RT = static_cast<int>((g.Tv + kGRows - 1) / kGRows);
@@ -612,7 +626,7 @@ bool tiled_supports(const srw_desc_t& d) {
   if (d.stats_mode != SRW_STATS_ONEPASS && d.stats_mode != SRW_STATS_CENTERED) return false;
   if (d.flags & (SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
   if (d.n_routes != 1 && d.n_routes != 2) return false;
-  if (d.d_model % kGK != 0 || d.d_route % kGK != 0) return false;
+  if (d.d_model % kNAlign != 0 || d.d_route % kNAlign != 0) return false;
   return true;
 }
 
@@ -633,7 +647,7 @@ hipError_t tiled_forward(const LaunchArgs& a) {
   hipError_t e;
   static_assert(kGemmLds <= 160 * 1024, "LDS per workgroup");
   for (const void* fn : {reinterpret_cast<const void*>(tiled_stats_kernel),
-                         reinterpret_cast<const void*>(tiled_gate_kernel),
+                         reinterpret_cast<const void*>(tiled_gate_kernel<false>),
                          reinterpret_cast<const void*>(tiled_write_kernel)})
     if ((e = set_lds(fn)) != hipSuccess) return e;
 
@@ -689,7 +703,7 @@ hipError_t tiled_forward(const LaunchArgs& a) {
   gp.gp = a.gp;
   gp.exp_scale = -d.sharpness * 1.4426950408889634f;
   dominant_kernel_begin(a.stream);
-  hipLaunchKernelGGL(tiled_gate_kernel, dim3(grid_rc), dim3(kGThreads), kGemmLds, a.stream, gp);
+  hipLaunchKernelGGL(tiled_gate_kernel<false>, dim3(grid_rc), dim3(kGThreads), kGemmLds, a.stream, gp);
   dominant_kernel_end(a.stream);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 
@@ -732,6 +746,595 @@ hipError_t tiled_forward(const LaunchArgs& a) {
   f.gp = a.gp;
   f.exp_scale = -d.sharpness * 1.4426950408889634f;
   return launch_finalize(f, a.stream);
+}
+
+// ===========================================================================
+// Backward (VJP) of fused_gate_srw for one route: the gradients of
+// <d_out, out> + d_lb * score_lb + d_pen * dead_penalty (the outputs the
+// reference's training loss uses, scripts/train_jax.py:586-603) with respect
+// to x, h, emb, tau_offset, read and write.  The forward's scores, gates and
+// products are recomputed (the reference checkpoints both scans, v41:434,
+// 489); every [T, N] intermediate lives in the workspace in bf16 (the
+// derivative of the gate in fp32), and the six contractions run on the same
+// tiled MFMA main loop as the forward:
+//   dP  = draw . W^T          (epilogue: the gate derivative -> dm, d(xr))
+//   dW  = P^T . draw,  dR = d(xr)^T . x,  dE = ds^T . h       (K = tokens)
+//   dx  = d(xr) . R,   dh = ds . E                             (K = units)
+// ===========================================================================
+namespace {
+
+// per-token mean, variance, std + 1e-8 and tau from the moment partials
+// (same expressions as srw_tau_kernel, v41:461-464)
+__global__ __launch_bounds__(256) void bwd_token_stats_kernel(const float* __restrict__ mom, int S_st, int64_t T,
+                                                              int64_t N, const float* __restrict__ tau_off,
+                                                              float* __restrict__ mean, float* __restrict__ var,
+                                                              float* __restrict__ sdev, float* __restrict__ tau) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float a = 0.f, b = 0.f;
+  for (int s = lane; s < S_st; s += 64) {
+    a += mom[(static_cast<int64_t>(s) * T + t) * 2];
+    b += mom[(static_cast<int64_t>(s) * T + t) * 2 + 1];
+  }
+  a = wave_sum(a);
+  b = wave_sum(b);
+  if (lane == 0) {
+    const float fN = static_cast<float>(N);
+    const float mu = a / fN;
+    const float v = b / fN - __fmul_rn(mu, mu);
+    const float sd = sqrtf(v) + 1e-8f;
+    mean[t] = mu;
+    var[t] = v;
+    sdev[t] = sd;
+    tau[t] = mu + __fmul_rn(tau_off[t], sd);
+  }
+}
+
+// draw = bf16(d_out * scale) / den as bf16 (the cotangent of the chunk dots),
+// and the den term dden = -sum_d dq * (raw / den) / den where den = max(sum
+// intensity, 1) is differentiable (v41:584-585); raw / den from the forward's
+// out
+__global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__ d_out,
+                                                       const uint16_t* __restrict__ out,
+                                                       const float* __restrict__ tok_sum, float scale, int D,
+                                                       uint16_t* __restrict__ draw, float* __restrict__ dden) {
+  __shared__ float red[4];
+  const int64_t t = blockIdx.x;
+  const float zsum = tok_sum[t * 4 + 1];
+  const float den = fmaxf(zsum, 1.0f);
+  float acc = 0.f;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    const float dq = round_bf16(d_out[t * D + d] * scale);
+    const float o = bf16_to_f32(out[t * D + d]) / scale;
+    acc += dq * o;
+    draw[t * D + d] = f32_to_bf16_bits(dq / den);
+  }
+  acc = block_sum<256>(acc, red);
+  if (threadIdx.x == 0) dden[t] = zsum > 1.0f ? -acc / den : 0.f;
+}
+
+// dP = draw . W^T per (256-unit, 256-token) tile, then the derivative of the
+// gate (v41:506-518) elementwise: d(gate_bf) and d(xr) from the bf16 product,
+// through act * intensity, the cutoff / cap clamps and the den term, to dm =
+// d loss / d margin; stores d(xr) (bf16) and dm (fp32), and per-token
+// partial sums of dm (the tau term)
+struct TBwdGateParams {
+  const uint16_t* write;  // [N, D]
+  const uint16_t* draw;   // [T, D]
+  const uint16_t* S;      // [T, N64] bf16 scores
+  const uint16_t* XR;     // [T, N64] bf16 x.r
+  const float* tau;       // [T]
+  const float* dden;      // [T]
+  uint16_t* DXR;          // [T, N64]
+  float* DM;              // [T, N64]
+  float* dm_part;         // [2 CT][T]
+  int64_t T, N, N64, D;
+  int RT, CT;
+  GateParams gp;
+  float exp_scale;        // -sharpness * log2(e)
+  float sharp;
+};
+
+__global__ __launch_bounds__(kGThreads) void tiled_bwd_gate_kernel(TBwdGateParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
+  int rt, ct;
+  if (!tile_of(p.RT, p.CT, rt, ct)) return;
+  const int64_t u0 = static_cast<int64_t>(ct) * kGRows, v0 = static_cast<int64_t>(rt) * kGRows;
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+  {
+    const Opnd A = make_opnd(p.write, p.D, u0, p.N, 1, wave, lane);
+    const Opnd B = make_opnd(p.draw, p.D, v0, p.T, 1, wave, lane);
+    gemm_loop(acc, A, B, 0, static_cast<int>(p.D / kGK), lds, wave, lane, NoHook{});
+  }
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  const int64_t nleft = p.N - (u0 + 128 * wa + 4 * h);
+  const float thr = p.gp.thr, cut = p.gp.cut, eps = p.gp.eps, maxi = p.gp.maxi;
+#pragma clang loop unroll(full)
+  for (int j = 0; j < 4; ++j) {
+    const int64_t t = v0 + 128 * wb + 32 * j + u;
+    const bool tok = t < p.T;
+    const int64_t tl = tok ? t : p.T - 1;
+    const float tau = p.tau[tl], dden = p.dden[tl];
+    float sdm = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t nb = u0 + 128 * wa + 32 * i + 4 * h;
+      u32x2_t sv[4], xv[4], xo[4];
+      float dmf[16];  // dm of element v (units 8 (v / 4) + v % 4 from nb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bool in = nb + 8 * q < p.N64;
+        sv[q] = in ? *reinterpret_cast<const u32x2_t*>(p.S + tl * p.N64 + nb + 8 * q) : u32x2_t{0u, 0u};
+        xv[q] = in ? *reinterpret_cast<const u32x2_t*>(p.XR + tl * p.N64 + nb + 8 * q) : u32x2_t{0u, 0u};
+      }
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const uint32_t dpq = pack_bf16(acc[i][j][v], acc[i][j][v + 1]);  // bf16 dot output
+        const uint32_t sp = sv[v >> 2][(v >> 1) & 1], xp = xv[v >> 2][(v >> 1) & 1];
+        float dxr2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float dp = e ? hi_f32(dpq) : lo_f32(dpq);
+          const float sc = e ? hi_f32(sp) : lo_f32(sp);
+          const float xr = e ? hi_f32(xp) : lo_f32(xp);
+          const float m = (sc - tau) - thr;
+          const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(m * p.exp_scale));
+          const float am = fmaxf(m - cut, 0.0f);
+          const float it = eps + fminf(am, maxi);
+          const float gb = round_bf16(act * it);
+          const float dgb = round_bf16(dp * xr);     // d(gate_bf): bf16 multiply transpose
+          float dx = round_bf16(dp * gb);            // d(xr)
+          const float dit = dgb * act + dden;
+          const float dam = am < maxi ? dit : 0.f;
+          float dm = (m - cut > 0.f ? dam : 0.f) + dgb * it * p.sharp * act * (1.0f - act);
+          const bool ok = 32 * i + 8 * ((v + e) >> 2) + ((v + e) & 3) < nleft;
+          dm = ok ? dm : 0.f;
+          dx = ok ? dx : 0.f;
+          sdm += dm;
+          dxr2[e] = dx;
+          dmf[v + e] = dm;
+        }
+        xo[v >> 2][(v >> 1) & 1] = pack_bf16(dxr2[0], dxr2[1]);
+      }
+      if (tok) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (nb + 8 * q < p.N64) {
+            *reinterpret_cast<u32x2_t*>(p.DXR + t * p.N64 + nb + 8 * q) = xo[q];
+            *reinterpret_cast<float4*>(p.DM + t * p.N64 + nb + 8 * q) =
+                float4{dmf[4 * q], dmf[4 * q + 1], dmf[4 * q + 2], dmf[4 * q + 3]};
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    sdm += __shfl_xor(sdm, 32);
+    if (h == 0 && tok) p.dm_part[static_cast<int64_t>(2 * ct + wa) * p.T + t] = sdm;
+  }
+}
+
+// tau chain per token (v41:461-464): dtau = -sum_n dm; tau = mean + off * std,
+// std = sqrt(E[s^2] - mean^2) + 1e-8.  Writes d tau_offset and the affine
+// coefficients of the score gradient, ds = dm + alpha + beta * s (+ unit term)
+__global__ __launch_bounds__(256) void bwd_token_kernel(const float* __restrict__ dm_part, int S2, int64_t T,
+                                                        int64_t N, const float* __restrict__ tau_off,
+                                                        const float* __restrict__ mean, const float* __restrict__ var,
+                                                        const float* __restrict__ sdev, float* __restrict__ dtau_off,
+                                                        float* __restrict__ alpha, float* __restrict__ beta) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float a = 0.f;
+  for (int s = lane; s < S2; s += 64) a += dm_part[static_cast<int64_t>(s) * T + t];
+  a = wave_sum(a);
+  if (lane == 0) {
+    const float fN = static_cast<float>(N);
+    const float dtau = -a;
+    dtau_off[t] = dtau * sdev[t];
+    const float dstd = dtau * tau_off[t];
+    const float dvar = dstd / (2.0f * sqrtf(var[t]));
+    const float dmean = dtau - 2.0f * mean[t] * dvar;
+    alpha[t] = dmean / fN;
+    beta[t] = 2.0f * dvar / fN;
+  }
+}
+
+// per-unit mean score over the tokens and max gate (the score_lb / dead
+// penalty inputs, v41:445-447, 543-549): partials over 128-token slices
+__global__ __launch_bounds__(256) void bwd_unit_part_kernel(const uint16_t* __restrict__ S,
+                                                            const float* __restrict__ tau, int64_t T, int64_t N64,
+                                                            GateParams gp, float exp_scale, float* __restrict__ psum,
+                                                            float* __restrict__ pmax) {
+  __shared__ float rs[4][64], rm[4][64];
+  const int c = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 64 + c;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * 128;
+  const int64_t t1 = t0 + 128 < T ? t0 + 128 : T;
+  float sum = 0.f, gmax = 0.f;
+  for (int64_t t = t0 + grp; t < t1; t += 4) {
+    const float sc = bf16_to_f32(S[t * N64 + n]);
+    sum += sc;
+    const float tau_thr = tau[t] + gp.thr;
+    const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(sc, exp_scale, -tau_thr * exp_scale)));
+    const float it = gp.eps + __builtin_amdgcn_fmed3f(sc - (tau_thr + gp.cut), 0.0f, gp.maxi);
+    gmax = fmaxf(gmax, act * it);
+  }
+  rs[grp][c] = sum;
+  rm[grp][c] = gmax;
+  __syncthreads();
+  if (grp == 0) {
+    psum[blockIdx.y * N64 + n] = (rs[0][c] + rs[1][c]) + (rs[2][c] + rs[3][c]);
+    pmax[blockIdx.y * N64 + n] = fmaxf(fmaxf(rm[0][c], rm[1][c]), fmaxf(rm[2][c], rm[3][c]));
+  }
+}
+
+// pn[n] = mean_t s, dead[n] = max_t gate < dead_threshold (v41:548), and
+// per-block sums of pn, pn^2 over the units (v41:445-447)
+__global__ __launch_bounds__(256) void bwd_unit_reduce_kernel(const float* __restrict__ psum,
+                                                              const float* __restrict__ pmax, int TS, int64_t T,
+                                                              int64_t N, int64_t N64, float dead_thr,
+                                                              float* __restrict__ pn, float* __restrict__ dead,
+                                                              float* __restrict__ blk) {
+  __shared__ float red[4];
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  float sum = 0.f, gmax = 0.f;
+  if (n < N64) {
+    for (int s = 0; s < TS; ++s) {
+      sum += psum[static_cast<int64_t>(s) * N64 + n];
+      gmax = fmaxf(gmax, pmax[static_cast<int64_t>(s) * N64 + n]);
+    }
+  }
+  const bool ok = n < N;
+  const float m = ok ? sum / static_cast<float>(T) : 0.f;
+  if (n < N64) {
+    pn[n] = m;
+    dead[n] = ok && gmax < dead_thr ? 1.0f : 0.0f;
+  }
+  const float a = block_sum<256>(m, red);
+  const float b = block_sum<256>(m * m, red);
+  if (threadIdx.x == 0) {
+    blk[2 * blockIdx.x] = a;
+    blk[2 * blockIdx.x + 1] = b;
+  }
+}
+
+// score_lb = var(pn) / (mean(pn)^2 + var(pn) + 1e-2) (v41:477-483): its
+// derivative in pn[n] is c0 + c1 pn[n]; coef = {c0, c1} times d_lb
+__global__ __launch_bounds__(256) void bwd_unit_coef_kernel(const float* __restrict__ blk, int nblk, int64_t N,
+                                                            float d_lb, float* __restrict__ coef) {
+  __shared__ float red[4];
+  float a = 0.f, b = 0.f;
+  for (int i = threadIdx.x; i < nblk; i += 256) {
+    a += blk[2 * i];
+    b += blk[2 * i + 1];
+  }
+  a = block_sum<256>(a, red);
+  b = block_sum<256>(b, red);
+  if (threadIdx.x == 0) {
+    const float fN = static_cast<float>(N);
+    const float ms = a / fN;
+    const float vs = b / fN - ms * ms;
+    const float Z = ms * ms + vs + 1e-2f;
+    const float dvs = (ms * ms + 1e-2f) / (Z * Z);
+    const float dms = -2.0f * ms * vs / (Z * Z);
+    coef[0] = d_lb * (-dvs * 2.0f * ms / fN + dms / fN);
+    coef[1] = d_lb * dvs * 2.0f / fN;
+  }
+}
+
+// ds = bf16(dm + alpha_t + beta_t s + (c0 + c1 pn[n] - d_pen [pn < 0] dead[n]) / T),
+// zero past N; eight units per thread
+__global__ __launch_bounds__(256) void bwd_ds_kernel(const uint16_t* __restrict__ S, const float* __restrict__ DM,
+                                                     const float* __restrict__ alpha, const float* __restrict__ beta,
+                                                     const float* __restrict__ pn, const float* __restrict__ dead,
+                                                     const float* __restrict__ coef, float d_pen, int64_t T,
+                                                     int64_t N, int64_t N64, uint16_t* __restrict__ DS) {
+  const int64_t per_row = N64 / 8;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= T * per_row) return;
+  const int64_t t = idx / per_row;
+  const int64_t n0 = (idx % per_row) * 8;
+  const float a = alpha[t], b = beta[t], c0 = coef[0], c1 = coef[1];
+  const float invT = 1.0f / static_cast<float>(T);
+  const u32x4_t sq = *reinterpret_cast<const u32x4_t*>(S + t * N64 + n0);
+  const float4 d0 = *reinterpret_cast<const float4*>(DM + t * N64 + n0);
+  const float4 d1 = *reinterpret_cast<const float4*>(DM + t * N64 + n0 + 4);
+  const float dm[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 8; k += 2) {
+    float r[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int64_t n = n0 + k + e;
+      const float sc = e ? hi_f32(sq[k >> 1]) : lo_f32(sq[k >> 1]);
+      const float p = pn[n];
+      const float unit = (c0 + c1 * p + (p < 0.f ? -d_pen * dead[n] : 0.f)) * invT;
+      r[e] = n < N ? dm[k + e] + a + b * sc + unit : 0.f;
+    }
+    o[k >> 1] = pack_bf16(r[0], r[1]);
+  }
+  *reinterpret_cast<u32x4_t*>(DS + t * N64 + n0) = u32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+// out[i] = bf16(sum_s part[s][i]) widened to fp32: the reference's gradient
+// contractions are bf16 dots (their outputs bf16), split over K here
+__global__ __launch_bounds__(256) void bwd_sum_kernel(const float* __restrict__ part, int S, int64_t n,
+                                                      float* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  float a = 0.f;
+  for (int s = 0; s < S; ++s) a += part[static_cast<int64_t>(s) * n + i];
+  out[i] = round_bf16(a);
+}
+
+struct BGemm {
+  int64_t M, Nc, K;  // out [M, Nc] = A [M, K] . B [Nc, K]^T
+  int RT, DT, spc;
+};
+
+BGemm bgemm(int64_t M, int64_t Nc, int64_t K) {
+  BGemm g{M, Nc, K, static_cast<int>((M + kGRows - 1) / kGRows), static_cast<int>((Nc + kGRows - 1) / kGRows), 1};
+  const int64_t blocks = (K + kGK - 1) / kGK;
+  int64_t spc = (512 + static_cast<int64_t>(g.RT) * g.DT - 1) / (static_cast<int64_t>(g.RT) * g.DT);
+  spc = spc < 1 ? 1 : (spc > blocks ? blocks : spc);
+  g.spc = static_cast<int>(spc);
+  return g;
+}
+
+struct BLayout {
+  size_t S, XR, P, DXR, DS, DM, PT, DXRT, DST, ET, RT, HT, XT, DRAWT, DRAW;
+  size_t mom, tok_part, tok_sum, dm_part, tokv, psum, pmax, pn, dead, blk, coef, part, total;
+  int64_t T64, N64;
+  int CT, RTt, TS, nblk;
+  BGemm g_dw, g_dh, g_dx, g_de, g_dr;
+};
+
+BLayout blayout(const srw_desc_t& d) {
+  BLayout l{};
+  const int64_t T = d.T, N = d.n_units, D = d.d_model, dr = d.d_route;
+  l.T64 = (T + kNAlign - 1) / kNAlign * kNAlign;
+  l.N64 = (N + kNAlign - 1) / kNAlign * kNAlign;
+  l.CT = static_cast<int>((N + kGRows - 1) / kGRows);
+  l.RTt = static_cast<int>((T + kGRows - 1) / kGRows);
+  l.TS = static_cast<int>((T + 127) / 128);
+  l.nblk = static_cast<int>((l.N64 + 255) / 256);
+  l.g_dw = bgemm(N, D, T);
+  l.g_dh = bgemm(T, dr, N);
+  l.g_dx = bgemm(T, D, N);
+  l.g_de = bgemm(N, dr, T);
+  l.g_dr = bgemm(N, D, T);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += al256(static_cast<int64_t>(bytes));
+    return at;
+  };
+  const size_t tn = static_cast<size_t>(T) * l.N64 * 2, nt = static_cast<size_t>(l.N64) * l.T64 * 2;
+  l.S = take(tn);
+  l.XR = take(tn);
+  l.P = take(tn);
+  l.DXR = take(tn);
+  l.DS = take(tn);
+  l.DM = take(2 * tn);
+  l.PT = take(nt);
+  l.DXRT = take(nt);
+  l.DST = take(nt);
+  l.ET = take(static_cast<size_t>(dr) * l.N64 * 2);
+  l.RT = take(static_cast<size_t>(D) * l.N64 * 2);
+  l.HT = take(static_cast<size_t>(dr) * l.T64 * 2);
+  l.XT = take(static_cast<size_t>(D) * l.T64 * 2);
+  l.DRAWT = take(static_cast<size_t>(D) * l.T64 * 2);
+  l.DRAW = take(static_cast<size_t>(T) * D * 2);
+  l.mom = take(static_cast<size_t>(2 * l.CT) * T * 2 * 4);
+  l.tok_part = take(static_cast<size_t>(2 * l.CT) * T * 4 * 4);
+  l.tok_sum = take(static_cast<size_t>(T) * 4 * 4);
+  l.dm_part = take(static_cast<size_t>(2 * l.CT) * T * 4);
+  l.tokv = take(static_cast<size_t>(T) * 8 * 4);
+  l.psum = take(static_cast<size_t>(l.TS) * l.N64 * 4);
+  l.pmax = take(static_cast<size_t>(l.TS) * l.N64 * 4);
+  l.pn = take(static_cast<size_t>(l.N64) * 4);
+  l.dead = take(static_cast<size_t>(l.N64) * 4);
+  l.blk = take(static_cast<size_t>(l.nblk) * 2 * 4);
+  l.coef = take(4 * 4);
+  size_t part = 0;
+  for (const BGemm& g : {l.g_dw, l.g_dh, l.g_dx, l.g_de, l.g_dr}) {
+    const size_t b = static_cast<size_t>(g.spc) * g.M * g.Nc * 4;
+    part = b > part ? b : part;
+  }
+  l.part = take(part);
+  l.total = off;
+  return l;
+}
+
+// src [rows, cols] -> dst [cols, rows_pad] (zero rows past `rows`)
+hipError_t transpose(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t rows_pad, int64_t cols,
+                     hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(rows_pad / 64), static_cast<unsigned>((cols + 63) / 64));
+  hipLaunchKernelGGL(pack_wt_kernel, grid, dim3(256), 0, s, src, dst, rows, rows_pad, static_cast<int>(cols));
+  return hipGetLastError();
+}
+
+// out [M, Nc] (fp32, bf16-rounded) = A [M, K] . B [Nc, K]^T, both with row
+// stride ld (elements), zero past K
+hipError_t bwd_gemm(const BGemm& g, const uint16_t* A, const uint16_t* B, int64_t ld, float* part, float* out,
+                    hipStream_t s) {
+  TWriteParams wp{};
+  wp.P = A;
+  wp.wt = B;
+  wp.out_part = part;
+  wp.Tv = g.M;
+  wp.N = g.K;
+  wp.N64 = ld;
+  wp.D = g.Nc;
+  wp.cs = g.K;
+  wp.nc = 1;
+  wp.spc = g.spc;
+  wp.S = g.spc;
+  wp.RT = g.RT;
+  wp.DT = g.DT;
+  const unsigned grid = static_cast<unsigned>(8 * g.DT * ((static_cast<int64_t>(g.RT) * g.spc + 7) / 8));
+  hipLaunchKernelGGL(tiled_write_kernel, dim3(grid), dim3(kGThreads), kGemmLds, s, wp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t n = g.M * g.Nc;
+  hipLaunchKernelGGL(bwd_sum_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, part, g.spc, n,
+                     out);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool tiled_backward_supports(const srw_desc_t& d) {
+  if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41 || d.stats_mode != SRW_STATS_ONEPASS) return false;
+  if (d.n_routes != 1) return false;
+  if (d.d_model % kNAlign != 0 || d.d_route % kNAlign != 0) return false;
+  if (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
+  return d.scale != 0.0f;
+}
+
+size_t tiled_backward_workspace_bytes(const srw_desc_t& d) { return blayout(d).total; }
+
+hipError_t tiled_backward(const BackwardArgs& a) {
+  const srw_desc_t& d = a.d;
+  const BLayout l = blayout(d);
+  const int64_t T = d.T, N = d.n_units, D = d.d_model, dr = d.d_route, N64 = l.N64, T64 = l.T64;
+  auto b16 = [&](size_t off) { return reinterpret_cast<uint16_t*>(a.ws + off); };
+  auto f32 = [&](size_t off) { return reinterpret_cast<float*>(a.ws + off); };
+  uint16_t *S = b16(l.S), *XR = b16(l.XR), *P = b16(l.P), *DXR = b16(l.DXR), *DS = b16(l.DS);
+  uint16_t *PT = b16(l.PT), *DXRT = b16(l.DXRT), *DST = b16(l.DST), *ET = b16(l.ET), *RT = b16(l.RT);
+  uint16_t *HT = b16(l.HT), *XT = b16(l.XT), *DRAWT = b16(l.DRAWT), *DRAW = b16(l.DRAW);
+  float *DM = f32(l.DM), *mom = f32(l.mom), *tok_part = f32(l.tok_part), *tok_sum = f32(l.tok_sum);
+  float *dm_part = f32(l.dm_part), *tokv = f32(l.tokv), *psum = f32(l.psum), *pmax = f32(l.pmax);
+  float *pn = f32(l.pn), *dead = f32(l.dead), *blk = f32(l.blk), *coef = f32(l.coef), *part = f32(l.part);
+  float *mean = tokv, *var = tokv + T, *sdev = tokv + 2 * T, *tau = tokv + 3 * T, *dden = tokv + 4 * T;
+  float *alpha = tokv + 5 * T, *beta = tokv + 6 * T;
+  const auto* emb = static_cast<const uint16_t*>(a.in.emb);
+  const auto* read = static_cast<const uint16_t*>(a.in.read);
+  const auto* write = static_cast<const uint16_t*>(a.in.write);
+  const auto* x = static_cast<const uint16_t*>(a.in.x);
+  const auto* h = static_cast<const uint16_t*>(a.in.h);
+  const float exp_scale = -d.sharpness * 1.4426950408889634f;
+  hipStream_t st = a.stream;
+  hipError_t e;
+  for (const void* fn : {reinterpret_cast<const void*>(tiled_stats_kernel),
+                         reinterpret_cast<const void*>(tiled_gate_kernel<true>),
+                         reinterpret_cast<const void*>(tiled_bwd_gate_kernel),
+                         reinterpret_cast<const void*>(tiled_write_kernel)})
+    if ((e = set_lds(fn)) != hipSuccess) return e;
+#define SRW_TRY(expr) \
+  if ((e = (expr)) != hipSuccess) return e
+  // operands of the K = units / K = tokens contractions, unit- or token-contiguous
+  SRW_TRY(transpose(emb, ET, N, N64, dr, st));
+  SRW_TRY(transpose(read, RT, N, N64, D, st));
+  SRW_TRY(transpose(h, HT, T, T64, dr, st));
+  SRW_TRY(transpose(x, XT, T, T64, D, st));
+
+  // forward recompute: scores, moments, tau, x.r, gates, P, sum intensity
+  const unsigned grid_rc = static_cast<unsigned>(8 * l.RTt * ((l.CT + 7) / 8));
+  TStatsParams sp{};
+  sp.h = h;
+  sp.emb = emb;
+  sp.S = S;
+  sp.mom = mom;
+  sp.Tv = T;
+  sp.N = N;
+  sp.N64 = N64;
+  sp.dr = dr;
+  sp.RT = l.RTt;
+  sp.CT = l.CT;
+  hipLaunchKernelGGL(tiled_stats_kernel, dim3(grid_rc), dim3(kGThreads), kGemmLds, st, sp);
+  SRW_TRY(hipGetLastError());
+  hipLaunchKernelGGL(bwd_token_stats_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, st, mom,
+                     2 * l.CT, T, N, a.in.tau_offset, mean, var, sdev, tau);
+  SRW_TRY(hipGetLastError());
+  TGateParams gp{};
+  gp.x = x;
+  gp.read = read;
+  gp.tau = tau;
+  gp.P = S;
+  gp.P_out = P;
+  gp.XR_out = XR;
+  gp.tok_part = tok_part;
+  gp.Tv = T;
+  gp.N = N;
+  gp.N64 = N64;
+  gp.D = D;
+  gp.routes = 1;
+  gp.RT = l.RTt;
+  gp.CT = l.CT;
+  gp.gp = a.gp;
+  gp.exp_scale = exp_scale;
+  hipLaunchKernelGGL(tiled_gate_kernel<true>, dim3(grid_rc), dim3(kGThreads), kGemmLds, st, gp);
+  SRW_TRY(hipGetLastError());
+  hipLaunchKernelGGL(tiled_tok_sum_kernel, dim3(static_cast<unsigned>((T + 63) / 64)), dim3(256), 0, st, tok_part,
+                     tok_sum, T, 2 * l.CT);
+  SRW_TRY(hipGetLastError());
+  // per-unit terms of score_lb and the dead penalty
+  hipLaunchKernelGGL(bwd_unit_part_kernel, dim3(static_cast<unsigned>(N64 / 64), static_cast<unsigned>(l.TS)),
+                     dim3(256), 0, st, S, tau, T, N64, a.gp, exp_scale, psum, pmax);
+  SRW_TRY(hipGetLastError());
+  hipLaunchKernelGGL(bwd_unit_reduce_kernel, dim3(static_cast<unsigned>(l.nblk)), dim3(256), 0, st, psum, pmax, l.TS,
+                     T, N, N64, d.dead_threshold, pn, dead, blk);
+  SRW_TRY(hipGetLastError());
+  hipLaunchKernelGGL(bwd_unit_coef_kernel, dim3(1), dim3(256), 0, st, blk, l.nblk, N, a.cot.d_score_lb, coef);
+  SRW_TRY(hipGetLastError());
+
+  // cotangent of the chunk dots, the den term, dP and the gate derivative
+  hipLaunchKernelGGL(bwd_prep_kernel, dim3(static_cast<unsigned>(T)), dim3(256), 0, st, a.cot.d_out,
+                     static_cast<const uint16_t*>(a.cot.out), tok_sum, d.scale, static_cast<int>(D), DRAW, dden);
+  SRW_TRY(hipGetLastError());
+  TBwdGateParams bp{};
+  bp.write = write;
+  bp.draw = DRAW;
+  bp.S = S;
+  bp.XR = XR;
+  bp.tau = tau;
+  bp.dden = dden;
+  bp.DXR = DXR;
+  bp.DM = DM;
+  bp.dm_part = dm_part;
+  bp.T = T;
+  bp.N = N;
+  bp.N64 = N64;
+  bp.D = D;
+  bp.RT = l.RTt;
+  bp.CT = l.CT;
+  bp.gp = a.gp;
+  bp.exp_scale = exp_scale;
+  bp.sharp = d.sharpness;
+  dominant_kernel_begin(st);
+  hipLaunchKernelGGL(tiled_bwd_gate_kernel, dim3(grid_rc), dim3(kGThreads), kGemmLds, st, bp);
+  dominant_kernel_end(st);
+  SRW_TRY(hipGetLastError());
+  hipLaunchKernelGGL(bwd_token_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, st, dm_part, 2 * l.CT,
+                     T, N, a.in.tau_offset, mean, var, sdev, a.g.dtau_offset, alpha, beta);
+  SRW_TRY(hipGetLastError());
+  hipLaunchKernelGGL(bwd_ds_kernel, dim3(static_cast<unsigned>((T * (N64 / 8) + 255) / 256)), dim3(256), 0, st, S, DM,
+                     alpha, beta, pn, dead, coef, a.cot.d_dead_penalty, T, N, N64, DS);
+  SRW_TRY(hipGetLastError());
+
+  // token-contiguous copies for the K = tokens contractions
+  SRW_TRY(transpose(P, PT, T, T64, N64, st));
+  SRW_TRY(transpose(DXR, DXRT, T, T64, N64, st));
+  SRW_TRY(transpose(DS, DST, T, T64, N64, st));
+  SRW_TRY(transpose(DRAW, DRAWT, T, T64, D, st));
+  // the six contractions (dP above): bf16 dots, fp32 accumulation
+  SRW_TRY(bwd_gemm(l.g_dw, PT, DRAWT, T64, part, a.g.dwrite, st));
+  SRW_TRY(bwd_gemm(l.g_dr, DXRT, XT, T64, part, a.g.dread, st));
+  SRW_TRY(bwd_gemm(l.g_de, DST, HT, T64, part, a.g.demb, st));
+  SRW_TRY(bwd_gemm(l.g_dx, DXR, RT, N64, part, a.g.dx, st));
+  SRW_TRY(bwd_gemm(l.g_dh, DS, ET, N64, part, a.g.dh, st));
+#undef SRW_TRY
+  return hipSuccess;
 }
 
 }  // namespace srw

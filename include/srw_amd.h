@@ -26,6 +26,12 @@
  *   gate = SRW_GATE_GELU_V401
  *       -> fused_gate_srw / _srw_inference of
  *          models/legacy/dawn_spatial_v401_exp.py:229-355, 1443-1463
+ *   srw_backward, n_routes = 1, SRW_STATS_ONEPASS, dtype = SRW_BF16
+ *       -> the VJP of fused_gate_srw that jax.value_and_grad(loss_fn) takes in
+ *          train_step (scripts/train_jax.py:548-726, through the sharded_fns
+ *          tuple of :2324-2333): cotangents of out, score_lb and
+ *          dead_penalty (the outputs the loss uses, :586-603) in, gradients of
+ *          x, h, emb, tau_offset, read and write out
  *   the closure constants of the factories (v41:297-301, 352-383) travel in
  *   srw_desc_t; srw_desc_init() fills the reference defaults.
  *
@@ -51,7 +57,7 @@
 extern "C" {
 #endif
 
-#define SRW_AMD_ABI_VERSION 2
+#define SRW_AMD_ABI_VERSION 3
 
 typedef enum srw_status {
   SRW_OK = 0,
@@ -177,6 +183,28 @@ typedef struct srw_outputs {
                               call that sets it runs the generic kernels. */
 } srw_outputs_t;
 
+/* Cotangents for srw_backward: of the three outputs of fused_gate_srw that
+ * enter the reference's training loss (scripts/train_jax.py:586-603). */
+typedef struct srw_cotangents {
+  const float* d_out;      /* [T, n_routes, D] cotangent of out (required) */
+  const void* out;         /* [T, n_routes, D] out of the forward call on the same
+                              inputs (desc->dtype; required: the den term) */
+  float d_score_lb;        /* cotangent of score_lb (v41:477-483) */
+  float d_dead_penalty;    /* cotangent of dead_penalty (v41:543-552) */
+} srw_cotangents_t;
+
+/* Gradients written by srw_backward, float32, all required.  When the
+ * forward's h was x itself (d_route == d_model), the gradient of x is
+ * dx + dh (the two paths are returned separately). */
+typedef struct srw_grads {
+  float* dx;               /* [T, D] */
+  float* dh;               /* [T, n_routes, d_route] */
+  float* demb;             /* [N, d_route] */
+  float* dtau_offset;      /* [T, n_routes] */
+  float* dread;            /* [N, D] */
+  float* dwrite;           /* [N, D] */
+} srw_grads_t;
+
 /* ABI version of the loaded library (SRW_AMD_ABI_VERSION). */
 int32_t srw_abi_version(void);
 
@@ -198,6 +226,22 @@ srw_status_t srw_workspace_size(const srw_desc_t* desc, size_t* bytes);
 srw_status_t srw_forward(const srw_desc_t* desc, const srw_tensors_t* in,
                          const srw_outputs_t* outs, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* Validate *desc for srw_backward and report its workspace (device bytes). */
+srw_status_t srw_backward_workspace_size(const srw_desc_t* desc, size_t* bytes);
+
+/* Enqueue the reverse-mode derivative (VJP) of one srw_forward call on
+ * `stream`: recomputes the forward's scores, gates and products from the
+ * inputs (as the reference's jax.checkpoint-ed scans do, v41:434, 489) and
+ * writes the gradients of <d_out, out> + d_score_lb * score_lb +
+ * d_dead_penalty * dead_penalty.  bf16, v4.1 gate, one route, one-pass
+ * statistics, d_model and d_route multiples of 64; anything else returns
+ * SRW_EUNSUPPORTED.  The cotangents of bf16 values are rounded to bf16 where
+ * the reference's bf16 casts, dots and products transpose (the gradients are
+ * bf16 dot outputs widened to float32). */
+srw_status_t srw_backward(const srw_desc_t* desc, const srw_tensors_t* in,
+                          const srw_cotangents_t* cot, const srw_grads_t* grads,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Name of the kernel family the last srw_forward on this thread used
  * ("generic", "mfma_bf16", ...), for tests and benchmarks. */

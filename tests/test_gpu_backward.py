@@ -1,0 +1,91 @@
+"""GPU parity of srw_backward (the VJP of fused_gate_srw, through the C ABI)
+against the oracle's hand-written VJP (oracle/srw_vjp.py) with the
+reference's bf16 rounding points, on the same seeded inputs.
+
+Bar: every gradient within 2e-2 relative (Frobenius) of the oracle's, and
+d tau_offset within 2e-2 relative per token row set.  The two sides differ
+by fp32 accumulation order inside the bf16 dots (a score or a product can
+round to the neighbouring bf16 value) and by where a cotangent is rounded
+when two paths meet (documented in the oracle).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import srw_vjp
+from tests.parity import rel_fro
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+
+CASES = [
+    # T, D, dr, N, h_is_x, seed, tau
+    (256, 384, 384, 2600, True, 1, -0.5),     # Know-pool form, ragged N
+    (200, 384, 128, 1580, False, 2, -0.5),    # router h, ragged T and N
+    (130, 128, 64, 1000, False, 3, 0.5),      # fewer passing units
+    (64, 1024, 1024, 700, True, 4, -0.5),     # configs[4] widths
+    (40, 128, 128, 300, True, 5, 2.5),        # dead units (score_lb / dead penalty terms)
+]
+
+
+def _inputs(pkg, T, D, dr, N, hx, seed, tau):
+    shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=1, h_is_x=hx)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=seed)
+    g = torch.Generator().manual_seed(seed + 7)
+    inp["tau_offset"] = tau + 0.2 * torch.randn(T, 1, generator=g)
+    return inp
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "T{}D{}dr{}N{}{}".format(
+    c[0], c[1], c[2], c[3], "x" if c[4] else ""))
+def test_backward_matches_oracle_vjp(pkg, dev, case):
+    T, D, dr, N, hx, seed, tau = case
+    print(f"[gpu] backward {case}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, hx, seed, tau)
+    xb = inp["x"].to(BF)
+    hb = xb if hx else inp["h"][:, 0].to(BF)
+    eb, rb, wb = (inp[k].to(BF) for k in ("emb", "read", "write"))
+    g = torch.Generator().manual_seed(seed + 99)
+    d_out = torch.randn(T, D, generator=g)
+    d_lb, d_pen = 0.37, -0.81
+    ref = srw_vjp.fused_gate_srw_vjp(xb.float(), hb.float(), eb.float(), inp["tau_offset"], rb.float(),
+                                     wb.float(), d_out, d_lb, d_pen, max_chunk_size=max(N, 1))
+    x = xb.to(dev)
+    h = x if hx else hb[:, None].contiguous().to(dev)
+    args = (x, h, eb.to(dev), inp["tau_offset"].to(dev), rb.to(dev), wb.to(dev))
+    fwd = pkg.srw_forward(*args, want_mask=False)
+    got = pkg.srw_backward(*args, fwd["out"], d_out[:, None].to(dev), d_lb, d_pen)
+    torch.cuda.synchronize()
+    assert got["path"] == "tiled_bwd_bf16"
+    pairs = dict(dx=got["dx"], dh=got["dh"][:, 0], demb=got["demb"], dtau_offset=got["dtau_offset"],
+                 dread=got["dread"], dwrite=got["dwrite"])
+    for k, v in pairs.items():
+        err = rel_fro(v.cpu(), ref[k].float())
+        print(f"  {k}: rel err {err:.3e}", flush=True)
+        assert torch.isfinite(v).all(), k
+        assert err <= 2e-2, (k, err)
+
+
+def test_backward_linear_in_cotangents(pkg, dev):
+    """The VJP is linear in (d_out, d_lb, d_pen): grad(a + b) = grad(a) + grad(b)
+    up to the bf16 rounding of each contraction."""
+    T, D, dr, N = 128, 384, 384, 1500
+    print(f"[gpu] backward linearity T{T} N{N}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, True, 11, -0.5)
+    x = inp["x"].to(BF).to(dev)
+    args = (x, x, inp["emb"].to(BF).to(dev), inp["tau_offset"].to(dev), inp["read"].to(BF).to(dev),
+            inp["write"].to(BF).to(dev))
+    out = pkg.srw_forward(*args, want_mask=False)["out"]
+    g = torch.Generator().manual_seed(5)
+    da = torch.randn(T, 1, D, generator=g).to(dev)
+    db = torch.randn(T, 1, D, generator=g).to(dev)
+    ga = pkg.srw_backward(*args, out, da, 0.5, 0.0)
+    gb = pkg.srw_backward(*args, out, db, 0.0, -1.0)
+    gs = pkg.srw_backward(*args, out, da + db, 0.5, -1.0)
+    torch.cuda.synchronize()
+    for k in ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite"):
+        err = rel_fro((ga[k] + gb[k]).cpu(), gs[k].cpu())
+        assert err <= 2e-2, (k, err)
