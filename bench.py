@@ -68,18 +68,28 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float) -> dict:
-    """The oracle's fused_gate_srw (bf16 emulation) on a token sample of the
-    same pool, timed on the host cores (test infrastructure as the timed CPU
-    restatement; never part of the GPU path)."""
+def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: bool = False) -> dict:
+    """The oracle's fused_gate_srw (bf16 emulation) -- or, with ``backward``,
+    its hand-written VJP -- on a token sample of the same pool, timed on the
+    host cores (test infrastructure as the timed CPU restatement; never part
+    of the GPU path)."""
     import torch
-    from oracle import srw_ref
+    from oracle import srw_ref, srw_vjp
 
     threads = torch.get_num_threads()
     T_s = min(shape.T, 1024)
     x = inp["x"][:T_s]
     tau = torch.full((T_s, shape.routes), tau_value)
-    if shape.routes == 1:
+    what = "fused_gate_srw"
+    if backward:
+        what = "fused_gate_srw VJP (oracle/srw_vjp.py)"
+        bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+        h = x if shape.h_is_x else inp["h"][:T_s, 0]
+        d_out = torch.randn(T_s, shape.D, generator=torch.Generator().manual_seed(1))
+        fn = lambda: srw_vjp.fused_gate_srw_vjp(  # noqa: E731
+            bf(x), bf(h), bf(inp["emb"]), tau, bf(inp["read"]), bf(inp["write"]), d_out, 1e-2, 1e-2,
+            max_chunk_size=chunk)
+    elif shape.routes == 1:
         h = x if shape.h_is_x else inp["h"][:T_s, 0]
         fn = lambda: srw_ref.fused_gate_srw(  # noqa: E731
             x[None], h[None], inp["emb"], tau[None], inp["read"], inp["write"],
@@ -100,7 +110,7 @@ def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float) -> dict:
     log(f"cpu baseline: T_sample={T_s} runs={len(times)} median={med * 1e3:.1f} ms "
         f"threads={threads}")
     return {"value": T_s / med, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle fused_gate_srw bf16 emulation, first {T_s} of the "
+            "sample": (f"oracle {what} bf16 emulation, first {T_s} of the "
                        f"{shape.T} tokens, full pool N={shape.N}, median of {len(times)} "
                        f"runs; {cpu_model()}")}
 
@@ -121,6 +131,9 @@ def main() -> int:
     ap.add_argument("--tiled", action="store_true",
                     help="run the tiled-GEMM kernels (P materialised) where a fused kernel "
                          "exists too (they serve d_model > 384 anyway)")
+    ap.add_argument("--backward", action="store_true",
+                    help="time the backward (srw_backward: the VJP of fused_gate_srw for the "
+                         "training step) instead of the forward; one route, bf16")
     ap.add_argument("--diag", action="store_true",
                     help="also compute the training diagnostics (SRW_FLAG_DIAG: the 22-tuple "
                          "path of the drop-in fused_gate_srw)")
@@ -135,6 +148,10 @@ def main() -> int:
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
+    if args.backward and (args.graph or args.diag or args.stats != "onepass"):
+        print("bench.py: --backward times srw_backward (one-pass statistics, no graph, no "
+              "diagnostics)", file=sys.stderr)
+        return 2
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the SRW layer on one GPU only; "
               "--gpus above 1 is not supported (token-sharding design is documented, "
@@ -188,6 +205,23 @@ def main() -> int:
     log(f"warm-up done, path={plan.path}, mean active/token="
         f"{plan.n_active.float().mean().item():.1f}")
 
+    def step():
+        plan.launch(stream, pool_cached=args.pool_cached)
+
+    if args.backward:
+        # cotangents of out (synthetic, seeded) and of score_lb / dead_penalty
+        gen = torch.Generator().manual_seed(args.seed + 1)
+        d_out = torch.randn(shape.T, 1, shape.D, generator=gen).to(dev)
+        bplan = pkg.SrwBackwardPlan(x, h, plan.inputs[2], plan.inputs[3], plan.inputs[4],
+                                    plan.inputs[5], plan.out, d_out, 1e-2, 1e-2)
+        for _ in range(args.warmup + 1):
+            bplan.launch(stream)
+        torch.cuda.synchronize()
+        log(f"backward warm-up done, path={bplan.path}, workspace {bplan.ws_bytes / 2**30:.2f} GiB")
+
+        def step():  # noqa: F811
+            bplan.launch(stream)
+
     graph = None
     if args.graph:
         # a side stream for capture, as torch requires; replays run on `stream`
@@ -223,7 +257,7 @@ def main() -> int:
             graph.replay()
             continue
         C.set_kernel_events(ev_k[i][0].cuda_event, ev_k[i][1].cuda_event)
-        plan.launch(stream, pool_cached=args.pool_cached)
+        step()
     t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
@@ -234,7 +268,7 @@ def main() -> int:
         # time it eagerly once more
         for a, b in ev_k:
             C.set_kernel_events(a.cuda_event, b.cuda_event)
-            plan.launch(stream, pool_cached=args.pool_cached)
+            step()
         torch.cuda.synchronize()
     kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev_k)
     log(f"timed {K} steps: {step_ms:.4f} ms/step (events), wall {wall / K * 1e3:.4f} ms/step, "
@@ -242,24 +276,29 @@ def main() -> int:
 
     T, D, dr, N, R = shape.T, shape.D, shape.dr, shape.N, shape.routes
     flops = 2.0 * T * N * (R * dr + D + R * D)          # score + read (once) + write
-    if plan.path == "tiled_bf16":
+    path = bplan.path if args.backward else plan.path
+    if args.backward:
+        # recompute (score + read), dP, dW, dR, dx (d_model) and dE, dh (d_route)
+        flops = 2.0 * T * N * (3 * dr + 5 * D)
+        kflops = 2.0 * T * N * D        # the dominant kernel: dP = draw . W^T with the gate derivative
+    elif plan.path == "tiled_bf16":
         # the dominant kernel of the tiled family is the gate GEMM pair (score
         # + read); the write GEMM is a kernel of its own
         kflops = 2.0 * T * N * (R * dr + D)
     else:
         kflops = flops
     achieved = kflops / (kern_ms * 1e-3) / 1e12
-    traffic = MEASURED_TRAFFIC.get((args.workload, args.stats, plan.path))
+    traffic = MEASURED_TRAFFIC.get((args.workload, args.stats, path))
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                "traffic": traffic, "kernel": plan.path,
+                "traffic": traffic, "kernel": path,
                 "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops,
                 "step_tflops": round(flops / (step_ms * 1e-3) / 1e12, 2)}
 
     cpu = None
     if args.cpu_seconds > 0:
         torch.set_num_threads(min(os.cpu_count() or 1, 16))
-        cpu = cpu_baseline(pkg, shape, inp, tau_value, max_chunk, args.cpu_seconds)
+        cpu = cpu_baseline(pkg, shape, inp, tau_value, max_chunk, args.cpu_seconds, args.backward)
 
     value = T / (step_ms * 1e-3)
     line = {
@@ -271,7 +310,7 @@ def main() -> int:
         "config": {"workload": args.workload, "note": note, "T": T, "d_model": D,
                    "d_route": dr, "n_units": N, "routes": R, "chunk": cs,
                    "stats": args.stats, "diag": args.diag, "pool_cached": args.pool_cached,
-                   "tiled": args.tiled,
+                   "tiled": args.tiled, "pass": "backward" if args.backward else "forward",
                    "graph": args.graph,
                    "tau_offset": round(tau_value, 4),
                    "parallelism": "single GPU"},

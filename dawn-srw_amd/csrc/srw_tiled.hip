@@ -857,42 +857,58 @@ __global__ __launch_bounds__(kGThreads) void tiled_bwd_gate_kernel(TBwdGateParam
   typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
   const int64_t nleft = p.N - (u0 + 128 * wa + 4 * h);
   const float thr = p.gp.thr, cut = p.gp.cut, eps = p.gp.eps, maxi = p.gp.maxi;
+  // 16 groups (token block j, unit block i); the scores and x.r of group g + 1
+  // are loaded while group g is computed (one wave per SIMD: nothing else
+  // would hide their latency)
+  int64_t tl[4];
+  float tau[4], dden[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t t = v0 + 128 * wb + 32 * j + u;
+    tl[j] = t < p.T ? t : p.T - 1;
+    tau[j] = p.tau[tl[j]];
+    dden[j] = p.dden[tl[j]];
+  }
+  auto load = [&](int j, int i, u32x2_t (&sv)[4], u32x2_t (&xv)[4]) {
+    const int64_t nb = u0 + 128 * wa + 32 * i + 4 * h;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool in = nb + 8 * q < p.N64;
+      sv[q] = in ? *reinterpret_cast<const u32x2_t*>(p.S + tl[j] * p.N64 + nb + 8 * q) : u32x2_t{0u, 0u};
+      xv[q] = in ? *reinterpret_cast<const u32x2_t*>(p.XR + tl[j] * p.N64 + nb + 8 * q) : u32x2_t{0u, 0u};
+    }
+  };
+  u32x2_t svc[4], xvc[4], svn[4], xvn[4];
+  load(0, 0, svc, xvc);
 #pragma clang loop unroll(full)
   for (int j = 0; j < 4; ++j) {
     const int64_t t = v0 + 128 * wb + 32 * j + u;
     const bool tok = t < p.T;
-    const int64_t tl = tok ? t : p.T - 1;
-    const float tau = p.tau[tl], dden = p.dden[tl];
     float sdm = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      if (4 * j + i < 15) load((4 * j + i + 1) >> 2, (i + 1) & 3, svn, xvn);
       const int64_t nb = u0 + 128 * wa + 32 * i + 4 * h;
-      u32x2_t sv[4], xv[4], xo[4];
+      u32x2_t xo[4];
       float dmf[16];  // dm of element v (units 8 (v / 4) + v % 4 from nb)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const bool in = nb + 8 * q < p.N64;
-        sv[q] = in ? *reinterpret_cast<const u32x2_t*>(p.S + tl * p.N64 + nb + 8 * q) : u32x2_t{0u, 0u};
-        xv[q] = in ? *reinterpret_cast<const u32x2_t*>(p.XR + tl * p.N64 + nb + 8 * q) : u32x2_t{0u, 0u};
-      }
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
         const uint32_t dpq = pack_bf16(acc[i][j][v], acc[i][j][v + 1]);  // bf16 dot output
-        const uint32_t sp = sv[v >> 2][(v >> 1) & 1], xp = xv[v >> 2][(v >> 1) & 1];
+        const uint32_t sp = svc[v >> 2][(v >> 1) & 1], xp = xvc[v >> 2][(v >> 1) & 1];
         float dxr2[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const float dp = e ? hi_f32(dpq) : lo_f32(dpq);
           const float sc = e ? hi_f32(sp) : lo_f32(sp);
           const float xr = e ? hi_f32(xp) : lo_f32(xp);
-          const float m = (sc - tau) - thr;
+          const float m = (sc - tau[j]) - thr;
           const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(m * p.exp_scale));
           const float am = fmaxf(m - cut, 0.0f);
           const float it = eps + fminf(am, maxi);
           const float gb = round_bf16(act * it);
           const float dgb = round_bf16(dp * xr);     // d(gate_bf): bf16 multiply transpose
           float dx = round_bf16(dp * gb);            // d(xr)
-          const float dit = dgb * act + dden;
+          const float dit = dgb * act + dden[j];
           const float dam = am < maxi ? dit : 0.f;
           float dm = (m - cut > 0.f ? dam : 0.f) + dgb * it * p.sharp * act * (1.0f - act);
           const bool ok = 32 * i + 8 * ((v + e) >> 2) + ((v + e) & 3) < nleft;
@@ -913,6 +929,11 @@ __global__ __launch_bounds__(kGThreads) void tiled_bwd_gate_kernel(TBwdGateParam
                 float4{dmf[4 * q], dmf[4 * q + 1], dmf[4 * q + 2], dmf[4 * q + 3]};
           }
         }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        svc[q] = svn[q];
+        xvc[q] = xvn[q];
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1037,17 +1058,19 @@ __global__ __launch_bounds__(256) void bwd_ds_kernel(const uint16_t* __restrict_
                                                      const float* __restrict__ pn, const float* __restrict__ dead,
                                                      const float* __restrict__ coef, float d_pen, int64_t T,
                                                      int64_t N, int64_t N64, uint16_t* __restrict__ DS) {
-  const int64_t per_row = N64 / 8;
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (idx >= T * per_row) return;
-  const int64_t t = idx / per_row;
-  const int64_t n0 = (idx % per_row) * 8;
+  const int64_t t = blockIdx.x;  // one token per grid column, 2048 units per workgroup
+  const int64_t n0 = (static_cast<int64_t>(blockIdx.y) * 256 + threadIdx.x) * 8;
+  if (n0 >= N64) return;
   const float a = alpha[t], b = beta[t], c0 = coef[0], c1 = coef[1];
   const float invT = 1.0f / static_cast<float>(T);
   const u32x4_t sq = *reinterpret_cast<const u32x4_t*>(S + t * N64 + n0);
   const float4 d0 = *reinterpret_cast<const float4*>(DM + t * N64 + n0);
   const float4 d1 = *reinterpret_cast<const float4*>(DM + t * N64 + n0 + 4);
+  const float4 p0 = *reinterpret_cast<const float4*>(pn + n0), p1 = *reinterpret_cast<const float4*>(pn + n0 + 4);
+  const float4 q0 = *reinterpret_cast<const float4*>(dead + n0), q1 = *reinterpret_cast<const float4*>(dead + n0 + 4);
   const float dm[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+  const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+  const float dv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
   uint32_t o[4];
 #pragma unroll
   for (int k = 0; k < 8; k += 2) {
@@ -1056,8 +1079,8 @@ __global__ __launch_bounds__(256) void bwd_ds_kernel(const uint16_t* __restrict_
     for (int e = 0; e < 2; ++e) {
       const int64_t n = n0 + k + e;
       const float sc = e ? hi_f32(sq[k >> 1]) : lo_f32(sq[k >> 1]);
-      const float p = pn[n];
-      const float unit = (c0 + c1 * p + (p < 0.f ? -d_pen * dead[n] : 0.f)) * invT;
+      const float p = pv[k + e];
+      const float unit = (c0 + c1 * p + (p < 0.f ? -d_pen * dv[k + e] : 0.f)) * invT;
       r[e] = n < N ? dm[k + e] + a + b * sc + unit : 0.f;
     }
     o[k >> 1] = pack_bf16(r[0], r[1]);
@@ -1084,7 +1107,9 @@ struct BGemm {
 BGemm bgemm(int64_t M, int64_t Nc, int64_t K) {
   BGemm g{M, Nc, K, static_cast<int>((M + kGRows - 1) / kGRows), static_cast<int>((Nc + kGRows - 1) / kGRows), 1};
   const int64_t blocks = (K + kGK - 1) / kGK;
-  int64_t spc = (512 + static_cast<int64_t>(g.RT) * g.DT - 1) / (static_cast<int64_t>(g.RT) * g.DT);
+  // one wave of workgroups over the 256 CUs (fewer splits: less fp32 partial traffic;
+  // measured 131 us per Know-pool gradient GEMM against 144 with two waves)
+  int64_t spc = (256 + static_cast<int64_t>(g.RT) * g.DT - 1) / (static_cast<int64_t>(g.RT) * g.DT);
   spc = spc < 1 ? 1 : (spc > blocks ? blocks : spc);
   g.spc = static_cast<int>(spc);
   return g;
@@ -1155,11 +1180,43 @@ BLayout blayout(const srw_desc_t& d) {
   return l;
 }
 
+// bf16 src [rows, cols] -> dst [cols, rows_pad] (zero rows past `rows`), 64 x
+// 64 tiles, 16-byte loads along src rows and 16-byte stores along dst rows
+// (cols a multiple of 8)
+__global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __restrict__ src,
+                                                          uint16_t* __restrict__ dst, int64_t rows,
+                                                          int64_t rows_pad, int64_t cols) {
+  __shared__ uint16_t tile[64][72];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64, c0 = static_cast<int64_t>(blockIdx.y) * 64;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int idx = threadIdx.x + 256 * k;  // 512 pieces: 64 rows x 8
+    const int r = idx >> 3, q = idx & 7;
+    const int64_t row = r0 + r, col = c0 + 8 * q;
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (row < rows && col < cols) v = *reinterpret_cast<const u32x4_t*>(src + row * cols + col);
+    *reinterpret_cast<u32x4_t*>(&tile[r][8 * q]) = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int idx = threadIdx.x + 256 * k;  // 512 pieces: 64 dst rows x 8
+    const int c = idx >> 3, q = idx & 7;
+    const int64_t col = c0 + c, row = r0 + 8 * q;
+    if (col >= cols || row >= rows_pad) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = static_cast<uint32_t>(tile[8 * q + 2 * e][c]) | (static_cast<uint32_t>(tile[8 * q + 2 * e + 1][c]) << 16);
+    *reinterpret_cast<u32x4_t*>(dst + col * rows_pad + row) = u32x4_t{w[0], w[1], w[2], w[3]};
+  }
+}
+
 // src [rows, cols] -> dst [cols, rows_pad] (zero rows past `rows`)
 hipError_t transpose(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t rows_pad, int64_t cols,
                      hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(rows_pad / 64), static_cast<unsigned>((cols + 63) / 64));
-  hipLaunchKernelGGL(pack_wt_kernel, grid, dim3(256), 0, s, src, dst, rows, rows_pad, static_cast<int>(cols));
+  hipLaunchKernelGGL(transpose16_kernel, grid, dim3(256), 0, s, src, dst, rows, rows_pad, cols);
   return hipGetLastError();
 }
 
@@ -1318,7 +1375,8 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   hipLaunchKernelGGL(bwd_token_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, st, dm_part, 2 * l.CT,
                      T, N, a.in.tau_offset, mean, var, sdev, a.g.dtau_offset, alpha, beta);
   SRW_TRY(hipGetLastError());
-  hipLaunchKernelGGL(bwd_ds_kernel, dim3(static_cast<unsigned>((T * (N64 / 8) + 255) / 256)), dim3(256), 0, st, S, DM,
+  hipLaunchKernelGGL(bwd_ds_kernel, dim3(static_cast<unsigned>(T), static_cast<unsigned>((N64 / 8 + 255) / 256)),
+                     dim3(256), 0, st, S, DM,
                      alpha, beta, pn, dead, coef, a.cot.d_dead_penalty, T, N, N64, DS);
   SRW_TRY(hipGetLastError());
 

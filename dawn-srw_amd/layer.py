@@ -208,6 +208,81 @@ def srw_forward(x, h, emb, tau_offset, read, write, *, gate: str = "v41",
     return plan.results()
 
 
+class SrwBackwardPlan:
+    """One bound ``srw_backward`` call: inputs checked, gradients and the
+    workspace allocated and the C structs built once, so that ``launch()``
+    is a single C call.  Arguments as :func:`srw_backward`; the tensors are
+    held by reference (overwrite them in place to feed new data)."""
+
+    def __init__(self, x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: float = 0.0,
+                 d_dead_penalty: float = 0.0, *, consts: GateConfig = GateConfig(),
+                 scale: float = 1.0):
+        if x.dim() != 2:
+            raise ValueError("x must be [T, D]")
+        T, D = x.shape
+        dev = x.device
+        if dev.type != "cuda":
+            raise ValueError("srw_backward runs on a HIP device; got " + str(dev))
+        if x.dtype != torch.bfloat16:
+            raise TypeError("srw_backward takes bfloat16 inputs")
+        h_is_x = h is x
+        if h_is_x:
+            dr = D
+        else:
+            if h.dim() != 3 or h.shape[1] != 1:
+                raise ValueError("h must be [T, 1, d_route] (one route)")
+            dr = h.shape[2]
+            _check_dev("h", h, dev, x.dtype, (T, 1, dr))
+        N = emb.shape[0]
+        _check_dev("x", x, dev, x.dtype)
+        _check_dev("emb", emb, dev, x.dtype, (N, dr))
+        _check_dev("tau_offset", tau_offset, dev, torch.float32, (T, 1))
+        _check_dev("read", read, dev, x.dtype, (N, D))
+        _check_dev("write", write, dev, x.dtype, (N, D))
+        _check_dev("out", out, dev, x.dtype, (T, 1, D))
+        _check_dev("d_out", d_out, dev, torch.float32, (T, 1, D))
+        desc = C.desc_init()
+        desc.T, desc.d_model, desc.d_route, desc.n_units = T, D, dr, N
+        desc.n_routes = 1
+        desc.dtype = C.SRW_BF16
+        desc.sharpness = consts.sharpness
+        desc.act_threshold = consts.activation_threshold
+        desc.act_cutoff = consts.activation_cutoff
+        desc.epsilon = consts.epsilon
+        desc.max_intensity = consts.max_intensity
+        desc.dead_threshold = consts.dead_threshold
+        desc.scale = scale
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.grads = dict(dx=torch.empty(T, D, **f32), dh=torch.empty(T, 1, dr, **f32),
+                          demb=torch.empty(N, dr, **f32), dtau_offset=torch.empty(T, 1, **f32),
+                          dread=torch.empty(N, D, **f32), dwrite=torch.empty(N, D, **f32))
+        self.ws_bytes = C.backward_workspace_size(desc)
+        self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
+        self.inputs = (x, h, emb, tau_offset, read, write, out, d_out)
+        self.device = dev
+        self._desc = desc
+        self._tens = C.SrwTensors(_ptr(x), _ptr(x if h_is_x else h), _ptr(emb), _ptr(tau_offset),
+                                  _ptr(read), _ptr(write))
+        self._cot = C.SrwCotangents(_ptr(d_out), _ptr(out), float(d_score_lb), float(d_dead_penalty))
+        self._g = C.SrwGrads(*(_ptr(self.grads[k]) for k in
+                               ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite")))
+        self._lib = C.load_library()
+        self.path = None
+
+    def launch(self, stream=None) -> None:
+        if stream is None:
+            with torch.cuda.device(self.device):
+                stream = torch.cuda.current_stream(self.device)
+        C.check(self._lib.srw_backward(
+            ctypes.byref(self._desc), ctypes.byref(self._tens), ctypes.byref(self._cot),
+            ctypes.byref(self._g), _ptr(self.workspace), ctypes.c_size_t(self.ws_bytes),
+            ctypes.c_void_p(stream.cuda_stream)))
+        self.path = C.last_path()
+
+    def results(self) -> dict:
+        return dict(self.grads, path=self.path, workspace_bytes=self.ws_bytes)
+
+
 def srw_backward(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: float = 0.0,
                  d_dead_penalty: float = 0.0, *, consts: GateConfig = GateConfig(),
                  scale: float = 1.0, stream=None) -> dict:
@@ -223,57 +298,7 @@ def srw_backward(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: flo
     dh [T, 1, dr], demb [N, dr], dtau_offset [T, 1], dread / dwrite [N, D];
     when ``h is x`` the total gradient of x is dx + dh[:, 0].
     """
-    if x.dim() != 2:
-        raise ValueError("x must be [T, D]")
-    T, D = x.shape
-    dev = x.device
-    if dev.type != "cuda":
-        raise ValueError("srw_backward runs on a HIP device; got " + str(dev))
-    if x.dtype != torch.bfloat16:
-        raise TypeError("srw_backward takes bfloat16 inputs")
-    h_is_x = h is x
-    if h_is_x:
-        dr = D
-    else:
-        if h.dim() != 3 or h.shape[1] != 1:
-            raise ValueError("h must be [T, 1, d_route] (one route)")
-        dr = h.shape[2]
-        _check_dev("h", h, dev, x.dtype, (T, 1, dr))
-    N = emb.shape[0]
-    _check_dev("x", x, dev, x.dtype)
-    _check_dev("emb", emb, dev, x.dtype, (N, dr))
-    _check_dev("tau_offset", tau_offset, dev, torch.float32, (T, 1))
-    _check_dev("read", read, dev, x.dtype, (N, D))
-    _check_dev("write", write, dev, x.dtype, (N, D))
-    _check_dev("out", out, dev, x.dtype, (T, 1, D))
-    _check_dev("d_out", d_out, dev, torch.float32, (T, 1, D))
-    desc = C.desc_init()
-    desc.T, desc.d_model, desc.d_route, desc.n_units = T, D, dr, N
-    desc.n_routes = 1
-    desc.dtype = C.SRW_BF16
-    desc.sharpness = consts.sharpness
-    desc.act_threshold = consts.activation_threshold
-    desc.act_cutoff = consts.activation_cutoff
-    desc.epsilon = consts.epsilon
-    desc.max_intensity = consts.max_intensity
-    desc.dead_threshold = consts.dead_threshold
-    desc.scale = scale
-    f32 = dict(dtype=torch.float32, device=dev)
-    grads = dict(dx=torch.empty(T, D, **f32), dh=torch.empty(T, 1, dr, **f32),
-                 demb=torch.empty(N, dr, **f32), dtau_offset=torch.empty(T, 1, **f32),
-                 dread=torch.empty(N, D, **f32), dwrite=torch.empty(N, D, **f32))
-    ws_bytes = C.backward_workspace_size(desc)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-    tens = C.SrwTensors(_ptr(x), _ptr(x if h_is_x else h), _ptr(emb), _ptr(tau_offset),
-                        _ptr(read), _ptr(write))
-    cot = C.SrwCotangents(_ptr(d_out), _ptr(out), float(d_score_lb), float(d_dead_penalty))
-    g = C.SrwGrads(*(_ptr(grads[k]) for k in ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite")))
-    if stream is None:
-        with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev)
-    C.check(C.load_library().srw_backward(
-        ctypes.byref(desc), ctypes.byref(tens), ctypes.byref(cot), ctypes.byref(g),
-        _ptr(ws), ctypes.c_size_t(ws_bytes), ctypes.c_void_p(stream.cuda_stream)))
-    grads["path"] = C.last_path()
-    grads["workspace_bytes"] = ws_bytes
-    return grads
+    plan = SrwBackwardPlan(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb,
+                           d_dead_penalty, consts=consts, scale=scale)
+    plan.launch(stream)
+    return plan.results()
