@@ -797,11 +797,12 @@ __global__ __launch_bounds__(256) void bwd_token_stats_kernel(const float* __res
 // out
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__ d_out,
                                                        const uint16_t* __restrict__ out,
-                                                       const float* __restrict__ tok_sum, float scale, int D,
-                                                       uint16_t* __restrict__ draw, float* __restrict__ dden) {
+                                                       const float* __restrict__ zsums, int zs_stride, float scale,
+                                                       int D, uint16_t* __restrict__ draw,
+                                                       float* __restrict__ dden) {
   __shared__ float red[4];
   const int64_t t = blockIdx.x;
-  const float zsum = tok_sum[t * 4 + 1];
+  const float zsum = zsums[t * zs_stride];  // sum intensity of the row
   const float den = fmaxf(zsum, 1.0f);
   float acc = 0.f;
   for (int d = threadIdx.x; d < D; d += 256) {
@@ -814,29 +815,20 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
   if (threadIdx.x == 0) dden[t] = zsum > 1.0f ? -acc / den : 0.f;
 }
 
-// dP = draw . W^T per (256-unit, 256-token) tile, then the derivative of the
-// gate (v41:506-518) elementwise: d(gate_bf) and d(xr) from the bf16 product,
-// through act * intensity, the cutoff / cap clamps and the den term, to dm =
-// d loss / d margin; stores d(xr) (bf16) and dm (fp32), and per-token
-// partial sums of dm (the tau term)
-struct TBwdGateParams {
-  const uint16_t* write;  // [N, D]
-  const uint16_t* draw;   // [T, D]
-  const uint16_t* S;      // [T, N64] bf16 scores
-  const uint16_t* XR;     // [T, N64] bf16 x.r
-  const float* tau;       // [T]
-  const float* dden;      // [T]
-  uint16_t* DXR;          // [T, N64]
-  float* DM;              // [T, N64]
-  float* dm_part;         // [2 CT][T]
-  int64_t T, N, N64, D;
-  int RT, CT;
-  GateParams gp;
-  float exp_scale;        // -sharpness * log2(e)
-  float sharp;
+// Plain MFMA GEMM, bf16 out: C[t][n] = A[n, :] . B[t / div, :] over K for a
+// 256-unit x 256-row tile (A = units, B = rows), stored as [rows, N64] bf16
+// (the dot outputs the reference rounds to bf16: x.r, v41:517; the dP
+// transpose of the chunk dots, v41:518).  Units past N hold values of the
+// clamped last row: every consumer masks them.
+struct TStoreParams {
+  const uint16_t* A;  // [N, K]
+  const uint16_t* B;  // [rows_b, K]
+  uint16_t* C;        // [rows, N64]
+  int64_t rows, rows_b, N, N64, K;
+  int div, RT, CT;
 };
 
-__global__ __launch_bounds__(kGThreads) void tiled_bwd_gate_kernel(TBwdGateParams p) {
+__global__ __launch_bounds__(kGThreads) void tiled_store_kernel(TStoreParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -850,96 +842,298 @@ __global__ __launch_bounds__(kGThreads) void tiled_bwd_gate_kernel(TBwdGateParam
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
   {
-    const Opnd A = make_opnd(p.write, p.D, u0, p.N, 1, wave, lane);
-    const Opnd B = make_opnd(p.draw, p.D, v0, p.T, 1, wave, lane);
-    gemm_loop(acc, A, B, 0, static_cast<int>(p.D / kGK), lds, wave, lane, NoHook{});
+    const Opnd A = make_opnd(p.A, p.K, u0, p.N, 1, wave, lane);
+    const Opnd B = make_opnd(p.B, p.K, v0, p.rows, p.div, wave, lane);
+    gemm_loop(acc, A, B, 0, static_cast<int>(p.K / kGK), lds, wave, lane, NoHook{});
   }
   typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-  const int64_t nleft = p.N - (u0 + 128 * wa + 4 * h);
-  const float thr = p.gp.thr, cut = p.gp.cut, eps = p.gp.eps, maxi = p.gp.maxi;
-  // 16 groups (token block j, unit block i); the scores and x.r of group g + 1
-  // are loaded while group g is computed (one wave per SIMD: nothing else
-  // would hide their latency)
-  int64_t tl[4];
-  float tau[4], dden[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int64_t t = v0 + 128 * wb + 32 * j + u;
-    tl[j] = t < p.T ? t : p.T - 1;
-    tau[j] = p.tau[tl[j]];
-    dden[j] = p.dden[tl[j]];
-  }
-  auto load = [&](int j, int i, u32x2_t (&sv)[4], u32x2_t (&xv)[4]) {
-    const int64_t nb = u0 + 128 * wa + 32 * i + 4 * h;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const bool in = nb + 8 * q < p.N64;
-      sv[q] = in ? *reinterpret_cast<const u32x2_t*>(p.S + tl[j] * p.N64 + nb + 8 * q) : u32x2_t{0u, 0u};
-      xv[q] = in ? *reinterpret_cast<const u32x2_t*>(p.XR + tl[j] * p.N64 + nb + 8 * q) : u32x2_t{0u, 0u};
-    }
-  };
-  u32x2_t svc[4], xvc[4], svn[4], xvn[4];
-  load(0, 0, svc, xvc);
-#pragma clang loop unroll(full)
-  for (int j = 0; j < 4; ++j) {
-    const int64_t t = v0 + 128 * wb + 32 * j + u;
-    const bool tok = t < p.T;
-    float sdm = 0.f;
+    if (t >= p.rows) continue;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (4 * j + i < 15) load((4 * j + i + 1) >> 2, (i + 1) & 3, svn, xvn);
-      const int64_t nb = u0 + 128 * wa + 32 * i + 4 * h;
-      u32x2_t xo[4];
-      float dmf[16];  // dm of element v (units 8 (v / 4) + v % 4 from nb)
 #pragma unroll
-      for (int v = 0; v < 16; v += 2) {
-        const uint32_t dpq = pack_bf16(acc[i][j][v], acc[i][j][v + 1]);  // bf16 dot output
-        const uint32_t sp = svc[v >> 2][(v >> 1) & 1], xp = xvc[v >> 2][(v >> 1) & 1];
-        float dxr2[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float dp = e ? hi_f32(dpq) : lo_f32(dpq);
-          const float sc = e ? hi_f32(sp) : lo_f32(sp);
-          const float xr = e ? hi_f32(xp) : lo_f32(xp);
-          const float m = (sc - tau[j]) - thr;
-          const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(m * p.exp_scale));
-          const float am = fmaxf(m - cut, 0.0f);
-          const float it = eps + fminf(am, maxi);
-          const float gb = round_bf16(act * it);
-          const float dgb = round_bf16(dp * xr);     // d(gate_bf): bf16 multiply transpose
-          float dx = round_bf16(dp * gb);            // d(xr)
-          const float dit = dgb * act + dden[j];
-          const float dam = am < maxi ? dit : 0.f;
-          float dm = (m - cut > 0.f ? dam : 0.f) + dgb * it * p.sharp * act * (1.0f - act);
-          const bool ok = 32 * i + 8 * ((v + e) >> 2) + ((v + e) & 3) < nleft;
-          dm = ok ? dm : 0.f;
-          dx = ok ? dx : 0.f;
-          sdm += dm;
-          dxr2[e] = dx;
-          dmf[v + e] = dm;
-        }
-        xo[v >> 2][(v >> 1) & 1] = pack_bf16(dxr2[0], dxr2[1]);
+      for (int v = 0; v < 16; v += 4) {
+        const int64_t n0 = u0 + 128 * wa + 32 * i + 8 * (v >> 2) + 4 * h;
+        if (n0 < p.N64)
+          *reinterpret_cast<u32x2_t*>(p.C + t * p.N64 + n0) =
+              u32x2_t{pack_bf16(acc[i][j][v], acc[i][j][v + 1]), pack_bf16(acc[i][j][v + 2], acc[i][j][v + 3])};
       }
-      if (tok) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (nb + 8 * q < p.N64) {
-            *reinterpret_cast<u32x2_t*>(p.DXR + t * p.N64 + nb + 8 * q) = xo[q];
-            *reinterpret_cast<float4*>(p.DM + t * p.N64 + nb + 8 * q) =
-                float4{dmf[4 * q], dmf[4 * q + 1], dmf[4 * q + 2], dmf[4 * q + 3]};
-          }
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        svc[q] = svn[q];
-        xvc[q] = xvn[q];
-      }
-      __builtin_amdgcn_sched_barrier(0);
     }
-    sdm += __shfl_xor(sdm, 32);
-    if (h == 0 && tok) p.dm_part[static_cast<int64_t>(2 * ct + wa) * p.T + t] = sdm;
   }
+}
+
+// Elementwise passes over 64-row x 64-unit tiles of the [rows, N64] arrays:
+// thread (rp, q) = (tid / 8, tid % 8) owns rows 2 rp, 2 rp + 1 (one token's
+// two routes when paired) and units 8 q .. 8 q + 7; transposed copies go
+// through an LDS tile and leave as 16-byte row pieces.
+constexpr int kTile = 64;
+
+struct ElemTile {
+  int64_t v0, n0;  // first row, first unit
+  int rp, q;
+};
+__device__ inline ElemTile elem_tile() {
+  return ElemTile{static_cast<int64_t>(blockIdx.y) * kTile, static_cast<int64_t>(blockIdx.x) * kTile,
+                  static_cast<int>(threadIdx.x >> 3), static_cast<int>(threadIdx.x & 7)};
+}
+__device__ inline void load8_bf16(const uint16_t* p, float (&f)[8]) {
+  const u32x4_t w = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f[2 * k] = lo_f32(w[k]);
+    f[2 * k + 1] = hi_f32(w[k]);
+  }
+}
+__device__ inline void store8_bf16(uint16_t* p, const float (&f)[8]) {
+  *reinterpret_cast<u32x4_t*>(p) = u32x4_t{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]),
+                                           pack_bf16(f[6], f[7])};
+}
+// sum over the 8 threads of one row pair (consecutive lanes)
+__device__ inline float rowsum8(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  return v;
+}
+// tile[r][c] (bf16 bits, rows = tile rows) -> dst [cols, ld]: column c of the
+// tile is dst row n0 + c, rows r0 .. r0 + nr - 1 (nr a multiple of 8)
+__device__ inline void store_transposed(const uint16_t (*tile)[kTile + 8], int nr, uint16_t* dst, int64_t ld,
+                                        int64_t n0, int64_t r0, int64_t ncols) {
+  for (int idx = threadIdx.x; idx < kTile * (nr / 8); idx += 256) {
+    const int c = idx / (nr / 8), k = idx % (nr / 8);
+    if (n0 + c >= ncols) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = static_cast<uint32_t>(tile[8 * k + 2 * e][c]) | (static_cast<uint32_t>(tile[8 * k + 2 * e + 1][c]) << 16);
+    *reinterpret_cast<u32x4_t*>(dst + (n0 + c) * ld + r0 + 8 * k) = u32x4_t{w[0], w[1], w[2], w[3]};
+  }
+}
+
+struct ElemParams {
+  const uint16_t* S;      // [Tv, N64] bf16 scores
+  const uint16_t* XR;     // [T, N64] bf16 x.r per token
+  const uint16_t* DP;     // [Tv, N64] bf16 dP (E2)
+  const float* tau;       // [Tv]
+  const float* dden;      // [Tv] (E2)
+  uint16_t* PT;           // [N64, Tv64] P^T (E1)
+  float* inten_part;      // [N64 / 64][Tv] sum intensity partials (E1)
+  float* psum;            // [Tv64 / 64][N64] column sums of s (E1)
+  float* pmax;            // [Tv64 / 64][N64] column maxima of the gate (E1)
+  float* DM;              // [Tv, N64] dm (E2)
+  uint16_t* DXR;          // [T, N64] d(xr) per token (E2)
+  uint16_t* DXRT;         // [N64, T64] (E2)
+  float* dm_part;         // [N64 / 64][Tv] (E2)
+  int64_t Tv, N, N64, Tv64, T64;
+  int routes;
+  GateParams gp;
+  float exp_scale, sharp;
+};
+
+// E1: the forward's gates from the stored scores and x.r: P^T = bf16(bf16(g) *
+// xr)^T (v41:516-518), per-row sum intensity partials (den, v41:527, 584),
+// per-unit column sums of s and maxima of the gate (score_lb / dead penalty,
+// v41:445, 543)
+__global__ __launch_bounds__(256) void bwd_fwd_elem_kernel(ElemParams p) {
+  __shared__ uint16_t tile[kTile][kTile + 8];
+  __shared__ float cs[32][kTile + 1], cm[32][kTile + 1];
+  const ElemTile et = elem_tile();
+  const float c_exp = p.exp_scale, eps = p.gp.eps, maxi = p.gp.maxi;
+  float colsum[8] = {}, colmax[8] = {};
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int r = 2 * et.rp + rr;
+    const int64_t v = et.v0 + r;
+    const int64_t n = et.n0 + 8 * et.q;
+    const bool row_ok = v < p.Tv;
+    const int64_t vl = row_ok ? v : p.Tv - 1;
+    float s[8], x[8], pr[8];
+    load8_bf16(p.S + vl * p.N64 + n, s);
+    load8_bf16(p.XR + (vl / p.routes) * p.N64 + n, x);
+    const float tau_thr = p.tau[vl] + p.gp.thr;
+    const float k_exp = -tau_thr * c_exp, tau_cut = tau_thr + p.gp.cut;
+    float isum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool ok = row_ok && n + e < p.N;
+      const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(s[e], c_exp, k_exp)));
+      const float it = eps + __builtin_amdgcn_fmed3f(s[e] - tau_cut, 0.0f, maxi);
+      const float g = act * it;
+      pr[e] = ok ? round_bf16(g) * x[e] : 0.f;  // bf16 product, rounded by the packing below
+      isum += ok ? it : 0.f;
+      colsum[e] += ok ? s[e] : 0.f;
+      colmax[e] = fmaxf(colmax[e], ok ? g : 0.f);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t w = pack_bf16(pr[2 * k], pr[2 * k + 1]);
+      tile[r][8 * et.q + 2 * k] = static_cast<uint16_t>(w);
+      tile[r][8 * et.q + 2 * k + 1] = static_cast<uint16_t>(w >> 16);
+    }
+    isum = rowsum8(isum);
+    if (et.q == 0 && row_ok) p.inten_part[static_cast<int64_t>(blockIdx.x) * p.Tv + v] = isum;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    cs[et.rp][8 * et.q + e] = colsum[e];
+    cm[et.rp][8 * et.q + e] = colmax[e];
+  }
+  __syncthreads();
+  if (threadIdx.x < kTile) {
+    float a = 0.f, m = 0.f;
+    for (int k = 0; k < 32; ++k) {
+      a += cs[k][threadIdx.x];
+      m = fmaxf(m, cm[k][threadIdx.x]);
+    }
+    p.psum[static_cast<int64_t>(blockIdx.y) * p.N64 + et.n0 + threadIdx.x] = a;
+    p.pmax[static_cast<int64_t>(blockIdx.y) * p.N64 + et.n0 + threadIdx.x] = m;
+  }
+  store_transposed(tile, kTile, p.PT, p.Tv64, et.n0, et.v0, p.N64);
+}
+
+// E2: the gate derivative (v41:506-518) from the stored scores, x.r and dP:
+// d(gate_bf) and d(xr) from the bf16 product, through act * intensity, the
+// cutoff / cap clamps and the den term to dm; d(xr) summed over the routes of
+// a token (the broadcast of x.r, v41:796-797) and stored in both layouts
+__global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
+  __shared__ uint16_t tile[kTile][kTile + 8];
+  const ElemTile et = elem_tile();
+  const float thr = p.gp.thr, cut = p.gp.cut, eps = p.gp.eps, maxi = p.gp.maxi;
+  const int64_t n = et.n0 + 8 * et.q;
+  float dxs[2][8];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int r = 2 * et.rp + rr;
+    const int64_t v = et.v0 + r;
+    const bool row_ok = v < p.Tv;
+    const int64_t vl = row_ok ? v : p.Tv - 1;
+    float s[8], x[8], dp[8], dm[8];
+    load8_bf16(p.S + vl * p.N64 + n, s);
+    load8_bf16(p.XR + (vl / p.routes) * p.N64 + n, x);
+    load8_bf16(p.DP + vl * p.N64 + n, dp);
+    const float tau = p.tau[vl], dden = p.dden[vl];
+    float sdm = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool ok = row_ok && n + e < p.N;
+      const float m = (s[e] - tau) - thr;
+      const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(m * p.exp_scale));
+      const float am = fmaxf(m - cut, 0.0f);
+      const float it = eps + fminf(am, maxi);
+      const float gb = round_bf16(act * it);
+      const float dgb = round_bf16(dp[e] * x[e]);  // d(gate_bf): bf16 multiply transpose
+      const float dx = round_bf16(dp[e] * gb);     // d(xr)
+      const float dit = dgb * act + dden;
+      const float dam = am < maxi ? dit : 0.f;
+      const float d = (m - cut > 0.f ? dam : 0.f) + dgb * it * p.sharp * act * (1.0f - act);
+      dm[e] = ok ? d : 0.f;
+      dxs[rr][e] = ok ? dx : 0.f;
+      sdm += dm[e];
+    }
+    if (row_ok) {
+      *reinterpret_cast<float4*>(p.DM + v * p.N64 + n) = float4{dm[0], dm[1], dm[2], dm[3]};
+      *reinterpret_cast<float4*>(p.DM + v * p.N64 + n + 4) = float4{dm[4], dm[5], dm[6], dm[7]};
+    }
+    sdm = rowsum8(sdm);
+    if (et.q == 0 && row_ok) p.dm_part[static_cast<int64_t>(blockIdx.x) * p.Tv + v] = sdm;
+  }
+  // d(xr) per token: one row per route (single) or the pair's sum (paired)
+  const int nt = p.routes == 2 ? kTile / 2 : kTile;  // tokens in this tile
+  const int64_t t0 = p.routes == 2 ? et.v0 / 2 : et.v0;
+  const int64_t T = p.Tv / p.routes;
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    if (p.routes == 2 && rr == 1) break;
+    const int tr = p.routes == 2 ? et.rp : 2 * et.rp + rr;  // token row within the tile
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = p.routes == 2 ? dxs[0][e] + dxs[1][e] : dxs[rr][e];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t w = pack_bf16(o[2 * k], o[2 * k + 1]);
+      tile[tr][8 * et.q + 2 * k] = static_cast<uint16_t>(w);
+      tile[tr][8 * et.q + 2 * k + 1] = static_cast<uint16_t>(w >> 16);
+    }
+    if (t0 + tr < T) store8_bf16(p.DXR + (t0 + tr) * p.N64 + n, o);
+  }
+  __syncthreads();
+  store_transposed(tile, nt, p.DXRT, p.T64, et.n0, t0, p.N64);
+}
+
+struct DsParams {
+  const uint16_t* S;    // [Tv, N64]
+  const float* DM;      // [Tv, N64]
+  const float* alpha;   // [Tv]
+  const float* beta;    // [Tv]
+  const float* pn;      // [N64]
+  const float* dead;    // [N64]
+  const float* coef;    // {c0, c1}
+  uint16_t* DS;         // [Tv, N64]
+  uint16_t* DST;        // [N64, Tv64]
+  float d_pen;
+  int64_t Tv, N, N64, Tv64;
+};
+
+// E3: ds = bf16(dm + alpha_v + beta_v s + (c0 + c1 pn[n] - d_pen [pn < 0] dead[n]) / Tv)
+// (the tau chain, v41:461-464, and the per-unit score_lb / dead-penalty
+// terms, v41:445-447, 543-552), zero past N; both layouts
+__global__ __launch_bounds__(256) void bwd_ds_elem_kernel(DsParams p) {
+  __shared__ uint16_t tile[kTile][kTile + 8];
+  const ElemTile et = elem_tile();
+  const int64_t n = et.n0 + 8 * et.q;
+  const float c0 = p.coef[0], c1 = p.coef[1];
+  const float inv = 1.0f / static_cast<float>(p.Tv);
+  float unit[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float pv = p.pn[n + e];
+    unit[e] = (c0 + c1 * pv + (pv < 0.f ? -p.d_pen * p.dead[n + e] : 0.f)) * inv;
+  }
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int r = 2 * et.rp + rr;
+    const int64_t v = et.v0 + r;
+    const bool row_ok = v < p.Tv;
+    const int64_t vl = row_ok ? v : p.Tv - 1;
+    float s[8], o[8];
+    load8_bf16(p.S + vl * p.N64 + n, s);
+    const float4 d0 = *reinterpret_cast<const float4*>(p.DM + vl * p.N64 + n);
+    const float4 d1 = *reinterpret_cast<const float4*>(p.DM + vl * p.N64 + n + 4);
+    const float dm[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+    const float a = p.alpha[vl], b = p.beta[vl];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = row_ok && n + e < p.N ? dm[e] + a + b * s[e] + unit[e] : 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t w = pack_bf16(o[2 * k], o[2 * k + 1]);
+      tile[r][8 * et.q + 2 * k] = static_cast<uint16_t>(w);
+      tile[r][8 * et.q + 2 * k + 1] = static_cast<uint16_t>(w >> 16);
+    }
+    if (row_ok) store8_bf16(p.DS + v * p.N64 + n, o);
+  }
+  __syncthreads();
+  store_transposed(tile, kTile, p.DST, p.Tv64, et.n0, et.v0, p.N64);
+}
+
+// sum[v] = sum over b of part[b][v] (fixed order), four partial groups per row
+__global__ __launch_bounds__(256) void bwd_rowsum_kernel(const float* __restrict__ part, int nb, int64_t rows,
+                                                         float* __restrict__ sum) {
+  __shared__ float red[4][64];
+  const int c = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * 64 + c;
+  const int64_t vl = v < rows ? v : rows - 1;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  int b = grp;
+  for (; b + 12 < nb; b += 16) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] += part[static_cast<int64_t>(b + 4 * k) * rows + vl];
+  }
+  for (; b < nb; b += 4) a[0] += part[static_cast<int64_t>(b) * rows + vl];
+  red[grp][c] = (a[0] + a[1]) + (a[2] + a[3]);
+  __syncthreads();
+  if (grp == 0 && v < rows) sum[v] = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
 }
 
 // tau chain per token (v41:461-464): dtau = -sum_n dm; tau = mean + off * std,
@@ -965,35 +1159,6 @@ __global__ __launch_bounds__(256) void bwd_token_kernel(const float* __restrict_
     const float dmean = dtau - 2.0f * mean[t] * dvar;
     alpha[t] = dmean / fN;
     beta[t] = 2.0f * dvar / fN;
-  }
-}
-
-// per-unit mean score over the tokens and max gate (the score_lb / dead
-// penalty inputs, v41:445-447, 543-549): partials over 128-token slices
-__global__ __launch_bounds__(256) void bwd_unit_part_kernel(const uint16_t* __restrict__ S,
-                                                            const float* __restrict__ tau, int64_t T, int64_t N64,
-                                                            GateParams gp, float exp_scale, float* __restrict__ psum,
-                                                            float* __restrict__ pmax) {
-  __shared__ float rs[4][64], rm[4][64];
-  const int c = threadIdx.x & 63, grp = threadIdx.x >> 6;
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * 64 + c;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * 128;
-  const int64_t t1 = t0 + 128 < T ? t0 + 128 : T;
-  float sum = 0.f, gmax = 0.f;
-  for (int64_t t = t0 + grp; t < t1; t += 4) {
-    const float sc = bf16_to_f32(S[t * N64 + n]);
-    sum += sc;
-    const float tau_thr = tau[t] + gp.thr;
-    const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(sc, exp_scale, -tau_thr * exp_scale)));
-    const float it = gp.eps + __builtin_amdgcn_fmed3f(sc - (tau_thr + gp.cut), 0.0f, gp.maxi);
-    gmax = fmaxf(gmax, act * it);
-  }
-  rs[grp][c] = sum;
-  rm[grp][c] = gmax;
-  __syncthreads();
-  if (grp == 0) {
-    psum[blockIdx.y * N64 + n] = (rs[0][c] + rs[1][c]) + (rs[2][c] + rs[3][c]);
-    pmax[blockIdx.y * N64 + n] = fmaxf(fmaxf(rm[0][c], rm[1][c]), fmaxf(rm[2][c], rm[3][c]));
   }
 }
 
@@ -1051,43 +1216,6 @@ __global__ __launch_bounds__(256) void bwd_unit_coef_kernel(const float* __restr
   }
 }
 
-// ds = bf16(dm + alpha_t + beta_t s + (c0 + c1 pn[n] - d_pen [pn < 0] dead[n]) / T),
-// zero past N; eight units per thread
-__global__ __launch_bounds__(256) void bwd_ds_kernel(const uint16_t* __restrict__ S, const float* __restrict__ DM,
-                                                     const float* __restrict__ alpha, const float* __restrict__ beta,
-                                                     const float* __restrict__ pn, const float* __restrict__ dead,
-                                                     const float* __restrict__ coef, float d_pen, int64_t T,
-                                                     int64_t N, int64_t N64, uint16_t* __restrict__ DS) {
-  const int64_t t = blockIdx.x;  // one token per grid column, 2048 units per workgroup
-  const int64_t n0 = (static_cast<int64_t>(blockIdx.y) * 256 + threadIdx.x) * 8;
-  if (n0 >= N64) return;
-  const float a = alpha[t], b = beta[t], c0 = coef[0], c1 = coef[1];
-  const float invT = 1.0f / static_cast<float>(T);
-  const u32x4_t sq = *reinterpret_cast<const u32x4_t*>(S + t * N64 + n0);
-  const float4 d0 = *reinterpret_cast<const float4*>(DM + t * N64 + n0);
-  const float4 d1 = *reinterpret_cast<const float4*>(DM + t * N64 + n0 + 4);
-  const float4 p0 = *reinterpret_cast<const float4*>(pn + n0), p1 = *reinterpret_cast<const float4*>(pn + n0 + 4);
-  const float4 q0 = *reinterpret_cast<const float4*>(dead + n0), q1 = *reinterpret_cast<const float4*>(dead + n0 + 4);
-  const float dm[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-  const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-  const float dv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int k = 0; k < 8; k += 2) {
-    float r[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int64_t n = n0 + k + e;
-      const float sc = e ? hi_f32(sq[k >> 1]) : lo_f32(sq[k >> 1]);
-      const float p = pv[k + e];
-      const float unit = (c0 + c1 * p + (p < 0.f ? -d_pen * dv[k + e] : 0.f)) * invT;
-      r[e] = n < N ? dm[k + e] + a + b * sc + unit : 0.f;
-    }
-    o[k >> 1] = pack_bf16(r[0], r[1]);
-  }
-  *reinterpret_cast<u32x4_t*>(DS + t * N64 + n0) = u32x4_t{o[0], o[1], o[2], o[3]};
-}
-
 // out[i] = bf16(sum_s part[s][i]) widened to fp32: the reference's gradient
 // contractions are bf16 dots (their outputs bf16), split over K here
 __global__ __launch_bounds__(256) void bwd_sum_kernel(const float* __restrict__ part, int S, int64_t n,
@@ -1113,71 +1241,6 @@ BGemm bgemm(int64_t M, int64_t Nc, int64_t K) {
   spc = spc < 1 ? 1 : (spc > blocks ? blocks : spc);
   g.spc = static_cast<int>(spc);
   return g;
-}
-
-struct BLayout {
-  size_t S, XR, P, DXR, DS, DM, PT, DXRT, DST, ET, RT, HT, XT, DRAWT, DRAW;
-  size_t mom, tok_part, tok_sum, dm_part, tokv, psum, pmax, pn, dead, blk, coef, part, total;
-  int64_t T64, N64;
-  int CT, RTt, TS, nblk;
-  BGemm g_dw, g_dh, g_dx, g_de, g_dr;
-};
-
-BLayout blayout(const srw_desc_t& d) {
-  BLayout l{};
-  const int64_t T = d.T, N = d.n_units, D = d.d_model, dr = d.d_route;
-  l.T64 = (T + kNAlign - 1) / kNAlign * kNAlign;
-  l.N64 = (N + kNAlign - 1) / kNAlign * kNAlign;
-  l.CT = static_cast<int>((N + kGRows - 1) / kGRows);
-  l.RTt = static_cast<int>((T + kGRows - 1) / kGRows);
-  l.TS = static_cast<int>((T + 127) / 128);
-  l.nblk = static_cast<int>((l.N64 + 255) / 256);
-  l.g_dw = bgemm(N, D, T);
-  l.g_dh = bgemm(T, dr, N);
-  l.g_dx = bgemm(T, D, N);
-  l.g_de = bgemm(N, dr, T);
-  l.g_dr = bgemm(N, D, T);
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    const size_t at = off;
-    off += al256(static_cast<int64_t>(bytes));
-    return at;
-  };
-  const size_t tn = static_cast<size_t>(T) * l.N64 * 2, nt = static_cast<size_t>(l.N64) * l.T64 * 2;
-  l.S = take(tn);
-  l.XR = take(tn);
-  l.P = take(tn);
-  l.DXR = take(tn);
-  l.DS = take(tn);
-  l.DM = take(2 * tn);
-  l.PT = take(nt);
-  l.DXRT = take(nt);
-  l.DST = take(nt);
-  l.ET = take(static_cast<size_t>(dr) * l.N64 * 2);
-  l.RT = take(static_cast<size_t>(D) * l.N64 * 2);
-  l.HT = take(static_cast<size_t>(dr) * l.T64 * 2);
-  l.XT = take(static_cast<size_t>(D) * l.T64 * 2);
-  l.DRAWT = take(static_cast<size_t>(D) * l.T64 * 2);
-  l.DRAW = take(static_cast<size_t>(T) * D * 2);
-  l.mom = take(static_cast<size_t>(2 * l.CT) * T * 2 * 4);
-  l.tok_part = take(static_cast<size_t>(2 * l.CT) * T * 4 * 4);
-  l.tok_sum = take(static_cast<size_t>(T) * 4 * 4);
-  l.dm_part = take(static_cast<size_t>(2 * l.CT) * T * 4);
-  l.tokv = take(static_cast<size_t>(T) * 8 * 4);
-  l.psum = take(static_cast<size_t>(l.TS) * l.N64 * 4);
-  l.pmax = take(static_cast<size_t>(l.TS) * l.N64 * 4);
-  l.pn = take(static_cast<size_t>(l.N64) * 4);
-  l.dead = take(static_cast<size_t>(l.N64) * 4);
-  l.blk = take(static_cast<size_t>(l.nblk) * 2 * 4);
-  l.coef = take(4 * 4);
-  size_t part = 0;
-  for (const BGemm& g : {l.g_dw, l.g_dh, l.g_dx, l.g_de, l.g_dr}) {
-    const size_t b = static_cast<size_t>(g.spc) * g.M * g.Nc * 4;
-    part = b > part ? b : part;
-  }
-  l.part = take(part);
-  l.total = off;
-  return l;
 }
 
 // bf16 src [rows, cols] -> dst [cols, rows_pad] (zero rows past `rows`), 64 x
@@ -1248,11 +1311,98 @@ hipError_t bwd_gemm(const BGemm& g, const uint16_t* A, const uint16_t* B, int64_
   return hipGetLastError();
 }
 
+struct BLayout {
+  size_t S, XR, DP, DM, DXR, DS, PT, DXRT, DST, ET, RT, HT, XT, DRAWT, DRAW;
+  size_t mom, inten_part, dm_part, tokv, psum, pmax, pn, dead, blk, coef, part, total;
+  int64_t Tv, T64, Tv64, N64;
+  int CT, RTv, RTt, NB, TS, nblk;
+  BGemm g_dw, g_dh, g_dx, g_de, g_dr;
+};
+
+BLayout blayout(const srw_desc_t& d) {
+  BLayout l{};
+  const int64_t T = d.T, N = d.n_units, D = d.d_model, dr = d.d_route, R = d.n_routes;
+  l.Tv = T * R;
+  l.T64 = (T + kNAlign - 1) / kNAlign * kNAlign;
+  l.Tv64 = (l.Tv + kNAlign - 1) / kNAlign * kNAlign;
+  l.N64 = (N + kNAlign - 1) / kNAlign * kNAlign;
+  l.CT = static_cast<int>((N + kGRows - 1) / kGRows);
+  l.RTv = static_cast<int>((l.Tv + kGRows - 1) / kGRows);
+  l.RTt = static_cast<int>((T + kGRows - 1) / kGRows);
+  l.NB = static_cast<int>(l.N64 / kTile);   // unit blocks of the elementwise passes
+  l.TS = static_cast<int>(l.Tv64 / kTile);  // row blocks
+  l.nblk = static_cast<int>((l.N64 + 255) / 256);
+  l.g_dw = bgemm(N, D, l.Tv);
+  l.g_dh = bgemm(l.Tv, dr, N);
+  l.g_dx = bgemm(T, D, N);
+  l.g_de = bgemm(N, dr, l.Tv);
+  l.g_dr = bgemm(N, D, T);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += al256(static_cast<int64_t>(bytes));
+    return at;
+  };
+  const size_t vn = static_cast<size_t>(l.Tv) * l.N64 * 2, tn = static_cast<size_t>(T) * l.N64 * 2;
+  l.S = take(vn);
+  l.XR = take(tn);
+  l.DP = take(vn);
+  l.DM = take(2 * vn);
+  l.DXR = take(tn);
+  l.DS = take(vn);
+  l.PT = take(static_cast<size_t>(l.N64) * l.Tv64 * 2);
+  l.DXRT = take(static_cast<size_t>(l.N64) * l.T64 * 2);
+  l.DST = take(static_cast<size_t>(l.N64) * l.Tv64 * 2);
+  l.ET = take(static_cast<size_t>(dr) * l.N64 * 2);
+  l.RT = take(static_cast<size_t>(D) * l.N64 * 2);
+  l.HT = take(static_cast<size_t>(dr) * l.Tv64 * 2);
+  l.XT = take(static_cast<size_t>(D) * l.T64 * 2);
+  l.DRAWT = take(static_cast<size_t>(D) * l.Tv64 * 2);
+  l.DRAW = take(static_cast<size_t>(l.Tv) * D * 2);
+  l.mom = take(static_cast<size_t>(2 * l.CT) * l.Tv * 2 * 4);
+  l.inten_part = take(static_cast<size_t>(l.NB) * l.Tv * 4);
+  l.dm_part = take(static_cast<size_t>(l.NB) * l.Tv * 4);
+  l.tokv = take(static_cast<size_t>(l.Tv) * 8 * 4);
+  l.psum = take(static_cast<size_t>(l.TS) * l.N64 * 4);
+  l.pmax = take(static_cast<size_t>(l.TS) * l.N64 * 4);
+  l.pn = take(static_cast<size_t>(l.N64) * 4);
+  l.dead = take(static_cast<size_t>(l.N64) * 4);
+  l.blk = take(static_cast<size_t>(l.nblk) * 2 * 4);
+  l.coef = take(4 * 4);
+  size_t part = 0;
+  for (const BGemm& g : {l.g_dw, l.g_dh, l.g_dx, l.g_de, l.g_dr}) {
+    const size_t b = static_cast<size_t>(g.spc) * g.M * g.Nc * 4;
+    part = b > part ? b : part;
+  }
+  l.part = take(part);
+  l.total = off;
+  return l;
+}
+
+hipError_t store_gemm(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t rows, int64_t rows_b, int div,
+                      int64_t N, int64_t N64, int64_t K, hipStream_t s) {
+  TStoreParams p{};
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.rows = rows;
+  p.rows_b = rows_b;
+  p.N = N;
+  p.N64 = N64;
+  p.K = K;
+  p.div = div;
+  p.RT = static_cast<int>((rows + kGRows - 1) / kGRows);
+  p.CT = static_cast<int>((N + kGRows - 1) / kGRows);
+  const unsigned grid = static_cast<unsigned>(8 * p.RT * ((p.CT + 7) / 8));
+  hipLaunchKernelGGL(tiled_store_kernel, dim3(grid), dim3(kGThreads), kGemmLds, s, p);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool tiled_backward_supports(const srw_desc_t& d) {
   if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41 || d.stats_mode != SRW_STATS_ONEPASS) return false;
-  if (d.n_routes != 1) return false;
+  if (d.n_routes != 1 && d.n_routes != 2) return false;
   if (d.d_model % kNAlign != 0 || d.d_route % kNAlign != 0) return false;
   if (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
   return d.scale != 0.0f;
@@ -1263,17 +1413,18 @@ size_t tiled_backward_workspace_bytes(const srw_desc_t& d) { return blayout(d).t
 hipError_t tiled_backward(const BackwardArgs& a) {
   const srw_desc_t& d = a.d;
   const BLayout l = blayout(d);
-  const int64_t T = d.T, N = d.n_units, D = d.d_model, dr = d.d_route, N64 = l.N64, T64 = l.T64;
+  const int R = d.n_routes;
+  const int64_t T = d.T, N = d.n_units, D = d.d_model, dr = d.d_route, N64 = l.N64, Tv = l.Tv;
   auto b16 = [&](size_t off) { return reinterpret_cast<uint16_t*>(a.ws + off); };
   auto f32 = [&](size_t off) { return reinterpret_cast<float*>(a.ws + off); };
-  uint16_t *S = b16(l.S), *XR = b16(l.XR), *P = b16(l.P), *DXR = b16(l.DXR), *DS = b16(l.DS);
+  uint16_t *S = b16(l.S), *XR = b16(l.XR), *DP = b16(l.DP), *DXR = b16(l.DXR), *DS = b16(l.DS);
   uint16_t *PT = b16(l.PT), *DXRT = b16(l.DXRT), *DST = b16(l.DST), *ET = b16(l.ET), *RT = b16(l.RT);
   uint16_t *HT = b16(l.HT), *XT = b16(l.XT), *DRAWT = b16(l.DRAWT), *DRAW = b16(l.DRAW);
-  float *DM = f32(l.DM), *mom = f32(l.mom), *tok_part = f32(l.tok_part), *tok_sum = f32(l.tok_sum);
-  float *dm_part = f32(l.dm_part), *tokv = f32(l.tokv), *psum = f32(l.psum), *pmax = f32(l.pmax);
-  float *pn = f32(l.pn), *dead = f32(l.dead), *blk = f32(l.blk), *coef = f32(l.coef), *part = f32(l.part);
-  float *mean = tokv, *var = tokv + T, *sdev = tokv + 2 * T, *tau = tokv + 3 * T, *dden = tokv + 4 * T;
-  float *alpha = tokv + 5 * T, *beta = tokv + 6 * T;
+  float *DM = f32(l.DM), *mom = f32(l.mom), *inten_part = f32(l.inten_part), *dm_part = f32(l.dm_part);
+  float *tokv = f32(l.tokv), *psum = f32(l.psum), *pmax = f32(l.pmax), *pn = f32(l.pn), *dead = f32(l.dead);
+  float *blk = f32(l.blk), *coef = f32(l.coef), *part = f32(l.part);
+  float *mean = tokv, *var = tokv + Tv, *sdev = tokv + 2 * Tv, *tau = tokv + 3 * Tv, *dden = tokv + 4 * Tv;
+  float *alpha = tokv + 5 * Tv, *beta = tokv + 6 * Tv, *zsum = tokv + 7 * Tv;
   const auto* emb = static_cast<const uint16_t*>(a.in.emb);
   const auto* read = static_cast<const uint16_t*>(a.in.read);
   const auto* write = static_cast<const uint16_t*>(a.in.write);
@@ -1283,112 +1434,109 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   hipStream_t st = a.stream;
   hipError_t e;
   for (const void* fn : {reinterpret_cast<const void*>(tiled_stats_kernel),
-                         reinterpret_cast<const void*>(tiled_gate_kernel<true>),
-                         reinterpret_cast<const void*>(tiled_bwd_gate_kernel),
+                         reinterpret_cast<const void*>(tiled_store_kernel),
                          reinterpret_cast<const void*>(tiled_write_kernel)})
     if ((e = set_lds(fn)) != hipSuccess) return e;
 #define SRW_TRY(expr) \
   if ((e = (expr)) != hipSuccess) return e
-  // operands of the K = units / K = tokens contractions, unit- or token-contiguous
+  // operands of the K = units / K = rows contractions, unit- or row-contiguous
   SRW_TRY(transpose(emb, ET, N, N64, dr, st));
   SRW_TRY(transpose(read, RT, N, N64, D, st));
-  SRW_TRY(transpose(h, HT, T, T64, dr, st));
-  SRW_TRY(transpose(x, XT, T, T64, D, st));
+  SRW_TRY(transpose(h, HT, Tv, l.Tv64, dr, st));
+  SRW_TRY(transpose(x, XT, T, l.T64, D, st));
 
-  // forward recompute: scores, moments, tau, x.r, gates, P, sum intensity
-  const unsigned grid_rc = static_cast<unsigned>(8 * l.RTt * ((l.CT + 7) / 8));
+  // forward recompute: scores (stored), moments, tau, x.r (stored)
   TStatsParams sp{};
   sp.h = h;
   sp.emb = emb;
   sp.S = S;
   sp.mom = mom;
-  sp.Tv = T;
+  sp.Tv = Tv;
   sp.N = N;
   sp.N64 = N64;
   sp.dr = dr;
-  sp.RT = l.RTt;
+  sp.RT = l.RTv;
   sp.CT = l.CT;
-  hipLaunchKernelGGL(tiled_stats_kernel, dim3(grid_rc), dim3(kGThreads), kGemmLds, st, sp);
+  hipLaunchKernelGGL(tiled_stats_kernel, dim3(static_cast<unsigned>(8 * l.RTv * ((l.CT + 7) / 8))),
+                     dim3(kGThreads), kGemmLds, st, sp);
   SRW_TRY(hipGetLastError());
-  hipLaunchKernelGGL(bwd_token_stats_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, st, mom,
-                     2 * l.CT, T, N, a.in.tau_offset, mean, var, sdev, tau);
+  hipLaunchKernelGGL(bwd_token_stats_kernel, dim3(static_cast<unsigned>((Tv + 3) / 4)), dim3(256), 0, st, mom,
+                     2 * l.CT, Tv, N, a.in.tau_offset, mean, var, sdev, tau);
   SRW_TRY(hipGetLastError());
-  TGateParams gp{};
-  gp.x = x;
-  gp.read = read;
-  gp.tau = tau;
-  gp.P = S;
-  gp.P_out = P;
-  gp.XR_out = XR;
-  gp.tok_part = tok_part;
-  gp.Tv = T;
-  gp.N = N;
-  gp.N64 = N64;
-  gp.D = D;
-  gp.routes = 1;
-  gp.RT = l.RTt;
-  gp.CT = l.CT;
-  gp.gp = a.gp;
-  gp.exp_scale = exp_scale;
-  hipLaunchKernelGGL(tiled_gate_kernel<true>, dim3(grid_rc), dim3(kGThreads), kGemmLds, st, gp);
+  SRW_TRY(store_gemm(read, x, XR, T, T, 1, N, N64, D, st));
+
+  // E1: gates, P^T, sum intensity, per-unit statistics
+  ElemParams ep{};
+  ep.S = S;
+  ep.XR = XR;
+  ep.DP = DP;
+  ep.tau = tau;
+  ep.dden = dden;
+  ep.PT = PT;
+  ep.inten_part = inten_part;
+  ep.psum = psum;
+  ep.pmax = pmax;
+  ep.DM = DM;
+  ep.DXR = DXR;
+  ep.DXRT = DXRT;
+  ep.dm_part = dm_part;
+  ep.Tv = Tv;
+  ep.N = N;
+  ep.N64 = N64;
+  ep.Tv64 = l.Tv64;
+  ep.T64 = l.T64;
+  ep.routes = R;
+  ep.gp = a.gp;
+  ep.exp_scale = exp_scale;
+  ep.sharp = d.sharpness;
+  const dim3 grid_e(static_cast<unsigned>(l.NB), static_cast<unsigned>(l.TS));
+  hipLaunchKernelGGL(bwd_fwd_elem_kernel, grid_e, dim3(256), 0, st, ep);
   SRW_TRY(hipGetLastError());
-  hipLaunchKernelGGL(tiled_tok_sum_kernel, dim3(static_cast<unsigned>((T + 63) / 64)), dim3(256), 0, st, tok_part,
-                     tok_sum, T, 2 * l.CT);
-  SRW_TRY(hipGetLastError());
-  // per-unit terms of score_lb and the dead penalty
-  hipLaunchKernelGGL(bwd_unit_part_kernel, dim3(static_cast<unsigned>(N64 / 64), static_cast<unsigned>(l.TS)),
-                     dim3(256), 0, st, S, tau, T, N64, a.gp, exp_scale, psum, pmax);
+  hipLaunchKernelGGL(bwd_rowsum_kernel, dim3(static_cast<unsigned>((Tv + 63) / 64)), dim3(256), 0, st, inten_part,
+                     l.NB, Tv, zsum);
   SRW_TRY(hipGetLastError());
   hipLaunchKernelGGL(bwd_unit_reduce_kernel, dim3(static_cast<unsigned>(l.nblk)), dim3(256), 0, st, psum, pmax, l.TS,
-                     T, N, N64, d.dead_threshold, pn, dead, blk);
+                     Tv, N, N64, d.dead_threshold, pn, dead, blk);
   SRW_TRY(hipGetLastError());
   hipLaunchKernelGGL(bwd_unit_coef_kernel, dim3(1), dim3(256), 0, st, blk, l.nblk, N, a.cot.d_score_lb, coef);
   SRW_TRY(hipGetLastError());
 
-  // cotangent of the chunk dots, the den term, dP and the gate derivative
-  hipLaunchKernelGGL(bwd_prep_kernel, dim3(static_cast<unsigned>(T)), dim3(256), 0, st, a.cot.d_out,
-                     static_cast<const uint16_t*>(a.cot.out), tok_sum, d.scale, static_cast<int>(D), DRAW, dden);
+  // cotangent of the chunk dots and the den term; dP; E2: the gate derivative
+  hipLaunchKernelGGL(bwd_prep_kernel, dim3(static_cast<unsigned>(Tv)), dim3(256), 0, st, a.cot.d_out,
+                     static_cast<const uint16_t*>(a.cot.out), zsum, 1, d.scale, static_cast<int>(D), DRAW, dden);
   SRW_TRY(hipGetLastError());
-  TBwdGateParams bp{};
-  bp.write = write;
-  bp.draw = DRAW;
-  bp.S = S;
-  bp.XR = XR;
-  bp.tau = tau;
-  bp.dden = dden;
-  bp.DXR = DXR;
-  bp.DM = DM;
-  bp.dm_part = dm_part;
-  bp.T = T;
-  bp.N = N;
-  bp.N64 = N64;
-  bp.D = D;
-  bp.RT = l.RTt;
-  bp.CT = l.CT;
-  bp.gp = a.gp;
-  bp.exp_scale = exp_scale;
-  bp.sharp = d.sharpness;
   dominant_kernel_begin(st);
-  hipLaunchKernelGGL(tiled_bwd_gate_kernel, dim3(grid_rc), dim3(kGThreads), kGemmLds, st, bp);
+  SRW_TRY(store_gemm(write, DRAW, DP, Tv, Tv, 1, N, N64, D, st));
   dominant_kernel_end(st);
+  hipLaunchKernelGGL(bwd_gate_elem_kernel, grid_e, dim3(256), 0, st, ep);
   SRW_TRY(hipGetLastError());
-  hipLaunchKernelGGL(bwd_token_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, st, dm_part, 2 * l.CT,
-                     T, N, a.in.tau_offset, mean, var, sdev, a.g.dtau_offset, alpha, beta);
+  hipLaunchKernelGGL(bwd_token_kernel, dim3(static_cast<unsigned>((Tv + 3) / 4)), dim3(256), 0, st, dm_part, l.NB,
+                     Tv, N, a.in.tau_offset, mean, var, sdev, a.g.dtau_offset, alpha, beta);
   SRW_TRY(hipGetLastError());
-  hipLaunchKernelGGL(bwd_ds_kernel, dim3(static_cast<unsigned>(T), static_cast<unsigned>((N64 / 8 + 255) / 256)),
-                     dim3(256), 0, st, S, DM,
-                     alpha, beta, pn, dead, coef, a.cot.d_dead_penalty, T, N, N64, DS);
+  // E3: ds in both layouts
+  DsParams dp{};
+  dp.S = S;
+  dp.DM = DM;
+  dp.alpha = alpha;
+  dp.beta = beta;
+  dp.pn = pn;
+  dp.dead = dead;
+  dp.coef = coef;
+  dp.DS = DS;
+  dp.DST = DST;
+  dp.d_pen = a.cot.d_dead_penalty;
+  dp.Tv = Tv;
+  dp.N = N;
+  dp.N64 = N64;
+  dp.Tv64 = l.Tv64;
+  hipLaunchKernelGGL(bwd_ds_elem_kernel, grid_e, dim3(256), 0, st, dp);
   SRW_TRY(hipGetLastError());
 
-  // token-contiguous copies for the K = tokens contractions
-  SRW_TRY(transpose(P, PT, T, T64, N64, st));
-  SRW_TRY(transpose(DXR, DXRT, T, T64, N64, st));
-  SRW_TRY(transpose(DS, DST, T, T64, N64, st));
-  SRW_TRY(transpose(DRAW, DRAWT, T, T64, D, st));
-  // the six contractions (dP above): bf16 dots, fp32 accumulation
-  SRW_TRY(bwd_gemm(l.g_dw, PT, DRAWT, T64, part, a.g.dwrite, st));
-  SRW_TRY(bwd_gemm(l.g_dr, DXRT, XT, T64, part, a.g.dread, st));
-  SRW_TRY(bwd_gemm(l.g_de, DST, HT, T64, part, a.g.demb, st));
+  // the five gradient contractions: bf16 dots, fp32 accumulation
+  SRW_TRY(transpose(DRAW, DRAWT, Tv, l.Tv64, D, st));
+  SRW_TRY(bwd_gemm(l.g_dw, PT, DRAWT, l.Tv64, part, a.g.dwrite, st));
+  SRW_TRY(bwd_gemm(l.g_dr, DXRT, XT, l.T64, part, a.g.dread, st));
+  SRW_TRY(bwd_gemm(l.g_de, DST, HT, l.Tv64, part, a.g.demb, st));
   SRW_TRY(bwd_gemm(l.g_dx, DXR, RT, N64, part, a.g.dx, st));
   SRW_TRY(bwd_gemm(l.g_dh, DS, ET, N64, part, a.g.dh, st));
 #undef SRW_TRY

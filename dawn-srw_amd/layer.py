@@ -227,23 +227,23 @@ class SrwBackwardPlan:
             raise TypeError("srw_backward takes bfloat16 inputs")
         h_is_x = h is x
         if h_is_x:
-            dr = D
+            R, dr = 1, D
         else:
-            if h.dim() != 3 or h.shape[1] != 1:
-                raise ValueError("h must be [T, 1, d_route] (one route)")
-            dr = h.shape[2]
-            _check_dev("h", h, dev, x.dtype, (T, 1, dr))
+            if h.dim() != 3 or h.shape[1] not in (1, 2):
+                raise ValueError("h must be [T, R, d_route] with R = 1 or 2")
+            R, dr = h.shape[1], h.shape[2]
+            _check_dev("h", h, dev, x.dtype, (T, R, dr))
         N = emb.shape[0]
         _check_dev("x", x, dev, x.dtype)
         _check_dev("emb", emb, dev, x.dtype, (N, dr))
-        _check_dev("tau_offset", tau_offset, dev, torch.float32, (T, 1))
+        _check_dev("tau_offset", tau_offset, dev, torch.float32, (T, R))
         _check_dev("read", read, dev, x.dtype, (N, D))
         _check_dev("write", write, dev, x.dtype, (N, D))
-        _check_dev("out", out, dev, x.dtype, (T, 1, D))
-        _check_dev("d_out", d_out, dev, torch.float32, (T, 1, D))
+        _check_dev("out", out, dev, x.dtype, (T, R, D))
+        _check_dev("d_out", d_out, dev, torch.float32, (T, R, D))
         desc = C.desc_init()
         desc.T, desc.d_model, desc.d_route, desc.n_units = T, D, dr, N
-        desc.n_routes = 1
+        desc.n_routes = R
         desc.dtype = C.SRW_BF16
         desc.sharpness = consts.sharpness
         desc.act_threshold = consts.activation_threshold
@@ -253,8 +253,8 @@ class SrwBackwardPlan:
         desc.dead_threshold = consts.dead_threshold
         desc.scale = scale
         f32 = dict(dtype=torch.float32, device=dev)
-        self.grads = dict(dx=torch.empty(T, D, **f32), dh=torch.empty(T, 1, dr, **f32),
-                          demb=torch.empty(N, dr, **f32), dtau_offset=torch.empty(T, 1, **f32),
+        self.grads = dict(dx=torch.empty(T, D, **f32), dh=torch.empty(T, R, dr, **f32),
+                          demb=torch.empty(N, dr, **f32), dtau_offset=torch.empty(T, R, **f32),
                           dread=torch.empty(N, D, **f32), dwrite=torch.empty(N, D, **f32))
         self.ws_bytes = C.backward_workspace_size(desc)
         self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
@@ -290,13 +290,14 @@ def srw_backward(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: flo
     fused_gate_srw that the reference's train_step takes with
     jax.value_and_grad, scripts/train_jax.py:548-726).
 
-    Inputs as :func:`srw_forward` (bf16, one route, h [T, 1, dr] or x
-    itself), ``out`` [T, 1, D] the forward's output on them, ``d_out`` the
-    cotangent of ``out`` (float32, same shape), ``d_score_lb`` /
-    ``d_dead_penalty`` the cotangents of the score_lb and dead_penalty
-    outputs (v41:477-483, 543-552).  Returns float32 gradients dx [T, D],
-    dh [T, 1, dr], demb [N, dr], dtau_offset [T, 1], dread / dwrite [N, D];
-    when ``h is x`` the total gradient of x is dx + dh[:, 0].
+    Inputs as :func:`srw_forward` (bf16; h [T, R, dr] with R = 1, or 2 for
+    the paired QK routes of fused_gate_srw_paired, v41:640-909, or x itself),
+    ``out`` [T, R, D] the forward's output on them, ``d_out`` the cotangent
+    of ``out`` (float32, same shape), ``d_score_lb`` / ``d_dead_penalty`` the
+    cotangents of the score_lb and dead_penalty outputs (v41:477-483,
+    543-552).  Returns float32 gradients dx [T, D], dh [T, R, dr], demb
+    [N, dr], dtau_offset [T, R], dread / dwrite [N, D]; when ``h is x`` the
+    total gradient of x is dx + dh[:, 0].
     """
     plan = SrwBackwardPlan(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb,
                            d_dead_penalty, consts=consts, scale=scale)

@@ -89,3 +89,35 @@ def test_backward_linear_in_cotangents(pkg, dev):
     for k in ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite"):
         err = rel_fro((ga[k] + gb[k]).cpu(), gs[k].cpu())
         assert err <= 2e-2, (k, err)
+
+
+@pytest.mark.parametrize("case", [(96, 384, 128, 1580, 21), (70, 128, 64, 777, 22)],
+                         ids=lambda c: "T{}D{}dr{}N{}".format(*c[:4]))
+def test_backward_paired_matches_oracle(pkg, dev, case):
+    """Paired QK routes (fused_gate_srw_paired, v41:640-909): rows are (token,
+    route) pairs sharing one x.R^T; the oracle is the single-route VJP on
+    those 2T rows with x repeated per route, dx summed over a token's routes."""
+    T, D, dr, N, seed = case
+    print(f"[gpu] backward paired {case}", flush=True)
+    shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=2)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=seed)
+    g = torch.Generator().manual_seed(seed + 7)
+    tau = -0.5 + 0.2 * torch.randn(T, 2, generator=g)
+    xb = inp["x"].to(BF)
+    hb = inp["h"].to(BF)
+    eb, rb, wb = (inp[k].to(BF) for k in ("emb", "read", "write"))
+    d_out = torch.randn(T, 2, D, generator=g)
+    d_lb, d_pen = 0.4, -0.6
+    ref = srw_vjp.fused_gate_srw_vjp(xb.float().repeat_interleave(2, dim=0), hb.float().reshape(2 * T, dr),
+                                     eb.float(), tau.reshape(2 * T, 1), rb.float(), wb.float(),
+                                     d_out.reshape(2 * T, D), d_lb, d_pen, max_chunk_size=N)
+    args = (xb.to(dev), hb.to(dev), eb.to(dev), tau.to(dev), rb.to(dev), wb.to(dev))
+    fwd = pkg.srw_forward(*args, want_mask=False)
+    got = pkg.srw_backward(*args, fwd["out"], d_out.to(dev), d_lb, d_pen)
+    torch.cuda.synchronize()
+    want = dict(dx=ref["dx"].reshape(T, 2, D).sum(dim=1), dh=ref["dh"].reshape(T, 2, dr), demb=ref["demb"],
+                dtau_offset=ref["dtau_offset"].reshape(T, 2), dread=ref["dread"], dwrite=ref["dwrite"])
+    for k, v in want.items():
+        err = rel_fro(got[k].cpu(), v.float())
+        print(f"  {k}: rel err {err:.3e}", flush=True)
+        assert err <= 2e-2, (k, err)
