@@ -19,7 +19,7 @@ import threading
 import torch  # noqa: F401  (must precede loading the HIP library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libsrw_amd.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # srw_status_t
 SRW_OK, SRW_EINVAL, SRW_EUNSUPPORTED, SRW_EHIP, SRW_EWORKSPACE = range(5)
@@ -84,7 +84,7 @@ class SrwCotangents(ctypes.Structure):
 
 class SrwGrads(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
-        "dx", "dh", "demb", "dtau_offset", "dread", "dwrite")]
+        "dx", "dh", "demb", "dtau_offset", "dread", "dwrite", "dscale")]
 
 
 class SrwError(RuntimeError):

@@ -115,7 +115,7 @@ srw_status_t srw_workspace_size(const srw_desc_t* d, size_t* bytes) {
   if (which < 0 && which_alias < 0) return SRW_EUNSUPPORTED;
   size_t need = 0;
   for (int w : {which, which_alias}) {
-    if (w < 0) continue;
+    if (w < 0 || d->T == 0) continue;  // no tokens: srw_forward needs no workspace
     const size_t n = align256(bytes_of(w, *d));
     need = n > need ? n : need;
   }
@@ -181,7 +181,7 @@ srw_status_t srw_backward_workspace_size(const srw_desc_t* d, size_t* bytes) {
   if (st != SRW_OK) return st;
   if (!bytes) return SRW_EINVAL;
   if (!srw::tiled_backward_supports(*d)) return SRW_EUNSUPPORTED;
-  *bytes = align256(srw::tiled_backward_workspace_bytes(*d));
+  *bytes = d->T == 0 ? 0 : align256(srw::tiled_backward_workspace_bytes(*d));
   return SRW_OK;
 }
 
@@ -191,7 +191,15 @@ srw_status_t srw_backward(const srw_desc_t* d, const srw_tensors_t* in, const sr
   if (st != SRW_OK) return st;
   if (!in || !cot || !grads) return SRW_EINVAL;
   if (!srw::tiled_backward_supports(*d)) return SRW_EUNSUPPORTED;
-  if (d->T == 0) {
+  if (d->T == 0) {  // no tokens: the pool gradients are zero
+    if (!grads->demb || !grads->dread || !grads->dwrite) return SRW_EINVAL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t N = d->n_units;
+    if (srw::fill_f32(grads->demb, N * d->d_route, 0.f, s) != hipSuccess ||
+        srw::fill_f32(grads->dread, N * d->d_model, 0.f, s) != hipSuccess ||
+        srw::fill_f32(grads->dwrite, N * d->d_model, 0.f, s) != hipSuccess ||
+        (grads->dscale && srw::fill_f32(grads->dscale, 1, 0.f, s) != hipSuccess))
+      return SRW_EHIP;
     g_last_path = "empty";
     return SRW_OK;
   }

@@ -794,25 +794,40 @@ __global__ __launch_bounds__(256) void bwd_token_stats_kernel(const float* __res
 // draw = bf16(d_out * scale) / den as bf16 (the cotangent of the chunk dots),
 // and the den term dden = -sum_d dq * (raw / den) / den where den = max(sum
 // intensity, 1) is differentiable (v41:584-585); raw / den from the forward's
-// out
+// out.  dsc[t] = sum_d d_out * out / scale: the row's share of the gradient
+// of the scale the caller multiplies out by (v41:1044-1053, 1175).
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__ d_out,
                                                        const uint16_t* __restrict__ out,
                                                        const float* __restrict__ zsums, int zs_stride, float scale,
                                                        int D, uint16_t* __restrict__ draw,
-                                                       float* __restrict__ dden) {
+                                                       float* __restrict__ dden, float* __restrict__ dsc) {
   __shared__ float red[4];
   const int64_t t = blockIdx.x;
   const float zsum = zsums[t * zs_stride];  // sum intensity of the row
   const float den = fmaxf(zsum, 1.0f);
-  float acc = 0.f;
+  float acc = 0.f, acc_s = 0.f;
   for (int d = threadIdx.x; d < D; d += 256) {
-    const float dq = round_bf16(d_out[t * D + d] * scale);
+    const float g = d_out[t * D + d];
+    const float dq = round_bf16(g * scale);
     const float o = bf16_to_f32(out[t * D + d]) / scale;
     acc += dq * o;
+    acc_s += g * o;
     draw[t * D + d] = f32_to_bf16_bits(dq / den);
   }
   acc = block_sum<256>(acc, red);
   if (threadIdx.x == 0) dden[t] = zsum > 1.0f ? -acc / den : 0.f;
+  acc_s = block_sum<256>(acc_s, red);
+  if (threadIdx.x == 0) dsc[t] = acc_s;
+}
+
+// out[0] = sum of v[0 .. n) in one workgroup (a fixed order: deterministic).
+__global__ __launch_bounds__(256) void bwd_total_kernel(const float* __restrict__ v, int64_t n,
+                                                        float* __restrict__ out) {
+  __shared__ float red[4];
+  float acc = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 256) acc += v[i];
+  acc = block_sum<256>(acc, red);
+  if (threadIdx.x == 0) out[0] = acc;
 }
 
 // Plain MFMA GEMM, bf16 out: C[t][n] = A[n, :] . B[t / div, :] over K for a
@@ -1362,7 +1377,7 @@ BLayout blayout(const srw_desc_t& d) {
   l.mom = take(static_cast<size_t>(2 * l.CT) * l.Tv * 2 * 4);
   l.inten_part = take(static_cast<size_t>(l.NB) * l.Tv * 4);
   l.dm_part = take(static_cast<size_t>(l.NB) * l.Tv * 4);
-  l.tokv = take(static_cast<size_t>(l.Tv) * 8 * 4);
+  l.tokv = take(static_cast<size_t>(l.Tv) * 9 * 4);
   l.psum = take(static_cast<size_t>(l.TS) * l.N64 * 4);
   l.pmax = take(static_cast<size_t>(l.TS) * l.N64 * 4);
   l.pn = take(static_cast<size_t>(l.N64) * 4);
@@ -1424,7 +1439,7 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   float *tokv = f32(l.tokv), *psum = f32(l.psum), *pmax = f32(l.pmax), *pn = f32(l.pn), *dead = f32(l.dead);
   float *blk = f32(l.blk), *coef = f32(l.coef), *part = f32(l.part);
   float *mean = tokv, *var = tokv + Tv, *sdev = tokv + 2 * Tv, *tau = tokv + 3 * Tv, *dden = tokv + 4 * Tv;
-  float *alpha = tokv + 5 * Tv, *beta = tokv + 6 * Tv, *zsum = tokv + 7 * Tv;
+  float *alpha = tokv + 5 * Tv, *beta = tokv + 6 * Tv, *zsum = tokv + 7 * Tv, *dsc = tokv + 8 * Tv;
   const auto* emb = static_cast<const uint16_t*>(a.in.emb);
   const auto* read = static_cast<const uint16_t*>(a.in.read);
   const auto* write = static_cast<const uint16_t*>(a.in.write);
@@ -1503,8 +1518,13 @@ hipError_t tiled_backward(const BackwardArgs& a) {
 
   // cotangent of the chunk dots and the den term; dP; E2: the gate derivative
   hipLaunchKernelGGL(bwd_prep_kernel, dim3(static_cast<unsigned>(Tv)), dim3(256), 0, st, a.cot.d_out,
-                     static_cast<const uint16_t*>(a.cot.out), zsum, 1, d.scale, static_cast<int>(D), DRAW, dden);
+                     static_cast<const uint16_t*>(a.cot.out), zsum, 1, d.scale, static_cast<int>(D), DRAW, dden,
+                     dsc);
   SRW_TRY(hipGetLastError());
+  if (a.g.dscale) {
+    hipLaunchKernelGGL(bwd_total_kernel, dim3(1), dim3(256), 0, st, dsc, Tv, a.g.dscale);
+    SRW_TRY(hipGetLastError());
+  }
   dominant_kernel_begin(st);
   SRW_TRY(store_gemm(write, DRAW, DP, Tv, Tv, 1, N, N64, D, st));
   dominant_kernel_end(st);

@@ -255,7 +255,8 @@ class SrwBackwardPlan:
         f32 = dict(dtype=torch.float32, device=dev)
         self.grads = dict(dx=torch.empty(T, D, **f32), dh=torch.empty(T, R, dr, **f32),
                           demb=torch.empty(N, dr, **f32), dtau_offset=torch.empty(T, R, **f32),
-                          dread=torch.empty(N, D, **f32), dwrite=torch.empty(N, D, **f32))
+                          dread=torch.empty(N, D, **f32), dwrite=torch.empty(N, D, **f32),
+                          dscale=torch.empty((), **f32))
         self.ws_bytes = C.backward_workspace_size(desc)
         self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
         self.inputs = (x, h, emb, tau_offset, read, write, out, d_out)
@@ -265,7 +266,7 @@ class SrwBackwardPlan:
                                   _ptr(read), _ptr(write))
         self._cot = C.SrwCotangents(_ptr(d_out), _ptr(out), float(d_score_lb), float(d_dead_penalty))
         self._g = C.SrwGrads(*(_ptr(self.grads[k]) for k in
-                               ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite")))
+                               ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite", "dscale")))
         self._lib = C.load_library()
         self.path = None
 
@@ -296,8 +297,9 @@ def srw_backward(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: flo
     of ``out`` (float32, same shape), ``d_score_lb`` / ``d_dead_penalty`` the
     cotangents of the score_lb and dead_penalty outputs (v41:477-483,
     543-552).  Returns float32 gradients dx [T, D], dh [T, R, dr], demb
-    [N, dr], dtau_offset [T, R], dread / dwrite [N, D]; when ``h is x`` the
-    total gradient of x is dx + dh[:, 0].
+    [N, dr], dtau_offset [T, R], dread / dwrite [N, D] and dscale [] (of
+    ``scale``, which multiplies out: the caller's *_scale, v41:1044-1053,
+    1175); when ``h is x`` the total gradient of x is dx + dh[:, 0].
     """
     plan = SrwBackwardPlan(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb,
                            d_dead_penalty, consts=consts, scale=scale)

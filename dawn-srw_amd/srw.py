@@ -22,13 +22,17 @@ functions cast x, h, emb, read and write to bf16 (:423-430) and return
 ``out`` as float32 holding bf16-rounded values (:586, :630).  The kernel
 computes every per-token and per-unit reduction; this module only turns
 those [T]- and [N]-sized vectors into the reference's scalars (:588-635).
+
+The fused functions are autograd nodes: out, score_lb and dead_penalty --
+the outputs the reference's training loss uses (scripts/train_jax.py:
+586-603) -- backpropagate to all six inputs through ``srw_backward``.
 """
 
 from __future__ import annotations
 
 import torch
 
-from .layer import GateConfig, srw_forward
+from .layer import GateConfig, srw_backward, srw_forward
 from . import _capi as C
 
 __all__ = ["make_sharded_srw", "make_sharded_srw_paired", "srw_inference",
@@ -111,6 +115,74 @@ def _diag_tuple(res, N, B, S, R, dead_threshold):
             col("int_max").max(), col("n_int_cap").sum() / float(B * S * R * N))
 
 
+# Positions in the 22-tuple (v41:630-635).  The training loss differentiates
+# out, score_lb and dead_penalty (scripts/train_jax.py:586-603).
+_OUT, _SCORE_LB, _DEAD_PENALTY = 0, 3, 18
+# Outputs without a gradient: behind stop_gradient in the reference (gate_max
+# :583, tau_abs_mean, z_lt_*, active_per_token_std, entropy, dead_count,
+# int_max, int_cap_frac, :599-629) or piecewise-constant counts (active_frac,
+# active_n_mean, strong_frac, boundary_frac).
+_NO_GRAD = (1, 2, 6, 7, 8, 10, 11, 12, 14, 15, 19, 20, 21)
+_NAMES = ("out", "active_frac", "gate_max", "score_lb", "score_std", "gate_sum_mean",
+          "active_n_mean", "strong_frac", "boundary_frac", "z_mean_active", "tau_abs_mean",
+          "z_lt_075", "z_lt_030", "skew", "active_per_token_std", "entropy", "intensity_sum_mean",
+          "kurt", "dead_penalty", "dead_count", "int_max", "int_cap_frac")
+
+
+class _FusedSrw(torch.autograd.Function):
+    """fused_gate_srw(_paired) as one autograd node: the forward runs
+    srw_forward (bf16, one-pass statistics, diagnostics), the backward runs
+    srw_backward with the cotangents of out, score_lb and dead_penalty -- the
+    VJP that jax.value_and_grad takes through the reference's checkpointed
+    scans (v41:434, 489; scripts/train_jax.py:726).  Differentiating any other
+    differentiable diagnostic (score_std, the gate and intensity sums, skew,
+    kurt) raises NotImplementedError; the rest carry no gradient, as in the
+    reference."""
+
+    @staticmethod
+    def forward(ctx, x, h, emb, tau_offset, read, write, routes, consts, cs):
+        B, S, D = x.shape
+        N = emb.shape[0]
+        bf = torch.bfloat16
+        xb = x.reshape(B * S, D).to(bf).contiguous()
+        hb = h.reshape(B * S, routes, h.shape[-1]).to(bf).contiguous()
+        tau = tau_offset.reshape(B * S, routes).to(torch.float32).contiguous()
+        eb, rdb, wb = (t.to(bf).contiguous() for t in (emb, read, write))
+        res = srw_forward(xb, hb, eb, tau, rdb, wb, stats="onepass", consts=consts,
+                          chunk_size=cs, diag=True, want_mask=False)
+        shape = (B, S, D) if routes == 1 else (B, S, 2, D)
+        out = res["out"].reshape(shape).to(torch.float32)
+        outs = (out,) + _diag_tuple(res, N, B, S, routes, consts.dead_threshold)
+        ctx.save_for_backward(xb, hb, eb, tau, rdb, wb, res["out"])
+        ctx.meta = (routes, consts, tuple(t.shape for t in (x, h, emb, tau_offset, read, write)),
+                    tuple(t.dtype for t in (x, h, emb, tau_offset, read, write)))
+        ctx.mark_non_differentiable(*(outs[i] for i in _NO_GRAD))
+        ctx.set_materialize_grads(False)
+        return outs
+
+    @staticmethod
+    def backward(ctx, *grads):
+        for i, g in enumerate(grads):
+            if g is not None and i not in (_OUT, _SCORE_LB, _DEAD_PENALTY) and i not in _NO_GRAD:
+                raise NotImplementedError(
+                    f"the gradient through output {i} ({_NAMES[i]}) of the fused SRW layer is not "
+                    "implemented; out, score_lb and dead_penalty are differentiable")
+        routes, consts, shapes, dtypes = ctx.meta
+        xb, hb, eb, tau, rdb, wb, out_b = ctx.saved_tensors
+        T, D = xb.shape
+        d_out = grads[_OUT]
+        if d_out is None:
+            d_out = torch.zeros(T, routes, D, dtype=torch.float32, device=xb.device)
+        else:
+            d_out = d_out.reshape(T, routes, D).to(torch.float32).contiguous()
+        d_lb = 0.0 if grads[_SCORE_LB] is None else float(grads[_SCORE_LB])
+        d_pen = 0.0 if grads[_DEAD_PENALTY] is None else float(grads[_DEAD_PENALTY])
+        g = srw_backward(xb, hb, eb, tau, rdb, wb, out_b, d_out, d_lb, d_pen, consts=consts)
+        res = [g[k] for k in ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite")]
+        res = [r.reshape(sh).to(dt) for r, sh, dt in zip(res, shapes, dtypes)]
+        return (*res, None, None, None)
+
+
 def _make(routes: int, mesh, max_chunk_size, dead_threshold, sharpness,
           activation_threshold, activation_cutoff, epsilon, max_intensity):
     _check_mesh(mesh)
@@ -119,26 +191,8 @@ def _make(routes: int, mesh, max_chunk_size, dead_threshold, sharpness,
                         float(max_intensity), float(dead_threshold))
 
     def fused(x, h, emb, tau_offset, read, write):
-        B, S, D = x.shape
-        N = emb.shape[0]
-        _, cs = chunk_plan(N, max_chunk_size)
-        bf = torch.bfloat16
-        xb = x.reshape(B * S, D).to(bf).contiguous()
-        if routes == 1:
-            hb = h.reshape(B * S, 1, h.shape[-1]).to(bf).contiguous()
-            tau = tau_offset.reshape(B * S, 1).to(torch.float32).contiguous()
-        else:
-            hb = h.reshape(B * S, 2, h.shape[-1]).to(bf).contiguous()
-            tau = tau_offset.reshape(B * S, 2).to(torch.float32).contiguous()
-        res = srw_forward(xb, hb, emb.to(bf).contiguous(), tau,
-                          read.to(bf).contiguous(), write.to(bf).contiguous(),
-                          stats="onepass", consts=consts, chunk_size=cs,
-                          diag=True, want_mask=False)
-        if routes == 1:
-            out = res["out"].reshape(B, S, D).to(torch.float32)
-        else:
-            out = res["out"].reshape(B, S, 2, D).to(torch.float32)
-        return (out,) + _diag_tuple(res, N, B, S, routes, dead_threshold)
+        _, cs = chunk_plan(emb.shape[0], max_chunk_size)
+        return _FusedSrw.apply(x, h, emb, tau_offset, read, write, routes, consts, cs)
 
     fused.__name__ = "fused_gate_srw" if routes == 1 else "fused_gate_srw_paired"
     return fused

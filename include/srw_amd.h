@@ -57,7 +57,7 @@
 extern "C" {
 #endif
 
-#define SRW_AMD_ABI_VERSION 3
+#define SRW_AMD_ABI_VERSION 4
 
 typedef enum srw_status {
   SRW_OK = 0,
@@ -193,9 +193,9 @@ typedef struct srw_cotangents {
   float d_dead_penalty;    /* cotangent of dead_penalty (v41:543-552) */
 } srw_cotangents_t;
 
-/* Gradients written by srw_backward, float32, all required.  When the
- * forward's h was x itself (d_route == d_model), the gradient of x is
- * dx + dh (the two paths are returned separately). */
+/* Gradients written by srw_backward, float32; all required but dscale.
+ * When the forward's h was x itself (d_route == d_model), the gradient of x
+ * is dx + dh (the two paths are returned separately). */
 typedef struct srw_grads {
   float* dx;               /* [T, D] */
   float* dh;               /* [T, n_routes, d_route] */
@@ -203,6 +203,9 @@ typedef struct srw_grads {
   float* dtau_offset;      /* [T, n_routes] */
   float* dread;            /* [N, D] */
   float* dwrite;           /* [N, D] */
+  float* dscale;           /* [1] gradient of desc->scale: sum d_out * out / scale,
+                              the gradient of the caller's *_scale multiply
+                              (v41:1044-1053, 1175); optional (NULL: skipped) */
 } srw_grads_t;
 
 /* ABI version of the loaded library (SRW_AMD_ABI_VERSION). */
@@ -234,9 +237,10 @@ srw_status_t srw_backward_workspace_size(const srw_desc_t* desc, size_t* bytes);
  * `stream`: recomputes the forward's scores, gates and products from the
  * inputs (as the reference's jax.checkpoint-ed scans do, v41:434, 489) and
  * writes the gradients of <d_out, out> + d_score_lb * score_lb +
- * d_dead_penalty * dead_penalty.  bf16, v4.1 gate, one route, one-pass
- * statistics, d_model and d_route multiples of 64; anything else returns
- * SRW_EUNSUPPORTED.  The cotangents of bf16 values are rounded to bf16 where
+ * d_dead_penalty * dead_penalty.  bf16, v4.1 gate, one route or the paired
+ * routes (n_routes = 2, fused_gate_srw_paired), one-pass statistics, d_model
+ * and d_route multiples of 64; anything else returns SRW_EUNSUPPORTED.  With
+ * T = 0 the gradients of emb, read, write (and dscale) are zero.  The cotangents of bf16 values are rounded to bf16 where
  * the reference's bf16 casts, dots and products transpose (the gradients are
  * bf16 dot outputs widened to float32). */
 srw_status_t srw_backward(const srw_desc_t* desc, const srw_tensors_t* in,

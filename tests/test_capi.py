@@ -41,8 +41,9 @@ def test_library_exports_every_header_symbol(C):
 def test_struct_layout_matches_header(C, tmp_path):
     fields = [f[0] for f in C.SrwDesc._fields_]
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "srw_amd.h"', "int main(void){",
-             'printf("%zu %zu %zu %d %d\\n", sizeof(srw_desc_t), sizeof(srw_tensors_t), '
-             'sizeof(srw_outputs_t), (int)SRW_TDIAG_COUNT, (int)SRW_UDIAG_COUNT);']
+             'printf("%zu %zu %zu %zu %zu %d %d\\n", sizeof(srw_desc_t), sizeof(srw_tensors_t), '
+             'sizeof(srw_outputs_t), sizeof(srw_cotangents_t), sizeof(srw_grads_t), '
+             '(int)SRW_TDIAG_COUNT, (int)SRW_UDIAG_COUNT);']
     for f in fields:
         lines.append(f'printf("{f} %zu\\n", offsetof(srw_desc_t, {f}));')
     lines.append("return 0;}")
@@ -54,7 +55,8 @@ def test_struct_layout_matches_header(C, tmp_path):
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
     sizes = [int(v) for v in out[0].split()]
     assert sizes == [ctypes.sizeof(C.SrwDesc), ctypes.sizeof(C.SrwTensors),
-                     ctypes.sizeof(C.SrwOutputs), len(C.TDIAG), len(C.UDIAG)]
+                     ctypes.sizeof(C.SrwOutputs), ctypes.sizeof(C.SrwCotangents),
+                     ctypes.sizeof(C.SrwGrads), len(C.TDIAG), len(C.UDIAG)]
     for line in out[1:]:
         if line:
             name, off = line.split()
@@ -117,6 +119,19 @@ def test_workspace_sizes(C):
     assert C.workspace_size(d) == 2 * 100 * 64 * 2
     d = _desc(C, gate=C.SRW_GATE_GELU_V401, dtype=C.SRW_F32)
     assert C.workspace_size(d) == 2 * 100 * 64 * 4
+
+
+@pytest.mark.parametrize("shape", [(384, 384, 1, 0), (384, 128, 2, 0), (1024, 1024, 1, 0),
+                                   (384, 384, 1, 0x20), (128, 64, 1, 0)])
+def test_no_tokens_need_no_workspace(C, shape):
+    """T = 0 sizes to zero bytes on every family, forward and backward (the
+    sizing divides nothing by T)."""
+    D, dr, R, flags = shape
+    d = _desc(C, T=0, d_model=D, d_route=dr, n_routes=R, n_units=300, flags=flags)
+    assert C.workspace_size(d) == 0
+    assert C.backward_workspace_size(d) == 0
+    d.T = 1
+    assert C.workspace_size(d) > 0 and C.backward_workspace_size(d) > 0
 
 
 def test_status_strings(C):

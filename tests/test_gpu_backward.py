@@ -121,3 +121,48 @@ def test_backward_paired_matches_oracle(pkg, dev, case):
         err = rel_fro(got[k].cpu(), v.float())
         print(f"  {k}: rel err {err:.3e}", flush=True)
         assert err <= 2e-2, (k, err)
+
+
+def test_backward_scale_and_dscale(pkg, dev):
+    """A scale folded into the call (the caller's *_scale multiply, v41:1044-1053,
+    1175): at scale 2 (a power of two, so every rounding commutes with it) the
+    gradients equal those at scale 1 with the cotangent doubled, bit for bit;
+    dscale equals <d_out, out at scale 1> from the oracle's forward."""
+    T, D, dr, N, seed = 96, 384, 128, 1580, 31
+    print(f"[gpu] backward scale T{T} N{N}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, False, seed, -0.5)
+    xb = inp["x"].to(BF)
+    hb = inp["h"][:, 0].to(BF)
+    eb, rb, wb = (inp[k].to(BF) for k in ("emb", "read", "write"))
+    g = torch.Generator().manual_seed(seed)
+    d_out = torch.randn(T, D, generator=g)
+    args = (xb.to(dev), hb[:, None].contiguous().to(dev), eb.to(dev), inp["tau_offset"].to(dev), rb.to(dev),
+            wb.to(dev))
+    out1 = pkg.srw_forward(*args, want_mask=False)["out"]
+    out2 = pkg.srw_forward(*args, want_mask=False, scale=2.0)["out"]
+    g1 = pkg.srw_backward(*args, out1, (2.0 * d_out)[:, None].to(dev), 0.3, -0.7)
+    g2 = pkg.srw_backward(*args, out2, d_out[:, None].to(dev), 0.3, -0.7, scale=2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(out2.float(), 2.0 * out1.float())
+    for k in ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite"):
+        assert torch.equal(g1[k], g2[k]), k
+    ref = srw_vjp.fused_gate_srw_vjp(xb.float(), hb.float(), eb.float(), inp["tau_offset"], rb.float(),
+                                     wb.float(), d_out, 0.3, -0.7, max_chunk_size=N)
+    want = float((d_out.double() * ref["out"].double()).sum())
+    got = float(g2["dscale"])
+    print(f"  dscale {got:.6f} oracle {want:.6f}", flush=True)
+    assert abs(got - want) <= 1e-2 * abs(want) + 1e-3
+
+
+def test_backward_empty_tokens(pkg, dev):
+    """T = 0: nothing flows into the pool, whose gradients are zero."""
+    D, N = 128, 300
+    z = torch.empty(0, D, dtype=BF, device=dev)
+    emb = torch.randn(N, D, device=dev).to(BF)
+    rw = torch.randn(N, D, device=dev).to(BF)
+    got = pkg.srw_backward(z, z, emb, torch.empty(0, 1, device=dev), rw, rw,
+                           torch.empty(0, 1, D, dtype=BF, device=dev), torch.empty(0, 1, D, device=dev), 0.5, 0.5)
+    torch.cuda.synchronize()
+    for k in ("demb", "dread", "dwrite", "dscale"):
+        assert torch.count_nonzero(got[k]) == 0, k
+    assert got["dx"].shape == (0, D) and got["dtau_offset"].shape == (0, 1)
