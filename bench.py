@@ -50,7 +50,11 @@ WORKLOADS = {
     "qk": ("qk", 12500, "configs[1] QK pool, paired routes sharing one x.R^T"),
     "decode_know": ("decode_know", 12500, "configs[3] decode-shaped Know pool, T=64, 3% pass"),
     "scaled": ("scaled", 12500, "configs[4] scaled Know pool d=1024 N=100000 T=16384, 2% pass"),
+    # the whole model (its own branch below): 12 layers, B = 32, S = 512, vocab 32 000
+    "model": (None, 12500, "configs[2] full 12-layer DAWN-SRW 40M prefill forward (logits), the SRW "
+                           "kernels timed inside it"),
 }
+MODEL_BATCH, MODEL_SEQ, MODEL_VOCAB = 32, 512, 32000
 
 
 def log(msg: str) -> None:
@@ -115,6 +119,89 @@ def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: b
                        f"runs; {cpu_model()}")}
 
 
+def bench_model(args, pkg, C, dev) -> dict:
+    """DAWN.__call__ (deterministic) over B x S uniform token ids
+    with random-init weights of the 40M architecture; a step is one forward
+    to the logits.  The dominant kernel is the Know pool's fused SRW kernel
+    (the last layer's call of each step is the one timed)."""
+    import torch
+    cfg = pkg.DawnConfig(vocab_size=MODEL_VOCAB)
+    B, S = MODEL_BATCH, MODEL_SEQ
+    T, D, dr, L = B * S, cfg.d_model, cfg.d_route, cfg.n_layers
+    params = pkg.init_params(cfg, seed=args.seed)
+    model = pkg.DawnModel(params, cfg, dev)
+    ids = torch.randint(0, cfg.vocab_size, (B, S), generator=torch.Generator().manual_seed(args.seed))
+    ids_dev = ids.to(dev)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(max(1, args.warmup)):
+        model.forward(ids_dev)
+    torch.cuda.synchronize()
+    log(f"model warm-up done: T={T}, paths " + ", ".join(
+        f"{k[0]}:{c.plan.path}" for k, c in model._calls.items()))
+    K = args.steps
+    ev_k = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(K)]
+    for a, b in ev_k:
+        a.record(stream)
+        b.record(stream)
+    t_begin = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_begin.record(stream)
+    for i in range(K):
+        C.set_kernel_events(ev_k[i][0].cuda_event, ev_k[i][1].cuda_event)
+        model.forward(ids_dev)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    C.set_kernel_events(None, None)
+    step_ms = t_begin.elapsed_time(t_end) / K
+    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev_k)
+    log(f"timed {K} forwards: {step_ms:.3f} ms/step, Know kernel {kern_ms:.4f} ms")
+    srw = L * 2.0 * T * (cfg.n_qk * (2 * dr + 3 * D) + cfg.n_v * (dr + 2 * D) + cfg.n_know * (dr + 2 * D))
+    glue = (L * (2.0 * T * D * (4 * dr + 4) + 2.0 * T * D * D + 4.0 * B * S * S * D)
+            + 2.0 * T * D * cfg.vocab_size)
+    kflops = 2.0 * T * cfg.n_know * (dr + 2 * D)
+    achieved = kflops / (kern_ms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "kernel": model._calls[("know", T, 1, "onepass")].plan.path,
+                "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops,
+                "step_tflops": round((srw + glue) / (step_ms * 1e-3) / 1e12, 2),
+                "srw_flop_per_step": srw, "glue_flop_per_step": glue}
+    cpu = None
+    if args.cpu_seconds > 0:
+        from oracle import dawn_ref
+        torch.set_num_threads(min(os.cpu_count() or 1, 16))
+        S_s = 64
+        sample = ids[:1, :S_s]
+        times = []
+        t0 = time.perf_counter()
+        while not times or (time.perf_counter() - t0 < args.cpu_seconds and len(times) < 5):
+            t1 = time.perf_counter()
+            dawn_ref.forward(params, cfg, sample)
+            times.append(time.perf_counter() - t1)
+        med = statistics.median(times)
+        log(f"cpu baseline: {S_s} tokens, runs={len(times)} median={med:.2f} s")
+        cpu = {"value": S_s / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": (f"oracle DAWN forward (oracle/dawn_ref.py, bf16-emulated SRW, f32 glue), "
+                          f"1 x {S_s} tokens of the same ids, full 40M model, median of {len(times)} "
+                          f"runs; {cpu_model()}")}
+    return {
+        "metric": METRIC, "value": round(T / (step_ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": K, "warmup": args.warmup, "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": ("synthetic (token ids uniform over the vocabulary, seeded; random-init weights "
+                 "with the reference's initialisers)"),
+        "config": {"workload": "model", "note": WORKLOADS["model"][2], "batch": B, "seq_len": S,
+                   "tokens": T, "n_layers": L, "d_model": D, "d_route": dr, "n_heads": cfg.n_heads,
+                   "vocab": cfg.vocab_size, "pools": [cfg.n_qk, cfg.n_v, cfg.n_know],
+                   "srw": "bf16, one-pass statistics, chunk 12500", "glue": "float32",
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -167,6 +254,12 @@ def main() -> int:
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.workload == "model":
+        if args.backward or args.graph or args.diag or args.tiled or args.stats != "onepass":
+            print("bench.py: --workload model times the plain forward", file=sys.stderr)
+            return 2
+        print(json.dumps(bench_model(args, pkg, C, dev)), flush=True)
+        return 0
     key, max_chunk, note = WORKLOADS[args.workload]
     shape = pkg.inputs.CONFIGS[key]
     _, cs = pkg.chunk_plan(shape.N, max_chunk)
