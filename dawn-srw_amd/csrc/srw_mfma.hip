@@ -1318,6 +1318,96 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
   }
 }
 
+// Few splits per chunk (spc < 16: prefill-sized T): one wave per row, lane l
+// owning columns l + 64 j (coalesced 256-byte loads), four rows per
+// workgroup.  Each chunk's splits are summed in the order of the NG = 1
+// kernel above (eight accumulators, a fixed tree), so both give the same
+// bits; the per-row partials and diagnostics are reduced across the wave.
+template <int DC>  // d_model / 64
+__global__ __launch_bounds__(256) void srw_finalize_rows_kernel(FinalParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= p.T) return;
+  float gs = 0.f, is = 0.f, na = 0.f;
+  for (int s = lane; s < p.S_tok; s += 64) {
+    const float* tp = p.tok_part + (static_cast<int64_t>(s) * p.T + t) * p.tps;
+    gs += tp[0];
+    is += tp[1];
+    na += tp[2];
+  }
+  gs = wave_sum(gs);
+  is = wave_sum(is);
+  na = wave_sum(na);
+  const float den = fmaxf(is, 1.0f);                          // v41:584
+  const int64_t stride = p.T * p.D;
+  const float* col = p.out_part + t * p.D + lane;
+  float raw[DC];
+#pragma unroll
+  for (int j = 0; j < DC; ++j) raw[j] = 0.f;
+  for (int s0 = 0; s0 < p.S; s0 += p.spc) {                   // one reference chunk
+    float acc[DC][8];
+#pragma unroll
+    for (int j = 0; j < DC; ++j)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[j][k] = 0.f;
+    int s = s0;
+    for (; s + 7 < s0 + p.spc; s += 8) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int j = 0; j < DC; ++j) acc[j][k] += col[(s + k) * stride + 64 * j];
+    }
+    for (; s < s0 + p.spc; ++s) {
+#pragma unroll
+      for (int j = 0; j < DC; ++j) acc[j][0] += col[s * stride + 64 * j];
+    }
+#pragma unroll
+    for (int j = 0; j < DC; ++j) {
+      const float* a = acc[j];
+      const float sum = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+      raw[j] += round_bf16(sum);                              // bf16 dot output (v41:518)
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < DC; ++j) {
+    const float o = round_bf16(raw[j] / den);                 // v41:585-586
+    p.out[t * p.D + lane + 64 * j] = f32_to_bf16_bits(o * p.scale);
+  }
+  if (lane == 0) {
+    if (p.gate_sum) p.gate_sum[t] = gs;
+    if (p.den) p.den[t] = den;
+    if (p.n_active) p.n_active[t] = static_cast<int32_t>(na);
+  }
+  if (p.token_diag) {
+    float smax = -INFINITY, c[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = lane; s < p.S_tok; s += 64) {
+      const float* tp = p.tok_part + (static_cast<int64_t>(s) * p.T + t) * p.tps;
+      smax = fmaxf(smax, tp[TP_SMAX]);
+#pragma unroll
+      for (int k = 0; k < 6; ++k) c[k] += tp[TP_STRONG + k];
+    }
+    smax = wave_max(smax);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) c[k] = wave_sum(c[k]);
+    if (lane == 0) {
+      const float tau_thr = p.tau[t] + p.gp.thr;
+      const float tau_cut = tau_thr + p.gp.cut;
+      const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(smax, p.exp_scale, -tau_thr * p.exp_scale)));
+      const float imax = p.gp.eps + __builtin_amdgcn_fmed3f(smax - tau_cut, 0.0f, p.gp.maxi);
+      float* td = p.token_diag + t * SRW_TDIAG_COUNT;
+      td[SRW_TDIAG_GATE_MAX] = act * imax;
+      td[SRW_TDIAG_INT_SUM] = is;
+      td[SRW_TDIAG_N_STRONG] = c[0];
+      td[SRW_TDIAG_N_BOUNDARY] = c[1];
+      td[SRW_TDIAG_N_BAND075] = c[2];
+      td[SRW_TDIAG_N_BAND030] = c[3];
+      td[SRW_TDIAG_N_INT_CAP] = c[4];
+      td[SRW_TDIAG_G_LOG_G] = c[5];
+      td[SRW_TDIAG_INT_MAX] = imax;
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -1608,6 +1698,13 @@ hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
   fp.exp_scale = f.exp_scale;
   // split groups per workgroup from the splits per chunk
   const int ng = f.spc >= 64 ? 16 : (f.spc >= 16 ? 4 : 1);
+  if (ng == 1 && (f.D == 64 || f.D == 128 || f.D == 384)) {
+    const dim3 grid_r(static_cast<unsigned>((f.T + 3) / 4));
+    if (f.D == 64) hipLaunchKernelGGL(srw_finalize_rows_kernel<1>, grid_r, dim3(256), 0, s, fp);
+    else if (f.D == 128) hipLaunchKernelGGL(srw_finalize_rows_kernel<2>, grid_r, dim3(256), 0, s, fp);
+    else hipLaunchKernelGGL(srw_finalize_rows_kernel<6>, grid_r, dim3(256), 0, s, fp);
+    return hipGetLastError();
+  }
   const dim3 grid_f(static_cast<unsigned>(f.T), static_cast<unsigned>((f.D + 256 / ng - 1) / (256 / ng)));
   if (ng == 16) hipLaunchKernelGGL(srw_finalize_kernel<16>, grid_f, dim3(256), 0, s, fp);
   else if (ng == 4) hipLaunchKernelGGL(srw_finalize_kernel<4>, grid_f, dim3(256), 0, s, fp);
