@@ -173,7 +173,7 @@ struct Geometry {
 // never cross a reference chunk; tiles are globally 32-aligned, so a tile
 // that holds a chunk boundary is shared by two splits (each masks the other's
 // units).
-__device__ inline void split_range(const Geometry& g, int spc, int split, int& ta, int& tb, int64_t& lo,
+__host__ __device__ inline void split_range(const Geometry& g, int spc, int split, int& ta, int& tb, int64_t& lo,
                                    int64_t& hi) {
   const int c = split / spc, sub = split % spc;
   const int64_t c_lo = c * g.cs;
@@ -1143,6 +1143,8 @@ __global__ __launch_bounds__(256) void srw_tau_kernel(const float* __restrict__ 
   const int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   float a = 0.f, b = 0.f, c = 0.f, d = 0.f;
+  // unrolled so that the partials' loads go out together (the sums keep their order)
+#pragma unroll 8
   for (int s = lane; s < S_st; s += 64) {
     const float* m = mom + (static_cast<int64_t>(s) * T + t) * ms;
     a += m[0];
@@ -1255,12 +1257,15 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
   }
   for (int s0 = 0; s0 < p.S && !(NG == 1 && p.spc == 1); s0 += p.spc) {  // one reference chunk
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    int s = s0 + g;
-    for (; s + 7 * NG < s0 + p.spc; s += 8 * NG) {
+    // rounds of eight splits per thread, all eight loads in flight at once
+    // (predicated past the chunk's end)
+    for (int s = s0 + g; s < s0 + p.spc; s += 8 * NG) {
+      float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += col[(s + NG * j) * stride];
+      for (int j = 0; j < 8; ++j) v[j] = s + NG * j < s0 + p.spc ? col[(s + NG * j) * stride] : 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += v[j];
     }
-    for (; s < s0 + p.spc; s += NG) acc[0] += col[s * stride];
     const float sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
     if constexpr (NG == 1) {
       raw += round_bf16(sum);                                // bf16 dot output (v41:518)
@@ -1409,6 +1414,234 @@ __global__ __launch_bounds__(256) void srw_finalize_rows_kernel(FinalParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// decode: at most 128 virtual rows (T <= 128, or T <= 64 paired).  The pool is
+// streamed once: one workgroup per N-split of at most four 32-unit tiles, so
+// every CU holds one split's operands.  Wave w loads the E and R fragments of
+// tile ta + w and the W^T fragments of its D / 4 output columns over all the
+// split's tiles straight into registers -- every load of the workgroup, the
+// rows' thresholds included, is issued before any arithmetic -- while X and
+// H (per virtual row) arrive in LDS.  Then wave w runs the score and read
+// GEMMs of its tile for all rows (rows = columns of the transposed GEMMs),
+// the gate epilogue, and hands P to LDS (over X, after a barrier); finally
+// each wave runs the write GEMM of its columns over the split's tiles.  The
+// per-row sums of the four tiles are combined in LDS in wave order.
+// ---------------------------------------------------------------------------
+constexpr int kDecTiles = 4;    // tiles per split (one per wave)
+constexpr int kDecMaxRows = 128;
+
+template <int TB, int DB, int KH>
+constexpr int decode_lds_bytes() {
+  return TB * (DB * 2 + KH) * kFragBytes + 4 * TB * 32 * 3 * 4;
+}
+
+template <int TB, int DB, int KH>
+__global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  constexpr int D = DB * 32, DR = KH * 16, KX = D / 16, NDB = DB / 4;
+  constexpr int FX = TB * KX, FH = TB * KH;
+  static_assert(DB % 4 == 0, "four waves split the output column blocks");
+  static_assert(FX % 4 == 0 && FH % 4 == 0, "fragments split evenly over the waves");
+  static_assert(FX >= kDecTiles * TB * 2, "P reuses the X region");
+  char* const xl = lds;                          // X fragments, later P
+  char* const hl = lds + FX * kFragBytes;        // H fragments
+  float* const red = reinterpret_cast<float*>(hl + FH * kFragBytes);  // [wave][TB][32][3]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = lane >> 5, col = lane & 31;
+  const int split = blockIdx.x;
+  int ta, tb;
+  int64_t lo, hi;
+  split_range(p.g, p.g.spc, split, ta, tb, lo, hi);
+  const int64_t Tv = p.g.T, N = p.g.N;
+  const int R = p.routes;
+
+  // X and H fragments of every 32-row block: fragment (block, k-step) is one
+  // KB, lane l's 16 bytes at 16 l (rows past Tv repeat the last row)
+#pragma unroll
+  for (int q = 0; q < FX / 4; ++q) {
+    const int f = wave + 4 * q, blk = f / KX, ks = f % KX;
+    int64_t v = 32 * blk + col;
+    v = v < Tv ? v : Tv - 1;
+    g2lds16(p.x + (v / R) * D + 16 * ks + 8 * half, xl + f * kFragBytes);
+  }
+#pragma unroll
+  for (int q = 0; q < FH / 4; ++q) {
+    const int f = wave + 4 * q, blk = f / KH, ks = f % KH;
+    int64_t v = 32 * blk + col;
+    v = v < Tv ? v : Tv - 1;
+    g2lds16(p.h + v * DR + 16 * ks + 8 * half, hl + f * kFragBytes);
+  }
+  // this wave's tile (a missing one reloads the split's last tile, unused)
+  const bool have = ta + wave < tb;
+  const int mt = have ? ta + wave : tb - 1;
+  int64_t ur = static_cast<int64_t>(mt) * kUnitTile + col;
+  ur = ur < N ? ur : N - 1;
+  u32x4_t ef[KH], rf[KX];
+#pragma unroll
+  for (int ks = 0; ks < KH; ++ks) ef[ks] = *reinterpret_cast<const u32x4_t*>(p.emb + ur * DR + 16 * ks + 8 * half);
+#pragma unroll
+  for (int ks = 0; ks < KX; ++ks) rf[ks] = *reinterpret_cast<const u32x4_t*>(p.read + ur * D + 16 * ks + 8 * half);
+  // W^T fragments of column blocks wave * NDB + c, for the split's tiles
+  u32x4_t wf[kDecTiles][2][NDB];
+#pragma unroll
+  for (int i = 0; i < kDecTiles; ++i) {
+    const int ti = ta + i < tb ? ta + i : tb - 1;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int c = 0; c < NDB; ++c) {
+        const int db = wave * NDB + c;
+        wf[i][j][c] = *reinterpret_cast<const u32x4_t*>(p.wp + ((static_cast<int64_t>(ti) * DB + db) * 2 + j) * 512 +
+                                                         lane * 8);
+      }
+  }
+  // the rows' thresholds (srw_tau_kernel, v41:461-464)
+  float tau_b[TB];
+#pragma unroll
+  for (int b = 0; b < TB; ++b) {
+    const int64_t t = 32 * b + col;
+    tau_b[b] = p.tau[t < Tv ? t : Tv - 1];
+  }
+  wait_vm0();
+  __syncthreads();
+
+  // score and read GEMMs of this wave's tile for every row block, gate epilogue
+  const GateParams gp = p.gp;
+  const int64_t u0 = static_cast<int64_t>(mt) * kUnitTile;
+  const bool shared_tile = (u0 < lo) || (u0 + kUnitTile > hi && hi < N);
+  uint32_t pk[TB][8];
+  float gsum[TB], isum[TB];
+  uint32_t nact[TB];
+#pragma unroll
+  for (int b = 0; b < TB; ++b) {
+    gsum[b] = 0.f;
+    isum[b] = 0.f;
+    nact[b] = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) pk[b][q] = 0;
+  }
+  if (have) {
+#pragma unroll
+    for (int b = 0; b < TB; ++b) {
+      f32x16_t sacc = {}, racc = {};
+#pragma unroll
+      for (int ks = 0; ks < KH; ++ks)
+        sacc = mfma(ef[ks], *reinterpret_cast<const u32x4_t*>(hl + (b * KH + ks) * kFragBytes + lane * 16), sacc);
+#pragma unroll
+      for (int ks = 0; ks < KX; ++ks)
+        racc = mfma(rf[ks], *reinterpret_cast<const u32x4_t*>(xl + (b * KX + ks) * kFragBytes + lane * 16), racc);
+      const int64_t t = 32 * b + col;
+      const float tau = tau_b[b];
+      uint32_t bits = 0;
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const uint32_t sp = pack_bf16(sacc[v], sacc[v + 1]);   // bf16 scores (v41:503)
+        const uint32_t xp = pack_bf16(racc[v], racc[v + 1]);   // bf16 x.r (v41:517)
+        float g2[2], in2[2];
+        bool on2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float sv = e ? hi_f32(sp) : lo_f32(sp);
+          const float raw = sv - tau;
+          const float margin = raw - gp.thr;
+          const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(margin * p.exp_scale));
+          const float am = fmaxf(margin - gp.cut, 0.0f);
+          const int64_t u = u0 + unit_of_acc(v + e, half);
+          const bool ok = u >= lo && u < hi;
+          g2[e] = ok ? act * (gp.eps + fminf(am, gp.maxi)) : 0.f;
+          in2[e] = ok ? gp.eps + fminf(am, gp.maxi) : 0.f;
+          on2[e] = ok && act > 0.5f;
+        }
+        gsum[b] += g2[0];
+        gsum[b] += g2[1];
+        isum[b] += in2[0];
+        isum[b] += in2[1];
+        bits = (bits << 2) | (on2[0] ? 2u : 0u) | (on2[1] ? 1u : 0u);
+        const uint32_t gq = pack_bf16(g2[0], g2[1]);             // gate_bf (v41:516)
+        pk[b][v >> 1] = pack_bf16(lo_f32(gq) * lo_f32(xp), hi_f32(gq) * hi_f32(xp));  // (v41:518)
+      }
+      // pass bits of (row, tile): element v at bit unit_of_acc(v, half)
+      const uint32_t br = __builtin_bitreverse32(bits) >> 16;
+      uint32_t m = (br & 0xFu) | ((br & 0xF0u) << 4) | ((br & 0xF00u) << 8) | ((br & 0xF000u) << 12);
+      m <<= 4 * half;
+      nact[b] = __builtin_popcount(m);
+      m |= __shfl_xor(m, 32);
+      if (p.mask32 && half == 0 && t < Tv) {
+        uint32_t* dst = p.mask32 + t * p.mask_words32 + mt;
+        if (shared_tile) atomicOr(dst, m);
+        else *dst = m;
+      }
+    }
+  }
+  // per-row sums of this tile (both lane halves) into LDS
+#pragma unroll
+  for (int b = 0; b < TB; ++b) {
+    const float g = gsum[b] + __shfl_xor(gsum[b], 32);
+    const float in = isum[b] + __shfl_xor(isum[b], 32);
+    const uint32_t na = nact[b] + __shfl_xor(nact[b], 32);
+    if (half == 0) {
+      float* r = red + ((wave * TB + b) * 32 + col) * 3;
+      r[0] = g;
+      r[1] = in;
+      r[2] = static_cast<float>(na);
+    }
+  }
+  __syncthreads();  // every wave is done reading X
+  // P of (tile wave, block b, k-step j) over X: lane l's 16 bytes at 16 l
+#pragma unroll
+  for (int b = 0; b < TB; ++b)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<u32x4_t*>(xl + ((wave * TB + b) * 2 + j) * kFragBytes + lane * 16) =
+          u32x4_t{pk[b][4 * j], pk[b][4 * j + 1], pk[b][4 * j + 2], pk[b][4 * j + 3]};
+  __syncthreads();
+
+  // write GEMM: OUT[rows x 32 (wave NDB + c) .. ] over the split's tiles
+  f32x16_t oacc[TB][NDB];
+#pragma unroll
+  for (int b = 0; b < TB; ++b)
+#pragma unroll
+    for (int c = 0; c < NDB; ++c) oacc[b][c] = f32x16_t{};
+  const int ntl = tb - ta;
+#pragma unroll
+  for (int i = 0; i < kDecTiles; ++i) {
+    if (i < ntl) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int b = 0; b < TB; ++b) {
+          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xl + ((i * TB + b) * 2 + j) * kFragBytes + lane * 16);
+#pragma unroll
+          for (int c = 0; c < NDB; ++c) oacc[b][c] = mfma(a, wf[i][j][c], oacc[b][c]);
+        }
+    }
+  }
+  float* op = p.out_part + static_cast<int64_t>(split) * Tv * D;
+#pragma unroll
+  for (int b = 0; b < TB; ++b)
+#pragma unroll
+    for (int c = 0; c < NDB; ++c)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t t = 32 * b + unit_of_acc(v, half);
+        if (t < Tv) op[t * D + 32 * (wave * NDB + c) + col] = oacc[b][c][v];
+      }
+  // per-row partials of the split: the four tiles in wave order
+  for (int r = threadIdx.x; r < TB * 32 && r < Tv; r += 256) {
+    const int b = r / 32, c = r % 32;
+    float acc[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kDecTiles; ++w)
+#pragma unroll
+      for (int k = 0; k < 3; ++k) acc[k] += red[((w * TB + b) * 32 + c) * 3 + k];
+    float* tp = p.tok_part + (static_cast<int64_t>(split) * Tv + r) * 4;
+    tp[0] = acc[0];
+    tp[1] = acc[1];
+    tp[2] = acc[2];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 struct Kernels {
@@ -1458,6 +1691,44 @@ bool pick(int64_t D, int64_t dr, bool hx, bool dg, Kernels* k) {
 }
 
 bool with_diag(const srw_desc_t& d) { return (d.flags & SRW_FLAG_DIAG) != 0; }
+
+// The decode kernel serves calls of at most 128 virtual rows without
+// diagnostics, for the (d_model, d_route) pairs below.
+bool decode_applies(const srw_desc_t& d) {
+  const int64_t Tv = d.T * d.n_routes;
+  if (with_diag(d) || Tv < 1 || Tv > kDecMaxRows) return false;
+  return (d.d_model == 384 && d.d_route == 128) || (d.d_model == 128 && (d.d_route == 128 || d.d_route == 64));
+}
+
+typedef void (*MainFn)(MainParams);
+template <int DB, int KH>
+void decode_for_rows(int64_t Tv, MainFn* fn, int* lds) {
+  if (Tv <= 32) {
+    *fn = srw_decode_kernel<1, DB, KH>;
+    *lds = decode_lds_bytes<1, DB, KH>();
+  } else if (Tv <= 64) {
+    *fn = srw_decode_kernel<2, DB, KH>;
+    *lds = decode_lds_bytes<2, DB, KH>();
+  } else {
+    *fn = srw_decode_kernel<4, DB, KH>;
+    *lds = decode_lds_bytes<4, DB, KH>();
+  }
+}
+bool pick_decode(int64_t Tv, int D, int dr, MainFn* fn, int* lds) {
+  if (D == 384 && dr == 128) {
+    decode_for_rows<12, 8>(Tv, fn, lds);
+    return true;
+  }
+  if (D == 128 && dr == 128) {
+    decode_for_rows<4, 8>(Tv, fn, lds);
+    return true;
+  }
+  if (D == 128 && dr == 64) {
+    decode_for_rows<4, 4>(Tv, fn, lds);
+    return true;
+  }
+  return false;
+}
 int mom_stride(const srw_desc_t& d) { return with_diag(d) && d.stats_mode == SRW_STATS_ONEPASS ? 4 : 2; }
 int tok_part_stride(const srw_desc_t& d) { return with_diag(d) ? kTokPartDiag : 4; }
 
@@ -1475,16 +1746,42 @@ Geometry geometry(const srw_desc_t& d, int64_t chunk) {
   int spc = static_cast<int>((kTargetBlocks + g.TT * g.nc - 1) / (g.TT * g.nc));
   if (spc < 1) spc = 1;
   if (spc > min_tiles) spc = static_cast<int>(min_tiles > 0 ? min_tiles : 1);
+  if (decode_applies(d)) {
+    // decode: splits of at most kDecTiles tiles, as few as fill the CUs
+    int64_t tpw = (g.ntiles + kTargetBlocks - 1) / kTargetBlocks;
+    tpw = tpw < 1 ? 1 : (tpw > kDecTiles ? kDecTiles : tpw);
+    int64_t nt_max = 0;
+    for (int c = 0; c < g.nc; ++c) {
+      const int64_t c_lo = c * g.cs, c_hi = (c + 1) * g.cs < g.N ? (c + 1) * g.cs : g.N;
+      const int64_t nt = (c_hi + kUnitTile - 1) / kUnitTile - c_lo / kUnitTile;
+      nt_max = nt > nt_max ? nt : nt_max;
+    }
+    const int64_t sd = (nt_max + tpw - 1) / tpw;
+    const int64_t mt = min_tiles > 0 ? min_tiles : 1;
+    spc = static_cast<int>(sd < mt ? sd : mt);
+  }
   g.spc = spc;
   g.S = g.nc * spc;
   g.TT_st = g.TT;  // the moments kernel uses the main kernel's token tiles, two workgroups per CU
   int spc_st = static_cast<int>((2 * kTargetBlocks + g.TT_st * g.nc - 1) / (g.TT_st * g.nc));
+  if (decode_applies(d)) spc_st = spc;  // one row tile: fewer, longer moment splits (fewer partials per row)
   if (spc_st < 1) spc_st = 1;
   if (spc_st > min_tiles) spc_st = static_cast<int>(min_tiles > 0 ? min_tiles : 1);
   g.spc_st = spc_st;
   g.S_st = g.nc * spc_st;
   if (d.stats_mode == SRW_STATS_GRAM) g.S_st = gram_moment_parts(d.d_route);  // moments from the Gram kernels
   return g;
+}
+
+// Every split of the decode kernel holds 1 .. kDecTiles tiles.
+bool decode_splits_fit(const Geometry& g) {
+  for (int sp = 0; sp < g.S; ++sp) {
+    int ta, tb;
+    int64_t lo, hi;
+    split_range(g, g.spc, sp, ta, tb, lo, hi);
+    if (tb <= ta || tb - ta > kDecTiles) return false;
+  }
+  return true;
 }
 
 struct WsLayout {
@@ -1639,14 +1936,30 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     mp.g = g;
     mp.gp = a.gp;
     mp.exp_scale = -d.sharpness * 1.4426950408889634f;
-    const size_t smem = static_cast<size_t>(k.main_lds);
-    if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(k.main),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem))) != hipSuccess)
-      return e;
-    dominant_kernel_begin(a.stream);
-    hipLaunchKernelGGL(k.main, dim3(grid), dim3(k.main_threads), smem, a.stream, mp);
-    dominant_kernel_end(a.stream);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    MainFn dec = nullptr;
+    int dec_lds = 0;
+    if (decode_applies(d) && pick_decode(g.T, D, static_cast<int>(d.d_route), &dec, &dec_lds) &&
+        decode_splits_fit(g)) {
+      *path_name = "mfma_decode_bf16";
+      if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(dec), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   dec_lds)) != hipSuccess)
+        return e;
+      dominant_kernel_begin(a.stream);
+      hipLaunchKernelGGL(dec, dim3(static_cast<unsigned>(g.S)), dim3(kThreads), static_cast<size_t>(dec_lds),
+                         a.stream, mp);
+      dominant_kernel_end(a.stream);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    } else {
+      const size_t smem = static_cast<size_t>(k.main_lds);
+      if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(k.main),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem))) !=
+          hipSuccess)
+        return e;
+      dominant_kernel_begin(a.stream);
+      hipLaunchKernelGGL(k.main, dim3(grid), dim3(k.main_threads), smem, a.stream, mp);
+      dominant_kernel_end(a.stream);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
   }
   // finalize
   FinalizeArgs f{};
