@@ -50,6 +50,9 @@ WORKLOADS = {
     "qk": ("qk", 12500, "configs[1] QK pool, paired routes sharing one x.R^T"),
     "decode_know": ("decode_know", 12500, "configs[3] decode-shaped Know pool, T=64, 3% pass"),
     "scaled": ("scaled", 12500, "configs[4] scaled Know pool d=1024 N=100000 T=16384, 2% pass"),
+    # a whole decode step (its own branch below): 12 layers x (QK paired, V, Know) at T = 64
+    "decode": (None, 12500, "configs[3] decode step: 64 single-token rows through the QK (paired), V and "
+                            "Know pools for 12 layers, Know calibrated to 3% pass"),
     # the whole model (its own branch below): 12 layers, B = 32, S = 512, vocab 32 000
     "model": (None, 12500, "configs[2] full 12-layer DAWN-SRW 40M prefill forward (logits), the SRW "
                            "kernels timed inside it"),
@@ -117,6 +120,119 @@ def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: b
             "sample": (f"oracle {what} bf16 emulation, first {T_s} of the "
                        f"{shape.T} tokens, full pool N={shape.N}, median of {len(times)} "
                        f"runs; {cpu_model()}")}
+
+
+DECODE_LAYERS = 12
+
+
+def bench_decode(args, pkg, C, dev) -> dict:
+    """one decode step = 12 layers x three SRW calls (the QK pool
+    with its paired routes, V, Know) on 64 rows, the pools shared by the
+    layers (v41:1393-1394), router h = x W + b with d_route 128, the Know
+    tau_offset calibrated to ~3 % pass.  Captured once as a HIP graph and
+    replayed.  The dominant kernel is the Know pool's decode kernel (timed by
+    an eager call after the replays)."""
+    import torch
+    bf = torch.bfloat16
+    plans, shapes = [], []
+    for key in ("decode_qk", "decode_v", "decode_know"):
+        shape = pkg.inputs.CONFIGS[key]
+        inp = pkg.inputs.make_pool_inputs(shape, seed=args.seed)
+        if shape.pass_target is not None:
+            inp["tau_offset"].fill_(pkg.inputs.calibrate_tau_offset(inp, shape.pass_target))
+        _, cs = pkg.chunk_plan(shape.N, 12500)
+        plan = pkg.SrwPlan(inp["x"].to(bf).to(dev), inp["h"].to(bf).to(dev), inp["emb"].to(bf).to(dev),
+                           inp["tau_offset"].to(dev), inp["read"].to(bf).to(dev), inp["write"].to(bf).to(dev),
+                           stats=args.stats, chunk_size=cs, want_mask=True)
+        plans.append(plan)
+        shapes.append(shape)
+    stream = torch.cuda.current_stream(dev)
+    for pl in plans:
+        pl.launch(stream)
+    torch.cuda.synchronize()
+    log("decode paths: " + ", ".join(f"{s_.note.split(':')[1].strip()} -> {pl.path}"
+                                     for s_, pl in zip(shapes, plans)))
+
+    def step(st):
+        for _ in range(DECODE_LAYERS):
+            for pl in plans:
+                pl.launch(st, pool_cached=True)
+
+    cap = torch.cuda.Stream(dev)
+    cap.wait_stream(stream)
+    with torch.cuda.stream(cap):
+        step(cap)
+    stream.wait_stream(cap)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        step(cap)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    K = args.steps
+    t_begin = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    t_begin.record(stream)
+    for _ in range(K):
+        graph.replay()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    step_ms = t_begin.elapsed_time(t_end) / K
+    # the Know decode kernel alone, eagerly
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
+    for a, b in ev:
+        a.record(stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    for a, b in ev:
+        C.set_kernel_events(a.cuda_event, b.cuda_event)
+        plans[2].launch(stream, pool_cached=True)
+    torch.cuda.synchronize()
+    C.set_kernel_events(None, None)
+    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    pool_bytes = [s_.N * (s_.dr + 2 * s_.D) * 2 for s_ in shapes]
+    step_bytes = DECODE_LAYERS * sum(pool_bytes)
+    log(f"timed {K} decode steps ({DECODE_LAYERS} layers x 3 pools): {step_ms:.4f} ms/step, "
+        f"Know kernel {kern_ms:.4f} ms, pool stream {step_bytes / (step_ms * 1e-3) / 1e9:.0f} GB/s")
+    achieved = pool_bytes[2] / (kern_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4),
+                "traffic": None, "kernel": plans[2].path, "kernel_ms": round(kern_ms, 5),
+                "algorithmic_bytes": pool_bytes[2],
+                "step_pool_bytes": step_bytes,
+                "step_gbs": round(step_bytes / (step_ms * 1e-3) / 1e9, 1)}
+    cpu = None
+    if args.cpu_seconds > 0:
+        from oracle import srw_ref
+        torch.set_num_threads(min(os.cpu_count() or 1, 16))
+        t0 = time.perf_counter()
+        for pl, s_ in zip(plans, shapes):
+            x, h, emb, tau, read, write = (t.float().cpu() for t in pl.inputs)
+            if s_.routes == 2:
+                srw_ref.fused_gate_srw_paired(x[None], h[None], emb, tau.reshape(1, s_.T, 2, 1), read, write,
+                                              max_chunk_size=12500)
+            else:
+                srw_ref.fused_gate_srw(x[None], h[:, 0][None], emb, tau[None], read, write, max_chunk_size=12500)
+        layer_s = time.perf_counter() - t0
+        log(f"cpu baseline: one layer (3 pools, 64 rows) {layer_s:.2f} s")
+        cpu = {"value": 64 / (layer_s * DECODE_LAYERS), "unit": "tokens/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": (f"oracle fused_gate_srw / _paired (bf16 emulation) of one of the {DECODE_LAYERS} layers "
+                          f"(QK, V, Know at 64 rows), scaled to {DECODE_LAYERS} layers; {cpu_model()}")}
+    return {
+        "metric": METRIC, "value": round(64 / (step_ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": K, "warmup": args.warmup, "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x RMS-normalised; router h = x W + b; E, R, W unit rows)",
+        "config": {"workload": "decode", "note": WORKLOADS["decode"][2], "T": 64, "layers": DECODE_LAYERS,
+                   "pools": {s_.note.split(":")[1].strip(): s_.N for s_ in shapes}, "d_model": 384,
+                   "d_route": 128, "stats": args.stats, "graph": True, "pool_cached": True,
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
 
 
 def bench_model(args, pkg, C, dev) -> dict:
@@ -254,6 +370,12 @@ def main() -> int:
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.workload == "decode":
+        if args.backward or args.diag or args.tiled:
+            print("bench.py: --workload decode times the forward decode step", file=sys.stderr)
+            return 2
+        print(json.dumps(bench_decode(args, pkg, C, dev)), flush=True)
+        return 0
     if args.workload == "model":
         if args.backward or args.graph or args.diag or args.tiled or args.stats != "onepass":
             print("bench.py: --workload model times the plain forward", file=sys.stderr)
@@ -387,6 +509,15 @@ def main() -> int:
                 "traffic": traffic, "kernel": path,
                 "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops,
                 "step_tflops": round(flops / (step_ms * 1e-3) / 1e12, 2)}
+    if args.workload.startswith("decode_") and not args.backward:
+        # decode shapes are pool-read bound: the algorithmic bytes are the pool
+        # (E, R, W rows) streamed once per call
+        pool_bytes = N * (dr + 2 * D) * 2
+        gbs = pool_bytes / (kern_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": path,
+                    "kernel_ms": round(kern_ms, 5), "algorithmic_bytes": pool_bytes,
+                    "step_gbs": round(pool_bytes / (step_ms * 1e-3) / 1e9, 1)}
 
     cpu = None
     if args.cpu_seconds > 0:

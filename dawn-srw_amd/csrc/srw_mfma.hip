@@ -392,6 +392,7 @@ struct MainParams {
   Geometry g;
   GateParams gp;
   float exp_scale;       // -sharpness * log2(e)
+  int rb;                // decode kernel: row-block groups per split (workgroup = split * rb + group)
 };
 
 // v4.1 gate of a margin m = s - tau - thr (v41:503-511), with the kernels' operations
@@ -1448,32 +1449,40 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = lane >> 5, col = lane & 31;
-  const int split = blockIdx.x;
+  // workgroup = (split, row-block group): with rb > 1 (TB == 1) each
+  // workgroup of a split takes one 32-row block, rows from row0
+  const int split = blockIdx.x / p.rb;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x % p.rb) * 32 * TB;
   int ta, tb;
   int64_t lo, hi;
   split_range(p.g, p.g.spc, split, ta, tb, lo, hi);
   const int64_t Tv = p.g.T, N = p.g.N;
   const int R = p.routes;
 
-  // X and H fragments of every 32-row block: fragment (block, k-step) is one
-  // KB, lane l's 16 bytes at 16 l (rows past Tv repeat the last row)
+  // X and H fragments of this workgroup's 32-row blocks: fragment (block,
+  // k-step) is one KB, lane l's 16 bytes at 16 l (rows past Tv repeat the last)
 #pragma unroll
   for (int q = 0; q < FX / 4; ++q) {
     const int f = wave + 4 * q, blk = f / KX, ks = f % KX;
-    int64_t v = 32 * blk + col;
+    int64_t v = row0 + 32 * blk + col;
     v = v < Tv ? v : Tv - 1;
     g2lds16(p.x + (v / R) * D + 16 * ks + 8 * half, xl + f * kFragBytes);
   }
 #pragma unroll
   for (int q = 0; q < FH / 4; ++q) {
     const int f = wave + 4 * q, blk = f / KH, ks = f % KH;
-    int64_t v = 32 * blk + col;
+    int64_t v = row0 + 32 * blk + col;
     v = v < Tv ? v : Tv - 1;
     g2lds16(p.h + v * DR + 16 * ks + 8 * half, hl + f * kFragBytes);
   }
-  // this wave's tile (a missing one reloads the split's last tile, unused)
-  const bool have = ta + wave < tb;
-  const int mt = have ? ta + wave : tb - 1;
+  // this wave's tile and row blocks: with fewer than four tiles the waves of
+  // a tile take its row blocks in turn (wpt waves per tile); a wave without
+  // work reloads the split's last tile, unused
+  const int ntl = tb - ta;
+  const int wpt = ntl == 1 ? 4 : (ntl == 2 ? 2 : 1);
+  const int wi = wave / wpt, wb = wave % wpt;
+  const bool have = wi < ntl && wb < TB;
+  const int mt = have ? ta + wi : tb - 1;
   int64_t ur = static_cast<int64_t>(mt) * kUnitTile + col;
   ur = ur < N ? ur : N - 1;
   u32x4_t ef[KH], rf[KX];
@@ -1485,21 +1494,22 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
   u32x4_t wf[kDecTiles][2][NDB];
 #pragma unroll
   for (int i = 0; i < kDecTiles; ++i) {
-    const int ti = ta + i < tb ? ta + i : tb - 1;
+    if (i < ntl) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int c = 0; c < NDB; ++c) {
-        const int db = wave * NDB + c;
-        wf[i][j][c] = *reinterpret_cast<const u32x4_t*>(p.wp + ((static_cast<int64_t>(ti) * DB + db) * 2 + j) * 512 +
-                                                         lane * 8);
-      }
+        for (int c = 0; c < NDB; ++c) {
+          const int db = wave * NDB + c;
+          wf[i][j][c] = *reinterpret_cast<const u32x4_t*>(
+              p.wp + ((static_cast<int64_t>(ta + i) * DB + db) * 2 + j) * 512 + lane * 8);
+        }
+    }
   }
   // the rows' thresholds (srw_tau_kernel, v41:461-464)
   float tau_b[TB];
 #pragma unroll
   for (int b = 0; b < TB; ++b) {
-    const int64_t t = 32 * b + col;
+    const int64_t t = row0 + 32 * b + col;
     tau_b[b] = p.tau[t < Tv ? t : Tv - 1];
   }
   wait_vm0();
@@ -1523,6 +1533,7 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
   if (have) {
 #pragma unroll
     for (int b = 0; b < TB; ++b) {
+      if (b % wpt != wb) continue;
       f32x16_t sacc = {}, racc = {};
 #pragma unroll
       for (int ks = 0; ks < KH; ++ks)
@@ -1530,7 +1541,7 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
 #pragma unroll
       for (int ks = 0; ks < KX; ++ks)
         racc = mfma(rf[ks], *reinterpret_cast<const u32x4_t*>(xl + (b * KX + ks) * kFragBytes + lane * 16), racc);
-      const int64_t t = 32 * b + col;
+      const int64_t t = row0 + 32 * b + col;
       const float tau = tau_b[b];
       uint32_t bits = 0;
 #pragma unroll
@@ -1573,27 +1584,34 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
       }
     }
   }
-  // per-row sums of this tile (both lane halves) into LDS
+  // per-row sums of each (tile, row block) this wave computed, into LDS
+  if (have) {
 #pragma unroll
-  for (int b = 0; b < TB; ++b) {
-    const float g = gsum[b] + __shfl_xor(gsum[b], 32);
-    const float in = isum[b] + __shfl_xor(isum[b], 32);
-    const uint32_t na = nact[b] + __shfl_xor(nact[b], 32);
-    if (half == 0) {
-      float* r = red + ((wave * TB + b) * 32 + col) * 3;
-      r[0] = g;
-      r[1] = in;
-      r[2] = static_cast<float>(na);
+    for (int b = 0; b < TB; ++b) {
+      if (b % wpt != wb) continue;
+      const float g = gsum[b] + __shfl_xor(gsum[b], 32);
+      const float in = isum[b] + __shfl_xor(isum[b], 32);
+      const uint32_t na = nact[b] + __shfl_xor(nact[b], 32);
+      if (half == 0) {
+        float* r = red + ((wi * TB + b) * 32 + col) * 3;
+        r[0] = g;
+        r[1] = in;
+        r[2] = static_cast<float>(na);
+      }
     }
   }
   __syncthreads();  // every wave is done reading X
-  // P of (tile wave, block b, k-step j) over X: lane l's 16 bytes at 16 l
+  // P of (tile wi, block b, k-step j) over X: lane l's 16 bytes at 16 l
+  if (have) {
 #pragma unroll
-  for (int b = 0; b < TB; ++b)
+    for (int b = 0; b < TB; ++b) {
+      if (b % wpt != wb) continue;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      *reinterpret_cast<u32x4_t*>(xl + ((wave * TB + b) * 2 + j) * kFragBytes + lane * 16) =
-          u32x4_t{pk[b][4 * j], pk[b][4 * j + 1], pk[b][4 * j + 2], pk[b][4 * j + 3]};
+      for (int j = 0; j < 2; ++j)
+        *reinterpret_cast<u32x4_t*>(xl + ((wi * TB + b) * 2 + j) * kFragBytes + lane * 16) =
+            u32x4_t{pk[b][4 * j], pk[b][4 * j + 1], pk[b][4 * j + 2], pk[b][4 * j + 3]};
+    }
+  }
   __syncthreads();
 
   // write GEMM: OUT[rows x 32 (wave NDB + c) .. ] over the split's tiles
@@ -1602,7 +1620,6 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
   for (int b = 0; b < TB; ++b)
 #pragma unroll
     for (int c = 0; c < NDB; ++c) oacc[b][c] = f32x16_t{};
-  const int ntl = tb - ta;
 #pragma unroll
   for (int i = 0; i < kDecTiles; ++i) {
     if (i < ntl) {
@@ -1623,18 +1640,17 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
     for (int c = 0; c < NDB; ++c)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int64_t t = 32 * b + unit_of_acc(v, half);
+        const int64_t t = row0 + 32 * b + unit_of_acc(v, half);
         if (t < Tv) op[t * D + 32 * (wave * NDB + c) + col] = oacc[b][c][v];
       }
-  // per-row partials of the split: the four tiles in wave order
-  for (int r = threadIdx.x; r < TB * 32 && r < Tv; r += 256) {
+  // per-row partials of the split: its tiles in order
+  for (int r = threadIdx.x; r < TB * 32 && row0 + r < Tv; r += 256) {
     const int b = r / 32, c = r % 32;
     float acc[3] = {0.f, 0.f, 0.f};
+    for (int i = 0; i < ntl; ++i)
 #pragma unroll
-    for (int w = 0; w < kDecTiles; ++w)
-#pragma unroll
-      for (int k = 0; k < 3; ++k) acc[k] += red[((w * TB + b) * 32 + c) * 3 + k];
-    float* tp = p.tok_part + (static_cast<int64_t>(split) * Tv + r) * 4;
+      for (int k = 0; k < 3; ++k) acc[k] += red[((i * TB + b) * 32 + c) * 3 + k];
+    float* tp = p.tok_part + (static_cast<int64_t>(split) * Tv + row0 + r) * 4;
     tp[0] = acc[0];
     tp[1] = acc[1];
     tp[2] = acc[2];
@@ -1936,16 +1952,21 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     mp.g = g;
     mp.gp = a.gp;
     mp.exp_scale = -d.sharpness * 1.4426950408889634f;
+    mp.rb = 1;
     MainFn dec = nullptr;
     int dec_lds = 0;
-    if (decode_applies(d) && pick_decode(g.T, D, static_cast<int>(d.d_route), &dec, &dec_lds) &&
+    // few splits (small pools): one workgroup per (split, 32-row block), so
+    // that more CUs share the pool and each loads only its rows' X and H
+    const int row_blocks = static_cast<int>((g.T + 31) / 32);
+    mp.rb = (row_blocks > 1 && static_cast<int64_t>(g.S) * row_blocks <= kTargetBlocks) ? row_blocks : 1;
+    if (decode_applies(d) && pick_decode(mp.rb > 1 ? 32 : g.T, D, static_cast<int>(d.d_route), &dec, &dec_lds) &&
         decode_splits_fit(g)) {
       *path_name = "mfma_decode_bf16";
       if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(dec), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    dec_lds)) != hipSuccess)
         return e;
       dominant_kernel_begin(a.stream);
-      hipLaunchKernelGGL(dec, dim3(static_cast<unsigned>(g.S)), dim3(kThreads), static_cast<size_t>(dec_lds),
+      hipLaunchKernelGGL(dec, dim3(static_cast<unsigned>(g.S * mp.rb)), dim3(kThreads), static_cast<size_t>(dec_lds),
                          a.stream, mp);
       dominant_kernel_end(a.stream);
       if ((e = hipGetLastError()) != hipSuccess) return e;
