@@ -41,6 +41,8 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 # has the runs.
 MEASURED_TRAFFIC = {
     ("know", "onepass", "mfma_bf16"): (41148 * 2.0 + 64190 * 1.0) * 1024,
+    # profiles/decode_know_T64_N25200_kernel_stats.md
+    ("decode_know", "onepass", "mfma_decode_bf16"): (22575.2 * 2.0 + 19704.9 * 1.0) * 1024,
 }
 
 WORKLOADS = {
