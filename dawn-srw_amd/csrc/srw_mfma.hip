@@ -237,7 +237,10 @@ struct StatsParams {
 // s, sum (s - mean)^2 with the row means of a first pass (_srw_inference's
 // two-pass std, v41:1719-1721).
 constexpr int kStatsPlain = 0, kStatsDiag = 1, kStatsCentered = 2;
-template <int KH, int MODE>
+// TBW 32-token blocks per wave (128 TBW tokens per workgroup): each E
+// fragment read from LDS feeds TBW MFMAs, and a CU's E stream serves
+// 128 TBW tokens.
+template <int KH, int MODE, int TBW>
 __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
   constexpr bool DG = MODE == kStatsDiag;
   constexpr int MS = DG ? 4 : 2;
@@ -249,8 +252,12 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
   const int half = lane >> 5, col = lane & 31;
   const int split = blockIdx.x % p.g.S_st;
   const int ttile = blockIdx.x / p.g.S_st;
-  const int64_t t = static_cast<int64_t>(ttile) * kTokTile + 32 * wave + col;
-  const int64_t tl = t < p.g.T ? t : p.g.T - 1;
+  int64_t tt[TBW], tl[TBW];
+#pragma unroll
+  for (int b = 0; b < TBW; ++b) {
+    tt[b] = static_cast<int64_t>(ttile) * kTokTile * TBW + 32 * (TBW * wave + b) + col;
+    tl[b] = tt[b] < p.g.T ? tt[b] : p.g.T - 1;
+  }
   int ta, tb;
   int64_t lo, hi;
   split_range(p.g, p.g.spc_st, split, ta, tb, lo, hi);
@@ -259,18 +266,26 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
   // tile) and the unused upper half of the last 64-bit word; the main kernel
   // ORs into the former and never writes the latter.
   if (p.mask32 && split == 0) {
-    for (int c = 1; c < p.g.nc; ++c) {
-      const int64_t b = c * p.g.cs;
-      if (b % kUnitTile && half == 0 && t < p.g.T) p.mask32[t * p.mask_words32 + b / kUnitTile] = 0u;
+#pragma unroll
+    for (int b = 0; b < TBW; ++b) {
+      const int64_t t = tt[b];
+      for (int c = 1; c < p.g.nc; ++c) {
+        const int64_t bd = c * p.g.cs;
+        if (bd % kUnitTile && half == 0 && t < p.g.T) p.mask32[t * p.mask_words32 + bd / kUnitTile] = 0u;
+      }
+      if ((p.g.ntiles & 1) && half == 0 && t < p.g.T) p.mask32[t * p.mask_words32 + p.g.ntiles] = 0u;
     }
-    if ((p.g.ntiles & 1) && half == 0 && t < p.g.T) p.mask32[t * p.mask_words32 + p.g.ntiles] = 0u;
   }
 
-  u32x4_t hq[KH];
+  u32x4_t hq[TBW][KH];
+  float mu[TBW];
 #pragma unroll
-  for (int ks = 0; ks < KH; ++ks)
-    hq[ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl * DR + 16 * ks + 8 * half);
-  const float mu = MODE == kStatsCentered ? p.mean[tl] : 0.f;
+  for (int b = 0; b < TBW; ++b) {
+#pragma unroll
+    for (int ks = 0; ks < KH; ++ks)
+      hq[b][ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl[b] * DR + 16 * ks + 8 * half);
+    mu[b] = MODE == kStatsCentered ? p.mean[tl[b]] : 0.f;
+  }
 
   using TileE = RowTile<KH>;
   const uint32_t lsrc[2] = {TileE::lane_src(lane, 0), TileE::lane_src(lane, 1)};
@@ -282,7 +297,9 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
 #pragma unroll
   for (int m = 0; m < TileE::NM; ++m) le[m] = TileE::lane_off(lane, m);
 
-  float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
+  float s1[TBW], s2[TBW], s3[TBW], s4[TBW];
+#pragma unroll
+  for (int b = 0; b < TBW; ++b) s1[b] = s2[b] = s3[b] = s4[b] = 0.f;
   if (ta < tb) {
     issue(ta, 0);
     wait_vm0();
@@ -291,7 +308,9 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
   for (int tile = ta; tile < tb; ++tile) {
     const int st = (tile - ta) & 1;
     const bool pre = tile + 1 < tb;  // the next tile's loads go out between this one's MFMAs
-    f32x16_t acc = {};
+    f32x16_t acc[TBW];
+#pragma unroll
+    for (int b = 0; b < TBW; ++b) acc[b] = f32x16_t{};
     const char* base = lds + st * STAGE;
     auto frag = [&](int ks) {
       return *reinterpret_cast<const u32x4_t*>(base + le[ks % TileE::NM] + TileE::step_off(ks));
@@ -305,62 +324,69 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
     for (int ks = 0; ks < KH; ++ks) {
       const u32x4_t e = ef[ks % PF];
       if (ks + PF < KH) ef[ks % PF] = frag(ks + PF);
-      if (pre && (ks % 4) == 0 && wave + ks < KH)  // block wave + ks: this wave's share, every 4th MFMA
+      if (pre && (ks % 4) == 0 && wave + ks < KH)  // block wave + ks: this wave's share, every 4th k-step
         TileE::load(p.emb, static_cast<int64_t>(tile + 1) * kUnitTile, p.g.N, wave + ks, lane, lsrc,
                     lds + (st ^ 1) * STAGE);
-      acc = mfma(e, hq[ks], acc);
+#pragma unroll
+      for (int b = 0; b < TBW; ++b) acc[b] = mfma(e, hq[b][ks], acc[b]);
       __builtin_amdgcn_sched_barrier(0);
     }
     const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
     const bool full = u0 >= lo && u0 + kUnitTile <= hi;
 #pragma unroll
-    for (int v = 0; v < 16; v += 2) {
-      const uint32_t sp = pack_bf16(acc[v], acc[v + 1]);
-      float a = lo_f32(sp), b = hi_f32(sp);
-      bool oka = true, okb = true;
-      if (!full) {
-        const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
-        oka = ua >= lo && ua < hi;
-        okb = ub >= lo && ub < hi;
-        if (!oka) a = 0.f;
-        if (!okb) b = 0.f;
-      }
-      float a2, b2;  // squares, or squared deviations from the row mean (centred)
-      if constexpr (MODE == kStatsCentered) {
-        const float da = oka ? a - mu : 0.f, db = okb ? b - mu : 0.f;
-        a2 = __fmul_rn(da, da);
-        b2 = __fmul_rn(db, db);
-      } else {
-        a2 = __fmul_rn(a, a);
-        b2 = __fmul_rn(b, b);
-      }
-      s1 += a;
-      s2 += a2;
-      s1 += b;
-      s2 += b2;
-      if constexpr (DG) {
-        s3 += __fmul_rn(a2, a);
-        s4 += __fmul_rn(a2, a2);
-        s3 += __fmul_rn(b2, b);
-        s4 += __fmul_rn(b2, b2);
+    for (int b = 0; b < TBW; ++b) {
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const uint32_t sp = pack_bf16(acc[b][v], acc[b][v + 1]);
+        float x0 = lo_f32(sp), x1 = hi_f32(sp);
+        bool ok0 = true, ok1 = true;
+        if (!full) {
+          const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
+          ok0 = ua >= lo && ua < hi;
+          ok1 = ub >= lo && ub < hi;
+          if (!ok0) x0 = 0.f;
+          if (!ok1) x1 = 0.f;
+        }
+        float q0, q1;  // squares, or squared deviations from the row mean (centred)
+        if constexpr (MODE == kStatsCentered) {
+          const float d0 = ok0 ? x0 - mu[b] : 0.f, d1 = ok1 ? x1 - mu[b] : 0.f;
+          q0 = __fmul_rn(d0, d0);
+          q1 = __fmul_rn(d1, d1);
+        } else {
+          q0 = __fmul_rn(x0, x0);
+          q1 = __fmul_rn(x1, x1);
+        }
+        s1[b] += x0;
+        s2[b] += q0;
+        s1[b] += x1;
+        s2[b] += q1;
+        if constexpr (DG) {
+          s3[b] += __fmul_rn(q0, x0);
+          s4[b] += __fmul_rn(q0, q0);
+          s3[b] += __fmul_rn(q1, x1);
+          s4[b] += __fmul_rn(q1, q1);
+        }
       }
     }
     wait_vm0();
     __syncthreads();
   }
-  s1 += __shfl_xor(s1, 32);
-  s2 += __shfl_xor(s2, 32);
-  if constexpr (DG) {
-    s3 += __shfl_xor(s3, 32);
-    s4 += __shfl_xor(s4, 32);
-  }
-  if (half == 0 && t < p.g.T) {
-    float* m = p.mom + (static_cast<int64_t>(split) * p.g.T + t) * MS;
-    m[0] = s1;
-    m[1] = s2;
+#pragma unroll
+  for (int b = 0; b < TBW; ++b) {
+    s1[b] += __shfl_xor(s1[b], 32);
+    s2[b] += __shfl_xor(s2[b], 32);
     if constexpr (DG) {
-      m[2] = s3;
-      m[3] = s4;
+      s3[b] += __shfl_xor(s3[b], 32);
+      s4[b] += __shfl_xor(s4[b], 32);
+    }
+    if (half == 0 && tt[b] < p.g.T) {
+      float* m = p.mom + (static_cast<int64_t>(split) * p.g.T + tt[b]) * MS;
+      m[0] = s1[b];
+      m[1] = s2[b];
+      if constexpr (DG) {
+        m[2] = s3[b];
+        m[3] = s4[b];
+      }
     }
   }
 }
@@ -1670,17 +1696,22 @@ struct Kernels {
 
 // WS: the warp-specialised main kernel (when both roles fit 256 registers);
 // DG: with training diagnostics (warp-specialised kernels only)
+// Token blocks per wave of the moments kernel.  Two (each E fragment feeding
+// two MFMAs, half the E traffic per token) measured slower at the Know pool
+// (0.431 against 0.402 ms per step): with x for 64 rows in registers one
+// wave per SIMD remains, and the tile loop's waits are no longer hidden.
+constexpr int kStatsTBW = 1;
 template <int DB, int KH, bool HX, bool WS>
 Kernels kernels_of(bool dg) {
   if constexpr (WS) {
     constexpr int lds = (2 * (KH + 2 * DB) + 2 * 2 * DB + 16) * kFragBytes;  // 2 E/R, 2 W^T, S
     if (dg)
-      return Kernels{srw_stats_kernel<KH, kStatsDiag>, srw_stats_kernel<KH, kStatsCentered>,
+      return Kernels{srw_stats_kernel<KH, kStatsDiag, 1>, srw_stats_kernel<KH, kStatsCentered, 1>,
                      srw_main_ws_kernel<DB, KH, HX, true>, kWsThreads, lds};
-    return Kernels{srw_stats_kernel<KH, kStatsPlain>, srw_stats_kernel<KH, kStatsCentered>,
+    return Kernels{srw_stats_kernel<KH, kStatsPlain, kStatsTBW>, srw_stats_kernel<KH, kStatsCentered, kStatsTBW>,
                    srw_main_ws_kernel<DB, KH, HX, false>, kWsThreads, lds};
   } else {
-    return Kernels{srw_stats_kernel<KH, kStatsPlain>, srw_stats_kernel<KH, kStatsCentered>,
+    return Kernels{srw_stats_kernel<KH, kStatsPlain, kStatsTBW>, srw_stats_kernel<KH, kStatsCentered, kStatsTBW>,
                    srw_main_kernel<DB, KH, HX>, kThreads, 2 * (KH + 2 * DB + 2 * DB) * kFragBytes};
   }
 }
@@ -1778,8 +1809,12 @@ Geometry geometry(const srw_desc_t& d, int64_t chunk) {
   }
   g.spc = spc;
   g.S = g.nc * spc;
-  g.TT_st = g.TT;  // the moments kernel uses the main kernel's token tiles, two workgroups per CU
-  int spc_st = static_cast<int>((2 * kTargetBlocks + g.TT_st * g.nc - 1) / (g.TT_st * g.nc));
+  // the moments kernel: token tiles of 128 TBW rows; with one block per wave
+  // two workgroups share a CU, with two (the registers of 64 rows) one does
+  const int tbw = with_diag(d) ? 1 : kStatsTBW;
+  g.TT_st = static_cast<int>((g.T + kTokTile * tbw - 1) / (kTokTile * tbw));
+  const int64_t st_blocks = tbw == 1 ? 2 * kTargetBlocks : kTargetBlocks;
+  int spc_st = static_cast<int>((st_blocks + g.TT_st * g.nc - 1) / (g.TT_st * g.nc));
   if (decode_applies(d)) spc_st = spc;  // one row tile: fewer, longer moment splits (fewer partials per row)
   if (spc_st < 1) spc_st = 1;
   if (spc_st > min_tiles) spc_st = static_cast<int>(min_tiles > 0 ? min_tiles : 1);
