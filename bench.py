@@ -62,6 +62,31 @@ WORKLOADS = {
 MODEL_BATCH, MODEL_SEQ, MODEL_VOCAB = 32, 512, 32000
 
 
+# Default run lengths, by GPU time: the clocks settle over the first ~70 ms
+# of sustained load (a 0.34 ms step runs ~10 % slower in its first hundred
+# launches than from the two-hundredth on), so the default warm-up covers
+# that ramp and the timed region measures the sustained rate.
+WARMUP_SECONDS = 0.3
+TIMED_SECONDS = 1.0
+
+
+def resolve_counts(args, run_once, sync) -> tuple[int, int]:
+    """(warmup, steps): the explicit --warmup / --steps, or counts sized from
+    one timed launch of ``run_once`` to WARMUP_SECONDS / TIMED_SECONDS."""
+    if args.warmup is not None and args.steps is not None:
+        return args.warmup, args.steps
+    run_once()
+    sync()
+    t0 = time.perf_counter()
+    run_once()
+    sync()
+    one = max(time.perf_counter() - t0, 1e-5)
+    warmup = args.warmup if args.warmup is not None else max(5, int(WARMUP_SECONDS / one))
+    steps = args.steps if args.steps is not None else min(5000, max(20, int(TIMED_SECONDS / one)))
+    log(f"one step ~{one * 1e3:.3f} ms: warm-up {warmup} steps, {steps} timed")
+    return warmup, steps
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -170,12 +195,14 @@ def bench_decode(args, pkg, C, dev) -> dict:
     with torch.cuda.graph(graph, stream=cap):
         step(cap)
     torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    K = args.steps
+    warmup, K = resolve_counts(args, graph.replay, torch.cuda.synchronize)
     t_begin = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
+    t_begin.record(stream)
+    t_end.record(stream)
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
     t_begin.record(stream)
     for _ in range(K):
         graph.replay()
@@ -225,7 +252,7 @@ def bench_decode(args, pkg, C, dev) -> dict:
                           f"(QK, V, Know at 64 rows), scaled to {DECODE_LAYERS} layers; {cpu_model()}")}
     return {
         "metric": METRIC, "value": round(64 / (step_ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": K, "warmup": args.warmup, "ms_per_step": round(step_ms, 5),
+        "steps": K, "warmup": warmup, "ms_per_step": round(step_ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) x RMS-normalised; router h = x W + b; E, R, W unit rows)",
         "config": {"workload": "decode", "note": WORKLOADS["decode"][2], "T": 64, "layers": DECODE_LAYERS,
@@ -251,12 +278,11 @@ def bench_model(args, pkg, C, dev) -> dict:
     ids = torch.randint(0, cfg.vocab_size, (B, S), generator=torch.Generator().manual_seed(args.seed))
     ids_dev = ids.to(dev)
     stream = torch.cuda.current_stream(dev)
-    for _ in range(max(1, args.warmup)):
-        model.forward(ids_dev)
+    model.forward(ids_dev)
     torch.cuda.synchronize()
-    log(f"model warm-up done: T={T}, paths " + ", ".join(
+    log(f"model built: T={T}, paths " + ", ".join(
         f"{k[0]}:{c.plan.path}" for k, c in model._calls.items()))
-    K = args.steps
+    warmup, K = resolve_counts(args, lambda: model.forward(ids_dev), torch.cuda.synchronize)
     ev_k = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in range(K)]
     for a, b in ev_k:
@@ -264,6 +290,10 @@ def bench_model(args, pkg, C, dev) -> dict:
         b.record(stream)
     t_begin = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
+    t_begin.record(stream)
+    t_end.record(stream)
+    for _ in range(warmup):
+        model.forward(ids_dev)
     torch.cuda.synchronize()
     t_begin.record(stream)
     for i in range(K):
@@ -306,7 +336,7 @@ def bench_model(args, pkg, C, dev) -> dict:
                           f"runs; {cpu_model()}")}
     return {
         "metric": METRIC, "value": round(T / (step_ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": K, "warmup": args.warmup, "ms_per_step": round(step_ms, 4),
+        "steps": K, "warmup": warmup, "ms_per_step": round(step_ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": ("synthetic (token ids uniform over the vocabulary, seeded; random-init weights "
                  "with the reference's initialisers)"),
@@ -324,8 +354,10 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: as many as take about %.0f s)" % TIMED_SECONDS)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps first (default: as many as take about %.1f s)" % WARMUP_SECONDS)
     ap.add_argument("--workload", default="know", choices=sorted(WORKLOADS))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--stats", default="onepass", choices=["onepass", "centered", "gram"])
@@ -416,10 +448,8 @@ def main() -> int:
     stream = torch.cuda.current_stream(dev)
 
     plan.launch(stream)
-    for _ in range(args.warmup):
-        plan.launch(stream, pool_cached=args.pool_cached)
     torch.cuda.synchronize()
-    log(f"warm-up done, path={plan.path}, mean active/token="
+    log(f"first call done, path={plan.path}, mean active/token="
         f"{plan.n_active.float().mean().item():.1f}")
 
     def step():
@@ -431,10 +461,9 @@ def main() -> int:
         d_out = torch.randn(shape.T, 1, shape.D, generator=gen).to(dev)
         bplan = pkg.SrwBackwardPlan(x, h, plan.inputs[2], plan.inputs[3], plan.inputs[4],
                                     plan.inputs[5], plan.out, d_out, 1e-2, 1e-2)
-        for _ in range(args.warmup + 1):
-            bplan.launch(stream)
+        bplan.launch(stream)
         torch.cuda.synchronize()
-        log(f"backward warm-up done, path={bplan.path}, workspace {bplan.ws_bytes / 2**30:.2f} GiB")
+        log(f"backward first call done, path={bplan.path}, workspace {bplan.ws_bytes / 2**30:.2f} GiB")
 
         def step():  # noqa: F811
             bplan.launch(stream)
@@ -452,20 +481,20 @@ def main() -> int:
         with torch.cuda.graph(graph, stream=cap):
             plan.launch(cap, pool_cached=args.pool_cached)
         torch.cuda.synchronize()
-        for _ in range(args.warmup):
-            graph.replay()
-        torch.cuda.synchronize()
         log("captured one call in a HIP graph")
 
-    K = args.steps
+    run_once = graph.replay if graph is not None else step
+    warmup, K = resolve_counts(args, run_once, torch.cuda.synchronize)
     ev_k = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             for _ in range(K)]
-    for a, b in ev_k:      # materialise the HIP events on this stream
-        a.record(stream)
-        b.record(stream)
-    torch.cuda.synchronize()
     t_begin = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
+    for a, b in ev_k + [(t_begin, t_end)]:      # materialise the HIP events on this stream
+        a.record(stream)
+        b.record(stream)
+    # the warm-up runs straight into the timed region (one synchronize between)
+    for _ in range(warmup):
+        run_once()
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     t_begin.record(stream)
@@ -483,10 +512,12 @@ def main() -> int:
     if graph is not None:
         # the dominant kernel's own events are not recorded inside a replay:
         # time it eagerly once more
+        ev_k = ev_k[:200]
         for a, b in ev_k:
             C.set_kernel_events(a.cuda_event, b.cuda_event)
             step()
         torch.cuda.synchronize()
+        C.set_kernel_events(None, None)
     kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev_k)
     log(f"timed {K} steps: {step_ms:.4f} ms/step (events), wall {wall / K * 1e3:.4f} ms/step, "
         f"dominant kernel {kern_ms:.4f} ms")
@@ -529,7 +560,7 @@ def main() -> int:
     value = T / (step_ms * 1e-3)
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": K, "warmup": args.warmup, "ms_per_step": round(step_ms, 5),
+        "steps": K, "warmup": warmup, "ms_per_step": round(step_ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (seeded N(0,1) x RMS-normalised; E ~ N(0,1/dr); "
                                   "R, W L2-normalised rows)",
