@@ -40,7 +40,9 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 # (workload, stats mode, kernel family); profiles/know_T4096_N25200_traffic.md
 # has the runs.
 MEASURED_TRAFFIC = {
-    ("know", "onepass", "mfma_bf16"): (41148 * 2.0 + 64190 * 1.0) * 1024,
+    # the scores-streaming main kernel: reads the 206 MB of bf16 scores the
+    # moments kernel stored, besides R, W^T and x
+    ("know", "onepass", "mfma_ss_bf16"): (133053.0 * 2.0 + 64575.2 * 1.0) * 1024,
     # profiles/decode_know_T64_N25200_kernel_stats.md
     ("decode_know", "onepass", "mfma_decode_bf16"): (22575.2 * 2.0 + 19704.9 * 1.0) * 1024,
 }
@@ -308,11 +310,13 @@ def bench_model(args, pkg, C, dev) -> dict:
     srw = L * 2.0 * T * (cfg.n_qk * (2 * dr + 3 * D) + cfg.n_v * (dr + 2 * D) + cfg.n_know * (dr + 2 * D))
     glue = (L * (2.0 * T * D * (4 * dr + 4) + 2.0 * T * D * D + 4.0 * B * S * S * D)
             + 2.0 * T * D * cfg.vocab_size)
-    kflops = 2.0 * T * cfg.n_know * (dr + 2 * D)
+    know_path = model._calls[("know", T, 1, "onepass")].plan.path
+    # the Know call's main kernel; the scores-streaming one leaves the score GEMM to the moments kernel
+    kflops = 2.0 * T * cfg.n_know * ((0 if know_path == "mfma_ss_bf16" else dr) + 2 * D)
     achieved = kflops / (kern_ms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                "kernel": model._calls[("know", T, 1, "onepass")].plan.path,
+                "kernel": know_path,
                 "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops,
                 "step_tflops": round((srw + glue) / (step_ms * 1e-3) / 1e12, 2),
                 "srw_flop_per_step": srw, "glue_flop_per_step": glue}
@@ -529,6 +533,10 @@ def main() -> int:
         # recompute (score + read), dP, dW, dR, dx (d_model) and dE, dh (d_route)
         flops = 2.0 * T * N * (3 * dr + 5 * D)
         kflops = 2.0 * T * N * D        # the dominant kernel: dP = draw . W^T with the gate derivative
+    elif plan.path == "mfma_ss_bf16":
+        # the main kernel streams the moments kernel's bf16 scores: its own
+        # work is the read (once per token) and write GEMMs
+        kflops = 2.0 * T * N * (D + R * D)
     elif plan.path == "tiled_bf16":
         # the dominant kernel of the tiled family is the gate GEMM pair (score
         # + read); the write GEMM is a kernel of its own

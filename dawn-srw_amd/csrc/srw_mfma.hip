@@ -230,7 +230,18 @@ struct StatsParams {
   uint32_t* mask32;    // pass bitmask as uint32 words [T][mask_words32] (may be null)
   int64_t mask_words32;
   Geometry g;
+  uint16_t* s_out;     // bf16 score buffer (score_tile_off layout) or null: plain moments only
 };
+
+// The bf16 scores as the scores-streaming main kernel reads them: per (token
+// tile of 128 rows, 32-unit tile, 32-row token block) the 32 x 32 score
+// accumulator of the wave that computed it, two 1 KB pieces of 64 lanes x
+// 16 B (lane l's elements 0-7, then 8-15, in accumulator order: unit
+// unit_of_acc(v, l / 32) of token l % 32).  Byte offset of a block:
+constexpr int kScoreTileBytes = 4 * 2 * kFragBytes;  // one (token tile, unit tile)
+__host__ __device__ inline int64_t score_tile_off(int ntiles, int64_t ttile, int64_t utile, int blk) {
+  return (ttile * ntiles + utile) * kScoreTileBytes + static_cast<int64_t>(blk) * 2 * kFragBytes;
+}
 
 // MODE kStatsPlain: sum s, sum s^2 (v41:441-442); kStatsDiag: also sum s^3,
 // s^4 (training diagnostics, v41:442-444; mom stride 4); kStatsCentered: sum
@@ -300,6 +311,23 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
   float s1[TBW], s2[TBW], s3[TBW], s4[TBW];
 #pragma unroll
   for (int b = 0; b < TBW; ++b) s1[b] = s2[b] = s3[b] = s4[b] = 0.f;
+  // score store (plain moments, one block per wave): each tile's packed
+  // scores go out at the start of the next tile's MFMAs, so the stores have
+  // a whole tile to complete before the end-of-tile vmcnt wait.  A tile that
+  // two splits share (a chunk boundary inside it) is stored by the split
+  // holding its first unit.
+  constexpr bool STORE = TBW == 1 && MODE == kStatsPlain;
+  uint32_t spd[8];
+  char* sdst = nullptr;
+  // Non-temporal stores (and loads in the main kernel): 206 MB per Know-pool
+  // call at T = 4096 that would otherwise displace the pool tiles the other
+  // token tiles share, in L2 and in the last-level cache across kernels
+  // (measured: moments kernel 101 -> 87 us, pack 12.8 -> 9.1 us).
+  auto store_scores = [&]() {
+    __builtin_nontemporal_store(u32x4_t{spd[0], spd[1], spd[2], spd[3]}, reinterpret_cast<u32x4_t*>(sdst));
+    __builtin_nontemporal_store(u32x4_t{spd[4], spd[5], spd[6], spd[7]},
+                                reinterpret_cast<u32x4_t*>(sdst + kFragBytes));
+  };
   if (ta < tb) {
     issue(ta, 0);
     wait_vm0();
@@ -322,6 +350,12 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
       if (g < KH) ef[g] = frag(g);
 #pragma unroll
     for (int ks = 0; ks < KH; ++ks) {
+      if constexpr (STORE) {
+        if (ks == 0 && sdst) {
+          store_scores();
+          sdst = nullptr;
+        }
+      }
       const u32x4_t e = ef[ks % PF];
       if (ks + PF < KH) ef[ks % PF] = frag(ks + PF);
       if (pre && (ks % 4) == 0 && wave + ks < KH)  // block wave + ks: this wave's share, every 4th k-step
@@ -333,6 +367,13 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
     }
     const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
     const bool full = u0 >= lo && u0 + kUnitTile <= hi;
+    if constexpr (STORE) {
+      if (p.s_out && u0 >= lo) {
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) spd[v >> 1] = pack_bf16(acc[0][v], acc[0][v + 1]);  // v41:503
+        sdst = reinterpret_cast<char*>(p.s_out) + score_tile_off(p.g.ntiles, ttile, tile, wave) + lane * 16;
+      }
+    }
 #pragma unroll
     for (int b = 0; b < TBW; ++b) {
 #pragma unroll
@@ -370,6 +411,9 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
     }
     wait_vm0();
     __syncthreads();
+  }
+  if constexpr (STORE) {
+    if (sdst) store_scores();
   }
 #pragma unroll
   for (int b = 0; b < TBW; ++b) {
@@ -419,6 +463,7 @@ struct MainParams {
   GateParams gp;
   float exp_scale;       // -sharpness * log2(e)
   int rb;                // decode kernel: row-block groups per split (workgroup = split * rb + group)
+  const uint16_t* s_in;  // scores-streaming kernel: the moments kernel's bf16 score buffer
 };
 
 // v4.1 gate of a margin m = s - tau - thr (v41:503-511), with the kernels' operations
@@ -1154,6 +1199,282 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
 }
 
 // ---------------------------------------------------------------------------
+// main, scores streamed: the warp-specialised layout of srw_main_ws_kernel
+// with the bf16 scores read back from the moments kernel's score buffer
+// (kScoreTileBytes per (token tile, unit tile)) instead of recomputed -- the
+// same bf16 values: the same fragments, MFMA and k order produced them.
+// Producers (waves 0-3) run only the read GEMM XR^T = R_t.X^T and hand the
+// bf16 x.r (v41:517) to a double-buffered LDS stage; consumers (waves 4-7)
+// load their 32 x 32 score block of the next tile (2 KB per wave, direct
+// global->LDS, beside the tile's W^T), run the gate epilogue of the current
+// one and its write GEMM.  With every stage doubled one workgroup barrier
+// per tile suffices: a stage is rewritten two tiles after it was filled,
+// past the barrier that ends the reads of it.  LDS = 2 R + 2 W^T + 2 x.r +
+// 2 score stages (128 KB at d_model = 384).
+// ---------------------------------------------------------------------------
+template <int DB>
+constexpr int ss_lds_bytes() {
+  return (2 * (DB * 2) + 2 * (2 * DB) + 2 * 8 + 2 * 8) * kFragBytes;
+}
+
+template <int DB>
+__global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  constexpr int TPS = 4;
+  constexpr int D = DB * 32;
+  constexpr int KX = D / 16;
+  constexpr int F_R = KX, F_W = 2 * DB;
+  constexpr int R_STAGE = F_R * kFragBytes;
+  constexpr int W_STAGE = F_W * kFragBytes;
+  constexpr int XR_BLK = 2 * kFragBytes;  // per token block: bf16 x.r (2 KB)
+  constexpr int XR_STAGE = 4 * XR_BLK;
+  constexpr int S_BLK = 2 * kFragBytes;   // per token block: bf16 scores (2 KB)
+  constexpr int S_STAGE = 4 * S_BLK;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool producer = wave < 4;
+  const int blk = wave & 3;                 // token block of this wave
+  const int half = lane >> 5, col = lane & 31;
+  const int split = blockIdx.x % p.g.S;
+  const int ttile = blockIdx.x / p.g.S;
+  const int64_t tw = static_cast<int64_t>(ttile) * kTokTile + 32 * blk;
+  const int64_t t = tw + col;
+  const int64_t tl = t < p.g.T ? t : p.g.T - 1;
+  int ta, tb;
+  int64_t lo, hi;
+  split_range(p.g, p.g.spc, split, ta, tb, lo, hi);
+  const int n = tb - ta;
+
+  char* const r_base = lds;
+  char* const w_base = lds + 2 * R_STAGE;
+  char* const xr_lane = w_base + 2 * W_STAGE + blk * XR_BLK + lane * 16;  // + stage * XR_STAGE
+  char* const s_wave = w_base + 2 * W_STAGE + 2 * XR_STAGE + blk * S_BLK;  // + stage * S_STAGE
+
+  // R and W^T tiles, direct global->LDS, each wave a contiguous run of blocks
+  constexpr int PR = (F_R + 3) / 4, PW = (F_W + 3) / 4;
+  using TileR = RowTile<KX>;
+  const uint32_t lsrc_r[2] = {TileR::lane_src(lane, 0), TileR::lane_src(lane, 1)};
+  auto r_load = [&](int tile, int stage, int q) {
+    if (PR * blk + q < F_R)
+      TileR::load(p.read, static_cast<int64_t>(tile) * kUnitTile, p.g.N, PR * blk + q, lane, lsrc_r,
+                  r_base + stage * R_STAGE);
+  };
+  const uint32_t w_voff = static_cast<uint32_t>(PW * blk * kFragBytes + lane * 16);
+  auto w_load = [&](int tile, int stage, int q) {
+    if (PW * blk + q < F_W)
+      g2lds16(reinterpret_cast<const char*>(p.wp) + static_cast<int64_t>(tile) * W_STAGE + (w_voff + q * kFragBytes),
+              w_base + stage * W_STAGE + (PW * blk + q) * kFragBytes);
+  };
+
+  // prologue: R of the first tile
+  if (n > 0 && producer) {
+#pragma unroll
+    for (int q = 0; q < PR; ++q) r_load(ta, 0, q);
+  }
+  wait_vm0();
+  __syncthreads();
+
+  if (producer) {
+    // ---------------- producer: read GEMM ----------------
+    u32x4_t xq[KX];
+#pragma unroll
+    for (int ks = 0; ks < KX; ++ks)
+      xq[ks] = *reinterpret_cast<const u32x4_t*>(p.x + (tl / p.routes) * D + 16 * ks + 8 * half);
+    int lr[TileR::NM];
+#pragma unroll
+    for (int m = 0; m < TileR::NM; ++m) lr[m] = TileR::lane_off(lane, m);
+    wait_vm0();  // x drained here, not at the first tile's vmcnt wait
+
+    for (int it = 0; it <= n; ++it) {
+      if (it < n) {
+        const bool pre = it + 1 < n;  // the next tile's R goes out during this one's MFMAs
+        const char* base = r_base + (it & 1) * R_STAGE;
+        constexpr int PF = 8;
+        auto frag = [&](int k) {
+          return *reinterpret_cast<const u32x4_t*>(base + lr[k % TileR::NM] + TileR::step_off(k));
+        };
+        u32x4_t fr[PF];
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+          if (k < KX) fr[k] = frag(k);
+        f32x16_t racc = {};
+#pragma unroll
+        for (int k = 0; k < KX; ++k) {
+#pragma unroll
+          for (int q = 0; q < PR; ++q)
+            if (k == q * KX / (2 * PR) && pre) r_load(ta + it + 1, (it + 1) & 1, q);  // first half
+          const u32x4_t a = fr[k % PF];
+          if (k + PF < KX) fr[k % PF] = frag(k + PF);
+          racc = mfma(a, xq[k], racc);
+          __builtin_amdgcn_sched_barrier(0);  // keep the reads PF steps ahead
+        }
+        uint32_t xr[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xr[q] = pack_bf16(racc[2 * q], racc[2 * q + 1]);  // bf16 x.r (v41:517)
+        char* dst = xr_lane + (it & 1) * XR_STAGE;
+        *reinterpret_cast<u32x4_t*>(dst) = u32x4_t{xr[0], xr[1], xr[2], xr[3]};
+        *reinterpret_cast<u32x4_t*>(dst + kFragBytes) = u32x4_t{xr[4], xr[5], xr[6], xr[7]};
+      }
+      wait_vm0();
+      barrier_lds();  // x.r of this tile, the next tile's R and W^T visible
+    }
+  } else {
+    // ---------------- consumer: gate epilogue and write GEMM, one tile behind ----------------
+    // tau folded with the gate's constant offsets (srw_main_ws_kernel):
+    //   margin = s - tau - thr,  exp argument = margin * c  (c = -sharpness log2 e)
+    float k_exp, tau_cut;
+    {
+      const float tau_thr = p.tau[tl] + p.gp.thr;
+      k_exp = -tau_thr * p.exp_scale;
+      tau_cut = tau_thr + p.gp.cut;
+    }
+    const float c_exp = p.exp_scale, eps = p.gp.eps, maxi = p.gp.maxi;
+    float gsum = 0.f, isum = 0.f;
+    uint32_t nact = 0;
+    f32x16_t oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
+    // this wave's score blocks: tile u at s_src + u * kScoreTileBytes (elements 0-7), + 1 KB (8-15)
+    const char* const s_src =
+        reinterpret_cast<const char*>(p.s_in) + score_tile_off(p.g.ntiles, ttile, 0, blk) + lane * 16;
+    auto s_load = [&](int tile, int stage) {
+      const char* src = s_src + static_cast<int64_t>(tile) * kScoreTileBytes;
+      g2lds16_nt(src, s_wave + stage * S_STAGE);  // read once
+      g2lds16_nt(src + kFragBytes, s_wave + stage * S_STAGE + kFragBytes);
+    };
+
+    // gate epilogue (v41:503-518) of one tile from its bf16 scores and x.r
+    // (LDS): P (k-step j in pk[4j..4j+3]) and the pass bits (element v at bit
+    // 15 - v); the next tile's W^T and score loads go out between element pairs
+    auto gate_tile = [&](auto full_tag, int64_t u0, uint32_t* pk, int wtile, int wstage, const char* srp,
+                         const char* xrp) -> uint32_t {
+      constexpr bool FULL = decltype(full_tag)::value;
+      uint32_t bits = 0;
+      u32x4_t sq, xq4;
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        if ((v & 7) == 0) {
+          sq = *reinterpret_cast<const u32x4_t*>(srp + (v >> 3) * kFragBytes);
+          xq4 = *reinterpret_cast<const u32x4_t*>(xrp + (v >> 3) * kFragBytes);
+        }
+        if ((v >> 1) < PW && wtile >= 0) w_load(wtile, wstage, v >> 1);
+        if (v == 2 * PW && wtile >= 0) s_load(wtile, wstage);
+        const uint32_t sp = sq[(v >> 1) & 3];
+        const uint32_t xp = xq4[(v >> 1) & 3];
+        float g2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float sv = e ? hi_f32(sp) : lo_f32(sp);
+          // sigmoid(sharpness * margin) = 1 / (1 + 2^(margin * c)); active <=> margin > 0 <=> arg < 0
+          const float arg = fmaf(sv, c_exp, k_exp);
+          const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(arg));
+          // intensity = eps + min(max(margin - cutoff, 0), max_intensity)
+          float inten = eps + __builtin_amdgcn_fmed3f(sv - tau_cut, 0.0f, maxi);
+          float g = act * inten;
+          uint32_t sign = __float_as_uint(arg);
+          if constexpr (!FULL) {
+            const int64_t u = u0 + unit_of_acc(v + e, half);
+            const bool ok = u >= lo && u < hi;
+            g = ok ? g : 0.f;
+            inten = ok ? inten : 0.f;
+            sign = ok ? sign : 0u;
+          }
+          gsum += g;
+          isum += inten;
+          bits = __builtin_amdgcn_alignbit(bits, sign, 31);   // bits << 1 | active
+          g2[e] = g;
+        }
+        const uint32_t gq = pack_bf16(g2[0], g2[1]);             // gate_bf (v41:516)
+        pk[v >> 1] = pack_bf16(lo_f32(gq) * lo_f32(xp), hi_f32(gq) * hi_f32(xp));  // (v41:518)
+      }
+      return bits;
+    };
+
+    for (int it = 0; it <= n; ++it) {
+      const bool cur = it < n;  // this tile's W^T goes out during the previous tile's epilogue
+      if (it == 0) {
+        if (cur) {
+#pragma unroll
+          for (int q = 0; q < PW; ++q) w_load(ta, 0, q);
+          s_load(ta, 0);
+        }
+      } else {
+        const int tile = ta + it - 1;
+        const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
+        const char* srp = s_wave + ((it - 1) & 1) * S_STAGE + lane * 16;
+        const char* xrp = xr_lane + ((it - 1) & 1) * XR_STAGE;
+        uint32_t pk[8];
+        uint32_t bits;
+        const int wtile = cur ? ta + it : -1;
+        if (u0 >= lo && u0 + kUnitTile <= hi)
+          bits = gate_tile(std::integral_constant<bool, true>{}, u0, pk, wtile, it & 1, srp, xrp);
+        else
+          bits = gate_tile(std::integral_constant<bool, false>{}, u0, pk, wtile, it & 1, srp, xrp);
+        {
+          const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
+          uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
+          m <<= 4 * half;
+          nact += __builtin_popcount(m);
+          m |= __shfl_xor(m, 32);
+          if (p.mask32 && half == 0 && t < p.g.T) {
+            uint32_t* dst = p.mask32 + t * p.mask_words32 + tile;
+            const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
+            if (shared) atomicOr(dst, m);
+            else *dst = m;
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // write GEMM: OUT[32 tok x D] += P[32 tok x 32 units] . W_t[32 units x D]
+        const char* wb = w_base + ((it - 1) & 1) * W_STAGE + lane * 16;
+        const u32x4_t a0 = {pk[0], pk[1], pk[2], pk[3]}, a1 = {pk[4], pk[5], pk[6], pk[7]};
+        constexpr int NC = 2 * DB, PF = 4;
+        auto frag = [&](int k) {  // MFMA k: j = k / DB, db = k % DB
+          return *reinterpret_cast<const u32x4_t*>(wb + (2 * (k % DB) + k / DB) * kFragBytes);
+        };
+        u32x4_t fr[PF];
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+          if (k < NC) fr[k] = frag(k);
+#pragma unroll
+        for (int k = 0; k < NC; ++k) {
+          const u32x4_t bq = fr[k % PF];
+          if (k + PF < NC) fr[k % PF] = frag(k + PF);
+          oacc[k % DB] = mfma(k < DB ? a0 : a1, bq, oacc[k % DB]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      wait_vm0();
+      barrier_lds();
+    }
+    gsum += __shfl_xor(gsum, 32);
+    isum += __shfl_xor(isum, 32);
+    nact += __shfl_xor(nact, 32);
+    if (half == 0 && t < p.g.T) {
+      float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * TPS;
+      tp[0] = gsum;
+      tp[1] = isum;
+      tp[2] = static_cast<float>(nact);
+    }
+    float* op = p.out_part + static_cast<int64_t>(split) * p.g.T * D;
+    if (tw + 32 <= p.g.T) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) op[(tw + unit_of_acc(v, half)) * D + 32 * db + col] = oacc[db][v];
+    } else {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t tt = tw + unit_of_acc(v, half);
+          if (tt < p.g.T) op[tt * D + 32 * db + col] = oacc[db][v];
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // tau: per row, the moment partials -> tau = mean + tau_offset * (sqrt(E[s^2]
 // - mean^2) + 1e-8) (v41:461-464).  One wave per row; lanes split the
 // partials.  mom holds ms floats per (split, row): s, s^2 [, s^3, s^4].  With
@@ -1835,8 +2156,31 @@ bool decode_splits_fit(const Geometry& g) {
   return true;
 }
 
+// The scores-streaming main kernel serves calls without diagnostics whose
+// moments come from the moments kernel (one-pass or centred statistics; the
+// Gram statistics compute no scores), that do not take the decode kernel, and
+// whose score GEMM is as wide as the read GEMM (d_route >= d_model).  The
+// score buffer costs 4 bytes of HBM traffic per (row, unit) whatever d_route
+// is, while the recompute it saves is a d_route / (d_route + 2 d_model) share
+// of the main kernel's MFMAs: at d_route = d_model = 384 (Know pool, T =
+// 4096) streaming took the moments + main kernels from 307 to 278 us, at
+// d_route = 128 (the model's pools, T = 16 384) from 394 to 416 us.
+bool ss_applies(const srw_desc_t& d, const Geometry& g) {
+  if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM) return false;
+  if (d.d_model != 384 && d.d_model != 128 && d.d_model != 64) return false;
+  if (d.d_route < d.d_model) return false;
+  if (decode_applies(d) && decode_splits_fit(g)) return false;
+  return g.TT_st == g.TT;  // the moments kernel's 128-row token tiles are the main kernel's
+}
+bool pick_ss(int64_t D, MainFn* fn, int* lds) {
+  if (D == 384) { *fn = srw_main_ss_kernel<12>; *lds = ss_lds_bytes<12>(); return true; }
+  if (D == 128) { *fn = srw_main_ss_kernel<4>; *lds = ss_lds_bytes<4>(); return true; }
+  if (D == 64) { *fn = srw_main_ss_kernel<2>; *lds = ss_lds_bytes<2>(); return true; }
+  return false;
+}
+
 struct WsLayout {
-  size_t wp, mom, tau, gram, out_part, tok_part, total;
+  size_t wp, mom, tau, gram, out_part, tok_part, scores, total;
 };
 
 size_t al(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
@@ -1856,6 +2200,8 @@ WsLayout ws_layout(const srw_desc_t& d, const Geometry& g) {
   off += al(static_cast<size_t>(g.S) * g.T * d.d_model * 4);
   w.tok_part = off;
   off += al(static_cast<size_t>(g.S) * g.T * tok_part_stride(d) * 4);
+  w.scores = off;
+  if (ss_applies(d, g)) off += al(static_cast<size_t>(g.TT) * g.ntiles * kScoreTileBytes);
   w.total = off;
   return w;
 }
@@ -1910,6 +2256,10 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   float* mom = reinterpret_cast<float*>(a.ws + L.mom);
   float* out_part = reinterpret_cast<float*>(a.ws + L.out_part);
   float* tok_part = reinterpret_cast<float*>(a.ws + L.tok_part);
+  uint16_t* scores = reinterpret_cast<uint16_t*>(a.ws + L.scores);
+  MainFn ss_fn = nullptr;
+  int ss_lds = 0;
+  const bool ss = ss_applies(d, g) && pick_ss(d.d_model, &ss_fn, &ss_lds);
   const int D = static_cast<int>(d.d_model);
   const int KH = static_cast<int>(d.d_route / 16);
   const int DB = D / 32;
@@ -1947,6 +2297,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     sp.mask32 = mask32;
     sp.mask_words32 = mw32;
     sp.g = g;
+    sp.s_out = ss ? scores : nullptr;
     const size_t smem = static_cast<size_t>(2 * KH) * kFragBytes;
     for (auto fn : {k.stats, k.stats_centered})
       if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1960,6 +2311,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
         return e;
       sp.mean = tau;
       sp.mask32 = nullptr;  // the first pass cleared the shared mask words
+      sp.s_out = nullptr;   // and stored the scores
       hipLaunchKernelGGL(k.stats_centered, dim3(grid_st), dim3(kThreads), smem, a.stream, sp);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }
@@ -2006,13 +2358,20 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
       dominant_kernel_end(a.stream);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     } else {
-      const size_t smem = static_cast<size_t>(k.main_lds);
-      if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(k.main),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem))) !=
-          hipSuccess)
+      MainFn fn = k.main;
+      int threads = k.main_threads, lds = k.main_lds;
+      if (ss) {  // the moments kernel stored the scores
+        *path_name = "mfma_ss_bf16";
+        fn = ss_fn;
+        threads = kWsThreads;
+        lds = ss_lds;
+        mp.s_in = scores;
+      }
+      if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   lds)) != hipSuccess)
         return e;
       dominant_kernel_begin(a.stream);
-      hipLaunchKernelGGL(k.main, dim3(grid), dim3(k.main_threads), smem, a.stream, mp);
+      hipLaunchKernelGGL(fn, dim3(grid), dim3(threads), static_cast<size_t>(lds), a.stream, mp);
       dominant_kernel_end(a.stream);
       if ((e = hipGetLastError()) != hipSuccess) return e;
     }

@@ -40,6 +40,11 @@ __device__ inline float hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff00
 __device__ inline void g2lds16(const void* g, char* lds) {
   __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 0);
 }
+// The same with the non-temporal (streaming) cache policy, for data read
+// once: it does not displace data other workgroups or kernels reuse.
+__device__ inline void g2lds16_nt(const void* g, char* lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 2);  // cache policy bit 1: nt
+}
 
 __device__ inline void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 

@@ -248,7 +248,7 @@ srw_status_t srw_backward(const srw_desc_t* desc, const srw_tensors_t* in,
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /* Name of the kernel family the last srw_forward on this thread used
- * ("generic", "mfma_bf16", ...), for tests and benchmarks. */
+ * ("generic", "mfma_bf16", "mfma_ss_bf16", ...), for tests and benchmarks. */
 const char* srw_last_path(void);
 
 /* Profiling hook; no counterpart in the reference (its timing is host-side

@@ -115,6 +115,9 @@ def test_workspace_sizes(C):
     want = (al(4 * 32 * D * 2) + al(S * T * 2 * 4) + al(T * 4) + al(S * T * D * 4)
             + al(S * T * 4 * 4))
     assert C.workspace_size(_desc(C)) == want
+    # d_route == d_model: also the bf16 scores the main kernel streams (8 KB
+    # per 128-token tile and 32-unit tile)
+    assert C.workspace_size(_desc(C, d_route=64)) == want + al(1 * 4 * 8192)
     d = _desc(C, gate=C.SRW_GATE_GELU_V401)      # forward-normalised R and W copies (bf16)
     assert C.workspace_size(d) == 2 * 100 * 64 * 2
     d = _desc(C, gate=C.SRW_GATE_GELU_V401, dtype=C.SRW_F32)
