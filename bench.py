@@ -158,8 +158,8 @@ def bench_decode(args, pkg, C, dev) -> dict:
     """one decode step = 12 layers x three SRW calls (the QK pool
     with its paired routes, V, Know) on 64 rows, the pools shared by the
     layers (v41:1393-1394), router h = x W + b with d_route 128, the Know
-    tau_offset calibrated to ~3 % pass.  Captured once as a HIP graph and
-    replayed.  The dominant kernel is the Know pool's decode kernel (timed by
+    tau_offset calibrated to ~3 % pass; per layer the QK and V calls as one
+    srw_forward_batch.  Captured once as a HIP graph and replayed.  The dominant kernel is the Know pool's decode kernel (timed by
     an eager call after the replays)."""
     import torch
     bf = torch.bfloat16
@@ -178,14 +178,18 @@ def bench_decode(args, pkg, C, dev) -> dict:
     stream = torch.cuda.current_stream(dev)
     for pl in plans:
         pl.launch(stream)
+    # the QK and V calls of a layer read the same input: one srw_forward_batch
+    # (one launch per stage); the Know call follows the attention, on its own
+    qkv = pkg.SrwBatchPlan(plans[:2])
+    qkv.launch(stream)
     torch.cuda.synchronize()
     log("decode paths: " + ", ".join(f"{s_.note.split(':')[1].strip()} -> {pl.path}"
                                      for s_, pl in zip(shapes, plans)))
 
     def step(st):
         for _ in range(DECODE_LAYERS):
-            for pl in plans:
-                pl.launch(st, pool_cached=True)
+            qkv.launch(st, pool_cached=True)
+            plans[2].launch(st, pool_cached=True)
 
     cap = torch.cuda.Stream(dev)
     cap.wait_stream(stream)
@@ -259,7 +263,7 @@ def bench_decode(args, pkg, C, dev) -> dict:
         "data": "synthetic (seeded N(0,1) x RMS-normalised; router h = x W + b; E, R, W unit rows)",
         "config": {"workload": "decode", "note": WORKLOADS["decode"][2], "T": 64, "layers": DECODE_LAYERS,
                    "pools": {s_.note.split(":")[1].strip(): s_.N for s_ in shapes}, "d_model": 384,
-                   "d_route": 128, "stats": args.stats, "graph": True, "pool_cached": True,
+                   "d_route": 128, "stats": args.stats, "graph": True, "pool_cached": True, "qk_v_batched": True,
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -19,7 +19,8 @@ import threading
 import torch  # noqa: F401  (must precede loading the HIP library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libsrw_amd.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
+MAX_BATCH = 4          # SRW_MAX_BATCH
 
 # srw_status_t
 SRW_OK, SRW_EINVAL, SRW_EUNSUPPORTED, SRW_EHIP, SRW_EWORKSPACE = range(5)
@@ -51,6 +52,7 @@ EXPORTED_SYMBOLS = (
     "srw_abi_version", "srw_status_string", "srw_desc_init",
     "srw_workspace_size", "srw_forward", "srw_last_path",
     "srw_set_kernel_events", "srw_backward_workspace_size", "srw_backward",
+    "srw_workspace_size_batch", "srw_forward_batch",
 )
 
 
@@ -128,6 +130,13 @@ def load_library() -> ctypes.CDLL:
         lib.srw_forward.argtypes = [
             ctypes.POINTER(SrwDesc), ctypes.POINTER(SrwTensors), ctypes.POINTER(SrwOutputs),
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.srw_workspace_size_batch.restype = ctypes.c_int
+        lib.srw_workspace_size_batch.argtypes = [ctypes.c_int32, ctypes.POINTER(SrwDesc),
+                                                 ctypes.POINTER(ctypes.c_size_t)]
+        lib.srw_forward_batch.restype = ctypes.c_int
+        lib.srw_forward_batch.argtypes = [
+            ctypes.c_int32, ctypes.POINTER(SrwDesc), ctypes.POINTER(SrwTensors), ctypes.POINTER(SrwOutputs),
+            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.srw_last_path.restype = ctypes.c_char_p
         lib.srw_last_path.argtypes = []
         lib.srw_set_kernel_events.restype = ctypes.c_int
@@ -160,6 +169,13 @@ def desc_init() -> SrwDesc:
 def workspace_size(desc: SrwDesc) -> int:
     n = ctypes.c_size_t(0)
     check(load_library().srw_workspace_size(ctypes.byref(desc), ctypes.byref(n)))
+    return int(n.value)
+
+
+def workspace_size_batch(descs) -> int:
+    """srw_workspace_size_batch over a ctypes array of SrwDesc."""
+    n = ctypes.c_size_t(0)
+    check(load_library().srw_workspace_size_batch(len(descs), descs, ctypes.byref(n)))
     return int(n.value)
 
 

@@ -123,43 +123,52 @@ srw_status_t srw_workspace_size(const srw_desc_t* d, size_t* bytes) {
   return SRW_OK;
 }
 
-srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw_outputs_t* o, void* workspace,
-                         size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+// Validation and launch arguments of one srw_forward call; *which = the kernel
+// family (or -2: no tokens, nothing to launch).
+srw_status_t prepare_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw_outputs_t* o, void* workspace,
+                             size_t workspace_bytes, void* stream, srw::LaunchArgs* a, int* which) {
   srw_status_t st = validate(d);
   if (st != SRW_OK) return st;
   if (!in || !o) return SRW_EINVAL;
-  int which = choose(*d, in->h != nullptr && in->h == in->x);
-  if (which > 0 && o->gate) which = srw::generic_supports(*d) ? 0 : -1;  // the dense gate: generic kernels
-  if (which < 0) return SRW_EUNSUPPORTED;
+  int w = choose(*d, in->h != nullptr && in->h == in->x);
+  if (w > 0 && o->gate) w = srw::generic_supports(*d) ? 0 : -1;  // the dense gate: generic kernels
+  if (w < 0) return SRW_EUNSUPPORTED;
   if (d->T == 0) {  // nothing to compute; empty tensors may carry null pointers
-    g_last_path = "empty";
+    *which = -2;
     return SRW_OK;
   }
   if (!in->x || !in->h || !in->emb || !in->tau_offset || !in->read || !in->write || !o->out) return SRW_EINVAL;
   if (in->h == in->x && !(d->n_routes == 1 && d->d_route == d->d_model)) return SRW_EINVAL;
-  const size_t need = align256(bytes_of(which, *d));
+  const size_t need = align256(bytes_of(w, *d));
   if (need > 0 && (!workspace || workspace_bytes < need)) return SRW_EWORKSPACE;
 
-  srw::LaunchArgs a{};
-  a.d = *d;
-  a.in = *in;
-  a.o = *o;
+  *a = srw::LaunchArgs{};
+  a->d = *d;
+  a->in = *in;
+  a->o = *o;
   if (!(d->flags & SRW_FLAG_DIAG)) {
-    a.o.token_diag = nullptr;
-    a.o.unit_diag = nullptr;
+    a->o.token_diag = nullptr;
+    a->o.unit_diag = nullptr;
   }
-  a.gp.sharp = d->sharpness;
-  a.gp.thr = d->act_threshold;
-  a.gp.cut = d->act_cutoff;
-  a.gp.eps = d->epsilon;
-  a.gp.maxi = d->max_intensity;
-  a.gp.cap_thresh = (d->epsilon + d->max_intensity) - 1e-3f;  // v41:487 in float32
-  a.words = (d->n_units + 63) / 64;
-  a.chunk = (d->chunk_size > 0 && d->chunk_size < d->n_units) ? d->chunk_size : d->n_units;
-  a.ws = static_cast<char*>(workspace);
-  a.ws_bytes = workspace_bytes;
-  a.stream = static_cast<hipStream_t>(stream);
+  a->gp.sharp = d->sharpness;
+  a->gp.thr = d->act_threshold;
+  a->gp.cut = d->act_cutoff;
+  a->gp.eps = d->epsilon;
+  a->gp.maxi = d->max_intensity;
+  a->gp.cap_thresh = (d->epsilon + d->max_intensity) - 1e-3f;  // v41:487 in float32
+  a->words = (d->n_units + 63) / 64;
+  a->chunk = (d->chunk_size > 0 && d->chunk_size < d->n_units) ? d->chunk_size : d->n_units;
+  a->ws = static_cast<char*>(workspace);
+  a->ws_bytes = workspace_bytes;
+  a->stream = static_cast<hipStream_t>(stream);
+  *which = w;
+  return SRW_OK;
+}
 
+srw_status_t launch_forward(const srw::LaunchArgs& a, int which) {
   (void)hipGetLastError();  // start from a clean error state
   hipError_t e;
   if (which == 1) {
@@ -174,6 +183,76 @@ srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw
     g_last_path = "generic";
   }
   return e == hipSuccess ? SRW_OK : SRW_EHIP;
+}
+}  // namespace
+
+extern "C" {
+
+srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw_outputs_t* o, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  srw::LaunchArgs a;
+  int which = -1;
+  const srw_status_t st = prepare_forward(d, in, o, workspace, workspace_bytes, stream, &a, &which);
+  if (st != SRW_OK) return st;
+  if (which == -2) {
+    g_last_path = "empty";
+    return SRW_OK;
+  }
+  return launch_forward(a, which);
+}
+
+srw_status_t srw_workspace_size_batch(int32_t n, const srw_desc_t* descs, size_t* bytes) {
+  if (n < 1 || n > SRW_MAX_BATCH || !descs || !bytes) return SRW_EINVAL;
+  size_t total = 0;
+  for (int32_t i = 0; i < n; ++i) {
+    size_t b = 0;
+    const srw_status_t st = srw_workspace_size(&descs[i], &b);
+    if (st != SRW_OK) return st;
+    total += align256(b);
+  }
+  *bytes = total;
+  return SRW_OK;
+}
+
+srw_status_t srw_forward_batch(int32_t n, const srw_desc_t* descs, const srw_tensors_t* ins,
+                               const srw_outputs_t* outs, void* workspace, size_t workspace_bytes, void* stream) {
+  if (n < 1 || n > SRW_MAX_BATCH || !descs || !ins || !outs) return SRW_EINVAL;
+  size_t need = 0;
+  srw_status_t st = srw_workspace_size_batch(n, descs, &need);
+  if (st != SRW_OK) return st;
+  if (need > 0 && (!workspace || workspace_bytes < need)) return SRW_EWORKSPACE;
+  // call i's workspace slice: the aligned sizes of calls 0 .. i-1 before it
+  srw::LaunchArgs a[SRW_MAX_BATCH];
+  int which[SRW_MAX_BATCH];
+  size_t off = 0;
+  bool all_mfma = true;
+  for (int32_t i = 0; i < n; ++i) {
+    size_t b = 0;
+    (void)srw_workspace_size(&descs[i], &b);
+    b = align256(b);
+    char* ws = b > 0 ? static_cast<char*>(workspace) + off : nullptr;
+    st = prepare_forward(&descs[i], &ins[i], &outs[i], ws, b, stream, &a[i], &which[i]);
+    if (st != SRW_OK) return st;
+    all_mfma = all_mfma && which[i] == 1;
+    off += b;
+  }
+  if (all_mfma && n > 1) {
+    (void)hipGetLastError();
+    const char* name = "mfma";
+    const hipError_t e = srw::mfma_forward_batch(a, n, &name);
+    if (e == hipSuccess) {
+      g_last_path = name;
+      return SRW_OK;
+    }
+    if (e != hipErrorNotSupported) return SRW_EHIP;
+  }
+  for (int32_t i = 0; i < n; ++i) {  // one after the other
+    if (which[i] == -2) continue;
+    st = launch_forward(a[i], which[i]);
+    if (st != SRW_OK) return st;
+  }
+  if (n > 1) g_last_path = "batch_sequential";
+  return SRW_OK;
 }
 
 srw_status_t srw_backward_workspace_size(const srw_desc_t* d, size_t* bytes) {

@@ -112,5 +112,8 @@ size_t mfma_workspace_bytes(const srw_desc_t& d);
 // h_is_x: h aliases x (d_route == d_model, one route), which some shapes need
 bool mfma_supports(const srw_desc_t& d, bool h_is_x);
 hipError_t mfma_forward(const LaunchArgs& a, const char** path_name);
+// Up to four decode-shaped calls in one launch per stage (srw_forward_batch);
+// hipErrorNotSupported, with nothing launched, when they cannot share one.
+hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name);
 
 }  // namespace srw

@@ -187,6 +187,21 @@ __host__ __device__ inline void split_range(const Geometry& g, int spc, int spli
   hi = static_cast<int64_t>(tb) * kUnitTile < c_hi ? static_cast<int64_t>(tb) * kUnitTile : c_hi;
 }
 
+// Several independent calls in one launch per stage (srw_forward_batch): the
+// parameters of each and the first block of each in the launch's grid.
+constexpr int kMaxBatch = 4;
+template <class P>
+struct Batch {
+  P p[kMaxBatch];
+  int start[kMaxBatch + 1];  // call i owns blocks [start[i], start[i + 1])
+  int n;
+};
+__device__ inline int batch_index(const int* start, int n, int bid) {
+  int i = 0;
+  for (int k = 1; k < n; ++k) i += bid >= start[k] ? 1 : 0;
+  return i;
+}
+
 // ---------------------------------------------------------------------------
 // pack: Wp[tile][db][j][lane][i] = W[32 tile + unit_of_k(j, lane/32, i)][32 db + lane%32]
 // (zero beyond N).  One thread per 16-byte output fragment row.
@@ -252,7 +267,7 @@ constexpr int kStatsPlain = 0, kStatsDiag = 1, kStatsCentered = 2;
 // fragment read from LDS feeds TBW MFMAs, and a CU's E stream serves
 // 128 TBW tokens.
 template <int KH, int MODE, int TBW>
-__global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
+__device__ __attribute__((always_inline)) inline void stats_body(const StatsParams& p, const int bid) {
   constexpr bool DG = MODE == kStatsDiag;
   constexpr int MS = DG ? 4 : 2;
   extern __shared__ __attribute__((aligned(1024))) char lds[];
@@ -261,8 +276,8 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = lane >> 5, col = lane & 31;
-  const int split = blockIdx.x % p.g.S_st;
-  const int ttile = blockIdx.x / p.g.S_st;
+  const int split = bid % p.g.S_st;
+  const int ttile = bid / p.g.S_st;
   int64_t tt[TBW], tl[TBW];
 #pragma unroll
   for (int b = 0; b < TBW; ++b) {
@@ -433,6 +448,16 @@ __global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
       }
     }
   }
+}
+
+template <int KH, int MODE, int TBW>
+__global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
+  stats_body<KH, MODE, TBW>(p, blockIdx.x);
+}
+template <int KH, int MODE>
+__global__ __launch_bounds__(kThreads) void srw_stats_batch_kernel(Batch<StatsParams> b) {
+  const int i = batch_index(b.start, b.n, blockIdx.x);
+  stats_body<KH, MODE, 1>(b.p[i], blockIdx.x - b.start[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1484,11 +1509,26 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p
 // mode kTauOnePass: std = sqrt(E[s^2] - mean^2) + 1e-8; kTauMean: store the
 // row mean in tau[] (input of the centred second pass); kTauCentered: std =
 // sqrt(sum (s - mean)^2 / N) + 1e-8 (v41:1719-1721).
-__global__ __launch_bounds__(256) void srw_tau_kernel(const float* __restrict__ mom, const float* __restrict__ tau_off,
-                                                      float* __restrict__ tau, int64_t T, int S_st, int64_t N, int ms,
-                                                      float* __restrict__ token_diag, int mode) {
+struct TauParams {
+  const float* mom;
+  const float* tau_off;
+  float* tau;
+  int64_t T;
+  int S_st;
+  int64_t N;
+  int ms;
+  float* token_diag;
+  int mode;
+};
+__device__ __attribute__((always_inline)) inline void tau_body(const TauParams& q, const int bid) {
+  const float* __restrict__ mom = q.mom;
+  const float* __restrict__ tau_off = q.tau_off;
+  float* __restrict__ tau = q.tau;
+  const int64_t T = q.T, N = q.N;
+  const int S_st = q.S_st, ms = q.ms, mode = q.mode;
+  float* __restrict__ token_diag = q.token_diag;
   const int lane = threadIdx.x & 63;
-  const int64_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t t = static_cast<int64_t>(bid) * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   float a = 0.f, b = 0.f, c = 0.f, d = 0.f;
   // unrolled so that the partials' loads go out together (the sums keep their order)
@@ -1528,6 +1568,11 @@ __global__ __launch_bounds__(256) void srw_tau_kernel(const float* __restrict__ 
     }
   }
 }
+__global__ __launch_bounds__(256) void srw_tau_kernel(TauParams q) { tau_body(q, blockIdx.x); }
+__global__ __launch_bounds__(256) void srw_tau_batch_kernel(Batch<TauParams> b) {
+  const int i = batch_index(b.start, b.n, blockIdx.x);
+  tau_body(b.p[i], blockIdx.x - b.start[i]);
+}
 
 // ---------------------------------------------------------------------------
 // finalize: reduce the N-splits, bf16-round each reference chunk's write GEMM,
@@ -1559,11 +1604,11 @@ struct FinalParams {
 // sums of a chunk combine in a fixed order, so the result is deterministic.
 // Few splits per chunk (large T) use NG = 1, many (decode) NG = 16.
 template <int NG>
-__global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
+__device__ __attribute__((always_inline)) inline void finalize_body(const FinalParams& p, const int bx) {
   constexpr int CW = 256 / NG;
   __shared__ float red[3][4];
   __shared__ float part[NG > 1 ? NG : 1][CW];
-  const int64_t t = blockIdx.x;
+  const int64_t t = bx;
   const int tid = threadIdx.x;
   const int g = tid / CW, c = tid % CW;
   float gs = 0.f, is = 0.f, na = 0.f;
@@ -1669,6 +1714,15 @@ __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
       td[SRW_TDIAG_INT_MAX] = imax;
     }
   }
+}
+template <int NG>
+__global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
+  finalize_body<NG>(p, blockIdx.x);
+}
+template <int NG>
+__global__ __launch_bounds__(256) void srw_finalize_batch_kernel(Batch<FinalParams> b) {
+  const int i = batch_index(b.start, b.n, blockIdx.x);
+  finalize_body<NG>(b.p[i], blockIdx.x - b.start[i]);
 }
 
 // Few splits per chunk (spc < 16: prefill-sized T): one wave per row, lane l
@@ -1782,14 +1836,17 @@ constexpr int decode_lds_bytes() {
   return TB * (DB * 2 + KH) * kFragBytes + 4 * TB * 32 * 3 * 4;
 }
 
-template <int TB, int DB, int KH>
-__global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
+// NT: the most tiles a split holds (the W^T registers are sized for it; two
+// at the small pools, whose splits hold one or two tiles)
+template <int TB, int DB, int KH, int NT>
+__device__ __attribute__((always_inline)) inline void decode_body(const MainParams& p, const int bid) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int D = DB * 32, DR = KH * 16, KX = D / 16, NDB = DB / 4;
   constexpr int FX = TB * KX, FH = TB * KH;
   static_assert(DB % 4 == 0, "four waves split the output column blocks");
   static_assert(FX % 4 == 0 && FH % 4 == 0, "fragments split evenly over the waves");
-  static_assert(FX >= kDecTiles * TB * 2, "P reuses the X region");
+  static_assert(NT >= 1 && NT <= kDecTiles, "one tile per wave at most");
+  static_assert(FX >= NT * TB * 2, "P reuses the X region");
   char* const xl = lds;                          // X fragments, later P
   char* const hl = lds + FX * kFragBytes;        // H fragments
   float* const red = reinterpret_cast<float*>(hl + FH * kFragBytes);  // [wave][TB][32][3]
@@ -1798,8 +1855,8 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
   const int half = lane >> 5, col = lane & 31;
   // workgroup = (split, row-block group): with rb > 1 (TB == 1) each
   // workgroup of a split takes one 32-row block, rows from row0
-  const int split = blockIdx.x / p.rb;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x % p.rb) * 32 * TB;
+  const int split = bid / p.rb;
+  const int64_t row0 = static_cast<int64_t>(bid % p.rb) * 32 * TB;
   int ta, tb;
   int64_t lo, hi;
   split_range(p.g, p.g.spc, split, ta, tb, lo, hi);
@@ -1838,9 +1895,9 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
 #pragma unroll
   for (int ks = 0; ks < KX; ++ks) rf[ks] = *reinterpret_cast<const u32x4_t*>(p.read + ur * D + 16 * ks + 8 * half);
   // W^T fragments of column blocks wave * NDB + c, for the split's tiles
-  u32x4_t wf[kDecTiles][2][NDB];
+  u32x4_t wf[NT][2][NDB];
 #pragma unroll
-  for (int i = 0; i < kDecTiles; ++i) {
+  for (int i = 0; i < NT; ++i) {
     if (i < ntl) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -1968,7 +2025,7 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
 #pragma unroll
     for (int c = 0; c < NDB; ++c) oacc[b][c] = f32x16_t{};
 #pragma unroll
-  for (int i = 0; i < kDecTiles; ++i) {
+  for (int i = 0; i < NT; ++i) {
     if (i < ntl) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -2002,6 +2059,17 @@ __global__ __launch_bounds__(256, 1) void srw_decode_kernel(MainParams p) {
     tp[1] = acc[1];
     tp[2] = acc[2];
   }
+}
+// two waves per SIMD (two workgroups per CU) where the registers allow: the
+// small pools' splits of one or two tiles
+template <int TB, int DB, int KH, int NT = kDecTiles>
+__global__ __launch_bounds__(256, NT <= 2 ? 2 : 1) void srw_decode_kernel(MainParams p) {
+  decode_body<TB, DB, KH, NT>(p, blockIdx.x);
+}
+template <int TB, int DB, int KH, int NT = kDecTiles>
+__global__ __launch_bounds__(256, NT <= 2 ? 2 : 1) void srw_decode_batch_kernel(Batch<MainParams> b) {
+  const int i = batch_index(b.start, b.n, blockIdx.x);
+  decode_body<TB, DB, KH, NT>(b.p[i], blockIdx.x - b.start[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -2070,8 +2138,11 @@ bool decode_applies(const srw_desc_t& d) {
 
 typedef void (*MainFn)(MainParams);
 template <int DB, int KH>
-void decode_for_rows(int64_t Tv, MainFn* fn, int* lds) {
-  if (Tv <= 32) {
+void decode_for_rows(int64_t Tv, int nt, MainFn* fn, int* lds) {
+  if (Tv <= 32 && nt <= 2) {
+    *fn = srw_decode_kernel<1, DB, KH, 2>;
+    *lds = decode_lds_bytes<1, DB, KH>();
+  } else if (Tv <= 32) {
     *fn = srw_decode_kernel<1, DB, KH>;
     *lds = decode_lds_bytes<1, DB, KH>();
   } else if (Tv <= 64) {
@@ -2082,20 +2153,36 @@ void decode_for_rows(int64_t Tv, MainFn* fn, int* lds) {
     *lds = decode_lds_bytes<4, DB, KH>();
   }
 }
-bool pick_decode(int64_t Tv, int D, int dr, MainFn* fn, int* lds) {
+// nt: the most tiles a split of the call holds (decode_max_tiles)
+bool pick_decode(int64_t Tv, int D, int dr, int nt, MainFn* fn, int* lds) {
   if (D == 384 && dr == 128) {
-    decode_for_rows<12, 8>(Tv, fn, lds);
+    decode_for_rows<12, 8>(Tv, nt, fn, lds);
     return true;
   }
   if (D == 128 && dr == 128) {
-    decode_for_rows<4, 8>(Tv, fn, lds);
+    decode_for_rows<4, 8>(Tv, nt, fn, lds);
     return true;
   }
   if (D == 128 && dr == 64) {
-    decode_for_rows<4, 4>(Tv, fn, lds);
+    decode_for_rows<4, 4>(Tv, nt, fn, lds);
     return true;
   }
   return false;
+}
+typedef void (*MainBatchFn)(Batch<MainParams>);
+template <int DB, int KH>
+MainBatchFn decode_batch_for(MainFn fn) {
+  if (fn == srw_decode_kernel<1, DB, KH, 2>) return srw_decode_batch_kernel<1, DB, KH, 2>;
+  if (fn == srw_decode_kernel<1, DB, KH>) return srw_decode_batch_kernel<1, DB, KH>;
+  if (fn == srw_decode_kernel<2, DB, KH>) return srw_decode_batch_kernel<2, DB, KH>;
+  if (fn == srw_decode_kernel<4, DB, KH>) return srw_decode_batch_kernel<4, DB, KH>;
+  return nullptr;
+}
+// the batch twin of a decode kernel pick_decode returned
+MainBatchFn decode_batch_of(MainFn fn) {
+  if (MainBatchFn b = decode_batch_for<12, 8>(fn)) return b;
+  if (MainBatchFn b = decode_batch_for<4, 8>(fn)) return b;
+  return decode_batch_for<4, 4>(fn);
 }
 int mom_stride(const srw_desc_t& d) { return with_diag(d) && d.stats_mode == SRW_STATS_ONEPASS ? 4 : 2; }
 int tok_part_stride(const srw_desc_t& d) { return with_diag(d) ? kTokPartDiag : 4; }
@@ -2145,16 +2232,20 @@ Geometry geometry(const srw_desc_t& d, int64_t chunk) {
   return g;
 }
 
-// Every split of the decode kernel holds 1 .. kDecTiles tiles.
-bool decode_splits_fit(const Geometry& g) {
+// The most tiles a split holds when every split of the decode kernel holds
+// 1 .. kDecTiles of them, else 0.
+int decode_max_tiles(const Geometry& g) {
+  int most = 0;
   for (int sp = 0; sp < g.S; ++sp) {
     int ta, tb;
     int64_t lo, hi;
     split_range(g, g.spc, sp, ta, tb, lo, hi);
-    if (tb <= ta || tb - ta > kDecTiles) return false;
+    if (tb <= ta || tb - ta > kDecTiles) return 0;
+    most = tb - ta > most ? tb - ta : most;
   }
-  return true;
+  return most;
 }
+bool decode_splits_fit(const Geometry& g) { return decode_max_tiles(g) > 0; }
 
 // The scores-streaming main kernel serves calls without diagnostics whose
 // moments come from the moments kernel (one-pass or centred statistics; the
@@ -2346,8 +2437,8 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     // that more CUs share the pool and each loads only its rows' X and H
     const int row_blocks = static_cast<int>((g.T + 31) / 32);
     mp.rb = (row_blocks > 1 && static_cast<int64_t>(g.S) * row_blocks <= kTargetBlocks) ? row_blocks : 1;
-    if (decode_applies(d) && pick_decode(mp.rb > 1 ? 32 : g.T, D, static_cast<int>(d.d_route), &dec, &dec_lds) &&
-        decode_splits_fit(g)) {
+    if (decode_applies(d) && decode_splits_fit(g) &&
+        pick_decode(mp.rb > 1 ? 32 : g.T, D, static_cast<int>(d.d_route), decode_max_tiles(g), &dec, &dec_lds)) {
       *path_name = "mfma_decode_bf16";
       if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(dec), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    dec_lds)) != hipSuccess)
@@ -2400,12 +2491,15 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
 
 hipError_t launch_tau(const float* mom, const float* tau_off, float* tau, int64_t T, int S_st, int64_t N, int ms,
                       float* token_diag, int mode, hipStream_t s) {
-  hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, s, mom, tau_off, tau, T,
-                     S_st, N, ms, token_diag, mode);
+  const TauParams q{mom, tau_off, tau, T, S_st, N, ms, token_diag, mode};
+  hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, s, q);
   return hipGetLastError();
 }
 
-hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
+// split groups per finalize workgroup from the splits per chunk
+int finalize_groups(int spc) { return spc >= 32 ? 16 : (spc >= 16 ? 4 : 1); }
+
+FinalParams final_params_of(const FinalizeArgs& f) {
   FinalParams fp{};
   fp.out_part = f.out_part;
   fp.tok_part = f.tok_part;
@@ -2424,8 +2518,12 @@ hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
   fp.token_diag = f.token_diag;
   fp.gp = f.gp;
   fp.exp_scale = f.exp_scale;
-  // split groups per workgroup from the splits per chunk
-  const int ng = f.spc >= 64 ? 16 : (f.spc >= 16 ? 4 : 1);
+  return fp;
+}
+
+hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
+  const FinalParams fp = final_params_of(f);
+  const int ng = finalize_groups(f.spc);
   if (ng == 1 && (f.D == 64 || f.D == 128 || f.D == 384)) {
     const dim3 grid_r(static_cast<unsigned>((f.T + 3) / 4));
     if (f.D == 64) hipLaunchKernelGGL(srw_finalize_rows_kernel<1>, grid_r, dim3(256), 0, s, fp);
@@ -2437,6 +2535,168 @@ hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
   if (ng == 16) hipLaunchKernelGGL(srw_finalize_kernel<16>, grid_f, dim3(256), 0, s, fp);
   else if (ng == 4) hipLaunchKernelGGL(srw_finalize_kernel<4>, grid_f, dim3(256), 0, s, fp);
   else hipLaunchKernelGGL(srw_finalize_kernel<1>, grid_f, dim3(256), 0, s, fp);
+  return hipGetLastError();
+}
+
+// Several decode-shaped calls, one launch per stage (srw_forward_batch):
+// every call must take the decode kernel with the same instantiation, the
+// same moments kernel and the same finalize grouping; otherwise nothing is
+// launched and hipErrorNotSupported returned (the caller runs the calls one
+// by one).  Each call keeps its own geometry, workspace and outputs, and its
+// blocks run exactly the code of its own srw_forward: equal bits.
+hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name) {
+  if (n < 1 || n > kMaxBatch) return hipErrorNotSupported;
+  Geometry g[kMaxBatch];
+  WsLayout L[kMaxBatch];
+  MainFn dec = nullptr;
+  int dec_lds = 0, rb[kMaxBatch];
+  const srw_desc_t& d0 = a[0].d;
+  for (int i = 0; i < n; ++i) {
+    const srw_desc_t& d = a[i].d;
+    if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM || !decode_applies(d)) return hipErrorNotSupported;
+    if (d.d_model != d0.d_model || d.d_route != d0.d_route || d.stats_mode != d0.stats_mode)
+      return hipErrorNotSupported;
+    g[i] = geometry(d, a[i].chunk);
+    L[i] = ws_layout(d, g[i]);
+    if (a[i].ws_bytes < L[i].total) return hipErrorInvalidValue;
+    if (!decode_splits_fit(g[i])) return hipErrorNotSupported;
+    const int row_blocks = static_cast<int>((g[i].T + 31) / 32);
+    rb[i] = (row_blocks > 1 && static_cast<int64_t>(g[i].S) * row_blocks <= kTargetBlocks) ? row_blocks : 1;
+    MainFn fn = nullptr;
+    int lds = 0;
+    if (!pick_decode(rb[i] > 1 ? 32 : g[i].T, static_cast<int>(d.d_model), static_cast<int>(d.d_route),
+                     decode_max_tiles(g[i]), &fn, &lds))
+      return hipErrorNotSupported;
+    if (i > 0 && (fn != dec || finalize_groups(g[i].spc) != finalize_groups(g[0].spc))) return hipErrorNotSupported;
+    dec = fn;
+    dec_lds = lds;
+  }
+  if (finalize_groups(g[0].spc) == 1) return hipErrorNotSupported;  // the row-per-wave finalize has no batch form
+  const int D = static_cast<int>(d0.d_model);
+  const int KH = static_cast<int>(d0.d_route / 16);
+  const bool centered = d0.stats_mode == SRW_STATS_CENTERED;
+  const hipStream_t st = a[0].stream;
+  hipError_t e;
+  *path_name = "mfma_decode_batch_bf16";
+
+  // per call: pack W^T unless cached (its own launch)
+  for (int i = 0; i < n; ++i) {
+    if (a[i].d.flags & SRW_FLAG_POOL_CACHED) continue;
+    if ((e = pack_unit_major(static_cast<const uint16_t*>(a[i].in.write), reinterpret_cast<uint16_t*>(a[i].ws + L[i].wp),
+                             a[i].d.n_units, D, st)) != hipSuccess)
+      return e;
+  }
+  // moments (and for centred statistics the row means, then the second pass)
+  void (*stats_plain)(Batch<StatsParams>) = nullptr;
+  void (*stats_cent)(Batch<StatsParams>) = nullptr;
+  if (KH == 8) {
+    stats_plain = srw_stats_batch_kernel<8, kStatsPlain>;
+    stats_cent = srw_stats_batch_kernel<8, kStatsCentered>;
+  } else if (KH == 4) {
+    stats_plain = srw_stats_batch_kernel<4, kStatsPlain>;
+    stats_cent = srw_stats_batch_kernel<4, kStatsCentered>;
+  } else {
+    return hipErrorNotSupported;
+  }
+  Batch<StatsParams> sb{};
+  Batch<TauParams> tb{};
+  sb.n = tb.n = n;
+  for (int i = 0; i < n; ++i) {
+    StatsParams& sp = sb.p[i];
+    sp.h = static_cast<const uint16_t*>(a[i].in.h);
+    sp.emb = static_cast<const uint16_t*>(a[i].in.emb);
+    sp.mom = reinterpret_cast<float*>(a[i].ws + L[i].mom);
+    sp.mask32 = reinterpret_cast<uint32_t*>(a[i].o.pass_mask);
+    sp.mask_words32 = 2 * a[i].words;
+    sp.g = g[i];
+    sb.start[i + 1] = sb.start[i] + g[i].TT_st * g[i].S_st;
+    tb.p[i] = TauParams{sp.mom, a[i].in.tau_offset, reinterpret_cast<float*>(a[i].ws + L[i].tau), g[i].T,
+                        g[i].S_st, g[i].N, 2, nullptr, centered ? kTauMean : kTauOnePass};
+    tb.start[i + 1] = tb.start[i] + static_cast<int>((g[i].T + 3) / 4);
+  }
+  const size_t smem = static_cast<size_t>(2 * KH) * kFragBytes;
+  for (auto fn : {stats_plain, stats_cent})
+    if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 static_cast<int>(smem))) != hipSuccess)
+      return e;
+  hipLaunchKernelGGL(stats_plain, dim3(static_cast<unsigned>(sb.start[n])), dim3(kThreads), smem, st, sb);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(srw_tau_batch_kernel, dim3(static_cast<unsigned>(tb.start[n])), dim3(256), 0, st, tb);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (centered) {
+    for (int i = 0; i < n; ++i) {
+      sb.p[i].mean = tb.p[i].tau;
+      sb.p[i].mask32 = nullptr;  // the first pass cleared the shared mask words
+      tb.p[i].mode = kTauCentered;
+    }
+    hipLaunchKernelGGL(stats_cent, dim3(static_cast<unsigned>(sb.start[n])), dim3(kThreads), smem, st, sb);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(srw_tau_batch_kernel, dim3(static_cast<unsigned>(tb.start[n])), dim3(256), 0, st, tb);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  // decode kernel
+  Batch<MainParams> mb{};
+  mb.n = n;
+  for (int i = 0; i < n; ++i) {
+    const srw_desc_t& d = a[i].d;
+    MainParams& mp = mb.p[i];
+    mp.x = static_cast<const uint16_t*>(a[i].in.x);
+    mp.routes = d.n_routes;
+    mp.h = static_cast<const uint16_t*>(a[i].in.h);
+    mp.emb = static_cast<const uint16_t*>(a[i].in.emb);
+    mp.read = static_cast<const uint16_t*>(a[i].in.read);
+    mp.wp = reinterpret_cast<const uint16_t*>(a[i].ws + L[i].wp);
+    mp.tau = tb.p[i].tau;
+    mp.out_part = reinterpret_cast<float*>(a[i].ws + L[i].out_part);
+    mp.tok_part = reinterpret_cast<float*>(a[i].ws + L[i].tok_part);
+    mp.mask32 = reinterpret_cast<uint32_t*>(a[i].o.pass_mask);
+    mp.mask_words32 = 2 * a[i].words;
+    mp.g = g[i];
+    mp.gp = a[i].gp;
+    mp.exp_scale = -d.sharpness * 1.4426950408889634f;
+    mp.rb = rb[i];
+    mb.start[i + 1] = mb.start[i] + g[i].S * rb[i];
+  }
+  MainBatchFn dec_batch = decode_batch_of(dec);
+  if (!dec_batch) return hipErrorNotSupported;
+  if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(dec_batch), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               dec_lds)) != hipSuccess)
+    return e;
+  dominant_kernel_begin(st);
+  hipLaunchKernelGGL(dec_batch, dim3(static_cast<unsigned>(mb.start[n])), dim3(kThreads),
+                     static_cast<size_t>(dec_lds), st, mb);
+  dominant_kernel_end(st);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  // finalize
+  Batch<FinalParams> fb{};
+  fb.n = n;
+  for (int i = 0; i < n; ++i) {
+    const srw_desc_t& d = a[i].d;
+    FinalizeArgs f{};
+    f.out_part = mb.p[i].out_part;
+    f.tok_part = mb.p[i].tok_part;
+    f.out = static_cast<uint16_t*>(a[i].o.out);
+    f.gate_sum = a[i].o.gate_sum;
+    f.den = a[i].o.den;
+    f.n_active = a[i].o.n_active;
+    f.T = g[i].T;
+    f.D = D;
+    f.S = g[i].S;
+    f.spc = g[i].spc;
+    f.S_tok = g[i].S;
+    f.tps = tok_part_stride(d);
+    f.scale = d.scale;
+    f.tau = tb.p[i].tau;
+    f.token_diag = nullptr;
+    f.gp = a[i].gp;
+    f.exp_scale = -d.sharpness * 1.4426950408889634f;
+    fb.p[i] = final_params_of(f);
+    fb.start[i + 1] = fb.start[i] + static_cast<int>(g[i].T);
+  }
+  const int ng = finalize_groups(g[0].spc);
+  const dim3 grid_f(static_cast<unsigned>(fb.start[n]), static_cast<unsigned>((D + 256 / ng - 1) / (256 / ng)));
+  if (ng == 16) hipLaunchKernelGGL(srw_finalize_batch_kernel<16>, grid_f, dim3(256), 0, st, fb);
+  else hipLaunchKernelGGL(srw_finalize_batch_kernel<4>, grid_f, dim3(256), 0, st, fb);
   return hipGetLastError();
 }
 

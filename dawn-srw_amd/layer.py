@@ -173,6 +173,62 @@ class SrwPlan:
                     path=self.path, workspace=self.workspace)
 
 
+class SrwBatchPlan:
+    """Several bound calls enqueued together through ``srw_forward_batch``.
+
+    The plans' descriptors, tensors and outputs are taken over (each plan's
+    results land in its own output tensors, as after its own launch); the
+    workspace is one batch workspace, sliced in plan order, so the plans' own
+    workspaces are not used.  Calls that all take the decode kernel with the
+    same shapes class (the QK and V calls of a decode step) run as one launch
+    per stage; others run one after the other -- the results equal separate
+    launches bit for bit either way.
+    """
+
+    def __init__(self, plans):
+        plans = list(plans)
+        if not 1 <= len(plans) <= C.MAX_BATCH:
+            raise ValueError(f"a batch holds 1 to {C.MAX_BATCH} plans, got {len(plans)}")
+        dev = plans[0].device
+        if any(p.device != dev for p in plans):
+            raise ValueError("the plans of a batch share one device")
+        n = len(plans)
+        self.plans = plans
+        self.device = dev
+        self._descs = (C.SrwDesc * n)(*[p._desc for p in plans])
+        self._tens = (C.SrwTensors * n)(*[p._tens for p in plans])
+        self._outs = (C.SrwOutputs * n)(*[p._outs for p in plans])
+        self.ws_bytes = C.workspace_size_batch(self._descs)
+        self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
+        self._lib = C.load_library()
+        self.path = None
+
+    def launch(self, stream=None, pool_cached: bool = False) -> None:
+        """Enqueue the calls on ``stream`` (default: torch's current stream);
+        ``pool_cached`` as in :meth:`SrwPlan.launch`, relative to this batch's
+        previous launch."""
+        if stream is None:
+            with torch.cuda.device(self.device):
+                stream = torch.cuda.current_stream(self.device)
+        if pool_cached and self.path is None:
+            raise ValueError("pool_cached needs an earlier launch of this batch")
+        base = [d.flags for d in self._descs]
+        if pool_cached:
+            for d in self._descs:
+                d.flags = d.flags | C.SRW_FLAG_POOL_CACHED
+        try:
+            C.check(self._lib.srw_forward_batch(
+                len(self.plans), self._descs, self._tens, self._outs,
+                _ptr(self.workspace), ctypes.c_size_t(self.ws_bytes),
+                ctypes.c_void_p(stream.cuda_stream)))
+        finally:
+            for d, f in zip(self._descs, base):
+                d.flags = f
+        self.path = C.last_path()
+        for p in self.plans:
+            p.path = self.path
+
+
 def srw_forward(x, h, emb, tau_offset, read, write, *, gate: str = "v41",
                 stats: str = "onepass", consts: GateConfig = GateConfig(),
                 scale: float = 1.0, chunk_size: int = 0, diag: bool = False,

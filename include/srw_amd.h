@@ -57,7 +57,7 @@
 extern "C" {
 #endif
 
-#define SRW_AMD_ABI_VERSION 4
+#define SRW_AMD_ABI_VERSION 5
 
 typedef enum srw_status {
   SRW_OK = 0,
@@ -229,6 +229,23 @@ srw_status_t srw_workspace_size(const srw_desc_t* desc, size_t* bytes);
 srw_status_t srw_forward(const srw_desc_t* desc, const srw_tensors_t* in,
                          const srw_outputs_t* outs, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* Several independent srw_forward calls on one stream.  No counterpart in
+ * the reference, whose layer issues each pool's SRW as a call of its own
+ * (the Q, K and V projections, v41:1784-1799 in the KV-cache step and
+ * :1036-1053 in the forward): equivalent to srw_forward(&descs[i], &ins[i],
+ * &outs[i], ws_i, bytes_i, stream) for i = 0 .. n-1 in order, where ws_i is
+ * call i's slice of `workspace` (srw_workspace_size_batch), with equal
+ * results bit for bit.  Calls that all take the decode kernel (at most 128
+ * rows, bf16, no diagnostics) with the same d_model, d_route and statistics
+ * run as one launch per stage -- the small pools' calls are bound by their
+ * launches; otherwise the calls run one after the other.  1 <= n <=
+ * SRW_MAX_BATCH; the calls must not share outputs. */
+#define SRW_MAX_BATCH 4
+srw_status_t srw_workspace_size_batch(int32_t n, const srw_desc_t* descs, size_t* bytes);
+srw_status_t srw_forward_batch(int32_t n, const srw_desc_t* descs, const srw_tensors_t* ins,
+                               const srw_outputs_t* outs, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* Validate *desc for srw_backward and report its workspace (device bytes). */
 srw_status_t srw_backward_workspace_size(const srw_desc_t* desc, size_t* bytes);

@@ -137,6 +137,31 @@ def test_no_tokens_need_no_workspace(C, shape):
     assert C.workspace_size(d) > 0 and C.backward_workspace_size(d) > 0
 
 
+def test_batch_workspace_is_the_aligned_sum(C):
+    """srw_workspace_size_batch: call i's workspace slice follows the 256-byte
+    aligned slices of calls 0 .. i-1 (srw_forward_batch)."""
+    al = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    descs = (C.SrwDesc * 3)(_desc(C), _desc(C, d_route=64), _desc(C, T=100, n_units=777))
+    want = sum(al(C.workspace_size(d)) for d in descs)
+    assert C.workspace_size_batch(descs) == want
+    assert C.workspace_size_batch((C.SrwDesc * 1)(descs[1])) == al(C.workspace_size(descs[1]))
+
+
+def test_batch_arguments_checked_before_any_launch(C):
+    lib = C.load_library()
+    n = ctypes.c_size_t(0)
+    five = (C.SrwDesc * 5)(*[_desc(C)] * 5)
+    assert lib.srw_workspace_size_batch(0, five, ctypes.byref(n)) == C.SRW_EINVAL
+    assert lib.srw_workspace_size_batch(5, five, ctypes.byref(n)) == C.SRW_EINVAL
+    bad = (C.SrwDesc * 2)(_desc(C), _desc(C, d_model=0))
+    assert lib.srw_workspace_size_batch(2, bad, ctypes.byref(n)) == C.SRW_EINVAL
+    t, o = (C.SrwTensors * 2)(), (C.SrwOutputs * 2)()
+    good = (C.SrwDesc * 2)(_desc(C), _desc(C))
+    # null tensors, then too small a workspace: refused on the host
+    assert lib.srw_forward_batch(2, good, t, o, None, 0, None) in (C.SRW_EINVAL, C.SRW_EWORKSPACE)
+    assert lib.srw_forward_batch(2, good, None, o, None, 0, None) == C.SRW_EINVAL
+
+
 def test_status_strings(C):
     lib = C.load_library()
     for s in range(5):

@@ -133,3 +133,65 @@ def test_decode_matches_prefill_kernel(pkg, dev):
     assert torch.allclose(dec["den"], pre["den"][:T], rtol=1e-4)
     mism = (unpack_mask(dec["pass_mask"][:, 0], N) != unpack_mask(pre["pass_mask"][:T, 0], N)).sum()
     assert int(mism) <= 4
+
+
+def _pool(pkg, T, N, routes, seed, D=384, dr=128):
+    shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=routes)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=seed)
+    inp["tau_offset"].uniform_(-0.9, 0.5, generator=torch.Generator().manual_seed(seed))
+    return inp
+
+
+def _plan(pkg, dev, inp, stats, max_chunk=12500):
+    _, cs = srw_ref.chunk_plan(inp["emb"].shape[0], max_chunk)
+    return pkg.SrwPlan(*(inp[k].to(BF).to(dev) if k != "tau_offset" else inp[k].to(dev)
+                         for k in ("x", "h", "emb", "tau_offset", "read", "write")),
+                       stats=stats, chunk_size=cs if stats == "onepass" else 0, want_mask=True)
+
+
+_KEYS = ("out", "gate_sum", "den", "n_active", "pass_mask")
+
+
+def _check_batch(pkg, dev, inps, stats, want_path):
+    """srw_forward_batch of the calls equals their separate launches bit for
+    bit: uncached, then with the pool declared cached."""
+    sep = [_plan(pkg, dev, inp, stats) for inp in inps]
+    for p in sep:
+        p.launch()
+    bat = pkg.SrwBatchPlan([_plan(pkg, dev, inp, stats) for inp in inps])
+    for cached in (False, True):
+        bat.launch(pool_cached=cached)
+        torch.cuda.synchronize()
+        assert bat.path == want_path, bat.path
+        for i, (a, b) in enumerate(zip(sep, bat.plans)):
+            ra, rb = a.results(), b.results()
+            for k in _KEYS:
+                assert torch.equal(ra[k], rb[k]), (i, k, cached)
+
+
+@pytest.mark.parametrize("stats", ["onepass", "centered"])
+def test_batch_qk_v_decode_one_launch_per_stage(pkg, dev, stats):
+    """The QK (paired routes, 128 rows) and V calls of a decode step, as one
+    launch per stage."""
+    print(f"[gpu] decode batch QK+V {stats}", flush=True)
+    inps = [_pool(pkg, 64, 1580, 2, 51), _pool(pkg, 64, 2600, 1, 52)]
+    _check_batch(pkg, dev, inps, stats, "mfma_decode_batch_bf16")
+
+
+def test_batch_three_small_pools_one_launch_per_stage(pkg, dev):
+    print("[gpu] decode batch three calls", flush=True)
+    inps = [_pool(pkg, 64, 1580, 1, 53), _pool(pkg, 64, 1580, 1, 54), _pool(pkg, 20, 2600, 1, 55)]
+    _check_batch(pkg, dev, inps, "centered", "mfma_decode_batch_bf16")
+
+
+@pytest.mark.parametrize("which", ["prefill_and_decode", "know_and_qk"])
+def test_batch_that_cannot_share_launches_runs_one_by_one(pkg, dev, which):
+    """A prefill-sized call, or decode calls of different kernel shapes (the
+    Know pool's four-tile splits against the small pools' row blocks): the
+    calls run one after the other, with the same results."""
+    print(f"[gpu] decode batch fallback {which}", flush=True)
+    if which == "prefill_and_decode":
+        inps = [_pool(pkg, 300, 1580, 1, 56), _pool(pkg, 64, 2600, 1, 57)]
+    else:
+        inps = [_pool(pkg, 64, 25200, 1, 58), _pool(pkg, 64, 1580, 2, 59)]
+    _check_batch(pkg, dev, inps, "onepass", "batch_sequential")
