@@ -1731,9 +1731,9 @@ __global__ __launch_bounds__(256) void srw_finalize_batch_kernel(Batch<FinalPara
 // kernel above (eight accumulators, a fixed tree), so both give the same
 // bits; the per-row partials and diagnostics are reduced across the wave.
 template <int DC>  // d_model / 64
-__global__ __launch_bounds__(256) void srw_finalize_rows_kernel(FinalParams p) {
+__device__ __attribute__((always_inline)) inline void finalize_rows_body(const FinalParams& p, const int bid) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t t = static_cast<int64_t>(bid) * 4 + (threadIdx.x >> 6);
   if (t >= p.T) return;
   float gs = 0.f, is = 0.f, na = 0.f;
   for (int s = lane; s < p.S_tok; s += 64) {
@@ -1813,6 +1813,16 @@ __global__ __launch_bounds__(256) void srw_finalize_rows_kernel(FinalParams p) {
       td[SRW_TDIAG_INT_MAX] = imax;
     }
   }
+}
+
+template <int DC>
+__global__ __launch_bounds__(256) void srw_finalize_rows_kernel(FinalParams p) {
+  finalize_rows_body<DC>(p, blockIdx.x);
+}
+template <int DC>
+__global__ __launch_bounds__(256) void srw_finalize_rows_batch_kernel(Batch<FinalParams> b) {
+  const int i = batch_index(b.start, b.n, blockIdx.x);
+  finalize_rows_body<DC>(b.p[i], blockIdx.x - b.start[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -2571,7 +2581,9 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     dec = fn;
     dec_lds = lds;
   }
-  if (finalize_groups(g[0].spc) == 1) return hipErrorNotSupported;  // the row-per-wave finalize has no batch form
+  const int ng = finalize_groups(g[0].spc);
+  const bool rows_fin = ng == 1;  // the row-per-wave finalize, as launch_finalize picks it
+  if (rows_fin && d0.d_model != 64 && d0.d_model != 128 && d0.d_model != 384) return hipErrorNotSupported;
   const int D = static_cast<int>(d0.d_model);
   const int KH = static_cast<int>(d0.d_route / 16);
   const bool centered = d0.stats_mode == SRW_STATS_CENTERED;
@@ -2691,9 +2703,15 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     f.gp = a[i].gp;
     f.exp_scale = -d.sharpness * 1.4426950408889634f;
     fb.p[i] = final_params_of(f);
-    fb.start[i + 1] = fb.start[i] + static_cast<int>(g[i].T);
+    fb.start[i + 1] = fb.start[i] + static_cast<int>(rows_fin ? (g[i].T + 3) / 4 : g[i].T);
   }
-  const int ng = finalize_groups(g[0].spc);
+  if (rows_fin) {
+    const dim3 grid_r(static_cast<unsigned>(fb.start[n]));
+    if (D == 64) hipLaunchKernelGGL(srw_finalize_rows_batch_kernel<1>, grid_r, dim3(256), 0, st, fb);
+    else if (D == 128) hipLaunchKernelGGL(srw_finalize_rows_batch_kernel<2>, grid_r, dim3(256), 0, st, fb);
+    else hipLaunchKernelGGL(srw_finalize_rows_batch_kernel<6>, grid_r, dim3(256), 0, st, fb);
+    return hipGetLastError();
+  }
   const dim3 grid_f(static_cast<unsigned>(fb.start[n]), static_cast<unsigned>((D + 256 / ng - 1) / (256 / ng)));
   if (ng == 16) hipLaunchKernelGGL(srw_finalize_batch_kernel<16>, grid_f, dim3(256), 0, st, fb);
   else hipLaunchKernelGGL(srw_finalize_batch_kernel<4>, grid_f, dim3(256), 0, st, fb);

@@ -25,7 +25,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from .layer import GateConfig, SrwPlan
+from .layer import GateConfig, SrwBatchPlan, SrwPlan
 from .srw import chunk_plan
 
 __all__ = ["DawnConfig", "init_params", "DawnModel"]
@@ -131,6 +131,26 @@ class _PoolCall:
         return self.plan.out
 
 
+class _BatchCall:
+    """Several pools' calls on the same rows as one ``srw_forward_batch``
+    (one launch per stage when all take the decode kernel; the results equal
+    separate calls bit for bit).  ``plan`` is the batch plan."""
+
+    def __init__(self, *calls):
+        self.calls = calls
+        self.plan = SrwBatchPlan([c.plan for c in calls])
+        self.launches = 0
+
+    def __call__(self, *args):
+        for c, (x, h, tau) in zip(self.calls, args):
+            c.x.copy_(x)
+            c.h.copy_(h)
+            c.tau.copy_(tau)
+        self.plan.launch(pool_cached=self.launches > 0)
+        self.launches += 1
+        return [c.plan.out for c in self.calls]
+
+
 class DawnModel:
     """Inference on one HIP device.
 
@@ -140,7 +160,8 @@ class DawnModel:
     are the reference's KV-cache inference API (v41:1836-1957), whose SRW
     layer is ``_srw_inference`` (two-pass centred statistics, unchunked); it
     runs here in bf16 on the matrix cores, Q and K as one paired call over
-    one x.R^T (the reference computes x.R^T twice, :1788-1793).
+    one x.R^T (the reference computes x.R^T twice, :1788-1793); at decode
+    sizes the QK and V calls of a layer are one ``srw_forward_batch``.
     """
 
     def __init__(self, params: dict, cfg: DawnConfig, device="cuda:0"):
@@ -171,6 +192,14 @@ class DawnModel:
             self._calls[key] = c
         return c
 
+    def _qkv_batch(self, T, stats):
+        key = ("qk+v", T, 1, stats)
+        b = self._calls.get(key)
+        if b is None:
+            b = _BatchCall(self._pool("qk", T, 2, stats), self._pool("v", T, 1, stats))
+            self._calls[key] = b
+        return b
+
     @staticmethod
     def _ln(x, prm):
         return F.layer_norm(x, (x.shape[-1],), prm["scale"], prm["bias"], eps=1e-6)  # v41:321-324
@@ -186,8 +215,14 @@ class DawnModel:
         T, dr = normed.shape[0], cfg.d_route
         h_all = self._dense(normed, rt["proj_attn"])                    # :1018
         tau_all = self._dense(normed, rt["tau_attn"])                   # :1022
-        qk = self._pool("qk", T, 2, stats)(normed, h_all[:, :2 * dr].reshape(T, 2, dr), tau_all[:, :2])
-        v = self._pool("v", T, 1, stats)(normed, h_all[:, 2 * dr:].reshape(T, 1, dr), tau_all[:, 2:3])
+        qk_args = (normed, h_all[:, :2 * dr].reshape(T, 2, dr), tau_all[:, :2])
+        v_args = (normed, h_all[:, 2 * dr:].reshape(T, 1, dr), tau_all[:, 2:3])
+        if 2 * T <= 128:
+            # decode-sized: both calls in one srw_forward_batch
+            qk, v = self._qkv_batch(T, stats)(qk_args, v_args)
+        else:
+            qk = self._pool("qk", T, 2, stats)(*qk_args)
+            v = self._pool("v", T, 1, stats)(*v_args)
         q = qk[:, 0].float() * self.scale["qk"]                         # :1044-1045
         k = qk[:, 1].float() * self.scale["qk"]
         v = v[:, 0].float() * self.scale["v"]                           # :1053

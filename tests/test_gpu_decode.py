@@ -195,3 +195,11 @@ def test_batch_that_cannot_share_launches_runs_one_by_one(pkg, dev, which):
     else:
         inps = [_pool(pkg, 64, 25200, 1, 58), _pool(pkg, 64, 1580, 2, 59)]
     _check_batch(pkg, dev, inps, "onepass", "batch_sequential")
+
+
+def test_batch_with_row_per_wave_finalize(pkg, dev):
+    """Pools of under 16 splits per chunk finalize one wave per row: the
+    batch takes that kernel's batch form (the model's small test pools)."""
+    print("[gpu] decode batch row finalize", flush=True)
+    inps = [_pool(pkg, 5, 300, 2, 60, D=128, dr=64), _pool(pkg, 5, 500, 1, 61, D=128, dr=64)]
+    _check_batch(pkg, dev, inps, "centered", "mfma_decode_batch_bf16")

@@ -59,6 +59,8 @@ def test_prefill_and_decode_match_oracle(small):
     w_lg, w_cK, w_cV, _ = dawn_ref.prefill(params, cfg, ids[:, :32])
     w_step, w_cK, w_cV, _ = dawn_ref.decode_step(params, cfg, ids[:, 32], w_cK, w_cV, 32)
     assert n2 == 33
+    # the decode step's QK and V calls ran as one batch of decode kernels
+    assert m._calls[("qk+v", 3, 1, "centered")].plan.path == "mfma_decode_batch_bf16"
     for name, a, b in (("prefill logits", lg, w_lg), ("decode logits", step, w_step),
                        ("cache K", cK[:, :, :, :33], w_cK[:, :, :, :33]),
                        ("cache V", cV[:, :, :, :33], w_cV[:, :, :, :33])):
