@@ -1228,14 +1228,16 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
 // with the bf16 scores read back from the moments kernel's score buffer
 // (kScoreTileBytes per (token tile, unit tile)) instead of recomputed -- the
 // same bf16 values: the same fragments, MFMA and k order produced them.
-// Producers (waves 0-3) run only the read GEMM XR^T = R_t.X^T and hand the
-// bf16 x.r (v41:517) to a double-buffered LDS stage; consumers (waves 4-7)
-// load their 32 x 32 score block of the next tile (2 KB per wave, direct
-// global->LDS, beside the tile's W^T), run the gate epilogue of the current
-// one and its write GEMM.  With every stage doubled one workgroup barrier
-// per tile suffices: a stage is rewritten two tiles after it was filled,
-// past the barrier that ends the reads of it.  LDS = 2 R + 2 W^T + 2 x.r +
-// 2 score stages (128 KB at d_model = 384).
+// Producers (waves 0-3) run only the read GEMM XR^T = R_t.X^T, hand the
+// bf16 x.r (v41:517) to a double-buffered LDS stage, and issue every load of
+// the workgroup beside their MFMAs: the next tile's R, this tile's W^T and
+// the consumers' 32 x 32 score blocks (2 KB per token block; the producers'
+// MFMA stream has the slack, the consumers' epilogue is the critical path).
+// Consumers (waves 4-7) run the gate epilogue of the previous tile and its
+// write GEMM, and never wait for memory.  With every stage doubled one
+// workgroup barrier per tile suffices: a stage is rewritten two tiles after
+// it was filled, past the barrier that ends the reads of it.  LDS = 2 R +
+// 2 W^T + 2 x.r + 2 score stages (128 KB at d_model = 384).
 // ---------------------------------------------------------------------------
 template <int DB>
 constexpr int ss_lds_bytes() {
@@ -1292,6 +1294,15 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p
               w_base + stage * W_STAGE + (PW * blk + q) * kFragBytes);
   };
 
+  // this wave's score blocks: tile u at s_src + u * kScoreTileBytes (elements 0-7), + 1 KB (8-15)
+  const char* const s_src =
+      reinterpret_cast<const char*>(p.s_in) + score_tile_off(p.g.ntiles, ttile, 0, blk) + lane * 16;
+  auto s_load = [&](int tile, int stage) {
+    const char* src = s_src + static_cast<int64_t>(tile) * kScoreTileBytes;
+    g2lds16_nt(src, s_wave + stage * S_STAGE);  // read once
+    g2lds16_nt(src + kFragBytes, s_wave + stage * S_STAGE + kFragBytes);
+  };
+
   // prologue: R of the first tile
   if (n > 0 && producer) {
 #pragma unroll
@@ -1329,6 +1340,11 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p
 #pragma unroll
           for (int q = 0; q < PR; ++q)
             if (k == q * KX / (2 * PR) && pre) r_load(ta + it + 1, (it + 1) & 1, q);  // first half
+          // this tile's W^T and scores, for the consumers' next iteration
+#pragma unroll
+          for (int q = 0; q < PW; ++q)
+            if (k == KX / 2 + q * (KX / 2 - 1) / (PW + 1)) w_load(ta + it, it & 1, q);
+          if (k == KX - 1) s_load(ta + it, it & 1);
           const u32x4_t a = fr[k % PF];
           if (k + PF < KX) fr[k % PF] = frag(k + PF);
           racc = mfma(a, xq[k], racc);
@@ -1360,20 +1376,10 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p
     f32x16_t oacc[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
-    // this wave's score blocks: tile u at s_src + u * kScoreTileBytes (elements 0-7), + 1 KB (8-15)
-    const char* const s_src =
-        reinterpret_cast<const char*>(p.s_in) + score_tile_off(p.g.ntiles, ttile, 0, blk) + lane * 16;
-    auto s_load = [&](int tile, int stage) {
-      const char* src = s_src + static_cast<int64_t>(tile) * kScoreTileBytes;
-      g2lds16_nt(src, s_wave + stage * S_STAGE);  // read once
-      g2lds16_nt(src + kFragBytes, s_wave + stage * S_STAGE + kFragBytes);
-    };
-
     // gate epilogue (v41:503-518) of one tile from its bf16 scores and x.r
     // (LDS): P (k-step j in pk[4j..4j+3]) and the pass bits (element v at bit
-    // 15 - v); the next tile's W^T and score loads go out between element pairs
-    auto gate_tile = [&](auto full_tag, int64_t u0, uint32_t* pk, int wtile, int wstage, const char* srp,
-                         const char* xrp) -> uint32_t {
+    // 15 - v)
+    auto gate_tile = [&](auto full_tag, int64_t u0, uint32_t* pk, const char* srp, const char* xrp) -> uint32_t {
       constexpr bool FULL = decltype(full_tag)::value;
       uint32_t bits = 0;
       u32x4_t sq, xq4;
@@ -1383,8 +1389,6 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p
           sq = *reinterpret_cast<const u32x4_t*>(srp + (v >> 3) * kFragBytes);
           xq4 = *reinterpret_cast<const u32x4_t*>(xrp + (v >> 3) * kFragBytes);
         }
-        if ((v >> 1) < PW && wtile >= 0) w_load(wtile, wstage, v >> 1);
-        if (v == 2 * PW && wtile >= 0) s_load(wtile, wstage);
         const uint32_t sp = sq[(v >> 1) & 3];
         const uint32_t xp = xq4[(v >> 1) & 3];
         float g2[2];
@@ -1416,26 +1420,20 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p
       return bits;
     };
 
+    // the producers load every tile (R, W^T, scores): a consumer's global
+    // accesses are its mask words and partials, stores it need not wait for
     for (int it = 0; it <= n; ++it) {
-      const bool cur = it < n;  // this tile's W^T goes out during the previous tile's epilogue
-      if (it == 0) {
-        if (cur) {
-#pragma unroll
-          for (int q = 0; q < PW; ++q) w_load(ta, 0, q);
-          s_load(ta, 0);
-        }
-      } else {
+      if (it > 0) {
         const int tile = ta + it - 1;
         const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
         const char* srp = s_wave + ((it - 1) & 1) * S_STAGE + lane * 16;
         const char* xrp = xr_lane + ((it - 1) & 1) * XR_STAGE;
         uint32_t pk[8];
         uint32_t bits;
-        const int wtile = cur ? ta + it : -1;
         if (u0 >= lo && u0 + kUnitTile <= hi)
-          bits = gate_tile(std::integral_constant<bool, true>{}, u0, pk, wtile, it & 1, srp, xrp);
+          bits = gate_tile(std::integral_constant<bool, true>{}, u0, pk, srp, xrp);
         else
-          bits = gate_tile(std::integral_constant<bool, false>{}, u0, pk, wtile, it & 1, srp, xrp);
+          bits = gate_tile(std::integral_constant<bool, false>{}, u0, pk, srp, xrp);
         {
           const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
           uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
@@ -1469,7 +1467,6 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      wait_vm0();
       barrier_lds();
     }
     gsum += __shfl_xor(gsum, 32);
