@@ -54,6 +54,9 @@ WORKLOADS = {
     "qk": ("qk", 12500, "configs[1] QK pool, paired routes sharing one x.R^T"),
     "decode_know": ("decode_know", 12500, "configs[3] decode-shaped Know pool, T=64, 3% pass"),
     "scaled": ("scaled", 12500, "configs[4] scaled Know pool d=1024 N=100000 T=16384, 2% pass"),
+    # configs[1] as one layer's projections (its own branch below): the QK and V calls as one batch
+    "qkv": (None, 12500, "configs[1] QK (paired) + V projections of one attention layer at T = 4096, "
+                         "one srw_forward_batch"),
     # a whole decode step (its own branch below): 12 layers x (QK paired, V, Know) at T = 64
     "decode": (None, 12500, "configs[3] decode step: 64 single-token rows through the QK (paired), V and "
                             "Know pools for 12 layers, Know calibrated to 3% pass"),
@@ -270,6 +273,73 @@ def bench_decode(args, pkg, C, dev) -> dict:
     }
 
 
+def bench_qkv(args, pkg, C, dev) -> dict:
+    """Q, K and V of one attention layer at T = 4096 -- the QK
+    pool's paired call and the V pool's call, issued as one
+    srw_forward_batch (one launch per stage).  The dominant kernel is the
+    batch's main kernel (both calls' workgroups)."""
+    import torch
+    bf = torch.bfloat16
+    plans, shapes = [], []
+    for key in ("qk", "v"):
+        shape = pkg.inputs.CONFIGS[key]
+        inp = pkg.inputs.make_pool_inputs(shape, seed=args.seed)
+        _, cs = pkg.chunk_plan(shape.N, 12500)
+        x = inp["x"].to(bf).to(dev)
+        h = x if shape.h_is_x else inp["h"].to(bf).to(dev)
+        plans.append(pkg.SrwPlan(x, h, inp["emb"].to(bf).to(dev), inp["tau_offset"].to(dev),
+                                 inp["read"].to(bf).to(dev), inp["write"].to(bf).to(dev),
+                                 stats=args.stats, chunk_size=cs, want_mask=True))
+        shapes.append(shape)
+    stream = torch.cuda.current_stream(dev)
+    batch = pkg.SrwBatchPlan(plans)
+    batch.launch(stream)
+    torch.cuda.synchronize()
+    log(f"qkv path: {batch.path}")
+
+    def step():
+        batch.launch(stream, pool_cached=args.pool_cached)
+
+    warmup, K = resolve_counts(args, step, torch.cuda.synchronize)
+    ev_k = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    t_begin = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    for a, b in ev_k + [(t_begin, t_end)]:
+        a.record(stream)
+        b.record(stream)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t_begin.record(stream)
+    for i in range(K):
+        C.set_kernel_events(ev_k[i][0].cuda_event, ev_k[i][1].cuda_event)
+        step()
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    C.set_kernel_events(None, None)
+    step_ms = t_begin.elapsed_time(t_end) / K
+    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev_k)
+    T = shapes[0].T
+    log(f"timed {K} steps (QK + V): {step_ms:.4f} ms/step, batch main kernel {kern_ms:.4f} ms")
+    # the streaming main kernel leaves the score GEMM to the moments kernel
+    ss = batch.path == "mfma_batch_bf16" and all(s_.dr >= s_.D for s_ in shapes)
+    kflops = sum(2.0 * T * s_.N * ((0 if ss else s_.routes * s_.dr) + s_.D + s_.routes * s_.D) for s_ in shapes)
+    achieved = kflops / (kern_ms * 1e-3) / 1e12
+    return {
+        "metric": METRIC, "value": round(T / (step_ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": K, "warmup": warmup, "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x RMS-normalised; E ~ N(0,1/dr); R, W L2-normalised rows)",
+        "config": {"workload": "qkv", "note": WORKLOADS["qkv"][2], "T": T, "d_model": 384, "d_route": 384,
+                   "pools": {"qk": shapes[0].N, "v": shapes[1].N}, "stats": args.stats,
+                   "pool_cached": args.pool_cached, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": batch.path, "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops},
+        "cpu_baseline": None,
+    }
+
+
 def bench_model(args, pkg, C, dev) -> dict:
     """DAWN.__call__ (deterministic) over B x S uniform token ids
     with random-init weights of the 40M architecture; a step is one forward
@@ -417,6 +487,12 @@ def main() -> int:
             print("bench.py: --workload decode times the forward decode step", file=sys.stderr)
             return 2
         print(json.dumps(bench_decode(args, pkg, C, dev)), flush=True)
+        return 0
+    if args.workload == "qkv":
+        if args.backward or args.graph or args.diag or args.tiled:
+            print("bench.py: --workload qkv times the batched forward", file=sys.stderr)
+            return 2
+        print(json.dumps(bench_qkv(args, pkg, C, dev)), flush=True)
         return 0
     if args.workload == "model":
         if args.backward or args.graph or args.diag or args.tiled or args.stats != "onepass":

@@ -840,7 +840,7 @@ constexpr int kWsThreads = 512;
 // DG: training diagnostics -- per-token extras in tok_part (TPS = 12), per-unit
 // score sums and gate maxima into unit_diag (atomics)
 template <int DB, int KH, bool HX, bool DG>
-__global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p) {
+__device__ __attribute__((always_inline)) inline void main_ws_body(const MainParams& p, const int bid) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int TPS = DG ? kTokPartDiag : 4;
   constexpr int D = DB * 32;
@@ -857,8 +857,8 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
   const bool producer = wave < 4;
   const int blk = wave & 3;                 // token block of this wave
   const int half = lane >> 5, col = lane & 31;
-  const int split = blockIdx.x % p.g.S;
-  const int ttile = blockIdx.x / p.g.S;
+  const int split = bid % p.g.S;
+  const int ttile = bid / p.g.S;
   const int64_t tw = static_cast<int64_t>(ttile) * kTokTile + 32 * blk;
   const int64_t t = tw + col;
   const int64_t tl = t < p.g.T ? t : p.g.T - 1;
@@ -1223,6 +1223,16 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p
   }
 }
 
+template <int DB, int KH, bool HX, bool DG>
+__global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p) {
+  main_ws_body<DB, KH, HX, DG>(p, blockIdx.x);
+}
+template <int DB, int KH, bool HX>
+__global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_batch_kernel(Batch<MainParams> b) {
+  const int i = batch_index(b.start, b.n, blockIdx.x);
+  main_ws_body<DB, KH, HX, false>(b.p[i], blockIdx.x - b.start[i]);
+}
+
 // ---------------------------------------------------------------------------
 // main, scores streamed: the warp-specialised layout of srw_main_ws_kernel
 // with the bf16 scores read back from the moments kernel's score buffer
@@ -1245,7 +1255,7 @@ constexpr int ss_lds_bytes() {
 }
 
 template <int DB>
-__global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p) {
+__device__ __attribute__((always_inline)) inline void main_ss_body(const MainParams& p, const int bid) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int TPS = 4;
   constexpr int D = DB * 32;
@@ -1263,8 +1273,8 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p
   const bool producer = wave < 4;
   const int blk = wave & 3;                 // token block of this wave
   const int half = lane >> 5, col = lane & 31;
-  const int split = blockIdx.x % p.g.S;
-  const int ttile = blockIdx.x / p.g.S;
+  const int split = bid % p.g.S;
+  const int ttile = bid / p.g.S;
   const int64_t tw = static_cast<int64_t>(ttile) * kTokTile + 32 * blk;
   const int64_t t = tw + col;
   const int64_t tl = t < p.g.T ? t : p.g.T - 1;
@@ -1494,6 +1504,16 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p
         }
     }
   }
+}
+
+template <int DB>
+__global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p) {
+  main_ss_body<DB>(p, blockIdx.x);
+}
+template <int DB>
+__global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_batch_kernel(Batch<MainParams> b) {
+  const int i = batch_index(b.start, b.n, blockIdx.x);
+  main_ss_body<DB>(b.p[i], blockIdx.x - b.start[i]);
 }
 
 // ---------------------------------------------------------------------------
@@ -2545,9 +2565,26 @@ hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Several decode-shaped calls, one launch per stage (srw_forward_batch):
-// every call must take the decode kernel with the same instantiation, the
-// same moments kernel and the same finalize grouping; otherwise nothing is
+// The batch twin of a prefill main kernel (non-diagnostic instantiations).
+MainBatchFn main_batch_of(MainFn fn) {
+  if (fn == srw_main_ss_kernel<12>) return srw_main_ss_batch_kernel<12>;
+  if (fn == srw_main_ss_kernel<4>) return srw_main_ss_batch_kernel<4>;
+  if (fn == srw_main_ss_kernel<2>) return srw_main_ss_batch_kernel<2>;
+  if (fn == srw_main_ws_kernel<12, 24, true, false>) return srw_main_ws_batch_kernel<12, 24, true>;
+  if (fn == srw_main_ws_kernel<4, 8, true, false>) return srw_main_ws_batch_kernel<4, 8, true>;
+  if (fn == srw_main_ws_kernel<2, 4, true, false>) return srw_main_ws_batch_kernel<2, 4, true>;
+  if (fn == srw_main_ws_kernel<12, 8, false, false>) return srw_main_ws_batch_kernel<12, 8, false>;
+  if (fn == srw_main_ws_kernel<4, 8, false, false>) return srw_main_ws_batch_kernel<4, 8, false>;
+  if (fn == srw_main_ws_kernel<4, 4, false, false>) return srw_main_ws_batch_kernel<4, 4, false>;
+  if (fn == srw_main_ws_kernel<2, 4, false, false>) return srw_main_ws_batch_kernel<2, 4, false>;
+  if (fn == srw_main_ws_kernel<2, 2, false, false>) return srw_main_ws_batch_kernel<2, 2, false>;
+  return nullptr;
+}
+
+// Several calls, one launch per stage (srw_forward_batch): every call must
+// take the same main kernel instantiation -- all the decode kernel, or all
+// the same prefill main kernel (scores streamed or recomputed) -- the same
+// moments kernel and the same finalize grouping; otherwise nothing is
 // launched and hipErrorNotSupported returned (the caller runs the calls one
 // by one).  Each call keeps its own geometry, workspace and outputs, and its
 // blocks run exactly the code of its own srw_forward: equal bits.
@@ -2555,38 +2592,69 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
   if (n < 1 || n > kMaxBatch) return hipErrorNotSupported;
   Geometry g[kMaxBatch];
   WsLayout L[kMaxBatch];
-  MainFn dec = nullptr;
-  int dec_lds = 0, rb[kMaxBatch];
+  bool ss[kMaxBatch];
+  int rb[kMaxBatch];
+  MainFn main0 = nullptr;
+  int lds0 = 0, threads0 = kThreads;
   const srw_desc_t& d0 = a[0].d;
+  bool decode = false;
   for (int i = 0; i < n; ++i) {
     const srw_desc_t& d = a[i].d;
-    if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM || !decode_applies(d)) return hipErrorNotSupported;
+    if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM) return hipErrorNotSupported;
     if (d.d_model != d0.d_model || d.d_route != d0.d_route || d.stats_mode != d0.stats_mode)
       return hipErrorNotSupported;
     g[i] = geometry(d, a[i].chunk);
     L[i] = ws_layout(d, g[i]);
     if (a[i].ws_bytes < L[i].total) return hipErrorInvalidValue;
-    if (!decode_splits_fit(g[i])) return hipErrorNotSupported;
-    const int row_blocks = static_cast<int>((g[i].T + 31) / 32);
-    rb[i] = (row_blocks > 1 && static_cast<int64_t>(g[i].S) * row_blocks <= kTargetBlocks) ? row_blocks : 1;
+    const bool dec_i = decode_applies(d) && decode_splits_fit(g[i]);
+    if (i == 0) decode = dec_i;
+    if (dec_i != decode) return hipErrorNotSupported;
     MainFn fn = nullptr;
-    int lds = 0;
-    if (!pick_decode(rb[i] > 1 ? 32 : g[i].T, static_cast<int>(d.d_model), static_cast<int>(d.d_route),
-                     decode_max_tiles(g[i]), &fn, &lds))
+    int lds = 0, threads = kThreads;
+    ss[i] = false;
+    rb[i] = 1;
+    if (decode) {
+      const int row_blocks = static_cast<int>((g[i].T + 31) / 32);
+      rb[i] = (row_blocks > 1 && static_cast<int64_t>(g[i].S) * row_blocks <= kTargetBlocks) ? row_blocks : 1;
+      if (!pick_decode(rb[i] > 1 ? 32 : g[i].T, static_cast<int>(d.d_model), static_cast<int>(d.d_route),
+                       decode_max_tiles(g[i]), &fn, &lds))
+        return hipErrorNotSupported;
+    } else {
+      Kernels k;
+      if (!pick(d.d_model, d.d_route, a[i].in.h == a[i].in.x, false, &k)) return hipErrorNotSupported;
+      MainFn ss_fn = nullptr;
+      int ss_lds = 0;
+      ss[i] = ss_applies(d, g[i]) && pick_ss(d.d_model, &ss_fn, &ss_lds);
+      fn = ss[i] ? ss_fn : k.main;
+      lds = ss[i] ? ss_lds : k.main_lds;
+      threads = ss[i] ? kWsThreads : k.main_threads;
+    }
+    if (i > 0 && (fn != main0 || finalize_groups(g[i].spc) != finalize_groups(g[0].spc)))
       return hipErrorNotSupported;
-    if (i > 0 && (fn != dec || finalize_groups(g[i].spc) != finalize_groups(g[0].spc))) return hipErrorNotSupported;
-    dec = fn;
-    dec_lds = lds;
+    main0 = fn;
+    lds0 = lds;
+    threads0 = threads;
   }
+  const MainBatchFn main_batch = decode ? decode_batch_of(main0) : main_batch_of(main0);
+  if (!main_batch) return hipErrorNotSupported;
   const int ng = finalize_groups(g[0].spc);
   const bool rows_fin = ng == 1;  // the row-per-wave finalize, as launch_finalize picks it
   if (rows_fin && d0.d_model != 64 && d0.d_model != 128 && d0.d_model != 384) return hipErrorNotSupported;
   const int D = static_cast<int>(d0.d_model);
   const int KH = static_cast<int>(d0.d_route / 16);
   const bool centered = d0.stats_mode == SRW_STATS_CENTERED;
+  void (*stats_plain)(Batch<StatsParams>) = nullptr;
+  void (*stats_cent)(Batch<StatsParams>) = nullptr;
+  switch (KH) {
+    case 24: stats_plain = srw_stats_batch_kernel<24, kStatsPlain>; stats_cent = srw_stats_batch_kernel<24, kStatsCentered>; break;
+    case 8: stats_plain = srw_stats_batch_kernel<8, kStatsPlain>; stats_cent = srw_stats_batch_kernel<8, kStatsCentered>; break;
+    case 4: stats_plain = srw_stats_batch_kernel<4, kStatsPlain>; stats_cent = srw_stats_batch_kernel<4, kStatsCentered>; break;
+    case 2: stats_plain = srw_stats_batch_kernel<2, kStatsPlain>; stats_cent = srw_stats_batch_kernel<2, kStatsCentered>; break;
+    default: return hipErrorNotSupported;
+  }
   const hipStream_t st = a[0].stream;
   hipError_t e;
-  *path_name = "mfma_decode_batch_bf16";
+  *path_name = decode ? "mfma_decode_batch_bf16" : "mfma_batch_bf16";
 
   // per call: pack W^T unless cached (its own launch)
   for (int i = 0; i < n; ++i) {
@@ -2596,17 +2664,6 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
       return e;
   }
   // moments (and for centred statistics the row means, then the second pass)
-  void (*stats_plain)(Batch<StatsParams>) = nullptr;
-  void (*stats_cent)(Batch<StatsParams>) = nullptr;
-  if (KH == 8) {
-    stats_plain = srw_stats_batch_kernel<8, kStatsPlain>;
-    stats_cent = srw_stats_batch_kernel<8, kStatsCentered>;
-  } else if (KH == 4) {
-    stats_plain = srw_stats_batch_kernel<4, kStatsPlain>;
-    stats_cent = srw_stats_batch_kernel<4, kStatsCentered>;
-  } else {
-    return hipErrorNotSupported;
-  }
   Batch<StatsParams> sb{};
   Batch<TauParams> tb{};
   sb.n = tb.n = n;
@@ -2618,6 +2675,7 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     sp.mask32 = reinterpret_cast<uint32_t*>(a[i].o.pass_mask);
     sp.mask_words32 = 2 * a[i].words;
     sp.g = g[i];
+    sp.s_out = ss[i] ? reinterpret_cast<uint16_t*>(a[i].ws + L[i].scores) : nullptr;
     sb.start[i + 1] = sb.start[i] + g[i].TT_st * g[i].S_st;
     tb.p[i] = TauParams{sp.mom, a[i].in.tau_offset, reinterpret_cast<float*>(a[i].ws + L[i].tau), g[i].T,
                         g[i].S_st, g[i].N, 2, nullptr, centered ? kTauMean : kTauOnePass};
@@ -2636,6 +2694,7 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     for (int i = 0; i < n; ++i) {
       sb.p[i].mean = tb.p[i].tau;
       sb.p[i].mask32 = nullptr;  // the first pass cleared the shared mask words
+      sb.p[i].s_out = nullptr;   // and stored the scores
       tb.p[i].mode = kTauCentered;
     }
     hipLaunchKernelGGL(stats_cent, dim3(static_cast<unsigned>(sb.start[n])), dim3(kThreads), smem, st, sb);
@@ -2643,7 +2702,7 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     hipLaunchKernelGGL(srw_tau_batch_kernel, dim3(static_cast<unsigned>(tb.start[n])), dim3(256), 0, st, tb);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  // decode kernel
+  // main (decode or prefill) kernel
   Batch<MainParams> mb{};
   mb.n = n;
   for (int i = 0; i < n; ++i) {
@@ -2664,16 +2723,15 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     mp.gp = a[i].gp;
     mp.exp_scale = -d.sharpness * 1.4426950408889634f;
     mp.rb = rb[i];
-    mb.start[i + 1] = mb.start[i] + g[i].S * rb[i];
+    mp.s_in = ss[i] ? reinterpret_cast<const uint16_t*>(a[i].ws + L[i].scores) : nullptr;
+    mb.start[i + 1] = mb.start[i] + (decode ? g[i].S * rb[i] : g[i].TT * g[i].S);
   }
-  MainBatchFn dec_batch = decode_batch_of(dec);
-  if (!dec_batch) return hipErrorNotSupported;
-  if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(dec_batch), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               dec_lds)) != hipSuccess)
+  if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(main_batch), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               lds0)) != hipSuccess)
     return e;
   dominant_kernel_begin(st);
-  hipLaunchKernelGGL(dec_batch, dim3(static_cast<unsigned>(mb.start[n])), dim3(kThreads),
-                     static_cast<size_t>(dec_lds), st, mb);
+  hipLaunchKernelGGL(main_batch, dim3(static_cast<unsigned>(mb.start[n])), dim3(threads0),
+                     static_cast<size_t>(lds0), st, mb);
   dominant_kernel_end(st);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   // finalize

@@ -179,10 +179,10 @@ class SrwBatchPlan:
     The plans' descriptors, tensors and outputs are taken over (each plan's
     results land in its own output tensors, as after its own launch); the
     workspace is one batch workspace, sliced in plan order, so the plans' own
-    workspaces are not used.  Calls that all take the decode kernel with the
-    same shapes class (the QK and V calls of a decode step) run as one launch
-    per stage; others run one after the other -- the results equal separate
-    launches bit for bit either way.
+    workspaces are not used.  Calls that all take the same kernel
+    instantiations (the QK and V calls of a layer, at decode or prefill
+    sizes) run as one launch per stage; others run one after the other --
+    the results equal separate launches bit for bit either way.
     """
 
     def __init__(self, plans):

@@ -236,10 +236,12 @@ srw_status_t srw_forward(const srw_desc_t* desc, const srw_tensors_t* in,
  * :1036-1053 in the forward): equivalent to srw_forward(&descs[i], &ins[i],
  * &outs[i], ws_i, bytes_i, stream) for i = 0 .. n-1 in order, where ws_i is
  * call i's slice of `workspace` (srw_workspace_size_batch), with equal
- * results bit for bit.  Calls that all take the decode kernel (at most 128
- * rows, bf16, no diagnostics) with the same d_model, d_route and statistics
- * run as one launch per stage -- the small pools' calls are bound by their
- * launches; otherwise the calls run one after the other.  1 <= n <=
+ * results bit for bit.  Calls on the matrix-core kernels (bf16, no
+ * diagnostics, one-pass or centred statistics) with the same d_model,
+ * d_route and statistics that take the same kernel instantiations -- all the
+ * decode kernel (at most 128 rows), or all the same prefill main kernel --
+ * run as one launch per stage (the small pools' calls are bound by their
+ * launches); otherwise the calls run one after the other.  1 <= n <=
  * SRW_MAX_BATCH; the calls must not share outputs. */
 #define SRW_MAX_BATCH 4
 srw_status_t srw_workspace_size_batch(int32_t n, const srw_desc_t* descs, size_t* bytes);

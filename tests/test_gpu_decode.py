@@ -186,9 +186,10 @@ def test_batch_three_small_pools_one_launch_per_stage(pkg, dev):
 
 @pytest.mark.parametrize("which", ["prefill_and_decode", "know_and_qk"])
 def test_batch_that_cannot_share_launches_runs_one_by_one(pkg, dev, which):
-    """A prefill-sized call, or decode calls of different kernel shapes (the
-    Know pool's four-tile splits against the small pools' row blocks): the
-    calls run one after the other, with the same results."""
+    """A prefill-sized call with a decode-sized one, or decode calls of
+    different kernel shapes (the Know pool's four-tile splits against the
+    small pools' row blocks): the calls run one after the other, with the
+    same results."""
     print(f"[gpu] decode batch fallback {which}", flush=True)
     if which == "prefill_and_decode":
         inps = [_pool(pkg, 300, 1580, 1, 56), _pool(pkg, 64, 2600, 1, 57)]
@@ -203,3 +204,13 @@ def test_batch_with_row_per_wave_finalize(pkg, dev):
     print("[gpu] decode batch row finalize", flush=True)
     inps = [_pool(pkg, 5, 300, 2, 60, D=128, dr=64), _pool(pkg, 5, 500, 1, 61, D=128, dr=64)]
     _check_batch(pkg, dev, inps, "centered", "mfma_decode_batch_bf16")
+
+
+@pytest.mark.parametrize("dr,stats", [(384, "onepass"), (128, "onepass"), (128, "centered")])
+def test_batch_prefill_qk_v_one_launch_per_stage(pkg, dev, dr, stats):
+    """Prefill-sized QK (paired) and V calls of one layer (configs[1] shapes
+    at 300 tokens): one launch per stage with the streaming main kernel
+    (d_route = d_model) or the recomputing one (d_route = 128)."""
+    print(f"[gpu] prefill batch QK+V dr{dr} {stats}", flush=True)
+    inps = [_pool(pkg, 300, 1580, 2, 62, dr=dr), _pool(pkg, 300, 2600, 1, 63, dr=dr)]
+    _check_batch(pkg, dev, inps, stats, "mfma_batch_bf16")
