@@ -107,6 +107,19 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+# The CPU baseline runs on at most this many threads: a one-GPU box's share
+# of the host's cores, whatever os.cpu_count() reports there.
+CPU_THREADS_MAX = 16
+
+
+def host_cpus() -> dict:
+    """The host's logical CPU count beside the threads the baseline used
+    ("cores"), so that a capped thread count is visible."""
+    import torch
+    return {"host_cpu_count": os.cpu_count(), "threads_used": torch.get_num_threads(),
+            "thread_cap": CPU_THREADS_MAX}
+
+
 def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: bool = False) -> dict:
     """The oracle's fused_gate_srw (bf16 emulation) -- or, with ``backward``,
     its hand-written VJP -- on a token sample of the same pool, timed on the
@@ -149,6 +162,7 @@ def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: b
     log(f"cpu baseline: T_sample={T_s} runs={len(times)} median={med * 1e3:.1f} ms "
         f"threads={threads}")
     return {"value": T_s / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            **host_cpus(),
             "sample": (f"oracle {what} bf16 emulation, first {T_s} of the "
                        f"{shape.T} tokens, full pool N={shape.N}, median of {len(times)} "
                        f"runs; {cpu_model()}")}
@@ -244,7 +258,7 @@ def bench_decode(args, pkg, C, dev) -> dict:
     cpu = None
     if args.cpu_seconds > 0:
         from oracle import srw_ref
-        torch.set_num_threads(min(os.cpu_count() or 1, 16))
+        torch.set_num_threads(min(os.cpu_count() or 1, CPU_THREADS_MAX))
         t0 = time.perf_counter()
         for pl, s_ in zip(plans, shapes):
             x, h, emb, tau, read, write = (t.float().cpu() for t in pl.inputs)
@@ -256,7 +270,7 @@ def bench_decode(args, pkg, C, dev) -> dict:
         layer_s = time.perf_counter() - t0
         log(f"cpu baseline: one layer (3 pools, 64 rows) {layer_s:.2f} s")
         cpu = {"value": 64 / (layer_s * DECODE_LAYERS), "unit": "tokens/s", "cores": torch.get_num_threads(),
-               "kind": "port",
+               "kind": "port", **host_cpus(),
                "sample": (f"oracle fused_gate_srw / _paired (bf16 emulation) of one of the {DECODE_LAYERS} layers "
                           f"(QK, V, Know at 64 rows), scaled to {DECODE_LAYERS} layers; {cpu_model()}")}
     return {
@@ -321,10 +335,22 @@ def bench_qkv(args, pkg, C, dev) -> dict:
     kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev_k)
     T = shapes[0].T
     log(f"timed {K} steps (QK + V): {step_ms:.4f} ms/step, batch main kernel {kern_ms:.4f} ms")
-    # the streaming main kernel leaves the score GEMM to the moments kernel
-    ss = batch.path == "mfma_batch_bf16" and all(s_.dr >= s_.D for s_ in shapes)
-    kflops = sum(2.0 * T * s_.N * ((0 if ss else s_.routes * s_.dr) + s_.D + s_.routes * s_.D) for s_ in shapes)
-    achieved = kflops / (kern_ms * 1e-3) / 1e12
+    # The roofline needs the batch's one main kernel: when the calls fell
+    # back to running one after the other, every call re-recorded the events
+    # and they bracket only the last call's main kernel.
+    roofline = None
+    if batch.path == "mfma_batch_bf16":
+        # the streaming main kernel leaves the score GEMM to the moments kernel
+        ss = all(s_.dr >= s_.D for s_ in shapes)
+        kflops = sum(2.0 * T * s_.N * ((0 if ss else s_.routes * s_.dr) + s_.D + s_.routes * s_.D)
+                     for s_ in shapes)
+        achieved = kflops / (kern_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                    "kernel": batch.path, "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops}
+    else:
+        log(f"qkv: the calls ran one after the other (path {batch.path}); no single main kernel, "
+            "roofline null")
     return {
         "metric": METRIC, "value": round(T / (step_ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": K, "warmup": warmup, "ms_per_step": round(step_ms, 5),
@@ -333,9 +359,7 @@ def bench_qkv(args, pkg, C, dev) -> dict:
         "config": {"workload": "qkv", "note": WORKLOADS["qkv"][2], "T": T, "d_model": 384, "d_route": 384,
                    "pools": {"qk": shapes[0].N, "v": shapes[1].N}, "stats": args.stats,
                    "pool_cached": args.pool_cached, "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": batch.path, "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops},
+        "roofline": roofline,
         "cpu_baseline": None,
     }
 
@@ -397,7 +421,7 @@ def bench_model(args, pkg, C, dev) -> dict:
     cpu = None
     if args.cpu_seconds > 0:
         from oracle import dawn_ref
-        torch.set_num_threads(min(os.cpu_count() or 1, 16))
+        torch.set_num_threads(min(os.cpu_count() or 1, CPU_THREADS_MAX))
         S_s = 64
         sample = ids[:1, :S_s]
         times = []
@@ -409,6 +433,7 @@ def bench_model(args, pkg, C, dev) -> dict:
         med = statistics.median(times)
         log(f"cpu baseline: {S_s} tokens, runs={len(times)} median={med:.2f} s")
         cpu = {"value": S_s / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               **host_cpus(),
                "sample": (f"oracle DAWN forward (oracle/dawn_ref.py, bf16-emulated SRW, f32 glue), "
                           f"1 x {S_s} tokens of the same ids, full 40M model, median of {len(times)} "
                           f"runs; {cpu_model()}")}
@@ -618,9 +643,11 @@ def main() -> int:
         # work is the read (once per token) and write GEMMs
         kflops = 2.0 * T * N * (D + R * D)
     elif plan.path == "tiled_bf16":
-        # the dominant kernel of the tiled family is the gate GEMM pair (score
-        # + read); the write GEMM is a kernel of its own
-        kflops = 2.0 * T * N * (R * dr + D)
+        # the dominant kernel of the tiled family is tiled_gate_kernel: the
+        # read GEMM over the T * R virtual rows, gating the scores that
+        # tiled_stats_kernel stored (the score and write GEMMs are kernels of
+        # their own)
+        kflops = 2.0 * T * R * N * D
     else:
         kflops = flops
     achieved = kflops / (kern_ms * 1e-3) / 1e12
@@ -642,7 +669,7 @@ def main() -> int:
 
     cpu = None
     if args.cpu_seconds > 0:
-        torch.set_num_threads(min(os.cpu_count() or 1, 16))
+        torch.set_num_threads(min(os.cpu_count() or 1, CPU_THREADS_MAX))
         cpu = cpu_baseline(pkg, shape, inp, tau_value, max_chunk, args.cpu_seconds, args.backward)
 
     value = T / (step_ms * 1e-3)

@@ -71,11 +71,20 @@ def _ext_hook(code, data):
     raise ValueError(f"unknown msgpack extension type {code} in checkpoint")
 
 
+def _dict_to_list(d):
+    """flax's _dict_to_tuple: a map keyed '0', '1', ... (how flax's _chunk
+    stores both the shape and the pieces of a chunked array) as a list; a
+    list is taken as it is."""
+    if isinstance(d, dict):
+        return [d[str(i)] for i in range(len(d))]
+    return list(d)
+
+
 def _unchunk(tree):
     if isinstance(tree, dict):
         if tree.get(_CHUNKED) is True:
-            shape = tuple(int(s) for s in tree["shape"])
-            pieces = [tree["chunks"][str(i)] for i in range(len(tree["chunks"]))]
+            shape = tuple(int(s) for s in _dict_to_list(tree["shape"]))
+            pieces = _dict_to_list(tree["chunks"])
             flat = torch.cat([p.reshape(-1) for p in pieces])
             return flat.reshape(shape)
         return {k: _unchunk(v) for k, v in tree.items()}
@@ -157,7 +166,8 @@ def _to_state(tree):
             flat = tree.reshape(-1)
             per = max(1, _MAX_CHUNK // (nbytes // max(1, flat.shape[0])))
             chunks = {str(i): flat[j:j + per] for i, j in enumerate(range(0, flat.shape[0], per))}
-            return {_CHUNKED: True, "shape": list(tree.shape), "chunks": chunks}
+            shape = {str(i): int(n) for i, n in enumerate(tree.shape)}  # flax's _tuple_to_dict
+            return {_CHUNKED: True, "shape": shape, "chunks": chunks}
     return tree
 
 

@@ -118,11 +118,12 @@ def _diag_tuple(res, N, B, S, R, dead_threshold):
 # Positions in the 22-tuple (v41:630-635).  The training loss differentiates
 # out, score_lb and dead_penalty (scripts/train_jax.py:586-603).
 _OUT, _SCORE_LB, _DEAD_PENALTY = 0, 3, 18
-# Outputs without a gradient: behind stop_gradient in the reference (gate_max
-# :583, tau_abs_mean, z_lt_*, active_per_token_std, entropy, dead_count,
-# int_max, int_cap_frac, :599-629) or piecewise-constant counts (active_frac,
-# active_n_mean, strong_frac, boundary_frac).
-_NO_GRAD = (1, 2, 6, 7, 8, 10, 11, 12, 14, 15, 19, 20, 21)
+# Outputs without a gradient: behind stop_gradient in the reference (score_skew
+# and score_kurt :466-474, gate_max :583, tau_abs_mean, z_lt_*,
+# active_per_token_std, entropy, dead_count, int_max, int_cap_frac, :599-629)
+# or piecewise-constant counts (active_frac, active_n_mean, strong_frac,
+# boundary_frac).
+_NO_GRAD = (1, 2, 6, 7, 8, 10, 11, 12, 13, 14, 15, 17, 19, 20, 21)
 _NAMES = ("out", "active_frac", "gate_max", "score_lb", "score_std", "gate_sum_mean",
           "active_n_mean", "strong_frac", "boundary_frac", "z_mean_active", "tau_abs_mean",
           "z_lt_075", "z_lt_030", "skew", "active_per_token_std", "entropy", "intensity_sum_mean",
@@ -135,9 +136,9 @@ class _FusedSrw(torch.autograd.Function):
     srw_backward with the cotangents of out, score_lb and dead_penalty -- the
     VJP that jax.value_and_grad takes through the reference's checkpointed
     scans (v41:434, 489; scripts/train_jax.py:726).  Differentiating any other
-    differentiable diagnostic (score_std, the gate and intensity sums, skew,
-    kurt) raises NotImplementedError; the rest carry no gradient, as in the
-    reference."""
+    differentiable diagnostic (score_std, the gate and intensity sums,
+    z_mean_active) raises NotImplementedError; the rest carry no gradient, as
+    in the reference."""
 
     @staticmethod
     def forward(ctx, x, h, emb, tau_offset, read, write, routes, consts, cs):

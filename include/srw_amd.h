@@ -126,8 +126,12 @@ typedef struct srw_desc {
   float max_intensity;    /* v4.1 MAX_INTENSITY        (default 10)   */
   float dead_threshold;   /* dead-unit threshold for unit_diag consumers (0.01) */
   float scale;            /* multiplies out after the den division (1 = reference fn) */
-  int32_t chunk_size;     /* N-chunk of the reference plan (v41:416-420); used by
-                             SRW_FLAG_EMULATE only; 0 = one chunk */
+  int32_t chunk_size;     /* N-chunk of the reference plan (v41:416-420); 0 = one
+                             chunk.  The matrix-core and tiled kernels round each
+                             chunk's partial write GEMM to bf16 before the chunks
+                             are summed (v41:518, the chunk scan :489-577) and
+                             never let an N-split cross a chunk; the generic
+                             kernels do so under SRW_FLAG_EMULATE */
   uint32_t flags;         /* SRW_FLAG_* */
   int32_t reserved[3];
 } srw_desc_t;

@@ -25,7 +25,20 @@ Pinning status (how each function is checked, see ``tests/test_oracle_*``):
   leave-one-out additivity, den closed form, den floor;
 * bf16 emulation: rounding points checked against explicit RNE rounding of
   fp64 results, and the bf16 layer against the fp64 layer within the bf16
-  error budget.
+  error budget;
+* the v4.0.1 fused function (``fused_gate_srw_gelu_v401``): its exact
+  (float64) form against the brute-force loop (R / W rows of non-unit norm,
+  two chunks), against the pinned ``srw_inference_gelu_v401`` and its
+  16-tuple against numpy / scipy closed forms; its bf16 form within the bf16
+  budget of the exact form; planted mistakes (den from sum z+, rows not
+  normalised, a gate below z = 0, Phi without 1/sqrt 2) are caught;
+* ``gate_norm`` of ``srw_inference_with_gates``: against gate / max(sum
+  gate, 1e-8) of the brute-force gates, rows summing to one, the 1e-8
+  floor, and three plausible wrong normalisers rejected.
+
+Every function of ``srw_ref`` has such a pin (``tests/test_oracle_pins.py``);
+``srw_vjp`` is pinned in ``tests/test_backward_oracle.py`` and ``dawn_ref``
+in ``tests/test_model_oracle.py``.
 
 The reference ships no tests, golden vectors or fixtures for this path
 (its ``tests/`` holds one docstring), and the arithmetic of its bf16 dots

@@ -69,6 +69,7 @@ class GateConsts:
 V41 = GateConsts()
 
 F32 = torch.float32
+F64 = torch.float64
 BF16 = torch.bfloat16
 
 
@@ -191,17 +192,21 @@ def srw_inference_with_gates(x, h, emb, tau_offset, w_read, w_write,
 # fused_gate_srw: chunked bf16 two-pass layer with diagnostics (v41:415-635)
 # --------------------------------------------------------------------------
 
-def _pass1_stats(h_bf, emb_bf, nc, cs, n_total, route_axis: bool):
-    """Pass 1 (v41:434-483; paired v41:713-763): exact stats over all chunks."""
+def _pass1_stats(h_bf, emb_bf, nc, cs, n_total, route_axis: bool, exact: bool = False):
+    """Pass 1 (v41:434-483; paired v41:713-763): exact stats over all chunks.
+
+    ``exact``: float64 operands and sums, no bf16 rounding of the scores (the
+    exact-arithmetic form the pins compare with brute force)."""
+    acc = F64 if exact else F32
     lead = h_bf.shape[:-1]
-    z = torch.zeros(*lead, 1, dtype=F32)
+    z = torch.zeros(*lead, 1, dtype=acc)
     s_sum, sq_sum, cube_sum, quad_sum = z.clone(), z.clone(), z.clone(), z.clone()
-    ns_sum = torch.zeros((), dtype=F32)
-    ns_sq = torch.zeros((), dtype=F32)
+    ns_sum = torch.zeros((), dtype=acc)
+    ns_sq = torch.zeros((), dtype=acc)
     red_axes = tuple(range(len(lead)))        # (0,1) single, (0,1,2) paired
     for i in range(nc):
         ec = emb_bf[i * cs:(i + 1) * cs]
-        scores_f = dot_bf16(h_bf, ec).to(F32)                      # :439-440
+        scores_f = (h_bf @ ec.T) if exact else dot_bf16(h_bf, ec).to(F32)  # :439-440
         s_sum = s_sum + scores_f.sum(dim=-1, keepdim=True)         # :441
         sq_sum = sq_sum + (scores_f ** 2).sum(dim=-1, keepdim=True)
         cube_sum = cube_sum + (scores_f ** 3).sum(dim=-1, keepdim=True)
@@ -210,7 +215,7 @@ def _pass1_stats(h_bf, emb_bf, nc, cs, n_total, route_axis: bool):
         ns_sum = ns_sum + per_neuron.sum()
         ns_sq = ns_sq + (per_neuron ** 2).sum()
     s_mean = s_sum / n_total                                       # :461
-    s_std = torch.sqrt(sq_sum / n_total - s_mean ** 2) + _f(1e-8, F32)  # :462
+    s_std = torch.sqrt(sq_sum / n_total - s_mean ** 2) + _f(1e-8, acc)  # :462
     cube_mean = cube_sum / n_total                                 # :467
     central_third = cube_mean - 3.0 * s_mean * (s_std ** 2) - s_mean ** 3
     score_skew = (central_third / (s_std ** 3 + 1e-8)).mean()      # :469
@@ -454,54 +459,77 @@ def srw_inference_gelu_v401(x, h, emb, tau_offset, w_read, w_write,
     return out
 
 
-def fused_gate_srw_gelu_v401(x, h, emb, tau_offset, read, write, *,
-                             max_chunk_size: int = 2048, return_trace=False):
-    """v4.0.1 ``fused_gate_srw`` (v401:229-355), 1x1 mesh -> 16-tuple.
+def _v401_den(gate_sum: torch.Tensor, zpos_sum: torch.Tensor) -> torch.Tensor:
+    """den = max(sum gate, 1) (v401:340: the psum of total_weighted_cost,
+    the chunk sums of gate at :310).  ``zpos_sum`` (sum of z+, the
+    z_mean_active numerator) is not part of it."""
+    return torch.clamp_min(gate_sum, 1.0)
 
-    Pass 1 as v4.1 but without the 4th moment.  Pass 2 forward-normalises
-    each chunk's R and W rows in bf16, gates with z Phi(z), den = max(sum
-    gate, 1).
+
+def fused_gate_srw_gelu_v401(x, h, emb, tau_offset, read, write, *,
+                             max_chunk_size: int = 2048, return_trace=False,
+                             exact: bool = False):
+    """v4.0.1 ``fused_gate_srw`` (v401:230-367), 1x1 mesh -> 16-tuple.
+
+    Pass 1 as v4.1 but without the 4th moment (v401:246-284).  Pass 2
+    forward-normalises each chunk's R and W rows in bf16 (v401:300-301),
+    gates with z Phi(z) (v401:303-306), den = max(sum gate, 1) (v401:340).
+
+    ``exact``: the same steps in float64 with no bf16 rounding anywhere (the
+    operands are widened, not rounded): the exact-arithmetic form the oracle
+    pins compare with the brute-force loop and with
+    ``srw_inference_gelu_v401``.
     """
     N = emb.shape[0]
-    nc, cs = chunk_plan(N, max_chunk_size)
+    nc, cs = chunk_plan(N, max_chunk_size)                         # v401:231-235
     B, S, D = x.shape
-    h_bf, x_bf, emb_bf, read_bf, write_bf = _prepare(x, h, emb, read, write)
-    st = _pass1_stats(h_bf, emb_bf, nc, cs, N, route_axis=False)
+    acc = F64 if exact else F32
+    if exact:
+        h_bf, x_bf, emb_bf, read_bf, write_bf = (t.to(F64) for t in (h, x, emb, read, write))
+        dot = lambda a, b: a @ b.T                                 # noqa: E731
+        rnd = lambda t: t                                          # noqa: E731
+    else:
+        h_bf, x_bf, emb_bf, read_bf, write_bf = _prepare(x, h, emb, read, write)  # v401:238-242
+        # operands held as float32 are bf16-exact here (rounded by ``rnd``)
+        dot = lambda a, b: dot_bf16(a.to(BF16), b.to(BF16)).to(F32)  # noqa: E731
+        rnd = bf16_round
+    st = _pass1_stats(h_bf, emb_bf, nc, cs, N, route_axis=False, exact=exact)
     s_mean, s_std = st["s_mean"], st["s_std"]
-    tau = s_mean + tau_offset.to(F32) * s_std
-    z1 = torch.zeros(B, S, 1, dtype=F32)
-    out = torch.zeros(B, S, D, dtype=F32)
-    wsum, gmax = z1.clone(), torch.full((B, S, 1), -1e9, dtype=F32)
+    tau = s_mean + tau_offset.to(acc) * s_std                      # v401:274
+    z1 = torch.zeros(B, S, 1, dtype=acc)
+    out = torch.zeros(B, S, D, dtype=acc)
+    wsum, gmax = z1.clone(), torch.full((B, S, 1), -1e9, dtype=acc)
     act_n, strong, phi_bin, zsum = z1.clone(), z1.clone(), z1.clone(), z1.clone()
     z075, z030, glogg = z1.clone(), z1.clone(), z1.clone()
-    trace_z = []
-    for i in range(nc):                                            # v401:296-336
+    trace_z, trace_gate = [], []
+    for i in range(nc):                                            # v401:286-335
         sl = slice(i * cs, (i + 1) * cs)
         ec = emb_bf[sl]
-        rc = _norm_rows(read_bf[sl])
-        wc = _norm_rows(write_bf[sl])
-        scores = dot_bf16(h_bf, ec)
-        raw = scores.to(F32) - tau
-        z, phi, gate = gate_gelu_v401(raw, s_std)
-        gate_bf = gate.to(BF16)
-        xr = dot_bf16(x_bf, rc)
-        prod = (gate_bf.to(F32) * xr.to(F32)).to(BF16)
-        out = out + dot_bf16(prod, wc.T.contiguous()).to(F32)
-        wsum = wsum + gate.sum(dim=-1, keepdim=True)
-        act_n = act_n + (gate > 0.0).to(F32).sum(dim=-1, keepdim=True)
-        strong = strong + (gate > 0.5).to(F32).sum(dim=-1, keepdim=True)
-        phi_bin = phi_bin + ((phi > 0.95) | (phi < 0.05)).to(F32).sum(dim=-1, keepdim=True)
-        zsum = zsum + torch.where(z > 0, z, torch.zeros((), dtype=F32)).sum(
-            dim=-1, keepdim=True)
-        z075 = z075 + ((z > 0) & (z < 0.75)).to(F32).sum(dim=-1, keepdim=True)
-        z030 = z030 + ((z > 0) & (z < 0.30)).to(F32).sum(dim=-1, keepdim=True)
-        glogg = glogg + (gate * torch.log(gate + 1e-8)).sum(dim=-1, keepdim=True)
+        rc = _norm_rows(read_bf[sl])                               # v401:300
+        wc = _norm_rows(write_bf[sl])                              # v401:301
+        scores = dot(h_bf, ec)                                     # v401:302 (bf16 dot output)
+        raw = scores - tau                                         # v401:303
+        z, phi, gate = gate_gelu_v401(raw, s_std)                  # v401:304-306
+        gate_bf = rnd(gate)                                        # v401:307
+        xr = dot(x_bf, rc)                                         # v401:308
+        prod = rnd(gate_bf * xr)                                   # v401:309 bf16 multiply
+        out = out + dot(prod, wc.T.contiguous())                   # v401:309 bf16 dot, as f32
+        wsum = wsum + gate.sum(dim=-1, keepdim=True)               # v401:310
+        act_n = act_n + (gate > 0.0).to(acc).sum(dim=-1, keepdim=True)
+        strong = strong + (gate > 0.5).to(acc).sum(dim=-1, keepdim=True)
+        phi_bin = phi_bin + ((phi > 0.95) | (phi < 0.05)).to(acc).sum(dim=-1, keepdim=True)
+        zsum = zsum + torch.where(z > 0, z, torch.zeros((), dtype=acc)).sum(
+            dim=-1, keepdim=True)                                  # v401:314
+        z075 = z075 + ((z > 0) & (z < 0.75)).to(acc).sum(dim=-1, keepdim=True)
+        z030 = z030 + ((z > 0) & (z < 0.30)).to(acc).sum(dim=-1, keepdim=True)
+        glogg = glogg + (gate * torch.log(gate + 1e-8)).sum(dim=-1, keepdim=True)  # v401:317-318
         gmax = torch.maximum(gmax, gate.amax(dim=-1, keepdim=True))
         if return_trace:
             trace_z.append(z)
-    den = torch.clamp_min(wsum, 1.0)                               # v401:340
-    out_f = (out / den).to(BF16).to(F32)
-    gate_sum_eps = wsum + 1e-8                                     # v401:360
+            trace_gate.append(gate)
+    den = _v401_den(wsum, zsum)                                    # v401:340
+    out_f = rnd(out / den)                                         # v401:341-342
+    gate_sum_eps = wsum + 1e-8                                     # v401:361
     ent = -glogg / gate_sum_eps + torch.log(gate_sum_eps)
     res = (
         out_f, act_n / N, gmax, st["score_lb"], s_std.mean(), wsum.mean(),
@@ -513,4 +541,5 @@ def fused_gate_srw_gelu_v401(x, h, emb, tau_offset, read, write, *,
         return res
     return res, dict(s_mean=s_mean, s_std=s_std, tau=tau, den=den,
                      gate_sum=wsum, n_active=act_n, raw_out=out,
-                     z=torch.cat(trace_z, dim=-1), nc=nc, cs=cs)
+                     z=torch.cat(trace_z, dim=-1), gate=torch.cat(trace_gate, dim=-1),
+                     nc=nc, cs=cs)

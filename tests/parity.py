@@ -7,7 +7,10 @@ Tolerances (from the hot path's contract):
     <= 2e-2 (and, per token row, <= 5e-2 of that row's norm);
   * passing set: identical outside a tie band |margin| <= delta, where
     delta covers one bf16 ulp of the score plus the tau difference (bf16),
-    or 1e-5 * max(1, s_std) (float32).
+    or 1e-5 * max(1, s_std) (float32); inside the band at most
+    MIS_BASE + MIS_PER_PAIR * (rows x units) mismatches (plus, where the
+    moments are computed another way on purpose -- Gram statistics -- every
+    pair inside that known tau shift).
 """
 
 from __future__ import annotations
@@ -48,6 +51,15 @@ def bf16_ulp(v: torch.Tensor) -> torch.Tensor:
     return torch.pow(2.0, e - 7)
 
 
+# Mismatches allowed inside the tie band.  A pair flips only when its fp32
+# score lies next to a bf16 rounding boundary (the matrix cores sum the 16-bit
+# products in another order than the CPU) and its margin is within that ulp of
+# zero, or when its margin is within the moments' fp32 summation difference
+# of zero: measured 0 - 1 per test at up to 1.3e7 (row, unit) pairs.
+MIS_BASE = 2
+MIS_PER_PAIR = 2e-7
+
+
 def check_pass_set(mask_got: torch.Tensor, margin_ref: torch.Tensor, delta: torch.Tensor):
     """Mismatches of the passing set must lie inside |margin_ref| <= delta.
 
@@ -56,3 +68,21 @@ def check_pass_set(mask_got: torch.Tensor, margin_ref: torch.Tensor, delta: torc
     mism = mask_got != ref
     outside = mism & (margin_ref.abs() > delta)
     return int(mism.sum()), int(outside.sum())
+
+
+def assert_pass_set(mask_got: torch.Tensor, margin_ref: torch.Tensor, delta: torch.Tensor,
+                    shift: torch.Tensor | None = None) -> int:
+    """The passing-set bar: no mismatch outside the tie band ``delta`` (+
+    ``shift``), and at most MIS_BASE + MIS_PER_PAIR per pair inside it, plus
+    every pair with |margin| <= ``shift`` (a known tau shift, e.g. Gram
+    moments of the unrounded scores).  Returns the mismatch count."""
+    band = delta if shift is None else delta + shift
+    n_mis, n_out = check_pass_set(mask_got, margin_ref, band)
+    bound = MIS_BASE + MIS_PER_PAIR * margin_ref.numel()
+    if shift is not None:
+        bound += int((margin_ref.abs() <= shift).sum())
+    print(f"  pass-set mismatches {n_mis} (outside tie band {n_out}; allowed in band {bound:.1f})",
+          flush=True)
+    assert n_out == 0, f"{n_out} passing-set mismatches outside the tie band ({n_mis} total)"
+    assert n_mis <= bound, f"{n_mis} passing-set mismatches inside the tie band, more than {bound:.1f}"
+    return n_mis

@@ -73,8 +73,12 @@ def test_flax_layout_is_read(pkg, tmp_path):
     tree = {
         "params": {"neuron_pool": {"know_emb": _ext_array(emb), "know_scale": _ext_array(scale)},
                    "block_0": {"attn": {"expand_O": {"kernel": _ext_array(bf_bits, "bfloat16")}}},
-                   "chunked": {"__msgpack_chunked_array__": True, "shape": [2, 5],
-                               "chunks": {"0": _ext_array(big[:6]), "1": _ext_array(big[6:])}}},
+                   # flax's _chunk: shape and pieces both as maps keyed '0', '1', ... (_tuple_to_dict)
+                   "chunked": {"__msgpack_chunked_array__": True, "shape": {"0": 2, "1": 5},
+                               "chunks": {"0": _ext_array(big[:6]), "1": _ext_array(big[6:])}},
+                   # a shape stored as a list is read as well
+                   "chunked_list": {"__msgpack_chunked_array__": True, "shape": [5, 2],
+                                    "chunks": {"0": _ext_array(big[:4]), "1": _ext_array(big[4:])}}},
         "opt_state": {"0": {"count": msgpack.ExtType(3, msgpack.packb(([], "int32", np.int32(7).tobytes())))},
                       "1": {}},
         "epoch": 2, "step": 12345, "best_val_loss": 3.25, "config": {"d_model": 16, "n_know": 40},
@@ -90,6 +94,7 @@ def test_flax_layout_is_read(pkg, tmp_path):
     assert torch.equal(p["block_0"]["attn"]["expand_O"]["kernel"].float(),
                        torch.from_numpy(w_bf).to(torch.bfloat16).float())
     assert torch.equal(p["chunked"], torch.from_numpy(big.reshape(2, 5)))
+    assert torch.equal(p["chunked_list"], torch.from_numpy(big.reshape(5, 2)))
     params = pkg.checkpoint.load_params(str(path))
     assert params["neuron_pool"]["know_emb"].shape == (40, 16)      # leading replica axis dropped
     assert params["neuron_pool"]["know_scale"].shape == (1,)        # 1-d arrays keep it
@@ -135,3 +140,19 @@ def test_model_params_round_trip(pkg, tmp_path):
     ckpt = pkg.checkpoint.load_checkpoint(str(path))
     assert ckpt["step"] == 99 and torch.equal(ckpt["opt_state"]["0"]["mu"], params["norm"]["scale"])
     assert pkg.checkpoint.config_from_checkpoint(ckpt).vocab_size == 50
+
+
+def test_chunked_array_round_trip(pkg, tmp_path, monkeypatch):
+    """An array above the chunk limit is written as flax's _chunk writes it
+    (shape and pieces as maps keyed '0', '1', ...) and read back whole."""
+    monkeypatch.setattr(pkg.checkpoint, "_MAX_CHUNK", 64)       # bytes: forces several pieces
+    big = torch.arange(3 * 7 * 5, dtype=torch.float32).reshape(3, 7, 5)
+    path = tmp_path / "chunked.flax"
+    pkg.checkpoint.save_checkpoint(str(path), {"pool": {"w": big}})
+    raw = msgpack.unpackb(path.read_bytes(), raw=False, strict_map_key=False)
+    stored = raw["params"]["pool"]["w"]
+    assert stored["__msgpack_chunked_array__"] is True
+    assert stored["shape"] == {"0": 3, "1": 7, "2": 5}
+    assert len(stored["chunks"]) > 1 and set(stored["chunks"]) == {str(i) for i in range(len(stored["chunks"]))}
+    back = pkg.checkpoint.load_checkpoint(str(path))["params"]["pool"]["w"]
+    assert torch.equal(back, big)

@@ -11,7 +11,8 @@ floor, and the full configs[0] size.
 Tolerances: out within 2e-2 relative (Frobenius) of the bf16 restatement,
 and the passing set identical outside a tie band of one bf16 score ulp plus
 the tau slack -- the score GEMM's fp32 accumulation order differs from the
-CPU matmul, so a score can round to the neighbouring bf16 value.
+CPU matmul, so a score can round to the neighbouring bf16 value -- with the
+count inside the band bounded (tests/parity.py).
 """
 
 from __future__ import annotations
@@ -20,7 +21,7 @@ import pytest
 import torch
 
 from oracle import srw_ref
-from tests.parity import (REL_BF16, bf16_ulp, check_pass_set, rel_fro, row_rel_max,
+from tests.parity import (REL_BF16, assert_pass_set, bf16_ulp, rel_fro, row_rel_max,
                           unpack_mask)
 
 pytestmark = pytest.mark.gpu
@@ -89,13 +90,12 @@ def _check(got, ref, tr, T, N, D, out_tol=REL_BF16, extra_delta=None):
     assert torch.allclose(got["gate_sum"][:, 0], tr["gate_sum"].reshape(T), rtol=2e-3, atol=1e-5)
     margin = tr["margin"].reshape(T, N)
     score = margin + tr["tau"].reshape(T, 1) + 0.5
-    delta = 2 * bf16_ulp(score) + 1e-4 * tr["s_std"].reshape(T, 1)
-    if extra_delta is not None:
-        delta = delta + extra_delta.reshape(T, 1)
+    # one bf16 ulp of the score + a bound on the moments' fp32 summation
+    # difference in tau
+    delta = bf16_ulp(score) + 1e-4 * tr["s_std"].reshape(T, 1)
     mask = unpack_mask(got["pass_mask"][:, 0], N)
-    n_mis, n_out = check_pass_set(mask, margin, delta)
-    print(f"  pass-set mismatches {n_mis} (outside tie band {n_out})", flush=True)
-    assert n_out == 0
+    assert_pass_set(mask, margin, delta,
+                    shift=None if extra_delta is None else extra_delta.reshape(T, 1).expand(T, N))
     # bits beyond N in the last word are zero
     words = got["pass_mask"][:, 0]
     full = unpack_mask(words, words.shape[-1] * 64)

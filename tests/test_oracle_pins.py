@@ -13,6 +13,7 @@ import math
 
 import numpy as np
 import pytest
+import scipy.optimize
 import scipy.special
 import scipy.stats
 import torch
@@ -382,3 +383,199 @@ def test_planted_transposed_operand_is_caught(monkeypatch):
         return (gate * xr) @ w_write / den, dict(den=den, tau=tau, gate=gate)
     monkeypatch.setattr(srw_ref, "_srw_inference_core", mutated)
     assert _brute_mismatch()
+
+
+# ---------------------------------------------------------------- v4.0.1 fused function
+#
+# fused_gate_srw_gelu_v401 (v401:230-367) is pinned through its exact-arithmetic
+# form (float64, no bf16 rounding): every output against the brute-force loop
+# and numpy / scipy closed forms computed from a textbook float64 score matrix;
+# its bf16 form against the exact form within the bf16 error budget; planted
+# mistakes (den from sum z+, R / W rows not normalised, gate below zero,
+# Phi without the 1/sqrt(2)) must fail the brute-force comparison.
+
+def _v401_inputs(seed, T=5, D=12, dr=8, N=40, tau=0.4):
+    """Inputs whose R and W rows are NOT unit-norm (scaled by 0.5 .. 2.5), so
+    that the forward normalisation of v401:300-301 changes the result."""
+    x, h, e, tau_off, r, w = _rand_inputs(T, D, dr, N, seed, tau=tau)
+    g = torch.Generator().manual_seed(seed + 1000)
+    r = r * (0.5 + 2.0 * torch.rand(N, 1, generator=g, dtype=F64))
+    w = w * (0.5 + 2.0 * torch.rand(N, 1, generator=g, dtype=F64))
+    return x, h, e, tau_off, r, w
+
+
+def _v401_exact(x, h, e, tau, r, w, max_chunk):
+    return srw_ref.fused_gate_srw_gelu_v401(x[None], h[None], e, tau[None], r, w,
+                                            max_chunk_size=max_chunk, exact=True,
+                                            return_trace=True)
+
+
+def _v401_brute_mismatch(seed=5, max_chunk=20):
+    """True iff the exact fused v4.0.1 oracle disagrees with the brute-force
+    loop (one-pass std, as the fused function's pass 1, v401:272-273)."""
+    x, h, e, tau, r, w = _v401_inputs(seed)
+    res, tr = _v401_exact(x, h, e, tau, r, w, max_chunk)
+    for t in range(x.shape[0]):
+        b = brute.srw_token(x[t].tolist(), h[t].tolist(), e.tolist(), float(tau[t, 0]),
+                            r.tolist(), w.tolist(), gate="gelu_v401", onepass=True)
+        if not (np.allclose(res[0][0, t].numpy(), b["out"], rtol=1e-10, atol=1e-13)
+                and math.isclose(float(tr["den"][0, t, 0]), b["den"], rel_tol=1e-12)
+                and math.isclose(float(tr["gate_sum"][0, t, 0]), b["gate_sum"], rel_tol=1e-12)):
+            return True
+    return False
+
+
+@pytest.mark.parametrize("seed", [5, 6, 7])
+@pytest.mark.parametrize("max_chunk", [20, 4096])
+def test_fused_v401_exact_matches_brute_force(seed, max_chunk):
+    x, h, e, tau, r, w = _v401_inputs(seed)
+    res, tr = _v401_exact(x, h, e, tau, r, w, max_chunk)
+    assert tr["nc"] == (2 if max_chunk == 20 else 1)
+    for t in range(x.shape[0]):
+        b = brute.srw_token(x[t].tolist(), h[t].tolist(), e.tolist(), float(tau[t, 0]),
+                            r.tolist(), w.tolist(), gate="gelu_v401", onepass=True)
+        assert np.allclose(res[0][0, t].numpy(), b["out"], rtol=1e-10, atol=1e-13)
+        assert math.isclose(float(tr["den"][0, t, 0]), b["den"], rel_tol=1e-12)
+        assert math.isclose(float(tr["tau"][0, t, 0]), b["tau"], rel_tol=1e-11, abs_tol=1e-13)
+        assert np.allclose(tr["gate"][0, t].numpy(), b["gates"], rtol=1e-10, atol=1e-15)
+        assert int(tr["n_active"][0, t, 0]) == b["n_active"]
+        assert b["den"] > 1.0       # the floor is not what the comparison rests on
+
+
+def test_fused_v401_exact_equals_inference_form():
+    """In exact arithmetic the fused function (one-pass std, chunked) and the
+    pinned _srw_inference v4.0.1 form (two-pass std, v401:1443-1463) agree."""
+    x, h, e, tau, r, w = _v401_inputs(8, T=6, D=16, dr=12, N=90)
+    res, _ = _v401_exact(x, h, e, tau, r, w, 30)
+    ref = srw_ref.srw_inference_gelu_v401(x, h, e, tau, r, w, acc_dtype=F64)
+    assert torch.allclose(res[0][0], ref, rtol=1e-9, atol=1e-13)
+
+
+def test_fused_v401_diagnostics_closed_forms():
+    """The 16-tuple (v401:343-367) against numpy / scipy on the textbook
+    float64 score matrix."""
+    T, D, dr, N = 24, 32, 16, 300
+    x, h, e, tau, r, w = _v401_inputs(9, T=T, D=D, dr=dr, N=N, tau=0.3)
+    res, tr = _v401_exact(x, h, e, tau, r, w, 100)
+    o = dict(zip(srw_ref.FUSED_V401_OUTPUT_NAMES, res))
+    s = (h.numpy() @ e.numpy().T)                                  # [T, N] float64
+    mean = s.mean(-1, keepdims=True)
+    std = np.sqrt((s * s).mean(-1, keepdims=True) - mean ** 2) + 1e-8
+    tau_np = mean + tau.numpy() * std
+    z = (s - tau_np) / std
+    gate = np.where(z > 0, z * scipy.special.ndtr(z), 0.0)
+    act = (z > 0).sum(-1)
+    assert np.allclose(tr["gate"][0].numpy(), gate, rtol=1e-10, atol=1e-14)
+    assert np.array_equal(np.rint(o["active_frac"][0, :, 0].numpy() * N), act)
+    assert np.allclose(o["gate_max"][0, :, 0].numpy(), gate.max(-1), rtol=1e-12)
+    z_star = scipy.optimize.brentq(lambda v: v * scipy.special.ndtr(v) - 0.5, 0.0, 3.0)
+    assert np.array_equal(np.rint(o["strong_frac"][0, :, 0].numpy() * N), (z > z_star).sum(-1))
+    z95 = scipy.special.ndtri(0.95)                                # Phi > .95 <=> z > z95
+    assert np.array_equal(np.rint(o["boundary_frac"][0, :, 0].numpy() * N), (np.abs(z) > z95).sum(-1))
+    assert np.allclose(o["z_mean_active"][0, :, 0].numpy(),
+                       np.where(z > 0, z, 0).sum(-1) / (act + 1e-8), rtol=1e-12)
+    assert math.isclose(float(o["tau_abs_mean"]), float(tau_np.mean()), rel_tol=1e-12)
+    assert math.isclose(float(o["z_lt_075_frac"]),
+                        float((((z > 0) & (z < 0.75)).sum(-1) / (act + 1e-8)).mean()), rel_tol=1e-12)
+    assert math.isclose(float(o["z_lt_030_frac"]),
+                        float((((z > 0) & (z < 0.30)).sum(-1) / (act + 1e-8)).mean()), rel_tol=1e-12)
+    assert math.isclose(float(o["score_std"]), float(std.mean()), rel_tol=1e-12)
+    assert math.isclose(float(o["gate_sum"]), float(gate.sum(-1).mean()), rel_tol=1e-12)
+    assert math.isclose(float(o["active_n_mean"]), float(act.mean()), rel_tol=1e-12)
+    assert math.isclose(float(o["active_per_token_std"]), float(act.std()), rel_tol=1e-12)
+    assert math.isclose(float(o["score_skew"]), float(scipy.stats.skew(s, axis=-1).mean()),
+                        rel_tol=1e-6, abs_tol=1e-9)
+    pn = s.mean(axis=0)
+    assert math.isclose(float(o["score_lb"]), float(pn.var() / (pn.mean() ** 2 + pn.var() + 1e-2)),
+                        rel_tol=1e-9)
+    assert math.isclose(float(o["gate_entropy"]), float(scipy.stats.entropy(gate, axis=-1).mean()),
+                        rel_tol=1e-6)
+
+
+def test_fused_v401_bf16_within_budget_of_exact():
+    """The bf16 form (the reference's rounding points) stays within the bf16
+    error budget of the exact form; chunking moves only the per-chunk bf16
+    rounding of the write GEMM."""
+    T, D, dr, N = 32, 64, 32, 900
+    x, h, e, tau, r, w = _v401_inputs(10, T=T, D=D, dr=dr, N=N, tau=0.5)
+    ex, _ = _v401_exact(x, h, e, tau, r, w, 300)
+    bf = srw_ref.fused_gate_srw_gelu_v401(x[None].float(), h[None].float(), e.float(), tau[None].float(),
+                                          r.float(), w.float(), max_chunk_size=300)
+    rel = float((bf[0][0].double() - ex[0][0]).norm() / ex[0][0].norm())
+    assert rel < 1.5e-2
+    one = srw_ref.fused_gate_srw_gelu_v401(x[None].float(), h[None].float(), e.float(), tau[None].float(),
+                                           r.float(), w.float(), max_chunk_size=4096)
+    relc = float((one[0][0] - bf[0][0]).norm() / one[0][0].norm())
+    assert 0 < relc < 1e-2
+
+
+def test_v401_pins_accept_unmutated_oracle():
+    assert not _v401_brute_mismatch()
+
+
+def _gate_gelu_below_zero(raw_f, s_std):
+    z = raw_f / s_std
+    phi = 0.5 * (1.0 + torch.erf(z * 0.7071067811865476))
+    return z, phi, z * phi                    # wrong: no zero for z <= 0
+
+
+def _gate_gelu_no_sqrt2(raw_f, s_std):
+    z = raw_f / s_std
+    phi = 0.5 * (1.0 + torch.erf(z))          # wrong: erf(z) for Phi(z)
+    return z, phi, torch.where(z > 0, z * phi, torch.zeros((), dtype=z.dtype))
+
+
+V401_MUTATIONS = {
+    "den_from_z_plus_sum": ("_v401_den", lambda g, zp: torch.clamp_min(zp, 1.0)),
+    "rows_not_normalised": ("_norm_rows", lambda t: t),
+    "gate_below_zero": ("gate_gelu_v401", _gate_gelu_below_zero),
+    "phi_without_sqrt2": ("gate_gelu_v401", _gate_gelu_no_sqrt2),
+}
+
+
+@pytest.mark.parametrize("name", sorted(V401_MUTATIONS))
+def test_planted_v401_mistakes_are_caught(monkeypatch, name):
+    attr, fn = V401_MUTATIONS[name]
+    monkeypatch.setattr(srw_ref, attr, fn)
+    assert _v401_brute_mismatch()
+
+
+# ---------------------------------------------------------------- gate_norm
+
+def _gate_norm_matches_brute(gate_norm, x, h, e, tau, r, w):
+    """gate_norm (v41:1760) against gate / max(sum gate, 1e-8) of the
+    brute-force loop's gates."""
+    for t in range(x.shape[0]):
+        b = brute.srw_token(x[t].tolist(), h[t].tolist(), e.tolist(), float(tau[t, 0]),
+                            r.tolist(), w.tolist())
+        g = np.array(b["gates"])
+        if not np.allclose(gate_norm[t].numpy(), g / max(g.sum(), 1e-8), rtol=1e-10, atol=1e-300):
+            return False
+    return True
+
+
+def test_gate_norm_matches_brute_force_and_sums_to_one():
+    T, D, dr, N = 4, 12, 8, 40
+    x, h, e, tau, r, w = _rand_inputs(T, D, dr, N, 21)
+    out, gate, gnorm = srw_ref.srw_inference_with_gates(x, h, e, tau, r, w, acc_dtype=F64)
+    assert _gate_norm_matches_brute(gnorm, x, h, e, tau, r, w)
+    assert torch.allclose(gnorm.sum(-1), torch.ones(T, dtype=F64), rtol=1e-12)
+    assert torch.equal(out, srw_ref.srw_inference(x, h, e, tau, r, w, acc_dtype=F64))
+    # plausible mistakes fail the same check
+    _, tr = srw_ref.srw_inference(x, h, e, tau, r, w, acc_dtype=F64, return_trace=True)
+    assert not _gate_norm_matches_brute(gate / tr["intensity"].sum(-1, keepdim=True), x, h, e, tau, r, w)
+    assert not _gate_norm_matches_brute(gate / tr["den"], x, h, e, tau, r, w)
+    assert not _gate_norm_matches_brute(tr["activation"] / tr["activation"].sum(-1, keepdim=True),
+                                        x, h, e, tau, r, w)
+
+
+def test_gate_norm_floor():
+    """Every margin well below zero: sum gate < 1e-8, so gate_norm = gate / 1e-8
+    (the clamp of v41:1760), not gate / sum gate."""
+    T, D, dr, N = 3, 12, 8, 40
+    x, h, e, tau, r, w = _rand_inputs(T, D, dr, N, 22, tau=2.4)
+    _, gate, gnorm = srw_ref.srw_inference_with_gates(x, h, e, tau, r, w, acc_dtype=F64)
+    assert bool((gate.sum(-1) < 1e-8).all()) and bool((gate.sum(-1) > 0).all())
+    assert torch.equal(gnorm, gate / 1e-8)
+    assert _gate_norm_matches_brute(gnorm, x, h, e, tau, r, w)
+    assert not _gate_norm_matches_brute(gate / gate.sum(-1, keepdim=True), x, h, e, tau, r, w)
