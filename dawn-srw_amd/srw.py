@@ -149,7 +149,10 @@ class _FusedSrw(torch.autograd.Function):
         hb = h.reshape(B * S, routes, h.shape[-1]).to(bf).contiguous()
         tau = tau_offset.reshape(B * S, routes).to(torch.float32).contiguous()
         eb, rdb, wb = (t.to(bf).contiguous() for t in (emb, read, write))
-        res = srw_forward(xb, hb, eb, tau, rdb, wb, stats="onepass", consts=consts,
+        # the caller's h is x itself (score = x.E^T, one route): pass the one
+        # tensor, which lets the kernels hold a single operand in registers
+        h_call = xb if (h is x and routes == 1) else hb
+        res = srw_forward(xb, h_call, eb, tau, rdb, wb, stats="onepass", consts=consts,
                           chunk_size=cs, diag=True, want_mask=False)
         shape = (B, S, D) if routes == 1 else (B, S, 2, D)
         out = res["out"].reshape(shape).to(torch.float32)

@@ -1,0 +1,213 @@
+"""GPU: the BASELINE configurations at their own sizes, and the training
+diagnostics of the matrix-core path with dead units present.
+
+* configs[0] at float32 (_srw_inference, models/dawn_spatial_v41_exp.py
+  :1713-1738): the full Know pool (N = 25 200, d = 384) on a 64-token
+  subset of the T = 4096 batch (rows are token-independent), within 1e-5;
+* the 12-layer 40M model at vocab 32 000 -- one 64-token
+  sequence against the oracle model (oracle/dawn_ref.py), and the full
+  B = 32 x S = 512 forward checked for finiteness and causality;
+* the scaled Know pool (d = 1024, N = 100 000, T = 16 384, tau
+  calibrated to 2 % pass) -- 128 token rows against the oracle's
+  fused_gate_srw (:415-635), plus whole-batch properties;
+* dead units on the matrix-core diagnostics path (SRW_FLAG_DIAG): the
+  drop-in 22-tuple's dead_count, dead_penalty and score_lb (:477-483,
+  :543-552) against the oracle with planted dead units.
+
+Every test prints its case before it touches the GPU.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import dawn_ref, srw_ref
+from tests.parity import (REL_BF16, REL_F32, ROW_REL_BF16, assert_pass_set, bf16_ulp, rel_fro,
+                          row_rel_max, unpack_mask)
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+F32 = torch.float32
+
+
+def test_configs0_fp32_full_pool_token_subset(pkg, dev):
+    """configs[0] as written (float32 _srw_inference) over the full Know pool;
+    64 of the 4096 tokens (the inputs' prefix)."""
+    shape = pkg.inputs.CONFIGS["know"]
+    T = 64
+    print(f"[gpu] configs[0] fp32 T{T} (of {shape.T}) D{shape.D} N{shape.N}", flush=True)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=0, T=T)
+    x = inp["x"].to(dev)
+    res = pkg.srw_forward(x, x, inp["emb"].to(dev), inp["tau_offset"].to(dev), inp["read"].to(dev),
+                          inp["write"].to(dev), stats="centered", want_mask=True)
+    torch.cuda.synchronize()
+    out = res["out"][:, 0].cpu()
+    ref, tr = srw_ref.srw_inference(inp["x"], inp["x"], inp["emb"], inp["tau_offset"], inp["read"],
+                                    inp["write"], return_trace=True)
+    err = rel_fro(out, ref)
+    print(f"  path {res['path']}, out rel err {err:.3e}", flush=True)
+    assert out.dtype == F32
+    assert err <= REL_F32
+    assert torch.allclose(res["den"][:, 0].cpu(), tr["den"][:, 0], rtol=1e-5)
+    delta = 1e-5 * torch.clamp_min(tr["s_std"], 1.0)
+    assert_pass_set(unpack_mask(res["pass_mask"][:, 0].cpu(), shape.N), tr["margin"], delta)
+
+
+@pytest.fixture(scope="module")
+def scaled(pkg, dev):
+    """configs[4] inputs (seed 0, tau calibrated to 2 %) and one GPU call."""
+    shape = pkg.inputs.CONFIGS["scaled"]
+    print(f"[gpu] configs[4] full call T{shape.T} D{shape.D} N{shape.N}", flush=True)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=0)
+    tau_value = pkg.inputs.calibrate_tau_offset(inp, shape.pass_target)
+    inp["tau_offset"].fill_(tau_value)
+    _, cs = srw_ref.chunk_plan(shape.N, 12500)
+    x = inp["x"].to(BF).to(dev)
+    res = pkg.srw_forward(x, x, inp["emb"].to(BF).to(dev), inp["tau_offset"].to(dev),
+                          inp["read"].to(BF).to(dev), inp["write"].to(BF).to(dev), chunk_size=cs)
+    torch.cuda.synchronize()
+    got = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in res.items()}
+    del res, x
+    torch.cuda.empty_cache()
+    return shape, inp, got
+
+
+def test_configs4_rows_match_oracle(scaled):
+    shape, inp, got = scaled
+    Ts = 128
+    print(f"[gpu] configs[4] first {Ts} rows against the oracle (path {got['path']})", flush=True)
+    assert got["path"] == "tiled_bf16"
+    x = inp["x"][:Ts]
+    ref, tr = srw_ref.fused_gate_srw(x[None], x[None], inp["emb"], inp["tau_offset"][:Ts][None],
+                                     inp["read"], inp["write"], max_chunk_size=12500,
+                                     return_trace=True)
+    out_ref = ref[0][0]
+    out = got["out"][:Ts, 0].float()
+    err = rel_fro(out, out_ref)
+    print(f"  out rel err {err:.3e}, worst row {row_rel_max(out, out_ref):.3e}", flush=True)
+    assert err <= REL_BF16
+    assert row_rel_max(out, out_ref) <= ROW_REL_BF16
+    assert bool(((got["den"][:Ts, 0] - tr["den"].reshape(Ts)).abs() <= 2e-4 * tr["den"].reshape(Ts)).all())
+    assert torch.allclose(got["gate_sum"][:Ts, 0], tr["gate_sum"].reshape(Ts), rtol=2e-3, atol=1e-5)
+    margin = tr["margin"].reshape(Ts, shape.N)
+    score = margin + tr["tau"].reshape(Ts, 1) + 0.5
+    delta = bf16_ulp(score) + 1e-4 * tr["s_std"].reshape(Ts, 1)
+    assert_pass_set(unpack_mask(got["pass_mask"][:Ts, 0], shape.N), margin, delta)
+
+
+def test_configs4_whole_batch_properties(scaled):
+    shape, inp, got = scaled
+    T, N, D = shape.T, shape.N, shape.D
+    print(f"[gpu] configs[4] whole-batch properties T{T}", flush=True)
+    out = got["out"][:, 0].float()
+    assert out.shape == (T, D) and bool(torch.isfinite(out).all())
+    frac = float(got["n_active"].double().mean()) / N
+    print(f"  mean pass fraction {frac:.4f}", flush=True)
+    assert 0.015 <= frac <= 0.025                     # calibrated to 2 % on the first 256 tokens
+    assert bool((got["den"] >= N * 1e-4 * (1 - 1e-5)).all())   # den >= N eps (v41:527, 584)
+    mask = unpack_mask(got["pass_mask"][:, 0], N)
+    assert torch.equal(got["n_active"][:, 0].long(), mask.sum(dim=1))
+    words = got["pass_mask"][:, 0]
+    assert not bool(unpack_mask(words, words.shape[-1] * 64)[:, N:].any())
+
+
+@pytest.fixture(scope="module")
+def model40m(pkg, dev):
+    cfg = pkg.DawnConfig(vocab_size=32000)
+    print(f"[gpu] configs[2] 40M model: {cfg}", flush=True)
+    params = pkg.init_params(cfg, seed=0)
+    return cfg, params, pkg.DawnModel(params, cfg, dev)
+
+
+def test_configs2_sequence_matches_oracle(model40m):
+    cfg, params, m = model40m
+    S = 64
+    ids = torch.randint(0, cfg.vocab_size, (1, S), generator=torch.Generator().manual_seed(11))
+    print(f"[gpu] configs[2] forward B1 S{S} against the oracle model", flush=True)
+    got = m.forward(ids)
+    torch.cuda.synchronize()
+    want = dawn_ref.forward(params, cfg, ids)
+    err = rel_fro(got.cpu(), want)
+    print(f"  logits rel err {err:.3e}", flush=True)
+    assert got.shape == (1, S, cfg.vocab_size)
+    assert err <= REL_BF16
+
+
+def test_configs2_full_batch_finite_and_causal(model40m, dev):
+    cfg, _, m = model40m
+    B, S, cut = 32, 512, 300
+    ids = torch.randint(0, cfg.vocab_size, (B, S), generator=torch.Generator().manual_seed(12))
+    alt = ids.clone()
+    alt[:, cut:] = (alt[:, cut:] + 101) % cfg.vocab_size
+    print(f"[gpu] configs[2] forward B{B} S{S}, tokens changed from position {cut}", flush=True)
+    a = m.forward(ids.to(dev))
+    torch.cuda.synchronize()
+    assert a.shape == (B, S, cfg.vocab_size)
+    assert bool(torch.isfinite(a).all())
+    head = a[:, :cut].clone()
+    tail = a[:, cut:].clone()
+    del a
+    b = m.forward(alt.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(head, b[:, :cut])               # no later token moves an earlier logit
+    assert (tail - b[:, cut:]).abs().max().item() > 1e-3
+    del b, head, tail
+    torch.cuda.empty_cache()
+
+
+def _dead_inputs(pkg, T, D, N, dr, seed, n_dead_every=37):
+    """Inputs with every 37th unit planted dead: its embedding row is
+    -0.05 mean(h) / |mean(h)|, so its score stays near 0 (|score| <= 0.05
+    |h_t|) while tau + 0.5 is ~1 -- it never passes -- and its mean score over
+    the tokens is negative (a nonzero dead penalty)."""
+    hx = dr == D
+    shape = pkg.inputs.PoolShape(T=T, D=D, N=N, dr=dr, routes=1, h_is_x=hx, router=not hx)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=seed)
+    inp["tau_offset"].fill_(0.5)
+    dead = torch.arange(0, N, n_dead_every)
+    h = inp["x"] if hx else inp["h"][:, 0]
+    hm = h.mean(0)
+    inp["emb"][dead] = -0.05 * hm / hm.norm()
+    return inp, dead
+
+
+@pytest.mark.parametrize("T,N,dr,chunk", [(256, 3000, 384, 1500), (512, 6000, 384, 12500),
+                                          (512, 25200, 128, 12500)])
+def test_diag_dead_units_match_oracle(pkg, dev, T, N, dr, chunk):
+    """The drop-in fused_gate_srw (SRW_FLAG_DIAG on the matrix cores) with
+    planted dead units: dead_count, dead_penalty and score_lb against the
+    oracle's 22-tuple.  d_route = d_model with h the very tensor x (score =
+    x.E^T), and the Know pool's own shape (router h, d_route 128)."""
+    D = 384
+    print(f"[gpu] diag dead units T{T} D{D} dr{dr} N{N} chunk {chunk}", flush=True)
+    inp, dead = _dead_inputs(pkg, T, D, N, dr, seed=T + N)
+    B, S = 1, T
+    x = inp["x"].reshape(B, S, D)
+    h = x if dr == D else inp["h"].reshape(B, S, dr)
+    tau = inp["tau_offset"].reshape(B, S, 1)
+    fused = pkg.make_sharded_srw(None, max_chunk_size=chunk)
+    xd = x.to(dev)
+    hd = xd if dr == D else h.to(dev)
+    got = fused(xd, hd, inp["emb"].to(dev), tau.to(dev), inp["read"].to(dev), inp["write"].to(dev))
+    torch.cuda.synchronize()
+    path = pkg._capi.last_path()
+    ref, tr = srw_ref.fused_gate_srw(x, h, inp["emb"], tau, inp["read"], inp["write"],
+                                     max_chunk_size=chunk, return_trace=True)
+    o = dict(zip(srw_ref.FUSED_OUTPUT_NAMES, (t.detach().cpu() for t in got)))
+    r = dict(zip(srw_ref.FUSED_OUTPUT_NAMES, ref))
+    gmax_unit = tr["gate"][0].amax(0)
+    # units whose max gate lies within rounding of the 0.01 threshold may fall either way
+    ambiguous = int(((gmax_unit - 0.01).abs() <= 2e-3 * 0.01 + 1e-7).sum())
+    print(f"  path {path}; dead_count {float(o['dead_count'])} vs {float(r['dead_count'])} "
+          f"(planted {len(dead)}, ambiguous {ambiguous}); dead_penalty {float(o['dead_penalty']):.6f} vs "
+          f"{float(r['dead_penalty']):.6f}; score_lb {float(o['score_lb']):.6e} vs {float(r['score_lb']):.6e}",
+          flush=True)
+    assert path in ("mfma_bf16", "mfma_ss_bf16")
+    assert float(r["dead_count"]) >= len(dead)
+    assert abs(float(o["dead_count"]) - float(r["dead_count"])) <= ambiguous
+    assert float(r["dead_penalty"]) > 0
+    assert abs(float(o["dead_penalty"]) - float(r["dead_penalty"])) <= 1e-3 * float(r["dead_penalty"]) + 1e-6
+    assert abs(float(o["score_lb"]) - float(r["score_lb"])) <= 2e-2 * abs(float(r["score_lb"])) + 1e-7
+    assert rel_fro(o["out"], r["out"]) <= REL_BF16
