@@ -19,11 +19,13 @@ import threading
 import torch  # noqa: F401  (must precede loading the HIP library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libsrw_amd.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 MAX_BATCH = 4          # SRW_MAX_BATCH
 
 # srw_status_t
-SRW_OK, SRW_EINVAL, SRW_EUNSUPPORTED, SRW_EHIP, SRW_EWORKSPACE = range(5)
+SRW_OK, SRW_EINVAL, SRW_EUNSUPPORTED, SRW_EHIP, SRW_EWORKSPACE, SRW_ESCRATCH = range(6)
+# bytes of srw_forward_noalloc's per-GPU scratch (SRW_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 64 << 20
 # srw_dtype_t
 SRW_F32, SRW_BF16 = 0, 1
 # srw_gate_t
@@ -52,7 +54,7 @@ EXPORTED_SYMBOLS = (
     "srw_abi_version", "srw_status_string", "srw_desc_init",
     "srw_workspace_size", "srw_forward", "srw_last_path",
     "srw_set_kernel_events", "srw_backward_workspace_size", "srw_backward",
-    "srw_workspace_size_batch", "srw_forward_batch",
+    "srw_workspace_size_batch", "srw_forward_batch", "srw_forward_noalloc",
 )
 
 
@@ -130,6 +132,10 @@ def load_library() -> ctypes.CDLL:
         lib.srw_forward.argtypes = [
             ctypes.POINTER(SrwDesc), ctypes.POINTER(SrwTensors), ctypes.POINTER(SrwOutputs),
             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+        lib.srw_forward_noalloc.restype = ctypes.c_int
+        lib.srw_forward_noalloc.argtypes = [
+            ctypes.POINTER(SrwDesc), ctypes.POINTER(SrwTensors), ctypes.POINTER(SrwOutputs),
+            ctypes.c_void_p]
         lib.srw_workspace_size_batch.restype = ctypes.c_int
         lib.srw_workspace_size_batch.argtypes = [ctypes.c_int32, ctypes.POINTER(SrwDesc),
                                                  ctypes.POINTER(ctypes.c_size_t)]

@@ -1,13 +1,24 @@
 // srw_capi.hip -- the extern "C" boundary of libsrw_amd.so.
 //
 // Validates a call, sizes the workspace, picks a kernel family and enqueues
-// it on the caller's stream.  No allocation, no global state beyond the
-// per-thread name of the last path taken.
+// it on the caller's stream.  No allocation; global state: the per-thread
+// name of the last path taken and, for srw_forward_noalloc, the device
+// address of the static scratch array per device.
 
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "srw_internal.hpp"
+
+// Workspace of srw_forward_noalloc: a static array in the library's code
+// object, so each GPU the library runs on holds its own copy (at its own
+// address) from the code object's load until the process ends.  Host code
+// never passes the name `scratch` to a kernel or a copy -- on the host it
+// names a shadow, not device memory -- but the device address that
+// hipGetSymbolAddress returns for the current device (scratch_address).
+static __device__ __align__(256) char scratch[SRW_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -52,6 +63,35 @@ int choose(const srw_desc_t& d, bool h_is_x) {
 
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
+// Device address of `scratch` per device, looked up once per device, with
+// that device current, on the first no-allocation call that runs there.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+srw_status_t scratch_address(hipStream_t stream, void** out) {
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return SRW_EHIP;
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t sd;
+    if (hipStreamGetDevice(stream, &sd) != hipSuccess) return SRW_EHIP;
+    dev = static_cast<int>(sd);
+  }
+  if (dev < 0 || dev >= kMaxDevices) return SRW_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) return SRW_EHIP;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess || p == nullptr) return SRW_EHIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SRW_OK;
+}
+
 size_t bytes_of(int which, const srw_desc_t& d) {
   if (which == 1) return srw::mfma_workspace_bytes(d);
   if (which == 2) return srw::tiled_workspace_bytes(d);
@@ -80,6 +120,9 @@ const char* srw_status_string(srw_status_t s) {
     case SRW_EUNSUPPORTED: return "SRW_EUNSUPPORTED: configuration not implemented";
     case SRW_EHIP: return "SRW_EHIP: HIP runtime error";
     case SRW_EWORKSPACE: return "SRW_EWORKSPACE: workspace missing or too small";
+    case SRW_ESCRATCH:
+      return "SRW_ESCRATCH: the call needs more workspace than srw_forward_noalloc's scratch holds "
+             "(SRW_NOALLOC_SCRATCH_BYTES = 64 MiB); use srw_forward with a workspace";
   }
   return "SRW_?: unknown status";
 }
@@ -199,6 +242,21 @@ srw_status_t srw_forward(const srw_desc_t* d, const srw_tensors_t* in, const srw
     return SRW_OK;
   }
   return launch_forward(a, which);
+}
+
+srw_status_t srw_forward_noalloc(const srw_desc_t* d, const srw_tensors_t* in, const srw_outputs_t* o,
+                                 void* stream) {
+  srw_status_t st = validate(d);
+  if (st != SRW_OK) return st;
+  // the scratch keeps whatever the last call on this GPU left there: a pool
+  // packed by another call must not be taken for this call's
+  if (d->flags & SRW_FLAG_POOL_CACHED) return SRW_EINVAL;
+  size_t need = 0;
+  if ((st = srw_workspace_size(d, &need)) != SRW_OK) return st;
+  if (need > SRW_NOALLOC_SCRATCH_BYTES) return SRW_ESCRATCH;
+  void* ws = nullptr;
+  if (need > 0 && (st = scratch_address(static_cast<hipStream_t>(stream), &ws)) != SRW_OK) return st;
+  return srw_forward(d, in, o, ws, need > 0 ? SRW_NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
 srw_status_t srw_workspace_size_batch(int32_t n, const srw_desc_t* descs, size_t* bytes) {

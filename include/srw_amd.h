@@ -37,8 +37,9 @@
  *
  * Conventions
  *   - Every pointer is a device pointer owned by the caller; row-major,
- *     contiguous.  The library allocates nothing: scratch memory is the
- *     caller's workspace (size from srw_workspace_size).
+ *     contiguous.  The library calls no allocator: scratch memory is the
+ *     caller's workspace (size from srw_workspace_size), or, for
+ *     srw_forward_noalloc, a static per-GPU array inside the library.
  *   - x, h, emb, read, write and out share desc->dtype (SRW_BF16 or SRW_F32).
  *     tau_offset and every per-token / per-unit statistic are float32.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
@@ -57,14 +58,15 @@
 extern "C" {
 #endif
 
-#define SRW_AMD_ABI_VERSION 5
+#define SRW_AMD_ABI_VERSION 6
 
 typedef enum srw_status {
   SRW_OK = 0,
   SRW_EINVAL = 1,       /* bad shape, pointer or constant */
   SRW_EUNSUPPORTED = 2, /* valid request the library does not implement */
   SRW_EHIP = 3,         /* a HIP runtime call failed (launch, device query) */
-  SRW_EWORKSPACE = 4    /* workspace missing or smaller than required */
+  SRW_EWORKSPACE = 4,   /* workspace missing or smaller than required */
+  SRW_ESCRATCH = 5      /* srw_forward_noalloc: the call needs more than its scratch */
 } srw_status_t;
 
 typedef enum srw_dtype {
@@ -233,6 +235,24 @@ srw_status_t srw_workspace_size(const srw_desc_t* desc, size_t* bytes);
 srw_status_t srw_forward(const srw_desc_t* desc, const srw_tensors_t* in,
                          const srw_outputs_t* outs, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* srw_forward without a workspace argument and without allocating.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory -- code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  The workspace is a static scratch array of
+ * SRW_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held from the
+ * library's first use on that GPU until the process ends; its device address
+ * is looked up once per device.  The same kernels run as in srw_forward, so
+ * the results are equal bit for bit.  Limits: a call whose
+ * srw_workspace_size exceeds the scratch returns SRW_ESCRATCH with nothing
+ * launched (64 MiB holds every decode-sized call of the 40M pools up to 128
+ * rows; prefill-sized calls need srw_forward); SRW_FLAG_POOL_CACHED is
+ * refused (SRW_EINVAL), since the scratch keeps whatever the last call on that
+ * GPU left in it.  All calls on one GPU share its scratch: calls that overlap
+ * on one GPU (two streams, two threads) race -- serialise them. */
+#define SRW_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+srw_status_t srw_forward_noalloc(const srw_desc_t* desc, const srw_tensors_t* in,
+                                 const srw_outputs_t* outs, void* stream);
 
 /* Several independent srw_forward calls on one stream.  No counterpart in
  * the reference, whose layer issues each pool's SRW as a call of its own

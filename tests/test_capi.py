@@ -162,9 +162,30 @@ def test_batch_arguments_checked_before_any_launch(C):
     assert lib.srw_forward_batch(2, good, None, o, None, 0, None) == C.SRW_EINVAL
 
 
+def test_noalloc_refusals_before_any_launch(C):
+    """srw_forward_noalloc checks its descriptor, the pool-cached flag and the
+    scratch size on the host: nothing reaches a GPU."""
+    lib = C.load_library()
+    t, o = C.SrwTensors(), C.SrwOutputs()
+    d = _desc(C, d_model=0)
+    assert lib.srw_forward_noalloc(ctypes.byref(d), ctypes.byref(t), ctypes.byref(o), None) == C.SRW_EINVAL
+    d = _desc(C, flags=C.SRW_FLAG_POOL_CACHED)
+    assert lib.srw_forward_noalloc(ctypes.byref(d), ctypes.byref(t), ctypes.byref(o), None) == C.SRW_EINVAL
+    # configs[0] at T = 4096: ~264 MiB of workspace, beyond the 64 MiB scratch
+    d = _desc(C, T=4096, d_model=384, d_route=384, n_units=25200, chunk_size=12600)
+    assert C.workspace_size(d) > C.NOALLOC_SCRATCH_BYTES
+    assert lib.srw_forward_noalloc(ctypes.byref(d), ctypes.byref(t), ctypes.byref(o), None) == C.SRW_ESCRATCH
+    # a decode-sized Know call (64 rows, d_route 128) fits
+    d = _desc(C, T=64, d_model=384, d_route=128, n_units=25200, chunk_size=12600)
+    assert 0 < C.workspace_size(d) <= C.NOALLOC_SCRATCH_BYTES
+    # no tokens: nothing to compute, no scratch looked up
+    d = _desc(C, T=0)
+    assert lib.srw_forward_noalloc(ctypes.byref(d), ctypes.byref(t), ctypes.byref(o), None) == C.SRW_OK
+
+
 def test_status_strings(C):
     lib = C.load_library()
-    for s in range(5):
+    for s in range(6):
         assert lib.srw_status_string(s).decode().startswith("SRW_")
     with pytest.raises(C.SrwError):
         C.check(C.SRW_EINVAL)
