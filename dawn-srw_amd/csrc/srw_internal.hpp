@@ -38,6 +38,11 @@ void dominant_kernel_end(hipStream_t s);
 // Fill kernel (graph-safe replacement for hipMemsetAsync).
 hipError_t fill_f32(float* p, int64_t n, float v, hipStream_t s);
 
+// dst row n = src row n / (||src row n|| + 1e-8) in bf16 for N rows of D
+// (v4.0.1 forward normalisation of the read / write rows, v401:300-301),
+// see srw_generic.hip.
+hipError_t normalize_rows_bf16(const uint16_t* src, uint16_t* dst, int64_t N, int64_t D, hipStream_t s);
+
 // Pack a bf16 [N, D] matrix unit-contiguous in matrix-core fragment order
 // (32-unit tiles; tail units zero), see srw_mfma.hip.
 hipError_t pack_unit_major(const uint16_t* src, uint16_t* dst, int64_t N, int D, hipStream_t s);
@@ -59,14 +64,16 @@ hipError_t gram_moments(const uint16_t* emb, const uint16_t* h, int64_t T, int64
 // stores the row mean in tau[] (input of a centred second pass);
 // kTauCentered: std = sqrt(sum (s - mean)^2 / N) + 1e-8 (v41:1719-1721).
 enum TauMode { kTauOnePass = 0, kTauMean = 1, kTauCentered = 2 };
+// sstd (or null): the row's s_std as well (the v4.0.1 gate's z scale).
 hipError_t launch_tau(const float* mom, const float* tau_off, float* tau, int64_t T, int S_st, int64_t N, int ms,
-                      float* token_diag, int mode, hipStream_t s);
+                      float* token_diag, int mode, hipStream_t s, float* sstd = nullptr);
 
 // Final reduction over N-splits (srw_mfma.hip): sums the fp32 partial outputs
 // out_part[S][T][D] split by split, rounds each reference chunk (spc
-// consecutive splits) to bf16, den = max(sum intensity, 1) from
-// tok_part[S_tok][T][tps] = (sum gate, sum intensity, active count, ...),
-// out = bf16(bf16(raw / den) * scale).
+// consecutive splits) to bf16, den = max(sum intensity, 1) (v4.1, v41:584)
+// or max(sum gate, 1) (den_gate: the v4.0.1 gate, v401:340) from
+// tok_part[S_tok][T][tps] = (sum gate, sum intensity or z+, active count,
+// ...), out = bf16(bf16(raw / den) * scale).
 struct FinalizeArgs {
   const float* out_part;
   const float* tok_part;
@@ -81,6 +88,7 @@ struct FinalizeArgs {
   float* token_diag;   // [T][SRW_TDIAG_COUNT] or null
   GateParams gp;
   float exp_scale;
+  int den_gate;        // den from the gate sum (v4.0.1)
 };
 hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s);
 

@@ -489,6 +489,8 @@ struct MainParams {
   float exp_scale;       // -sharpness * log2(e)
   int rb;                // decode kernel: row-block groups per split (workgroup = split * rb + group)
   const uint16_t* s_in;  // scores-streaming kernel: the moments kernel's bf16 score buffer
+  const float* sstd;     // [T] s_std per row (the v4.0.1 gate) or null
+  int gl_raw_bf16;       // the v4.0.1 gate of _srw_inference: s - tau in bf16 (v401:1451-1452)
 };
 
 // v4.1 gate of a margin m = s - tau - thr (v41:503-511), with the kernels' operations
@@ -498,6 +500,31 @@ __device__ inline float gate_of_margin(float m, const GateParams& gp, float exp_
   return act * inten;
 }
 __device__ inline float gate_of_margin(float m, const MainParams& p) { return gate_of_margin(m, p.gp, p.exp_scale); }
+
+// v4.0.1 GELU gate of a score s (v401:303-306): z = (s - tau) / s_std,
+// Phi(z) = 0.5 (1 + erf(z / sqrt 2)), gate = z Phi(z) for z > 0, else 0.
+// zpos = max(z, 0) (the row's z sum, v401:314); the unit passes <=> z > 0
+// <=> s > tau, the sign bit of tau - s.  inv_std = 1 / s_std of the row.
+// raw_bf16: s - tau rounded to bf16, as _srw_inference computes it in the
+// scores' dtype (v401:1451-1452; tau is then bf16 as well).
+// erf of the non-negative argument by Abramowitz & Stegun 7.1.26:
+// erf(x) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^(-x^2),
+// t = 1 / (1 + p x), |error| <= 1.5e-7 -- a few registers, where the
+// library erff spills the kernels' registers.
+__device__ inline float gelu_gate(float s, float tau, float inv_std, float& zpos, bool raw_bf16 = false) {
+  float raw = s - tau;
+  if (raw_bf16) raw = __uint_as_float(pack_bf16(0.0f, raw));  // the high half: bf16(raw)
+  const float z = raw * inv_std;
+  const float x = fmaxf(z, 0.0f) * 0.7071067811865476f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, x, 1.0f));
+  float q = fmaf(1.061405429f, t, -1.453152027f);
+  q = fmaf(q, t, 1.421413741f);
+  q = fmaf(q, t, -0.284496736f);
+  q = fmaf(q, t, 0.254829592f);
+  const float erf = 1.0f - q * t * __builtin_amdgcn_exp2f(-x * x * 1.4426950408889634f);
+  zpos = z > 0.0f ? z : 0.0f;
+  return z > 0.0f ? z * (0.5f * (1.0f + erf)) : 0.0f;
+}
 
 // Software pipeline over the split's 32-unit tiles.  Iteration i runs the
 // score/read GEMMs of tile i+1 interleaved (sched_group_barrier) with the gate
@@ -838,9 +865,16 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
 constexpr int kWsThreads = 512;
 
 // DG: training diagnostics -- per-token extras in tok_part (TPS = 12), per-unit
-// score sums and gate maxima into unit_diag (atomics)
-template <int DB, int KH, bool HX, bool DG>
+// score sums and gate maxima into unit_diag (atomics).  GL: the v4.0.1 GELU
+// gate (p.sstd; the row sums carry z+ where v4.1 has the intensity), without
+// diagnostics.
+template <int DB, int KH, bool HX, bool DG, bool GL = false>
 __device__ __attribute__((always_inline)) inline void main_ws_body(const MainParams& p, const int bid) {
+  static_assert(!(DG && GL), "the GELU gate has no diagnostics variant here");
+  // With the GELU gate the producer gates (its registers have room for the
+  // longer element chain; the consumer's are held by the write GEMM's
+  // accumulators): it hands the consumer bf16(gate) where the scores go,
+  // keeps the row sums and emits the pass bits.
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int TPS = DG ? kTokPartDiag : 4;
   constexpr int D = DB * 32;
@@ -928,6 +962,10 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
     // 0.9 <=> |arg| < log2 9; 0.05 / 0.95: log2 19; 0.2 / 0.8: 2), capped
     // intensities (s >= tau + thr + cut + max_intensity - 1e-3)
     const float tau_t = DG ? p.tau[tl] : 0.f;
+    // the GELU gate's row: tau (bf16 for _srw_inference) and 1 / s_std
+    const float gl_tau = GL ? (p.gl_raw_bf16 ? __uint_as_float(pack_bf16(0.0f, p.tau[tl])) : p.tau[tl]) : 0.f;
+    const float gl_istd = GL ? 1.0f / p.sstd[tl] : 1.f;
+    float gl_gsum = 0.f;
     float smax = -INFINITY, isum = 0.f;
     uint32_t n_strong = 0, n_bound = 0, n_075 = 0, n_030 = 0, n_cap = 0, nact = 0;
     // Drain the x / h loads here: left pending into the tile loop, they make
@@ -977,6 +1015,48 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
           sx[4 * q + 1] = pack_bf16(sacc[4 * q + 2], sacc[4 * q + 3]);
           sx[4 * q + 2] = pack_bf16(racc[4 * q], racc[4 * q + 1]);      // bf16 x.r (v41:517)
           sx[4 * q + 3] = pack_bf16(racc[4 * q + 2], racc[4 * q + 3]);
+        }
+        if constexpr (GL) {
+          // v4.0.1 gate of the 16 elements (v401:303-310): bf16(gate) replaces
+          // the score pairs of sx; gate and z+ sums, pass bits (z > 0)
+          const int64_t u0 = static_cast<int64_t>(ta + it) * kUnitTile;
+          const bool full = u0 >= lo && u0 + kUnitTile <= hi;
+          uint32_t bits = 0;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int w = 4 * (q >> 1) + (q & 1);  // the word of elements 2q, 2q + 1
+            float g2[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const float sv = e ? hi_f32(sx[w]) : lo_f32(sx[w]);
+              float zp;
+              float g = gelu_gate(sv, gl_tau, gl_istd, zp, p.gl_raw_bf16 != 0);
+              uint32_t sign = __float_as_uint(gl_tau - sv);
+              if (!full) {
+                const int64_t u = u0 + unit_of_acc(2 * q + e, half);
+                const bool ok = u >= lo && u < hi;
+                g = ok ? g : 0.f;
+                zp = ok ? zp : 0.f;
+                sign = ok ? sign : 0u;
+              }
+              gl_gsum += g;
+              isum += zp;
+              bits = __builtin_amdgcn_alignbit(bits, sign, 31);  // bits << 1 | active
+              g2[e] = g;
+            }
+            sx[w] = pack_bf16(g2[0], g2[1]);  // gate_bf (v401:307)
+          }
+          const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
+          uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
+          m <<= 4 * half;
+          nact += __builtin_popcount(m);
+          m |= __shfl_xor(m, 32);
+          if (p.mask32 && half == 0 && t < p.g.T) {
+            uint32_t* dst = p.mask32 + t * p.mask_words32 + (ta + it);
+            const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
+            if (shared) atomicOr(dst, m);
+            else *dst = m;
+          }
         }
         if constexpr (DG) {
           // per-unit sum of scores and max of (score - tau) over this wave's 32
@@ -1048,6 +1128,17 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
       wait_vm0();
       barrier_lds();  // end: S, next E/R and W^T visible
     }
+    if constexpr (GL) {
+      gl_gsum += __shfl_xor(gl_gsum, 32);
+      isum += __shfl_xor(isum, 32);
+      nact += __shfl_xor(nact, 32);
+      if (half == 0 && t < p.g.T) {
+        float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * TPS;
+        tp[0] = gl_gsum;
+        tp[1] = isum;  // sum of z+
+        tp[2] = static_cast<float>(nact);
+      }
+    }
     if constexpr (DG) {
       smax = fmaxf(smax, __shfl_xor(smax, 32));
       n_strong += __shfl_xor(n_strong, 32);
@@ -1102,6 +1193,11 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
         if ((v & 3) == 0) sq = *reinterpret_cast<const u32x4_t*>(s_blk + (v >> 2) * kFragBytes);
         if ((v >> 1) < PW && wtile >= 0) w_load(wtile, wstage, v >> 1);
         const uint32_t sp = sq[(v >> 1) & 1], xp = sq[2 + ((v >> 1) & 1)];
+        if constexpr (GL) {
+          // the producer's bf16 gate pair in place of the scores
+          pk[v >> 1] = pack_bf16(lo_f32(sp) * lo_f32(xp), hi_f32(sp) * hi_f32(xp));  // (v401:309)
+          continue;
+        }
         float g2[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -1153,8 +1249,9 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
           bits = gate_tile(std::integral_constant<bool, true>{}, u0, pk, wtile, it & 1);
         else
           bits = gate_tile(std::integral_constant<bool, false>{}, u0, pk, wtile, it & 1);
-        // pass bitmask of the tile (the producer emits it with diagnostics)
-        if constexpr (!DG) {
+        // pass bitmask of the tile (the producer emits it with diagnostics and
+        // the GELU gate)
+        if constexpr (!DG && !GL) {
           const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
           uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
           m <<= 4 * half;
@@ -1195,7 +1292,7 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
     isum += __shfl_xor(isum, 32);
     nact += __shfl_xor(nact, 32);
     if constexpr (DG) glogg += __shfl_xor(glogg, 32);
-    if (half == 0 && t < p.g.T) {
+    if (!GL && half == 0 && t < p.g.T) {  // the producer has the GELU gate's sums
       float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * TPS;
       tp[0] = gsum;
       if constexpr (DG) {
@@ -1223,9 +1320,9 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
   }
 }
 
-template <int DB, int KH, bool HX, bool DG>
+template <int DB, int KH, bool HX, bool DG, bool GL = false>
 __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_kernel(MainParams p) {
-  main_ws_body<DB, KH, HX, DG>(p, blockIdx.x);
+  main_ws_body<DB, KH, HX, DG, GL>(p, blockIdx.x);
 }
 template <int DB, int KH, bool HX>
 __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_batch_kernel(Batch<MainParams> b) {
@@ -1536,6 +1633,7 @@ struct TauParams {
   int ms;
   float* token_diag;
   int mode;
+  float* sstd;  // [T] s_std per row, or null
 };
 __device__ __attribute__((always_inline)) inline void tau_body(const TauParams& q, const int bid) {
   const float* __restrict__ mom = q.mom;
@@ -1575,6 +1673,7 @@ __device__ __attribute__((always_inline)) inline void tau_body(const TauParams& 
     const float sd = (mode == kTauCentered ? sqrtf(b / fN) : sqrtf(b / fN - __fmul_rn(mean, mean))) + 1e-8f;
     const float tv = mean + __fmul_rn(tau_off[t], sd);
     tau[t] = tv;
+    if (q.sstd) q.sstd[t] = sd;
     if (token_diag) {
       float* td = token_diag + t * SRW_TDIAG_COUNT;
       td[SRW_TDIAG_S_MEAN] = mean;
@@ -1613,6 +1712,7 @@ struct FinalParams {
   float* token_diag;     // [T][SRW_TDIAG_COUNT] or null
   GateParams gp;
   float exp_scale;
+  int den_gate;          // den = max(sum gate, 1) (the v4.0.1 gate, v401:340)
 };
 
 // NG: split groups per workgroup.  One workgroup per (row, block of 256 / NG
@@ -1647,7 +1747,7 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
   const float G = red[0][0] + red[0][1] + red[0][2] + red[0][3];
   const float I = red[1][0] + red[1][1] + red[1][2] + red[1][3];
   const float NA = red[2][0] + red[2][1] + red[2][2] + red[2][3];
-  const float den = fmaxf(I, 1.0f);                          // v41:584
+  const float den = fmaxf(p.den_gate ? G : I, 1.0f);          // v41:584, v401:340
   const int64_t stride = p.T * p.D;
   const int d = blockIdx.y * CW + c;
   const bool dok = d < p.D;
@@ -1762,7 +1862,7 @@ __device__ __attribute__((always_inline)) inline void finalize_rows_body(const F
   gs = wave_sum(gs);
   is = wave_sum(is);
   na = wave_sum(na);
-  const float den = fmaxf(is, 1.0f);                          // v41:584
+  const float den = fmaxf(p.den_gate ? gs : is, 1.0f);        // v41:584, v401:340
   const int64_t stride = p.T * p.D;
   const float* col = p.out_part + t * p.D + lane;
   float raw[DC];
@@ -1864,8 +1964,9 @@ constexpr int decode_lds_bytes() {
 }
 
 // NT: the most tiles a split holds (the W^T registers are sized for it; two
-// at the small pools, whose splits hold one or two tiles)
-template <int TB, int DB, int KH, int NT>
+// at the small pools, whose splits hold one or two tiles).  GL: the v4.0.1
+// GELU gate (p.sstd; the row sums carry z+ where v4.1 has the intensity).
+template <int TB, int DB, int KH, int NT, bool GL = false>
 __device__ __attribute__((always_inline)) inline void decode_body(const MainParams& p, const int bid) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int D = DB * 32, DR = KH * 16, KX = D / 16, NDB = DB / 4;
@@ -1937,11 +2038,14 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
     }
   }
   // the rows' thresholds (srw_tau_kernel, v41:461-464)
-  float tau_b[TB];
+  float tau_b[TB], sstd_b[TB];
 #pragma unroll
   for (int b = 0; b < TB; ++b) {
     const int64_t t = row0 + 32 * b + col;
     tau_b[b] = p.tau[t < Tv ? t : Tv - 1];
+    sstd_b[b] = GL ? 1.0f / p.sstd[t < Tv ? t : Tv - 1] : 1.f;  // its reciprocal
+    // the GELU gate of _srw_inference compares with bf16(tau)
+    if (GL && p.gl_raw_bf16) tau_b[b] = __uint_as_float(pack_bf16(0.0f, tau_b[b]));
   }
   wait_vm0();
   __syncthreads();
@@ -1973,7 +2077,7 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
       for (int ks = 0; ks < KX; ++ks)
         racc = mfma(rf[ks], *reinterpret_cast<const u32x4_t*>(xl + (b * KX + ks) * kFragBytes + lane * 16), racc);
       const int64_t t = row0 + 32 * b + col;
-      const float tau = tau_b[b];
+      const float tau = tau_b[b], istd = sstd_b[b];
       uint32_t bits = 0;
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
@@ -1984,15 +2088,23 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const float sv = e ? hi_f32(sp) : lo_f32(sp);
-          const float raw = sv - tau;
-          const float margin = raw - gp.thr;
-          const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(margin * p.exp_scale));
-          const float am = fmaxf(margin - gp.cut, 0.0f);
           const int64_t u = u0 + unit_of_acc(v + e, half);
           const bool ok = u >= lo && u < hi;
-          g2[e] = ok ? act * (gp.eps + fminf(am, gp.maxi)) : 0.f;
-          in2[e] = ok ? gp.eps + fminf(am, gp.maxi) : 0.f;
-          on2[e] = ok && act > 0.5f;
+          if constexpr (GL) {
+            float zp;
+            const float g = gelu_gate(sv, tau, istd, zp, p.gl_raw_bf16 != 0);
+            g2[e] = ok ? g : 0.f;
+            in2[e] = ok ? zp : 0.f;
+            on2[e] = ok && zp > 0.0f;
+          } else {
+            const float raw = sv - tau;
+            const float margin = raw - gp.thr;
+            const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(margin * p.exp_scale));
+            const float am = fmaxf(margin - gp.cut, 0.0f);
+            g2[e] = ok ? act * (gp.eps + fminf(am, gp.maxi)) : 0.f;
+            in2[e] = ok ? gp.eps + fminf(am, gp.maxi) : 0.f;
+            on2[e] = ok && act > 0.5f;
+          }
         }
         gsum[b] += g2[0];
         gsum[b] += g2[1];
@@ -2089,9 +2201,9 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
 }
 // two waves per SIMD (two workgroups per CU) where the registers allow: the
 // small pools' splits of one or two tiles
-template <int TB, int DB, int KH, int NT = kDecTiles>
+template <int TB, int DB, int KH, int NT = kDecTiles, bool GL = false>
 __global__ __launch_bounds__(256, NT <= 2 ? 2 : 1) void srw_decode_kernel(MainParams p) {
-  decode_body<TB, DB, KH, NT>(p, blockIdx.x);
+  decode_body<TB, DB, KH, NT, GL>(p, blockIdx.x);
 }
 template <int TB, int DB, int KH, int NT = kDecTiles>
 __global__ __launch_bounds__(256, NT <= 2 ? 2 : 1) void srw_decode_batch_kernel(Batch<MainParams> b) {
@@ -2118,12 +2230,15 @@ struct Kernels {
 // wave per SIMD remains, and the tile loop's waits are no longer hidden.
 constexpr int kStatsTBW = 1;
 template <int DB, int KH, bool HX, bool WS>
-Kernels kernels_of(bool dg) {
+Kernels kernels_of(bool dg, bool gl = false) {
   if constexpr (WS) {
     constexpr int lds = (2 * (KH + 2 * DB) + 2 * 2 * DB + 16) * kFragBytes;  // 2 E/R, 2 W^T, S
     if (dg)
       return Kernels{srw_stats_kernel<KH, kStatsDiag, 1>, srw_stats_kernel<KH, kStatsCentered, 1>,
                      srw_main_ws_kernel<DB, KH, HX, true>, kWsThreads, lds};
+    if (gl)
+      return Kernels{srw_stats_kernel<KH, kStatsPlain, kStatsTBW>, srw_stats_kernel<KH, kStatsCentered, kStatsTBW>,
+                     srw_main_ws_kernel<DB, KH, HX, false, true>, kWsThreads, lds};
     return Kernels{srw_stats_kernel<KH, kStatsPlain, kStatsTBW>, srw_stats_kernel<KH, kStatsCentered, kStatsTBW>,
                    srw_main_ws_kernel<DB, KH, HX, false>, kWsThreads, lds};
   } else {
@@ -2134,22 +2249,25 @@ Kernels kernels_of(bool dg) {
 
 // Instantiated shapes (d_model, d_route); for d_route == d_model there is a
 // variant whose score operand is the x registers themselves (h aliases x).
-bool pick(int64_t D, int64_t dr, bool hx, bool dg, Kernels* k) {
+// gl: the v4.0.1 GELU gate (warp-specialised kernels, no diagnostics).
+bool pick(int64_t D, int64_t dr, bool hx, bool dg, Kernels* k, bool gl = false) {
+  if (dg && gl) return false;
   if (hx && D == dr) {
-    if (D == 384) { *k = kernels_of<12, 24, true, true>(dg); return true; }
-    if (D == 128) { *k = kernels_of<4, 8, true, true>(dg); return true; }
-    if (D == 64) { *k = kernels_of<2, 4, true, true>(dg); return true; }
+    if (D == 384) { *k = kernels_of<12, 24, true, true>(dg, gl); return true; }
+    if (D == 128) { *k = kernels_of<4, 8, true, true>(dg, gl); return true; }
+    if (D == 64) { *k = kernels_of<2, 4, true, true>(dg, gl); return true; }
   }
   if (D == 384 && dr == 384) {
-    if (dg) return false;  // the pipelined single-role kernel has no diagnostics variant
+    // the pipelined single-role kernel has no diagnostics or GELU variant
+    if (dg || gl) return false;
     *k = kernels_of<12, 24, false, false>(false);
     return true;
   }
-  if (D == 384 && dr == 128) { *k = kernels_of<12, 8, false, true>(dg); return true; }
-  if (D == 128 && dr == 128) { *k = kernels_of<4, 8, false, true>(dg); return true; }
-  if (D == 128 && dr == 64) { *k = kernels_of<4, 4, false, true>(dg); return true; }
-  if (D == 64 && dr == 64) { *k = kernels_of<2, 4, false, true>(dg); return true; }
-  if (D == 64 && dr == 32) { *k = kernels_of<2, 2, false, true>(dg); return true; }
+  if (D == 384 && dr == 128) { *k = kernels_of<12, 8, false, true>(dg, gl); return true; }
+  if (D == 128 && dr == 128) { *k = kernels_of<4, 8, false, true>(dg, gl); return true; }
+  if (D == 128 && dr == 64) { *k = kernels_of<4, 4, false, true>(dg, gl); return true; }
+  if (D == 64 && dr == 64) { *k = kernels_of<2, 4, false, true>(dg, gl); return true; }
+  if (D == 64 && dr == 32) { *k = kernels_of<2, 2, false, true>(dg, gl); return true; }
   return false;
 }
 
@@ -2164,37 +2282,42 @@ bool decode_applies(const srw_desc_t& d) {
 }
 
 typedef void (*MainFn)(MainParams);
-template <int DB, int KH>
+template <int DB, int KH, bool GL>
 void decode_for_rows(int64_t Tv, int nt, MainFn* fn, int* lds) {
   if (Tv <= 32 && nt <= 2) {
-    *fn = srw_decode_kernel<1, DB, KH, 2>;
+    *fn = srw_decode_kernel<1, DB, KH, 2, GL>;
     *lds = decode_lds_bytes<1, DB, KH>();
   } else if (Tv <= 32) {
-    *fn = srw_decode_kernel<1, DB, KH>;
+    *fn = srw_decode_kernel<1, DB, KH, kDecTiles, GL>;
     *lds = decode_lds_bytes<1, DB, KH>();
   } else if (Tv <= 64) {
-    *fn = srw_decode_kernel<2, DB, KH>;
+    *fn = srw_decode_kernel<2, DB, KH, kDecTiles, GL>;
     *lds = decode_lds_bytes<2, DB, KH>();
   } else {
-    *fn = srw_decode_kernel<4, DB, KH>;
+    *fn = srw_decode_kernel<4, DB, KH, kDecTiles, GL>;
     *lds = decode_lds_bytes<4, DB, KH>();
   }
 }
-// nt: the most tiles a split of the call holds (decode_max_tiles)
-bool pick_decode(int64_t Tv, int D, int dr, int nt, MainFn* fn, int* lds) {
+template <bool GL>
+bool pick_decode_t(int64_t Tv, int D, int dr, int nt, MainFn* fn, int* lds) {
   if (D == 384 && dr == 128) {
-    decode_for_rows<12, 8>(Tv, nt, fn, lds);
+    decode_for_rows<12, 8, GL>(Tv, nt, fn, lds);
     return true;
   }
   if (D == 128 && dr == 128) {
-    decode_for_rows<4, 8>(Tv, nt, fn, lds);
+    decode_for_rows<4, 8, GL>(Tv, nt, fn, lds);
     return true;
   }
   if (D == 128 && dr == 64) {
-    decode_for_rows<4, 4>(Tv, nt, fn, lds);
+    decode_for_rows<4, 4, GL>(Tv, nt, fn, lds);
     return true;
   }
   return false;
+}
+// nt: the most tiles a split of the call holds (decode_max_tiles); gl: the
+// v4.0.1 GELU gate
+bool pick_decode(int64_t Tv, int D, int dr, int nt, MainFn* fn, int* lds, bool gl = false) {
+  return gl ? pick_decode_t<true>(Tv, D, dr, nt, fn, lds) : pick_decode_t<false>(Tv, D, dr, nt, fn, lds);
 }
 typedef void (*MainBatchFn)(Batch<MainParams>);
 template <int DB, int KH>
@@ -2284,7 +2407,7 @@ bool decode_splits_fit(const Geometry& g) { return decode_max_tiles(g) > 0; }
 // 4096) streaming took the moments + main kernels from 307 to 278 us, at
 // d_route = 128 (the model's pools, T = 16 384) from 394 to 416 us.
 bool ss_applies(const srw_desc_t& d, const Geometry& g) {
-  if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM) return false;
+  if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM || d.gate != SRW_GATE_V41) return false;
   if (d.d_model != 384 && d.d_model != 128 && d.d_model != 64) return false;
   if (d.d_route < d.d_model) return false;
   if (decode_applies(d) && decode_splits_fit(g)) return false;
@@ -2298,7 +2421,7 @@ bool pick_ss(int64_t D, MainFn* fn, int* lds) {
 }
 
 struct WsLayout {
-  size_t wp, mom, tau, gram, out_part, tok_part, scores, total;
+  size_t wp, mom, tau, gram, out_part, tok_part, scores, rn, wn, sstd, total;
 };
 
 size_t al(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
@@ -2320,6 +2443,14 @@ WsLayout ws_layout(const srw_desc_t& d, const Geometry& g) {
   off += al(static_cast<size_t>(g.S) * g.T * tok_part_stride(d) * 4);
   w.scores = off;
   if (ss_applies(d, g)) off += al(static_cast<size_t>(g.TT) * g.ntiles * kScoreTileBytes);
+  // the v4.0.1 gate: forward-normalised read and write rows, the rows' s_std
+  w.rn = w.wn = w.sstd = off;
+  if (d.gate == SRW_GATE_GELU_V401) {
+    const size_t rows = al(static_cast<size_t>(d.n_units) * d.d_model * 2);
+    w.wn = w.rn + rows;
+    w.sstd = w.wn + rows;
+    off = w.sstd + al(static_cast<size_t>(g.T) * 4);
+  }
   w.total = off;
   return w;
 }
@@ -2340,7 +2471,8 @@ hipError_t pack_unit_major(const uint16_t* src, uint16_t* dst, int64_t N, int D,
 }
 
 bool mfma_supports(const srw_desc_t& d, bool h_is_x) {
-  if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41) return false;
+  if (d.dtype != SRW_BF16) return false;
+  const bool gl = d.gate == SRW_GATE_GELU_V401;  // the GELU gate runs without diagnostics here
   if (d.stats_mode != SRW_STATS_ONEPASS && d.stats_mode != SRW_STATS_CENTERED &&
       !(d.stats_mode == SRW_STATS_GRAM && gram_supports(d.d_route)))
     return false;
@@ -2348,7 +2480,7 @@ bool mfma_supports(const srw_desc_t& d, bool h_is_x) {
   if (d.n_routes != 1 && d.n_routes != 2) return false;  // paired QK: 2 rows per token
   if (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
   Kernels k;
-  if (!pick(d.d_model, d.d_route, h_is_x, with_diag(d), &k)) return false;
+  if (!pick(d.d_model, d.d_route, h_is_x, with_diag(d), &k, gl)) return false;
   // every reference chunk must hold at least one whole 32-unit tile
   const int64_t cs = chunk_of(d);
   const int64_t last = d.n_units - ((d.n_units + cs - 1) / cs - 1) * cs;
@@ -2365,8 +2497,9 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   *path_name = "mfma_bf16";
   const bool hx = a.in.h == a.in.x;
   const bool dg = with_diag(d);
+  const bool gl = d.gate == SRW_GATE_GELU_V401;
   Kernels k;
-  if (!pick(d.d_model, d.d_route, hx, dg, &k)) return hipErrorNotSupported;
+  if (!pick(d.d_model, d.d_route, hx, dg, &k, gl)) return hipErrorNotSupported;
   const Geometry g = geometry(d, a.chunk);
   const WsLayout L = ws_layout(d, g);
   if (a.ws_bytes < L.total) return hipErrorInvalidValue;
@@ -2391,13 +2524,27 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   float* unit_diag = dg ? a.o.unit_diag : nullptr;
   if (unit_diag && (e = fill_f32(unit_diag, d.n_units * SRW_UDIAG_COUNT, 0.f, a.stream)) != hipSuccess) return e;
 
+  // the v4.0.1 gate reads forward-normalised rows (v401:300-301)
+  const uint16_t* read_rows = static_cast<const uint16_t*>(a.in.read);
+  const uint16_t* write_rows = static_cast<const uint16_t*>(a.in.write);
+  float* sstd = gl ? reinterpret_cast<float*>(a.ws + L.sstd) : nullptr;
+  if (gl) {
+    uint16_t* rn = reinterpret_cast<uint16_t*>(a.ws + L.rn);
+    uint16_t* wn = reinterpret_cast<uint16_t*>(a.ws + L.wn);
+    if (!cached) {
+      if ((e = normalize_rows_bf16(read_rows, rn, d.n_units, D, a.stream)) != hipSuccess) return e;
+      if ((e = normalize_rows_bf16(write_rows, wn, d.n_units, D, a.stream)) != hipSuccess) return e;
+    }
+    read_rows = rn;
+    write_rows = wn;
+  }
   // pack W^T (kept in the workspace across calls that declare the pool cached)
   if (!cached) {
     const int64_t rows = static_cast<int64_t>(g.ntiles) * 2 * DB * 64;
     int64_t blocks = (rows + 255) / 256;
     if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL(pack_w_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, a.stream,
-                       static_cast<const uint16_t*>(a.in.write), wp, d.n_units, D, rows);
+    hipLaunchKernelGGL(pack_w_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, a.stream, write_rows, wp,
+                       d.n_units, D, rows);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   const unsigned grid = static_cast<unsigned>(g.TT * g.S);
@@ -2436,7 +2583,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   }
   // tau per row from the moment partials
   if ((e = launch_tau(mom, a.in.tau_offset, tau, g.T, g.S_st, g.N, d.stats_mode == SRW_STATS_GRAM ? 2 : mom_stride(d),
-                      token_diag, d.stats_mode == SRW_STATS_CENTERED ? kTauCentered : kTauOnePass, a.stream)) !=
+                      token_diag, d.stats_mode == SRW_STATS_CENTERED ? kTauCentered : kTauOnePass, a.stream, sstd)) !=
       hipSuccess)
     return e;
   // main
@@ -2446,9 +2593,11 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     mp.routes = d.n_routes;
     mp.h = static_cast<const uint16_t*>(a.in.h);
     mp.emb = static_cast<const uint16_t*>(a.in.emb);
-    mp.read = static_cast<const uint16_t*>(a.in.read);
+    mp.read = read_rows;
     mp.wp = wp;
     mp.tau = tau;
+    mp.sstd = sstd;
+    mp.gl_raw_bf16 = gl && d.stats_mode == SRW_STATS_CENTERED;
     mp.out_part = out_part;
     mp.tok_part = tok_part;
     mp.unit_diag = unit_diag;
@@ -2465,7 +2614,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     const int row_blocks = static_cast<int>((g.T + 31) / 32);
     mp.rb = (row_blocks > 1 && static_cast<int64_t>(g.S) * row_blocks <= kTargetBlocks) ? row_blocks : 1;
     if (decode_applies(d) && decode_splits_fit(g) &&
-        pick_decode(mp.rb > 1 ? 32 : g.T, D, static_cast<int>(d.d_route), decode_max_tiles(g), &dec, &dec_lds)) {
+        pick_decode(mp.rb > 1 ? 32 : g.T, D, static_cast<int>(d.d_route), decode_max_tiles(g), &dec, &dec_lds, gl)) {
       *path_name = "mfma_decode_bf16";
       if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(dec), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    dec_lds)) != hipSuccess)
@@ -2513,12 +2662,13 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   f.token_diag = token_diag;
   f.gp = a.gp;
   f.exp_scale = -d.sharpness * 1.4426950408889634f;
+  f.den_gate = gl ? 1 : 0;
   return launch_finalize(f, a.stream);
 }
 
 hipError_t launch_tau(const float* mom, const float* tau_off, float* tau, int64_t T, int S_st, int64_t N, int ms,
-                      float* token_diag, int mode, hipStream_t s) {
-  const TauParams q{mom, tau_off, tau, T, S_st, N, ms, token_diag, mode};
+                      float* token_diag, int mode, hipStream_t s, float* sstd) {
+  const TauParams q{mom, tau_off, tau, T, S_st, N, ms, token_diag, mode, sstd};
   hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, s, q);
   return hipGetLastError();
 }
@@ -2545,6 +2695,7 @@ FinalParams final_params_of(const FinalizeArgs& f) {
   fp.token_diag = f.token_diag;
   fp.gp = f.gp;
   fp.exp_scale = f.exp_scale;
+  fp.den_gate = f.den_gate;
   return fp;
 }
 
@@ -2600,7 +2751,8 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
   bool decode = false;
   for (int i = 0; i < n; ++i) {
     const srw_desc_t& d = a[i].d;
-    if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM) return hipErrorNotSupported;
+    // one call at a time: diagnostics, Gram statistics, the v4.0.1 gate
+    if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM || d.gate != SRW_GATE_V41) return hipErrorNotSupported;
     if (d.d_model != d0.d_model || d.d_route != d0.d_route || d.stats_mode != d0.stats_mode)
       return hipErrorNotSupported;
     g[i] = geometry(d, a[i].chunk);

@@ -118,8 +118,11 @@ def test_workspace_sizes(C):
     # d_route == d_model: also the bf16 scores the main kernel streams (8 KB
     # per 128-token tile and 32-unit tile)
     assert C.workspace_size(_desc(C, d_route=64)) == want + al(1 * 4 * 8192)
-    d = _desc(C, gate=C.SRW_GATE_GELU_V401)      # forward-normalised R and W copies (bf16)
-    assert C.workspace_size(d) == 2 * 100 * 64 * 2
+    # the v4.0.1 gate on the matrix cores: also forward-normalised R and W
+    # copies (bf16) and the rows' s_std
+    d = _desc(C, gate=C.SRW_GATE_GELU_V401)
+    assert C.workspace_size(d) == want + 2 * al(100 * 64 * 2) + al(T * 4)
+    # ... on the generic kernels (f32): the two row copies only
     d = _desc(C, gate=C.SRW_GATE_GELU_V401, dtype=C.SRW_F32)
     assert C.workspace_size(d) == 2 * 100 * 64 * 4
 

@@ -101,3 +101,53 @@ def test_sequence_longer_than_max_seq_len_refused(small):
     cfg, _, m = small
     with pytest.raises(ValueError, match="max_seq_len"):
         m.forward(torch.zeros(1, cfg.max_seq_len + 1, dtype=torch.long))
+
+
+def test_checkpoint_file_to_gpu_model_matches_oracle(pkg, dev, tmp_path):
+    """End to end: parameters written as the reference's training script
+    writes them (a ``.flax`` msgpack file, device-replicated arrays with a
+    leading axis of 1, the model config in the checkpoint), read back with
+    ``checkpoint.load_params`` / ``config_from_checkpoint`` into a
+    ``DawnModel`` on the GPU, against the oracle on the same loaded
+    parameters and against the model built from the original ones."""
+    import dataclasses
+
+    cfg = pkg.DawnConfig(vocab_size=160, d_model=128, n_layers=2, n_heads=2, max_seq_len=48, d_route=64,
+                         n_qk=260, n_v=420, n_know=900, max_chunk_size=500)
+    params = pkg.init_params(cfg, seed=11)
+    g = torch.Generator().manual_seed(12)
+    params["router"]["tau_attn"]["kernel"] = 0.05 * torch.randn(128, 3, generator=g)
+    params["router"]["tau_know"]["kernel"] = 0.05 * torch.randn(128, 1, generator=g)
+
+    def replicate(t):
+        return {k: replicate(v) for k, v in t.items()} if isinstance(t, dict) else t.unsqueeze(0)
+
+    path = tmp_path / "best_model.flax"
+    pkg.checkpoint.save_checkpoint(str(path), replicate(params), epoch=3, step=4567,
+                                   config=dataclasses.asdict(cfg))
+    loaded = pkg.checkpoint.load_params(str(path))
+    cfg2 = pkg.checkpoint.config_from_checkpoint(pkg.checkpoint.load_checkpoint(str(path)))
+    assert cfg2 == cfg
+
+    def flat(t, pre=""):
+        if isinstance(t, dict):
+            out = {}
+            for k, v in t.items():
+                out.update(flat(v, f"{pre}/{k}"))
+            return out
+        return {pre: t}
+
+    a, b = flat(params), flat(loaded)
+    assert a.keys() == b.keys()
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
+    ids = _ids(2, 36, cfg.vocab_size, 9)
+    print("[gpu] checkpoint -> model forward B2 S36", flush=True)
+    got = pkg.DawnModel(loaded, cfg2, dev).forward(ids)
+    ref_model = pkg.DawnModel(params, cfg, dev).forward(ids)
+    torch.cuda.synchronize()
+    want = dawn_ref.forward(loaded, cfg2, ids)
+    err = rel_fro(got.cpu(), want)
+    print(f"  logits rel err vs oracle {err:.3e}", flush=True)
+    assert err <= 2e-2
+    assert torch.equal(got, ref_model)
