@@ -56,8 +56,7 @@ int choose(const srw_desc_t& d, bool h_is_x) {
     if (srw::tiled_supports(d)) return 2;
   }
   if (d.stats_mode == SRW_STATS_GRAM) return -1;  // only the MFMA family implements it
-  if (d.flags & SRW_FLAG_SPARSE_SKIP) return -1;
-  if (srw::generic_supports(d)) return 0;
+  if (srw::generic_supports(d)) return 0;  // dense under SRW_FLAG_SPARSE_SKIP
   return -1;
 }
 

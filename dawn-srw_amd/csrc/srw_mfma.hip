@@ -1960,13 +1960,22 @@ constexpr int kDecMaxRows = 128;
 
 template <int TB, int DB, int KH>
 constexpr int decode_lds_bytes() {
-  return TB * (DB * 2 + KH) * kFragBytes + 4 * TB * 32 * 3 * 4;
+  return TB * (DB * 2 + KH) * kFragBytes + 4 * TB * 32 * 3 * 4 + 4 * 4;  // + the sparse-skip tile masks
 }
 
 // NT: the most tiles a split holds (the W^T registers are sized for it; two
 // at the small pools, whose splits hold one or two tiles).  GL: the v4.0.1
 // GELU gate (p.sstd; the row sums carry z+ where v4.1 has the intensity).
-template <int TB, int DB, int KH, int NT, bool GL = false>
+// SP: sparse skip (SRW_FLAG_SPARSE_SKIP): X, H, E and tau are loaded first;
+// each wave marks the units of its tile that pass for some row (v4.1:
+// margin > 0; GELU: s > tau, i.e. gate > 0), the marks of the split's tiles
+// meet in LDS, and only then go out the R rows of marked units (a lane's
+// row) and the W^T fragments' halves holding a marked unit (8 units, two runs
+// of 4 (unit_of_k), x 32 columns: 512 contiguous bytes).  An unmarked unit's R row is zero, so its
+// x.r and P are zero: exact under the GELU gate (its gate is 0 there); under
+// v4.1 its epsilon-sized gate times x.r is left out of out only -- the gate
+// and intensity sums, den and the pass bits still come from its score.
+template <int TB, int DB, int KH, int NT, bool GL = false, bool SP = false>
 __device__ __attribute__((always_inline)) inline void decode_body(const MainParams& p, const int bid) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int D = DB * 32, DR = KH * 16, KX = D / 16, NDB = DB / 4;
@@ -1978,6 +1987,7 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
   char* const xl = lds;                          // X fragments, later P
   char* const hl = lds + FX * kFragBytes;        // H fragments
   float* const red = reinterpret_cast<float*>(hl + FH * kFragBytes);  // [wave][TB][32][3]
+  uint32_t* const umask = reinterpret_cast<uint32_t*>(red + 4 * TB * 32 * 3);  // [wave]: marked units (SP)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = lane >> 5, col = lane & 31;
@@ -2020,23 +2030,36 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
   u32x4_t ef[KH], rf[KX];
 #pragma unroll
   for (int ks = 0; ks < KH; ++ks) ef[ks] = *reinterpret_cast<const u32x4_t*>(p.emb + ur * DR + 16 * ks + 8 * half);
-#pragma unroll
-  for (int ks = 0; ks < KX; ++ks) rf[ks] = *reinterpret_cast<const u32x4_t*>(p.read + ur * D + 16 * ks + 8 * half);
-  // W^T fragments of column blocks wave * NDB + c, for the split's tiles
+  // the R row of unit col of this wave's tile, and the W^T fragments of
+  // column blocks wave * NDB + c for the split's tiles (SP: of marked units
+  // only, tmask[i] the marks of tile i)
   u32x4_t wf[NT][2][NDB];
+  auto load_rw = [&](const uint32_t* tmask) {
 #pragma unroll
-  for (int i = 0; i < NT; ++i) {
-    if (i < ntl) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int c = 0; c < NDB; ++c) {
-          const int db = wave * NDB + c;
-          wf[i][j][c] = *reinterpret_cast<const u32x4_t*>(
-              p.wp + ((static_cast<int64_t>(ta + i) * DB + db) * 2 + j) * 512 + lane * 8);
-        }
+    for (int ks = 0; ks < KX; ++ks) {
+      rf[ks] = u32x4_t{};
+      if (!SP || ((tmask[wi < NT ? wi : 0] >> col) & 1u))
+        rf[ks] = *reinterpret_cast<const u32x4_t*>(p.read + ur * D + 16 * ks + 8 * half);
     }
-  }
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      if (i < ntl) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int c = 0; c < NDB; ++c) {
+            const int db = wave * NDB + c;
+            wf[i][j][c] = u32x4_t{};
+            // lane half h of k-step j holds units 16 j + 4 h + (0..3) and
+            // 16 j + 8 + 4 h + (0..3) (unit_of_k)
+            if (!SP || (((tmask[i] >> (16 * j + 4 * half)) | (tmask[i] >> (16 * j + 8 + 4 * half))) & 0xFu))
+              wf[i][j][c] = *reinterpret_cast<const u32x4_t*>(
+                  p.wp + ((static_cast<int64_t>(ta + i) * DB + db) * 2 + j) * 512 + lane * 8);
+          }
+      }
+    }
+  };
+  if constexpr (!SP) load_rw(nullptr);
   // the rows' thresholds (srw_tau_kernel, v41:461-464)
   float tau_b[TB], sstd_b[TB];
 #pragma unroll
@@ -2049,6 +2072,47 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
   }
   wait_vm0();
   __syncthreads();
+  if constexpr (SP) {
+    // mark the tile's units that pass for some row of this wave's blocks
+    uint32_t um = 0;
+    if (have) {
+      const int64_t ut = static_cast<int64_t>(mt) * kUnitTile;
+#pragma unroll
+      for (int b = 0; b < TB; ++b) {
+        if (b % wpt != wb) continue;
+        f32x16_t sacc = {};
+#pragma unroll
+        for (int ks = 0; ks < KH; ++ks)
+          sacc = mfma(ef[ks], *reinterpret_cast<const u32x4_t*>(hl + (b * KH + ks) * kFragBytes + lane * 16), sacc);
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) {
+          const uint32_t sp = pack_bf16(sacc[v], sacc[v + 1]);   // the bf16 scores the gate sees
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float sv = e ? hi_f32(sp) : lo_f32(sp);
+            const bool pass = GL ? sv - tau_b[b] > 0.0f : (sv - tau_b[b]) - p.gp.thr > 0.0f;
+            const int uo = unit_of_acc(v + e, half);
+            const int64_t u = ut + uo;
+            if (pass && u >= lo && u < hi) um |= 1u << uo;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) um |= __shfl_xor(um, o);
+    if (lane == 0) umask[wave] = um;
+    __syncthreads();
+    uint32_t tmask[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      tmask[i] = 0u;
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        if (w / wpt == i) tmask[i] |= umask[w];
+    }
+    load_rw(tmask);
+    wait_vm0();
+  }
 
   // score and read GEMMs of this wave's tile for every row block, gate epilogue
   const GateParams gp = p.gp;
@@ -2201,9 +2265,9 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
 }
 // two waves per SIMD (two workgroups per CU) where the registers allow: the
 // small pools' splits of one or two tiles
-template <int TB, int DB, int KH, int NT = kDecTiles, bool GL = false>
+template <int TB, int DB, int KH, int NT = kDecTiles, bool GL = false, bool SP = false>
 __global__ __launch_bounds__(256, NT <= 2 ? 2 : 1) void srw_decode_kernel(MainParams p) {
-  decode_body<TB, DB, KH, NT, GL>(p, blockIdx.x);
+  decode_body<TB, DB, KH, NT, GL, SP>(p, blockIdx.x);
 }
 template <int TB, int DB, int KH, int NT = kDecTiles>
 __global__ __launch_bounds__(256, NT <= 2 ? 2 : 1) void srw_decode_batch_kernel(Batch<MainParams> b) {
@@ -2282,42 +2346,43 @@ bool decode_applies(const srw_desc_t& d) {
 }
 
 typedef void (*MainFn)(MainParams);
-template <int DB, int KH, bool GL>
+template <int DB, int KH, bool GL, bool SP>
 void decode_for_rows(int64_t Tv, int nt, MainFn* fn, int* lds) {
   if (Tv <= 32 && nt <= 2) {
-    *fn = srw_decode_kernel<1, DB, KH, 2, GL>;
+    *fn = srw_decode_kernel<1, DB, KH, 2, GL, SP>;
     *lds = decode_lds_bytes<1, DB, KH>();
   } else if (Tv <= 32) {
-    *fn = srw_decode_kernel<1, DB, KH, kDecTiles, GL>;
+    *fn = srw_decode_kernel<1, DB, KH, kDecTiles, GL, SP>;
     *lds = decode_lds_bytes<1, DB, KH>();
   } else if (Tv <= 64) {
-    *fn = srw_decode_kernel<2, DB, KH, kDecTiles, GL>;
+    *fn = srw_decode_kernel<2, DB, KH, kDecTiles, GL, SP>;
     *lds = decode_lds_bytes<2, DB, KH>();
   } else {
-    *fn = srw_decode_kernel<4, DB, KH, kDecTiles, GL>;
+    *fn = srw_decode_kernel<4, DB, KH, kDecTiles, GL, SP>;
     *lds = decode_lds_bytes<4, DB, KH>();
   }
 }
-template <bool GL>
+template <bool GL, bool SP>
 bool pick_decode_t(int64_t Tv, int D, int dr, int nt, MainFn* fn, int* lds) {
   if (D == 384 && dr == 128) {
-    decode_for_rows<12, 8, GL>(Tv, nt, fn, lds);
+    decode_for_rows<12, 8, GL, SP>(Tv, nt, fn, lds);
     return true;
   }
   if (D == 128 && dr == 128) {
-    decode_for_rows<4, 8, GL>(Tv, nt, fn, lds);
+    decode_for_rows<4, 8, GL, SP>(Tv, nt, fn, lds);
     return true;
   }
   if (D == 128 && dr == 64) {
-    decode_for_rows<4, 4, GL>(Tv, nt, fn, lds);
+    decode_for_rows<4, 4, GL, SP>(Tv, nt, fn, lds);
     return true;
   }
   return false;
 }
 // nt: the most tiles a split of the call holds (decode_max_tiles); gl: the
-// v4.0.1 GELU gate
-bool pick_decode(int64_t Tv, int D, int dr, int nt, MainFn* fn, int* lds, bool gl = false) {
-  return gl ? pick_decode_t<true>(Tv, D, dr, nt, fn, lds) : pick_decode_t<false>(Tv, D, dr, nt, fn, lds);
+// v4.0.1 GELU gate; sp: sparse skip
+bool pick_decode(int64_t Tv, int D, int dr, int nt, MainFn* fn, int* lds, bool gl = false, bool sp = false) {
+  if (sp) return gl ? pick_decode_t<true, true>(Tv, D, dr, nt, fn, lds) : pick_decode_t<false, true>(Tv, D, dr, nt, fn, lds);
+  return gl ? pick_decode_t<true, false>(Tv, D, dr, nt, fn, lds) : pick_decode_t<false, false>(Tv, D, dr, nt, fn, lds);
 }
 typedef void (*MainBatchFn)(Batch<MainParams>);
 template <int DB, int KH>
@@ -2478,7 +2543,8 @@ bool mfma_supports(const srw_desc_t& d, bool h_is_x) {
     return false;
   if (d.stats_mode == SRW_STATS_CENTERED && with_diag(d)) return false;  // diagnostics: one-pass moments only
   if (d.n_routes != 1 && d.n_routes != 2) return false;  // paired QK: 2 rows per token
-  if (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
+  // SRW_FLAG_SPARSE_SKIP: the decode kernel skips; the prefill kernels run dense
+  if (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST)) return false;
   Kernels k;
   if (!pick(d.d_model, d.d_route, h_is_x, with_diag(d), &k, gl)) return false;
   // every reference chunk must hold at least one whole 32-unit tile
@@ -2614,8 +2680,9 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     const int row_blocks = static_cast<int>((g.T + 31) / 32);
     mp.rb = (row_blocks > 1 && static_cast<int64_t>(g.S) * row_blocks <= kTargetBlocks) ? row_blocks : 1;
     if (decode_applies(d) && decode_splits_fit(g) &&
-        pick_decode(mp.rb > 1 ? 32 : g.T, D, static_cast<int>(d.d_route), decode_max_tiles(g), &dec, &dec_lds, gl)) {
-      *path_name = "mfma_decode_bf16";
+        pick_decode(mp.rb > 1 ? 32 : g.T, D, static_cast<int>(d.d_route), decode_max_tiles(g), &dec, &dec_lds, gl,
+                    (d.flags & SRW_FLAG_SPARSE_SKIP) != 0)) {
+      *path_name = (d.flags & SRW_FLAG_SPARSE_SKIP) ? "mfma_decode_sparse_bf16" : "mfma_decode_bf16";
       if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(dec), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    dec_lds)) != hipSuccess)
         return e;
@@ -2751,8 +2818,10 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
   bool decode = false;
   for (int i = 0; i < n; ++i) {
     const srw_desc_t& d = a[i].d;
-    // one call at a time: diagnostics, Gram statistics, the v4.0.1 gate
-    if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM || d.gate != SRW_GATE_V41) return hipErrorNotSupported;
+    // one call at a time: diagnostics, Gram statistics, the v4.0.1 gate, sparse skip
+    if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM || d.gate != SRW_GATE_V41 ||
+        (d.flags & SRW_FLAG_SPARSE_SKIP))
+      return hipErrorNotSupported;
     if (d.d_model != d0.d_model || d.d_route != d0.d_route || d.stats_mode != d0.stats_mode)
       return hipErrorNotSupported;
     g[i] = geometry(d, a[i].chunk);
