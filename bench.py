@@ -453,6 +453,50 @@ def bench_model(args, pkg, C, dev) -> dict:
     }
 
 
+def sparse_accounting(plan, T, D, dr, N, R, path):
+    """What SRW_FLAG_SPARSE_SKIP can leave out, from the call's pass mask.
+
+    Decode kernel (path mfma_decode_sparse_bf16): a unit's R row (D bf16) is
+    read when some row of the call passes it, a W^T fragment half (8 units,
+    D / 32 pieces of 512 bytes) when one of its units passes; E is read
+    whole.  Prefill shapes have no sparse kernel: reported is the share of
+    32-token x 32-unit blocks no row passes (what a block skip could drop).
+    """
+    import torch
+    words = plan.pass_mask.reshape(T * R, -1)                                  # [rows, ceil(N/64)] 64-bit words
+    info = {"pass_frac": round(float(plan.n_active.double().sum()) / (T * R * N), 5)}
+    if path == "mfma_decode_sparse_bf16":
+        anyw = words[0].clone()
+        for r in range(1, T * R):                                              # OR over the call's rows
+            anyw |= words[r]
+        act = ((anyw.unsqueeze(-1) >> torch.arange(64, device=anyw.device)) & 1).reshape(-1)[:N].bool()
+        ntiles = (N + 31) // 32
+        pad = torch.zeros(ntiles * 32, dtype=torch.bool, device=act.device)
+        pad[:N] = act
+        t = pad.reshape(ntiles, 2, 2, 2, 4)                                    # [tile][j][run][half][4]
+        halves = t.any(dim=-1).any(dim=2)                                      # [tile][j][half]
+        need = N * dr * 2 + int(act.sum()) * D * 2 + int(halves.sum()) * (D // 32) * 512
+        info.update({"active_units_frac": round(float(act.float().mean()), 5),
+                     "w_halves_read_frac": round(float(halves.float().mean()), 5),
+                     "needed_bytes": need, "pool_bytes": N * (dr + 2 * D) * 2})
+    else:
+        rows = T * R
+        tb = (rows + 31) // 32
+        pad = torch.zeros(tb * 32, words.shape[1], dtype=words.dtype, device=words.device)
+        pad[:rows] = words
+        blk = pad.reshape(tb, 32, -1)
+        ored = blk[:, 0].clone()
+        for i in range(1, 32):                                                 # OR over each 32-row block
+            ored |= blk[:, i]
+        lo_half = (ored & 0xFFFFFFFF) != 0                                     # units 64 w .. 64 w + 31
+        hi_half = (ored >> 32) != 0                                            # units 64 w + 32 .. 64 w + 63
+        n_ub = (N + 31) // 32
+        busy = torch.stack([lo_half, hi_half], dim=-1).reshape(tb, -1)[:, :n_ub]
+        info.update({"note": "no sparse kernel for this shape (more than 128 rows): run dense",
+                     "skippable_block_frac": round(1.0 - float(busy.float().mean()), 6)})
+    return info
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -480,6 +524,15 @@ def main() -> int:
     ap.add_argument("--pool-cached", action="store_true",
                     help="steps after the first reuse the pool data kept in the workspace "
                          "(SRW_FLAG_POOL_CACHED: decode steps / layers sharing one pool)")
+    ap.add_argument("--sparse", action="store_true",
+                    help="SRW_FLAG_SPARSE_SKIP: the decode kernel loads only the R rows and W^T fragment "
+                         "halves of units some row passes; the roofline then counts the bytes it needs "
+                         "(prefill shapes run dense: the line reports how many 32x32 (token, unit) blocks "
+                         "a skip could drop)")
+    ap.add_argument("--tokens", type=int, default=0,
+                    help="override the workload's token count (e.g. 1 or 8 rows for a decode shape)")
+    ap.add_argument("--gate", default="v41", choices=["v41", "gelu_v401"],
+                    help="v4.1 gate (default) or the v4.0.1 GELU gate")
     ap.add_argument("--graph", action="store_true",
                     help="capture one call in a HIP graph and time graph replays (launch-bound "
                          "shapes such as decode)")
@@ -527,6 +580,10 @@ def main() -> int:
         return 0
     key, max_chunk, note = WORKLOADS[args.workload]
     shape = pkg.inputs.CONFIGS[key]
+    if args.tokens > 0:
+        import dataclasses
+        shape = dataclasses.replace(shape, T=args.tokens)
+        note += f" (T overridden to {args.tokens})"
     _, cs = pkg.chunk_plan(shape.N, max_chunk)
     log(f"workload {args.workload}: T={shape.T} D={shape.D} dr={shape.dr} N={shape.N} "
         f"R={shape.routes} chunk={cs}")
@@ -553,7 +610,8 @@ def main() -> int:
     plan = pkg.SrwPlan(x, h, inp["emb"].to(bf).to(dev), inp["tau_offset"].to(dev),
                        inp["read"].to(bf).to(dev), inp["write"].to(bf).to(dev),
                        stats=args.stats, chunk_size=cs, want_mask=True, diag=args.diag,
-                       force_generic=args.force_generic, tiled=args.tiled)
+                       force_generic=args.force_generic, tiled=args.tiled, sparse_skip=args.sparse,
+                       gate=args.gate)
     stream = torch.cuda.current_stream(dev)
 
     plan.launch(stream)
@@ -657,15 +715,24 @@ def main() -> int:
                 "traffic": traffic, "kernel": path,
                 "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops,
                 "step_tflops": round(flops / (step_ms * 1e-3) / 1e12, 2)}
+    sparse_info = None
+    if args.sparse and not args.backward:
+        sparse_info = sparse_accounting(plan, T, D, dr, N, R, path)
     if args.workload.startswith("decode_") and not args.backward:
         # decode shapes are pool-read bound: the algorithmic bytes are the pool
-        # (E, R, W rows) streamed once per call
+        # (E, R, W rows) streamed once per call -- with the sparse kernel the
+        # E rows and the R rows / W^T halves of units some row passes
         pool_bytes = N * (dr + 2 * D) * 2
-        gbs = pool_bytes / (kern_ms * 1e-3) / 1e9
+        need = sparse_info["needed_bytes"] if (sparse_info and "needed_bytes" in sparse_info) else pool_bytes
+        gbs = need / (kern_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": path,
-                    "kernel_ms": round(kern_ms, 5), "algorithmic_bytes": pool_bytes,
-                    "step_gbs": round(pool_bytes / (step_ms * 1e-3) / 1e9, 1)}
+                    "kernel_ms": round(kern_ms, 5), "algorithmic_bytes": need,
+                    "step_gbs": round(need / (step_ms * 1e-3) / 1e9, 1)}
+        if sparse_info is not None:
+            roofline["dense_equivalent_gbs"] = round(pool_bytes / (kern_ms * 1e-3) / 1e9, 1)
+    if sparse_info is not None:
+        roofline["sparse"] = sparse_info
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -683,7 +750,7 @@ def main() -> int:
                    "d_route": dr, "n_units": N, "routes": R, "chunk": cs,
                    "stats": args.stats, "diag": args.diag, "pool_cached": args.pool_cached,
                    "tiled": args.tiled, "pass": "backward" if args.backward else "forward",
-                   "graph": args.graph,
+                   "graph": args.graph, "sparse_skip": args.sparse, "gate": args.gate,
                    "tau_offset": round(tau_value, 4),
                    "parallelism": "single GPU"},
         "roofline": roofline,

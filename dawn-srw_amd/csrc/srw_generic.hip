@@ -338,10 +338,30 @@ hipError_t generic_forward_t(const LaunchArgs& a) {
 
 }  // namespace
 
+// The same per row for bf16 with one wave per row (four rows a workgroup):
+// the pools' rows are short (D <= 4096), and a workgroup per row leaves most
+// of its threads idle.
+__global__ __launch_bounds__(256) void normalize_rows_wave_kernel(const bf16_t* __restrict__ src,
+                                                                  bf16_t* __restrict__ dst, int64_t N, int64_t D) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (r >= N) return;
+  const int lane = threadIdx.x & 63;
+  const bf16_t* row = src + r * D;
+  bf16_t* orow = dst + r * D;
+  float ss = 0.f;
+  for (int64_t i = lane; i < D; i += 64) {
+    const float v = Elt<bf16_t>::load(row + i);
+    ss += v * v;
+  }
+  const float nrm = sqrtf(wave_sum(ss));
+  const float denom = Elt<bf16_t>::round(Elt<bf16_t>::round(nrm) + 1e-8f);
+  for (int64_t i = lane; i < D; i += 64) Elt<bf16_t>::store(orow + i, Elt<bf16_t>::load(row + i) / denom);
+}
+
 hipError_t normalize_rows_bf16(const uint16_t* src, uint16_t* dst, int64_t N, int64_t D, hipStream_t s) {
   if (N <= 0) return hipSuccess;
-  hipLaunchKernelGGL((normalize_rows_kernel<bf16_t>), dim3(static_cast<unsigned>(N)), dim3(kGT), 0, s,
-                     reinterpret_cast<const bf16_t*>(src), reinterpret_cast<bf16_t*>(dst), D);
+  hipLaunchKernelGGL(normalize_rows_wave_kernel, dim3(static_cast<unsigned>((N + 3) / 4)), dim3(256), 0, s,
+                     reinterpret_cast<const bf16_t*>(src), reinterpret_cast<bf16_t*>(dst), N, D);
   return hipGetLastError();
 }
 

@@ -116,14 +116,17 @@ def test_sparse_skip_v41_within_bound_of_dense(pkg, dev, case):
     assert err <= REL_BF16
 
 
-def test_sparse_flag_runs_dense_where_no_sparse_kernel(pkg, dev):
-    """Prefill shapes have no sparse kernel: the flag leaves them dense (the
-    same bits as without it)."""
-    T, D, dr, N = 300, 128, 128, 900
-    print("[gpu] sparse flag on a prefill shape", flush=True)
+@pytest.mark.parametrize("shape", [(300, 128, 128, 900, "mfma_ss_bf16"), (300, 1024, 1024, 700, "tiled_bf16")],
+                         ids=["fused", "tiled"])
+def test_sparse_flag_runs_dense_where_no_sparse_kernel(pkg, dev, shape):
+    """Prefill shapes have no sparse kernel: the flag leaves them on their
+    dense matrix-core path (the same bits as without it), never on the
+    scalar kernels."""
+    T, D, dr, N, path = shape
+    print(f"[gpu] sparse flag on a prefill shape {shape}", flush=True)
     inp = _inputs(pkg, T, D, dr, N, 9, 0.5)
     dense = _run(pkg, dev, inp, False)
     sparse = _run(pkg, dev, inp, True)
-    assert sparse["path"] == dense["path"] and "decode" not in dense["path"]
+    assert sparse["path"] == dense["path"] == path
     for k in ("out", "gate_sum", "den", "n_active", "pass_mask"):
         assert torch.equal(sparse[k], dense[k]), k
