@@ -331,7 +331,7 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
   // a whole tile to complete before the end-of-tile vmcnt wait.  A tile that
   // two splits share (a chunk boundary inside it) is stored by the split
   // holding its first unit.
-  constexpr bool STORE = TBW == 1 && MODE == kStatsPlain;
+  constexpr bool STORE = TBW == 1 && (MODE == kStatsPlain || MODE == kStatsDiag);
   uint32_t spd[8];
   char* sdst = nullptr;
   // Non-temporal stores (and loads in the main kernel): 206 MB per Know-pool
@@ -481,7 +481,8 @@ struct MainParams {
   const float* tau;      // [T] thresholds (srw_tau_kernel)
   float* out_part;       // [S][T][D]
   float* tok_part;       // [S][T][TPS]: sum gate, sum intensity, active count, - [, diagnostics]
-  float* unit_diag;      // [N][SRW_UDIAG_COUNT] (diagnostics) or null
+  float2* unit_part;     // [ceil(T / 32)][N] per 32-row block and unit: (sum of scores, max of s - tau),
+                         // reduced into unit_diag by srw_unit_diag_kernel (diagnostics) or null
   uint32_t* mask32;      // [T][mask_words32] or null
   int64_t mask_words32;
   Geometry g;
@@ -500,6 +501,132 @@ __device__ inline float gate_of_margin(float m, const GateParams& gp, float exp_
   return act * inten;
 }
 __device__ inline float gate_of_margin(float m, const MainParams& p) { return gate_of_margin(m, p.gp, p.exp_scale); }
+
+// After reduce_scatter16 over a tile, lanes with bit 4 clear hold one unit
+// each (unit unit_of_acc(bitreverse4(lane & 15), half) of the tile): its sum
+// of scores and max of s - tau over the wave's 32 rows, stored as one float2
+// per (32-row block, unit) -- plain stores, each element written by exactly
+// one wave (atomics into unit_diag, 2 x 128 per unit at T = 4096 from every
+// CU, doubled the Know-pool main kernel's time).  tw: the wave's first row.
+__device__ __attribute__((always_inline)) inline void store_unit_part(const MainParams& p, float su, float mx,
+                                                                      int64_t u0, int lane, int half, int64_t lo,
+                                                                      int64_t hi, int64_t tw) {
+  const int k = 8 * (lane & 1) + 4 * ((lane >> 1) & 1) + 2 * ((lane >> 2) & 1) + ((lane >> 3) & 1);
+  const int64_t u = u0 + unit_of_acc(k, half);
+  if (p.unit_part && !(lane & 16) && u >= lo && u < hi && tw < p.g.T)
+    p.unit_part[(tw >> 5) * p.g.N + u] = make_float2(su, mx);
+}
+
+// Training diagnostics of one (token, 32-unit tile) -- the producer-side
+// half of the main kernels' DIAG work: per token the max score, act-band
+// counts as thresholds on the exp argument (act > 0.9 <=> arg < -log2 9;
+// 0.1 < act < 0.9 <=> |arg| < log2 9; 0.05 / 0.95: log2 19; 0.2 / 0.8: 2),
+// capped intensities (s >= tau + thr + cut + max_intensity - 1e-3), the
+// intensity sum and the pass bits (v41:503-534); per unit of the tile the
+// sum of scores and the max of s - tau over the wave's 32 rows (v41:445-447,
+// 543-552), by a butterfly over the lanes of each half, into unit_part.
+// sw: the lane's bf16 scores, element v (unit unit_of_acc(v, half) of its
+// token) in word v / 2, the low half for even v.  The tile's pass-mask words
+// and unit partials go to an LDS block (DiagLds) from which another wave
+// stores them: the storing wave need not wait for the stores to complete.
+struct DiagLds {
+  uint32_t mask[32];  // per token of the wave block: the tile's pass-mask word
+  float2 unit[32];    // per unit of the tile: (sum of scores, max of s - tau) over the block's rows
+};
+struct TileDiag {
+  float smax = -INFINITY, isum = 0.f;
+  uint32_t n_strong = 0, n_bound = 0, n_075 = 0, n_030 = 0, n_cap = 0, nact = 0;
+  // FAST: every unit of the tile in [lo, hi) and every row of the wave
+  // block valid (the selects drop out)
+  template <bool FAST>
+  __device__ __attribute__((always_inline)) void tile(const MainParams& p, const uint32_t (&sw)[8], int utile,
+                                                      int half, int lane, int64_t lo, int64_t hi, int64_t t,
+                                                      float tau_t, DiagLds* dl) {
+    const int64_t u0 = static_cast<int64_t>(utile) * kUnitTile;
+    const float tau_thr = tau_t + p.gp.thr;
+    const float k_exp = -tau_thr * p.exp_scale;
+    const float tau_cut = tau_thr + p.gp.cut;
+    const float cap_s = tau_cut + (p.gp.maxi - 1e-3f);
+    const bool full = FAST || (u0 >= lo && u0 + kUnitTile <= hi);
+    uint32_t bits = 0;
+    float su[16], mx[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const float sv = (v & 1) ? hi_f32(sw[v >> 1]) : lo_f32(sw[v >> 1]);
+      const int64_t u = u0 + unit_of_acc(v, half);
+      const bool uok = full || (u >= lo && u < hi);
+      const bool ok = FAST || (t < p.g.T && uok);
+      su[v] = ok ? sv : 0.f;
+      mx[v] = ok ? sv - tau_t : -INFINITY;
+      const float arg = fmaf(sv, p.exp_scale, k_exp);
+      const float aa = fabsf(arg);
+      smax = fmaxf(smax, uok ? sv : -INFINITY);
+      n_strong += (uok && arg < -3.169925001442312f) ? 1u : 0u;
+      n_bound += (uok && aa < 3.169925001442312f) ? 1u : 0u;
+      n_075 += (uok && aa < 4.247927513443585f) ? 1u : 0u;
+      n_030 += (uok && aa < 2.0f) ? 1u : 0u;
+      n_cap += (uok && sv >= cap_s) ? 1u : 0u;
+      // intensity sum and pass bits (v41:503-511, 528) as in the gate epilogue
+      const float inten = p.gp.eps + __builtin_amdgcn_fmed3f(sv - tau_cut, 0.0f, p.gp.maxi);
+      isum += uok ? inten : 0.f;
+      bits = __builtin_amdgcn_alignbit(bits, uok ? __float_as_uint(arg) : 0u, 31);
+    }
+    {
+      const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
+      uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
+      m <<= 4 * half;
+      nact += __builtin_popcount(m);
+      m |= __shfl_xor(m, 32);
+      if (half == 0) dl->mask[lane] = m;
+    }
+    reduce_scatter16(su, lane, [](float x, float y) { return x + y; });
+    reduce_scatter16(mx, lane, [](float x, float y) { return fmaxf(x, y); });
+    if (!(lane & 16)) {
+      const int k = 8 * (lane & 1) + 4 * ((lane >> 1) & 1) + 2 * ((lane >> 2) & 1) + ((lane >> 3) & 1);
+      dl->unit[unit_of_acc(k, half)] = make_float2(su[0], mx[0]);
+    }
+  }
+  // a block's mask words and unit partials of tile utile from LDS to global
+  // memory (lane l: token tw + l's mask word; lanes 0-31: unit u0 + l)
+  __device__ __attribute__((always_inline)) static void emit(const MainParams& p, const DiagLds* dl, int utile,
+                                                             int lane, int64_t lo, int64_t hi, int64_t tw) {
+    const int64_t u0 = static_cast<int64_t>(utile) * kUnitTile;
+    const int64_t t = tw + (lane & 31);
+    if (lane < 32) {
+      if (p.mask32 && t < p.g.T) {
+        const uint32_t m = dl->mask[lane];
+        uint32_t* dst = p.mask32 + t * p.mask_words32 + utile;
+        const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
+        if (shared) atomicOr(dst, m);
+        else *dst = m;
+      }
+    } else {
+      const int64_t u = u0 + (lane - 32);
+      if (p.unit_part && u >= lo && u < hi && tw < p.g.T) p.unit_part[(tw >> 5) * p.g.N + u] = dl->unit[lane - 32];
+    }
+  }
+  // the token's counts over the two lane halves into its partial slots
+  __device__ __attribute__((always_inline)) void finish(float* tp, int half, bool row_ok) {
+    smax = fmaxf(smax, __shfl_xor(smax, 32));
+    n_strong += __shfl_xor(n_strong, 32);
+    n_bound += __shfl_xor(n_bound, 32);
+    n_075 += __shfl_xor(n_075, 32);
+    n_030 += __shfl_xor(n_030, 32);
+    n_cap += __shfl_xor(n_cap, 32);
+    isum += __shfl_xor(isum, 32);
+    nact += __shfl_xor(nact, 32);
+    if (half == 0 && row_ok) {
+      tp[1] = isum;
+      tp[2] = static_cast<float>(nact);
+      tp[TP_SMAX] = smax;
+      tp[TP_STRONG] = static_cast<float>(n_strong);
+      tp[TP_BOUND] = static_cast<float>(n_bound);
+      tp[TP_075] = static_cast<float>(n_075);
+      tp[TP_030] = static_cast<float>(n_030);
+      tp[TP_CAP] = static_cast<float>(n_cap);
+    }
+  }
+};
 
 // v4.0.1 GELU gate of a score s (v401:303-306): z = (s - tau) / s_std,
 // Phi(z) = 0.5 (1 + erf(z / sqrt 2)), gate = z Phi(z) for z > 0, else 0.
@@ -865,7 +992,7 @@ __global__ __launch_bounds__(kThreads, 1) void srw_main_kernel(MainParams p) {
 constexpr int kWsThreads = 512;
 
 // DG: training diagnostics -- per-token extras in tok_part (TPS = 12), per-unit
-// score sums and gate maxima into unit_diag (atomics).  GL: the v4.0.1 GELU
+// score sums and max margins per 32-row block into unit_part.  GL: the v4.0.1 GELU
 // gate (p.sstd; the row sums carry z+ where v4.1 has the intensity), without
 // diagnostics.
 template <int DB, int KH, bool HX, bool DG, bool GL = false>
@@ -972,8 +1099,25 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
     // the compiler wait for every load in flight (the next tile's LDS
     // prefetch included) at the top of each iteration.
     wait_vm0();
+    // diagnostics: a tile's pass-mask word and unit partial are stored at the
+    // top of the next iteration, so that the tile's GEMMs cover their latency
+    // before the end-of-tile vmcnt wait
+    uint32_t pend_m = 0;
+    float pend_su = 0.f, pend_mx = 0.f;
 
     for (int it = 0; it <= n; ++it) {
+      if constexpr (DG) {
+        if (it >= 1) {
+          const int64_t pu0 = static_cast<int64_t>(ta + it - 1) * kUnitTile;
+          if (p.mask32 && half == 0 && t < p.g.T) {
+            uint32_t* dst = p.mask32 + t * p.mask_words32 + (ta + it - 1);
+            const bool shared = (pu0 < lo) || (pu0 + kUnitTile > hi && hi < p.g.N);
+            if (shared) atomicOr(dst, pend_m);
+            else *dst = pend_m;
+          }
+          store_unit_part(p, pend_su, pend_mx, pu0, lane, half, lo, hi, tw);
+        }
+      }
       const bool pre = it + 1 < n;  // the next tile's E/R go out during this one's MFMAs
       // S piece q (16 B per lane) = bf16 scores and x.r of elements 4q..4q+3:
       // {s[4q], s[4q+1]}, {s[4q+2], s[4q+3]}, {xr[4q], xr[4q+1]}, {xr[4q+2], xr[4q+3]}
@@ -1060,62 +1204,52 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
         }
         if constexpr (DG) {
           // per-unit sum of scores and max of (score - tau) over this wave's 32
-          // tokens (v41:445-447, 543-552): butterfly over the lanes of each half
+          // rows (v41:445-447, 543-552): butterfly over the lanes of each half
           const int64_t u0 = static_cast<int64_t>(ta + it) * kUnitTile;
           const float tau_thr = tau_t + p.gp.thr;
           const float k_exp = -tau_thr * p.exp_scale;
           const float tau_cut = tau_thr + p.gp.cut;
           const float cap_s = tau_cut + (p.gp.maxi - 1e-3f);
           const bool full = u0 >= lo && u0 + kUnitTile <= hi;
+          const bool row_ok = t < p.g.T;
           uint32_t bits = 0;
           float su[16], mx[16];
+          // A unit outside [lo, hi), or a row past T, enters as score -inf:
+          // no band, pass bit, cap or max score counts it (exp argument
+          // +inf); only its score sum and intensity need a select.
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const uint32_t pr = sx[4 * (v >> 2) + ((v & 3) >> 1)];
-            const float sv = (v & 1) ? hi_f32(pr) : lo_f32(pr);
+            const float s_raw = (v & 1) ? hi_f32(pr) : lo_f32(pr);
             const int64_t u = u0 + unit_of_acc(v, half);
-            const bool uok = full || (u >= lo && u < hi);
-            const bool ok = t < p.g.T && uok;
-            su[v] = ok ? sv : 0.f;
-            mx[v] = ok ? sv - tau_t : -INFINITY;
+            const bool ok = row_ok && (full || (u >= lo && u < hi));
+            const float sv = ok ? s_raw : -INFINITY;
+            su[v] = ok ? s_raw : 0.f;
+            mx[v] = sv - tau_t;
             const float arg = fmaf(sv, p.exp_scale, k_exp);
             const float aa = fabsf(arg);
-            smax = fmaxf(smax, uok ? sv : -INFINITY);
-            n_strong += (uok && arg < -3.169925001442312f) ? 1u : 0u;
-            n_bound += (uok && aa < 3.169925001442312f) ? 1u : 0u;
-            n_075 += (uok && aa < 4.247927513443585f) ? 1u : 0u;
-            n_030 += (uok && aa < 2.0f) ? 1u : 0u;
-            n_cap += (uok && sv >= cap_s) ? 1u : 0u;
+            smax = fmaxf(smax, sv);
+            n_strong += arg < -3.169925001442312f ? 1u : 0u;
+            n_bound += aa < 3.169925001442312f ? 1u : 0u;
+            n_075 += aa < 4.247927513443585f ? 1u : 0u;
+            n_030 += aa < 2.0f ? 1u : 0u;
+            n_cap += sv >= cap_s ? 1u : 0u;
             // intensity sum and pass bits (v41:503-511, 528) as in the gate epilogue
             const float inten = p.gp.eps + __builtin_amdgcn_fmed3f(sv - tau_cut, 0.0f, p.gp.maxi);
-            isum += uok ? inten : 0.f;
-            bits = __builtin_amdgcn_alignbit(bits, uok ? __float_as_uint(arg) : 0u, 31);
+            isum += ok ? inten : 0.f;
+            bits = __builtin_amdgcn_alignbit(bits, __float_as_uint(arg), 31);
           }
           {
             const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
             uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
             m <<= 4 * half;
             nact += __builtin_popcount(m);
-            m |= __shfl_xor(m, 32);
-            if (p.mask32 && half == 0 && t < p.g.T) {
-              uint32_t* dst = p.mask32 + t * p.mask_words32 + (ta + it);
-              const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
-              if (shared) atomicOr(dst, m);
-              else *dst = m;
-            }
+            pend_m = m | __shfl_xor(m, 32);
           }
           reduce_scatter16(su, lane, [](float x, float y) { return x + y; });
           reduce_scatter16(mx, lane, [](float x, float y) { return fmaxf(x, y); });
-          const int k = 8 * (lane & 1) + 4 * ((lane >> 1) & 1) + 2 * ((lane >> 2) & 1) + ((lane >> 3) & 1);
-          const int64_t u = u0 + unit_of_acc(k, half);
-          if (p.unit_diag && !(lane & 16) && u >= lo && u < hi) {
-            atomicAdd(p.unit_diag + u * SRW_UDIAG_COUNT + SRW_UDIAG_SCORE_SUM, su[0]);
-            if (mx[0] > -INFINITY) {
-              const float g = gate_of_margin(mx[0] - p.gp.thr, p);
-              atomicMax(reinterpret_cast<unsigned int*>(p.unit_diag + u * SRW_UDIAG_COUNT + SRW_UDIAG_GATE_MAX),
-                        __float_as_uint(g));
-            }
-          }
+          pend_su = su[0];
+          pend_mx = mx[0];
         }
       }
       barrier_lds();  // mid: consumers have read S (tile it - 1)
@@ -1346,15 +1480,19 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ws_batch_kernel(Batch<
 // it was filled, past the barrier that ends the reads of it.  LDS = 2 R +
 // 2 W^T + 2 x.r + 2 score stages (128 KB at d_model = 384).
 // ---------------------------------------------------------------------------
-template <int DB>
+template <int DB, bool DG = false>
 constexpr int ss_lds_bytes() {
-  return (2 * (DB * 2) + 2 * (2 * DB) + 2 * 8 + 2 * 8) * kFragBytes;
+  return (2 * (DB * 2) + 2 * (2 * DB) + 2 * 8 + 2 * 8) * kFragBytes + (DG ? 2 * 4 * static_cast<int>(sizeof(DiagLds)) : 0);
 }
 
-template <int DB>
+// DG: training diagnostics, split as in srw_main_ws_kernel -- the producers
+// take the per-token counts, pass bits and per-unit statistics of the tile
+// the consumers gate (from the same score stage, one tile behind their own
+// read GEMM), the consumers the gate sum and sum gate log gate.
+template <int DB, bool DG = false>
 __device__ __attribute__((always_inline)) inline void main_ss_body(const MainParams& p, const int bid) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
-  constexpr int TPS = 4;
+  constexpr int TPS = DG ? kTokPartDiag : 4;
   constexpr int D = DB * 32;
   constexpr int KX = D / 16;
   constexpr int F_R = KX, F_W = 2 * DB;
@@ -1384,6 +1522,9 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
   char* const w_base = lds + 2 * R_STAGE;
   char* const xr_lane = w_base + 2 * W_STAGE + blk * XR_BLK + lane * 16;  // + stage * XR_STAGE
   char* const s_wave = w_base + 2 * W_STAGE + 2 * XR_STAGE + blk * S_BLK;  // + stage * S_STAGE
+  // diagnostics: the producers' mask words and unit partials of a tile, which
+  // the consumers store one tile later ([stage][block])
+  DiagLds* const d_blk = reinterpret_cast<DiagLds*>(w_base + 2 * W_STAGE + 2 * XR_STAGE + 2 * S_STAGE) + blk;
 
   // R and W^T tiles, direct global->LDS, each wave a contiguous run of blocks
   constexpr int PR = (F_R + 3) / 4, PW = (F_W + 3) / 4;
@@ -1428,8 +1569,25 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
 #pragma unroll
     for (int m = 0; m < TileR::NM; ++m) lr[m] = TileR::lane_off(lane, m);
     wait_vm0();  // x drained here, not at the first tile's vmcnt wait
+    TileDiag dgs;                            // diagnostics
+    const float tau_t = DG ? p.tau[tl] : 0.f;
 
     for (int it = 0; it <= n; ++it) {
+      if constexpr (DG) {
+        // diagnostics of the tile the consumers gate now (its scores came in
+        // with the previous tile's loads)
+        if (it >= 1) {
+          const char* sb = s_wave + ((it - 1) & 1) * S_STAGE + lane * 16;
+          const u32x4_t s0 = *reinterpret_cast<const u32x4_t*>(sb);
+          const u32x4_t s1 = *reinterpret_cast<const u32x4_t*>(sb + kFragBytes);
+          const uint32_t sw[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+          const int64_t u0 = static_cast<int64_t>(ta + it - 1) * kUnitTile;
+          if (u0 >= lo && u0 + kUnitTile <= hi && tw + 32 <= p.g.T)
+            dgs.tile<true>(p, sw, ta + it - 1, half, lane, lo, hi, t, tau_t, d_blk + ((it - 1) & 1) * 4);
+          else
+            dgs.tile<false>(p, sw, ta + it - 1, half, lane, lo, hi, t, tau_t, d_blk + ((it - 1) & 1) * 4);
+        }
+      }
       if (it < n) {
         const bool pre = it + 1 < n;  // the next tile's R goes out during this one's MFMAs
         const char* base = r_base + (it & 1) * R_STAGE;
@@ -1467,6 +1625,7 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
       wait_vm0();
       barrier_lds();  // x.r of this tile, the next tile's R and W^T visible
     }
+    if constexpr (DG) dgs.finish(p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * TPS, half, t < p.g.T);
   } else {
     // ---------------- consumer: gate epilogue and write GEMM, one tile behind ----------------
     // tau folded with the gate's constant offsets (srw_main_ws_kernel):
@@ -1480,6 +1639,7 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
     const float c_exp = p.exp_scale, eps = p.gp.eps, maxi = p.gp.maxi;
     float gsum = 0.f, isum = 0.f;
     uint32_t nact = 0;
+    float glogg = 0.f;  // diagnostics: sum gate * log2(gate + 1e-8) (v41:533-534)
     f32x16_t oacc[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[db] = f32x16_t{};
@@ -1517,8 +1677,12 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
             sign = ok ? sign : 0u;
           }
           gsum += g;
-          isum += inten;
-          bits = __builtin_amdgcn_alignbit(bits, sign, 31);   // bits << 1 | active
+          if constexpr (DG) {
+            glogg = fmaf(g, __builtin_amdgcn_logf(g + 1e-8f), glogg);  // sum gate log2 (gate + 1e-8)
+          } else {
+            isum += inten;
+            bits = __builtin_amdgcn_alignbit(bits, sign, 31);   // bits << 1 | active
+          }
           g2[e] = g;
         }
         const uint32_t gq = pack_bf16(g2[0], g2[1]);             // gate_bf (v41:516)
@@ -1530,6 +1694,10 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
     // the producers load every tile (R, W^T, scores): a consumer's global
     // accesses are its mask words and partials, stores it need not wait for
     for (int it = 0; it <= n; ++it) {
+      // diagnostics: the producers' mask words and unit partials of tile
+      // ta + it - 2 (written in the previous iteration)
+      if constexpr (DG)
+        if (it >= 2) TileDiag::emit(p, d_blk + (it & 1) * 4, ta + it - 2, lane, lo, hi, tw);
       if (it > 0) {
         const int tile = ta + it - 1;
         const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
@@ -1541,7 +1709,8 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
           bits = gate_tile(std::integral_constant<bool, true>{}, u0, pk, srp, xrp);
         else
           bits = gate_tile(std::integral_constant<bool, false>{}, u0, pk, srp, xrp);
-        {
+        // pass bitmask of the tile (the producers emit it with diagnostics)
+        if constexpr (!DG) {
           const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
           uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
           m <<= 4 * half;
@@ -1576,14 +1745,21 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
       }
       barrier_lds();
     }
+    if constexpr (DG)
+      if (n >= 1) TileDiag::emit(p, d_blk + ((n + 1) & 1) * 4, ta + n - 1, lane, lo, hi, tw);
     gsum += __shfl_xor(gsum, 32);
     isum += __shfl_xor(isum, 32);
     nact += __shfl_xor(nact, 32);
+    if constexpr (DG) glogg += __shfl_xor(glogg, 32);
     if (half == 0 && t < p.g.T) {
       float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * TPS;
       tp[0] = gsum;
-      tp[1] = isum;
-      tp[2] = static_cast<float>(nact);
+      if constexpr (DG) {
+        tp[TP_GLOGG] = glogg * 0.69314718055994531f;  // log2 -> ln
+      } else {
+        tp[1] = isum;
+        tp[2] = static_cast<float>(nact);
+      }
     }
     float* op = p.out_part + static_cast<int64_t>(split) * p.g.T * D;
     if (tw + 32 <= p.g.T) {
@@ -1603,9 +1779,9 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
   }
 }
 
-template <int DB>
+template <int DB, bool DG = false>
 __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_kernel(MainParams p) {
-  main_ss_body<DB>(p, blockIdx.x);
+  main_ss_body<DB, DG>(p, blockIdx.x);
 }
 template <int DB>
 __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_batch_kernel(Batch<MainParams> b) {
@@ -1940,6 +2116,53 @@ template <int DC>
 __global__ __launch_bounds__(256) void srw_finalize_rows_batch_kernel(Batch<FinalParams> b) {
   const int i = batch_index(b.start, b.n, blockIdx.x);
   finalize_rows_body<DC>(b.p[i], blockIdx.x - b.start[i]);
+}
+
+// ---------------------------------------------------------------------------
+// unit diagnostics: unit_diag[u] = (sum of the unit's scores over all rows,
+// its max gate) from the main kernel's per-32-row-block partials
+// (v41:445-447, 543-552).  The gate is non-decreasing in the margin, so the
+// max gate is the gate of the max margin (max of s - tau, minus thr).  A
+// workgroup holds 64 units x 4 row slices; each slice sums its blocks in
+// order, the slices combine in LDS in slice order: the result is the same on
+// every call (the atomics it replaces summed in arrival order).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void srw_unit_diag_kernel(const float2* __restrict__ part, int64_t rows, int64_t N,
+                                                            float* __restrict__ unit_diag, GateParams gp,
+                                                            float exp_scale) {
+  __shared__ float2 red[4][64];
+  const int ul = threadIdx.x & 63, slice = threadIdx.x >> 6;
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * 64 + ul;
+  float su = 0.f, mx = -INFINITY;
+  if (u < N) {
+    int64_t r = slice;
+    for (; r + 12 < rows; r += 16) {  // four blocks in flight per thread
+      const float2 a = part[r * N + u], b = part[(r + 4) * N + u];
+      const float2 c = part[(r + 8) * N + u], e = part[(r + 12) * N + u];
+      su += a.x;
+      su += b.x;
+      su += c.x;
+      su += e.x;
+      mx = fmaxf(fmaxf(mx, fmaxf(a.y, b.y)), fmaxf(c.y, e.y));
+    }
+    for (; r < rows; r += 4) {
+      const float2 a = part[r * N + u];
+      su += a.x;
+      mx = fmaxf(mx, a.y);
+    }
+  }
+  red[slice][ul] = make_float2(su, mx);
+  __syncthreads();
+  if (slice == 0 && u < N) {
+    float s = red[0][ul].x, m = red[0][ul].y;
+#pragma unroll
+    for (int q = 1; q < 4; ++q) {
+      s += red[q][ul].x;
+      m = fmaxf(m, red[q][ul].y);
+    }
+    unit_diag[u * SRW_UDIAG_COUNT + SRW_UDIAG_SCORE_SUM] = s;
+    unit_diag[u * SRW_UDIAG_COUNT + SRW_UDIAG_GATE_MAX] = m > -INFINITY ? gate_of_margin(m - gp.thr, gp, exp_scale) : 0.f;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2472,21 +2695,34 @@ bool decode_splits_fit(const Geometry& g) { return decode_max_tiles(g) > 0; }
 // 4096) streaming took the moments + main kernels from 307 to 278 us, at
 // d_route = 128 (the model's pools, T = 16 384) from 394 to 416 us.
 bool ss_applies(const srw_desc_t& d, const Geometry& g) {
-  if (with_diag(d) || d.stats_mode == SRW_STATS_GRAM || d.gate != SRW_GATE_V41) return false;
+  if (d.stats_mode == SRW_STATS_GRAM || d.gate != SRW_GATE_V41) return false;
   if (d.d_model != 384 && d.d_model != 128 && d.d_model != 64) return false;
   if (d.d_route < d.d_model) return false;
   if (decode_applies(d) && decode_splits_fit(g)) return false;
   return g.TT_st == g.TT;  // the moments kernel's 128-row token tiles are the main kernel's
 }
-bool pick_ss(int64_t D, MainFn* fn, int* lds) {
-  if (D == 384) { *fn = srw_main_ss_kernel<12>; *lds = ss_lds_bytes<12>(); return true; }
-  if (D == 128) { *fn = srw_main_ss_kernel<4>; *lds = ss_lds_bytes<4>(); return true; }
-  if (D == 64) { *fn = srw_main_ss_kernel<2>; *lds = ss_lds_bytes<2>(); return true; }
+// dg: with training diagnostics
+bool pick_ss(int64_t D, MainFn* fn, int* lds, bool dg = false) {
+  if (D == 384) {
+    *fn = dg ? srw_main_ss_kernel<12, true> : srw_main_ss_kernel<12>;
+    *lds = dg ? ss_lds_bytes<12, true>() : ss_lds_bytes<12>();
+    return true;
+  }
+  if (D == 128) {
+    *fn = dg ? srw_main_ss_kernel<4, true> : srw_main_ss_kernel<4>;
+    *lds = dg ? ss_lds_bytes<4, true>() : ss_lds_bytes<4>();
+    return true;
+  }
+  if (D == 64) {
+    *fn = dg ? srw_main_ss_kernel<2, true> : srw_main_ss_kernel<2>;
+    *lds = dg ? ss_lds_bytes<2, true>() : ss_lds_bytes<2>();
+    return true;
+  }
   return false;
 }
 
 struct WsLayout {
-  size_t wp, mom, tau, gram, out_part, tok_part, scores, rn, wn, sstd, total;
+  size_t wp, mom, tau, gram, out_part, tok_part, scores, rn, wn, sstd, upart, total;
 };
 
 size_t al(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
@@ -2516,6 +2752,9 @@ WsLayout ws_layout(const srw_desc_t& d, const Geometry& g) {
     w.sstd = w.wn + rows;
     off = w.sstd + al(static_cast<size_t>(g.T) * 4);
   }
+  // diagnostics: the unit statistics per 32-row block (MainParams::unit_part)
+  w.upart = off;
+  if (with_diag(d)) off += al(static_cast<size_t>((g.T + 31) / 32) * d.n_units * sizeof(float2));
   w.total = off;
   return w;
 }
@@ -2576,7 +2815,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   uint16_t* scores = reinterpret_cast<uint16_t*>(a.ws + L.scores);
   MainFn ss_fn = nullptr;
   int ss_lds = 0;
-  const bool ss = ss_applies(d, g) && pick_ss(d.d_model, &ss_fn, &ss_lds);
+  const bool ss = ss_applies(d, g) && pick_ss(d.d_model, &ss_fn, &ss_lds, dg);
   const int D = static_cast<int>(d.d_model);
   const int KH = static_cast<int>(d.d_route / 16);
   const int DB = D / 32;
@@ -2588,7 +2827,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   const bool cached = (d.flags & SRW_FLAG_POOL_CACHED) != 0;
   float* token_diag = dg ? a.o.token_diag : nullptr;
   float* unit_diag = dg ? a.o.unit_diag : nullptr;
-  if (unit_diag && (e = fill_f32(unit_diag, d.n_units * SRW_UDIAG_COUNT, 0.f, a.stream)) != hipSuccess) return e;
+  float2* unit_part = unit_diag ? reinterpret_cast<float2*>(a.ws + L.upart) : nullptr;
 
   // the v4.0.1 gate reads forward-normalised rows (v401:300-301)
   const uint16_t* read_rows = static_cast<const uint16_t*>(a.in.read);
@@ -2666,7 +2905,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     mp.gl_raw_bf16 = gl && d.stats_mode == SRW_STATS_CENTERED;
     mp.out_part = out_part;
     mp.tok_part = tok_part;
-    mp.unit_diag = unit_diag;
+    mp.unit_part = unit_part;
     mp.mask32 = mask32;
     mp.mask_words32 = mw32;
     mp.g = g;
@@ -2730,7 +2969,14 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   f.gp = a.gp;
   f.exp_scale = -d.sharpness * 1.4426950408889634f;
   f.den_gate = gl ? 1 : 0;
-  return launch_finalize(f, a.stream);
+  if ((e = launch_finalize(f, a.stream)) != hipSuccess) return e;
+  if (unit_part) {
+    const int64_t rows = (g.T + 31) / 32;
+    hipLaunchKernelGGL(srw_unit_diag_kernel, dim3(static_cast<unsigned>((d.n_units + 63) / 64)), dim3(256), 0,
+                       a.stream, unit_part, rows, static_cast<int64_t>(d.n_units), unit_diag, a.gp, f.exp_scale);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_tau(const float* mom, const float* tau_off, float* tau, int64_t T, int S_st, int64_t N, int ms,

@@ -37,8 +37,8 @@ def _inputs(pkg, T, D, dr, N, h_is_x, seed, tau=-0.5):
 
 
 # the fused family: the main kernel that recomputes the scores, the one that
-# streams the moments kernel's scores (d_route >= d_model, no diagnostics),
-# and the decode kernel for calls of at most 128 rows
+# streams the moments kernel's scores (d_route >= d_model), and the decode
+# kernel for calls of at most 128 rows
 FUSED = ("mfma_bf16", "mfma_ss_bf16", "mfma_decode_bf16")
 FAMILIES = {"fused": (FUSED, {}), "tiled": (("tiled_bf16",), {"tiled": True})}
 
@@ -135,21 +135,23 @@ def test_mfma_matches_fused_oracle(pkg, dev, case, family):
     (200, 128, 128, 777, False, 300, 23),     # three chunks
     (33, 64, 64, 100, True, 2048, 24),        # d_model 64, one partial tile
 ], ids=lambda c: "T{}D{}dr{}N{}{}c{}".format(c[0], c[1], c[2], c[3], "x" if c[4] else "", c[5]))
-def test_mfma_streamed_scores_equal_recomputed(pkg, dev, case):
-    """Without diagnostics (and d_route >= d_model) the fused forward's main
-    kernel reads back the bf16 scores the moments kernel stored
-    (srw_main_ss_kernel); with diagnostics it recomputes them
-    (srw_main_ws_kernel).  Same bf16 scores, same tau (the diagnostics only
-    add power sums), the same gate epilogue and write GEMM in the same order:
-    the outputs are equal bit for bit."""
+def test_mfma_streamed_scores_diag_split_equals_plain(pkg, dev, case):
+    """With d_route >= d_model the fused forward's main kernel reads back the
+    bf16 scores the moments kernel stored (srw_main_ss_kernel).  With
+    diagnostics its producer waves take the intensity sum, pass bits and
+    active count of the tile the consumers gate (from the same LDS score
+    stage) while the consumers keep the gate sum: the same scores, tau and
+    element order, so the layer outputs are equal bit for bit to the call
+    without diagnostics.  (The diagnostics themselves are checked against the
+    scalar kernels in test_mfma_diagnostics_match_generic.)"""
     T, D, dr, N, hx, max_chunk, seed = case
-    print(f"[gpu] streamed vs recomputed scores {case}", flush=True)
+    print(f"[gpu] streamed scores, diagnostics on and off {case}", flush=True)
     inp = _inputs(pkg, T, D, dr, N, hx, seed)
     inp["tau_offset"].uniform_(-0.9, 0.6, generator=torch.Generator().manual_seed(seed))
     _, cs = srw_ref.chunk_plan(N, max_chunk)
     a = _gpu(pkg, dev, inp, cs)
     b = _gpu(pkg, dev, inp, cs, diag=True)
-    assert a["path"] == "mfma_ss_bf16" and b["path"] == "mfma_bf16"
+    assert a["path"] == b["path"] == "mfma_ss_bf16"
     for k in ("out", "den", "gate_sum", "n_active", "pass_mask"):
         assert torch.equal(a[k], b[k]), k
 
@@ -379,6 +381,7 @@ DIAG_CASES = [
     (256, 384, 384, 6000, True, 1, 2500, 41),   # Know form, two reference chunks
     (200, 384, 128, 1580, False, 2, 12500, 42),  # paired QK pool with the router's d_route
     (130, 128, 64, 1000, False, 1, 300, 43),    # four chunks, ragged T
+    (300, 128, 128, 1580, False, 1, 700, 44),   # streamed scores with the router's h, chunk edge in a tile
 ]
 
 
