@@ -33,6 +33,9 @@ sys.path.insert(0, ROOT)
 METRIC = "SRW layer tokens/sec on 1 MI355X (40M Know pool); % bf16 MFMA / HBM peak"
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+# --cold: bytes written between timed calls, four times the 256 MB Infinity
+# Cache (MALL), so that each call's pool reads come from HBM
+COLD_FLUSH_BYTES = 1 << 30
 
 # HBM bytes per launch of the dominant kernel: rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (KiB per dispatch) scaled by what the same counters read for a
@@ -533,6 +536,9 @@ def main() -> int:
                     help="override the workload's token count (e.g. 1 or 8 rows for a decode shape)")
     ap.add_argument("--gate", default="v41", choices=["v41", "gelu_v401"],
                     help="v4.1 gate (default) or the v4.0.1 GELU gate")
+    ap.add_argument("--cold", action="store_true",
+                    help="write 1 GiB between timed calls (evicting the Infinity Cache and the L2s) "
+                         "and time each call on its own: pool reads from HBM")
     ap.add_argument("--graph", action="store_true",
                     help="capture one call in a HIP graph and time graph replays (launch-bound "
                          "shapes such as decode)")
@@ -560,6 +566,9 @@ def main() -> int:
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.cold and (args.graph or args.workload in ("decode", "qkv", "model")):
+        print("bench.py: --cold times single eager calls of one pool", file=sys.stderr)
+        return 2
     if args.workload == "decode":
         if args.backward or args.diag or args.tiled:
             print("bench.py: --workload decode times the forward decode step", file=sys.stderr)
@@ -663,19 +672,40 @@ def main() -> int:
     for _ in range(warmup):
         run_once()
     torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    t_begin.record(stream)
-    for i in range(K):
-        if graph is not None:
-            graph.replay()
-            continue
-        C.set_kernel_events(ev_k[i][0].cuda_event, ev_k[i][1].cuda_event)
-        step()
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    C.set_kernel_events(None, None)
-    step_ms = t_begin.elapsed_time(t_end) / K
+    if args.cold:
+        # each call timed on its own, after 1 GiB of writes: no pool line left
+        # in the Infinity Cache or an L2
+        flush = torch.empty(COLD_FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+        ev_call = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(K)]
+        torch.cuda.synchronize()
+        wall0 = time.perf_counter()
+        for i in range(K):
+            flush.fill_(float(i))
+            flush.sum()   # read back: the cache then holds clean flush lines, no dirty ones to evict
+            ev_call[i][0].record(stream)
+            C.set_kernel_events(ev_k[i][0].cuda_event, ev_k[i][1].cuda_event)
+            step()
+            ev_call[i][1].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        C.set_kernel_events(None, None)
+        step_ms = statistics.mean(a.elapsed_time(b) for a, b in ev_call)
+        del flush
+    else:
+        wall0 = time.perf_counter()
+        t_begin.record(stream)
+        for i in range(K):
+            if graph is not None:
+                graph.replay()
+                continue
+            C.set_kernel_events(ev_k[i][0].cuda_event, ev_k[i][1].cuda_event)
+            step()
+        t_end.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        C.set_kernel_events(None, None)
+        step_ms = t_begin.elapsed_time(t_end) / K
     if graph is not None:
         # the dominant kernel's own events are not recorded inside a replay:
         # time it eagerly once more
@@ -751,6 +781,7 @@ def main() -> int:
                    "stats": args.stats, "diag": args.diag, "pool_cached": args.pool_cached,
                    "tiled": args.tiled, "pass": "backward" if args.backward else "forward",
                    "graph": args.graph, "sparse_skip": args.sparse, "gate": args.gate,
+                   "cold": args.cold,
                    "tau_offset": round(tau_value, 4),
                    "parallelism": "single GPU"},
         "roofline": roofline,
