@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "SRW layer tokens/sec on 1 MI355X (40M Know pool); % bf16 MFMA / HBM peak"
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+PEAK_F32_TFLOPS = 157.3        # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 # --cold: bytes written between timed calls, four times the 256 MB Infinity
 # Cache (MALL), so that each call's pool reads come from HBM
@@ -123,11 +124,13 @@ def host_cpus() -> dict:
             "thread_cap": CPU_THREADS_MAX}
 
 
-def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: bool = False) -> dict:
+def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: bool = False,
+                 f32_inference: bool = False) -> dict:
     """The oracle's fused_gate_srw (bf16 emulation) -- or, with ``backward``,
-    its hand-written VJP -- on a token sample of the same pool, timed on the
-    host cores (test infrastructure as the timed CPU restatement; never part
-    of the GPU path)."""
+    its hand-written VJP; with ``f32_inference`` its fp32 srw_inference --
+    on a token sample of the same pool, timed on the host cores (test
+    infrastructure as the timed CPU restatement; never part of the GPU
+    path)."""
     import torch
     from oracle import srw_ref, srw_vjp
 
@@ -144,6 +147,10 @@ def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: b
         fn = lambda: srw_vjp.fused_gate_srw_vjp(  # noqa: E731
             bf(x), bf(h), bf(inp["emb"]), tau, bf(inp["read"]), bf(inp["write"]), d_out, 1e-2, 1e-2,
             max_chunk_size=chunk)
+    elif f32_inference and shape.routes == 1:
+        what = "srw_inference fp32"
+        h = x if shape.h_is_x else inp["h"][:T_s, 0]
+        fn = lambda: srw_ref.srw_inference(x, h, inp["emb"], tau, inp["read"], inp["write"])  # noqa: E731
     elif shape.routes == 1:
         h = x if shape.h_is_x else inp["h"][:T_s, 0]
         fn = lambda: srw_ref.fused_gate_srw(  # noqa: E731
@@ -166,7 +173,7 @@ def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: b
         f"threads={threads}")
     return {"value": T_s / med, "unit": "tokens/s", "cores": threads, "kind": "port",
             **host_cpus(),
-            "sample": (f"oracle {what} bf16 emulation, first {T_s} of the "
+            "sample": (f"oracle {what}{'' if f32_inference else ' bf16 emulation'}, first {T_s} of the "
                        f"{shape.T} tokens, full pool N={shape.N}, median of {len(times)} "
                        f"runs; {cpu_model()}")}
 
@@ -536,6 +543,9 @@ def main() -> int:
                     help="override the workload's token count (e.g. 1 or 8 rows for a decode shape)")
     ap.add_argument("--gate", default="v41", choices=["v41", "gelu_v401"],
                     help="v4.1 gate (default) or the v4.0.1 GELU gate")
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "f32"],
+                    help="operand dtype of the single-pool workloads (f32: the fp32 matrix-core "
+                         "family; configs[0] as written is f32 with --stats centered)")
     ap.add_argument("--cold", action="store_true",
                     help="write 1 GiB between timed calls (evicting the Infinity Cache and the L2s) "
                          "and time each call on its own: pool reads from HBM")
@@ -566,6 +576,9 @@ def main() -> int:
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.dtype == "f32" and (args.workload in ("decode", "qkv", "model") or args.backward or args.tiled):
+        print("bench.py: --dtype f32 times the single-pool forward", file=sys.stderr)
+        return 2
     if args.cold and (args.graph or args.workload in ("decode", "qkv", "model")):
         print("bench.py: --cold times single eager calls of one pool", file=sys.stderr)
         return 2
@@ -613,7 +626,7 @@ def main() -> int:
     if shape.pass_target is not None:
         tau_value = pkg.inputs.calibrate_tau_offset(inp, shape.pass_target)
         inp["tau_offset"].fill_(tau_value)
-    bf = torch.bfloat16
+    bf = torch.float32 if args.dtype == "f32" else torch.bfloat16
     x = inp["x"].to(bf).to(dev)
     h = x if shape.h_is_x else inp["h"].to(bf).to(dev)
     plan = pkg.SrwPlan(x, h, inp["emb"].to(bf).to(dev), inp["tau_offset"].to(dev),
@@ -730,7 +743,7 @@ def main() -> int:
         # the main kernel streams the moments kernel's bf16 scores: its own
         # work is the read (once per token) and write GEMMs
         kflops = 2.0 * T * N * (D + R * D)
-    elif plan.path == "tiled_bf16":
+    elif plan.path in ("tiled_bf16", "tiled_f32"):
         # the dominant kernel of the tiled family is tiled_gate_kernel: the
         # read GEMM over the T * R virtual rows, gating the scores that
         # tiled_stats_kernel stored (the score and write GEMMs are kernels of
@@ -740,8 +753,9 @@ def main() -> int:
         kflops = flops
     achieved = kflops / (kern_ms * 1e-3) / 1e12
     traffic = MEASURED_TRAFFIC.get((args.workload, args.stats, path))
-    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+    peak = PEAK_F32_TFLOPS if args.dtype == "f32" else PEAK_BF16_TFLOPS
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
+                "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                 "traffic": traffic, "kernel": path,
                 "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops,
                 "step_tflops": round(flops / (step_ms * 1e-3) / 1e12, 2)}
@@ -767,14 +781,15 @@ def main() -> int:
     cpu = None
     if args.cpu_seconds > 0:
         torch.set_num_threads(min(os.cpu_count() or 1, CPU_THREADS_MAX))
-        cpu = cpu_baseline(pkg, shape, inp, tau_value, max_chunk, args.cpu_seconds, args.backward)
+        cpu = cpu_baseline(pkg, shape, inp, tau_value, max_chunk, args.cpu_seconds, args.backward,
+                           f32_inference=args.dtype == "f32" and args.stats == "centered")
 
     value = T / (step_ms * 1e-3)
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": K, "warmup": warmup, "ms_per_step": round(step_ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic (seeded N(0,1) x RMS-normalised; E ~ N(0,1/dr); "
+        "dtype": args.dtype, "data": "synthetic (seeded N(0,1) x RMS-normalised; E ~ N(0,1/dr); "
                                   "R, W L2-normalised rows)",
         "config": {"workload": args.workload, "note": note, "T": T, "d_model": D,
                    "d_route": dr, "n_units": N, "routes": R, "chunk": cs,

@@ -46,7 +46,7 @@ srw_status_t validate(const srw_desc_t* d) {
 }
 
 // Which family serves this descriptor: 1 = fused MFMA, 2 = tiled GEMMs,
-// 0 = generic, -1 = none.  h_is_x: h aliases x (known to srw_forward from
+// 3 = fp32 tiled GEMMs, 0 = generic, -1 = none.  h_is_x: h aliases x (known to srw_forward from
 // the pointers).
 int choose(const srw_desc_t& d, bool h_is_x) {
   const bool force_generic = (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST)) != 0;
@@ -54,6 +54,7 @@ int choose(const srw_desc_t& d, bool h_is_x) {
     if ((d.flags & SRW_FLAG_TILED) && srw::tiled_supports(d)) return 2;
     if (srw::mfma_supports(d, h_is_x)) return 1;
     if (srw::tiled_supports(d)) return 2;
+    if (srw::tiled_f32_supports(d)) return 3;
   }
   if (d.stats_mode == SRW_STATS_GRAM) return -1;  // only the MFMA family implements it
   if (srw::generic_supports(d)) return 0;  // dense under SRW_FLAG_SPARSE_SKIP
@@ -94,6 +95,7 @@ srw_status_t scratch_address(hipStream_t stream, void** out) {
 size_t bytes_of(int which, const srw_desc_t& d) {
   if (which == 1) return srw::mfma_workspace_bytes(d);
   if (which == 2) return srw::tiled_workspace_bytes(d);
+  if (which == 3) return srw::tiled_f32_workspace_bytes(d);
   return srw::generic_workspace_bytes(d);
 }
 
@@ -220,6 +222,9 @@ srw_status_t launch_forward(const srw::LaunchArgs& a, int which) {
   } else if (which == 2) {
     e = srw::tiled_forward(a);
     g_last_path = "tiled_bf16";
+  } else if (which == 3) {
+    e = srw::tiled_f32_forward(a);
+    g_last_path = "tiled_f32";
   } else {
     e = srw::generic_forward(a);
     g_last_path = "generic";

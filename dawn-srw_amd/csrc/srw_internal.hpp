@@ -115,6 +115,13 @@ bool tiled_supports(const srw_desc_t& d);
 size_t tiled_workspace_bytes(const srw_desc_t& d);
 hipError_t tiled_forward(const LaunchArgs& a);
 
+// fp32 tiled GEMMs on the fp32 matrix cores, see srw_tiled_f32.hip: the v4.1
+// gate with one-pass or centred statistics (the fp32 _srw_inference);
+// d_model and d_route multiples of 32.
+bool tiled_f32_supports(const srw_desc_t& d);
+size_t tiled_f32_workspace_bytes(const srw_desc_t& d);
+hipError_t tiled_f32_forward(const LaunchArgs& a);
+
 // MFMA kernels (bf16 / f32 matrix cores), see srw_mfma.hip.
 size_t mfma_workspace_bytes(const srw_desc_t& d);
 // h_is_x: h aliases x (d_route == d_model, one route), which some shapes need

@@ -1,0 +1,660 @@
+// srw_tiled_f32.hip -- fp32 SRW forward on the fp32 matrix cores
+// (v_mfma_f32_32x32x2_f32): the dtype-preserving fp32 `_srw_inference`
+// (v41:1713-1738: centred two-pass statistics, one chunk) and fp32
+// fused_gate_srw calls (one-pass statistics; in fp32 the chunk plan changes
+// no rounding: every chunk's partial write GEMM stays fp32, v41:518).
+//
+// The layer runs as the bf16 tiled family does (srw_tiled.hip), with every
+// operand and intermediate in fp32:
+//
+//   pack   W [N, D] -> W^T [D, N64] (unit-contiguous rows, zero tail)
+//   stats  S = E.H^T per 256-unit x 256-token tile, stored as S [T, N64]
+//          fp32 (v41:1717-1718); per-token partials sum s, sum s^2
+//   centre (centred statistics) sum (s - mean)^2 from the stored S
+//          (v41:1719-1721)
+//   gate   per tile XR = R.X^T, the v4.1 gate of the stored scores in the
+//          reference's fp32 expression order (v41:1723-1728), P = gate * xr
+//          over S in place (v41:1735); per-token
+//          sum gate, sum intensity, active count, and the pass bits
+//   write  OUT = P . W over N-splits of the units, fp32 partials
+//   final  out = sum of the partials / max(sum intensity, 1) * scale in fp32
+//          (v41:1736-1737)
+//
+// The GEMM main loop: a 256 x 256 output tile per workgroup (4 waves as 2 x
+// 2, 128 x 128 = 16 accumulators of 32 x 32 each), operands K-contiguous in
+// memory, 32-wide k blocks (one 128-byte line per row) in a double-buffered
+// LDS ring filled by direct global->LDS loads, 16-byte pieces XOR-swizzled by
+// row.  In the 32 x 32 x 2 MFMA the lanes of half h supply k index h of the
+// step; here step s of a k block takes k = s from half 0 and k = 16 + s from
+// half 1 (any assignment of k to (step, half) shared by both operands gives
+// the same sum), so a lane's 16 steps read 64 contiguous bytes of its row:
+// four 16-byte LDS reads per operand row block.
+
+#include "srw_internal.hpp"
+#include "srw_mfma_util.hpp"
+
+namespace srw {
+
+namespace {
+
+constexpr int kFThreads = 256;              // 4 waves
+constexpr int kFRows = 256;                 // rows per operand tile = output tile side
+constexpr int kFK = 32;                     // fp32 k per stage: one 128-byte line per row
+constexpr int kFOpBytes = kFRows * kFK * 4;  // 32 KB
+constexpr int kFStageBytes = 2 * kFOpBytes;  // A and B tiles
+constexpr int kFGemmLds = 2 * kFStageBytes;  // two stages: 128 KB
+constexpr int kFGroupBytes = 32 * kFK * 4;   // 32 rows: one MFMA operand's rows
+constexpr int kFNAlign = 64;                 // padding of the stored [., N] rows
+
+__device__ inline f32x16_t mfma_f32(float a, float b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// An operand tile in LDS: 32-row groups of 4 KB; row u of a group at
+// (u / 8) * 1 KB + (u % 8) * 128 B, its 16-byte piece q in slot q ^ fswz(u).
+__device__ inline int fswz(int u) { return (u & 7) ^ ((u >> 3) & 1); }
+
+// The eight rows a wave loads per stage: rows 32 i + 8 wave + lane / 8 of the
+// tile (i = 0..7), 16 bytes each per lane.  Memory row of tile row r =
+// min(row0 + r, rows - 1) / div (div = 2 maps paired-route rows to x rows).
+struct FOpnd {
+  const char* base;  // byte address of memory row row0 / div, k = 0 (uniform)
+  uint32_t off[8];   // per-lane byte offsets from base: row and swizzled piece
+};
+
+__device__ inline FOpnd make_fopnd(const float* p, int64_t ld, int64_t row0, int64_t rows, int div, int wave,
+                                   int lane) {
+  FOpnd o;
+  const int64_t base_row = row0 / div;
+  o.base = reinterpret_cast<const char*>(p + base_row * ld);
+  const int r8 = lane >> 3;
+  const int piece = (lane & 7) ^ r8 ^ (wave & 1);  // fswz(8 wave + r8) = r8 ^ (wave & 1)
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int64_t row = row0 + 32 * i + 8 * wave + r8;
+    row = row < rows ? row : rows - 1;
+    o.off[i] = static_cast<uint32_t>(((row / div - base_row) * ld + 4 * piece) * 4);
+  }
+  return o;
+}
+
+// acc[i][j] += A-tile rows (128 wa + 32 i ..) . B-tile rows (128 wb + 32 j ..)^T
+// over k in [k0, k0 + 32 nk), wave = 2 wa + wb.
+//
+// Per k block: 16 steps of 16 MFMAs in two halves (steps 0-7: pieces 4 h,
+// 4 h + 1 of each row; steps 8-15: pieces 4 h + 2, 4 h + 3).  A half's
+// fragments are read while the other half's MFMAs run: the second half of
+// block kb under the first half's MFMAs, the first half of block kb + 1
+// under the second half's.  Between the two halves the workgroup barrier
+// that ends the reads of block kb's stage, the loads of block kb + 2 into
+// it, and the wait for block kb + 1 (loaded one block earlier).
+__device__ inline void fgemm_loop(f32x16_t (&acc)[4][4], const FOpnd& A, const FOpnd& B, int64_t k0, int nk,
+                                  char* lds, int wave, int lane) {
+  const int wa = wave >> 1, wb = wave & 1;
+  const int u = lane & 31, h = lane >> 5;
+  int le[4];  // piece 4 h + m of row u
+#pragma unroll
+  for (int m = 0; m < 4; ++m) le[m] = (u >> 3) * 1024 + (u & 7) * 128 + (((4 * h + m) ^ fswz(u)) * 16);
+  // block b's 16 loads per thread: eight A pieces, eight B pieces
+  auto issue = [&](int b, char* stage) {
+    const int64_t kbyte = (k0 + static_cast<int64_t>(b) * kFK) * 4;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) g2lds16(A.base + kbyte + A.off[q], stage + q * kFGroupBytes + wave * 1024);
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      g2lds16(B.base + kbyte + B.off[q], stage + kFOpBytes + q * kFGroupBytes + wave * 1024);
+  };
+  // half hf of block kb's fragments: 8 floats a lane per row block of A (B)
+  auto read = [&](const char* st, int hf, float (&fa)[4][8], float (&fb)[4][8]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const char* ra = st + (4 * wa + g) * kFGroupBytes;
+      const char* rb = st + kFOpBytes + (4 * wb + g) * kFGroupBytes;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const float4 qa = *reinterpret_cast<const float4*>(ra + le[2 * hf + m]);
+        const float4 qb = *reinterpret_cast<const float4*>(rb + le[2 * hf + m]);
+        fa[g][4 * m] = qa.x;
+        fa[g][4 * m + 1] = qa.y;
+        fa[g][4 * m + 2] = qa.z;
+        fa[g][4 * m + 3] = qa.w;
+        fb[g][4 * m] = qb.x;
+        fb[g][4 * m + 1] = qb.y;
+        fb[g][4 * m + 2] = qb.z;
+        fb[g][4 * m + 3] = qb.w;
+      }
+    }
+  };
+  auto steps = [&](const float (&fa)[4][8], const float (&fb)[4][8]) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[q >> 2][q & 3] = mfma_f32(fa[q >> 2][s], fb[q & 3][s], acc[q >> 2][q & 3]);
+  };
+  // block kb has landed in every wave's share (kb + 1 the last block issued)
+  auto landed = [&](int kb) {
+    if (kb + 1 < nk)
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (16 & 0xF) | ((16 >> 4) << 14));  // vmcnt(16): block kb + 1 in flight
+    else
+      wait_vm0();
+    barrier_lds();
+  };
+  float fa0[4][8], fb0[4][8], fa1[4][8], fb1[4][8];
+  issue(0, lds);
+  if (nk > 1) issue(1, lds + kFStageBytes);
+  landed(0);
+  read(lds, 0, fa0, fb0);
+  for (int kb = 0; kb < nk; ++kb) {
+    char* st = lds + (kb & 1) * kFStageBytes;
+    read(st, 1, fa1, fb1);
+    steps(fa0, fb0);
+    barrier_lds();  // no wave reads block kb's stage any more
+    if (kb + 2 < nk) issue(kb + 2, st);
+    if (kb + 1 < nk) {
+      landed(kb + 1);
+      read(lds + ((kb + 1) & 1) * kFStageBytes, 0, fa0, fb0);
+    }
+    steps(fa1, fb1);
+  }
+}
+
+// Workgroup -> (row tile, column tile) with the column tile shared by the
+// workgroups of one XCD (blockIdx % 8): they walk the row tiles of one column
+// tile together, so its operand rows are fetched into that XCD's L2 once.
+__device__ inline bool ftile_of(int nrow, int ncol, int& rt, int& ct) {
+  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+  ct = (k / nrow) * 8 + x;
+  rt = k % nrow;
+  return ct < ncol;
+}
+
+// ---------------------------------------------------------------------------
+// pack: W [N, D] -> W^T [D, N64], zero for units >= N
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void pack_wt_f32_kernel(const float* __restrict__ W, float* __restrict__ WT,
+                                                          int64_t N, int64_t N64, int D) {
+  __shared__ float tile[64][65];
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int d0 = blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t n = n0 + r;
+    const int d = d0 + tx;
+    tile[r][tx] = (n < N && d < D) ? W[n * D + d] : 0.f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int d = d0 + r;
+    const int64_t n = n0 + tx;
+    if (d < D && n < N64) WT[static_cast<int64_t>(d) * N64 + n] = tile[tx][r];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// stats: the fp32 scores of a tile, stored, and per-token moment partials
+// ---------------------------------------------------------------------------
+struct FStatsParams {
+  const float* h;    // [Tv, dr]
+  const float* emb;  // [N, dr]
+  float* S;          // [Tv, N64] fp32 scores (zero for units >= N)
+  float* mom;        // [2 CT][Tv][2]
+  int64_t Tv, N, N64, dr;
+  int RT, CT;
+};
+
+__global__ __launch_bounds__(kFThreads, 1) void f32_stats_kernel(FStatsParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
+  int rt, ct;
+  if (!ftile_of(p.RT, p.CT, rt, ct)) return;
+  const int64_t u0 = static_cast<int64_t>(ct) * kFRows, v0 = static_cast<int64_t>(rt) * kFRows;
+  const FOpnd A = make_fopnd(p.emb, p.dr, u0, p.N, 1, wave, lane);
+  const FOpnd B = make_fopnd(p.h, p.dr, v0, p.Tv, 1, wave, lane);
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+  fgemm_loop(acc, A, B, 0, static_cast<int>(p.dr / kFK), lds, wave, lane);
+
+  // element v of accumulator (i, j): unit 128 wa + 32 i + 8 (v / 4) + 4 h + v % 4
+  // of the tile, token 128 wb + 32 j + u
+  const int64_t nleft = p.N - (u0 + 128 * wa + 4 * h);  // units of this wave-row left in the pool
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t t = v0 + 128 * wb + 32 * j + u;
+    float* srow = p.S + (t < p.Tv ? t : 0) * p.N64;
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int v = 0; v < 16; v += 4) {
+        const int r = 32 * i + 8 * (v >> 2);  // unit offset from u0 + 128 wa + 4 h
+        float4 q;
+        q.x = r < nleft ? acc[i][j][v] : 0.f;
+        q.y = r + 1 < nleft ? acc[i][j][v + 1] : 0.f;
+        q.z = r + 2 < nleft ? acc[i][j][v + 2] : 0.f;
+        q.w = r + 3 < nleft ? acc[i][j][v + 3] : 0.f;
+        s1 += q.x;
+        s2 += q.x * q.x;
+        s1 += q.y;
+        s2 += q.y * q.y;
+        s1 += q.z;
+        s2 += q.z * q.z;
+        s1 += q.w;
+        s2 += q.w * q.w;
+        const int64_t n0 = u0 + 128 * wa + r + 4 * h;
+        if (t < p.Tv && n0 < p.N64) *reinterpret_cast<float4*>(srow + n0) = q;
+      }
+    }
+    s1 += __shfl_xor(s1, 32);
+    s2 += __shfl_xor(s2, 32);
+    if (h == 0 && t < p.Tv) {
+      float* m = p.mom + ((static_cast<int64_t>(2 * ct + wa)) * p.Tv + t) * 2;
+      m[0] = s1;
+      m[1] = s2;
+    }
+  }
+}
+
+// centred second moments of the stored scores: mom[t] = (sum s, sum (s - mean)^2)
+// over the N units of row t (v41:1719-1721); one wave per row
+__global__ __launch_bounds__(256) void f32_centre_kernel(const float* __restrict__ S, const float* __restrict__ mean,
+                                                         float* __restrict__ mom, int64_t Tv, int64_t N, int64_t N64) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= Tv) return;
+  const float mu = mean[t];
+  const float* row = S + t * N64;
+  float s1 = 0.f, s2 = 0.f;
+  for (int64_t n0 = 4 * lane; n0 < N; n0 += 256) {
+    const float4 q = *reinterpret_cast<const float4*>(row + n0);
+    const float e[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool ok = n0 + k < N;
+      const float d = ok ? e[k] - mu : 0.f;
+      s1 += ok ? e[k] : 0.f;
+      s2 += d * d;
+    }
+  }
+  s1 = wave_sum(s1);
+  s2 = wave_sum(s2);
+  if (lane == 0) {
+    mom[2 * t] = s1;
+    mom[2 * t + 1] = s2;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gate: XR of one tile, the v4.1 gate of the stored scores, P over S in place
+// ---------------------------------------------------------------------------
+struct FGateParams {
+  const float* x;     // [T, D] (row v / routes)
+  const float* read;  // [N, D]
+  const float* tau;   // [Tv]
+  float* P;           // [Tv, N64]: the scores in, P out (in place)
+  float* tok_part;    // [2 CT][Tv][4]: sum gate, sum intensity, active count
+  uint32_t* mask32;   // [Tv][mask_words32] or null
+  int64_t mask_words32;
+  int64_t Tv, N, N64, D;
+  int routes, RT, CT;
+  GateParams gp;
+};
+
+__global__ __launch_bounds__(kFThreads, 1) void f32_gate_kernel(FGateParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
+  int rt, ct;
+  if (!ftile_of(p.RT, p.CT, rt, ct)) return;
+  const int64_t u0 = static_cast<int64_t>(ct) * kFRows, v0 = static_cast<int64_t>(rt) * kFRows;
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+  {
+    const FOpnd A = make_fopnd(p.read, p.D, u0, p.N, 1, wave, lane);
+    const FOpnd B = make_fopnd(p.x, p.D, v0, p.Tv, p.routes, wave, lane);
+    fgemm_loop(acc, A, B, 0, static_cast<int>(p.D / kFK), lds, wave, lane);
+  }
+
+  // gate epilogue (v41:1723-1735) in the reference's fp32 expression order;
+  // four consecutive units per load / store
+  const int64_t nleft = p.N - (u0 + 128 * wa + 4 * h);  // units of this wave-row left in the pool
+  const float k_exp2 = -p.gp.sharp * 1.4426950408889634f;   // e^(-sharpness m) = 2^(m k_exp2)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t t = v0 + 128 * wb + 32 * j + u;
+    const bool tok = t < p.Tv;
+    float* prow = p.P + (tok ? t : p.Tv - 1) * p.N64;
+    const float tau = p.tau[tok ? t : p.Tv - 1];
+    float gs = 0.f, is = 0.f;
+    int na = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t m = 0;  // pass bits of the 32-unit block: element v at bit unit_of_acc(v, h)
+#pragma unroll
+      for (int v = 0; v < 16; v += 4) {
+        const int r = 32 * i + 8 * (v >> 2);
+        const int64_t nb = u0 + 128 * wa + r + 4 * h;
+        const bool in_row = nb < p.N64;  // the last unit tile may reach past the row's N64 columns
+        float4 q = in_row ? *reinterpret_cast<const float4*>(prow + nb) : float4{0.f, 0.f, 0.f, 0.f};
+        float e[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          // margin = (s - tau) - thr, sigmoid(sharpness margin) through the
+          // hardware exp2 (within 2 ulp of expf), intensity and gate in the
+          // reference's order (v41:1723-1728)
+          const float margin = (e[k] - tau) - p.gp.thr;
+          const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(margin * k_exp2));
+          const float inten = p.gp.eps + fminf(fmaxf(margin - p.gp.cut, 0.0f), p.gp.maxi);
+          const bool ok = r + k < nleft;  // units past N count for nothing
+          const float gate = ok ? act * inten : 0.f;
+          gs += gate;
+          is += ok ? inten : 0.f;
+          if (ok && act > 0.5f) m |= 1u << (8 * (v >> 2) + 4 * h + k);
+          e[k] = gate * acc[i][j][v + k];  // P = gate * xr (v41:1735)
+        }
+        if (tok && in_row) *reinterpret_cast<float4*>(prow + nb) = float4{e[0], e[1], e[2], e[3]};
+      }
+      na += __builtin_popcount(m);
+      m |= __shfl_xor(m, 32);
+      const int64_t word = (u0 + 128 * wa + 32 * i) / 32;
+      if (p.mask32 && h == 0 && tok && word < p.mask_words32) p.mask32[t * p.mask_words32 + word] = m;
+    }
+    gs += __shfl_xor(gs, 32);
+    is += __shfl_xor(is, 32);
+    na += __shfl_xor(na, 32);
+    if (h == 0 && tok) {
+      float* tp = p.tok_part + (static_cast<int64_t>(2 * ct + wa) * p.Tv + t) * 4;
+      tp[0] = gs;
+      tp[1] = is;
+      tp[2] = static_cast<float>(na);
+      tp[3] = 0.f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// write: OUT partial of one N-split = P[:, split units] . W^T[:, split units]^T
+// ---------------------------------------------------------------------------
+struct FWriteParams {
+  const float* P;   // [Tv, N64]
+  const float* wt;  // [D, N64]
+  float* out_part;  // [S][Tv][D]
+  int64_t Tv, N64, D;
+  int S, RT, DT, nkb;  // nkb: 32-unit k blocks over N64
+};
+
+__global__ __launch_bounds__(kFThreads, 1) void f32_write_kernel(FWriteParams p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
+  // workgroups of one (token tile, split) on one XCD, consecutive: their D
+  // tiles share the P tile
+  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int dt = k % p.DT;
+  const int w = (k / p.DT) * 8 + x;
+  if (w >= p.RT * p.S) return;
+  const int rt = w % p.RT, split = w / p.RT;
+  const int64_t kb0 = static_cast<int64_t>(p.nkb) * split / p.S, kb1 = static_cast<int64_t>(p.nkb) * (split + 1) / p.S;
+  const int64_t v0 = static_cast<int64_t>(rt) * kFRows, d0 = static_cast<int64_t>(dt) * kFRows;
+  const FOpnd A = make_fopnd(p.P, p.N64, v0, p.Tv, 1, wave, lane);
+  const FOpnd B = make_fopnd(p.wt, p.N64, d0, p.D, 1, wave, lane);
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+  fgemm_loop(acc, A, B, kb0 * kFK, static_cast<int>(kb1 - kb0), lds, wave, lane);
+
+  float* dst = p.out_part + static_cast<int64_t>(split) * p.Tv * p.D;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t t = v0 + 128 * wa + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (t >= p.Tv) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t d = d0 + 128 * wb + 32 * j + u;
+        if (d < p.D) dst[t * p.D + d] = acc[i][j][v];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// final: per row the gate kernel's partials in tile order, den, and out =
+// (sum over splits of the partial rows) / den * scale in fp32 (v41:1736-1737).
+// One workgroup per row.
+// ---------------------------------------------------------------------------
+struct FFinalParams {
+  const float* out_part;  // [S][Tv][D]
+  const float* tok_part;  // [S_tok][Tv][4]
+  float* out;             // [Tv, D]
+  float* gate_sum;
+  float* den;
+  int32_t* n_active;
+  int64_t Tv, D;
+  int S, S_tok;
+  float scale;
+};
+
+__global__ __launch_bounds__(256) void f32_final_kernel(FFinalParams p) {
+  __shared__ float red[3][4];
+  __shared__ float den_s;
+  const int64_t t = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float g = 0.f, in = 0.f, na = 0.f;
+  for (int s = threadIdx.x; s < p.S_tok; s += 256) {
+    const float4 q = *reinterpret_cast<const float4*>(p.tok_part + (static_cast<int64_t>(s) * p.Tv + t) * 4);
+    g += q.x;
+    in += q.y;
+    na += q.z;
+  }
+  g = wave_sum(g);
+  in = wave_sum(in);
+  na = wave_sum(na);
+  if (lane == 0) {
+    red[0][wave] = g;
+    red[1][wave] = in;
+    red[2][wave] = na;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float G = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    const float I = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    const float A = red[2][0] + red[2][1] + red[2][2] + red[2][3];
+    const float den = fmaxf(I, 1.0f);  // v41:1736
+    den_s = den;
+    if (p.gate_sum) p.gate_sum[t] = G;
+    if (p.den) p.den[t] = den;
+    if (p.n_active) p.n_active[t] = static_cast<int32_t>(A);
+  }
+  __syncthreads();
+  const float den = den_s;
+  for (int64_t d = threadIdx.x; d < p.D; d += 256) {
+    float acc = 0.f;
+    for (int s = 0; s < p.S; ++s) acc += p.out_part[(static_cast<int64_t>(s) * p.Tv + t) * p.D + d];
+    p.out[t * p.D + d] = acc / den * p.scale;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct FGeo {
+  int64_t Tv, N, N64;
+  int RT, CT, DT, S, nkb;
+};
+
+int64_t fal256(int64_t b) { return (b + 255) & ~static_cast<int64_t>(255); }
+
+FGeo fgeo(const srw_desc_t& d) {
+  FGeo g{};
+  g.Tv = d.T * d.n_routes;
+  g.N = d.n_units;
+  g.N64 = (g.N + kFNAlign - 1) / kFNAlign * kFNAlign;
+  g.RT = static_cast<int>((g.Tv + kFRows - 1) / kFRows);
+  g.CT = static_cast<int>((g.N + kFRows - 1) / kFRows);
+  g.DT = static_cast<int>((d.d_model + kFRows - 1) / kFRows);
+  g.nkb = static_cast<int>(g.N64 / kFK);
+  // splits of the write GEMM: enough workgroups for 256 CUs, each at least
+  // four k blocks
+  const int64_t per_split = static_cast<int64_t>(g.RT) * g.DT;
+  int64_t S = (512 + per_split - 1) / per_split;
+  const int64_t most = g.nkb / 4 > 1 ? g.nkb / 4 : 1;
+  S = S < 1 ? 1 : (S > most ? most : S);
+  g.S = static_cast<int>(S);
+  return g;
+}
+
+struct FLayout {
+  size_t wt, P, mom, tau, out_part, tok_part, total;
+};
+
+FLayout flayout(const srw_desc_t& d, const FGeo& g) {
+  FLayout l{};
+  size_t off = 0;
+  l.wt = off;
+  off += fal256(d.d_model * g.N64 * 4);
+  l.P = off;
+  off += fal256(g.Tv * g.N64 * 4);
+  l.mom = off;
+  off += fal256(static_cast<int64_t>(2 * g.CT) * g.Tv * 2 * 4);
+  l.tau = off;
+  off += fal256(g.Tv * 4);
+  l.out_part = off;
+  off += fal256(static_cast<int64_t>(g.S) * g.Tv * d.d_model * 4);
+  l.tok_part = off;
+  off += fal256(static_cast<int64_t>(2 * g.CT) * g.Tv * 4 * 4);
+  l.total = off;
+  return l;
+}
+
+}  // namespace
+
+bool tiled_f32_supports(const srw_desc_t& d) {
+  if (d.dtype != SRW_F32 || d.gate != SRW_GATE_V41) return false;
+  if (d.stats_mode != SRW_STATS_ONEPASS && d.stats_mode != SRW_STATS_CENTERED) return false;
+  if (d.flags & (SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST)) return false;
+  if (d.n_routes != 1 && d.n_routes != 2) return false;
+  if (d.d_model % kFK != 0 || d.d_route % kFK != 0) return false;
+  return true;
+}
+
+size_t tiled_f32_workspace_bytes(const srw_desc_t& d) { return flayout(d, fgeo(d)).total; }
+
+hipError_t tiled_f32_forward(const LaunchArgs& a) {
+  const srw_desc_t& d = a.d;
+  const FGeo g = fgeo(d);
+  const FLayout l = flayout(d, g);
+  if (a.ws_bytes < l.total) return hipErrorInvalidValue;
+  float* wt = reinterpret_cast<float*>(a.ws + l.wt);
+  float* P = reinterpret_cast<float*>(a.ws + l.P);
+  float* mom = reinterpret_cast<float*>(a.ws + l.mom);
+  float* tau = reinterpret_cast<float*>(a.ws + l.tau);
+  float* out_part = reinterpret_cast<float*>(a.ws + l.out_part);
+  float* tok_part = reinterpret_cast<float*>(a.ws + l.tok_part);
+  const int D = static_cast<int>(d.d_model);
+  hipError_t e;
+  static_assert(kFGemmLds <= 160 * 1024, "LDS per workgroup");
+  for (const void* fn : {reinterpret_cast<const void*>(f32_stats_kernel),
+                         reinterpret_cast<const void*>(f32_gate_kernel),
+                         reinterpret_cast<const void*>(f32_write_kernel)})
+    if ((e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kFGemmLds)) != hipSuccess) return e;
+
+  if (!(d.flags & SRW_FLAG_POOL_CACHED)) {
+    const dim3 grid_p(static_cast<unsigned>(g.N64 / 64), static_cast<unsigned>((D + 63) / 64));
+    hipLaunchKernelGGL(pack_wt_f32_kernel, grid_p, dim3(256), 0, a.stream, static_cast<const float*>(a.in.write),
+                       wt, g.N, g.N64, D);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  const unsigned grid_rc = static_cast<unsigned>(8 * g.RT * ((g.CT + 7) / 8));
+  FStatsParams sp{};
+  sp.h = static_cast<const float*>(a.in.h);
+  sp.emb = static_cast<const float*>(a.in.emb);
+  sp.S = P;
+  sp.mom = mom;
+  sp.Tv = g.Tv;
+  sp.N = g.N;
+  sp.N64 = g.N64;
+  sp.dr = d.d_route;
+  sp.RT = g.RT;
+  sp.CT = g.CT;
+  hipLaunchKernelGGL(f32_stats_kernel, dim3(grid_rc), dim3(kFThreads), kFGemmLds, a.stream, sp);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  int S_st = 2 * g.CT;
+  if (d.stats_mode == SRW_STATS_CENTERED) {
+    // row means, then sum (s - mean)^2 over the stored scores into mom[0][t]
+    if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, S_st, g.N, 2, nullptr, kTauMean, a.stream)) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(f32_centre_kernel, dim3(static_cast<unsigned>((g.Tv + 3) / 4)), dim3(256), 0, a.stream, P, tau,
+                       mom, g.Tv, g.N, g.N64);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    S_st = 1;
+  }
+  if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, S_st, g.N, 2, nullptr,
+                      d.stats_mode == SRW_STATS_CENTERED ? kTauCentered : kTauOnePass, a.stream)) != hipSuccess)
+    return e;
+
+  FGateParams gp{};
+  gp.x = static_cast<const float*>(a.in.x);
+  gp.read = static_cast<const float*>(a.in.read);
+  gp.tau = tau;
+  gp.P = P;
+  gp.tok_part = tok_part;
+  gp.mask32 = reinterpret_cast<uint32_t*>(a.o.pass_mask);
+  gp.mask_words32 = 2 * a.words;
+  gp.Tv = g.Tv;
+  gp.N = g.N;
+  gp.N64 = g.N64;
+  gp.D = D;
+  gp.routes = d.n_routes;
+  gp.RT = g.RT;
+  gp.CT = g.CT;
+  gp.gp = a.gp;
+  dominant_kernel_begin(a.stream);
+  hipLaunchKernelGGL(f32_gate_kernel, dim3(grid_rc), dim3(kFThreads), kFGemmLds, a.stream, gp);
+  dominant_kernel_end(a.stream);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+
+  FWriteParams wp{};
+  wp.P = P;
+  wp.wt = wt;
+  wp.out_part = out_part;
+  wp.Tv = g.Tv;
+  wp.N64 = g.N64;
+  wp.D = D;
+  wp.S = g.S;
+  wp.RT = g.RT;
+  wp.DT = g.DT;
+  wp.nkb = g.nkb;
+  const unsigned grid_w = static_cast<unsigned>(8 * g.DT * ((static_cast<int64_t>(g.RT) * g.S + 7) / 8));
+  hipLaunchKernelGGL(f32_write_kernel, dim3(grid_w), dim3(kFThreads), kFGemmLds, a.stream, wp);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+
+  FFinalParams fp{};
+  fp.out_part = out_part;
+  fp.tok_part = tok_part;
+  fp.out = static_cast<float*>(a.o.out);
+  fp.gate_sum = a.o.gate_sum;
+  fp.den = a.o.den;
+  fp.n_active = a.o.n_active;
+  fp.Tv = g.Tv;
+  fp.D = D;
+  fp.S = g.S;
+  fp.S_tok = 2 * g.CT;
+  fp.scale = d.scale;
+  hipLaunchKernelGGL(f32_final_kernel, dim3(static_cast<unsigned>(g.Tv)), dim3(256), 0, a.stream, fp);
+  return hipGetLastError();
+}
+
+}  // namespace srw

@@ -102,7 +102,8 @@ def test_generic_f32_matches_srw_inference(pkg, dev, case):
     T, D, dr, N, hx = case
     print(f"[gpu] generic f32 centered {case}", flush=True)
     inp = _inputs(pkg, T, D, dr, N, 1, hx, seed=3 * T + N)
-    got = _run(pkg, inp, dev, F32, stats="centered", want_mask=True)
+    got = _run(pkg, inp, dev, F32, stats="centered", want_mask=True, force_generic=True)
+    assert got["path"] == "generic"
     h = inp["x"] if hx else inp["h"][:, 0]
     out_ref, tr = srw_ref.srw_inference(inp["x"], h, inp["emb"], inp["tau_offset"],
                                         inp["read"], inp["write"], return_trace=True)
