@@ -115,7 +115,12 @@ extern "C" {
 int32_t srw_abi_version(void) { return SRW_AMD_ABI_VERSION; }
 
 const char* srw_status_string(srw_status_t s) {
-  switch (s) {
+  // A C caller may pass any int here; read its bits as an int (loading a C++
+  // enum outside its enumerators' range is undefined behaviour)
+  static_assert(sizeof(srw_status_t) == sizeof(int32_t), "srw_status_t is int-sized");
+  int32_t v;
+  memcpy(&v, &s, sizeof v);
+  switch (v) {
     case SRW_OK: return "SRW_OK";
     case SRW_EINVAL: return "SRW_EINVAL: invalid argument";
     case SRW_EUNSUPPORTED: return "SRW_EUNSUPPORTED: configuration not implemented";
