@@ -54,23 +54,25 @@ __device__ inline f32x16_t mfma_f32(float a, float b, f32x16_t c) {
 // (u / 8) * 1 KB + (u % 8) * 128 B, its 16-byte piece q in slot q ^ fswz(u).
 __device__ inline int fswz(int u) { return (u & 7) ^ ((u >> 3) & 1); }
 
-// The eight rows a wave loads per stage: rows 32 i + 8 wave + lane / 8 of the
-// tile (i = 0..7), 16 bytes each per lane.  Memory row of tile row r =
+// The G rows a wave loads per stage: rows 32 i + 8 wave + lane / 8 of the
+// tile (i = 0..G-1, one per 32-row group), 16 bytes each per lane.  Memory row of tile row r =
 // min(row0 + r, rows - 1) / div (div = 2 maps paired-route rows to x rows).
+template <int G>
 struct FOpnd {
   const char* base;  // byte address of memory row row0 / div, k = 0 (uniform)
-  uint32_t off[8];   // per-lane byte offsets from base: row and swizzled piece
+  uint32_t off[G];   // per-lane byte offsets from base: row and swizzled piece
 };
 
-__device__ inline FOpnd make_fopnd(const float* p, int64_t ld, int64_t row0, int64_t rows, int div, int wave,
-                                   int lane) {
-  FOpnd o;
+template <int G = 8>
+__device__ inline FOpnd<G> make_fopnd(const float* p, int64_t ld, int64_t row0, int64_t rows, int div, int wave,
+                                      int lane) {
+  FOpnd<G> o;
   const int64_t base_row = row0 / div;
   o.base = reinterpret_cast<const char*>(p + base_row * ld);
   const int r8 = lane >> 3;
   const int piece = (lane & 7) ^ r8 ^ (wave & 1);  // fswz(8 wave + r8) = r8 ^ (wave & 1)
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < G; ++i) {
     int64_t row = row0 + 32 * i + 8 * wave + r8;
     row = row < rows ? row : rows - 1;
     o.off[i] = static_cast<uint32_t>(((row / div - base_row) * ld + 4 * piece) * 4);
@@ -78,46 +80,56 @@ __device__ inline FOpnd make_fopnd(const float* p, int64_t ld, int64_t row0, int
   return o;
 }
 
-// acc[i][j] += A-tile rows (128 wa + 32 i ..) . B-tile rows (128 wb + 32 j ..)^T
-// over k in [k0, k0 + 32 nk), wave = 2 wa + wb.
+// acc[i][j] += A-tile rows (32 (ga0 + i) ..) . B-tile rows (32 (gb0 + j) ..)^T
+// over k in [k0, k0 + 32 nk), for an A tile of GA 32-row groups and a B tile
+// of GB groups (a stage holds both: (GA + GB) x 4 KB); the wave's accumulator
+// block is MI x MJ MFMA tiles at groups (ga0, gb0).
 //
-// Per k block: 16 steps of 16 MFMAs in two halves (steps 0-7: pieces 4 h,
+// Per k block: 16 steps of MI x MJ MFMAs in two halves (steps 0-7: pieces 4 h,
 // 4 h + 1 of each row; steps 8-15: pieces 4 h + 2, 4 h + 3).  A half's
 // fragments are read while the other half's MFMAs run: the second half of
 // block kb under the first half's MFMAs, the first half of block kb + 1
 // under the second half's.  Between the two halves the workgroup barrier
 // that ends the reads of block kb's stage, the loads of block kb + 2 into
 // it, and the wait for block kb + 1 (loaded one block earlier).
-__device__ inline void fgemm_loop(f32x16_t (&acc)[4][4], const FOpnd& A, const FOpnd& B, int64_t k0, int nk,
-                                  char* lds, int wave, int lane) {
-  const int wa = wave >> 1, wb = wave & 1;
+template <int GA, int GB, int MI, int MJ>
+__device__ inline void fgemm_loop(f32x16_t (&acc)[MI][MJ], const FOpnd<GA>& A, const FOpnd<GB>& B, int64_t k0,
+                                  int nk, char* lds, int ga0, int gb0, int wave, int lane) {
+  constexpr int kOpA = GA * kFGroupBytes, kStage = (GA + GB) * kFGroupBytes;
+  static_assert(2 * kStage <= kFGemmLds, "two stages fit the LDS allocation");
+  static_assert(GA + GB <= 63, "loads per block within the vmcnt range");
   const int u = lane & 31, h = lane >> 5;
   int le[4];  // piece 4 h + m of row u
 #pragma unroll
   for (int m = 0; m < 4; ++m) le[m] = (u >> 3) * 1024 + (u & 7) * 128 + (((4 * h + m) ^ fswz(u)) * 16);
-  // block b's 16 loads per thread: eight A pieces, eight B pieces
+  // block b's GA + GB loads per thread: one piece per 32-row group
   auto issue = [&](int b, char* stage) {
     const int64_t kbyte = (k0 + static_cast<int64_t>(b) * kFK) * 4;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) g2lds16(A.base + kbyte + A.off[q], stage + q * kFGroupBytes + wave * 1024);
+    for (int q = 0; q < GA; ++q) g2lds16(A.base + kbyte + A.off[q], stage + q * kFGroupBytes + wave * 1024);
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
-      g2lds16(B.base + kbyte + B.off[q], stage + kFOpBytes + q * kFGroupBytes + wave * 1024);
+    for (int q = 0; q < GB; ++q) g2lds16(B.base + kbyte + B.off[q], stage + kOpA + q * kFGroupBytes + wave * 1024);
   };
   // half hf of block kb's fragments: 8 floats a lane per row block of A (B)
-  auto read = [&](const char* st, int hf, float (&fa)[4][8], float (&fb)[4][8]) {
+  auto read = [&](const char* st, int hf, float (&fa)[MI][8], float (&fb)[MJ][8]) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const char* ra = st + (4 * wa + g) * kFGroupBytes;
-      const char* rb = st + kFOpBytes + (4 * wb + g) * kFGroupBytes;
+    for (int g = 0; g < MI; ++g) {
+      const char* ra = st + (ga0 + g) * kFGroupBytes;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const float4 qa = *reinterpret_cast<const float4*>(ra + le[2 * hf + m]);
-        const float4 qb = *reinterpret_cast<const float4*>(rb + le[2 * hf + m]);
         fa[g][4 * m] = qa.x;
         fa[g][4 * m + 1] = qa.y;
         fa[g][4 * m + 2] = qa.z;
         fa[g][4 * m + 3] = qa.w;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < MJ; ++g) {
+      const char* rb = st + kOpA + (gb0 + g) * kFGroupBytes;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const float4 qb = *reinterpret_cast<const float4*>(rb + le[2 * hf + m]);
         fb[g][4 * m] = qb.x;
         fb[g][4 * m + 1] = qb.y;
         fb[g][4 * m + 2] = qb.z;
@@ -125,34 +137,36 @@ __device__ inline void fgemm_loop(f32x16_t (&acc)[4][4], const FOpnd& A, const F
       }
     }
   };
-  auto steps = [&](const float (&fa)[4][8], const float (&fb)[4][8]) {
+  auto steps = [&](const float (&fa)[MI][8], const float (&fb)[MJ][8]) {
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
-      for (int q = 0; q < 16; ++q) acc[q >> 2][q & 3] = mfma_f32(fa[q >> 2][s], fb[q & 3][s], acc[q >> 2][q & 3]);
+      for (int q = 0; q < MI * MJ; ++q)
+        acc[q / MJ][q % MJ] = mfma_f32(fa[q / MJ][s], fb[q % MJ][s], acc[q / MJ][q % MJ]);
   };
   // block kb has landed in every wave's share (kb + 1 the last block issued)
   auto landed = [&](int kb) {
+    constexpr int kN = GA + GB;  // loads of block kb + 1, still in flight
     if (kb + 1 < nk)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | (16 & 0xF) | ((16 >> 4) << 14));  // vmcnt(16): block kb + 1 in flight
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (kN & 0xF) | ((kN >> 4) << 14));  // vmcnt(GA + GB)
     else
       wait_vm0();
     barrier_lds();
   };
-  float fa0[4][8], fb0[4][8], fa1[4][8], fb1[4][8];
+  float fa0[MI][8], fb0[MJ][8], fa1[MI][8], fb1[MJ][8];
   issue(0, lds);
-  if (nk > 1) issue(1, lds + kFStageBytes);
+  if (nk > 1) issue(1, lds + kStage);
   landed(0);
   read(lds, 0, fa0, fb0);
   for (int kb = 0; kb < nk; ++kb) {
-    char* st = lds + (kb & 1) * kFStageBytes;
+    char* st = lds + (kb & 1) * kStage;
     read(st, 1, fa1, fb1);
     steps(fa0, fb0);
     barrier_lds();  // no wave reads block kb's stage any more
     if (kb + 2 < nk) issue(kb + 2, st);
     if (kb + 1 < nk) {
       landed(kb + 1);
-      read(lds + ((kb + 1) & 1) * kFStageBytes, 0, fa0, fb0);
+      read(lds + ((kb + 1) & 1) * kStage, 0, fa0, fb0);
     }
     steps(fa1, fb1);
   }
@@ -210,14 +224,14 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_stats_kernel(FStatsParams p)
   int rt, ct;
   if (!ftile_of(p.RT, p.CT, rt, ct)) return;
   const int64_t u0 = static_cast<int64_t>(ct) * kFRows, v0 = static_cast<int64_t>(rt) * kFRows;
-  const FOpnd A = make_fopnd(p.emb, p.dr, u0, p.N, 1, wave, lane);
-  const FOpnd B = make_fopnd(p.h, p.dr, v0, p.Tv, 1, wave, lane);
+  const FOpnd<8> A = make_fopnd(p.emb, p.dr, u0, p.N, 1, wave, lane);
+  const FOpnd<8> B = make_fopnd(p.h, p.dr, v0, p.Tv, 1, wave, lane);
   f32x16_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
-  fgemm_loop(acc, A, B, 0, static_cast<int>(p.dr / kFK), lds, wave, lane);
+  fgemm_loop(acc, A, B, 0, static_cast<int>(p.dr / kFK), lds, 4 * wa, 4 * wb, wave, lane);
 
   // element v of accumulator (i, j): unit 128 wa + 32 i + 8 (v / 4) + 4 h + v % 4
   // of the tile, token 128 wb + 32 j + u
@@ -318,9 +332,9 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_gate_kernel(FGateParams p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
   {
-    const FOpnd A = make_fopnd(p.read, p.D, u0, p.N, 1, wave, lane);
-    const FOpnd B = make_fopnd(p.x, p.D, v0, p.Tv, p.routes, wave, lane);
-    fgemm_loop(acc, A, B, 0, static_cast<int>(p.D / kFK), lds, wave, lane);
+    const FOpnd<8> A = make_fopnd(p.read, p.D, u0, p.N, 1, wave, lane);
+    const FOpnd<8> B = make_fopnd(p.x, p.D, v0, p.Tv, p.routes, wave, lane);
+    fgemm_loop(acc, A, B, 0, static_cast<int>(p.D / kFK), lds, 4 * wa, 4 * wb, wave, lane);
   }
 
   // gate epilogue (v41:1723-1735) in the reference's fp32 expression order;
@@ -388,42 +402,54 @@ struct FWriteParams {
   const float* wt;  // [D, N64]
   float* out_part;  // [S][Tv][D]
   int64_t Tv, N64, D;
-  int S, RT, DT, nkb;  // nkb: 32-unit k blocks over N64
+  int S, RT, DT, nkb;  // RT, DT: token and column tiles of this kernel's tile shape; nkb: 32-unit k blocks
+  int W8;              // (token tile, split) pairs per XCD
 };
 
+// A workgroup computes a (32 GA tokens) x (32 GB columns) tile of one split's
+// partial; its waves hold MI x MJ MFMA tiles each, GB / MJ waves across the
+// columns.  Shapes: 256 x 256 (GA = GB = 8, 2 x 2 waves) and, for D = 384,
+// 128 x 384 (GA = 4, GB = 12, 1 x 4 waves of 128 x 96) so that no output
+// column is padded and every P tile is read once.
+template <int GA, int GB, int MI, int MJ>
 __global__ __launch_bounds__(kFThreads, 1) void f32_write_kernel(FWriteParams p) {
+  static_assert(GA % MI == 0 && GB % MJ == 0 && (GA / MI) * (GB / MJ) == kFThreads / 64,
+                "one accumulator block per wave");
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
-  // workgroups of one (token tile, split) on one XCD, consecutive: their D
-  // tiles share the P tile
+  constexpr int WB = GB / MJ;
+  const int wa = wave / WB, wb = wave % WB, u = lane & 31, h = lane >> 5;
+  // XCD x (blockIdx % 8) takes the W8 consecutive (token tile, split) pairs
+  // from x W8 on, token tile fastest, each with its DT column tiles in a row:
+  // the column tiles share the P tile and the token tiles of a split share
+  // its W^T rows in the XCD's L2.
   const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
   const int dt = k % p.DT;
-  const int w = (k / p.DT) * 8 + x;
-  if (w >= p.RT * p.S) return;
+  const int w = x * p.W8 + k / p.DT;
+  if (k / p.DT >= p.W8 || w >= p.RT * p.S) return;
   const int rt = w % p.RT, split = w / p.RT;
   const int64_t kb0 = static_cast<int64_t>(p.nkb) * split / p.S, kb1 = static_cast<int64_t>(p.nkb) * (split + 1) / p.S;
-  const int64_t v0 = static_cast<int64_t>(rt) * kFRows, d0 = static_cast<int64_t>(dt) * kFRows;
-  const FOpnd A = make_fopnd(p.P, p.N64, v0, p.Tv, 1, wave, lane);
-  const FOpnd B = make_fopnd(p.wt, p.N64, d0, p.D, 1, wave, lane);
-  f32x16_t acc[4][4];
+  const int64_t v0 = static_cast<int64_t>(rt) * 32 * GA, d0 = static_cast<int64_t>(dt) * 32 * GB;
+  const FOpnd<GA> A = make_fopnd<GA>(p.P, p.N64, v0, p.Tv, 1, wave, lane);
+  const FOpnd<GB> B = make_fopnd<GB>(p.wt, p.N64, d0, p.D, 1, wave, lane);
+  f32x16_t acc[MI][MJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
-  fgemm_loop(acc, A, B, kb0 * kFK, static_cast<int>(kb1 - kb0), lds, wave, lane);
+    for (int j = 0; j < MJ; ++j) acc[i][j] = f32x16_t{};
+  fgemm_loop(acc, A, B, kb0 * kFK, static_cast<int>(kb1 - kb0), lds, MI * wa, MJ * wb, wave, lane);
 
   float* dst = p.out_part + static_cast<int64_t>(split) * p.Tv * p.D;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < MI; ++i) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int64_t t = v0 + 128 * wa + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+      const int64_t t = v0 + 32 * (MI * wa + i) + 8 * (v >> 2) + 4 * h + (v & 3);
       if (t >= p.Tv) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t d = d0 + 128 * wb + 32 * j + u;
+      for (int j = 0; j < MJ; ++j) {
+        const int64_t d = d0 + 32 * (MJ * wb + j) + u;
         if (d < p.D) dst[t * p.D + d] = acc[i][j][v];
       }
     }
@@ -492,7 +518,9 @@ __global__ __launch_bounds__(256) void f32_final_kernel(FFinalParams p) {
 // ---------------------------------------------------------------------------
 struct FGeo {
   int64_t Tv, N, N64;
-  int RT, CT, DT, S, nkb;
+  int RT, CT, nkb;
+  bool w384;              // write tiles of 128 tokens x 384 columns (else 256 x 256)
+  int WRT, DT, S, W8;     // write: token tiles, column tiles, splits, pairs per XCD
 };
 
 int64_t fal256(int64_t b) { return (b + 255) & ~static_cast<int64_t>(255); }
@@ -504,15 +532,21 @@ FGeo fgeo(const srw_desc_t& d) {
   g.N64 = (g.N + kFNAlign - 1) / kFNAlign * kFNAlign;
   g.RT = static_cast<int>((g.Tv + kFRows - 1) / kFRows);
   g.CT = static_cast<int>((g.N + kFRows - 1) / kFRows);
-  g.DT = static_cast<int>((d.d_model + kFRows - 1) / kFRows);
   g.nkb = static_cast<int>(g.N64 / kFK);
+  // write tile shape: the one that pads fewer output columns, 256 wide on a tie
+  const int64_t D = d.d_model, pad256 = (D + 255) / 256 * 256 - D, pad384 = (D + 383) / 384 * 384 - D;
+  g.w384 = pad384 < pad256;
+  const int wr = g.w384 ? 128 : 256, wc = g.w384 ? 384 : 256;
+  g.WRT = static_cast<int>((g.Tv + wr - 1) / wr);
+  g.DT = static_cast<int>((D + wc - 1) / wc);
   // splits of the write GEMM: enough workgroups for 256 CUs, each at least
   // four k blocks
-  const int64_t per_split = static_cast<int64_t>(g.RT) * g.DT;
+  const int64_t per_split = static_cast<int64_t>(g.WRT) * g.DT;
   int64_t S = (512 + per_split - 1) / per_split;
   const int64_t most = g.nkb / 4 > 1 ? g.nkb / 4 : 1;
   S = S < 1 ? 1 : (S > most ? most : S);
   g.S = static_cast<int>(S);
+  g.W8 = static_cast<int>((static_cast<int64_t>(g.WRT) * g.S + 7) / 8);
   return g;
 }
 
@@ -568,7 +602,8 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   static_assert(kFGemmLds <= 160 * 1024, "LDS per workgroup");
   for (const void* fn : {reinterpret_cast<const void*>(f32_stats_kernel),
                          reinterpret_cast<const void*>(f32_gate_kernel),
-                         reinterpret_cast<const void*>(f32_write_kernel)})
+                         reinterpret_cast<const void*>(f32_write_kernel<8, 8, 4, 4>),
+                         reinterpret_cast<const void*>(f32_write_kernel<4, 12, 4, 3>)})
     if ((e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kFGemmLds)) != hipSuccess) return e;
 
   if (!(d.flags & SRW_FLAG_POOL_CACHED)) {
@@ -634,11 +669,15 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   wp.N64 = g.N64;
   wp.D = D;
   wp.S = g.S;
-  wp.RT = g.RT;
+  wp.RT = g.WRT;
   wp.DT = g.DT;
   wp.nkb = g.nkb;
-  const unsigned grid_w = static_cast<unsigned>(8 * g.DT * ((static_cast<int64_t>(g.RT) * g.S + 7) / 8));
-  hipLaunchKernelGGL(f32_write_kernel, dim3(grid_w), dim3(kFThreads), kFGemmLds, a.stream, wp);
+  wp.W8 = g.W8;
+  const unsigned grid_w = static_cast<unsigned>(8 * g.DT * g.W8);
+  if (g.w384)
+    hipLaunchKernelGGL((f32_write_kernel<4, 12, 4, 3>), dim3(grid_w), dim3(kFThreads), kFGemmLds, a.stream, wp);
+  else
+    hipLaunchKernelGGL((f32_write_kernel<8, 8, 4, 4>), dim3(grid_w), dim3(kFThreads), kFGemmLds, a.stream, wp);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 
   FFinalParams fp{};

@@ -49,6 +49,7 @@ CENTRED = [
     (300, 384, 128, 5000, 1, False, 0.8, 3),    # two token tiles, ragged
     (77, 128, 64, 777, 2, False, 0.0, 4),       # paired routes: 154 virtual rows
     (40, 256, 96, 300, 1, False, 1.5, 5),       # few units pass; N below one tile
+    (70, 1152, 64, 1000, 1, False, 0.4, 8),     # three 384-wide write column tiles
 ]
 
 
