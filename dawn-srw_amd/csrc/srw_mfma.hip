@@ -383,44 +383,49 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
     const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
     const bool full = u0 >= lo && u0 + kUnitTile <= hi;
     if constexpr (STORE) {
-      if (p.s_out && u0 >= lo) {
+      // the bf16 scores (v41:503), packed whether or not this split stores
+      // them: a conditional assignment would keep the previous tile's words
+      // alive in copies
 #pragma unroll
-        for (int v = 0; v < 16; v += 2) spd[v >> 1] = pack_bf16(acc[0][v], acc[0][v + 1]);  // v41:503
+      for (int v = 0; v < 16; v += 2) spd[v >> 1] = pack_bf16(acc[0][v], acc[0][v + 1]);
+      if (p.s_out && u0 >= lo)
         sdst = reinterpret_cast<char*>(p.s_out) + score_tile_off(p.g.ntiles, ttile, tile, wave) + lane * 16;
-      }
     }
+    // sum s and sum s^2 of a packed bf16 pair in one v_dot2c_f32_bf16 each
+    // (the squares of bf16 values are exact in fp32); units outside the
+    // split's range enter as zeros
+    const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 #pragma unroll
     for (int b = 0; b < TBW; ++b) {
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
-        const uint32_t sp = pack_bf16(acc[b][v], acc[b][v + 1]);
-        float x0 = lo_f32(sp), x1 = hi_f32(sp);
+        uint32_t sp = pack_bf16(acc[b][v], acc[b][v + 1]);
         bool ok0 = true, ok1 = true;
         if (!full) {
           const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
           ok0 = ua >= lo && ua < hi;
           ok1 = ub >= lo && ub < hi;
-          if (!ok0) x0 = 0.f;
-          if (!ok1) x1 = 0.f;
+          sp &= (ok0 ? 0x0000ffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
         }
-        float q0, q1;  // squares, or squared deviations from the row mean (centred)
+        const float x0 = lo_f32(sp), x1 = hi_f32(sp);
         if constexpr (MODE == kStatsCentered) {
+          // squared deviations from the row mean
           const float d0 = ok0 ? x0 - mu[b] : 0.f, d1 = ok1 ? x1 - mu[b] : 0.f;
-          q0 = __fmul_rn(d0, d0);
-          q1 = __fmul_rn(d1, d1);
+          s1[b] += x0;
+          s2[b] += __fmul_rn(d0, d0);
+          s1[b] += x1;
+          s2[b] += __fmul_rn(d1, d1);
         } else {
-          q0 = __fmul_rn(x0, x0);
-          q1 = __fmul_rn(x1, x1);
-        }
-        s1[b] += x0;
-        s2[b] += q0;
-        s1[b] += x1;
-        s2[b] += q1;
-        if constexpr (DG) {
-          s3[b] += __fmul_rn(q0, x0);
-          s4[b] += __fmul_rn(q0, q0);
-          s3[b] += __fmul_rn(q1, x1);
-          s4[b] += __fmul_rn(q1, q1);
+          const bf16x2_t sb = __builtin_bit_cast(bf16x2_t, sp);
+          s1[b] = __builtin_amdgcn_fdot2_f32_bf16(sb, ones, s1[b], false);
+          s2[b] = __builtin_amdgcn_fdot2_f32_bf16(sb, sb, s2[b], false);
+          if constexpr (DG) {
+            const float q0 = __fmul_rn(x0, x0), q1 = __fmul_rn(x1, x1);
+            s3[b] += __fmul_rn(q0, x0);
+            s4[b] += __fmul_rn(q0, q0);
+            s3[b] += __fmul_rn(q1, x1);
+            s4[b] += __fmul_rn(q1, q1);
+          }
         }
       }
     }
