@@ -213,9 +213,15 @@ struct FStatsParams {
   float* S;          // [Tv, N64] fp32 scores (zero for units >= N)
   float* mom;        // [2 CT][Tv][2]
   int64_t Tv, N, N64, dr;
-  int RT, CT;
+  int RT, CT;  // this launch: token tiles, unit tiles
+  int ct0;     // this launch's first unit tile
 };
 
+// A workgroup takes 256 units x 64 MJ tokens (2 x 2 waves of 128 units x
+// 32 MJ tokens): MJ = 4 for the rounds that fill every CU, MJ = 1 for the
+// unit tiles of a last, partly filled round (a quarter of the work each, so
+// that round ends four times sooner).
+template <int MJ>
 __global__ __launch_bounds__(kFThreads, 1) void f32_stats_kernel(FStatsParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
@@ -223,22 +229,23 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_stats_kernel(FStatsParams p)
   const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
   int rt, ct;
   if (!ftile_of(p.RT, p.CT, rt, ct)) return;
-  const int64_t u0 = static_cast<int64_t>(ct) * kFRows, v0 = static_cast<int64_t>(rt) * kFRows;
-  const FOpnd<8> A = make_fopnd(p.emb, p.dr, u0, p.N, 1, wave, lane);
-  const FOpnd<8> B = make_fopnd(p.h, p.dr, v0, p.Tv, 1, wave, lane);
-  f32x16_t acc[4][4];
+  ct += p.ct0;
+  const int64_t u0 = static_cast<int64_t>(ct) * kFRows, v0 = static_cast<int64_t>(rt) * 64 * MJ;
+  const FOpnd<8> A = make_fopnd<8>(p.emb, p.dr, u0, p.N, 1, wave, lane);
+  const FOpnd<2 * MJ> B = make_fopnd<2 * MJ>(p.h, p.dr, v0, p.Tv, 1, wave, lane);
+  f32x16_t acc[4][MJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
-  fgemm_loop(acc, A, B, 0, static_cast<int>(p.dr / kFK), lds, 4 * wa, 4 * wb, wave, lane);
+    for (int j = 0; j < MJ; ++j) acc[i][j] = f32x16_t{};
+  fgemm_loop(acc, A, B, 0, static_cast<int>(p.dr / kFK), lds, 4 * wa, MJ * wb, wave, lane);
 
   // element v of accumulator (i, j): unit 128 wa + 32 i + 8 (v / 4) + 4 h + v % 4
-  // of the tile, token 128 wb + 32 j + u
+  // of the tile, token 32 (MJ wb + j) + u
   const int64_t nleft = p.N - (u0 + 128 * wa + 4 * h);  // units of this wave-row left in the pool
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t t = v0 + 128 * wb + 32 * j + u;
+  for (int j = 0; j < MJ; ++j) {
+    const int64_t t = v0 + 32 * (MJ * wb + j) + u;
     float* srow = p.S + (t < p.Tv ? t : 0) * p.N64;
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
@@ -314,10 +321,13 @@ struct FGateParams {
   uint32_t* mask32;   // [Tv][mask_words32] or null
   int64_t mask_words32;
   int64_t Tv, N, N64, D;
-  int routes, RT, CT;
+  int routes, RT, CT;  // this launch: token tiles, unit tiles
+  int ct0;             // this launch's first unit tile
   GateParams gp;
 };
 
+// tiles as f32_stats_kernel's
+template <int MJ>
 __global__ __launch_bounds__(kFThreads, 1) void f32_gate_kernel(FGateParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
@@ -325,16 +335,17 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_gate_kernel(FGateParams p) {
   const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
   int rt, ct;
   if (!ftile_of(p.RT, p.CT, rt, ct)) return;
-  const int64_t u0 = static_cast<int64_t>(ct) * kFRows, v0 = static_cast<int64_t>(rt) * kFRows;
-  f32x16_t acc[4][4];
+  ct += p.ct0;
+  const int64_t u0 = static_cast<int64_t>(ct) * kFRows, v0 = static_cast<int64_t>(rt) * 64 * MJ;
+  f32x16_t acc[4][MJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < MJ; ++j) acc[i][j] = f32x16_t{};
   {
-    const FOpnd<8> A = make_fopnd(p.read, p.D, u0, p.N, 1, wave, lane);
-    const FOpnd<8> B = make_fopnd(p.x, p.D, v0, p.Tv, p.routes, wave, lane);
-    fgemm_loop(acc, A, B, 0, static_cast<int>(p.D / kFK), lds, 4 * wa, 4 * wb, wave, lane);
+    const FOpnd<8> A = make_fopnd<8>(p.read, p.D, u0, p.N, 1, wave, lane);
+    const FOpnd<2 * MJ> B = make_fopnd<2 * MJ>(p.x, p.D, v0, p.Tv, p.routes, wave, lane);
+    fgemm_loop(acc, A, B, 0, static_cast<int>(p.D / kFK), lds, 4 * wa, MJ * wb, wave, lane);
   }
 
   // gate epilogue (v41:1723-1735) in the reference's fp32 expression order;
@@ -342,8 +353,8 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_gate_kernel(FGateParams p) {
   const int64_t nleft = p.N - (u0 + 128 * wa + 4 * h);  // units of this wave-row left in the pool
   const float k_exp2 = -p.gp.sharp * 1.4426950408889634f;   // e^(-sharpness m) = 2^(m k_exp2)
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t t = v0 + 128 * wb + 32 * j + u;
+  for (int j = 0; j < MJ; ++j) {
+    const int64_t t = v0 + 32 * (MJ * wb + j) + u;
     const bool tok = t < p.Tv;
     float* prow = p.P + (tok ? t : p.Tv - 1) * p.N64;
     const float tau = p.tau[tok ? t : p.Tv - 1];
@@ -519,6 +530,7 @@ __global__ __launch_bounds__(256) void f32_final_kernel(FFinalParams p) {
 struct FGeo {
   int64_t Tv, N, N64;
   int RT, CT, nkb;
+  int CTa, RTq;           // score / gate kernels: unit tiles in whole rounds of 256-token tiles; 64-token tiles
   bool w384;              // write tiles of 128 tokens x 384 columns (else 256 x 256)
   int WRT, DT, S, W8;     // write: token tiles, column tiles, splits, pairs per XCD
 };
@@ -533,6 +545,18 @@ FGeo fgeo(const srw_desc_t& d) {
   g.RT = static_cast<int>((g.Tv + kFRows - 1) / kFRows);
   g.CT = static_cast<int>((g.N + kFRows - 1) / kFRows);
   g.nkb = static_cast<int>(g.N64 / kFK);
+  // score and gate kernels: 256-unit x 256-token tiles, one workgroup per CU;
+  // when the last round would run less than half the CUs, its unit tiles go
+  // to a second launch in 64-token tiles (four times as many workgroups of a
+  // quarter of the work); fewer tiles than CUs: all in 64-token tiles
+  g.RTq = static_cast<int>((g.Tv + 63) / 64);
+  {
+    const int64_t F = static_cast<int64_t>(g.RT) * g.CT, rem = F % 256;
+    int64_t tail = 0;
+    if (F < 256) tail = g.CT;
+    else if (rem > 0 && rem <= 128) tail = (rem + g.RT - 1) / g.RT;
+    g.CTa = static_cast<int>(g.CT - (tail < g.CT ? tail : g.CT));
+  }
   // write tile shape: the one that pads fewer output columns, 256 wide on a tie
   const int64_t D = d.d_model, pad256 = (D + 255) / 256 * 256 - D, pad384 = (D + 383) / 384 * 384 - D;
   g.w384 = pad384 < pad256;
@@ -600,8 +624,10 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   const int D = static_cast<int>(d.d_model);
   hipError_t e;
   static_assert(kFGemmLds <= 160 * 1024, "LDS per workgroup");
-  for (const void* fn : {reinterpret_cast<const void*>(f32_stats_kernel),
-                         reinterpret_cast<const void*>(f32_gate_kernel),
+  for (const void* fn : {reinterpret_cast<const void*>(f32_stats_kernel<4>),
+                         reinterpret_cast<const void*>(f32_stats_kernel<1>),
+                         reinterpret_cast<const void*>(f32_gate_kernel<4>),
+                         reinterpret_cast<const void*>(f32_gate_kernel<1>),
                          reinterpret_cast<const void*>(f32_write_kernel<8, 8, 4, 4>),
                          reinterpret_cast<const void*>(f32_write_kernel<4, 12, 4, 3>)})
     if ((e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kFGemmLds)) != hipSuccess) return e;
@@ -612,7 +638,9 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
                        wt, g.N, g.N64, D);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  const unsigned grid_rc = static_cast<unsigned>(8 * g.RT * ((g.CT + 7) / 8));
+  // the unit tiles [0, CTa) in 256-token tiles, [CTa, CT) in 64-token tiles
+  auto grid_of = [](int rt, int ct) { return dim3(static_cast<unsigned>(8 * rt * ((ct + 7) / 8))); };
+  constexpr size_t kLdsQ = 2 * (8 + 2) * kFGroupBytes;  // two stages of 256 + 64 operand rows
   FStatsParams sp{};
   sp.h = static_cast<const float*>(a.in.h);
   sp.emb = static_cast<const float*>(a.in.emb);
@@ -622,10 +650,20 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   sp.N = g.N;
   sp.N64 = g.N64;
   sp.dr = d.d_route;
-  sp.RT = g.RT;
-  sp.CT = g.CT;
-  hipLaunchKernelGGL(f32_stats_kernel, dim3(grid_rc), dim3(kFThreads), kFGemmLds, a.stream, sp);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (g.CTa > 0) {
+    sp.RT = g.RT;
+    sp.CT = g.CTa;
+    sp.ct0 = 0;
+    hipLaunchKernelGGL(f32_stats_kernel<4>, grid_of(sp.RT, sp.CT), dim3(kFThreads), kFGemmLds, a.stream, sp);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (g.CTa < g.CT) {
+    sp.RT = g.RTq;
+    sp.CT = g.CT - g.CTa;
+    sp.ct0 = g.CTa;
+    hipLaunchKernelGGL(f32_stats_kernel<1>, grid_of(sp.RT, sp.CT), dim3(kFThreads), kLdsQ, a.stream, sp);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   int S_st = 2 * g.CT;
   if (d.stats_mode == SRW_STATS_CENTERED) {
     // row means, then sum (s - mean)^2 over the stored scores into mom[0][t]
@@ -653,13 +691,23 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   gp.N64 = g.N64;
   gp.D = D;
   gp.routes = d.n_routes;
-  gp.RT = g.RT;
-  gp.CT = g.CT;
   gp.gp = a.gp;
   dominant_kernel_begin(a.stream);
-  hipLaunchKernelGGL(f32_gate_kernel, dim3(grid_rc), dim3(kFThreads), kFGemmLds, a.stream, gp);
+  if (g.CTa > 0) {
+    gp.RT = g.RT;
+    gp.CT = g.CTa;
+    gp.ct0 = 0;
+    hipLaunchKernelGGL(f32_gate_kernel<4>, grid_of(gp.RT, gp.CT), dim3(kFThreads), kFGemmLds, a.stream, gp);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (g.CTa < g.CT) {
+    gp.RT = g.RTq;
+    gp.CT = g.CT - g.CTa;
+    gp.ct0 = g.CTa;
+    hipLaunchKernelGGL(f32_gate_kernel<1>, grid_of(gp.RT, gp.CT), dim3(kFThreads), kLdsQ, a.stream, gp);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   dominant_kernel_end(a.stream);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
 
   FWriteParams wp{};
   wp.P = P;
