@@ -1815,6 +1815,7 @@ struct TauParams {
   float* token_diag;
   int mode;
   float* sstd;  // [T] s_std per row, or null
+  int upp;      // kTauChan: units per partial
 };
 __device__ __attribute__((always_inline)) inline void tau_body(const TauParams& q, const int bid) {
   const float* __restrict__ mom = q.mom;
@@ -1839,6 +1840,20 @@ __device__ __attribute__((always_inline)) inline void tau_body(const TauParams& 
     }
   }
   a = wave_sum(a);
+  if (mode == kTauChan) {
+    // between-partial term of the merged centred sum of squares, about the
+    // row mean (b holds the partials' own centred sums)
+    const float mean = a / static_cast<float>(N);
+#pragma unroll 8
+    for (int s = lane; s < S_st; s += 64) {
+      const int64_t left = N - static_cast<int64_t>(s) * q.upp;
+      const float n = static_cast<float>(left <= 0 ? 0 : (left < q.upp ? left : q.upp));
+      if (n > 0.f) {
+        const float dm = mom[(static_cast<int64_t>(s) * T + t) * ms] / n - mean;
+        b += n * dm * dm;
+      }
+    }
+  }
   b = wave_sum(b);
   if (token_diag && ms == 4) {
     c = wave_sum(c);
@@ -1851,7 +1866,8 @@ __device__ __attribute__((always_inline)) inline void tau_body(const TauParams& 
       tau[t] = mean;
       return;
     }
-    const float sd = (mode == kTauCentered ? sqrtf(b / fN) : sqrtf(b / fN - __fmul_rn(mean, mean))) + 1e-8f;
+    const float sd =
+        (mode == kTauCentered || mode == kTauChan ? sqrtf(b / fN) : sqrtf(b / fN - __fmul_rn(mean, mean))) + 1e-8f;
     const float tv = mean + __fmul_rn(tau_off[t], sd);
     tau[t] = tv;
     if (q.sstd) q.sstd[t] = sd;
@@ -2985,8 +3001,9 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
 }
 
 hipError_t launch_tau(const float* mom, const float* tau_off, float* tau, int64_t T, int S_st, int64_t N, int ms,
-                      float* token_diag, int mode, hipStream_t s, float* sstd) {
-  const TauParams q{mom, tau_off, tau, T, S_st, N, ms, token_diag, mode, sstd};
+                      float* token_diag, int mode, hipStream_t s, float* sstd, int upp) {
+  if (mode == kTauChan && upp <= 0) return hipErrorInvalidValue;
+  const TauParams q{mom, tau_off, tau, T, S_st, N, ms, token_diag, mode, sstd, upp};
   hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, s, q);
   return hipGetLastError();
 }

@@ -9,9 +9,10 @@
 //
 //   pack   W [N, D] -> W^T [D, N64] (unit-contiguous rows, zero tail)
 //   stats  S = E.H^T per 256-unit x 256-token tile, stored as S [T, N64]
-//          fp32 (v41:1717-1718); per-token partials sum s, sum s^2
-//   centre (centred statistics) sum (s - mean)^2 from the stored S
-//          (v41:1719-1721)
+//          fp32 (v41:1717-1718); per token and 128 units: sum s and sum
+//          s^2, or (centred statistics) sum (s - their mean)^2 from the
+//          registers, which the tau kernel merges into the row's centred
+//          sum of squares (v41:1719-1721) without a second pass over S
 //   gate   per tile XR = R.X^T, the v4.1 gate of the stored scores in the
 //          reference's fp32 expression order (v41:1723-1728), P = gate * xr
 //          over S in place (v41:1735); per-token
@@ -211,10 +212,11 @@ struct FStatsParams {
   const float* h;    // [Tv, dr]
   const float* emb;  // [N, dr]
   float* S;          // [Tv, N64] fp32 scores (zero for units >= N)
-  float* mom;        // [2 CT][Tv][2]
+  float* mom;        // [2 CT][Tv][2]: per 128 units (sum s, sum s^2), or (sum s, sum (s - their mean)^2)
   int64_t Tv, N, N64, dr;
-  int RT, CT;  // this launch: token tiles, unit tiles
-  int ct0;     // this launch's first unit tile
+  int RT, CT;    // this launch: token tiles, unit tiles
+  int ct0;       // this launch's first unit tile
+  int centred;   // second moments about the 128 units' own mean (merged by srw_tau_kernel's kTauChan)
 };
 
 // A workgroup takes 256 units x 64 MJ tokens (2 x 2 waves of 128 units x
@@ -271,41 +273,28 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_stats_kernel(FStatsParams p)
       }
     }
     s1 += __shfl_xor(s1, 32);
+    if (p.centred) {
+      // sum (s - mean)^2 over these units, their mean from s1 (v41:1719-1721
+      // over a 128-unit slice; the slices merge exactly in srw_tau_kernel)
+      const int64_t nrow = p.N - (u0 + 128 * wa);
+      const float n = static_cast<float>(nrow <= 0 ? 0 : (nrow < 128 ? nrow : 128));
+      const float mu = n > 0.f ? s1 / n : 0.f;
+      s2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = 32 * i + 8 * (v >> 2) + (v & 3);
+          const float d = r < nleft ? acc[i][j][v] - mu : 0.f;
+          s2 += d * d;
+        }
+    }
     s2 += __shfl_xor(s2, 32);
     if (h == 0 && t < p.Tv) {
       float* m = p.mom + ((static_cast<int64_t>(2 * ct + wa)) * p.Tv + t) * 2;
       m[0] = s1;
       m[1] = s2;
     }
-  }
-}
-
-// centred second moments of the stored scores: mom[t] = (sum s, sum (s - mean)^2)
-// over the N units of row t (v41:1719-1721); one wave per row
-__global__ __launch_bounds__(256) void f32_centre_kernel(const float* __restrict__ S, const float* __restrict__ mean,
-                                                         float* __restrict__ mom, int64_t Tv, int64_t N, int64_t N64) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (t >= Tv) return;
-  const float mu = mean[t];
-  const float* row = S + t * N64;
-  float s1 = 0.f, s2 = 0.f;
-  for (int64_t n0 = 4 * lane; n0 < N; n0 += 256) {
-    const float4 q = *reinterpret_cast<const float4*>(row + n0);
-    const float e[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const bool ok = n0 + k < N;
-      const float d = ok ? e[k] - mu : 0.f;
-      s1 += ok ? e[k] : 0.f;
-      s2 += d * d;
-    }
-  }
-  s1 = wave_sum(s1);
-  s2 = wave_sum(s2);
-  if (lane == 0) {
-    mom[2 * t] = s1;
-    mom[2 * t + 1] = s2;
   }
 }
 
@@ -650,6 +639,7 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   sp.N = g.N;
   sp.N64 = g.N64;
   sp.dr = d.d_route;
+  sp.centred = d.stats_mode == SRW_STATS_CENTERED;
   if (g.CTa > 0) {
     sp.RT = g.RT;
     sp.CT = g.CTa;
@@ -664,18 +654,11 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
     hipLaunchKernelGGL(f32_stats_kernel<1>, grid_of(sp.RT, sp.CT), dim3(kFThreads), kLdsQ, a.stream, sp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  int S_st = 2 * g.CT;
-  if (d.stats_mode == SRW_STATS_CENTERED) {
-    // row means, then sum (s - mean)^2 over the stored scores into mom[0][t]
-    if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, S_st, g.N, 2, nullptr, kTauMean, a.stream)) != hipSuccess)
-      return e;
-    hipLaunchKernelGGL(f32_centre_kernel, dim3(static_cast<unsigned>((g.Tv + 3) / 4)), dim3(256), 0, a.stream, P, tau,
-                       mom, g.Tv, g.N, g.N64);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    S_st = 1;
-  }
-  if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, S_st, g.N, 2, nullptr,
-                      d.stats_mode == SRW_STATS_CENTERED ? kTauCentered : kTauOnePass, a.stream)) != hipSuccess)
+  // tau per row from the 2 CT partials of 128 units (centred: merged by
+  // Chan's formula, no second pass over the stored scores)
+  if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, 2 * g.CT, g.N, 2, nullptr,
+                      d.stats_mode == SRW_STATS_CENTERED ? kTauChan : kTauOnePass, a.stream, nullptr, 128)) !=
+      hipSuccess)
     return e;
 
   FGateParams gp{};
