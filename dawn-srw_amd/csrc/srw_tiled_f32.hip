@@ -21,11 +21,12 @@
 //   final  out = sum of the partials / max(sum intensity, 1) * scale in fp32
 //          (v41:1736-1737)
 //
-// The GEMM main loop: a 256 x 256 output tile per workgroup (4 waves as 2 x
-// 2, 128 x 128 = 16 accumulators of 32 x 32 each), operands K-contiguous in
-// memory, 32-wide k blocks (one 128-byte line per row) in a double-buffered
-// LDS ring filled by direct global->LDS loads, 16-byte pieces XOR-swizzled by
-// row.  In the 32 x 32 x 2 MFMA the lanes of half h supply k index h of the
+// The GEMM main loop (fgemm_loop): an output tile of 32 GA x 32 GB per
+// workgroup of 4 waves (256 units x 64 tokens in the score and gate kernels,
+// 128 tokens x 192 or 256 x 256 columns in the write kernel), operands
+// K-contiguous in memory, 32-wide k blocks (one 128-byte line per row) in a
+// double-buffered LDS ring filled by direct global->LDS loads, 16-byte
+// pieces XOR-swizzled by row.  In the 32 x 32 x 2 MFMA the lanes of half h supply k index h of the
 // step; here step s of a k block takes k = s from half 0 and k = 16 + s from
 // half 1 (any assignment of k to (step, half) shared by both operands gives
 // the same sum), so a lane's 16 steps read 64 contiguous bytes of its row:
@@ -214,15 +215,16 @@ struct FStatsParams {
   float* S;          // [Tv, N64] fp32 scores (zero for units >= N)
   float* mom;        // [2 CT][Tv][2]: per 128 units (sum s, sum s^2), or (sum s, sum (s - their mean)^2)
   int64_t Tv, N, N64, dr;
-  int RT, CT;    // this launch: token tiles, unit tiles
-  int ct0;       // this launch's first unit tile
+  int RT, CT;    // token tiles, unit tiles
   int centred;   // second moments about the 128 units' own mean (merged by srw_tau_kernel's kTauChan)
 };
 
 // A workgroup takes 256 units x 64 MJ tokens (2 x 2 waves of 128 units x
-// 32 MJ tokens): MJ = 4 for the rounds that fill every CU, MJ = 1 for the
-// unit tiles of a last, partly filled round (a quarter of the work each, so
-// that round ends four times sooner).
+// 32 MJ tokens).  The launches use MJ = 1: 80 KB of LDS and ~180 registers a
+// wave, so two workgroups share a CU and one's epilogue (the moments and
+// score stores here, the gate and P stores in f32_gate_kernel) runs beside
+// the other's MFMAs -- a wave's own VALU work does not overlap its MFMAs.
+// (256-token tiles, MJ = 4, one workgroup per CU: 5% slower per call.)
 template <int MJ>
 __global__ __launch_bounds__(kFThreads, 1) void f32_stats_kernel(FStatsParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
@@ -231,7 +233,6 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_stats_kernel(FStatsParams p)
   const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
   int rt, ct;
   if (!ftile_of(p.RT, p.CT, rt, ct)) return;
-  ct += p.ct0;
   const int64_t u0 = static_cast<int64_t>(ct) * kFRows, v0 = static_cast<int64_t>(rt) * 64 * MJ;
   const FOpnd<8> A = make_fopnd<8>(p.emb, p.dr, u0, p.N, 1, wave, lane);
   const FOpnd<2 * MJ> B = make_fopnd<2 * MJ>(p.h, p.dr, v0, p.Tv, 1, wave, lane);
@@ -310,8 +311,7 @@ struct FGateParams {
   uint32_t* mask32;   // [Tv][mask_words32] or null
   int64_t mask_words32;
   int64_t Tv, N, N64, D;
-  int routes, RT, CT;  // this launch: token tiles, unit tiles
-  int ct0;             // this launch's first unit tile
+  int routes, RT, CT;  // token tiles, unit tiles
   GateParams gp;
 };
 
@@ -324,7 +324,6 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_gate_kernel(FGateParams p) {
   const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
   int rt, ct;
   if (!ftile_of(p.RT, p.CT, rt, ct)) return;
-  ct += p.ct0;
   const int64_t u0 = static_cast<int64_t>(ct) * kFRows, v0 = static_cast<int64_t>(rt) * 64 * MJ;
   f32x16_t acc[4][MJ];
 #pragma unroll
@@ -408,9 +407,11 @@ struct FWriteParams {
 
 // A workgroup computes a (32 GA tokens) x (32 GB columns) tile of one split's
 // partial; its waves hold MI x MJ MFMA tiles each, GB / MJ waves across the
-// columns.  Shapes: 256 x 256 (GA = GB = 8, 2 x 2 waves) and, for D = 384,
-// 128 x 384 (GA = 4, GB = 12, 1 x 4 waves of 128 x 96) so that no output
-// column is padded and every P tile is read once.
+// columns.  Shapes: 128 x 192 (GA = 4, GB = 6, 2 x 2 waves of 64 x 96: 80 KB
+// of LDS and ~200 registers a wave, two workgroups per CU) where it pads no
+// more output columns than 256 x 256 (GA = GB = 8, 2 x 2 waves of 128 x 128,
+// one workgroup per CU), e.g. D = 384 (128 x 384 tiles, one workgroup per
+// CU: 14% slower).
 template <int GA, int GB, int MI, int MJ>
 __global__ __launch_bounds__(kFThreads, 1) void f32_write_kernel(FWriteParams p) {
   static_assert(GA % MI == 0 && GB % MJ == 0 && (GA / MI) * (GB / MJ) == kFThreads / 64,
@@ -518,9 +519,9 @@ __global__ __launch_bounds__(256) void f32_final_kernel(FFinalParams p) {
 // ---------------------------------------------------------------------------
 struct FGeo {
   int64_t Tv, N, N64;
-  int RT, CT, nkb;
-  int CTa, RTq;           // score / gate kernels: unit tiles in whole rounds of 256-token tiles; 64-token tiles
-  bool w384;              // write tiles of 128 tokens x 384 columns (else 256 x 256)
+  int CT, nkb;
+  int RTq;                // score / gate kernels: 64-token tiles
+  bool w192;              // write tiles of 128 tokens x 192 columns (else 256 x 256)
   int WRT, DT, S, W8;     // write: token tiles, column tiles, splits, pairs per XCD
 };
 
@@ -531,25 +532,13 @@ FGeo fgeo(const srw_desc_t& d) {
   g.Tv = d.T * d.n_routes;
   g.N = d.n_units;
   g.N64 = (g.N + kFNAlign - 1) / kFNAlign * kFNAlign;
-  g.RT = static_cast<int>((g.Tv + kFRows - 1) / kFRows);
   g.CT = static_cast<int>((g.N + kFRows - 1) / kFRows);
   g.nkb = static_cast<int>(g.N64 / kFK);
-  // score and gate kernels: 256-unit x 256-token tiles, one workgroup per CU;
-  // when the last round would run less than half the CUs, its unit tiles go
-  // to a second launch in 64-token tiles (four times as many workgroups of a
-  // quarter of the work); fewer tiles than CUs: all in 64-token tiles
-  g.RTq = static_cast<int>((g.Tv + 63) / 64);
-  {
-    const int64_t F = static_cast<int64_t>(g.RT) * g.CT, rem = F % 256;
-    int64_t tail = 0;
-    if (F < 256) tail = g.CT;
-    else if (rem > 0 && rem <= 128) tail = (rem + g.RT - 1) / g.RT;
-    g.CTa = static_cast<int>(g.CT - (tail < g.CT ? tail : g.CT));
-  }
-  // write tile shape: the one that pads fewer output columns, 256 wide on a tie
-  const int64_t D = d.d_model, pad256 = (D + 255) / 256 * 256 - D, pad384 = (D + 383) / 384 * 384 - D;
-  g.w384 = pad384 < pad256;
-  const int wr = g.w384 ? 128 : 256, wc = g.w384 ? 384 : 256;
+  g.RTq = static_cast<int>((g.Tv + 63) / 64);  // score and gate kernels: 256-unit x 64-token tiles
+  // write tile shape: 192 wide unless that pads more output columns
+  const int64_t D = d.d_model, pad256 = (D + 255) / 256 * 256 - D, pad192 = (D + 191) / 192 * 192 - D;
+  g.w192 = pad192 <= pad256;
+  const int wr = g.w192 ? 128 : 256, wc = g.w192 ? 192 : 256;
   g.WRT = static_cast<int>((g.Tv + wr - 1) / wr);
   g.DT = static_cast<int>((D + wc - 1) / wc);
   // splits of the write GEMM: enough workgroups for 256 CUs, each at least
@@ -613,12 +602,10 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   const int D = static_cast<int>(d.d_model);
   hipError_t e;
   static_assert(kFGemmLds <= 160 * 1024, "LDS per workgroup");
-  for (const void* fn : {reinterpret_cast<const void*>(f32_stats_kernel<4>),
-                         reinterpret_cast<const void*>(f32_stats_kernel<1>),
-                         reinterpret_cast<const void*>(f32_gate_kernel<4>),
+  for (const void* fn : {reinterpret_cast<const void*>(f32_stats_kernel<1>),
                          reinterpret_cast<const void*>(f32_gate_kernel<1>),
                          reinterpret_cast<const void*>(f32_write_kernel<8, 8, 4, 4>),
-                         reinterpret_cast<const void*>(f32_write_kernel<4, 12, 4, 3>)})
+                         reinterpret_cast<const void*>(f32_write_kernel<4, 6, 2, 3>)})
     if ((e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kFGemmLds)) != hipSuccess) return e;
 
   if (!(d.flags & SRW_FLAG_POOL_CACHED)) {
@@ -627,9 +614,9 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
                        wt, g.N, g.N64, D);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
-  // the unit tiles [0, CTa) in 256-token tiles, [CTa, CT) in 64-token tiles
-  auto grid_of = [](int rt, int ct) { return dim3(static_cast<unsigned>(8 * rt * ((ct + 7) / 8))); };
-  constexpr size_t kLdsQ = 2 * (8 + 2) * kFGroupBytes;  // two stages of 256 + 64 operand rows
+  // score and gate kernels: 256-unit x 64-token tiles, two stages of 256 + 64 operand rows
+  const dim3 grid_q(static_cast<unsigned>(8 * g.RTq * ((g.CT + 7) / 8)));
+  constexpr size_t kLdsQ = 2 * (8 + 2) * kFGroupBytes;
   FStatsParams sp{};
   sp.h = static_cast<const float*>(a.in.h);
   sp.emb = static_cast<const float*>(a.in.emb);
@@ -640,20 +627,10 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   sp.N64 = g.N64;
   sp.dr = d.d_route;
   sp.centred = d.stats_mode == SRW_STATS_CENTERED;
-  if (g.CTa > 0) {
-    sp.RT = g.RT;
-    sp.CT = g.CTa;
-    sp.ct0 = 0;
-    hipLaunchKernelGGL(f32_stats_kernel<4>, grid_of(sp.RT, sp.CT), dim3(kFThreads), kFGemmLds, a.stream, sp);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  if (g.CTa < g.CT) {
-    sp.RT = g.RTq;
-    sp.CT = g.CT - g.CTa;
-    sp.ct0 = g.CTa;
-    hipLaunchKernelGGL(f32_stats_kernel<1>, grid_of(sp.RT, sp.CT), dim3(kFThreads), kLdsQ, a.stream, sp);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
+  sp.RT = g.RTq;
+  sp.CT = g.CT;
+  hipLaunchKernelGGL(f32_stats_kernel<1>, grid_q, dim3(kFThreads), kLdsQ, a.stream, sp);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
   // tau per row from the 2 CT partials of 128 units (centred: merged by
   // Chan's formula, no second pass over the stored scores)
   if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, 2 * g.CT, g.N, 2, nullptr,
@@ -676,21 +653,11 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   gp.routes = d.n_routes;
   gp.gp = a.gp;
   dominant_kernel_begin(a.stream);
-  if (g.CTa > 0) {
-    gp.RT = g.RT;
-    gp.CT = g.CTa;
-    gp.ct0 = 0;
-    hipLaunchKernelGGL(f32_gate_kernel<4>, grid_of(gp.RT, gp.CT), dim3(kFThreads), kFGemmLds, a.stream, gp);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  if (g.CTa < g.CT) {
-    gp.RT = g.RTq;
-    gp.CT = g.CT - g.CTa;
-    gp.ct0 = g.CTa;
-    hipLaunchKernelGGL(f32_gate_kernel<1>, grid_of(gp.RT, gp.CT), dim3(kFThreads), kLdsQ, a.stream, gp);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
+  gp.RT = g.RTq;
+  gp.CT = g.CT;
+  hipLaunchKernelGGL(f32_gate_kernel<1>, grid_q, dim3(kFThreads), kLdsQ, a.stream, gp);
   dominant_kernel_end(a.stream);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
 
   FWriteParams wp{};
   wp.P = P;
@@ -705,8 +672,9 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   wp.nkb = g.nkb;
   wp.W8 = g.W8;
   const unsigned grid_w = static_cast<unsigned>(8 * g.DT * g.W8);
-  if (g.w384)
-    hipLaunchKernelGGL((f32_write_kernel<4, 12, 4, 3>), dim3(grid_w), dim3(kFThreads), kFGemmLds, a.stream, wp);
+  if (g.w192)
+    hipLaunchKernelGGL((f32_write_kernel<4, 6, 2, 3>), dim3(grid_w), dim3(kFThreads), 2 * (4 + 6) * kFGroupBytes,
+                       a.stream, wp);
   else
     hipLaunchKernelGGL((f32_write_kernel<8, 8, 4, 4>), dim3(grid_w), dim3(kFThreads), kFGemmLds, a.stream, wp);
   if ((e = hipGetLastError()) != hipSuccess) return e;
