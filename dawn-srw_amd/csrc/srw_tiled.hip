@@ -8,10 +8,10 @@
 //
 //   pack   W [N, D] -> W^T [D, N64] (unit-contiguous rows, zero tail)
 //   stats  S = E.H^T per 256-unit x 256-token tile, rounded to bf16
-//          (v41:439) and stored as S [T, N64] bf16; per-token partials sum s
-//          and sum s^2 (v41:441-442)
-//   centre (_srw_inference only) sum (s - mean)^2 streamed from the stored S
-//          (v41:1719-1721)
+//          (v41:439) and stored as S [T, N64] bf16; per token and 128 units
+//          sum s and sum s^2 (v41:441-442), or (_srw_inference) sum
+//          (s - their mean)^2, merged by the tau kernel into the row's
+//          centred sum of squares (v41:1719-1721)
 //   gate   per tile: XR = R.X^T, the v4.1 gate of the stored scores
 //          (v41:506-511) and P = bf16(bf16(g) * bf16(xr)) (v41:516-518),
 //          written over S in place; the pass bits and per-token sum gate /
@@ -195,9 +195,10 @@ struct TStatsParams {
   const uint16_t* h;    // [Tv, dr]
   const uint16_t* emb;  // [N, dr]
   uint16_t* S;          // [Tv, N64] bf16 scores (zero for units >= N)
-  float* mom;           // [2 CT][Tv][2]
+  float* mom;           // [2 CT][Tv][2]: per 128 units (sum s, sum s^2), or (sum s, sum (s - their mean)^2)
   int64_t Tv, N, N64, dr;
   int RT, CT;
+  int centred;          // second moments about the 128 units' own mean (merged by srw_tau_kernel's kTauChan)
 };
 
 __global__ __launch_bounds__(kGThreads) void tiled_stats_kernel(TStatsParams p) {
@@ -251,42 +252,30 @@ __global__ __launch_bounds__(kGThreads) void tiled_stats_kernel(TStatsParams p) 
       __builtin_amdgcn_sched_barrier(0);
     }
     s1 += __shfl_xor(s1, 32);
+    if (p.centred) {
+      // sum (s - mean)^2 over these units' bf16 scores, their mean from s1
+      // (v41:1719-1721 over a 128-unit slice; merged in srw_tau_kernel)
+      const int64_t nrow = p.N - (u0 + 128 * wa);
+      const float n = static_cast<float>(nrow <= 0 ? 0 : (nrow < 128 ? nrow : 128));
+      const float mu = n > 0.f ? s1 / n : 0.f;
+      s2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) {
+          const uint32_t sp = pack_bf16(acc[i][j][v], acc[i][j][v + 1]);
+          const int r = 32 * i + 8 * (v >> 2) + (v & 3);
+          const float da = r < nleft ? lo_f32(sp) - mu : 0.f, db = r + 1 < nleft ? hi_f32(sp) - mu : 0.f;
+          s2 += __fmul_rn(da, da);
+          s2 += __fmul_rn(db, db);
+        }
+    }
     s2 += __shfl_xor(s2, 32);
     if (h == 0 && t < p.Tv) {
       float* m = p.mom + ((static_cast<int64_t>(2 * ct + wa)) * p.Tv + t) * 2;
       m[0] = s1;
       m[1] = s2;
     }
-  }
-}
-
-// centred second moments of the stored scores: mom[t] = (sum s, sum (s - mean)^2)
-// over the N units of row t (v41:1719-1721); one wave per row
-__global__ __launch_bounds__(256) void tiled_centre_kernel(const uint16_t* __restrict__ S,
-                                                           const float* __restrict__ mean, float* __restrict__ mom,
-                                                           int64_t Tv, int64_t N, int64_t N64) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (t >= Tv) return;
-  const float mu = mean[t];
-  const uint16_t* row = S + t * N64;
-  float s1 = 0.f, s2 = 0.f;
-  for (int64_t n0 = 8 * lane; n0 < N; n0 += 512) {
-    const u32x4_t q = *reinterpret_cast<const u32x4_t*>(row + n0);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float s = (k & 1) ? hi_f32(q[k >> 1]) : lo_f32(q[k >> 1]);
-      const bool ok = n0 + k < N;
-      const float d = ok ? s - mu : 0.f;
-      s1 += ok ? s : 0.f;
-      s2 += __fmul_rn(d, d);
-    }
-  }
-  s1 = wave_sum(s1);
-  s2 = wave_sum(s2);
-  if (lane == 0) {
-    mom[2 * t] = s1;
-    mom[2 * t + 1] = s2;
   }
 }
 
@@ -671,20 +660,14 @@ hipError_t tiled_forward(const LaunchArgs& a) {
   sp.dr = d.d_route;
   sp.RT = g.RT;
   sp.CT = g.CT;
+  sp.centred = d.stats_mode == SRW_STATS_CENTERED;
   hipLaunchKernelGGL(tiled_stats_kernel, dim3(grid_rc), dim3(kGThreads), kGemmLds, a.stream, sp);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  int S_st = 2 * g.CT;
-  if (d.stats_mode == SRW_STATS_CENTERED) {
-    // row means, then sum (s - mean)^2 over the stored scores into mom[0][t]
-    if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, S_st, g.N, 2, nullptr, kTauMean, a.stream)) != hipSuccess)
-      return e;
-    hipLaunchKernelGGL(tiled_centre_kernel, dim3(static_cast<unsigned>((g.Tv + 3) / 4)), dim3(256), 0, a.stream, P,
-                       tau, mom, g.Tv, g.N, g.N64);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    S_st = 1;
-  }
-  if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, S_st, g.N, 2, nullptr,
-                      d.stats_mode == SRW_STATS_CENTERED ? kTauCentered : kTauOnePass, a.stream)) != hipSuccess)
+  // tau per row from the 2 CT partials of 128 units (centred: merged by
+  // Chan's formula, no second pass over the stored scores)
+  if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, 2 * g.CT, g.N, 2, nullptr,
+                      d.stats_mode == SRW_STATS_CENTERED ? kTauChan : kTauOnePass, a.stream, nullptr, 128)) !=
+      hipSuccess)
     return e;
 
   TGateParams gp{};
