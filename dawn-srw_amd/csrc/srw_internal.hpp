@@ -60,15 +60,15 @@ hipError_t gram_moments(const uint16_t* emb, const uint16_t* h, int64_t T, int64
                         bool pool_cached);
 
 // Per-row tau from moment partials mom[S_st][T][ms] (srw_mfma.hip).
-// kTauOnePass: std = sqrt(E[s^2] - mean^2) + 1e-8 (v41:461-462); kTauMean:
-// stores the row mean in tau[] (input of a centred second pass);
-// kTauCentered: std = sqrt(sum (s - mean)^2 / N) + 1e-8 (v41:1719-1721);
-// kTauChan: the same std from per-partial (sum s, sum (s - partial mean)^2)
+// kTauOnePass: std = sqrt(E[s^2] - mean^2) + 1e-8 (v41:461-462);
+// kTauChan: the centred std = sqrt(sum (s - mean)^2 / N) + 1e-8
+// (v41:1719-1721) from per-partial (sum s, sum (s - partial mean)^2)
 // over upp consecutive units each (partial i: units [upp i, upp i + upp) of
-// the N), merged by Chan et al.'s parallel formula M2 = sum M2_i + sum n_i
-// (mean_i - mean)^2 -- the centred sum of squares without a second pass
-// over the scores.
-enum TauMode { kTauOnePass = 0, kTauMean = 1, kTauCentered = 2, kTauChan = 3 };
+// the N; upp = 0: the partial's count in its third float, ms = 3), merged
+// by Chan et al.'s parallel formula M2 = sum M2_i + sum n_i (mean_i -
+// mean)^2 -- the centred sum of squares without a second pass over the
+// scores.
+enum TauMode { kTauOnePass = 0, kTauChan = 3 };
 // sstd (or null): the row's s_std as well (the v4.0.1 gate's z scale).
 hipError_t launch_tau(const float* mom, const float* tau_off, float* tau, int64_t T, int S_st, int64_t N, int ms,
                       float* token_diag, int mode, hipStream_t s, float* sstd = nullptr, int upp = 0);

@@ -240,8 +240,7 @@ __global__ __launch_bounds__(256) void pack_w_kernel(const uint16_t* __restrict_
 struct StatsParams {
   const uint16_t* h;   // [T, dr]
   const uint16_t* emb; // [N, dr]
-  const float* mean;   // [T] row means (second pass of the centred moments) or null
-  float* mom;          // [S][T][2 or 4]
+  float* mom;          // [S][T][2, 3 or 4]
   uint32_t* mask32;    // pass bitmask as uint32 words [T][mask_words32] (may be null)
   int64_t mask_words32;
   Geometry g;
@@ -259,17 +258,21 @@ __host__ __device__ inline int64_t score_tile_off(int ntiles, int64_t ttile, int
 }
 
 // MODE kStatsPlain: sum s, sum s^2 (v41:441-442); kStatsDiag: also sum s^3,
-// s^4 (training diagnostics, v41:442-444; mom stride 4); kStatsCentered: sum
-// s, sum (s - mean)^2 with the row means of a first pass (_srw_inference's
-// two-pass std, v41:1719-1721).
-constexpr int kStatsPlain = 0, kStatsDiag = 1, kStatsCentered = 2;
+// s^4 (training diagnostics, v41:442-444; mom stride 4); kStatsChan: sum s,
+// the sum of squares about the split's own mean and the split's unit count
+// (mom stride 3), for _srw_inference's centred std (v41:1719-1721) in one
+// pass: each tile's sum and sum of squares about the tile mean join the
+// running (count, mean, M2) by Chan et al.'s pairwise update, and
+// srw_tau_kernel merges the splits the same way.
+constexpr int kStatsPlain = 0, kStatsDiag = 1, kStatsChan = 3;
 // TBW 32-token blocks per wave (128 TBW tokens per workgroup): each E
 // fragment read from LDS feeds TBW MFMAs, and a CU's E stream serves
 // 128 TBW tokens.
 template <int KH, int MODE, int TBW>
 __device__ __attribute__((always_inline)) inline void stats_body(const StatsParams& p, const int bid) {
   constexpr bool DG = MODE == kStatsDiag;
-  constexpr int MS = DG ? 4 : 2;
+  constexpr bool CHAN = MODE == kStatsChan;
+  constexpr int MS = DG ? 4 : (CHAN ? 3 : 2);
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int STAGE = KH * kFragBytes;
   constexpr int DR = KH * 16;
@@ -304,13 +307,11 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
   }
 
   u32x4_t hq[TBW][KH];
-  float mu[TBW];
 #pragma unroll
   for (int b = 0; b < TBW; ++b) {
 #pragma unroll
     for (int ks = 0; ks < KH; ++ks)
       hq[b][ks] = *reinterpret_cast<const u32x4_t*>(p.h + tl[b] * DR + 16 * ks + 8 * half);
-    mu[b] = MODE == kStatsCentered ? p.mean[tl[b]] : 0.f;
   }
 
   using TileE = RowTile<KH>;
@@ -324,14 +325,15 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
   for (int m = 0; m < TileE::NM; ++m) le[m] = TileE::lane_off(lane, m);
 
   float s1[TBW], s2[TBW], s3[TBW], s4[TBW];
+  float cn[TBW], cmean[TBW];  // kStatsChan: the running unit count and mean (s1: sum, s2: M2, both lane halves)
 #pragma unroll
-  for (int b = 0; b < TBW; ++b) s1[b] = s2[b] = s3[b] = s4[b] = 0.f;
+  for (int b = 0; b < TBW; ++b) s1[b] = s2[b] = s3[b] = s4[b] = cn[b] = cmean[b] = 0.f;
   // score store (plain moments, one block per wave): each tile's packed
   // scores go out at the start of the next tile's MFMAs, so the stores have
   // a whole tile to complete before the end-of-tile vmcnt wait.  A tile that
   // two splits share (a chunk boundary inside it) is stored by the split
   // holding its first unit.
-  constexpr bool STORE = TBW == 1 && (MODE == kStatsPlain || MODE == kStatsDiag);
+  constexpr bool STORE = TBW == 1 && (MODE == kStatsPlain || MODE == kStatsDiag || MODE == kStatsChan);
   uint32_t spd[8];
   char* sdst = nullptr;
   // Non-temporal stores (and loads in the main kernel): 206 MB per Know-pool
@@ -391,6 +393,50 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
       if (p.s_out && u0 >= lo)
         sdst = reinterpret_cast<char*>(p.s_out) + score_tile_off(p.g.ntiles, ttile, tile, wave) + lane * 16;
     }
+    if constexpr (CHAN) {
+      // this tile's units in the split, their sum and sum of squares about
+      // their mean (both lane halves), joined to the running (count, mean, M2)
+      const int64_t c_lo = u0 > lo ? u0 : lo, c_hi = u0 + kUnitTile < hi ? u0 + kUnitTile : hi;
+      const float nt = static_cast<float>(c_hi > c_lo ? c_hi - c_lo : 0);
+#pragma unroll
+      for (int b = 0; b < TBW; ++b) {
+        float xs[16];
+        bool oks[16];
+        float ts = 0.f;
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) {
+          const uint32_t sp = pack_bf16(acc[b][v], acc[b][v + 1]);  // the bf16 scores (v41:503)
+          bool ok0 = true, ok1 = true;
+          if (!full) {
+            const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
+            ok0 = ua >= lo && ua < hi;
+            ok1 = ub >= lo && ub < hi;
+          }
+          xs[v] = ok0 ? lo_f32(sp) : 0.f;
+          xs[v + 1] = ok1 ? hi_f32(sp) : 0.f;
+          oks[v] = ok0;
+          oks[v + 1] = ok1;
+          ts += xs[v];
+          ts += xs[v + 1];
+        }
+        ts += __shfl_xor(ts, 32);
+        if (nt > 0.f) {
+          const float mt = ts / nt;
+          float m2 = 0.f;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float dv = oks[v] ? xs[v] - mt : 0.f;
+            m2 += __fmul_rn(dv, dv);
+          }
+          m2 += __shfl_xor(m2, 32);
+          const float nn = cn[b] + nt, dl = mt - cmean[b];
+          cmean[b] += dl * (nt / nn);
+          s2[b] += m2 + dl * dl * (cn[b] * nt / nn);
+          s1[b] += ts;
+          cn[b] = nn;
+        }
+      }
+    } else {
     // sum s and sum s^2 of a packed bf16 pair in one v_dot2c_f32_bf16 each
     // (the squares of bf16 values are exact in fp32); units outside the
     // split's range enter as zeros
@@ -400,34 +446,24 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
         uint32_t sp = pack_bf16(acc[b][v], acc[b][v + 1]);
-        bool ok0 = true, ok1 = true;
         if (!full) {
           const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
-          ok0 = ua >= lo && ua < hi;
-          ok1 = ub >= lo && ub < hi;
+          const bool ok0 = ua >= lo && ua < hi, ok1 = ub >= lo && ub < hi;
           sp &= (ok0 ? 0x0000ffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
         }
-        const float x0 = lo_f32(sp), x1 = hi_f32(sp);
-        if constexpr (MODE == kStatsCentered) {
-          // squared deviations from the row mean
-          const float d0 = ok0 ? x0 - mu[b] : 0.f, d1 = ok1 ? x1 - mu[b] : 0.f;
-          s1[b] += x0;
-          s2[b] += __fmul_rn(d0, d0);
-          s1[b] += x1;
-          s2[b] += __fmul_rn(d1, d1);
-        } else {
-          const bf16x2_t sb = __builtin_bit_cast(bf16x2_t, sp);
-          s1[b] = __builtin_amdgcn_fdot2_f32_bf16(sb, ones, s1[b], false);
-          s2[b] = __builtin_amdgcn_fdot2_f32_bf16(sb, sb, s2[b], false);
-          if constexpr (DG) {
-            const float q0 = __fmul_rn(x0, x0), q1 = __fmul_rn(x1, x1);
-            s3[b] += __fmul_rn(q0, x0);
-            s4[b] += __fmul_rn(q0, q0);
-            s3[b] += __fmul_rn(q1, x1);
-            s4[b] += __fmul_rn(q1, q1);
-          }
+        const bf16x2_t sb = __builtin_bit_cast(bf16x2_t, sp);
+        s1[b] = __builtin_amdgcn_fdot2_f32_bf16(sb, ones, s1[b], false);
+        s2[b] = __builtin_amdgcn_fdot2_f32_bf16(sb, sb, s2[b], false);
+        if constexpr (DG) {
+          const float x0 = lo_f32(sp), x1 = hi_f32(sp);
+          const float q0 = __fmul_rn(x0, x0), q1 = __fmul_rn(x1, x1);
+          s3[b] += __fmul_rn(q0, x0);
+          s4[b] += __fmul_rn(q0, q0);
+          s3[b] += __fmul_rn(q1, x1);
+          s4[b] += __fmul_rn(q1, q1);
         }
       }
+    }
     }
     wait_vm0();
     __syncthreads();
@@ -437,8 +473,10 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
   }
 #pragma unroll
   for (int b = 0; b < TBW; ++b) {
-    s1[b] += __shfl_xor(s1[b], 32);
-    s2[b] += __shfl_xor(s2[b], 32);
+    if constexpr (!CHAN) {  // (the Chan sums already hold both lane halves)
+      s1[b] += __shfl_xor(s1[b], 32);
+      s2[b] += __shfl_xor(s2[b], 32);
+    }
     if constexpr (DG) {
       s3[b] += __shfl_xor(s3[b], 32);
       s4[b] += __shfl_xor(s4[b], 32);
@@ -451,6 +489,7 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
         m[2] = s3[b];
         m[3] = s4[b];
       }
+      if constexpr (CHAN) m[2] = cn[b];
     }
   }
 }
@@ -1801,9 +1840,9 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_batch_kernel(Batch<
 // token_diag, also the row's mean, std, tau and third / fourth power sums
 // (zero without them).
 // ---------------------------------------------------------------------------
-// mode kTauOnePass: std = sqrt(E[s^2] - mean^2) + 1e-8; kTauMean: store the
-// row mean in tau[] (input of the centred second pass); kTauCentered: std =
-// sqrt(sum (s - mean)^2 / N) + 1e-8 (v41:1719-1721).
+// mode kTauOnePass: std = sqrt(E[s^2] - mean^2) + 1e-8; kTauChan: std =
+// sqrt(M2 / N) + 1e-8 (v41:1719-1721) with M2 the partials' centred sums of
+// squares merged by Chan et al.'s formula.
 struct TauParams {
   const float* mom;
   const float* tau_off;
@@ -1846,8 +1885,13 @@ __device__ __attribute__((always_inline)) inline void tau_body(const TauParams& 
     const float mean = a / static_cast<float>(N);
 #pragma unroll 8
     for (int s = lane; s < S_st; s += 64) {
-      const int64_t left = N - static_cast<int64_t>(s) * q.upp;
-      const float n = static_cast<float>(left <= 0 ? 0 : (left < q.upp ? left : q.upp));
+      float n;
+      if (q.upp > 0) {
+        const int64_t left = N - static_cast<int64_t>(s) * q.upp;
+        n = static_cast<float>(left <= 0 ? 0 : (left < q.upp ? left : q.upp));
+      } else {
+        n = mom[(static_cast<int64_t>(s) * T + t) * ms + 2];  // the partial's unit count (stride 3)
+      }
       if (n > 0.f) {
         const float dm = mom[(static_cast<int64_t>(s) * T + t) * ms] / n - mean;
         b += n * dm * dm;
@@ -1862,12 +1906,7 @@ __device__ __attribute__((always_inline)) inline void tau_body(const TauParams& 
   if (lane == 0) {
     const float fN = static_cast<float>(N);
     const float mean = a / fN;
-    if (mode == kTauMean) {
-      tau[t] = mean;
-      return;
-    }
-    const float sd =
-        (mode == kTauCentered || mode == kTauChan ? sqrtf(b / fN) : sqrtf(b / fN - __fmul_rn(mean, mean))) + 1e-8f;
+    const float sd = (mode == kTauChan ? sqrtf(b / fN) : sqrtf(b / fN - __fmul_rn(mean, mean))) + 1e-8f;
     const float tv = mean + __fmul_rn(tau_off[t], sd);
     tau[t] = tv;
     if (q.sstd) q.sstd[t] = sd;
@@ -2524,7 +2563,7 @@ __global__ __launch_bounds__(256, NT <= 2 ? 2 : 1) void srw_decode_batch_kernel(
 // ---------------------------------------------------------------------------
 struct Kernels {
   void (*stats)(StatsParams);
-  void (*stats_centered)(StatsParams);  // second pass of the centred moments
+  void (*stats_chan)(StatsParams);  // the centred moments (kStatsChan), one pass
   void (*main)(MainParams);
   int main_threads;
   int main_lds;  // bytes
@@ -2542,15 +2581,15 @@ Kernels kernels_of(bool dg, bool gl = false) {
   if constexpr (WS) {
     constexpr int lds = (2 * (KH + 2 * DB) + 2 * 2 * DB + 16) * kFragBytes;  // 2 E/R, 2 W^T, S
     if (dg)
-      return Kernels{srw_stats_kernel<KH, kStatsDiag, 1>, srw_stats_kernel<KH, kStatsCentered, 1>,
+      return Kernels{srw_stats_kernel<KH, kStatsDiag, 1>, srw_stats_kernel<KH, kStatsChan, 1>,
                      srw_main_ws_kernel<DB, KH, HX, true>, kWsThreads, lds};
     if (gl)
-      return Kernels{srw_stats_kernel<KH, kStatsPlain, kStatsTBW>, srw_stats_kernel<KH, kStatsCentered, kStatsTBW>,
+      return Kernels{srw_stats_kernel<KH, kStatsPlain, kStatsTBW>, srw_stats_kernel<KH, kStatsChan, 1>,
                      srw_main_ws_kernel<DB, KH, HX, false, true>, kWsThreads, lds};
-    return Kernels{srw_stats_kernel<KH, kStatsPlain, kStatsTBW>, srw_stats_kernel<KH, kStatsCentered, kStatsTBW>,
+    return Kernels{srw_stats_kernel<KH, kStatsPlain, kStatsTBW>, srw_stats_kernel<KH, kStatsChan, 1>,
                    srw_main_ws_kernel<DB, KH, HX, false>, kWsThreads, lds};
   } else {
-    return Kernels{srw_stats_kernel<KH, kStatsPlain, kStatsTBW>, srw_stats_kernel<KH, kStatsCentered, kStatsTBW>,
+    return Kernels{srw_stats_kernel<KH, kStatsPlain, kStatsTBW>, srw_stats_kernel<KH, kStatsChan, 1>,
                    srw_main_kernel<DB, KH, HX>, kThreads, 2 * (KH + 2 * DB + 2 * DB) * kFragBytes};
   }
 }
@@ -2643,7 +2682,10 @@ MainBatchFn decode_batch_of(MainFn fn) {
   if (MainBatchFn b = decode_batch_for<4, 8>(fn)) return b;
   return decode_batch_for<4, 4>(fn);
 }
-int mom_stride(const srw_desc_t& d) { return with_diag(d) && d.stats_mode == SRW_STATS_ONEPASS ? 4 : 2; }
+int mom_stride(const srw_desc_t& d) {
+  if (d.stats_mode == SRW_STATS_CENTERED) return 3;  // kStatsChan: sum, M2, count
+  return with_diag(d) && d.stats_mode == SRW_STATS_ONEPASS ? 4 : 2;
+}
 int tok_part_stride(const srw_desc_t& d) { return with_diag(d) ? kTokPartDiag : 4; }
 
 Geometry geometry(const srw_desc_t& d, int64_t chunk) {
@@ -2890,26 +2932,17 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     sp.g = g;
     sp.s_out = ss ? scores : nullptr;
     const size_t smem = static_cast<size_t>(2 * KH) * kFragBytes;
-    for (auto fn : {k.stats, k.stats_centered})
-      if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   static_cast<int>(smem))) != hipSuccess)
-        return e;
-    hipLaunchKernelGGL(k.stats, dim3(grid_st), dim3(kThreads), smem, a.stream, sp);
+    // centred statistics: one pass (kStatsChan), the splits merged in srw_tau_kernel
+    const auto stats_fn = d.stats_mode == SRW_STATS_CENTERED ? k.stats_chan : k.stats;
+    if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(stats_fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 static_cast<int>(smem))) != hipSuccess)
+      return e;
+    hipLaunchKernelGGL(stats_fn, dim3(grid_st), dim3(kThreads), smem, a.stream, sp);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (d.stats_mode == SRW_STATS_CENTERED) {
-      // row means, then the sums of squared deviations from them (two-pass std)
-      if ((e = launch_tau(mom, a.in.tau_offset, tau, g.T, g.S_st, g.N, 2, nullptr, kTauMean, a.stream)) != hipSuccess)
-        return e;
-      sp.mean = tau;
-      sp.mask32 = nullptr;  // the first pass cleared the shared mask words
-      sp.s_out = nullptr;   // and stored the scores
-      hipLaunchKernelGGL(k.stats_centered, dim3(grid_st), dim3(kThreads), smem, a.stream, sp);
-      if ((e = hipGetLastError()) != hipSuccess) return e;
-    }
   }
   // tau per row from the moment partials
   if ((e = launch_tau(mom, a.in.tau_offset, tau, g.T, g.S_st, g.N, d.stats_mode == SRW_STATS_GRAM ? 2 : mom_stride(d),
-                      token_diag, d.stats_mode == SRW_STATS_CENTERED ? kTauCentered : kTauOnePass, a.stream, sstd)) !=
+                      token_diag, d.stats_mode == SRW_STATS_CENTERED ? kTauChan : kTauOnePass, a.stream, sstd)) !=
       hipSuccess)
     return e;
   // main
@@ -3002,7 +3035,7 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
 
 hipError_t launch_tau(const float* mom, const float* tau_off, float* tau, int64_t T, int S_st, int64_t N, int ms,
                       float* token_diag, int mode, hipStream_t s, float* sstd, int upp) {
-  if (mode == kTauChan && upp <= 0) return hipErrorInvalidValue;
+  if (mode == kTauChan && upp <= 0 && ms < 3) return hipErrorInvalidValue;
   const TauParams q{mom, tau_off, tau, T, S_st, N, ms, token_diag, mode, sstd, upp};
   hipLaunchKernelGGL(srw_tau_kernel, dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0, s, q);
   return hipGetLastError();
@@ -3135,10 +3168,10 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
   void (*stats_plain)(Batch<StatsParams>) = nullptr;
   void (*stats_cent)(Batch<StatsParams>) = nullptr;
   switch (KH) {
-    case 24: stats_plain = srw_stats_batch_kernel<24, kStatsPlain>; stats_cent = srw_stats_batch_kernel<24, kStatsCentered>; break;
-    case 8: stats_plain = srw_stats_batch_kernel<8, kStatsPlain>; stats_cent = srw_stats_batch_kernel<8, kStatsCentered>; break;
-    case 4: stats_plain = srw_stats_batch_kernel<4, kStatsPlain>; stats_cent = srw_stats_batch_kernel<4, kStatsCentered>; break;
-    case 2: stats_plain = srw_stats_batch_kernel<2, kStatsPlain>; stats_cent = srw_stats_batch_kernel<2, kStatsCentered>; break;
+    case 24: stats_plain = srw_stats_batch_kernel<24, kStatsPlain>; stats_cent = srw_stats_batch_kernel<24, kStatsChan>; break;
+    case 8: stats_plain = srw_stats_batch_kernel<8, kStatsPlain>; stats_cent = srw_stats_batch_kernel<8, kStatsChan>; break;
+    case 4: stats_plain = srw_stats_batch_kernel<4, kStatsPlain>; stats_cent = srw_stats_batch_kernel<4, kStatsChan>; break;
+    case 2: stats_plain = srw_stats_batch_kernel<2, kStatsPlain>; stats_cent = srw_stats_batch_kernel<2, kStatsChan>; break;
     default: return hipErrorNotSupported;
   }
   const hipStream_t st = a[0].stream;
@@ -3152,7 +3185,7 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
                              a[i].d.n_units, D, st)) != hipSuccess)
       return e;
   }
-  // moments (and for centred statistics the row means, then the second pass)
+  // moments (centred statistics: kStatsChan, merged in the tau kernel)
   Batch<StatsParams> sb{};
   Batch<TauParams> tb{};
   sb.n = tb.n = n;
@@ -3167,7 +3200,7 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     sp.s_out = ss[i] ? reinterpret_cast<uint16_t*>(a[i].ws + L[i].scores) : nullptr;
     sb.start[i + 1] = sb.start[i] + g[i].TT_st * g[i].S_st;
     tb.p[i] = TauParams{sp.mom, a[i].in.tau_offset, reinterpret_cast<float*>(a[i].ws + L[i].tau), g[i].T,
-                        g[i].S_st, g[i].N, 2, nullptr, centered ? kTauMean : kTauOnePass};
+                        g[i].S_st, g[i].N, centered ? 3 : 2, nullptr, centered ? kTauChan : kTauOnePass};
     tb.start[i + 1] = tb.start[i] + static_cast<int>((g[i].T + 3) / 4);
   }
   const size_t smem = static_cast<size_t>(2 * KH) * kFragBytes;
@@ -3175,22 +3208,11 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                  static_cast<int>(smem))) != hipSuccess)
       return e;
-  hipLaunchKernelGGL(stats_plain, dim3(static_cast<unsigned>(sb.start[n])), dim3(kThreads), smem, st, sb);
+  hipLaunchKernelGGL(centered ? stats_cent : stats_plain, dim3(static_cast<unsigned>(sb.start[n])), dim3(kThreads),
+                     smem, st, sb);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(srw_tau_batch_kernel, dim3(static_cast<unsigned>(tb.start[n])), dim3(256), 0, st, tb);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  if (centered) {
-    for (int i = 0; i < n; ++i) {
-      sb.p[i].mean = tb.p[i].tau;
-      sb.p[i].mask32 = nullptr;  // the first pass cleared the shared mask words
-      sb.p[i].s_out = nullptr;   // and stored the scores
-      tb.p[i].mode = kTauCentered;
-    }
-    hipLaunchKernelGGL(stats_cent, dim3(static_cast<unsigned>(sb.start[n])), dim3(kThreads), smem, st, sb);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(srw_tau_batch_kernel, dim3(static_cast<unsigned>(tb.start[n])), dim3(256), 0, st, tb);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
   // main (decode or prefill) kernel
   Batch<MainParams> mb{};
   mb.n = n;
