@@ -2100,10 +2100,28 @@ __device__ __attribute__((always_inline)) inline void finalize_rows_body(const F
   na = wave_sum(na);
   const float den = fmaxf(p.den_gate ? gs : is, 1.0f);        // v41:584, v401:340
   const int64_t stride = p.T * p.D;
-  const float* col = p.out_part + t * p.D + lane;
+  // columns of element j of a lane: DC even, pairs (2 lane, 2 lane + 1) +
+  // 128 (j / 2) read as 8-byte loads; DC odd, lane + 64 j.  The sum over the
+  // splits runs in the same order for every column either way.
+  constexpr bool PAIR = DC % 2 == 0;
+  auto col_of = [&](int j) { return PAIR ? 2 * lane + (j & 1) + 128 * (j >> 1) : lane + 64 * j; };
+  const float* row = p.out_part + t * p.D;
   float raw[DC];
 #pragma unroll
   for (int j = 0; j < DC; ++j) raw[j] = 0.f;
+  auto load_split = [&](int s, float (&v)[DC]) {
+    const float* src = row + static_cast<int64_t>(s) * stride;
+#pragma unroll
+    for (int j = 0; j < DC; j += PAIR ? 2 : 1) {
+      if constexpr (PAIR) {
+        const float2 q = *reinterpret_cast<const float2*>(src + col_of(j));
+        v[j] = q.x;
+        v[j + 1] = q.y;
+      } else {
+        v[j] = src[col_of(j)];
+      }
+    }
+  };
   for (int s0 = 0; s0 < p.S; s0 += p.spc) {                   // one reference chunk
     float acc[DC][8];
 #pragma unroll
@@ -2113,13 +2131,18 @@ __device__ __attribute__((always_inline)) inline void finalize_rows_body(const F
     int s = s0;
     for (; s + 7 < s0 + p.spc; s += 8) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
+      for (int k = 0; k < 8; ++k) {
+        float v[DC];
+        load_split(s + k, v);
 #pragma unroll
-        for (int j = 0; j < DC; ++j) acc[j][k] += col[(s + k) * stride + 64 * j];
+        for (int j = 0; j < DC; ++j) acc[j][k] += v[j];
+      }
     }
     for (; s < s0 + p.spc; ++s) {
+      float v[DC];
+      load_split(s, v);
 #pragma unroll
-      for (int j = 0; j < DC; ++j) acc[j][0] += col[s * stride + 64 * j];
+      for (int j = 0; j < DC; ++j) acc[j][0] += v[j];
     }
 #pragma unroll
     for (int j = 0; j < DC; ++j) {
@@ -2129,9 +2152,15 @@ __device__ __attribute__((always_inline)) inline void finalize_rows_body(const F
     }
   }
 #pragma unroll
-  for (int j = 0; j < DC; ++j) {
-    const float o = round_bf16(raw[j] / den);                 // v41:585-586
-    p.out[t * p.D + lane + 64 * j] = f32_to_bf16_bits(o * p.scale);
+  for (int j = 0; j < DC; j += PAIR ? 2 : 1) {
+    if constexpr (PAIR) {
+      const uint32_t lo = f32_to_bf16_bits(round_bf16(raw[j] / den) * p.scale);       // v41:585-586
+      const uint32_t hi = f32_to_bf16_bits(round_bf16(raw[j + 1] / den) * p.scale);
+      *reinterpret_cast<uint32_t*>(p.out + t * p.D + col_of(j)) = lo | (hi << 16);
+    } else {
+      const float o = round_bf16(raw[j] / den);                 // v41:585-586
+      p.out[t * p.D + col_of(j)] = f32_to_bf16_bits(o * p.scale);
+    }
   }
   if (lane == 0) {
     if (p.gate_sum) p.gate_sum[t] = gs;
