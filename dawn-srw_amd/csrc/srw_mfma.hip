@@ -2346,44 +2346,51 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
   // column blocks wave * NDB + c for the split's tiles (SP: of marked units
   // only, tmask[i] the marks of tile i)
   u32x4_t wf[NT][2][NDB];
-  auto load_rw = [&](const uint32_t* tmask) {
+  auto load_r = [&](const uint32_t* tmask) {
 #pragma unroll
     for (int ks = 0; ks < KX; ++ks) {
       rf[ks] = u32x4_t{};
       if (!SP || ((tmask[wi < NT ? wi : 0] >> col) & 1u))
         rf[ks] = *reinterpret_cast<const u32x4_t*>(p.read + ur * D + 16 * ks + 8 * half);
     }
+  };
+  // (every slot is set: past the split's tiles without SP the last tile is
+  // loaded again, with SP zeros, so that the write GEMM runs over all NT
+  // slots with P zero there, without branches)
+  auto load_w = [&](const uint32_t* tmask) {
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
-      if (i < ntl) {
+      const int64_t tile = ta + (i < ntl ? i : ntl - 1);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int c = 0; c < NDB; ++c) {
-            const int db = wave * NDB + c;
-            wf[i][j][c] = u32x4_t{};
-            // lane half h of k-step j holds units 16 j + 4 h + (0..3) and
-            // 16 j + 8 + 4 h + (0..3) (unit_of_k)
-            if (!SP || (((tmask[i] >> (16 * j + 4 * half)) | (tmask[i] >> (16 * j + 8 + 4 * half))) & 0xFu))
-              wf[i][j][c] = *reinterpret_cast<const u32x4_t*>(
-                  p.wp + ((static_cast<int64_t>(ta + i) * DB + db) * 2 + j) * 512 + lane * 8);
-          }
-      }
+        for (int c = 0; c < NDB; ++c) {
+          const int db = wave * NDB + c;
+          wf[i][j][c] = u32x4_t{};
+          // lane half h of k-step j holds units 16 j + 4 h + (0..3) and
+          // 16 j + 8 + 4 h + (0..3) (unit_of_k)
+          if (!SP || (i < ntl && (((tmask[i] >> (16 * j + 4 * half)) | (tmask[i] >> (16 * j + 8 + 4 * half))) & 0xFu)))
+            wf[i][j][c] = *reinterpret_cast<const u32x4_t*>(p.wp + ((tile * DB + db) * 2 + j) * 512 + lane * 8);
+        }
     }
   };
-  if constexpr (!SP) load_rw(nullptr);
+  if constexpr (!SP) load_r(nullptr);
   // the rows' thresholds (srw_tau_kernel, v41:461-464)
   float tau_b[TB], sstd_b[TB];
 #pragma unroll
   for (int b = 0; b < TB; ++b) {
     const int64_t t = row0 + 32 * b + col;
     tau_b[b] = p.tau[t < Tv ? t : Tv - 1];
-    sstd_b[b] = GL ? 1.0f / p.sstd[t < Tv ? t : Tv - 1] : 1.f;  // its reciprocal
+    sstd_b[b] = GL ? p.sstd[t < Tv ? t : Tv - 1] : 1.f;
+  }
+  wait_vm0();
+  barrier_lds();
+#pragma unroll
+  for (int b = 0; b < TB; ++b) {
+    if (GL) sstd_b[b] = 1.0f / sstd_b[b];  // its reciprocal
     // the GELU gate of _srw_inference compares with bf16(tau)
     if (GL && p.gl_raw_bf16) tau_b[b] = __uint_as_float(pack_bf16(0.0f, tau_b[b]));
   }
-  wait_vm0();
-  __syncthreads();
   if constexpr (SP) {
     // mark the tile's units that pass for some row of this wave's blocks
     uint32_t um = 0;
@@ -2422,7 +2429,8 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
       for (int w = 0; w < 4; ++w)
         if (w / wpt == i) tmask[i] |= umask[w];
     }
-    load_rw(tmask);
+    load_r(tmask);
+    load_w(tmask);
     wait_vm0();
   }
 
@@ -2430,6 +2438,7 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
   const GateParams gp = p.gp;
   const int64_t u0 = static_cast<int64_t>(mt) * kUnitTile;
   const bool shared_tile = (u0 < lo) || (u0 + kUnitTile > hi && hi < N);
+  const bool full_tile = u0 >= lo && u0 + kUnitTile <= hi;
   uint32_t pk[TB][8];
   float gsum[TB], isum[TB];
   uint32_t nact[TB];
@@ -2441,55 +2450,102 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
 #pragma unroll
     for (int q = 0; q < 8; ++q) pk[b][q] = 0;
   }
+  f32x16_t sacc[TB], racc[TB];
   if (have) {
 #pragma unroll
     for (int b = 0; b < TB; ++b) {
       if (b % wpt != wb) continue;
-      f32x16_t sacc = {}, racc = {};
+      // the block's H and X fragments are read from LDS in groups ahead of
+      // their MFMAs, so that the MFMAs issue back to back instead of each
+      // waiting out one LDS read (SP: W^T is in registers already, and the
+      // buffers would not fit beside it)
+      sacc[b] = f32x16_t{};
+      racc[b] = f32x16_t{};
+      if constexpr (SP) {
 #pragma unroll
-      for (int ks = 0; ks < KH; ++ks)
-        sacc = mfma(ef[ks], *reinterpret_cast<const u32x4_t*>(hl + (b * KH + ks) * kFragBytes + lane * 16), sacc);
+        for (int ks = 0; ks < KH; ++ks)
+          sacc[b] = mfma(ef[ks], *reinterpret_cast<const u32x4_t*>(hl + (b * KH + ks) * kFragBytes + lane * 16), sacc[b]);
 #pragma unroll
-      for (int ks = 0; ks < KX; ++ks)
-        racc = mfma(rf[ks], *reinterpret_cast<const u32x4_t*>(xl + (b * KX + ks) * kFragBytes + lane * 16), racc);
+        for (int ks = 0; ks < KX; ++ks)
+          racc[b] = mfma(rf[ks], *reinterpret_cast<const u32x4_t*>(xl + (b * KX + ks) * kFragBytes + lane * 16), racc[b]);
+        continue;
+      }
+      u32x4_t hq[KH];
+#pragma unroll
+      for (int ks = 0; ks < KH; ++ks) hq[ks] = *reinterpret_cast<const u32x4_t*>(hl + (b * KH + ks) * kFragBytes + lane * 16);
+      constexpr int G = KX % 8 == 0 ? 8 : KX;
+      u32x4_t xq[2][G];
+#pragma unroll
+      for (int k = 0; k < G; ++k) xq[0][k] = *reinterpret_cast<const u32x4_t*>(xl + (b * KX + k) * kFragBytes + lane * 16);
+      __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the MFMAs
+#pragma unroll
+      for (int ks = 0; ks < KH; ++ks) sacc[b] = mfma(ef[ks], hq[ks], sacc[b]);
+#pragma unroll
+      for (int g = 0; g < KX / G; ++g) {
+        if (g + 1 < KX / G) {
+#pragma unroll
+          for (int k = 0; k < G; ++k)
+            xq[(g + 1) & 1][k] = *reinterpret_cast<const u32x4_t*>(xl + (b * KX + (g + 1) * G + k) * kFragBytes + lane * 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < G; ++k) racc[b] = mfma(rf[g * G + k], xq[g & 1][k], racc[b]);
+      }
+    }
+  }
+  // the W^T fragments go out now, into the registers E and R held: they
+  // stream in under the gate, and only the write GEMM waits for them
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (!SP) load_w(nullptr);
+  __builtin_amdgcn_sched_barrier(0);
+  if (have) {
+#pragma unroll
+    for (int b = 0; b < TB; ++b) {
+      if (b % wpt != wb) continue;
       const int64_t t = row0 + 32 * b + col;
       const float tau = tau_b[b], istd = sstd_b[b];
       uint32_t bits = 0;
+      // the bounds test per unit only in a tile the split shares or the pool ends in
+      auto gate16 = [&](auto full_t) {
+        constexpr bool FULL = decltype(full_t)::value;
 #pragma unroll
-      for (int v = 0; v < 16; v += 2) {
-        const uint32_t sp = pack_bf16(sacc[v], sacc[v + 1]);   // bf16 scores (v41:503)
-        const uint32_t xp = pack_bf16(racc[v], racc[v + 1]);   // bf16 x.r (v41:517)
-        float g2[2], in2[2];
-        bool on2[2];
+        for (int v = 0; v < 16; v += 2) {
+          const uint32_t sp = pack_bf16(sacc[b][v], sacc[b][v + 1]);   // bf16 scores (v41:503)
+          const uint32_t xp = pack_bf16(racc[b][v], racc[b][v + 1]);   // bf16 x.r (v41:517)
+          float g2[2], in2[2];
+          bool on2[2];
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float sv = e ? hi_f32(sp) : lo_f32(sp);
-          const int64_t u = u0 + unit_of_acc(v + e, half);
-          const bool ok = u >= lo && u < hi;
-          if constexpr (GL) {
-            float zp;
-            const float g = gelu_gate(sv, tau, istd, zp, p.gl_raw_bf16 != 0);
-            g2[e] = ok ? g : 0.f;
-            in2[e] = ok ? zp : 0.f;
-            on2[e] = ok && zp > 0.0f;
-          } else {
-            const float raw = sv - tau;
-            const float margin = raw - gp.thr;
-            const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(margin * p.exp_scale));
-            const float am = fmaxf(margin - gp.cut, 0.0f);
-            g2[e] = ok ? act * (gp.eps + fminf(am, gp.maxi)) : 0.f;
-            in2[e] = ok ? gp.eps + fminf(am, gp.maxi) : 0.f;
-            on2[e] = ok && act > 0.5f;
+          for (int e = 0; e < 2; ++e) {
+            const float sv = e ? hi_f32(sp) : lo_f32(sp);
+            const int64_t u = u0 + unit_of_acc(v + e, half);
+            const bool ok = FULL || (u >= lo && u < hi);
+            if constexpr (GL) {
+              float zp;
+              const float g = gelu_gate(sv, tau, istd, zp, p.gl_raw_bf16 != 0);
+              g2[e] = ok ? g : 0.f;
+              in2[e] = ok ? zp : 0.f;
+              on2[e] = ok && zp > 0.0f;
+            } else {
+              const float raw = sv - tau;
+              const float margin = raw - gp.thr;
+              const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(margin * p.exp_scale));
+              const float am = fmaxf(margin - gp.cut, 0.0f);
+              g2[e] = ok ? act * (gp.eps + fminf(am, gp.maxi)) : 0.f;
+              in2[e] = ok ? gp.eps + fminf(am, gp.maxi) : 0.f;
+              on2[e] = ok && act > 0.5f;
+            }
           }
+          gsum[b] += g2[0];
+          gsum[b] += g2[1];
+          isum[b] += in2[0];
+          isum[b] += in2[1];
+          bits = (bits << 2) | (on2[0] ? 2u : 0u) | (on2[1] ? 1u : 0u);
+          const uint32_t gq = pack_bf16(g2[0], g2[1]);             // gate_bf (v41:516)
+          pk[b][v >> 1] = pack_bf16(lo_f32(gq) * lo_f32(xp), hi_f32(gq) * hi_f32(xp));  // (v41:518)
         }
-        gsum[b] += g2[0];
-        gsum[b] += g2[1];
-        isum[b] += in2[0];
-        isum[b] += in2[1];
-        bits = (bits << 2) | (on2[0] ? 2u : 0u) | (on2[1] ? 1u : 0u);
-        const uint32_t gq = pack_bf16(g2[0], g2[1]);             // gate_bf (v41:516)
-        pk[b][v >> 1] = pack_bf16(lo_f32(gq) * lo_f32(xp), hi_f32(gq) * hi_f32(xp));  // (v41:518)
-      }
+      };
+      if (full_tile) gate16(std::true_type{});
+      else gate16(std::false_type{});
       // pass bits of (row, tile): element v at bit unit_of_acc(v, half)
       const uint32_t br = __builtin_bitreverse32(bits) >> 16;
       uint32_t m = (br & 0xFu) | ((br & 0xF0u) << 4) | ((br & 0xF00u) << 8) | ((br & 0xF000u) << 12);
@@ -2519,7 +2575,7 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
       }
     }
   }
-  __syncthreads();  // every wave is done reading X
+  barrier_lds();  // every wave is done reading X (the W^T loads stay in flight)
   // P of (tile wi, block b, k-step j) over X: lane l's 16 bytes at 16 l
   if (have) {
 #pragma unroll
@@ -2531,37 +2587,48 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
             u32x4_t{pk[b][4 * j], pk[b][4 * j + 1], pk[b][4 * j + 2], pk[b][4 * j + 3]};
     }
   }
-  __syncthreads();
+  barrier_lds();
 
-  // write GEMM: OUT[rows x 32 (wave NDB + c) .. ] over the split's tiles
-  f32x16_t oacc[TB][NDB];
+  // write GEMM: OUT[rows x 32 (wave NDB + c) .. ] over the split's tiles, one
+  // column block at a time, each stored while the next one runs
+  u32x4_t pf[NT][2][TB];  // zero past the split's tiles
 #pragma unroll
-  for (int b = 0; b < TB; ++b)
+  for (int i = 0; i < NT; ++i)
 #pragma unroll
-    for (int c = 0; c < NDB; ++c) oacc[b][c] = f32x16_t{};
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-  for (int i = 0; i < NT; ++i) {
-    if (i < ntl) {
+      for (int b = 0; b < TB; ++b) {
+        pf[i][j][b] = u32x4_t{};
+        if (i < ntl) pf[i][j][b] = *reinterpret_cast<const u32x4_t*>(xl + ((i * TB + b) * 2 + j) * kFragBytes + lane * 16);
+      }
+  float* op = p.out_part + static_cast<int64_t>(split) * Tv * D;
+#pragma unroll
+  for (int c = 0; c < NDB; ++c) {
+    f32x16_t oacc[TB];
+#pragma unroll
+    for (int b = 0; b < TB; ++b) oacc[b] = f32x16_t{};
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int b = 0; b < TB; ++b) {
-          const u32x4_t a = *reinterpret_cast<const u32x4_t*>(xl + ((i * TB + b) * 2 + j) * kFragBytes + lane * 16);
+        for (int b = 0; b < TB; ++b) oacc[b] = mfma(pf[i][j][b], wf[i][j][c], oacc[b]);
+    if (row0 + 32 * TB <= Tv) {
 #pragma unroll
-          for (int c = 0; c < NDB; ++c) oacc[b][c] = mfma(a, wf[i][j][c], oacc[b][c]);
+      for (int b = 0; b < TB; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          op[(row0 + 32 * b + unit_of_acc(v, half)) * D + 32 * (wave * NDB + c) + col] = oacc[b][v];
+    } else {
+#pragma unroll
+      for (int b = 0; b < TB; ++b)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t t = row0 + 32 * b + unit_of_acc(v, half);
+          if (t < Tv) op[t * D + 32 * (wave * NDB + c) + col] = oacc[b][v];
         }
     }
   }
-  float* op = p.out_part + static_cast<int64_t>(split) * Tv * D;
-#pragma unroll
-  for (int b = 0; b < TB; ++b)
-#pragma unroll
-    for (int c = 0; c < NDB; ++c)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t t = row0 + 32 * b + unit_of_acc(v, half);
-        if (t < Tv) op[t * D + 32 * (wave * NDB + c) + col] = oacc[b][c][v];
-      }
   // per-row partials of the split: its tiles in order
   for (int r = threadIdx.x; r < TB * 32 && row0 + r < Tv; r += 256) {
     const int b = r / 32, c = r % 32;
