@@ -1951,16 +1951,21 @@ struct FinalParams {
   int den_gate;          // den = max(sum gate, 1) (the v4.0.1 gate, v401:340)
 };
 
-// NG: split groups per workgroup.  One workgroup per (row, block of 256 / NG
-// columns); thread (g, c) = (tid / CW, tid % CW) sums column c over splits
-// s = g, g + NG, ... of each chunk with eight loads in flight; the NG group
-// sums of a chunk combine in a fixed order, so the result is deterministic.
-// Few splits per chunk (large T) use NG = 1, many (decode) NG = 16.
-template <int NG>
+// NG: split groups per workgroup; VW: columns per thread (1, 2 or 4: 4-,
+// 8- or 16-byte loads; the widest that leaves two workgroups per CU).  One workgroup per (row, block of 256 / NG
+// x VW columns); thread (g, c) = (tid / CW, tid % CW) sums columns
+// VW c .. VW c + VW - 1 of its block over splits s = g, g + NG, ... of each
+// chunk with eight loads in flight; the NG group sums of a chunk combine in
+// a fixed order, so the result is deterministic (and the same for either
+// VW: each column keeps its order of additions).  Few splits per chunk
+// (large T) use NG = 1, many (decode) NG = 16.
+template <int NG, int VW>
 __device__ __attribute__((always_inline)) inline void finalize_body(const FinalParams& p, const int bx) {
   constexpr int CW = 256 / NG;
+  static_assert(VW == 1 || VW == 2 || VW == 4, "one, two or four columns per thread");
+  typedef float vec_t __attribute__((ext_vector_type(VW)));
   __shared__ float red[3][4];
-  __shared__ float part[NG > 1 ? NG : 1][CW];
+  __shared__ vec_t part[NG > 1 ? NG : 1][CW];
   const int64_t t = bx;
   const int tid = threadIdx.x;
   const int g = tid / CW, c = tid % CW;
@@ -1985,51 +1990,61 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
   const float NA = red[2][0] + red[2][1] + red[2][2] + red[2][3];
   const float den = fmaxf(p.den_gate ? G : I, 1.0f);          // v41:584, v401:340
   const int64_t stride = p.T * p.D;
-  const int d = blockIdx.y * CW + c;
+  const int d = (blockIdx.y * CW + c) * VW;
   const bool dok = d < p.D;
-  const float* col = p.out_part + t * p.D + (dok ? d : 0);
-  float raw = 0.f;
+  const vec_t* col = reinterpret_cast<const vec_t*>(p.out_part + t * p.D + (dok ? d : 0));
+  const int64_t vstride = stride / VW;
+  vec_t raw = {};
+  auto round_v = [](vec_t x) {
+    vec_t r;
+#pragma unroll
+    for (int k = 0; k < VW; ++k) r[k] = round_bf16(x[k]);
+    return r;
+  };
   if (NG == 1 && p.spc == 1) {
     // one split per chunk: the chunks' loads go out eight at a time, the
     // rounded chunk results add in chunk order
     for (int s0 = 0; s0 < p.S; s0 += 8) {
-      float v[8];
+      vec_t v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = s0 + j < p.S ? col[(s0 + j) * stride] : 0.f;
+      for (int j = 0; j < 8; ++j) v[j] = s0 + j < p.S ? col[(s0 + j) * vstride] : vec_t{};
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        if (s0 + j < p.S) raw += round_bf16(v[j]);               // bf16 dot output (v41:518)
+        if (s0 + j < p.S) raw += round_v(v[j]);                  // bf16 dot output (v41:518)
     }
   }
   for (int s0 = 0; s0 < p.S && !(NG == 1 && p.spc == 1); s0 += p.spc) {  // one reference chunk
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    vec_t acc[8] = {};
     // rounds of eight splits per thread, all eight loads in flight at once
     // (predicated past the chunk's end)
     for (int s = s0 + g; s < s0 + p.spc; s += 8 * NG) {
-      float v[8];
+      vec_t v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = s + NG * j < s0 + p.spc ? col[(s + NG * j) * stride] : 0.f;
+      for (int j = 0; j < 8; ++j) v[j] = s + NG * j < s0 + p.spc ? col[(s + NG * j) * vstride] : vec_t{};
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] += v[j];
     }
-    const float sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    const vec_t sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
     if constexpr (NG == 1) {
-      raw += round_bf16(sum);                                // bf16 dot output (v41:518)
+      raw += round_v(sum);                                   // bf16 dot output (v41:518)
     } else {
       part[g][c] = sum;
       __syncthreads();
       if (g == 0) {
-        float q = part[0][c];
+        vec_t q = part[0][c];
 #pragma unroll
         for (int k = 1; k < NG; ++k) q += part[k][c];
-        raw += round_bf16(q);                                // bf16 dot output (v41:518)
+        raw += round_v(q);                                   // bf16 dot output (v41:518)
       }
       __syncthreads();
     }
   }
   if (g == 0 && dok) {
-    const float o = round_bf16(raw / den);                  // v41:585-586
-    p.out[t * p.D + d] = f32_to_bf16_bits(o * p.scale);
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      const float o = round_bf16(raw[k] / den);             // v41:585-586
+      p.out[t * p.D + d + k] = f32_to_bf16_bits(o * p.scale);
+    }
   }
   if (blockIdx.y != 0) return;
   if (tid == 0) {
@@ -2068,14 +2083,14 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
     }
   }
 }
-template <int NG>
+template <int NG, int VW = 1>
 __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
-  finalize_body<NG>(p, blockIdx.x);
+  finalize_body<NG, VW>(p, blockIdx.x);
 }
-template <int NG>
+template <int NG, int VW = 1>
 __global__ __launch_bounds__(256) void srw_finalize_batch_kernel(Batch<FinalParams> b) {
   const int i = batch_index(b.start, b.n, blockIdx.x);
-  finalize_body<NG>(b.p[i], blockIdx.x - b.start[i]);
+  finalize_body<NG, VW>(b.p[i], blockIdx.x - b.start[i]);
 }
 
 // Few splits per chunk (spc < 16: prefill-sized T): one wave per row, lane l
@@ -3139,6 +3154,15 @@ hipError_t launch_tau(const float* mom, const float* tau_off, float* tau, int64_
 
 // split groups per finalize workgroup from the splits per chunk
 int finalize_groups(int spc) { return spc >= 32 ? 16 : (spc >= 16 ? 4 : 1); }
+// columns per thread of srw_finalize_kernel: the widest loads (4, 2, 1
+// floats) that D allows and that still leave at least two workgroups per CU
+int finalize_width(int64_t rows, int D, int ng) {
+  for (int vw = 4; vw > 1; vw /= 2) {
+    const int cols = 256 / ng * vw;
+    if (D % vw == 0 && rows * ((D + cols - 1) / cols) >= 2 * 256) return vw;
+  }
+  return 1;
+}
 
 FinalParams final_params_of(const FinalizeArgs& f) {
   FinalParams fp{};
@@ -3173,10 +3197,22 @@ hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
     else hipLaunchKernelGGL(srw_finalize_rows_kernel<6>, grid_r, dim3(256), 0, s, fp);
     return hipGetLastError();
   }
-  const dim3 grid_f(static_cast<unsigned>(f.T), static_cast<unsigned>((f.D + 256 / ng - 1) / (256 / ng)));
-  if (ng == 16) hipLaunchKernelGGL(srw_finalize_kernel<16>, grid_f, dim3(256), 0, s, fp);
-  else if (ng == 4) hipLaunchKernelGGL(srw_finalize_kernel<4>, grid_f, dim3(256), 0, s, fp);
-  else hipLaunchKernelGGL(srw_finalize_kernel<1>, grid_f, dim3(256), 0, s, fp);
+  const int vw = finalize_width(f.T, f.D, ng);
+  const int cols = 256 / ng * vw;  // per workgroup
+  const dim3 grid_f(static_cast<unsigned>(f.T), static_cast<unsigned>((f.D + cols - 1) / cols));
+  if (vw == 4) {
+    if (ng == 16) hipLaunchKernelGGL((srw_finalize_kernel<16, 4>), grid_f, dim3(256), 0, s, fp);
+    else if (ng == 4) hipLaunchKernelGGL((srw_finalize_kernel<4, 4>), grid_f, dim3(256), 0, s, fp);
+    else hipLaunchKernelGGL((srw_finalize_kernel<1, 4>), grid_f, dim3(256), 0, s, fp);
+  } else if (vw == 2) {
+    if (ng == 16) hipLaunchKernelGGL((srw_finalize_kernel<16, 2>), grid_f, dim3(256), 0, s, fp);
+    else if (ng == 4) hipLaunchKernelGGL((srw_finalize_kernel<4, 2>), grid_f, dim3(256), 0, s, fp);
+    else hipLaunchKernelGGL((srw_finalize_kernel<1, 2>), grid_f, dim3(256), 0, s, fp);
+  } else {
+    if (ng == 16) hipLaunchKernelGGL(srw_finalize_kernel<16>, grid_f, dim3(256), 0, s, fp);
+    else if (ng == 4) hipLaunchKernelGGL(srw_finalize_kernel<4>, grid_f, dim3(256), 0, s, fp);
+    else hipLaunchKernelGGL(srw_finalize_kernel<1>, grid_f, dim3(256), 0, s, fp);
+  }
   return hipGetLastError();
 }
 
@@ -3374,9 +3410,19 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     else hipLaunchKernelGGL(srw_finalize_rows_batch_kernel<6>, grid_r, dim3(256), 0, st, fb);
     return hipGetLastError();
   }
-  const dim3 grid_f(static_cast<unsigned>(fb.start[n]), static_cast<unsigned>((D + 256 / ng - 1) / (256 / ng)));
-  if (ng == 16) hipLaunchKernelGGL(srw_finalize_batch_kernel<16>, grid_f, dim3(256), 0, st, fb);
-  else hipLaunchKernelGGL(srw_finalize_batch_kernel<4>, grid_f, dim3(256), 0, st, fb);
+  const int vw = finalize_width(fb.start[n], D, ng);
+  const int cols = 256 / ng * vw;  // per workgroup
+  const dim3 grid_f(static_cast<unsigned>(fb.start[n]), static_cast<unsigned>((D + cols - 1) / cols));
+  if (vw == 4) {
+    if (ng == 16) hipLaunchKernelGGL((srw_finalize_batch_kernel<16, 4>), grid_f, dim3(256), 0, st, fb);
+    else hipLaunchKernelGGL((srw_finalize_batch_kernel<4, 4>), grid_f, dim3(256), 0, st, fb);
+  } else if (vw == 2) {
+    if (ng == 16) hipLaunchKernelGGL((srw_finalize_batch_kernel<16, 2>), grid_f, dim3(256), 0, st, fb);
+    else hipLaunchKernelGGL((srw_finalize_batch_kernel<4, 2>), grid_f, dim3(256), 0, st, fb);
+  } else {
+    if (ng == 16) hipLaunchKernelGGL(srw_finalize_batch_kernel<16>, grid_f, dim3(256), 0, st, fb);
+    else hipLaunchKernelGGL(srw_finalize_batch_kernel<4>, grid_f, dim3(256), 0, st, fb);
+  }
   return hipGetLastError();
 }
 
