@@ -2283,6 +2283,7 @@ __global__ __launch_bounds__(256) void srw_unit_diag_kernel(const float2* __rest
 // per-row sums of the four tiles are combined in LDS in wave order.
 // ---------------------------------------------------------------------------
 constexpr int kDecTiles = 4;    // tiles per split (one per wave)
+constexpr int kDecMinTiles = 3; // the fewest per split the geometry aims for
 constexpr int kDecMaxRows = 128;
 
 template <int TB, int DB, int KH>
@@ -2814,9 +2815,17 @@ Geometry geometry(const srw_desc_t& d, int64_t chunk) {
   if (spc < 1) spc = 1;
   if (spc > min_tiles) spc = static_cast<int>(min_tiles > 0 ? min_tiles : 1);
   if (decode_applies(d)) {
-    // decode: splits of at most kDecTiles tiles, as few as fill the CUs
+    // decode: splits of kDecMinTiles .. kDecTiles tiles, as few as fill the
+    // CUs.  Small pools take more tiles per split than filling the CUs asks
+    // for: every
+    // split writes fp32 partials for all its rows (rows x d_model x 4 bytes,
+    // more than the split's share of the pool when it holds one tile), so
+    // fewer, longer splits win there -- at the 40M decode step the QK and V
+    // calls (50 and 82 tiles, 128 and 64 rows) wrote 18 MB of partials for
+    // 7.5 MB of pool with one tile per split; with three, 0.818 -> 0.728 ms
+    // per step
     int64_t tpw = (g.ntiles + kTargetBlocks - 1) / kTargetBlocks;
-    tpw = tpw < 1 ? 1 : (tpw > kDecTiles ? kDecTiles : tpw);
+    tpw = tpw < kDecMinTiles ? kDecMinTiles : (tpw > kDecTiles ? kDecTiles : tpw);
     int64_t nt_max = 0;
     for (int c = 0; c < g.nc; ++c) {
       const int64_t c_lo = c * g.cs, c_hi = (c + 1) * g.cs < g.N ? (c + 1) * g.cs : g.N;
