@@ -48,7 +48,7 @@ MEASURED_TRAFFIC = {
     # moments kernel stored, besides R, W^T and x
     ("know", "onepass", "mfma_ss_bf16"): (133053.0 * 2.0 + 64575.2 * 1.0) * 1024,
     # profiles/decode_know_T64_N25200_kernel_stats.md
-    ("decode_know", "onepass", "mfma_decode_bf16"): (22595.6 * 2.0 + 19704.0 * 1.0) * 1024,
+    ("decode_know", "onepass", "mfma_decode_bf16"): (22586.8 * 2.0 + 19709.4 * 1.0) * 1024,
 }
 
 WORKLOADS = {

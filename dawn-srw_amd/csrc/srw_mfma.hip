@@ -2629,19 +2629,23 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int b = 0; b < TB; ++b) oacc[b] = mfma(pf[i][j][b], wf[i][j][c], oacc[b]);
+    // non-temporal stores: the partials go out to memory while the kernel
+    // runs instead of as dirty L2 lines written back at its end (the Know
+    // call's decode kernel 19.0 -> 17.4 us; the finalize then reads them from
+    // memory, 6.1 -> 7.3 us; the decode step 0.727 -> 0.721 ms)
     if (row0 + 32 * TB <= Tv) {
 #pragma unroll
       for (int b = 0; b < TB; ++b)
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-          op[(row0 + 32 * b + unit_of_acc(v, half)) * D + 32 * (wave * NDB + c) + col] = oacc[b][v];
+          __builtin_nontemporal_store(oacc[b][v], &op[(row0 + 32 * b + unit_of_acc(v, half)) * D + 32 * (wave * NDB + c) + col]);
     } else {
 #pragma unroll
       for (int b = 0; b < TB; ++b)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int64_t t = row0 + 32 * b + unit_of_acc(v, half);
-          if (t < Tv) op[t * D + 32 * (wave * NDB + c) + col] = oacc[b][v];
+          if (t < Tv) __builtin_nontemporal_store(oacc[b][v], &op[t * D + 32 * (wave * NDB + c) + col]);
         }
     }
   }
