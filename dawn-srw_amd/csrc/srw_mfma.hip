@@ -2373,9 +2373,10 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
   // (every slot is set: past the split's tiles without SP the last tile is
   // loaded again, with SP zeros, so that the write GEMM runs over all NT
   // slots with P zero there, without branches)
-  auto load_w = [&](const uint32_t* tmask) {
+  auto load_w = [&](const uint32_t* tmask, int i_lo = 0, int i_hi = NT) {
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
+      if (i < i_lo || i >= i_hi) continue;
       const int64_t tile = ta + (i < ntl ? i : ntl - 1);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -2467,53 +2468,72 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
     for (int q = 0; q < 8; ++q) pk[b][q] = 0;
   }
   f32x16_t sacc[TB], racc[TB];
-  if (have) {
 #pragma unroll
-    for (int b = 0; b < TB; ++b) {
-      if (b % wpt != wb) continue;
-      // the block's H and X fragments are read from LDS in groups ahead of
-      // their MFMAs, so that the MFMAs issue back to back instead of each
-      // waiting out one LDS read (SP: W^T is in registers already, and the
-      // buffers would not fit beside it)
-      sacc[b] = f32x16_t{};
-      racc[b] = f32x16_t{};
-      if constexpr (SP) {
+  for (int b = 0; b < TB; ++b) {
+    sacc[b] = f32x16_t{};
+    racc[b] = f32x16_t{};
+  }
+  if constexpr (SP) {
+    // (W^T is in registers already: no room for fragment buffers)
+    if (have) {
+#pragma unroll
+      for (int b = 0; b < TB; ++b) {
+        if (b % wpt != wb) continue;
 #pragma unroll
         for (int ks = 0; ks < KH; ++ks)
           sacc[b] = mfma(ef[ks], *reinterpret_cast<const u32x4_t*>(hl + (b * KH + ks) * kFragBytes + lane * 16), sacc[b]);
 #pragma unroll
         for (int ks = 0; ks < KX; ++ks)
           racc[b] = mfma(rf[ks], *reinterpret_cast<const u32x4_t*>(xl + (b * KX + ks) * kFragBytes + lane * 16), racc[b]);
-        continue;
-      }
-      u32x4_t hq[KH];
-#pragma unroll
-      for (int ks = 0; ks < KH; ++ks) hq[ks] = *reinterpret_cast<const u32x4_t*>(hl + (b * KH + ks) * kFragBytes + lane * 16);
-      constexpr int G = KX % 8 == 0 ? 8 : KX;
-      u32x4_t xq[2][G];
-#pragma unroll
-      for (int k = 0; k < G; ++k) xq[0][k] = *reinterpret_cast<const u32x4_t*>(xl + (b * KX + k) * kFragBytes + lane * 16);
-      __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the MFMAs
-#pragma unroll
-      for (int ks = 0; ks < KH; ++ks) sacc[b] = mfma(ef[ks], hq[ks], sacc[b]);
-#pragma unroll
-      for (int g = 0; g < KX / G; ++g) {
-        if (g + 1 < KX / G) {
-#pragma unroll
-          for (int k = 0; k < G; ++k)
-            xq[(g + 1) & 1][k] = *reinterpret_cast<const u32x4_t*>(xl + (b * KX + (g + 1) * G + k) * kFragBytes + lane * 16);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int k = 0; k < G; ++k) racc[b] = mfma(rf[g * G + k], xq[g & 1][k], racc[b]);
       }
     }
+  } else {
+    // the score GEMMs of every row block first; then the first half of the
+    // W^T fragments goes out into the registers E held, streaming in under
+    // the read GEMMs, and the second half after them, under the gate.  The
+    // blocks' H and X fragments are read from LDS in groups ahead of their
+    // MFMAs (scheduling barriers keep the reads ahead), so that the MFMAs
+    // issue back to back instead of each waiting out one LDS read.
+    if (have) {
+#pragma unroll
+      for (int b = 0; b < TB; ++b) {
+        if (b % wpt != wb) continue;
+        u32x4_t hq[KH];
+#pragma unroll
+        for (int ks = 0; ks < KH; ++ks) hq[ks] = *reinterpret_cast<const u32x4_t*>(hl + (b * KH + ks) * kFragBytes + lane * 16);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < KH; ++ks) sacc[b] = mfma(ef[ks], hq[ks], sacc[b]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(nullptr, 0, NT / 2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (have) {
+#pragma unroll
+      for (int b = 0; b < TB; ++b) {
+        if (b % wpt != wb) continue;
+        constexpr int G = KX % 8 == 0 ? 8 : KX;
+        u32x4_t xq[2][G];
+#pragma unroll
+        for (int k = 0; k < G; ++k) xq[0][k] = *reinterpret_cast<const u32x4_t*>(xl + (b * KX + k) * kFragBytes + lane * 16);
+#pragma unroll
+        for (int g = 0; g < KX / G; ++g) {
+          if (g + 1 < KX / G) {
+#pragma unroll
+            for (int k = 0; k < G; ++k)
+              xq[(g + 1) & 1][k] = *reinterpret_cast<const u32x4_t*>(xl + (b * KX + (g + 1) * G + k) * kFragBytes + lane * 16);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int k = 0; k < G; ++k) racc[b] = mfma(rf[g * G + k], xq[g & 1][k], racc[b]);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(nullptr, NT / 2, NT);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  // the W^T fragments go out now, into the registers E and R held: they
-  // stream in under the gate, and only the write GEMM waits for them
-  __builtin_amdgcn_sched_barrier(0);
-  if constexpr (!SP) load_w(nullptr);
-  __builtin_amdgcn_sched_barrier(0);
   if (have) {
 #pragma unroll
     for (int b = 0; b < TB; ++b) {
