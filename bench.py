@@ -361,6 +361,9 @@ def bench_qkv(args, pkg, C, dev) -> dict:
     else:
         log(f"qkv: the calls ran one after the other (path {batch.path}); no single main kernel, "
             "roofline null")
+    cpu = None
+    if args.cpu_seconds > 0:
+        cpu = qkv_cpu_baseline(pkg, shapes, args.seed, args.cpu_seconds)
     return {
         "metric": METRIC, "value": round(T / (step_ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": K, "warmup": warmup, "ms_per_step": round(step_ms, 5),
@@ -370,8 +373,45 @@ def bench_qkv(args, pkg, C, dev) -> dict:
                    "pools": {"qk": shapes[0].N, "v": shapes[1].N}, "stats": args.stats,
                    "pool_cached": args.pool_cached, "parallelism": "single GPU"},
         "roofline": roofline,
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
+
+
+def qkv_cpu_baseline(pkg, shapes, seed, budget_s: float) -> dict:
+    """configs[1] on the host: the oracle's fused_gate_srw_paired (QK pool)
+    and fused_gate_srw (V pool) -- the reference's two calls of one layer,
+    v41:1036-1053 -- on the first 512 of the 4096 tokens of the same seeded
+    inputs, bf16 emulation (test infrastructure timed as the CPU
+    restatement; never part of the GPU path)."""
+    import torch
+    from oracle import srw_ref
+    torch.set_num_threads(min(os.cpu_count() or 1, CPU_THREADS_MAX))
+    T_s = min(shapes[0].T, 512)
+    qk = pkg.inputs.make_pool_inputs(shapes[0], seed=seed, T=T_s)
+    v = pkg.inputs.make_pool_inputs(shapes[1], seed=seed, T=T_s)
+
+    def fn():
+        srw_ref.fused_gate_srw_paired(qk["x"][None], qk["h"][None], qk["emb"],
+                                      qk["tau_offset"].reshape(1, T_s, 2, 1), qk["read"], qk["write"],
+                                      max_chunk_size=12500)
+        srw_ref.fused_gate_srw(v["x"][None], v["x"][None], v["emb"], v["tau_offset"][None], v["read"],
+                               v["write"], max_chunk_size=12500)
+
+    fn()  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    log(f"cpu baseline (qkv): T_sample={T_s} runs={len(times)} median={med * 1e3:.1f} ms "
+        f"threads={torch.get_num_threads()}")
+    return {"value": T_s / med, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            **host_cpus(),
+            "sample": (f"oracle fused_gate_srw_paired (QK, N={shapes[0].N}) + fused_gate_srw (V, "
+                       f"N={shapes[1].N}), bf16 emulation, first {T_s} of the {shapes[0].T} tokens, "
+                       f"median of {len(times)} runs; {cpu_model()}")}
 
 
 def bench_model(args, pkg, C, dev) -> dict:

@@ -192,6 +192,24 @@ def srw_inference_with_gates(x, h, emb, tau_offset, w_read, w_write,
 # fused_gate_srw: chunked bf16 two-pass layer with diagnostics (v41:415-635)
 # --------------------------------------------------------------------------
 
+def _unit_means(scores_f, red_axes):
+    """Per-unit mean score over every token row: (B, S) single, (B, S,
+    route) paired (v41:445, :725) -- the score_lb statistic."""
+    return scores_f.mean(dim=red_axes)
+
+
+def _route_mean(t):
+    """[B,S,2,1] -> [B,S,1]: the paired call's per-token diagnostics are the
+    mean over the two routes (v41:864-871)."""
+    return t.mean(dim=2)
+
+
+def _cell_count(B, S, R, N):
+    """(token, route, unit) cells the intensity-cap fraction is over:
+    B*S*2*N for the paired call (v41:900-901)."""
+    return float(B * S * R * N)
+
+
 def _pass1_stats(h_bf, emb_bf, nc, cs, n_total, route_axis: bool, exact: bool = False):
     """Pass 1 (v41:434-483; paired v41:713-763): exact stats over all chunks.
 
@@ -211,7 +229,7 @@ def _pass1_stats(h_bf, emb_bf, nc, cs, n_total, route_axis: bool, exact: bool = 
         sq_sum = sq_sum + (scores_f ** 2).sum(dim=-1, keepdim=True)
         cube_sum = cube_sum + (scores_f ** 3).sum(dim=-1, keepdim=True)
         quad_sum = quad_sum + (scores_f ** 4).sum(dim=-1, keepdim=True)
-        per_neuron = scores_f.mean(dim=red_axes)                   # :445 / :725
+        per_neuron = _unit_means(scores_f, red_axes)               # :445 / :725
         ns_sum = ns_sum + per_neuron.sum()
         ns_sq = ns_sq + (per_neuron ** 2).sum()
     s_mean = s_sum / n_total                                       # :461
@@ -404,13 +422,13 @@ def fused_gate_srw_paired(x, h, emb, tau_offset, read, write, *,
     ent = -safe_glogg / gate_sum_eps + torch.log(gate_sum_eps)
     ent = torch.where(torch.isfinite(ent), ent, torch.zeros((), dtype=F32))
     res = (
-        out_f, active_frac.mean(dim=2), gmax.mean(dim=2), st["score_lb"],
-        s_std.mean(), wsum.mean(), act_n.mean(), (strong / N).mean(dim=2),
-        (phi_bin / N).mean(dim=2), z_mean_active.mean(dim=2), tau.mean(),
+        out_f, _route_mean(active_frac), _route_mean(gmax), st["score_lb"],
+        s_std.mean(), wsum.mean(), act_n.mean(), _route_mean(strong / N),
+        _route_mean(phi_bin / N), _route_mean(z_mean_active), tau.mean(),
         (z075 / active_denom).mean(), (z030 / active_denom).mean(),
         st["score_skew"], act_n.std(correction=0), ent.mean(), zsum.mean(),
         st["score_kurt"], dead_pen, dead_cnt, int_max,
-        int_cap / float(B * S * R * N),
+        int_cap / _cell_count(B, S, R, N),                         # :900-901
     )
     if not return_trace:
         return res

@@ -4,6 +4,11 @@ diagnostics of the matrix-core path with dead units present.
 * configs[0] at float32 (_srw_inference, models/dawn_spatial_v41_exp.py
   :1713-1738): the full Know pool (N = 25 200, d = 384) on a 64-token
   subset of the T = 4096 batch (rows are token-independent), within 1e-5;
+* the QK (paired, N = 1580) and V (N = 2600) calls of one
+  attention layer at T = 4096, d_route = d_model = 384, as one
+  srw_forward_batch -- 258 tokens of each against the oracle's
+  fused_gate_srw_paired / fused_gate_srw (:640-909, :415-635), and every
+  row's whole-batch properties;
 * the 12-layer 40M model at vocab 32 000 -- one 64-token
   sequence against the oracle model (oracle/dawn_ref.py), and the full
   B = 32 x S = 512 forward checked for finiteness and causality;
@@ -111,6 +116,112 @@ def test_configs4_whole_batch_properties(scaled):
     assert torch.equal(got["n_active"][:, 0].long(), mask.sum(dim=1))
     words = got["pass_mask"][:, 0]
     assert not bool(unpack_mask(words, words.shape[-1] * 64)[:, N:].any())
+
+
+def _cfg1_rows(T):
+    """258 of configs[1]'s 4096 tokens: the first and last token tiles (128
+    rows each: every 32-row block and both tile edges of the main kernel) and
+    the two rows either side of the middle token-tile boundary."""
+    idx = list(range(0, 128)) + [2047, 2048] + list(range(T - 128, T))
+    return torch.tensor(sorted(set(idx)), dtype=torch.long)
+
+
+@pytest.fixture(scope="module")
+def qkv(pkg, dev):
+    """configs[1] as its workload: the T = 4096 QK call (one pool of 1580
+    units, Q and K routed independently, d_route = d_model = 384) and the V
+    call (2600 units, h = x) of one attention layer, issued as one
+    srw_forward_batch -- the bench's qkv line -- with the reference chunk
+    plan (max_chunk_size 12500: one chunk each)."""
+    bf = torch.bfloat16
+    plans, inps = [], []
+    for key in ("qk", "v"):
+        shape = pkg.inputs.CONFIGS[key]
+        inp = pkg.inputs.make_pool_inputs(shape, seed=0)
+        _, cs = srw_ref.chunk_plan(shape.N, 12500)
+        x = inp["x"].to(bf).to(dev)
+        h = x if shape.h_is_x else inp["h"].to(bf).to(dev)
+        plans.append(pkg.SrwPlan(x, h, inp["emb"].to(bf).to(dev), inp["tau_offset"].to(dev),
+                                 inp["read"].to(bf).to(dev), inp["write"].to(bf).to(dev),
+                                 chunk_size=cs, want_mask=True))
+        inps.append((shape, inp))
+    print(f"[gpu] configs[1] QK (paired, N{inps[0][0].N}) + V (N{inps[1][0].N}) at T{inps[0][0].T}, "
+          "one srw_forward_batch", flush=True)
+    batch = pkg.SrwBatchPlan(plans)
+    batch.launch()
+    torch.cuda.synchronize()
+    got = [{k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in p.results().items()
+            if k in ("out", "gate_sum", "den", "n_active", "pass_mask")} for p in batch.plans]
+    path = batch.path
+    del plans, batch
+    torch.cuda.empty_cache()
+    return inps, got, path
+
+
+def _rows_of(got, idx):
+    return {k: v[idx] for k, v in got.items()}
+
+
+def test_configs1_qk_paired_rows_match_oracle(qkv):
+    """The QK pool's paired call at configs[1]'s own shape against
+    fused_gate_srw_paired (v41:640-909), 258 tokens = 516 (token, route)
+    rows."""
+    from tests.test_gpu_mfma import _check
+    (shape, inp), got, path = qkv[0][0], qkv[1][0], qkv[2]
+    assert path == "mfma_batch_bf16", path
+    idx = _cfg1_rows(shape.T)
+    Ts, N, D = len(idx), shape.N, shape.D
+    print(f"[gpu] configs[1] QK rows {Ts} x 2 routes against the paired oracle", flush=True)
+    ref, tr = srw_ref.fused_gate_srw_paired(
+        inp["x"][idx][None], inp["h"][idx][None], inp["emb"], inp["tau_offset"][idx].reshape(1, Ts, 2, 1),
+        inp["read"], inp["write"], max_chunk_size=12500, return_trace=True)
+    flat = dict(margin=tr["margin"].reshape(2 * Ts, N), tau=tr["tau"].reshape(2 * Ts, 1),
+                s_std=tr["s_std"].reshape(2 * Ts, 1), den=tr["den"].reshape(2 * Ts),
+                gate_sum=tr["gate_sum"].reshape(2 * Ts), n_active=tr["n_active"].reshape(2 * Ts))
+    g = _rows_of(got, idx)
+    got2 = {k: v.reshape(2 * Ts, *v.shape[2:])[:, None] for k, v in g.items()}
+    _check(got2, (ref[0].reshape(2 * Ts, D),), flat, 2 * Ts, N, D)
+
+
+def test_configs1_v_rows_match_oracle(qkv):
+    """The V pool's call at configs[1]'s shape against fused_gate_srw
+    (v41:415-635), the same 258 tokens."""
+    from tests.test_gpu_mfma import _check
+    (shape, inp), got = qkv[0][1], qkv[1][1]
+    idx = _cfg1_rows(shape.T)
+    Ts = len(idx)
+    print(f"[gpu] configs[1] V rows {Ts} against the oracle", flush=True)
+    x = inp["x"][idx]
+    ref, tr = srw_ref.fused_gate_srw(x[None], x[None], inp["emb"], inp["tau_offset"][idx][None],
+                                     inp["read"], inp["write"], max_chunk_size=12500, return_trace=True)
+    _check(_rows_of(got, idx), ref, tr, Ts, shape.N, shape.D)
+
+
+@pytest.mark.parametrize("which", [0, 1], ids=["qk", "v"])
+def test_configs1_whole_batch_properties(qkv, which):
+    """Every row of both calls: finite outputs; den = max(sum intensity, 1)
+    >= 1 (the floor binds below N eps = 0.16 / 0.26, v41:584); n_active is
+    the mask's popcount and gate_sum / den agree with it (each active unit
+    adds act * intensity > 0.5 eps to the gate sum); no bits past N; about
+    half of the units pass (tau_offset -0.5: tau = mean - 0.5 std, margin =
+    s - mean)."""
+    (shape, _), got = qkv[0][which], qkv[1][which]
+    T, N, D, R = shape.T, shape.N, shape.D, shape.routes
+    print(f"[gpu] configs[1] {'QK' if which == 0 else 'V'} whole-batch properties T{T} R{R}", flush=True)
+    out = got["out"].float()
+    assert out.shape == (T, R, D) and bool(torch.isfinite(out).all())
+    assert bool((out.norm(dim=-1) > 0).all())
+    den, gs = got["den"], got["gate_sum"]
+    assert bool(torch.isfinite(den).all()) and bool((den >= 1.0).all())
+    mask = unpack_mask(got["pass_mask"].reshape(T * R, -1), N)
+    na = got["n_active"].reshape(T * R).long()
+    assert torch.equal(na, mask.sum(dim=1))
+    words = got["pass_mask"].reshape(T * R, -1)
+    assert not bool(unpack_mask(words, words.shape[-1] * 64)[:, N:].any())
+    assert bool((gs.reshape(-1) >= 0.5 * 1e-4 * na.float()).all())
+    frac = float(na.double().mean()) / N
+    print(f"  mean pass fraction {frac:.4f}", flush=True)
+    assert 0.45 <= frac <= 0.55
 
 
 @pytest.fixture(scope="module")

@@ -288,6 +288,78 @@ def test_paired_equals_two_singles():
         assert torch.allclose(pr[0][0, :, k], sg[0][0], rtol=0, atol=1e-6)
 
 
+# Per-token [B,S,1] outputs of the paired 22-tuple: route means (v41:864-871).
+_PAIRED_ROUTE_MEAN = ("active_frac", "gate_max", "strong_frac", "boundary_frac", "z_mean_active")
+
+
+def _paired_vs_single_mismatch(seed=17):
+    """The paired call's 22-tuple against ONE single-route call over the
+    2*B*S virtual rows (token t, route r) -> row (s, r) of a [B, 2S] batch,
+    with x repeated per route.  fused_gate_srw_paired's statistics are all
+    per (token, route) row over N (v41:713-763), so that single call holds
+    every row of it; its reductions then fix the paired ones:
+
+    * out: the single's rows, route by route (v41:854-860);
+    * active / gate-max / strong / boundary fractions and z_mean_active: the
+      mean over the two routes of the single's per-row values (v41:864-871);
+    * every scalar -- score_lb and the dead-unit penalty / count from per-unit
+      means and maxima over (B, S, 2) (v41:725, 817-818), the moments,
+      entropy, int_max, and int_cap_frac over B*S*2*N cells (v41:900-901) --
+      the single's scalar over its 2*B*S rows.
+
+    The single-route function is pinned against the brute-force loop, closed
+    forms and scipy above.  Inputs plant dead units and units capped at
+    max_intensity so that dead_count, dead_penalty and int_cap_frac are not
+    zero.  Returns the names that disagree."""
+    B, S, D, dr, N = 2, 6, 32, 16, 600
+    x, h, e, tau, r, w = _rand_inputs(B * S, D, dr, N, seed, dtype=F32, tau=0.0)
+    g = torch.Generator().manual_seed(seed + 1)
+    h2 = torch.stack([h, torch.randn(B * S, dr, generator=g)], dim=1)      # [T, 2, dr]
+    tau2 = torch.stack([tau, tau + 0.4], dim=1)                           # [T, 2, 1]
+    hm = h2.mean(dim=(0, 1))
+    e[:4] = 25.0 * hm / hm.norm() ** 2                                     # capped intensity
+    e[10:600:83] = -0.02 * hm / hm.norm()                                  # dead units
+    pr = srw_ref.fused_gate_srw_paired(x.reshape(B, S, D), h2.reshape(B, S, 2, dr), e,
+                                       tau2.reshape(B, S, 2, 1), r, w, max_chunk_size=100)
+    xs = x.reshape(B, S, 1, D).expand(B, S, 2, D).reshape(B, 2 * S, D)
+    sg = srw_ref.fused_gate_srw(xs, h2.reshape(B, 2 * S, dr), e, tau2.reshape(B, 2 * S, 1), r, w,
+                                max_chunk_size=100)
+    P = dict(zip(srw_ref.FUSED_OUTPUT_NAMES, pr))
+    Q = dict(zip(srw_ref.FUSED_OUTPUT_NAMES, sg))
+    assert float(Q["dead_count"]) >= 7 and float(Q["int_cap_frac"]) > 0 and float(Q["dead_penalty"]) > 0
+    bad = []
+    for name in srw_ref.FUSED_OUTPUT_NAMES:
+        p, q = P[name], Q[name]
+        if name == "out":
+            q = q.reshape(B, S, 2, D)
+        elif name in _PAIRED_ROUTE_MEAN:
+            q = q.reshape(B, S, 2, 1).mean(dim=2)
+        if p.shape != q.shape or not torch.allclose(p, q, rtol=2e-5, atol=1e-7):
+            bad.append(name)
+    return bad
+
+
+def test_paired_diagnostics_equal_one_single_over_route_rows():
+    assert _paired_vs_single_mismatch() == []
+
+
+PAIRED_MUTATIONS = {
+    # per-unit score means taken per route (over (B, S) only) for score_lb
+    "score_lb_per_route": ("_unit_means", lambda s, axes: s.mean(dim=axes[:2]), "score_lb"),
+    # the cap fraction over B*S*N cells (the single call's count)
+    "int_cap_over_BSN": ("_cell_count", lambda B, S, R, N: float(B * S * N), "int_cap_frac"),
+    # per-token fractions of route 0 instead of the route mean
+    "active_frac_unaveraged": ("_route_mean", lambda t: t[:, :, 0], "active_frac"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PAIRED_MUTATIONS))
+def test_planted_paired_diagnostic_mistakes_are_caught(monkeypatch, name):
+    attr, fn, field = PAIRED_MUTATIONS[name]
+    monkeypatch.setattr(srw_ref, attr, fn)
+    assert field in _paired_vs_single_mismatch()
+
+
 def test_den_floor_active_for_small_pools():
     T, D, dr, N = 8, 16, 16, 158
     x, h, e, tau, r, w = _rand_inputs(T, D, dr, N, 16, tau=2.5)
