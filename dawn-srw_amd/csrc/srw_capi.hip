@@ -65,6 +65,9 @@ size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
 // Device address of `scratch` per device, looked up once per device, with
 // that device current, on the first no-allocation call that runs there.
+// That call may come while the caller's stream is being captured into a HIP
+// graph: the lookup (no stream work) runs with this thread's capture mode
+// relaxed, so that a capture in global mode does not refuse it.
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
@@ -81,10 +84,14 @@ srw_status_t scratch_address(hipStream_t stream, void** out) {
   if (dev < 0 || dev >= kMaxDevices) return SRW_EUNSUPPORTED;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
-    if (dev != cur && hipSetDevice(dev) != hipSuccess) return SRW_EHIP;
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) return SRW_EHIP;
+    hipError_t e = hipSuccess;
+    if (dev != cur) e = hipSetDevice(dev);
     void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (dev != cur) (void)hipSetDevice(cur);
+    (void)hipThreadExchangeStreamCaptureMode(&mode);  // the caller's mode back
     if (e != hipSuccess || p == nullptr) return SRW_EHIP;
     g_scratch_ptr[dev] = p;
   }

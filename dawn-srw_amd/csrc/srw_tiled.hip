@@ -610,8 +610,14 @@ hipError_t set_lds(const void* fn) {
 
 }  // namespace
 
+// The operand loaders keep each lane's byte offset within a 256-row tile in
+// 32 bits: 256 rows of ld bf16 elements must stay below 4 GiB (ld = N or T
+// padded to 64 for the stored [., N64] / [., T64] arrays).
+static bool tile_offsets_fit(int64_t ld) { return 256 * ((ld + kNAlign - 1) / kNAlign * kNAlign) * 2 < (int64_t(1) << 32); }
+
 bool tiled_supports(const srw_desc_t& d) {
   if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41) return false;
+  if (!tile_offsets_fit(d.n_units)) return false;
   if (d.stats_mode != SRW_STATS_ONEPASS && d.stats_mode != SRW_STATS_CENTERED) return false;
   // SRW_FLAG_SPARSE_SKIP runs dense here: no 32-token x 32-unit block of a
   // prefill call is free of passing units at the reference's pass rates
@@ -1405,6 +1411,7 @@ bool tiled_backward_supports(const srw_desc_t& d) {
   if (d.n_routes != 1 && d.n_routes != 2) return false;
   if (d.d_model % kNAlign != 0 || d.d_route % kNAlign != 0) return false;
   if (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
+  if (!tile_offsets_fit(d.n_units) || !tile_offsets_fit(d.T * d.n_routes)) return false;
   return d.scale != 0.0f;
 }
 

@@ -1,8 +1,10 @@
 // srw_tiled_f32.hip -- fp32 SRW forward on the fp32 matrix cores
 // (v_mfma_f32_32x32x2_f32): the dtype-preserving fp32 `_srw_inference`
-// (v41:1713-1738: centred two-pass statistics, one chunk) and fp32
-// fused_gate_srw calls (one-pass statistics; in fp32 the chunk plan changes
-// no rounding: every chunk's partial write GEMM stays fp32, v41:518).
+// (v41:1713-1738: centred two-pass statistics, one chunk), and fp32 calls
+// with one-pass statistics -- an extension with no reference counterpart
+// (the reference's fused_gate_srw casts every operand to bf16, v41:422-428),
+// checked against this library's scalar kernels only; in fp32 the chunk
+// plan changes no rounding (every chunk's partial write GEMM stays fp32).
 //
 // The layer runs as the bf16 tiled family does (srw_tiled.hip), with every
 // operand and intermediate in fp32:
@@ -579,6 +581,9 @@ FLayout flayout(const srw_desc_t& d, const FGeo& g) {
 
 bool tiled_f32_supports(const srw_desc_t& d) {
   if (d.dtype != SRW_F32 || d.gate != SRW_GATE_V41) return false;
+  // operand offsets within a 256-row tile are 32-bit: 256 rows of the
+  // [T, N64] fp32 scores / P must stay below 4 GiB
+  if (256 * ((d.n_units + 63) / 64 * 64) * 4 >= (int64_t(1) << 32)) return false;
   if (d.stats_mode != SRW_STATS_ONEPASS && d.stats_mode != SRW_STATS_CENTERED) return false;
   if (d.flags & (SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST)) return false;
   if (d.n_routes != 1 && d.n_routes != 2) return false;

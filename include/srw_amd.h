@@ -32,6 +32,10 @@
  *          tuple of :2324-2333): cotangents of out, score_lb and
  *          dead_penalty (the outputs the loss uses, :586-603) in, gradients of
  *          x, h, emb, tau_offset, read and write out
+ *   srw_forward, dtype = SRW_F32, SRW_STATS_ONEPASS
+ *       -> no reference counterpart (an extension: the reference's
+ *          fused_gate_srw casts every operand to bf16, v41:422-428); checked
+ *          against this library's scalar kernels only (parity unpinned)
  *   the closure constants of the factories (v41:297-301, 352-383) travel in
  *   srw_desc_t; srw_desc_init() fills the reference defaults.
  *
@@ -43,8 +47,10 @@
  *   - x, h, emb, read, write and out share desc->dtype (SRW_BF16 or SRW_F32).
  *     tau_offset and every per-token / per-unit statistic are float32.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream) and
- *     is asynchronous.  The library keeps no state between calls and is
- *     thread-safe; calls that share a workspace must not overlap.
+ *     is asynchronous.  srw_forward keeps no state between calls beyond the
+ *     caller's workspace and is thread-safe; calls that share a workspace
+ *     must not overlap (srw_forward_noalloc: every call on one GPU shares
+ *     its scratch).
  *   - Errors are status codes; no C++ exception crosses the ABI.  NaN / Inf
  *     inputs propagate as in the reference (no extra clamping).
  */

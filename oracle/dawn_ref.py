@@ -72,6 +72,22 @@ def _dense(x, prm):
     return x @ prm["kernel"] + prm["bias"]
 
 
+def _route_blocks(h_all, dr):
+    """h_Q, h_K, h_V: the router output split in three along the last axis
+    (jnp.split(h_all, 3, axis=-1), v41:1019)."""
+    return h_all[..., :dr], h_all[..., dr:2 * dr], h_all[..., 2 * dr:]
+
+
+def _tau_columns(tau_all):
+    """tau_offset of Q, K and V: columns 0, 1, 2 of the tau router (v41:1036, :1053)."""
+    return tau_all[..., 0:1], tau_all[..., 1:2], tau_all[..., 2:3]
+
+
+def _qk_scaled(QK, qk_scale):
+    """Q and K from the paired call's two routes, both times qk_scale (v41:1044-1045)."""
+    return QK[:, :, 0, :] * qk_scale, QK[:, :, 1, :] * qk_scale
+
+
 def forward(params, cfg, input_ids, *, max_chunk_size=None):
     """logits [B, S, vocab] of DAWN.__call__(input_ids, deterministic=True)."""
     chunk = cfg.max_chunk_size if max_chunk_size is None else max_chunk_size
@@ -82,16 +98,14 @@ def forward(params, cfg, input_ids, *, max_chunk_size=None):
     for i in range(cfg.n_layers):
         bp = params[f"block_{i}"]
         normed = layer_norm(x, bp["norm1"]["scale"], bp["norm1"]["bias"])          # :1412-1413
-        h_all = _dense(normed, rt["proj_attn"])                                  # :1018
-        h_Q, h_K, h_V = h_all[..., :dr], h_all[..., dr:2 * dr], h_all[..., 2 * dr:]
-        tau_all = _dense(normed, rt["tau_attn"])                                 # :1022
+        h_Q, h_K, h_V = _route_blocks(_dense(normed, rt["proj_attn"]), dr)       # :1018-1019
+        t_Q, t_K, t_V = _tau_columns(_dense(normed, rt["tau_attn"]))             # :1022
         h_QK = torch.stack([h_Q, h_K], dim=2)                                    # :1035
-        tau_QK = torch.stack([tau_all[..., 0:1], tau_all[..., 1:2]], dim=2)      # :1036
+        tau_QK = torch.stack([t_Q, t_K], dim=2)                                  # :1036
         QK = srw_ref.fused_gate_srw_paired(normed, h_QK, pool["qk_emb"], tau_QK, pool["qk_read"],
                                            pool["qk_write"], max_chunk_size=chunk)[0]
-        Q = QK[:, :, 0, :] * pool["qk_scale"]                                    # :1044-1045
-        K = QK[:, :, 1, :] * pool["qk_scale"]
-        V = srw_ref.fused_gate_srw(normed, h_V, pool["v_emb"], tau_all[..., 2:3], pool["v_read"],
+        Q, K = _qk_scaled(QK, pool["qk_scale"])                                  # :1044-1045
+        V = srw_ref.fused_gate_srw(normed, h_V, pool["v_emb"], t_V, pool["v_read"],
                                    pool["v_write"], max_chunk_size=chunk)[0] * pool["v_scale"]  # :1046-1053
         a = _merge(causal_attention(_heads(Q, H), _heads(K, H), _heads(V, H)))   # :1056-1081
         x = x + a @ bp["attn"]["expand_O"]["kernel"]                             # :1082, :1438
@@ -115,12 +129,11 @@ def _srw_inf(x, h, emb, tau, read, write, srw_dtype):
 def _attn_qkv(normed, params, cfg, srw_dtype):
     pool, rt = params["neuron_pool"], params["router"]
     dr = cfg.d_route
-    h_all = _dense(normed, rt["proj_attn"])                                      # :1784 / :1866
-    h_Q, h_K, h_V = h_all[..., :dr], h_all[..., dr:2 * dr], h_all[..., 2 * dr:]
-    tau_all = _dense(normed, rt["tau_attn"])
-    Q = _srw_inf(normed, h_Q, pool["qk_emb"], tau_all[..., 0:1], pool["qk_read"], pool["qk_write"], srw_dtype)
-    K = _srw_inf(normed, h_K, pool["qk_emb"], tau_all[..., 1:2], pool["qk_read"], pool["qk_write"], srw_dtype)
-    V = _srw_inf(normed, h_V, pool["v_emb"], tau_all[..., 2:3], pool["v_read"], pool["v_write"], srw_dtype)
+    h_Q, h_K, h_V = _route_blocks(_dense(normed, rt["proj_attn"]), dr)           # :1784 / :1866
+    t_Q, t_K, t_V = _tau_columns(_dense(normed, rt["tau_attn"]))
+    Q = _srw_inf(normed, h_Q, pool["qk_emb"], t_Q, pool["qk_read"], pool["qk_write"], srw_dtype)
+    K = _srw_inf(normed, h_K, pool["qk_emb"], t_K, pool["qk_read"], pool["qk_write"], srw_dtype)
+    V = _srw_inf(normed, h_V, pool["v_emb"], t_V, pool["v_read"], pool["v_write"], srw_dtype)
     return Q * pool["qk_scale"], K * pool["qk_scale"], V * pool["v_scale"]      # :1794-1799, :1876-1880
 
 

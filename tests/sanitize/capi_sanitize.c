@@ -52,7 +52,10 @@ int main(void) {
   const int64_t Ts[] = {0, 1, 7, 64, 129, 4096};
   const int64_t Ds[] = {40, 64, 128, 384, 1024};
   const int64_t drs[] = {24, 32, 64, 128, 384, 1024};
-  const int64_t Ns[] = {1, 33, 100, 1580, 25200};
+  /* 4194304 / 8388608 units: the fp32 / bf16 tiled families' 32-bit tile
+     offsets end there (256 rows x N64 x 4 or 2 bytes = 4 GiB); such shapes
+     fall back to other families */
+  const int64_t Ns[] = {1, 33, 100, 1580, 25200, 4194304, 8388608};
   const uint32_t flag_sets[] = {0, SRW_FLAG_DIAG, SRW_FLAG_EMULATE, SRW_FLAG_SPARSE_SKIP, SRW_FLAG_NO_FAST,
                                 SRW_FLAG_POOL_CACHED, SRW_FLAG_TILED, SRW_FLAG_DIAG | SRW_FLAG_POOL_CACHED};
   long sized = 0, unsupported = 0;

@@ -37,7 +37,7 @@ def test_bin_dataset_rows_and_batches(pkg, tmp_path):
     assert ds.get_batch(14, 8).shape == (1, 64)               # short last batch
     assert ds.get_batch(15, 8) is None
     assert len(pkg.data.BinDataset(str(path), seq_len=64, max_sequences=5)) == 5
-    with pytest.raises(ValueError, match="Not enough tokens"):
+    with pytest.raises(ValueError, match="no full row"):
         pkg.data.BinDataset(str(path), seq_len=4096)
 
 

@@ -95,3 +95,105 @@ def test_prefill_then_decode_equals_longer_prefill(tiny, srw_dtype):
     assert torch.allclose(cK2[:, :, :, :10], fK[:, :, :, :10], rtol=1e-4, atol=1e-6)
     assert torch.allclose(cV2[:, :, :, :10], fV[:, :, :, :10], rtol=1e-4, atol=1e-6)
     assert torch.count_nonzero(cK2[:, :, :, 10:]) == 0
+
+
+# ---------------------------------------------------------------- router split, tau columns, scales
+
+def _attn_params(cfg, p, seed):
+    """One layer, the Know branch off (know_scale 0), distinct tau routers for
+    Q, K and V (kernel and bias), so that the attention half of the block is
+    the whole residual update."""
+    g = torch.Generator().manual_seed(seed)
+    q = {k: (dict(v) if isinstance(v, dict) else v) for k, v in p.items()}
+    q["neuron_pool"] = dict(p["neuron_pool"], know_scale=torch.zeros(1))
+    q["router"] = dict(p["router"], tau_attn={"kernel": 0.3 * torch.randn(cfg.d_model, 3, generator=g),
+                                              "bias": torch.tensor([-0.6, -0.1, 0.3])})
+    q["router"]["proj_attn"] = {"kernel": p["router"]["proj_attn"]["kernel"],
+                                "bias": 0.5 * torch.randn(3 * cfg.d_route, generator=g)}
+    return q
+
+
+def _one_layer(cfg):
+    return type(cfg)(**{**cfg.__dict__, "n_layers": 1})
+
+
+def _attention_by_single_calls(p, cfg, ids):
+    """The attention block of v41:1018-1082 written from single-route calls:
+    h = LN(x) W + b split in three column blocks (Q, K, V in that order,
+    :1019), tau columns 0 / 1 / 2 (:1022, :1036, :1053), Q and K each from
+    fused_gate_srw on their own block times qk_scale (:1044-1045), V times
+    v_scale, torch's causal scaled_dot_product_attention, then expand_O."""
+    from oracle import srw_ref
+    B, S = ids.shape
+    D, dr, H = cfg.d_model, cfg.d_route, cfg.n_heads
+    pool, rt, bp = p["neuron_pool"], p["router"], p["block_0"]
+    x = p["token_emb"]["embedding"][ids] + p["pos_emb"]["embedding"][:S][None]
+    n = F.layer_norm(x, (D,), bp["norm1"]["scale"], bp["norm1"]["bias"], eps=1e-6)
+    h = n @ rt["proj_attn"]["kernel"] + rt["proj_attn"]["bias"]
+    t = n @ rt["tau_attn"]["kernel"] + rt["tau_attn"]["bias"]
+    one = lambda k, emb, rd, wr: srw_ref.fused_gate_srw(  # noqa: E731
+        n, h[..., k * dr:(k + 1) * dr], emb, t[..., k:k + 1], rd, wr, max_chunk_size=cfg.max_chunk_size)[0]
+    Q = one(0, pool["qk_emb"], pool["qk_read"], pool["qk_write"]) * pool["qk_scale"]
+    K = one(1, pool["qk_emb"], pool["qk_read"], pool["qk_write"]) * pool["qk_scale"]
+    V = one(2, pool["v_emb"], pool["v_read"], pool["v_write"]) * pool["v_scale"]
+    hd = lambda u: u.reshape(B, S, H, D // H).transpose(1, 2)  # noqa: E731
+    a = F.scaled_dot_product_attention(hd(Q), hd(K), hd(V), is_causal=True)
+    x = x + a.transpose(1, 2).reshape(B, S, D) @ bp["attn"]["expand_O"]["kernel"]
+    x = F.layer_norm(x, (D,), p["norm"]["scale"], p["norm"]["bias"], eps=1e-6)
+    return x @ p["token_emb"]["embedding"].T
+
+
+def _attn_block_mismatch(tiny):
+    cfg, p = tiny
+    cfg1 = _one_layer(cfg)
+    q = _attn_params(cfg1, p, 21)
+    ids = _ids(2, 11, cfg.vocab_size, 22)
+    want = _attention_by_single_calls(q, cfg1, ids)
+    got = dawn_ref.forward(q, cfg1, ids)
+    return float((got - want).abs().max() / want.abs().max())
+
+
+def test_attention_block_matches_single_route_formulation(tiny):
+    """dawn_ref.forward's paired QK call, router split, tau columns and
+    qk_scale placement against the block written from single-route calls
+    and library attention (paired == two singles to ~1e-6)."""
+    assert _attn_block_mismatch(tiny) < 1e-4
+
+
+def _sign_flip_diff(tiny):
+    cfg, p = tiny
+    q = _attn_params(cfg, p, 23)
+    ids = _ids(2, 9, cfg.vocab_size, 24)
+    neg = dict(q, neuron_pool=dict(q["neuron_pool"], qk_scale=-q["neuron_pool"]["qk_scale"]))
+    d_fwd = (dawn_ref.forward(q, cfg, ids) - dawn_ref.forward(neg, cfg, ids)).abs().max()
+    d_pre = (dawn_ref.prefill(q, cfg, ids)[0] - dawn_ref.prefill(neg, cfg, ids)[0]).abs().max()
+    return float(max(d_fwd, d_pre))
+
+
+def test_qk_scale_sign_flip_leaves_logits_unchanged(tiny):
+    """Q and K both carry qk_scale (v41:1044-1045, :1794-1797), so the
+    attention logits Q K^T -- and everything after them -- are unchanged
+    when qk_scale changes sign (the SRW outputs are linear in the scale), in
+    forward and in prefill; a scale on one of the two flips every logit."""
+    assert _sign_flip_diff(tiny) <= 1e-6
+
+
+MODEL_MUTATIONS = {
+    # h_Q and h_K blocks of the router taken in the wrong order
+    "router_blocks_swapped": ("_route_blocks", lambda h, dr: (h[..., dr:2 * dr], h[..., :dr], h[..., 2 * dr:])),
+    # tau columns of Q and K swapped
+    "tau_columns_swapped": ("_tau_columns", lambda t: (t[..., 1:2], t[..., 0:1], t[..., 2:3])),
+    # qk_scale applied to Q only
+    "qk_scale_on_q_only": ("_qk_scaled", lambda QK, s: (QK[:, :, 0, :] * s, QK[:, :, 1, :])),
+}
+
+
+@pytest.mark.parametrize("name", sorted(MODEL_MUTATIONS))
+def test_planted_router_and_scale_mistakes_are_caught(tiny, monkeypatch, name):
+    attr, fn = MODEL_MUTATIONS[name]
+    monkeypatch.setattr(dawn_ref, attr, fn)
+    mis = _attn_block_mismatch(tiny)
+    print(f"  {name}: block mismatch {mis:.2e}", flush=True)
+    assert mis >= 1e-3
+    if name == "qk_scale_on_q_only":
+        assert _sign_flip_diff(tiny) > 1e-4

@@ -45,6 +45,46 @@ def _noalloc(pkg, plan, stream):
     return st, outs
 
 
+def test_noalloc_first_call_under_graph_capture(pkg, dev):
+    """The first srw_forward_noalloc call of the process on this GPU -- the
+    one that looks up the scratch's device address -- made while the stream
+    is being captured into a graph (torch.cuda.graph, global capture mode).
+    The graph is replayed three times, with eager work and a synchronisation
+    between the replays and the outputs refilled with a sentinel before
+    each; every replay equals srw_forward with a caller workspace bit for
+    bit.  (This test comes first in the file so that no other no-allocation
+    call precedes it.)"""
+    shape = pkg.inputs.CONFIGS["decode_qk"]
+    print(f"[gpu] noalloc first call under capture: decode_qk T64 N{shape.N} R{shape.routes}", flush=True)
+    plan = _plan(pkg, shape, 64, seed=9)
+    C = pkg._capi
+    eager = torch.cuda.current_stream(dev)
+    plan.launch(eager)                     # the reference result; also loads the kernels
+    torch.cuda.synchronize()
+    want = {k: getattr(plan, k).clone() for k in KEYS}
+    outs = {k: torch.full_like(want[k], -7) for k in KEYS}
+    o = C.SrwOutputs(*(ctypes.c_void_p(outs[k].data_ptr()) for k in KEYS), None, None, None)
+    lib = C.load_library()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream(dev)
+    cap.wait_stream(eager)
+    with torch.cuda.graph(graph, stream=cap):
+        st = lib.srw_forward_noalloc(ctypes.byref(plan._desc), ctypes.byref(plan._tens), ctypes.byref(o),
+                                     ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    torch.cuda.synchronize()
+    assert st == C.SRW_OK, lib.srw_status_string(st)
+    for rep in range(3):
+        for k in KEYS:
+            outs[k].fill_(-7)
+        plan.launch(eager)                 # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for k in KEYS:
+            assert torch.equal(outs[k], want[k]), (rep, k)
+        print(f"  replay {rep + 1}: equal bit for bit", flush=True)
+
+
 @pytest.mark.parametrize("key,sizes", [("decode_know", (64, 16)), ("v", (256, 100)), ("decode_qk", (64, 7))])
 def test_noalloc_equals_srw_forward(pkg, dev, key, sizes):
     shape = pkg.inputs.CONFIGS[key]
