@@ -265,14 +265,119 @@ __host__ __device__ inline int64_t score_tile_off(int ntiles, int64_t ttile, int
 // running (count, mean, M2) by Chan et al.'s pairwise update, and
 // srw_tau_kernel merges the splits the same way.
 constexpr int kStatsPlain = 0, kStatsDiag = 1, kStatsChan = 3;
+// A lane's running moments of one row's scores over the tiles of an N-split
+// (the moments kernel, and the one-launch decode kernel, which runs the same
+// arithmetic so that both give the same bits).  kStatsPlain / kStatsDiag:
+// s1..s4 = sum s^k of the lane's elements; kStatsChan: cn, cmean = the
+// split's unit count and mean so far, s1 = sum s, s2 = the centred sum of
+// squares (both lane halves).
+struct MomState {
+  float s1, s2, s3, s4, cn, cmean;
+};
+
+// Join one 32-unit tile (sp: the lane's 16 packed bf16 scores, v41:503, in
+// accumulator order) to the state; units outside [lo, hi) enter as zeros.
+template <int MODE>
+__device__ __attribute__((always_inline)) inline void moment_tile(MomState& m, const uint32_t (&sp)[8], int64_t u0,
+                                                                   int64_t lo, int64_t hi, int half) {
+  const bool full = u0 >= lo && u0 + kUnitTile <= hi;
+  if constexpr (MODE == kStatsChan) {
+    // this tile's units in the split, their sum and sum of squares about
+    // their mean (both lane halves), joined to the running (count, mean, M2)
+    const int64_t c_lo = u0 > lo ? u0 : lo, c_hi = u0 + kUnitTile < hi ? u0 + kUnitTile : hi;
+    const float nt = static_cast<float>(c_hi > c_lo ? c_hi - c_lo : 0);
+    float xs[16];
+    bool oks[16];
+    float ts = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      bool ok0 = true, ok1 = true;
+      if (!full) {
+        const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
+        ok0 = ua >= lo && ua < hi;
+        ok1 = ub >= lo && ub < hi;
+      }
+      xs[v] = ok0 ? lo_f32(sp[v >> 1]) : 0.f;
+      xs[v + 1] = ok1 ? hi_f32(sp[v >> 1]) : 0.f;
+      oks[v] = ok0;
+      oks[v + 1] = ok1;
+      ts += xs[v];
+      ts += xs[v + 1];
+    }
+    ts += __shfl_xor(ts, 32);
+    if (nt > 0.f) {
+      const float mt = ts / nt;
+      float m2 = 0.f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float dv = oks[v] ? xs[v] - mt : 0.f;
+        m2 += __fmul_rn(dv, dv);
+      }
+      m2 += __shfl_xor(m2, 32);
+      const float nn = m.cn + nt, dl = mt - m.cmean;
+      m.cmean += dl * (nt / nn);
+      m.s2 += m2 + dl * dl * (m.cn * nt / nn);
+      m.s1 += ts;
+      m.cn = nn;
+    }
+  } else {
+    // sum s and sum s^2 of a packed bf16 pair in one v_dot2c_f32_bf16 each
+    // (the squares of bf16 values are exact in fp32)
+    const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      uint32_t q = sp[v >> 1];
+      if (!full) {
+        const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
+        const bool ok0 = ua >= lo && ua < hi, ok1 = ub >= lo && ub < hi;
+        q &= (ok0 ? 0x0000ffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
+      }
+      const bf16x2_t sb = __builtin_bit_cast(bf16x2_t, q);
+      m.s1 = __builtin_amdgcn_fdot2_f32_bf16(sb, ones, m.s1, false);
+      m.s2 = __builtin_amdgcn_fdot2_f32_bf16(sb, sb, m.s2, false);
+      if constexpr (MODE == kStatsDiag) {
+        const float x0 = lo_f32(q), x1 = hi_f32(q);
+        const float q0 = __fmul_rn(x0, x0), q1 = __fmul_rn(x1, x1);
+        m.s3 += __fmul_rn(q0, x0);
+        m.s4 += __fmul_rn(q0, q0);
+        m.s3 += __fmul_rn(q1, x1);
+        m.s4 += __fmul_rn(q1, q1);
+      }
+    }
+  }
+}
+
+// The split's partial of row t: mom[split][t][MS] = (sum s, sum s^2 [, sum
+// s^3, sum s^4]) or, kStatsChan, (sum s, M2, count); lane halves joined.
+template <int MODE>
+__device__ __attribute__((always_inline)) inline void moment_store(MomState m, float* mom, int split, int64_t T,
+                                                                    int64_t t, int half) {
+  constexpr int MS = MODE == kStatsDiag ? 4 : (MODE == kStatsChan ? 3 : 2);
+  if constexpr (MODE != kStatsChan) {  // (the Chan sums already hold both lane halves)
+    m.s1 += __shfl_xor(m.s1, 32);
+    m.s2 += __shfl_xor(m.s2, 32);
+  }
+  if constexpr (MODE == kStatsDiag) {
+    m.s3 += __shfl_xor(m.s3, 32);
+    m.s4 += __shfl_xor(m.s4, 32);
+  }
+  if (half == 0 && t < T) {
+    float* q = mom + (static_cast<int64_t>(split) * T + t) * MS;
+    q[0] = m.s1;
+    q[1] = m.s2;
+    if constexpr (MODE == kStatsDiag) {
+      q[2] = m.s3;
+      q[3] = m.s4;
+    }
+    if constexpr (MODE == kStatsChan) q[2] = m.cn;
+  }
+}
+
 // TBW 32-token blocks per wave (128 TBW tokens per workgroup): each E
 // fragment read from LDS feeds TBW MFMAs, and a CU's E stream serves
 // 128 TBW tokens.
 template <int KH, int MODE, int TBW>
 __device__ __attribute__((always_inline)) inline void stats_body(const StatsParams& p, const int bid) {
-  constexpr bool DG = MODE == kStatsDiag;
-  constexpr bool CHAN = MODE == kStatsChan;
-  constexpr int MS = DG ? 4 : (CHAN ? 3 : 2);
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int STAGE = KH * kFragBytes;
   constexpr int DR = KH * 16;
@@ -324,10 +429,9 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
 #pragma unroll
   for (int m = 0; m < TileE::NM; ++m) le[m] = TileE::lane_off(lane, m);
 
-  float s1[TBW], s2[TBW], s3[TBW], s4[TBW];
-  float cn[TBW], cmean[TBW];  // kStatsChan: the running unit count and mean (s1: sum, s2: M2, both lane halves)
+  MomState ms[TBW];
 #pragma unroll
-  for (int b = 0; b < TBW; ++b) s1[b] = s2[b] = s3[b] = s4[b] = cn[b] = cmean[b] = 0.f;
+  for (int b = 0; b < TBW; ++b) ms[b] = MomState{};
   // score store (plain moments, one block per wave): each tile's packed
   // scores go out at the start of the next tile's MFMAs, so the stores have
   // a whole tile to complete before the end-of-tile vmcnt wait.  A tile that
@@ -383,7 +487,6 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
       __builtin_amdgcn_sched_barrier(0);
     }
     const int64_t u0 = static_cast<int64_t>(tile) * kUnitTile;
-    const bool full = u0 >= lo && u0 + kUnitTile <= hi;
     if constexpr (STORE) {
       // the bf16 scores (v41:503), packed whether or not this split stores
       // them: a conditional assignment would keep the previous tile's words
@@ -393,77 +496,14 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
       if (p.s_out && u0 >= lo)
         sdst = reinterpret_cast<char*>(p.s_out) + score_tile_off(p.g.ntiles, ttile, tile, wave) + lane * 16;
     }
-    if constexpr (CHAN) {
-      // this tile's units in the split, their sum and sum of squares about
-      // their mean (both lane halves), joined to the running (count, mean, M2)
-      const int64_t c_lo = u0 > lo ? u0 : lo, c_hi = u0 + kUnitTile < hi ? u0 + kUnitTile : hi;
-      const float nt = static_cast<float>(c_hi > c_lo ? c_hi - c_lo : 0);
-#pragma unroll
-      for (int b = 0; b < TBW; ++b) {
-        float xs[16];
-        bool oks[16];
-        float ts = 0.f;
-#pragma unroll
-        for (int v = 0; v < 16; v += 2) {
-          const uint32_t sp = pack_bf16(acc[b][v], acc[b][v + 1]);  // the bf16 scores (v41:503)
-          bool ok0 = true, ok1 = true;
-          if (!full) {
-            const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
-            ok0 = ua >= lo && ua < hi;
-            ok1 = ub >= lo && ub < hi;
-          }
-          xs[v] = ok0 ? lo_f32(sp) : 0.f;
-          xs[v + 1] = ok1 ? hi_f32(sp) : 0.f;
-          oks[v] = ok0;
-          oks[v + 1] = ok1;
-          ts += xs[v];
-          ts += xs[v + 1];
-        }
-        ts += __shfl_xor(ts, 32);
-        if (nt > 0.f) {
-          const float mt = ts / nt;
-          float m2 = 0.f;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const float dv = oks[v] ? xs[v] - mt : 0.f;
-            m2 += __fmul_rn(dv, dv);
-          }
-          m2 += __shfl_xor(m2, 32);
-          const float nn = cn[b] + nt, dl = mt - cmean[b];
-          cmean[b] += dl * (nt / nn);
-          s2[b] += m2 + dl * dl * (cn[b] * nt / nn);
-          s1[b] += ts;
-          cn[b] = nn;
-        }
-      }
-    } else {
-    // sum s and sum s^2 of a packed bf16 pair in one v_dot2c_f32_bf16 each
-    // (the squares of bf16 values are exact in fp32); units outside the
-    // split's range enter as zeros
-    const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+    // this tile's moments (v41:441-444): the packed bf16 scores (v41:503),
+    // units outside the split excluded
 #pragma unroll
     for (int b = 0; b < TBW; ++b) {
+      uint32_t sp[8];
 #pragma unroll
-      for (int v = 0; v < 16; v += 2) {
-        uint32_t sp = pack_bf16(acc[b][v], acc[b][v + 1]);
-        if (!full) {
-          const int64_t ua = u0 + unit_of_acc(v, half), ub = u0 + unit_of_acc(v + 1, half);
-          const bool ok0 = ua >= lo && ua < hi, ok1 = ub >= lo && ub < hi;
-          sp &= (ok0 ? 0x0000ffffu : 0u) | (ok1 ? 0xffff0000u : 0u);
-        }
-        const bf16x2_t sb = __builtin_bit_cast(bf16x2_t, sp);
-        s1[b] = __builtin_amdgcn_fdot2_f32_bf16(sb, ones, s1[b], false);
-        s2[b] = __builtin_amdgcn_fdot2_f32_bf16(sb, sb, s2[b], false);
-        if constexpr (DG) {
-          const float x0 = lo_f32(sp), x1 = hi_f32(sp);
-          const float q0 = __fmul_rn(x0, x0), q1 = __fmul_rn(x1, x1);
-          s3[b] += __fmul_rn(q0, x0);
-          s4[b] += __fmul_rn(q0, q0);
-          s3[b] += __fmul_rn(q1, x1);
-          s4[b] += __fmul_rn(q1, q1);
-        }
-      }
-    }
+      for (int v = 0; v < 16; v += 2) sp[v >> 1] = pack_bf16(acc[b][v], acc[b][v + 1]);
+      moment_tile<MODE>(ms[b], sp, u0, lo, hi, half);
     }
     wait_vm0();
     __syncthreads();
@@ -472,26 +512,7 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
     if (sdst) store_scores();
   }
 #pragma unroll
-  for (int b = 0; b < TBW; ++b) {
-    if constexpr (!CHAN) {  // (the Chan sums already hold both lane halves)
-      s1[b] += __shfl_xor(s1[b], 32);
-      s2[b] += __shfl_xor(s2[b], 32);
-    }
-    if constexpr (DG) {
-      s3[b] += __shfl_xor(s3[b], 32);
-      s4[b] += __shfl_xor(s4[b], 32);
-    }
-    if (half == 0 && tt[b] < p.g.T) {
-      float* m = p.mom + (static_cast<int64_t>(split) * p.g.T + tt[b]) * MS;
-      m[0] = s1[b];
-      m[1] = s2[b];
-      if constexpr (DG) {
-        m[2] = s3[b];
-        m[3] = s4[b];
-      }
-      if constexpr (CHAN) m[2] = cn[b];
-    }
-  }
+  for (int b = 0; b < TBW; ++b) moment_store<MODE>(ms[b], p.mom, split, p.g.T, tt[b], half);
 }
 
 template <int KH, int MODE, int TBW>
@@ -515,6 +536,41 @@ enum { TP_SMAX = 4, TP_STRONG, TP_BOUND, TP_075, TP_030, TP_CAP, TP_GLOGG };
 // Rows of the main kernel are "virtual tokens" v = t * routes + r: h, tau,
 // outputs and every partial are indexed by v, x by v / routes (paired QK runs
 // as 2T rows sharing each x row).
+// Per-row tau from the moment partials (srw_tau_kernel).
+struct TauParams {
+  const float* mom;
+  const float* tau_off;
+  float* tau;
+  int64_t T;
+  int S_st;
+  int64_t N;
+  int ms;
+  float* token_diag;
+  int mode;
+  float* sstd;  // [T] s_std per row, or null
+  int upp;      // kTauChan: units per partial
+};
+
+// The finalize of a call: reduce the N-splits' partials (srw_finalize_kernel).
+struct FinalParams {
+  const float* out_part;
+  const float* tok_part;
+  uint16_t* out;         // [T, D] bf16
+  float* gate_sum;
+  float* den;
+  int32_t* n_active;
+  int64_t T;
+  int D, S, spc;
+  int S_tok;             // per-token partial slots in tok_part (S for the fused kernels)
+  float scale;
+  int tps;               // floats per (split, row) in tok_part: 4, or kTokPartDiag with diagnostics
+  const float* tau;      // [T] (diagnostics)
+  float* token_diag;     // [T][SRW_TDIAG_COUNT] or null
+  GateParams gp;
+  float exp_scale;
+  int den_gate;          // den = max(sum gate, 1) (the v4.0.1 gate, v401:340)
+};
+
 struct MainParams {
   const uint16_t* x;     // [T / routes, D]
   const uint16_t* h;     // [T, dr] (== x when HX)
@@ -1843,80 +1899,122 @@ __global__ __launch_bounds__(kWsThreads, 1) void srw_main_ss_batch_kernel(Batch<
 // mode kTauOnePass: std = sqrt(E[s^2] - mean^2) + 1e-8; kTauChan: std =
 // sqrt(M2 / N) + 1e-8 (v41:1719-1721) with M2 the partials' centred sums of
 // squares merged by Chan et al.'s formula.
-struct TauParams {
-  const float* mom;
-  const float* tau_off;
-  float* tau;
-  int64_t T;
-  int S_st;
-  int64_t N;
-  int ms;
-  float* token_diag;
-  int mode;
-  float* sstd;  // [T] s_std per row, or null
-  int upp;      // kTauChan: units per partial
+// Row t's statistics from the moment partials mom[S_st][T][ms], by one wave:
+// the lanes stride over the partials in a fixed order and a fixed butterfly
+// joins them.  Up to 256 partials (every decode and fused prefill call) a
+// lane's (at most four) partials are loaded at once, one round trip instead
+// of a chain of dependent loads; the sums keep the loop's order (the same
+// bits).
+struct TauRow {
+  float mean, sd, tv, c, d;  // c, d: the row's sums of s^3, s^4 (ms == 4)
 };
-__device__ __attribute__((always_inline)) inline void tau_body(const TauParams& q, const int bid) {
-  const float* __restrict__ mom = q.mom;
-  const float* __restrict__ tau_off = q.tau_off;
-  float* __restrict__ tau = q.tau;
+__device__ __attribute__((always_inline)) inline TauRow tau_row(const TauParams& q, const int64_t t, const int lane) {
   const int64_t T = q.T, N = q.N;
   const int S_st = q.S_st, ms = q.ms, mode = q.mode;
-  float* __restrict__ token_diag = q.token_diag;
-  const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(bid) * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
+  const float* __restrict__ mcol = q.mom + t * ms;  // partial s at mcol + s * T * ms
+  const int64_t sstr = T * ms;
+  // the partial's unit count (kTauChan): the third float, or from upp
+  auto count_of = [&](int s, float stored) {
+    if (q.upp <= 0) return stored;
+    const int64_t left = N - static_cast<int64_t>(s) * q.upp;
+    return static_cast<float>(left <= 0 ? 0 : (left < q.upp ? left : q.upp));
+  };
   float a = 0.f, b = 0.f, c = 0.f, d = 0.f;
-  // unrolled so that the partials' loads go out together (the sums keep their order)
-#pragma unroll 8
-  for (int s = lane; s < S_st; s += 64) {
-    const float* m = mom + (static_cast<int64_t>(s) * T + t) * ms;
-    a += m[0];
-    b += m[1];
-    if (ms == 4) {
-      c += m[2];
-      d += m[3];
+  if (S_st <= 256) {
+    // (no branches around the loads: lanes past S_st load the last partial
+    // and add +0, which leaves a sum's bits unchanged)
+    float v0[4], v1[4], v2[4], v3[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int s = lane + 64 * j < S_st ? lane + 64 * j : S_st - 1;
+      const float* m = mcol + s * sstr;
+      v0[j] = m[0];
+      v1[j] = m[1];
+      v2[j] = ms >= 3 ? m[2] : 0.f;
+      v3[j] = ms == 4 ? m[3] : 0.f;
     }
-  }
-  a = wave_sum(a);
-  if (mode == kTauChan) {
-    // between-partial term of the merged centred sum of squares, about the
-    // row mean (b holds the partials' own centred sums)
-    const float mean = a / static_cast<float>(N);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool in = lane + 64 * j < S_st;
+      a += in ? v0[j] : 0.f;
+      b += in ? v1[j] : 0.f;
+      if (ms == 4) {
+        c += in ? v2[j] : 0.f;
+        d += in ? v3[j] : 0.f;
+      }
+    }
+    a = wave_sum(a);
+    if (mode == kTauChan) {
+      // between-partial term of the merged centred sum of squares, about the
+      // row mean (b holds the partials' own centred sums)
+      const float mean = a / static_cast<float>(N);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int s = lane + 64 * j;
+        if (s < S_st) {
+          const float n = count_of(s, v2[j]);
+          if (n > 0.f) {
+            const float dm = v0[j] / n - mean;
+            b += n * dm * dm;
+          }
+        }
+      }
+    }
+  } else {
+    // unrolled so that the partials' loads go out together (the sums keep their order)
 #pragma unroll 8
     for (int s = lane; s < S_st; s += 64) {
-      float n;
-      if (q.upp > 0) {
-        const int64_t left = N - static_cast<int64_t>(s) * q.upp;
-        n = static_cast<float>(left <= 0 ? 0 : (left < q.upp ? left : q.upp));
-      } else {
-        n = mom[(static_cast<int64_t>(s) * T + t) * ms + 2];  // the partial's unit count (stride 3)
+      const float* m = mcol + s * sstr;
+      a += m[0];
+      b += m[1];
+      if (ms == 4) {
+        c += m[2];
+        d += m[3];
       }
-      if (n > 0.f) {
-        const float dm = mom[(static_cast<int64_t>(s) * T + t) * ms] / n - mean;
-        b += n * dm * dm;
+    }
+    a = wave_sum(a);
+    if (mode == kTauChan) {
+      const float mean = a / static_cast<float>(N);
+#pragma unroll 8
+      for (int s = lane; s < S_st; s += 64) {
+        const float n = count_of(s, ms >= 3 ? mcol[s * sstr + 2] : 0.f);
+        if (n > 0.f) {
+          const float dm = mcol[s * sstr] / n - mean;
+          b += n * dm * dm;
+        }
       }
     }
   }
   b = wave_sum(b);
-  if (token_diag && ms == 4) {
+  if (q.token_diag && ms == 4) {
     c = wave_sum(c);
     d = wave_sum(d);
   }
+  TauRow r;
+  const float fN = static_cast<float>(N);
+  r.mean = a / fN;
+  r.sd = (mode == kTauChan ? sqrtf(b / fN) : sqrtf(b / fN - __fmul_rn(r.mean, r.mean))) + 1e-8f;
+  r.tv = r.mean + __fmul_rn(q.tau_off[t], r.sd);
+  r.c = c;
+  r.d = d;
+  return r;
+}
+
+__device__ __attribute__((always_inline)) inline void tau_body(const TauParams& q, const int bid) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(bid) * 4 + (threadIdx.x >> 6);
+  if (t >= q.T) return;
+  const TauRow r = tau_row(q, t, lane);
   if (lane == 0) {
-    const float fN = static_cast<float>(N);
-    const float mean = a / fN;
-    const float sd = (mode == kTauChan ? sqrtf(b / fN) : sqrtf(b / fN - __fmul_rn(mean, mean))) + 1e-8f;
-    const float tv = mean + __fmul_rn(tau_off[t], sd);
-    tau[t] = tv;
-    if (q.sstd) q.sstd[t] = sd;
-    if (token_diag) {
-      float* td = token_diag + t * SRW_TDIAG_COUNT;
-      td[SRW_TDIAG_S_MEAN] = mean;
-      td[SRW_TDIAG_S_STD] = sd;
-      td[SRW_TDIAG_TAU] = tv;
-      td[SRW_TDIAG_SUM_S3] = c;
-      td[SRW_TDIAG_SUM_S4] = d;
+    q.tau[t] = r.tv;
+    if (q.sstd) q.sstd[t] = r.sd;
+    if (q.token_diag) {
+      float* td = q.token_diag + t * SRW_TDIAG_COUNT;
+      td[SRW_TDIAG_S_MEAN] = r.mean;
+      td[SRW_TDIAG_S_STD] = r.sd;
+      td[SRW_TDIAG_TAU] = r.tv;
+      td[SRW_TDIAG_SUM_S3] = r.c;
+      td[SRW_TDIAG_SUM_S4] = r.d;
     }
   }
 }
@@ -1932,24 +2030,6 @@ __global__ __launch_bounds__(256) void srw_tau_batch_kernel(Batch<TauParams> b) 
 // are reduced once, then each thread sums its columns over the splits with
 // eight independent loads in flight.
 // ---------------------------------------------------------------------------
-struct FinalParams {
-  const float* out_part;
-  const float* tok_part;
-  uint16_t* out;         // [T, D] bf16
-  float* gate_sum;
-  float* den;
-  int32_t* n_active;
-  int64_t T;
-  int D, S, spc;
-  int S_tok;             // per-token partial slots in tok_part (S for the fused kernels)
-  float scale;
-  int tps;               // floats per (split, row) in tok_part: 4, or kTokPartDiag with diagnostics
-  const float* tau;      // [T] (diagnostics)
-  float* token_diag;     // [T][SRW_TDIAG_COUNT] or null
-  GateParams gp;
-  float exp_scale;
-  int den_gate;          // den = max(sum gate, 1) (the v4.0.1 gate, v401:340)
-};
 
 // NG: split groups per workgroup; VW: columns per thread (1, 2 or 4: 4-,
 // 8- or 16-byte loads; the widest that leaves two workgroups per CU).  One workgroup per (row, block of 256 / NG
@@ -1960,7 +2040,7 @@ struct FinalParams {
 // VW: each column keeps its order of additions).  Few splits per chunk
 // (large T) use NG = 1, many (decode) NG = 16.
 template <int NG, int VW>
-__device__ __attribute__((always_inline)) inline void finalize_body(const FinalParams& p, const int bx) {
+__device__ __attribute__((always_inline)) inline void finalize_body(const FinalParams& p, const int bx, const int by) {
   constexpr int CW = 256 / NG;
   static_assert(VW == 1 || VW == 2 || VW == 4, "one, two or four columns per thread");
   typedef float vec_t __attribute__((ext_vector_type(VW)));
@@ -1990,7 +2070,7 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
   const float NA = red[2][0] + red[2][1] + red[2][2] + red[2][3];
   const float den = fmaxf(p.den_gate ? G : I, 1.0f);          // v41:584, v401:340
   const int64_t stride = p.T * p.D;
-  const int d = (blockIdx.y * CW + c) * VW;
+  const int d = (by * CW + c) * VW;
   const bool dok = d < p.D;
   const vec_t* col = reinterpret_cast<const vec_t*>(p.out_part + t * p.D + (dok ? d : 0));
   const int64_t vstride = stride / VW;
@@ -2046,7 +2126,7 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
       p.out[t * p.D + d + k] = f32_to_bf16_bits(o * p.scale);
     }
   }
-  if (blockIdx.y != 0) return;
+  if (by != 0) return;
   if (tid == 0) {
     if (p.gate_sum) p.gate_sum[t] = G;
     if (p.den) p.den[t] = den;
@@ -2085,12 +2165,12 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
 }
 template <int NG, int VW = 1>
 __global__ __launch_bounds__(256) void srw_finalize_kernel(FinalParams p) {
-  finalize_body<NG, VW>(p, blockIdx.x);
+  finalize_body<NG, VW>(p, blockIdx.x, blockIdx.y);
 }
 template <int NG, int VW = 1>
 __global__ __launch_bounds__(256) void srw_finalize_batch_kernel(Batch<FinalParams> b) {
   const int i = batch_index(b.start, b.n, blockIdx.x);
-  finalize_body<NG, VW>(b.p[i], blockIdx.x - b.start[i]);
+  finalize_body<NG, VW>(b.p[i], blockIdx.x - b.start[i], blockIdx.y);
 }
 
 // Few splits per chunk (spc < 16: prefill-sized T): one wave per row, lane l
@@ -2981,6 +3061,9 @@ hipError_t pack_unit_major(const uint16_t* src, uint16_t* dst, int64_t N, int D,
   return hipGetLastError();
 }
 
+int finalize_groups(int spc);
+FinalParams final_params_of(const FinalizeArgs& f);
+
 bool mfma_supports(const srw_desc_t& d, bool h_is_x) {
   if (d.dtype != SRW_BF16) return false;
   const bool gl = d.gate == SRW_GATE_GELU_V401;  // the GELU gate runs without diagnostics here
@@ -3050,6 +3133,16 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     read_rows = rn;
     write_rows = wn;
   }
+  // decode-sized calls: the decode kernel (few splits -- small pools -- one
+  // workgroup per (split, 32-row block), so that more CUs share the pool and
+  // each loads only its rows' X and H)
+  const int row_blocks = static_cast<int>((g.T + 31) / 32);
+  const int rb = (row_blocks > 1 && static_cast<int64_t>(g.S) * row_blocks <= kTargetBlocks) ? row_blocks : 1;
+  MainFn dec = nullptr;
+  int dec_lds = 0;
+  const bool decode = decode_applies(d) && decode_splits_fit(g) &&
+                      pick_decode(rb > 1 ? 32 : g.T, D, static_cast<int>(d.d_route), decode_max_tiles(g), &dec, &dec_lds,
+                                  gl, (d.flags & SRW_FLAG_SPARSE_SKIP) != 0);
   // pack W^T (kept in the workspace across calls that declare the pool cached)
   if (!cached) {
     const int64_t rows = static_cast<int64_t>(g.ntiles) * 2 * DB * 64;
@@ -3059,6 +3152,26 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
                        d.n_units, D, rows);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
+  // the finalize of the call
+  FinalizeArgs f{};
+  f.out_part = out_part;
+  f.tok_part = tok_part;
+  f.out = static_cast<uint16_t*>(a.o.out);
+  f.gate_sum = a.o.gate_sum;
+  f.den = a.o.den;
+  f.n_active = a.o.n_active;
+  f.T = g.T;
+  f.D = D;
+  f.S = g.S;
+  f.spc = g.spc;
+  f.S_tok = g.S;
+  f.tps = tok_part_stride(d);
+  f.scale = d.scale;
+  f.tau = tau;
+  f.token_diag = token_diag;
+  f.gp = a.gp;
+  f.exp_scale = -d.sharpness * 1.4426950408889634f;
+  f.den_gate = gl ? 1 : 0;
   const unsigned grid = static_cast<unsigned>(g.TT * g.S);
   const unsigned grid_st = static_cast<unsigned>(g.TT_st * g.S_st);
   if (d.stats_mode == SRW_STATS_GRAM) {
@@ -3109,16 +3222,8 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     mp.g = g;
     mp.gp = a.gp;
     mp.exp_scale = -d.sharpness * 1.4426950408889634f;
-    mp.rb = 1;
-    MainFn dec = nullptr;
-    int dec_lds = 0;
-    // few splits (small pools): one workgroup per (split, 32-row block), so
-    // that more CUs share the pool and each loads only its rows' X and H
-    const int row_blocks = static_cast<int>((g.T + 31) / 32);
-    mp.rb = (row_blocks > 1 && static_cast<int64_t>(g.S) * row_blocks <= kTargetBlocks) ? row_blocks : 1;
-    if (decode_applies(d) && decode_splits_fit(g) &&
-        pick_decode(mp.rb > 1 ? 32 : g.T, D, static_cast<int>(d.d_route), decode_max_tiles(g), &dec, &dec_lds, gl,
-                    (d.flags & SRW_FLAG_SPARSE_SKIP) != 0)) {
+    mp.rb = rb;
+    if (decode) {
       *path_name = (d.flags & SRW_FLAG_SPARSE_SKIP) ? "mfma_decode_sparse_bf16" : "mfma_decode_bf16";
       if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(dec), hipFuncAttributeMaxDynamicSharedMemorySize,
                                    dec_lds)) != hipSuccess)
@@ -3148,25 +3253,6 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
     }
   }
   // finalize
-  FinalizeArgs f{};
-  f.out_part = out_part;
-  f.tok_part = tok_part;
-  f.out = static_cast<uint16_t*>(a.o.out);
-  f.gate_sum = a.o.gate_sum;
-  f.den = a.o.den;
-  f.n_active = a.o.n_active;
-  f.T = g.T;
-  f.D = D;
-  f.S = g.S;
-  f.spc = g.spc;
-  f.S_tok = g.S;
-  f.tps = tok_part_stride(d);
-  f.scale = d.scale;
-  f.tau = tau;
-  f.token_diag = token_diag;
-  f.gp = a.gp;
-  f.exp_scale = -d.sharpness * 1.4426950408889634f;
-  f.den_gate = gl ? 1 : 0;
   if ((e = launch_finalize(f, a.stream)) != hipSuccess) return e;
   if (unit_part) {
     const int64_t rows = (g.T + 31) / 32;
@@ -3402,15 +3488,7 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     mp.s_in = ss[i] ? reinterpret_cast<const uint16_t*>(a[i].ws + L[i].scores) : nullptr;
     mb.start[i + 1] = mb.start[i] + (decode ? g[i].S * rb[i] : g[i].TT * g[i].S);
   }
-  if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(main_batch), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               lds0)) != hipSuccess)
-    return e;
-  dominant_kernel_begin(st);
-  hipLaunchKernelGGL(main_batch, dim3(static_cast<unsigned>(mb.start[n])), dim3(threads0),
-                     static_cast<size_t>(lds0), st, mb);
-  dominant_kernel_end(st);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  // finalize
+  // the calls' finalize parameters
   Batch<FinalParams> fb{};
   fb.n = n;
   for (int i = 0; i < n; ++i) {
@@ -3436,6 +3514,15 @@ hipError_t mfma_forward_batch(const LaunchArgs* a, int n, const char** path_name
     fb.p[i] = final_params_of(f);
     fb.start[i + 1] = fb.start[i] + static_cast<int>(rows_fin ? (g[i].T + 3) / 4 : g[i].T);
   }
+  if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(main_batch), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               lds0)) != hipSuccess)
+    return e;
+  dominant_kernel_begin(st);
+  hipLaunchKernelGGL(main_batch, dim3(static_cast<unsigned>(mb.start[n])), dim3(threads0),
+                     static_cast<size_t>(lds0), st, mb);
+  dominant_kernel_end(st);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+
   if (rows_fin) {
     const dim3 grid_r(static_cast<unsigned>(fb.start[n]));
     if (D == 64) hipLaunchKernelGGL(srw_finalize_rows_batch_kernel<1>, grid_r, dim3(256), 0, st, fb);
