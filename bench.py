@@ -503,19 +503,45 @@ def bench_model(args, pkg, C, dev) -> dict:
     }
 
 
-def sparse_accounting(plan, T, D, dr, N, R, path):
+def sparse_accounting(plan, T, D, dr, N, R, path, cs=None):
     """What SRW_FLAG_SPARSE_SKIP can leave out, from the call's pass mask.
 
     Decode kernel (path mfma_decode_sparse_bf16): a unit's R row (D bf16) is
     read when some row of the call passes it, a W^T fragment half (8 units,
     D / 32 pieces of 512 bytes) when one of its units passes; E is read
-    whole.  Prefill shapes have no sparse kernel: reported is the share of
-    32-token x 32-unit blocks no row passes (what a block skip could drop).
+    whole.  Tiled family (path tiled_sparse_bf16): per 32-row tile the read
+    and write GEMMs run over the union of the units some row of the tile
+    passes, in blocks of 32 listed units that never cross a reference chunk
+    (cs units): executed_flop counts those blocks (4 * 32 * 32 * D each),
+    dense_flop the dense read + write GEMMs, pass_pair_flop the (row, unit)
+    pairs that pass.  Other prefill shapes run dense: reported is the share
+    of 32-token x 32-unit blocks no row passes (what a block skip could drop).
     """
     import torch
     words = plan.pass_mask.reshape(T * R, -1)                                  # [rows, ceil(N/64)] 64-bit words
     info = {"pass_frac": round(float(plan.n_active.double().sum()) / (T * R * N), 5)}
-    if path == "mfma_decode_sparse_bf16":
+    if path == "tiled_sparse_bf16":
+        rows = T * R
+        tb = (rows + 31) // 32
+        pad = torch.zeros(tb * 32, words.shape[1], dtype=words.dtype, device=words.device)
+        pad[:rows] = words
+        blk = pad.reshape(tb, 32, -1)
+        ored = blk[:, 0].clone()
+        for i in range(1, 32):                                                 # OR over each 32-row tile
+            ored |= blk[:, i]
+        shifts = torch.arange(64, device=ored.device)
+        uni = ((ored.unsqueeze(-1) >> shifts) & 1).reshape(tb, -1)[:, :N].to(torch.int32)   # [tiles, N]
+        cs = cs or N
+        bounds = list(range(0, N, cs)) + [N]
+        counts = torch.stack([uni[:, a:b].sum(dim=1) for a, b in zip(bounds[:-1], bounds[1:])], dim=1)
+        blocks = int(((counts + 31) // 32).sum())
+        listed = int(counts.sum())
+        info.update({"union_frac": round(listed / (tb * N), 5),
+                     "listed_units_per_tile": round(listed / tb, 1),
+                     "executed_flop": 4.0 * 32 * 32 * D * blocks,
+                     "dense_flop": 4.0 * rows * N * D,
+                     "pass_pair_flop": 4.0 * D * float(plan.n_active.double().sum())})
+    elif path == "mfma_decode_sparse_bf16":
         anyw = words[0].clone()
         for r in range(1, T * R):                                              # OR over the call's rows
             anyw |= words[r]
@@ -547,6 +573,43 @@ def sparse_accounting(plan, T, D, dr, N, R, path):
     return info
 
 
+def time_dense_twin(args, pkg, C, plan, cs, stream, K, warmup, sparse_step_ms, T, R, N, D):
+    """The same call without SRW_FLAG_SPARSE_SKIP (the dense tiled kernels),
+    timed like the sparse one: its step, its dominant kernel (the gate
+    kernel: read GEMM + gate) and the write GEMM's share of the read + write
+    work it does densely."""
+    import torch
+    x, h, emb, tau, read, write = plan.inputs
+    dense = pkg.SrwPlan(x, h, emb, tau, read, write, stats=args.stats, chunk_size=cs, want_mask=True,
+                        tiled=args.tiled, sparse_skip=False, gate=args.gate)
+    for _ in range(warmup):
+        dense.launch(stream)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for a, b in ev + [(t0, t1)]:      # materialise the HIP events on this stream
+        a.record(stream)
+        b.record(stream)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for a, b in ev:
+        C.set_kernel_events(a.cuda_event, b.cuda_event)
+        dense.launch(stream)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    C.set_kernel_events(None, None)
+    step_ms = t0.elapsed_time(t1) / K
+    kern_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    same = bool(torch.equal(dense.n_active, plan.n_active) and torch.equal(dense.den, plan.den))
+    kflops = 2.0 * T * R * N * D
+    log(f"dense twin ({dense.path}): {step_ms:.4f} ms/step, gate kernel {kern_ms:.4f} ms")
+    return {"path": dense.path, "ms_per_step": round(step_ms, 5), "kernel": "tiled_gate_kernel",
+            "kernel_ms": round(kern_ms, 5),
+            "kernel_mfma_frac": round(kflops / (kern_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "step_speedup_of_sparse": round(step_ms / sparse_step_ms, 3),
+            "same_n_active_and_den": same}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -576,9 +639,11 @@ def main() -> int:
                          "(SRW_FLAG_POOL_CACHED: decode steps / layers sharing one pool)")
     ap.add_argument("--sparse", action="store_true",
                     help="SRW_FLAG_SPARSE_SKIP: the decode kernel loads only the R rows and W^T fragment "
-                         "halves of units some row passes; the roofline then counts the bytes it needs "
-                         "(prefill shapes run dense: the line reports how many 32x32 (token, unit) blocks "
-                         "a skip could drop)")
+                         "halves of units some row passes (the roofline counts the bytes it needs); the "
+                         "tiled family (d_model 256 / 512 / 1024) runs the read and write GEMMs over each "
+                         "32-token tile's passing units (the roofline counts the executed MFMA work, and "
+                         "the same call without the flag is timed beside it); other prefill shapes run "
+                         "dense (the line reports how many 32x32 (token, unit) blocks a skip could drop)")
     ap.add_argument("--tokens", type=int, default=0,
                     help="override the workload's token count (e.g. 1 or 8 rows for a decode shape)")
     ap.add_argument("--gate", default="v41", choices=["v41", "gelu_v401"],
@@ -783,6 +848,8 @@ def main() -> int:
         # the main kernel streams the moments kernel's bf16 scores: its own
         # work is the read (once per token) and write GEMMs
         kflops = 2.0 * T * N * (D + R * D)
+    elif plan.path == "tiled_sparse_bf16":
+        kflops = None   # the gather kernel's executed MFMA work, from the pass mask below
     elif plan.path in ("tiled_bf16", "tiled_f32"):
         # the dominant kernel of the tiled family is tiled_gate_kernel: the
         # read GEMM over the T * R virtual rows, gating the scores that
@@ -791,6 +858,14 @@ def main() -> int:
         kflops = 2.0 * T * R * N * D
     else:
         kflops = flops
+    sparse_info = None
+    if args.sparse and not args.backward:
+        sparse_info = sparse_accounting(plan, T, D, dr, N, R, path, cs)
+        if path == "tiled_sparse_bf16":
+            # sp_gather_kernel: the read and write GEMMs over the listed blocks
+            kflops = sparse_info["executed_flop"]
+            sparse_info["dense_equivalent_tflops"] = round(sparse_info["dense_flop"] / (kern_ms * 1e-3) / 1e12, 2)
+            sparse_info["dense"] = time_dense_twin(args, pkg, C, plan, cs, stream, K, warmup, step_ms, T, R, N, D)
     achieved = kflops / (kern_ms * 1e-3) / 1e12
     traffic = MEASURED_TRAFFIC.get((args.workload, args.stats, path))
     peak = PEAK_F32_TFLOPS if args.dtype == "f32" else PEAK_BF16_TFLOPS
@@ -799,9 +874,6 @@ def main() -> int:
                 "traffic": traffic, "kernel": path,
                 "kernel_ms": round(kern_ms, 5), "algorithmic_flop": kflops,
                 "step_tflops": round(flops / (step_ms * 1e-3) / 1e12, 2)}
-    sparse_info = None
-    if args.sparse and not args.backward:
-        sparse_info = sparse_accounting(plan, T, D, dr, N, R, path)
     if args.workload.startswith("decode_") and not args.backward:
         # decode shapes are pool-read bound: the algorithmic bytes are the pool
         # (E, R, W rows) streamed once per call -- with the sparse kernel the

@@ -233,7 +233,7 @@ srw_status_t launch_forward(const srw::LaunchArgs& a, int which) {
     g_last_path = name;
   } else if (which == 2) {
     e = srw::tiled_forward(a);
-    g_last_path = "tiled_bf16";
+    g_last_path = srw::tiled_runs_sparse(a.d) ? "tiled_sparse_bf16" : "tiled_bf16";
   } else if (which == 3) {
     e = srw::tiled_f32_forward(a);
     g_last_path = "tiled_f32";

@@ -118,6 +118,7 @@ hipError_t tiled_backward(const BackwardArgs& a);
 // product materialised in HBM; d_model and d_route multiples of 64.
 bool tiled_supports(const srw_desc_t& d);
 size_t tiled_workspace_bytes(const srw_desc_t& d);
+bool tiled_runs_sparse(const srw_desc_t& d);  // SRW_FLAG_SPARSE_SKIP at a width the sparse kernels take
 hipError_t tiled_forward(const LaunchArgs& a);
 
 // fp32 tiled GEMMs on the fp32 matrix cores, see srw_tiled_f32.hip: the v4.1

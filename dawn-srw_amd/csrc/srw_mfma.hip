@@ -142,13 +142,6 @@ struct RowTile {
   static constexpr int step_off(int ks) { return (ks / NM) * RG * kFragBytes; }
 };
 
-// Unit (within a 32-unit tile) carried by k index 8*half + i of k-step j of
-// the write GEMM: the accumulator row of score-GEMM register v = 8 j + i.
-__host__ __device__ inline int unit_of_k(int j, int half, int i) {
-  return 16 * j + 8 * (i >> 2) + 4 * half + (i & 3);
-}
-// Unit (within the tile) of score-accumulator register v in lane-half `half`.
-__device__ inline int unit_of_acc(int v, int half) { return 8 * (v >> 2) + 4 * half + (v & 3); }
 
 // The gate epilogue of a tile as 48 micro-steps (type * 16 + element):
 // type 0 = bf16 score, margin, exp; 1 = sigmoid, intensity, gate; 2 = sums,

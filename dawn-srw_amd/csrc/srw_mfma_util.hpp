@@ -35,6 +35,16 @@ __device__ inline uint32_t pack_bf16(float lo, float hi) {
 __device__ inline float lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ inline float hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
 
+// Unit (within a 32-unit tile) carried by k index 8*half + i of k-step j of
+// the write GEMM: the accumulator row of score-GEMM register v = 8 j + i.
+// (A 32 x 32 accumulator -- rows = units, lane = token -- is the A operand of
+// the write GEMM under this unit permutation.)
+__host__ __device__ inline int unit_of_k(int j, int half, int i) {
+  return 16 * j + 8 * (i >> 2) + 4 * half + (i & 3);
+}
+// Unit (within the tile) of score-accumulator register v in lane-half `half`.
+__device__ inline int unit_of_acc(int v, int half) { return 8 * (v >> 2) + 4 * half + (v & 3); }
+
 // One 16-byte direct global->LDS load per lane; the LDS destination of the
 // wave is `lds` (wave-uniform) + 16 * lane.
 __device__ inline void g2lds16(const void* g, char* lds) {

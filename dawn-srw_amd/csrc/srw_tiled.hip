@@ -298,6 +298,24 @@ struct TGateParams {
   float exp_scale;       // -sharpness * log2(e)
 };
 
+// The v4.1 gate of one bf16 score in the folded form (v41:503-511):
+// arg = s c + k (c = -sharpness log2 e, k = -(tau + thr) c), act = 1 / (1 +
+// 2^arg), intensity = eps + min(max(s - tau - thr - cut, 0), maxi), g = act
+// intensity; the sign bit of arg is the pass bit.  The product stays a
+// rounded multiply (no contraction into a caller's running sum), so the
+// dense gate kernel and the sparse mark kernel sum the same gate values.
+struct GateElem {
+  float g, inten;
+  uint32_t sign;
+};
+__device__ inline GateElem gate_elem(float s, float c_exp, float k_exp, float tau_cut, float eps, float maxi) {
+#pragma clang fp contract(off)
+  const float arg = fmaf(s, c_exp, k_exp);
+  const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(arg));
+  const float inten = eps + __builtin_amdgcn_fmed3f(s - tau_cut, 0.0f, maxi);
+  return GateElem{act * inten, inten, __float_as_uint(arg)};
+}
+
 // KEEP (the backward's recompute): P and x.r go to P_out / XR_out and the
 // stored scores stay.
 template <bool KEEP>
@@ -354,12 +372,9 @@ __global__ __launch_bounds__(kGThreads) void tiled_gate_kernel(TGateParams p) {
           float g2[2];
 #pragma unroll
           for (int e = 0; e < 2; ++e) {
-            const float s = e ? hi_f32(sp) : lo_f32(sp);
-            const float arg = fmaf(s, c_exp, k_exp);
-            const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(arg));
-            float inten = eps + __builtin_amdgcn_fmed3f(s - tau_cut, 0.0f, maxi);
-            float g = act * inten;
-            uint32_t sign = __float_as_uint(arg);
+            const GateElem ge = gate_elem(e ? hi_f32(sp) : lo_f32(sp), c_exp, k_exp, tau_cut, eps, maxi);
+            float g = ge.g, inten = ge.inten;
+            uint32_t sign = ge.sign;
             if constexpr (!FULL) {  // units past N count for nothing
               const bool ok = 32 * i + 8 * ((v + e) >> 2) + ((v + e) & 3) < nleft;
               g = ok ? g : 0.f;
@@ -414,6 +429,412 @@ __global__ __launch_bounds__(kGThreads) void tiled_gate_kernel(TGateParams p) {
     epilogue(std::integral_constant<bool, true>{});
   else
     epilogue(std::integral_constant<bool, false>{});
+}
+
+// ---------------------------------------------------------------------------
+// Sparse skip (SRW_FLAG_SPARSE_SKIP) at prefill sizes.  The score GEMM runs
+// dense (the stats kernel, S stored); then
+//   mark    the gate of every (token, unit) from the stored scores -- the
+//           gate kernel's epilogue without its GEMM: the same pass bits and
+//           per-token partial sums, so gate_sum, den, n_active and the mask
+//           equal the dense path's bit for bit -- plus, per 32-token tile,
+//           the union of the units some token passes (v41:505-511: margin >
+//           0 <=> act > 0.5)
+//           and the bf16 gates of the union's units, 32 tokens contiguous
+//           per unit (G: the union units of each 128-unit slice packed at
+//           the slice's start)
+//   list    per 32-token tile, the union compacted into an index list (and
+//           each entry's slot in G), with the reference chunks' boundaries
+//   gather  per 32-token tile, the read and write GEMMs over the union's
+//           units only, 32 at a time: their R and W rows gathered, x.R^T
+//           split over eight waves' k-slabs and summed in LDS, P =
+//           bf16(bf16(g) bf16(xr)) with the gates from G, OUT += P . W; one
+//           fp32 partial per reference chunk for the shared finalize.
+// Units no token of a tile passes are left out of out only (their gates are
+// epsilon-sized: act < 0.5 and intensity = eps, v41:509-511); the sums, den
+// and the mask keep them.
+// ---------------------------------------------------------------------------
+struct SpMarkParams {
+  const uint16_t* S;     // [Tv, N64] bf16 scores
+  const float* tau;      // [Tv]
+  float* tok_part;       // [2 CT][Tv][4] as the gate kernel's
+  uint32_t* mask32;      // [Tv][mask_words32] or null
+  uint32_t* uni;         // [TT32][W32]: units some token of the 32-token tile passes
+  uint16_t* G;           // [TT32][GS][32]: bf16 gates, slice sl's union units at slots 128 sl + rank
+  int64_t mask_words32, W32, GS;
+  int64_t Tv, N, N64;
+  int CT;
+  GateParams gp;
+  float exp_scale;
+};
+
+// One wave per (32 tokens, 128-unit slice): lane u + 32 h holds token 32
+// tile + u and the slice's units 32 i + 8 (v / 4) + 4 h + v % 4 -- the gate
+// kernel's epilogue layout and arithmetic.
+__global__ __launch_bounds__(256) void sp_mark_kernel(SpMarkParams p) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int u = lane & 31, h = lane >> 5;
+  const int nsl = 2 * p.CT;                      // 128-unit slices (the gate kernel's partials)
+  const int sgroups = (nsl + 3) / 4;
+  const int tile = blockIdx.x / sgroups;
+  const int sl = (blockIdx.x % sgroups) * 4 + wave;
+  if (sl >= nsl) return;
+  const int64_t t = static_cast<int64_t>(tile) * 32 + u;
+  const bool tok = t < p.Tv;
+  const uint16_t* prow = p.S + (tok ? t : p.Tv - 1) * p.N64;
+  const float c_exp = p.exp_scale, eps = p.gp.eps, maxi = p.gp.maxi;
+  const float tau_thr = p.tau[tok ? t : p.Tv - 1] + p.gp.thr;
+  const float k_exp = -tau_thr * c_exp;
+  const float tau_cut = tau_thr + p.gp.cut;
+  const int64_t u0 = static_cast<int64_t>(sl) * 128;
+  const int64_t nleft = p.N - (u0 + 4 * h);
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  uint16_t* gtile = p.G + (static_cast<int64_t>(tile) * p.GS + static_cast<int64_t>(sl) * 128) * 32 + u;
+  float gs = 0.f, is = 0.f;
+  int na = 0, gbase = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t nb = u0 + 32 * i + 4 * h;
+    u32x2_t sv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sv[q] = nb + 8 * q < p.N64 ? *reinterpret_cast<const u32x2_t*>(prow + nb + 8 * q) : u32x2_t{0u, 0u};
+    uint32_t bits = 0;
+    uint32_t gq[8];  // bf16 gates of elements 2 k, 2 k + 1
+#pragma unroll
+    for (int v = 0; v < 16; v += 2) {
+      const uint32_t sp = sv[v >> 2][(v >> 1) & 1];
+      float g2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const GateElem ge = gate_elem(e ? hi_f32(sp) : lo_f32(sp), c_exp, k_exp, tau_cut, eps, maxi);
+        float g = ge.g, inten = ge.inten;
+        uint32_t sign = ge.sign;
+        const bool ok = 32 * i + 8 * ((v + e) >> 2) + ((v + e) & 3) < nleft;  // units past N count for nothing
+        g = ok ? g : 0.f;
+        inten = ok ? inten : 0.f;
+        sign = ok ? sign : 0u;
+        gs += g;
+        is += inten;
+        bits = __builtin_amdgcn_alignbit(bits, sign, 31);
+        g2[e] = g;
+      }
+      gq[v >> 1] = pack_bf16(g2[0], g2[1]);  // gate_bf (v41:516)
+    }
+    const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
+    uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
+    m <<= 4 * h;
+    na += __builtin_popcount(m);
+    m |= __shfl_xor(m, 32);
+    const int64_t word = (u0 + 32 * i) / 32;
+    if (p.mask32 && h == 0 && tok && word < p.mask_words32) p.mask32[t * p.mask_words32 + word] = m;
+    // the union over the tile's tokens
+    uint32_t um = tok ? m : 0u;
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) um |= __shfl_xor(um, o);
+    if (lane == 0 && word < p.W32) p.uni[static_cast<int64_t>(tile) * p.W32 + word] = um;
+    // the union units' gates: unit w of the word at slot gbase + (union units below w)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int w = 8 * (v >> 2) + 4 * h + (v & 3);
+      if ((um >> w) & 1u) {
+        const int slot = gbase + __builtin_popcount(um & ((1u << w) - 1u));
+        gtile[slot * 32] = static_cast<uint16_t>((v & 1) ? gq[v >> 1] >> 16 : gq[v >> 1] & 0xffffu);
+      }
+    }
+    gbase += __builtin_popcount(um);
+  }
+  gs += __shfl_xor(gs, 32);
+  is += __shfl_xor(is, 32);
+  na += __shfl_xor(na, 32);
+  if (h == 0 && tok) {
+    float* tp = p.tok_part + (static_cast<int64_t>(sl) * p.Tv + t) * 4;
+    tp[0] = gs;
+    tp[1] = is;
+    tp[2] = static_cast<float>(na);
+    tp[3] = 0.f;
+  }
+}
+
+// Per 32-token tile: its union's units in increasing order, list[tile][k],
+// and cstart[tile][c] = the list position of the first unit of reference
+// chunk c (c = 0..nc; cstart[nc] = the count).  One workgroup per tile, 256
+// union words per round, an exclusive scan of their popcounts.
+__global__ __launch_bounds__(256) void sp_list_kernel(const uint32_t* __restrict__ uni, int64_t W32, int64_t N,
+                                                      int64_t cs, int nc, int32_t* __restrict__ list,
+                                                      int32_t* __restrict__ glist, int32_t* __restrict__ cstart) {
+  __shared__ int wsum[4];
+  const int tile = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t* uw = uni + static_cast<int64_t>(tile) * W32;
+  int32_t* out = list + static_cast<int64_t>(tile) * N;
+  int32_t* gout = glist + static_cast<int64_t>(tile) * N;
+  int32_t* cst = cstart + static_cast<int64_t>(tile) * (nc + 1);
+  int base = 0;
+  for (int64_t w0 = 0; w0 < W32; w0 += 256) {
+    const int64_t w = w0 + tid;
+    const uint32_t bits = w < W32 ? uw[w] : 0u;
+    const int pc = __builtin_popcount(bits);
+    // inclusive scan over the wave, then over the waves
+    int x = pc;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    int before = base;
+    for (int k = 0; k < wave; ++k) before += wsum[k];
+    const int start = before + x - pc;  // this word's first list position
+    // the slot in G: 128 (w / 4) + the entry's rank among its 128-unit slice's
+    // union units (the slice's first word is handled by lane & ~3)
+    const int sfirst = __shfl(start, lane & ~3);
+    const int gslot = static_cast<int>(w / 4) * 128 + (start - sfirst);
+    uint32_t b = bits;
+    int k = 0;
+    while (b) {
+      const int bit = __builtin_ctz(b);
+      out[start + k] = static_cast<int32_t>(w * 32 + bit);
+      gout[start + k] = gslot + k;
+      b &= b - 1;
+      ++k;
+    }
+    // chunk boundaries inside this word's 32 units
+    for (int c = 1; c < nc; ++c) {
+      const int64_t bu = c * cs;
+      if (bu / 32 == w) cst[c] = start + __builtin_popcount(bits & ((1u << (bu % 32)) - 1u));
+    }
+    const int total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();  // wsum is rewritten next round
+    base += total;
+  }
+  if (tid == 0) {
+    cst[0] = 0;
+    cst[nc] = base;
+  }
+}
+
+// The gathered read and write GEMMs of one 32-token tile over the listed
+// units of one reference chunk (one workgroup, eight waves; workgroups in
+// chunk-major order), in blocks of 32 listed units.  Wave w owns the read
+// GEMM's k-slab [w D / 8, (w + 1) D / 8) (its x fragments in LDS) and the
+// output columns of the same range: lane l holds columns w D / 8 + F (l % 32)
+// + f, f < F, so that one 2F-byte load of a W row gives a lane its F columns
+// of one unit.  Per block:
+//   XR^T = R_blk . X^T over the slab (A: the units' R rows, 16-byte loads),
+//   the eight partial accumulators summed in LDS in wave order; each wave
+//   takes 1 / 8 of the 32 x 32 elements (accumulator registers 2 w, 2 w + 1),
+//   their bf16 gates from G, and writes P = bf16(bf16(g) bf16(xr)) in the
+//   write GEMM's A-operand order (unit_of_k == unit_of_acc) back to LDS;
+//   OUT += P . W_blk, the B fragments (8 units x 1 column) assembled in
+//   registers from the eight units' 2F-byte row pieces.
+// Software pipeline: the next block's W pieces, gates and R rows are
+// requested during the current block, the list entries two blocks ahead;
+// lane l keeps unit l % 32 of a block and the other lanes' units come by
+// cross-lane shuffles.  OUT goes to out_part[chunk] (zeros for a
+// chunk none of whose units is listed).
+template <int F>  // D = 256 F
+struct SpGemm {
+  static constexpr int D = 256 * F;
+  static constexpr int KS = 2 * F;  // the read GEMM's k-steps per wave (D / 8 / 16)
+};
+struct SpGatherParams {
+  const uint16_t* x;     // [T, D] (row v / routes)
+  const uint16_t* read;  // [N, D]
+  const uint16_t* write; // [N, D]
+  const uint16_t* G;     // [TT32][GS][32] the union units' bf16 gates (sp_mark_kernel)
+  const int32_t* list;   // [TT32][N] units
+  const int32_t* glist;  // [TT32][N] their slots in G
+  const int32_t* cstart; // [TT32][nc + 1]
+  float* out_part;       // [nc][Tv][D]
+  int64_t Tv, N, GS;
+  int routes, nc, TT32;
+};
+constexpr int kSpThreads = 512;
+
+// lane's list entry at position k of [.., bend) (-1: padding past the end) and its slot in G
+struct SpEntry {
+  int32_t u, g;
+};
+__device__ inline SpEntry sp_entry(const int32_t* lst, const int32_t* glst, int k, int bend) {
+  if (k < bend) return SpEntry{lst[k], glst[k]};
+  return SpEntry{-1, 0};
+}
+
+template <int F>
+struct SpPiece;  // F bf16 of one W row
+template <>
+struct SpPiece<1> {
+  typedef uint16_t T;
+  __device__ static uint32_t at(T v, int) { return v; }
+};
+template <>
+struct SpPiece<2> {
+  typedef uint32_t T;
+  __device__ static uint32_t at(T v, int f) { return f ? v >> 16 : v & 0xffffu; }
+};
+template <>
+struct SpPiece<4> {
+  typedef uint32_t T __attribute__((ext_vector_type(2)));
+  __device__ static uint32_t at(T v, int f) { return (f & 1) ? v[f >> 1] >> 16 : v[f >> 1] & 0xffffu; }
+};
+
+template <int F>
+__global__ __launch_bounds__(kSpThreads, 1) void sp_gather_kernel(SpGatherParams p) {
+  constexpr int D = SpGemm<F>::D, KS = SpGemm<F>::KS;
+  typedef typename SpPiece<F>::T piece_t;
+  __shared__ u32x4_t xs[8][KS][64];  // wave w's x fragments (B operand of XR^T), [k-step][lane]
+  __shared__ float4 part[8][4][64];  // wave q's x.r partial: [q][v / 4][lane] = elements 4 (v / 4) .. + 3
+  __shared__ uint32_t pl[8][64];     // P: [w][lane] = elements 2 w, 2 w + 1 (A operand of the write GEMM)
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  // chunk-major: the workgroups resident at one time work on the same
+  // reference chunk, so that each XCD's L2 serves the R / W rows they share
+  const int c = blockIdx.x / p.TT32, tile = blockIdx.x % p.TT32;
+  const int64_t t = static_cast<int64_t>(tile) * 32 + col;
+  const int64_t tl = t < p.Tv ? t : p.Tv - 1;
+  const int32_t* lst = p.list + static_cast<int64_t>(tile) * p.N;
+  const int32_t* glst = p.glist + static_cast<int64_t>(tile) * p.N;
+  const int32_t* cs = p.cstart + static_cast<int64_t>(tile) * (p.nc + 1);
+  const int b_lo = cs[c], b_hi = cs[c + 1];
+  const int k0 = wave * (D / 8);  // this wave's k-slab and output columns
+  // x of this wave's k-slab (B operand of XR^T: lane l, token l % 32), kept
+  // in LDS (each wave reads back only its own fragments)
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    xs[wave][ks][lane] = *reinterpret_cast<const u32x4_t*>(p.x + (tl / p.routes) * D + k0 + 16 * ks + 8 * half);
+  const uint16_t* gcol = p.G + static_cast<int64_t>(tile) * p.GS * 32 + col;  // this lane's token in G
+  // R / W rows by 32-bit byte offsets from the wave's (uniform) slab base
+  const char* rbase = reinterpret_cast<const char*>(p.read + k0);
+  const char* wbase = reinterpret_cast<const char*>(p.write + k0);
+  const uint32_t rlane = 16u * half, wlane = 2u * F * col;
+  const uint32_t gsh = 16u * (col & 1);  // this lane's gate in a token pair's 4 bytes
+  f32x16_t oacc[F];
+#pragma unroll
+  for (int f = 0; f < F; ++f) oacc[f] = f32x16_t{};
+  // a block's W row pieces (unit unit_of_k(j, half, i) of the block), the
+  // bf16 gates of this lane's elements 2 wave, 2 wave + 1 (padding: 0)
+  struct BlockLoads {
+    piece_t wp[2][8];
+    uint32_t q0, q1;  // 4-byte loads of the gates of this lane's token pair (taken apart where used)
+    bool pad0, pad1;
+  };
+  auto issue = [&](const SpEntry& e, BlockLoads& bl) {
+    // all shuffles first, then all loads: one wait for the shuffles
+    int32_t wu[2][8], gs[2], un[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) wu[j][i] = __shfl(e.u, unit_of_k(j, half, i));
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      gs[q] = __shfl(e.g, unit_of_acc(2 * wave + q, half));
+      un[q] = __shfl(e.u, unit_of_acc(2 * wave + q, half));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        bl.wp[j][i] = *reinterpret_cast<const piece_t*>(
+            wbase + (static_cast<uint32_t>(wu[j][i] >= 0 ? wu[j][i] : 0) * (2u * D) + wlane));
+    // (4-byte loads, no 16-bit extension next to the load; padding entries: slot 0)
+    const uint32_t* gp = reinterpret_cast<const uint32_t*>(gcol - (col & 1));
+    bl.q0 = gp[static_cast<int64_t>(gs[0]) * 16];
+    bl.q1 = gp[static_cast<int64_t>(gs[1]) * 16];
+    bl.pad0 = un[0] < 0;
+    bl.pad1 = un[1] < 0;
+  };
+
+  // ping-pong (no register copies, which would wait for loads in flight):
+  // the current block's loads and the next one's; the next block's list
+  // entries and the ones after
+  SpEntry ul_a = sp_entry(lst, glst, b_lo + 32 + col, b_hi), ul_b;
+  u32x4_t rf[KS];
+  BlockLoads bl_a, bl_b;
+  {
+    const SpEntry e = sp_entry(lst, glst, b_lo + col, b_hi);
+    const uint32_t ro = static_cast<uint32_t>(e.u >= 0 ? e.u : 0) * (2u * D) + rlane;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) rf[ks] = *reinterpret_cast<const u32x4_t*>(rbase + ro + 32 * ks);
+    issue(e, bl_a);
+  }
+  // one block: the next block's W pieces, gates and R rows are requested
+  // into `nxt` / rf while this block (`cur`, rf) is computed
+  auto block = [&](int b0, const BlockLoads& cur, BlockLoads& nxt, const SpEntry& ul_nxt, SpEntry& ul_nx2) {
+    __builtin_amdgcn_sched_barrier(0);  // nothing of the next block moves up into this one
+    issue(ul_nxt, nxt);
+    ul_nx2 = sp_entry(lst, glst, b0 + 64 + col, b_hi);  // list entries two blocks ahead
+    // read GEMM over this wave's k-slab
+    f32x16_t racc = {};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) racc = mfma(rf[ks], xs[wave][ks][lane], racc);
+    // the next block's R rows
+    {
+      const uint32_t ro = static_cast<uint32_t>(ul_nxt.u >= 0 ? ul_nxt.u : 0) * (2u * D) + rlane;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) rf[ks] = *reinterpret_cast<const u32x4_t*>(rbase + ro + 32 * ks);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) part[wave][g][lane] = float4{racc[4 * g], racc[4 * g + 1], racc[4 * g + 2], racc[4 * g + 3]};
+    __syncthreads();
+    // elements 2 wave, 2 wave + 1: x.r summed over the k-slabs in order, the
+    // bf16 gates from G (v41:503-518)
+    {
+      float xr2[2];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float2 v2 = reinterpret_cast<const float2*>(&part[q][wave >> 1][lane])[wave & 1];
+        xr2[0] = q ? xr2[0] + v2.x : v2.x;
+        xr2[1] = q ? xr2[1] + v2.y : v2.y;
+      }
+      const uint32_t xq2 = pack_bf16(xr2[0], xr2[1]);                                   // bf16 x.r (v41:517)
+      const uint32_t g2 = ((cur.q0 >> gsh) & 0xffffu) | ((cur.q1 >> gsh) << 16);
+      const uint32_t gq = g2 & ((cur.pad0 ? 0u : 0xffffu) | (cur.pad1 ? 0u : 0xffff0000u));  // gate_bf (v41:516)
+      pl[wave][lane] = pack_bf16(lo_f32(gq) * lo_f32(xq2), hi_f32(gq) * hi_f32(xq2));  // (v41:518)
+    }
+    __syncthreads();
+    // write GEMM: OUT[32 tokens x this wave's columns] += P . W_blk
+    const u32x4_t a0 = {pl[0][lane], pl[1][lane], pl[2][lane], pl[3][lane]};
+    const u32x4_t a1 = {pl[4][lane], pl[5][lane], pl[6][lane], pl[7][lane]};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int f = 0; f < F; ++f) {
+        u32x4_t bf;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          bf[e] = SpPiece<F>::at(cur.wp[j][2 * e], f) | (SpPiece<F>::at(cur.wp[j][2 * e + 1], f) << 16);
+        oacc[f] = mfma(j ? a1 : a0, bf, oacc[f]);
+      }
+    }
+  };
+  // blocks in pairs; past the end a block is all padding (zero gates: P = 0
+  // adds nothing), which keeps the loop body free of a branch whose merge
+  // would need register copies
+  for (int b0 = b_lo; b0 < b_hi; b0 += 64) {
+    block(b0, bl_a, bl_b, ul_a, ul_b);
+    block(b0 + 32, bl_b, bl_a, ul_b, ul_a);
+  }
+  // the chunk's partial (zeros where none of its units is listed); the
+  // lane's first token row, register v is row 8 (v / 4) + v % 4 after it
+  const bool full_tile = static_cast<int64_t>(tile) * 32 + 32 <= p.Tv;
+  const int64_t t0 = static_cast<int64_t>(tile) * 32 + 4 * half;
+  float* op = p.out_part + (static_cast<int64_t>(c) * p.Tv + t0) * D + k0 + F * col;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int r = 8 * (v >> 2) + (v & 3);
+    if (!full_tile && t0 + r >= p.Tv) continue;
+    float* dst = op + r * D;
+    if constexpr (F == 4) {
+      *reinterpret_cast<float4*>(dst) = float4{oacc[0][v], oacc[1][v], oacc[2][v], oacc[3][v]};
+    } else if constexpr (F == 2) {
+      *reinterpret_cast<float2*>(dst) = float2{oacc[0][v], oacc[1][v]};
+    } else {
+      dst[0] = oacc[0][v];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -580,8 +1001,17 @@ TGeo tgeo(const srw_desc_t& d) {
 }
 
 struct TLayout {
-  size_t wt, P, mom, tau, out_part, tok_part, tok_sum, total;
+  size_t wt, P, mom, tau, out_part, tok_part, tok_sum, uni, list, glist, cstart, G, total;
 };
+
+// sparse skip at prefill sizes: the gathered GEMMs' widths (D = 256 F; a
+// wider D would not keep the gather kernel's fragments in 256 registers),
+// R and W rows addressed by 32-bit byte offsets
+bool sparse_width_ok(int64_t D) { return D == 256 || D == 512 || D == 1024; }
+bool tiled_sparse(const srw_desc_t& d) {
+  return (d.flags & SRW_FLAG_SPARSE_SKIP) && sparse_width_ok(d.d_model) &&
+         d.n_units * d.d_model * 2 < (int64_t(1) << 32);
+}
 
 TLayout tlayout(const srw_desc_t& d, const TGeo& g) {
   TLayout l{};
@@ -600,6 +1030,17 @@ TLayout tlayout(const srw_desc_t& d, const TGeo& g) {
   off += al256(static_cast<int64_t>(2 * g.CT) * g.Tv * 4 * 4);
   l.tok_sum = off;
   off += al256(g.Tv * 4 * 4);
+  // sparse skip: per 32-token tile the union words, the unit list and the
+  // units' slots in G, the chunk starts, and G (256 CT slots of 32 gates)
+  l.uni = l.list = l.glist = l.cstart = l.G = off;
+  if (tiled_sparse(d)) {
+    const int64_t tt = (g.Tv + 31) / 32, w32 = (g.N + 31) / 32;
+    l.list = l.uni + al256(tt * w32 * 4);
+    l.glist = l.list + al256(tt * g.N * 4);
+    l.cstart = l.glist + al256(tt * g.N * 4);
+    l.G = l.cstart + al256(tt * (g.nc + 1) * 4);
+    off = l.G + al256(tt * (static_cast<int64_t>(g.CT) * 256) * 32 * 2);
+  }
   l.total = off;
   return l;
 }
@@ -619,8 +1060,8 @@ bool tiled_supports(const srw_desc_t& d) {
   if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41) return false;
   if (!tile_offsets_fit(d.n_units)) return false;
   if (d.stats_mode != SRW_STATS_ONEPASS && d.stats_mode != SRW_STATS_CENTERED) return false;
-  // SRW_FLAG_SPARSE_SKIP runs dense here: no 32-token x 32-unit block of a
-  // prefill call is free of passing units at the reference's pass rates
+  // SRW_FLAG_SPARSE_SKIP: d_model = 256, 512 or 1024 takes the sparse-skip
+  // kernels (mark, list, gathered GEMMs); other widths run dense
   if (d.flags & (SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST)) return false;
   if (d.n_routes != 1 && d.n_routes != 2) return false;
   if (d.d_model % kNAlign != 0 || d.d_route % kNAlign != 0) return false;
@@ -628,6 +1069,94 @@ bool tiled_supports(const srw_desc_t& d) {
 }
 
 size_t tiled_workspace_bytes(const srw_desc_t& d) { return tlayout(d, tgeo(d)).total; }
+
+bool tiled_runs_sparse(const srw_desc_t& d) { return tiled_sparse(d); }
+
+// Sparse skip after the dense score GEMM and tau: mark, list, the gathered
+// GEMMs, then the token sums and the finalize as on the dense path.
+hipError_t tiled_sparse_rest(const LaunchArgs& a, const TGeo& g, const TLayout& l) {
+  const srw_desc_t& d = a.d;
+  const int D = static_cast<int>(d.d_model);
+  const uint16_t* S = reinterpret_cast<const uint16_t*>(a.ws + l.P);
+  const float* tau = reinterpret_cast<const float*>(a.ws + l.tau);
+  float* out_part = reinterpret_cast<float*>(a.ws + l.out_part);
+  float* tok_part = reinterpret_cast<float*>(a.ws + l.tok_part);
+  float* tok_sum = reinterpret_cast<float*>(a.ws + l.tok_sum);
+  uint32_t* uni = reinterpret_cast<uint32_t*>(a.ws + l.uni);
+  int32_t* list = reinterpret_cast<int32_t*>(a.ws + l.list);
+  int32_t* glist = reinterpret_cast<int32_t*>(a.ws + l.glist);
+  int32_t* cstart = reinterpret_cast<int32_t*>(a.ws + l.cstart);
+  uint16_t* G = reinterpret_cast<uint16_t*>(a.ws + l.G);
+  const int64_t TT32 = (g.Tv + 31) / 32, W32 = (g.N + 31) / 32, GS = static_cast<int64_t>(g.CT) * 256;
+  const float exp_scale = -d.sharpness * 1.4426950408889634f;
+  hipError_t e;
+  SpMarkParams mp{};
+  mp.S = S;
+  mp.tau = tau;
+  mp.tok_part = tok_part;
+  mp.mask32 = reinterpret_cast<uint32_t*>(a.o.pass_mask);
+  mp.uni = uni;
+  mp.G = G;
+  mp.mask_words32 = 2 * a.words;
+  mp.W32 = W32;
+  mp.GS = GS;
+  mp.Tv = g.Tv;
+  mp.N = g.N;
+  mp.N64 = g.N64;
+  mp.CT = g.CT;
+  mp.gp = a.gp;
+  mp.exp_scale = exp_scale;
+  const int64_t sgroups = (2 * g.CT + 3) / 4;
+  hipLaunchKernelGGL(sp_mark_kernel, dim3(static_cast<unsigned>(TT32 * sgroups)), dim3(256), 0, a.stream, mp);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(tiled_tok_sum_kernel, dim3(static_cast<unsigned>((g.Tv + 63) / 64)), dim3(256), 0, a.stream,
+                     tok_part, tok_sum, g.Tv, 2 * g.CT);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(sp_list_kernel, dim3(static_cast<unsigned>(TT32)), dim3(256), 0, a.stream, uni, W32, g.N, g.cs,
+                     g.nc, list, glist, cstart);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  SpGatherParams sp{};
+  sp.x = static_cast<const uint16_t*>(a.in.x);
+  sp.read = static_cast<const uint16_t*>(a.in.read);
+  sp.write = static_cast<const uint16_t*>(a.in.write);
+  sp.G = G;
+  sp.list = list;
+  sp.glist = glist;
+  sp.cstart = cstart;
+  sp.out_part = out_part;
+  sp.Tv = g.Tv;
+  sp.N = g.N;
+  sp.GS = GS;
+  sp.routes = d.n_routes;
+  sp.nc = g.nc;
+  sp.TT32 = static_cast<int>(TT32);
+  const dim3 grid_g(static_cast<unsigned>(TT32 * g.nc));  // (chunk, tile), chunk-major
+  dominant_kernel_begin(a.stream);
+  switch (D / 256) {
+    case 1: hipLaunchKernelGGL(sp_gather_kernel<1>, grid_g, dim3(kSpThreads), 0, a.stream, sp); break;
+    case 2: hipLaunchKernelGGL(sp_gather_kernel<2>, grid_g, dim3(kSpThreads), 0, a.stream, sp); break;
+    default: hipLaunchKernelGGL(sp_gather_kernel<4>, grid_g, dim3(kSpThreads), 0, a.stream, sp); break;
+  }
+  dominant_kernel_end(a.stream);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  FinalizeArgs f{};
+  f.out_part = out_part;
+  f.tok_part = tok_sum;
+  f.out = static_cast<uint16_t*>(a.o.out);
+  f.gate_sum = a.o.gate_sum;
+  f.den = a.o.den;
+  f.n_active = a.o.n_active;
+  f.T = g.Tv;
+  f.D = D;
+  f.S = g.nc;  // one partial per reference chunk
+  f.spc = 1;
+  f.S_tok = 1;
+  f.tps = 4;
+  f.scale = d.scale;
+  f.gp = a.gp;
+  f.exp_scale = exp_scale;
+  return launch_finalize(f, a.stream);
+}
 
 hipError_t tiled_forward(const LaunchArgs& a) {
   const srw_desc_t& d = a.d;
@@ -648,7 +1177,7 @@ hipError_t tiled_forward(const LaunchArgs& a) {
                          reinterpret_cast<const void*>(tiled_write_kernel)})
     if ((e = set_lds(fn)) != hipSuccess) return e;
 
-  if (!(d.flags & SRW_FLAG_POOL_CACHED)) {
+  if (!(d.flags & SRW_FLAG_POOL_CACHED) && !tiled_sparse(d)) {  // (the sparse path gathers W's rows)
     const dim3 grid_p(static_cast<unsigned>(g.N64 / 64), static_cast<unsigned>((D + 63) / 64));
     hipLaunchKernelGGL(pack_wt_kernel, grid_p, dim3(256), 0, a.stream, static_cast<const uint16_t*>(a.in.write), wt,
                        g.N, g.N64, D);
@@ -675,6 +1204,8 @@ hipError_t tiled_forward(const LaunchArgs& a) {
                       d.stats_mode == SRW_STATS_CENTERED ? kTauChan : kTauOnePass, a.stream, nullptr, 128)) !=
       hipSuccess)
     return e;
+
+  if (tiled_sparse(d)) return tiled_sparse_rest(a, g, l);
 
   TGateParams gp{};
   gp.x = static_cast<const uint16_t*>(a.in.x);

@@ -102,12 +102,15 @@ typedef enum srw_stats_mode {
 #define SRW_FLAG_EMULATE 0x2u     /* reference rounding emulation (per-chunk bf16 rounding
                                      of the partial write GEMM, v41:518); selects the
                                      bit-faithful scalar kernels */
-#define SRW_FLAG_SPARSE_SKIP 0x4u /* skip the read rows and write-fragment halves of units
-                                     no row of the call passes (the decode kernel, calls of
-                                     <= 128 rows): exact for the v4.0.1 gate (their gates
-                                     are 0); under v4.1 their epsilon-sized gates are left
-                                     out of out only (sums, den and the mask keep them).
-                                     Other paths run dense (no counterpart in the
+#define SRW_FLAG_SPARSE_SKIP 0x4u /* skip units no row passes: the decode kernel (calls of
+                                     <= 128 rows) leaves out the read rows and write-fragment
+                                     halves of units no row of the call passes; the tiled
+                                     family (d_model 256 / 512 / 1024) runs the read and
+                                     write GEMMs of each 32-row tile over the units some row
+                                     of the tile passes.  Exact for the v4.0.1 gate (their
+                                     gates are 0); under v4.1 their epsilon-sized gates are
+                                     left out of out only (sums, den and the mask keep
+                                     them).  Other paths run dense (no counterpart in the
                                      reference, which computes every unit). */
 #define SRW_FLAG_NO_FAST 0x8u     /* force the generic kernels (testing) */
 #define SRW_FLAG_POOL_CACHED 0x10u /* emb, read and write are unchanged since the last call

@@ -377,7 +377,7 @@ def fused_gate_srw_paired(x, h, emb, tau_offset, read, write, *,
     dead_cnt = torch.zeros((), dtype=F32)
     int_max = torch.zeros((), dtype=F32)
     int_cap = torch.zeros((), dtype=F32)
-    trace_margin = []
+    trace_margin, trace_gate = [], []
     for i in range(nc):                                            # :768-840
         sl = slice(i * cs, (i + 1) * cs)
         ec, rc, wc = emb_bf[sl], read_bf[sl], write_bf[sl]
@@ -411,6 +411,7 @@ def fused_gate_srw_paired(x, h, emb, tau_offset, read, write, *,
         int_cap = int_cap + chunk_int_cap
         if return_trace:
             trace_margin.append(margin)
+            trace_gate.append(gate)
 
     den = torch.clamp_min(zsum, 1.0)                               # :858
     out_f = (out / den).to(BF16).to(F32)                           # :859-860
@@ -434,7 +435,8 @@ def fused_gate_srw_paired(x, h, emb, tau_offset, read, write, *,
         return res
     trace = dict(s_mean=s_mean, s_std=s_std, tau=tau, den=den, gate_sum=wsum,
                  intensity_sum=zsum, n_active=act_n, raw_out=out,
-                 margin=torch.cat(trace_margin, dim=-1), nc=nc, cs=cs)
+                 margin=torch.cat(trace_margin, dim=-1),
+                 gate=torch.cat(trace_gate, dim=-1), nc=nc, cs=cs)
     return res, trace
 
 
