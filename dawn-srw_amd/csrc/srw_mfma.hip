@@ -457,6 +457,23 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
     auto frag = [&](int ks) {
       return *reinterpret_cast<const u32x4_t*>(base + le[ks % TileE::NM] + TileE::step_off(ks));
     };
+    // the next tile's blocks (this wave's share: blocks wave, wave + 4, ...),
+    // requested before this tile's k-loop; a whole tile inside the pool from
+    // a uniform base plus the lane's offset
+    if (pre) {
+      const int64_t row0 = static_cast<int64_t>(tile + 1) * kUnitTile;
+      if (row0 + kUnitTile <= p.g.N) {
+        const char* enext = reinterpret_cast<const char*>(p.emb) + row0 * TileE::K * 2;
+#pragma unroll
+        for (int j0 = 0; j0 < KH; j0 += 4) {
+          const int j = j0 + wave;
+          if (KH % 4 == 0 || j < KH)
+            g2lds16(enext + TileE::block_off(j) + lsrc[(j % TileE::RG) & 1], lds + (st ^ 1) * STAGE + j * kFragBytes);
+        }
+      } else {
+        for (int j = wave; j < KH; j += 4) TileE::load(p.emb, row0, p.g.N, j, lane, lsrc, lds + (st ^ 1) * STAGE);
+      }
+    }
     constexpr int PF = 4;
     u32x4_t ef[PF];
 #pragma unroll
@@ -472,9 +489,6 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
       }
       const u32x4_t e = ef[ks % PF];
       if (ks + PF < KH) ef[ks % PF] = frag(ks + PF);
-      if (pre && (ks % 4) == 0 && wave + ks < KH)  // block wave + ks: this wave's share, every 4th k-step
-        TileE::load(p.emb, static_cast<int64_t>(tile + 1) * kUnitTile, p.g.N, wave + ks, lane, lsrc,
-                    lds + (st ^ 1) * STAGE);
 #pragma unroll
       for (int b = 0; b < TBW; ++b) acc[b] = mfma(e, hq[b][ks], acc[b]);
       __builtin_amdgcn_sched_barrier(0);
@@ -508,12 +522,18 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
   for (int b = 0; b < TBW; ++b) moment_store<MODE>(ms[b], p.mom, split, p.g.T, tt[b], half);
 }
 
+// Three workgroups per CU where the registers allow it without spills (not
+// with the diagnostics' extra power sums, nor in the batch kernel): a third
+// wave per SIMD covers the tile loop's LDS and barrier waits (measured 97.1
+// -> 93.6 us at the Know pool).
+template <int MODE>
+constexpr int stats_min_blocks() { return MODE == kStatsDiag ? 2 : 3; }
 template <int KH, int MODE, int TBW>
-__global__ __launch_bounds__(kThreads) void srw_stats_kernel(StatsParams p) {
+__global__ __launch_bounds__(kThreads, stats_min_blocks<MODE>()) void srw_stats_kernel(StatsParams p) {
   stats_body<KH, MODE, TBW>(p, blockIdx.x);
 }
 template <int KH, int MODE>
-__global__ __launch_bounds__(kThreads) void srw_stats_batch_kernel(Batch<StatsParams> b) {
+__global__ __launch_bounds__(kThreads) void srw_stats_batch_kernel(Batch<StatsParams> b) {  // (3 would spill)
   const int i = batch_index(b.start, b.n, blockIdx.x);
   stats_body<KH, MODE, 1>(b.p[i], blockIdx.x - b.start[i]);
 }
