@@ -39,6 +39,7 @@ SRW_FLAG_SPARSE_SKIP = 0x4
 SRW_FLAG_NO_FAST = 0x8
 SRW_FLAG_POOL_CACHED = 0x10
 SRW_FLAG_TILED = 0x20
+SRW_FLAG_GATE_OUT = 0x40
 
 # token_diag columns (SRW_TDIAG_*) and unit_diag columns (SRW_UDIAG_*)
 TDIAG = (

@@ -40,7 +40,7 @@ srw_status_t validate(const srw_desc_t* d) {
       !isfinite(d->epsilon) || !isfinite(d->max_intensity) || !isfinite(d->scale))
     return SRW_EINVAL;
   if (d->flags & ~(SRW_FLAG_DIAG | SRW_FLAG_EMULATE | SRW_FLAG_SPARSE_SKIP | SRW_FLAG_NO_FAST | SRW_FLAG_POOL_CACHED |
-                   SRW_FLAG_TILED))
+                   SRW_FLAG_TILED | SRW_FLAG_GATE_OUT))
     return SRW_EINVAL;
   return SRW_OK;
 }
@@ -50,7 +50,10 @@ srw_status_t validate(const srw_desc_t* d) {
 // the pointers).
 int choose(const srw_desc_t& d, bool h_is_x) {
   const bool force_generic = (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST)) != 0;
-  if (!force_generic) {
+  if (!force_generic && (d.flags & SRW_FLAG_GATE_OUT)) {  // the dense gate from the tiled gate epilogue
+    if (srw::tiled_supports(d)) return 2;
+    if (srw::tiled_f32_supports(d)) return 3;
+  } else if (!force_generic) {
     if ((d.flags & SRW_FLAG_TILED) && srw::tiled_supports(d)) return 2;
     if (srw::mfma_supports(d, h_is_x)) return 1;
     if (srw::tiled_supports(d)) return 2;
@@ -190,7 +193,9 @@ srw_status_t prepare_forward(const srw_desc_t* d, const srw_tensors_t* in, const
   if (st != SRW_OK) return st;
   if (!in || !o) return SRW_EINVAL;
   int w = choose(*d, in->h != nullptr && in->h == in->x);
-  if (w > 0 && o->gate) w = srw::generic_supports(*d) ? 0 : -1;  // the dense gate: generic kernels
+  // the dense gate: the tiled families under SRW_FLAG_GATE_OUT, else the generic kernels
+  if (w > 0 && o->gate && !((d->flags & SRW_FLAG_GATE_OUT) && (w == 2 || w == 3)))
+    w = srw::generic_supports(*d) ? 0 : -1;
   if (w < 0) return SRW_EUNSUPPORTED;
   if (d->T == 0) {  // nothing to compute; empty tensors may carry null pointers
     *which = -2;

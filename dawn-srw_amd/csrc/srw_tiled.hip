@@ -291,6 +291,7 @@ struct TGateParams {
   uint16_t* XR_out;      // KEEP: bf16 x.r [Tv, N64]
   float* tok_part;       // [2 CT][Tv][4]: sum gate, sum intensity, active count
   uint32_t* mask32;      // [Tv][mask_words32] or null
+  float* G;              // [Tv, N] every unit's fp32 gate (SRW_FLAG_GATE_OUT) or null
   int64_t mask_words32;
   int64_t Tv, N, N64, D;
   int routes, RT, CT;
@@ -385,6 +386,10 @@ __global__ __launch_bounds__(kGThreads) void tiled_gate_kernel(TGateParams p) {
             is += inten;
             bits = __builtin_amdgcn_alignbit(bits, sign, 31);  // bits << 1 | sign bit
             g2[e] = g;
+            if constexpr (!KEEP) {
+              const int64_t un = nb + 8 * ((v + e) >> 2) + ((v + e) & 3);
+              if (p.G && tok && un < p.N) p.G[t * p.N + un] = g;
+            }
           }
           const uint32_t gq = pack_bf16(g2[0], g2[1]);                              // gate_bf (v41:516)
           const uint32_t xq = pack_bf16(acc[i][j][v], acc[i][j][v + 1]);            // xr (v41:517)
@@ -1009,7 +1014,7 @@ struct TLayout {
 // R and W rows addressed by 32-bit byte offsets
 bool sparse_width_ok(int64_t D) { return D == 256 || D == 512 || D == 1024; }
 bool tiled_sparse(const srw_desc_t& d) {
-  return (d.flags & SRW_FLAG_SPARSE_SKIP) && sparse_width_ok(d.d_model) &&
+  return (d.flags & SRW_FLAG_SPARSE_SKIP) && !(d.flags & SRW_FLAG_GATE_OUT) && sparse_width_ok(d.d_model) &&
          d.n_units * d.d_model * 2 < (int64_t(1) << 32);
 }
 
@@ -1214,6 +1219,7 @@ hipError_t tiled_forward(const LaunchArgs& a) {
   gp.P = P;
   gp.tok_part = tok_part;
   gp.mask32 = reinterpret_cast<uint32_t*>(a.o.pass_mask);
+  gp.G = (d.flags & SRW_FLAG_GATE_OUT) ? a.o.gate : nullptr;
   gp.mask_words32 = 2 * a.words;
   gp.Tv = g.Tv;
   gp.N = g.N;

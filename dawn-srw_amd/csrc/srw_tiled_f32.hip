@@ -311,6 +311,7 @@ struct FGateParams {
   float* P;           // [Tv, N64]: the scores in, P out (in place)
   float* tok_part;    // [2 CT][Tv][4]: sum gate, sum intensity, active count
   uint32_t* mask32;   // [Tv][mask_words32] or null
+  float* G;           // [Tv, N] every unit's gate (SRW_FLAG_GATE_OUT) or null
   int64_t mask_words32;
   int64_t Tv, N, N64, D;
   int routes, RT, CT;  // token tiles, unit tiles
@@ -373,6 +374,7 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_gate_kernel(FGateParams p) {
           gs += gate;
           is += ok ? inten : 0.f;
           if (ok && act > 0.5f) m |= 1u << (8 * (v >> 2) + 4 * h + k);
+          if (p.G && tok && ok) p.G[t * p.N + nb + k] = gate;
           e[k] = gate * acc[i][j][v + k];  // P = gate * xr (v41:1735)
         }
         if (tok && in_row) *reinterpret_cast<float4*>(prow + nb) = float4{e[0], e[1], e[2], e[3]};
@@ -650,6 +652,7 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   gp.P = P;
   gp.tok_part = tok_part;
   gp.mask32 = reinterpret_cast<uint32_t*>(a.o.pass_mask);
+  gp.G = (d.flags & SRW_FLAG_GATE_OUT) ? a.o.gate : nullptr;
   gp.mask_words32 = 2 * a.words;
   gp.Tv = g.Tv;
   gp.N = g.N;

@@ -111,7 +111,8 @@ class SrwPlan:
         desc.flags = ((C.SRW_FLAG_DIAG if diag else 0) | (C.SRW_FLAG_EMULATE if emulate else 0)
                       | (C.SRW_FLAG_SPARSE_SKIP if sparse_skip else 0)
                       | (C.SRW_FLAG_NO_FAST if force_generic else 0)
-                      | (C.SRW_FLAG_TILED if tiled else 0))
+                      | (C.SRW_FLAG_TILED if tiled else 0)
+                      | (C.SRW_FLAG_GATE_OUT if want_gate else 0))
 
         words = (N + 63) // 64
         self.out = torch.empty((T, R, D), dtype=dt, device=dev)

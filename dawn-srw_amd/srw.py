@@ -248,7 +248,8 @@ def srw_inference_with_gates(x, h, emb_norm, tau_offset, w_read, w_write, *,
     gate_norm)`` with out float32 [..., D] as :func:`srw_inference`, gate_raw
     float32 [..., N] (activation x intensity of every unit) and
     gate_norm = gate_raw / max(sum_n gate_raw, 1e-8) (:1760).  The dense
-    gate comes from the generic kernels.
+    gate comes from the tiled families' gate epilogue (bf16 widths multiples
+    of 64, fp32 multiples of 32), else from the generic kernels.
     """
     lead = x.shape[:-1]
     D = x.shape[-1]

@@ -125,6 +125,12 @@ typedef enum srw_stats_mode {
                                      fused kernels do not (d_model > 384, e.g. 1024 / 1280 /
                                      2048; both widths multiples of 64).  No counterpart in
                                      the reference (a kernel-family choice). */
+#define SRW_FLAG_GATE_OUT 0x40u   /* the call passes outputs->gate: the workspace query and
+                                     the kernel choice take the tiled matrix-core families
+                                     (bf16 d_model / d_route multiples of 64, fp32 multiples
+                                     of 32; v4.1, one-pass or centred statistics), whose
+                                     gate epilogue also writes every unit's fp32 gate.
+                                     Without it a gate output runs the generic kernels. */
 
 typedef struct srw_desc {
   int64_t T;          /* tokens (B*S) */
@@ -199,8 +205,9 @@ typedef struct srw_outputs {
   float* unit_diag;        /* [N, SRW_UDIAG_COUNT]            needs SRW_FLAG_DIAG */
   float* gate;             /* [T, n_routes, N] gate (activation x intensity, fp32) of every
                               unit: the gate_raw of _srw_inference_with_gates
-                              (models/dawn_spatial_v41_exp.py:1741-1769).  Optional; a
-                              call that sets it runs the generic kernels. */
+                              (models/dawn_spatial_v41_exp.py:1741-1769).  Optional; with
+                              SRW_FLAG_GATE_OUT the tiled families write it, else the
+                              call runs the generic kernels. */
 } srw_outputs_t;
 
 /* Cotangents for srw_backward: of the three outputs of fused_gate_srw that

@@ -10,7 +10,8 @@ Tolerances (from the hot path's contract):
     or 1e-5 * max(1, s_std) (float32); inside the band at most
     MIS_BASE + MIS_PER_PAIR * (rows x units) mismatches (plus, where the
     moments are computed another way on purpose -- Gram statistics -- every
-    pair inside that known tau shift).
+    pair inside that known tau shift);
+  * dense gate (every unit's fp32 gate): see gate_close.
 """
 
 from __future__ import annotations
@@ -86,3 +87,32 @@ def assert_pass_set(mask_got: torch.Tensor, margin_ref: torch.Tensor, delta: tor
     assert n_out == 0, f"{n_out} passing-set mismatches outside the tie band ({n_mis} total)"
     assert n_mis <= bound, f"{n_mis} passing-set mismatches inside the tie band, more than {bound:.1f}"
     return n_mis
+
+
+def gate_close(got: torch.Tensor, ref: torch.Tensor, h: torch.Tensor, emb: torch.Tensor) -> tuple[bool, int]:
+    """Dense gates [T, N] of two correct evaluations: equal within rtol 1e-3,
+    atol 1e-7 where the score is determined, else anything.
+
+    The gate act x intensity with act = sigmoid(500 margin): an fp32
+    evaluation of the exponent 500 log2(e) margin rounds by up to ~721 x 2^-24
+    x (|s| + |tau| + thr) absolute, moving act by as much relative (rtol
+    1e-3).  The score itself comes from a dot product summed in different
+    orders: in bf16 (h, emb bf16) a score within the fp32 accumulation error
+    bound 2 dr 2^-24 sum|h||e| of a bf16 rounding midpoint may round either
+    way (one ulp, which the slope 500 amplifies without bound) and is left
+    out; in fp32 that bound, times 721 ln 2, joins the relative tolerance.
+    Returns (ok, number of gates compared)."""
+    hh, ee = h.double(), emb.double()
+    s64 = hh @ ee.T
+    acc = 2 * hh.shape[-1] * 2.0 ** -24 * (hh.abs() @ ee.abs().T)
+    if h.dtype == torch.bfloat16:
+        sb = s64.to(torch.bfloat16).double()
+        keep = (bf16_ulp(sb) / 2 - (s64 - sb).abs()) > 2 * acc
+        rtol = torch.full_like(s64, 1e-3)
+    else:
+        keep = torch.ones_like(s64, dtype=torch.bool)
+        rtol = 1e-3 + 721 * 0.7 * acc
+    g, r = got.double(), ref.double()
+    ok = bool((((g - r).abs() <= rtol * r.abs() + 1e-7) | ~keep).all())
+    return ok, int(keep.sum())
+

@@ -127,6 +127,18 @@ def test_workspace_sizes(C):
     assert C.workspace_size(d) == 2 * 100 * 64 * 4
 
 
+def test_gate_out_sizes_the_tiled_families(C):
+    """SRW_FLAG_GATE_OUT: the dense gate comes from the tiled gate epilogue
+    (bf16 widths multiples of 64, fp32 of 32), else the generic kernels."""
+    bf_tiled = C.workspace_size(_desc(C, d_route=64, flags=C.SRW_FLAG_TILED))
+    assert bf_tiled > 0
+    assert C.workspace_size(_desc(C, d_route=64, flags=C.SRW_FLAG_GATE_OUT)) == bf_tiled
+    # d_route = 32 has no bf16 tiled kernel: the generic kernels, no workspace
+    assert C.workspace_size(_desc(C, flags=C.SRW_FLAG_GATE_OUT)) == 0
+    f32 = C.workspace_size(_desc(C, dtype=C.SRW_F32))
+    assert f32 > 0 and C.workspace_size(_desc(C, dtype=C.SRW_F32, flags=C.SRW_FLAG_GATE_OUT)) == f32
+
+
 @pytest.mark.parametrize("shape", [(384, 384, 1, 0), (384, 128, 2, 0), (1024, 1024, 1, 0),
                                    (384, 384, 1, 0x20), (128, 64, 1, 0)])
 def test_no_tokens_need_no_workspace(C, shape):

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from oracle import srw_ref
-from tests.parity import rel_fro, unpack_mask
+from tests.parity import gate_close, rel_fro, unpack_mask
 from tests.test_gpu_mfma import _check, _gpu, _inputs, _oracle
 
 pytestmark = pytest.mark.gpu
@@ -113,3 +113,49 @@ def test_tiled_pool_cached(pkg, dev):
     fresh = _gpu(pkg, dev, dict(inp, x=torch.roll(inp["x"], 1, dims=0)), 0)
     assert torch.equal(plan.out.cpu(), fresh["out"])
     assert torch.equal(torch.roll(first, 1, dims=0).cpu(), fresh["out"])
+
+
+GATE_CASES = [
+    # dtype, T, D, dr, N, stats, path
+    (torch.bfloat16, 200, 128, 64, 1500, "centered", "tiled_bf16"),
+    (torch.bfloat16, 130, 256, 128, 700, "onepass", "tiled_bf16"),
+    (torch.float32, 150, 96, 32, 900, "centered", "tiled_f32"),
+]
+
+
+@pytest.mark.parametrize("case", GATE_CASES, ids=lambda c: "{}T{}D{}dr{}N{}{}".format(
+    "bf16" if c[0] == torch.bfloat16 else "f32", *c[1:6]))
+def test_tiled_dense_gate_output(pkg, dev, case):
+    """The dense fp32 gate of every unit (_srw_inference_with_gates' gate_raw,
+    v41:1741-1769) written by the tiled gate epilogue under
+    SRW_FLAG_GATE_OUT: against the oracle's gates and the generic kernels'
+    gates on the same inputs, with out / den unchanged from the call without
+    the gate (tolerance: tests.parity.gate_close; the epilogue's exponent
+    is s c + k with k = -(tau + thr) c in bf16, and its tau comes from
+    one-pass sums or Chan-merged centred slices)."""
+    dt, T, D, dr, N, stats, path = case
+    print(f"[gpu] tiled dense gate output {case}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, False, seed=46)
+    x = inp["x"].to(dt).to(dev)
+    h = inp["h"].to(dt).to(dev)
+    args = (x, h, inp["emb"].to(dt).to(dev), inp["tau_offset"].to(dev), inp["read"].to(dt).to(dev),
+            inp["write"].to(dt).to(dev))
+    got = pkg.srw_forward(*args, stats=stats, want_gate=True)
+    plain = pkg.srw_forward(*args, stats=stats, tiled=dt == torch.bfloat16)
+    gen = pkg.srw_forward(*args, stats=stats, want_gate=True, force_generic=True)
+    torch.cuda.synchronize()
+    assert got["path"] == path and gen["path"] == "generic"
+    assert plain["path"] == path
+    for k in ("out", "den", "gate_sum", "n_active"):
+        assert torch.equal(got[k].cpu(), plain[k].cpu()), k
+    g = got["gate"].cpu().reshape(T, N)
+    h1, e1 = inp["h"][:, 0].to(dt), inp["emb"].to(dt)
+    ok, n = gate_close(g, gen["gate"].cpu().reshape(T, N), h1, e1)
+    print(f"  compared {n} of {T * N} gates (tie band excluded)", flush=True)
+    assert ok
+    if stats == "centered":
+        _, rg, _ = srw_ref.srw_inference_with_gates(inp["x"].to(dt), h1, e1, inp["tau_offset"], inp["read"].to(dt),
+                                                    inp["write"].to(dt))
+        assert gate_close(g, rg.reshape(T, N), h1, e1)[0]
+    # the gate sums of the dense gate are the call's gate_sum
+    assert torch.allclose(g.sum(dim=-1), got["gate_sum"].cpu().reshape(T), rtol=1e-4, atol=1e-6)
