@@ -365,6 +365,12 @@ hipError_t normalize_rows_bf16(const uint16_t* src, uint16_t* dst, int64_t N, in
   return hipGetLastError();
 }
 
+hipError_t normalize_rows_f32(const float* src, float* dst, int64_t N, int64_t D, hipStream_t s) {
+  if (N <= 0) return hipSuccess;
+  hipLaunchKernelGGL((normalize_rows_kernel<float>), dim3(static_cast<unsigned>(N)), dim3(kGT), 0, s, src, dst, D);
+  return hipGetLastError();
+}
+
 hipError_t fill_f32(float* p, int64_t n, float v, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   int64_t blocks = (n + 255) / 256;

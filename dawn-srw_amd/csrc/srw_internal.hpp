@@ -42,6 +42,8 @@ hipError_t fill_f32(float* p, int64_t n, float v, hipStream_t s);
 // (v4.0.1 forward normalisation of the read / write rows, v401:300-301),
 // see srw_generic.hip.
 hipError_t normalize_rows_bf16(const uint16_t* src, uint16_t* dst, int64_t N, int64_t D, hipStream_t s);
+// r / (||r|| + 1e-8) per row in fp32 (v401:1456-1457), one workgroup per row
+hipError_t normalize_rows_f32(const float* src, float* dst, int64_t N, int64_t D, hipStream_t s);
 
 // Pack a bf16 [N, D] matrix unit-contiguous in matrix-core fragment order
 // (32-unit tiles; tail units zero), see srw_mfma.hip.

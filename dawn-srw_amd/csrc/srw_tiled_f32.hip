@@ -312,14 +312,18 @@ struct FGateParams {
   float* tok_part;    // [2 CT][Tv][4]: sum gate, sum intensity, active count
   uint32_t* mask32;   // [Tv][mask_words32] or null
   float* G;           // [Tv, N] every unit's gate (SRW_FLAG_GATE_OUT) or null
+  const float* sstd;  // [Tv] s_std (the v4.0.1 gate)
   int64_t mask_words32;
   int64_t Tv, N, N64, D;
   int routes, RT, CT;  // token tiles, unit tiles
   GateParams gp;
 };
 
-// tiles as f32_stats_kernel's
-template <int MJ>
+// tiles as f32_stats_kernel's.  GL: the v4.0.1 gate of _srw_inference
+// (v401:1451-1453): z = (s - tau) / s_std, gate = z Phi(z) for z > 0; a unit
+// is active where its gate is > 0, and the row sums carry z+ where v4.1 has
+// the intensity
+template <int MJ, bool GL>
 __global__ __launch_bounds__(kFThreads, 1) void f32_gate_kernel(FGateParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
@@ -349,6 +353,7 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_gate_kernel(FGateParams p) {
     const bool tok = t < p.Tv;
     float* prow = p.P + (tok ? t : p.Tv - 1) * p.N64;
     const float tau = p.tau[tok ? t : p.Tv - 1];
+    const float sstd = GL ? p.sstd[tok ? t : p.Tv - 1] : 1.f;
     float gs = 0.f, is = 0.f;
     int na = 0;
 #pragma unroll
@@ -366,14 +371,22 @@ __global__ __launch_bounds__(kFThreads, 1) void f32_gate_kernel(FGateParams p) {
           // margin = (s - tau) - thr, sigmoid(sharpness margin) through the
           // hardware exp2 (within 2 ulp of expf), intensity and gate in the
           // reference's order (v41:1723-1728)
-          const float margin = (e[k] - tau) - p.gp.thr;
-          const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(margin * k_exp2));
-          const float inten = p.gp.eps + fminf(fmaxf(margin - p.gp.cut, 0.0f), p.gp.maxi);
           const bool ok = r + k < nleft;  // units past N count for nothing
-          const float gate = ok ? act * inten : 0.f;
+          float gate;
+          if constexpr (GL) {
+            const GeluOut go = gate_gelu_v401(e[k], tau, sstd);
+            gate = ok ? go.gate : 0.f;
+            is += ok && go.z > 0.f ? go.z : 0.f;
+            if (gate > 0.f) m |= 1u << (8 * (v >> 2) + 4 * h + k);
+          } else {
+            const float margin = (e[k] - tau) - p.gp.thr;
+            const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(margin * k_exp2));
+            const float inten = p.gp.eps + fminf(fmaxf(margin - p.gp.cut, 0.0f), p.gp.maxi);
+            gate = ok ? act * inten : 0.f;
+            is += ok ? inten : 0.f;
+            if (ok && act > 0.5f) m |= 1u << (8 * (v >> 2) + 4 * h + k);
+          }
           gs += gate;
-          is += ok ? inten : 0.f;
-          if (ok && act > 0.5f) m |= 1u << (8 * (v >> 2) + 4 * h + k);
           if (p.G && tok && ok) p.G[t * p.N + nb + k] = gate;
           e[k] = gate * acc[i][j][v + k];  // P = gate * xr (v41:1735)
         }
@@ -475,6 +488,7 @@ struct FFinalParams {
   int32_t* n_active;
   int64_t Tv, D;
   int S, S_tok;
+  int den_gate;           // den = max(sum gate, 1) (the v4.0.1 gate, v401:1461-1462)
   float scale;
 };
 
@@ -503,7 +517,7 @@ __global__ __launch_bounds__(256) void f32_final_kernel(FFinalParams p) {
     const float G = red[0][0] + red[0][1] + red[0][2] + red[0][3];
     const float I = red[1][0] + red[1][1] + red[1][2] + red[1][3];
     const float A = red[2][0] + red[2][1] + red[2][2] + red[2][3];
-    const float den = fmaxf(I, 1.0f);  // v41:1736
+    const float den = fmaxf(p.den_gate ? G : I, 1.0f);  // v41:1736, v401:1461-1462
     den_s = den;
     if (p.gate_sum) p.gate_sum[t] = G;
     if (p.den) p.den[t] = den;
@@ -557,7 +571,7 @@ FGeo fgeo(const srw_desc_t& d) {
 }
 
 struct FLayout {
-  size_t wt, P, mom, tau, out_part, tok_part, total;
+  size_t wt, P, mom, tau, out_part, tok_part, rn, wn, sstd, total;
 };
 
 FLayout flayout(const srw_desc_t& d, const FGeo& g) {
@@ -575,6 +589,13 @@ FLayout flayout(const srw_desc_t& d, const FGeo& g) {
   off += fal256(static_cast<int64_t>(g.S) * g.Tv * d.d_model * 4);
   l.tok_part = off;
   off += fal256(static_cast<int64_t>(2 * g.CT) * g.Tv * 4 * 4);
+  // the v4.0.1 gate: forward-normalised R and W (v401:1456-1457), s_std per row
+  l.rn = l.wn = l.sstd = off;
+  if (d.gate == SRW_GATE_GELU_V401) {
+    l.wn = l.rn + fal256(d.n_units * d.d_model * 4);
+    l.sstd = l.wn + fal256(d.n_units * d.d_model * 4);
+    off = l.sstd + fal256(g.Tv * 4);
+  }
   l.total = off;
   return l;
 }
@@ -582,7 +603,7 @@ FLayout flayout(const srw_desc_t& d, const FGeo& g) {
 }  // namespace
 
 bool tiled_f32_supports(const srw_desc_t& d) {
-  if (d.dtype != SRW_F32 || d.gate != SRW_GATE_V41) return false;
+  if (d.dtype != SRW_F32) return false;  // v4.1, or the v4.0.1 GELU gate of _srw_inference
   // operand offsets within a 256-row tile are 32-bit: 256 rows of the
   // [T, N64] fp32 scores / P must stay below 4 GiB
   if (256 * ((d.n_units + 63) / 64 * 64) * 4 >= (int64_t(1) << 32)) return false;
@@ -609,16 +630,31 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   const int D = static_cast<int>(d.d_model);
   hipError_t e;
   static_assert(kFGemmLds <= 160 * 1024, "LDS per workgroup");
+  const bool gl = d.gate == SRW_GATE_GELU_V401;
   for (const void* fn : {reinterpret_cast<const void*>(f32_stats_kernel<1>),
-                         reinterpret_cast<const void*>(f32_gate_kernel<1>),
+                         reinterpret_cast<const void*>(f32_gate_kernel<1, false>),
+                         reinterpret_cast<const void*>(f32_gate_kernel<1, true>),
                          reinterpret_cast<const void*>(f32_write_kernel<8, 8, 4, 4>),
                          reinterpret_cast<const void*>(f32_write_kernel<4, 6, 2, 3>)})
     if ((e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kFGemmLds)) != hipSuccess) return e;
 
+  // the v4.0.1 gate reads forward-normalised rows (kept in the workspace
+  // across calls that declare the pool cached)
+  const float* read_rows = static_cast<const float*>(a.in.read);
+  const float* write_rows = static_cast<const float*>(a.in.write);
+  if (gl) {
+    float* rn = reinterpret_cast<float*>(a.ws + l.rn);
+    float* wn = reinterpret_cast<float*>(a.ws + l.wn);
+    if (!(d.flags & SRW_FLAG_POOL_CACHED)) {
+      if ((e = normalize_rows_f32(read_rows, rn, g.N, D, a.stream)) != hipSuccess) return e;
+      if ((e = normalize_rows_f32(write_rows, wn, g.N, D, a.stream)) != hipSuccess) return e;
+    }
+    read_rows = rn;
+    write_rows = wn;
+  }
   if (!(d.flags & SRW_FLAG_POOL_CACHED)) {
     const dim3 grid_p(static_cast<unsigned>(g.N64 / 64), static_cast<unsigned>((D + 63) / 64));
-    hipLaunchKernelGGL(pack_wt_f32_kernel, grid_p, dim3(256), 0, a.stream, static_cast<const float*>(a.in.write),
-                       wt, g.N, g.N64, D);
+    hipLaunchKernelGGL(pack_wt_f32_kernel, grid_p, dim3(256), 0, a.stream, write_rows, wt, g.N, g.N64, D);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   // score and gate kernels: 256-unit x 64-token tiles, two stages of 256 + 64 operand rows
@@ -640,14 +676,16 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   if ((e = hipGetLastError()) != hipSuccess) return e;
   // tau per row from the 2 CT partials of 128 units (centred: merged by
   // Chan's formula, no second pass over the stored scores)
+  float* sstd = gl ? reinterpret_cast<float*>(a.ws + l.sstd) : nullptr;
   if ((e = launch_tau(mom, a.in.tau_offset, tau, g.Tv, 2 * g.CT, g.N, 2, nullptr,
-                      d.stats_mode == SRW_STATS_CENTERED ? kTauChan : kTauOnePass, a.stream, nullptr, 128)) !=
+                      d.stats_mode == SRW_STATS_CENTERED ? kTauChan : kTauOnePass, a.stream, sstd, 128)) !=
       hipSuccess)
     return e;
 
   FGateParams gp{};
   gp.x = static_cast<const float*>(a.in.x);
-  gp.read = static_cast<const float*>(a.in.read);
+  gp.read = read_rows;
+  gp.sstd = sstd;
   gp.tau = tau;
   gp.P = P;
   gp.tok_part = tok_part;
@@ -663,7 +701,10 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   dominant_kernel_begin(a.stream);
   gp.RT = g.RTq;
   gp.CT = g.CT;
-  hipLaunchKernelGGL(f32_gate_kernel<1>, grid_q, dim3(kFThreads), kLdsQ, a.stream, gp);
+  if (gl)
+    hipLaunchKernelGGL((f32_gate_kernel<1, true>), grid_q, dim3(kFThreads), kLdsQ, a.stream, gp);
+  else
+    hipLaunchKernelGGL((f32_gate_kernel<1, false>), grid_q, dim3(kFThreads), kLdsQ, a.stream, gp);
   dominant_kernel_end(a.stream);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 
@@ -698,6 +739,7 @@ hipError_t tiled_f32_forward(const LaunchArgs& a) {
   fp.D = D;
   fp.S = g.S;
   fp.S_tok = 2 * g.CT;
+  fp.den_gate = gl;
   fp.scale = d.scale;
   hipLaunchKernelGGL(f32_final_kernel, dim3(static_cast<unsigned>(g.Tv)), dim3(256), 0, a.stream, fp);
   return hipGetLastError();

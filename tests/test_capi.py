@@ -122,8 +122,13 @@ def test_workspace_sizes(C):
     # copies (bf16) and the rows' s_std
     d = _desc(C, gate=C.SRW_GATE_GELU_V401)
     assert C.workspace_size(d) == want + 2 * al(100 * 64 * 2) + al(T * 4)
-    # ... on the generic kernels (f32): the two row copies only
+    # ... in fp32 on the fp32 matrix cores: the v4.1 layout plus forward-
+    # normalised R and W (fp32) and the rows' s_std
+    f32 = C.workspace_size(_desc(C, dtype=C.SRW_F32))
     d = _desc(C, gate=C.SRW_GATE_GELU_V401, dtype=C.SRW_F32)
+    assert C.workspace_size(d) == f32 + 2 * al(100 * 64 * 4) + al(T * 4)
+    # ... on the generic kernels (f32): the two row copies only
+    d = _desc(C, gate=C.SRW_GATE_GELU_V401, dtype=C.SRW_F32, flags=C.SRW_FLAG_NO_FAST)
     assert C.workspace_size(d) == 2 * 100 * 64 * 4
 
 

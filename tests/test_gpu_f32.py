@@ -11,6 +11,9 @@ srw_tiled_f32.hip, v_mfma_f32_32x32x2_f32) through the C ABI.
   family, pinned to the oracle in tests/test_gpu_parity.py) to the same bar.
 * configs[0] as written: the full T = 4096 x N = 25 200 Know-pool call in
   fp32, 512 of its rows against the oracle (rows are independent).
+* The v4.0.1 ``_srw_inference`` in fp32 (v401:1443-1463: forward-normalised
+  rows, z Phi(z) gate, den = max(sum gate, 1)) against the oracle's
+  ``srw_inference_gelu_v401``, to the same bar (pass <=> z > 0).
 """
 
 from __future__ import annotations
@@ -118,3 +121,37 @@ def test_configs0_fp32_full_call(pkg, dev):
     assert torch.allclose(res["den"][rows, 0].cpu(), tr["den"][:, 0], rtol=1e-5)
     delta = 1e-5 * torch.clamp_min(tr["s_std"], 1.0)
     assert_pass_set(unpack_mask(res["pass_mask"][rows, 0].cpu(), shape.N), tr["margin"], delta)
+
+
+V401 = [
+    # T, D, dr, N, R, h_is_x, tau_offset, seed
+    (150, 384, 128, 2600, 1, False, 0.6, 11),   # the reference's inference shape family, ragged
+    (64, 96, 32, 700, 1, False, 1.2, 12),       # narrow widths, a partial unit tile
+    (40, 128, 128, 900, 2, False, 0.3, 13),     # paired routes
+]
+
+
+@pytest.mark.parametrize("case", V401, ids=lambda c: "T{}D{}dr{}N{}R{}".format(*c[:5]))
+def test_f32_gelu_v401_matches_srw_inference(pkg, dev, case):
+    T, D, dr, N, R, hx, tau, seed = case
+    print(f"[gpu] tiled f32 v4.0.1 srw_inference {case}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, R, hx, seed, tau)
+    got = _gpu(pkg, dev, inp, stats="centered", gate="gelu_v401")
+    assert got["path"] == "tiled_f32"
+    for r in range(R):
+        h = inp["h"][:, r]
+        ref, tr = srw_ref.srw_inference_gelu_v401(inp["x"], h, inp["emb"], inp["tau_offset"][:, r:r + 1],
+                                                  inp["read"], inp["write"], return_trace=True)
+        err = rel_fro(got["out"][:, r], ref)
+        print(f"  route {r}: out rel err {err:.3e}, active per row {got['n_active'][:, r].float().mean():.1f}",
+              flush=True)
+        assert err <= REL_F32
+        assert torch.allclose(got["den"][:, r], tr["den"][:, 0], rtol=1e-5)
+        assert torch.allclose(got["gate_sum"][:, r], tr["gate"].sum(dim=-1), rtol=1e-5, atol=1e-6)
+        # pass <=> z > 0 <=> s - tau > 0, band as for the v4.1 margin
+        raw = tr["z"] * tr["s_std"]
+        delta = 1e-5 * torch.clamp_min(tr["s_std"], 1.0)
+        mask = unpack_mask(got["pass_mask"][:, r], N)
+        assert_pass_set(mask, raw, delta)
+        assert torch.equal(got["n_active"][:, r].long(), mask.sum(dim=1))
+

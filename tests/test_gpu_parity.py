@@ -118,7 +118,8 @@ def test_generic_gelu_v401_f32(pkg, dev):
     print(f"[gpu] generic gelu v401 f32 T{T} D{D} dr{dr} N{N}", flush=True)
     inp = _inputs(pkg, T, D, dr, N, seed=11)
     inp["tau_offset"].fill_(0.7)
-    got = _run(pkg, inp, dev, F32, gate="gelu_v401", stats="centered")
+    got = _run(pkg, inp, dev, F32, gate="gelu_v401", stats="centered", force_generic=True)
+    assert got["path"] == "generic"
     ref = srw_ref.srw_inference_gelu_v401(inp["x"], inp["h"][:, 0], inp["emb"], inp["tau_offset"],
                                           inp["read"], inp["write"])
     assert rel_fro(got["out"][:, 0], ref) <= REL_F32
