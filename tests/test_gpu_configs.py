@@ -14,7 +14,8 @@ diagnostics of the matrix-core path with dead units present.
   B = 32 x S = 512 forward checked for finiteness and causality;
 * the scaled Know pool (d = 1024, N = 100 000, T = 16 384, tau
   calibrated to 2 % pass) -- 128 token rows against the oracle's
-  fused_gate_srw (:415-635), plus whole-batch properties;
+  fused_gate_srw (:415-635), plus whole-batch properties; the same call
+  with SRW_FLAG_SPARSE_SKIP against the dense one at full size;
 * dead units on the matrix-core diagnostics path (SRW_FLAG_DIAG): the
   drop-in 22-tuple's dead_count, dead_penalty and score_lb (:477-483,
   :543-552) against the oracle with planted dead units.
@@ -116,6 +117,41 @@ def test_configs4_whole_batch_properties(scaled):
     assert torch.equal(got["n_active"][:, 0].long(), mask.sum(dim=1))
     words = got["pass_mask"][:, 0]
     assert not bool(unpack_mask(words, words.shape[-1] * 64)[:, N:].any())
+
+
+def test_configs4_sparse_skip_full_call(scaled, pkg, dev):
+    """configs[4] with SRW_FLAG_SPARSE_SKIP (the gathered read / write GEMMs
+    over each 32-token tile's passing units) against the dense call of the
+    same inputs at full size: gate_sum, den, n_active and the pass mask equal
+    bit for bit (the mark kernel's arithmetic is the gate kernel's), out
+    within 1e-2 of the dense out (the epsilon-sized gates of units no token of
+    a tile passes are left out) and the first 64 rows within the bf16 bar of
+    the oracle."""
+    shape, inp, dense = scaled
+    T, N = shape.T, shape.N
+    print(f"[gpu] configs[4] sparse skip, full call T{T} N{N}", flush=True)
+    _, cs = srw_ref.chunk_plan(N, 12500)
+    x = inp["x"].to(BF).to(dev)
+    res = pkg.srw_forward(x, x, inp["emb"].to(BF).to(dev), inp["tau_offset"].to(dev),
+                          inp["read"].to(BF).to(dev), inp["write"].to(BF).to(dev), chunk_size=cs,
+                          sparse_skip=True)
+    torch.cuda.synchronize()
+    got = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in res.items()}
+    del res, x
+    torch.cuda.empty_cache()
+    assert got["path"] == "tiled_sparse_bf16"
+    for k in ("gate_sum", "den", "n_active", "pass_mask"):
+        assert torch.equal(got[k], dense[k]), k
+    err_d = rel_fro(got["out"][:, 0].float(), dense["out"][:, 0].float())
+    print(f"  out rel err vs dense {err_d:.3e}", flush=True)
+    assert err_d <= 1e-2
+    Ts = 64
+    xs = inp["x"][:Ts]
+    ref = srw_ref.fused_gate_srw(xs[None], xs[None], inp["emb"], inp["tau_offset"][:Ts][None],
+                                 inp["read"], inp["write"], max_chunk_size=12500)
+    err = rel_fro(got["out"][:Ts, 0].float(), ref[0][0])
+    print(f"  first {Ts} rows: out rel err vs oracle {err:.3e}", flush=True)
+    assert err <= REL_BF16
 
 
 def _cfg1_rows(T):
