@@ -49,6 +49,17 @@ hipError_t normalize_rows_f32(const float* src, float* dst, int64_t N, int64_t D
 // (32-unit tiles; tail units zero), see srw_mfma.hip.
 hipError_t pack_unit_major(const uint16_t* src, uint16_t* dst, int64_t N, int D, hipStream_t s);
 
+// out[r][u] = bf16(a[r] . b[u]) for r < rows and u < ceil(n / 32) * 32 (b's
+// rows past n repeat its last row), row stride ld elements, with a [rows, k]
+// and b [n, k] bf16 row-major, on the moments kernel's tile loop
+// (srw_mfma.hip).  With mom non-null also the per-split moment partials
+// mom[rows_gemm_splits(rows, n)][rows][2] = (sum, sum of squares) of each
+// row's bf16 values over the units [0, n).  k: 32, 64, 128 or 384.
+bool rows_gemm_supports(int64_t k);
+int rows_gemm_splits(int64_t rows, int64_t n);
+hipError_t rows_gemm(const uint16_t* a, int64_t rows, const uint16_t* b, int64_t n, int64_t k, uint16_t* out,
+                     int64_t ld, float* mom, hipStream_t s);
+
 // Gram statistics (SRW_STATS_GRAM), see srw_gram.hip: writes the per-token
 // moment partials mom[gram_moment_parts(dr)][T][2] = (sum s, sum s^2).
 bool gram_supports(int64_t dr);

@@ -238,6 +238,7 @@ struct StatsParams {
   int64_t mask_words32;
   Geometry g;
   uint16_t* s_out;     // bf16 score buffer (score_tile_off layout) or null: plain moments only
+  int64_t s_ld;        // kStatsRows / kStatsRowsOnly: row stride (elements) of the row-major s_out
 };
 
 // The bf16 scores as the scores-streaming main kernel reads them: per (token
@@ -256,8 +257,12 @@ __host__ __device__ inline int64_t score_tile_off(int ntiles, int64_t ttile, int
 // (mom stride 3), for _srw_inference's centred std (v41:1719-1721) in one
 // pass: each tile's sum and sum of squares about the tile mean join the
 // running (count, mean, M2) by Chan et al.'s pairwise update, and
-// srw_tau_kernel merges the splits the same way.
-constexpr int kStatsPlain = 0, kStatsDiag = 1, kStatsChan = 3;
+// srw_tau_kernel merges the splits the same way.  kStatsRows: the plain
+// moments, with the bf16 scores stored row-major ([T, s_ld], units as
+// columns) instead of in the streaming layout; kStatsRowsOnly: the row-major
+// store alone, no moments (the same tile loop as a plain bf16 GEMM with a
+// bf16 output, K = 16 KH).
+constexpr int kStatsPlain = 0, kStatsDiag = 1, kStatsChan = 3, kStatsRows = 4, kStatsRowsOnly = 5;
 // A lane's running moments of one row's scores over the tiles of an N-split
 // (the moments kernel, and the one-launch decode kernel, which runs the same
 // arithmetic so that both give the same bits).  kStatsPlain / kStatsDiag:
@@ -430,7 +435,8 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
   // a whole tile to complete before the end-of-tile vmcnt wait.  A tile that
   // two splits share (a chunk boundary inside it) is stored by the split
   // holding its first unit.
-  constexpr bool STORE = TBW == 1 && (MODE == kStatsPlain || MODE == kStatsDiag || MODE == kStatsChan);
+  constexpr bool ROWS = MODE == kStatsRows || MODE == kStatsRowsOnly;
+  constexpr bool STORE = TBW == 1 && (MODE == kStatsPlain || MODE == kStatsDiag || MODE == kStatsChan || ROWS);
   uint32_t spd[8];
   char* sdst = nullptr;
   // Non-temporal stores (and loads in the main kernel): 206 MB per Know-pool
@@ -438,9 +444,16 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
   // token tiles share, in L2 and in the last-level cache across kernels
   // (measured: moments kernel 101 -> 87 us, pack 12.8 -> 9.1 us).
   auto store_scores = [&]() {
-    __builtin_nontemporal_store(u32x4_t{spd[0], spd[1], spd[2], spd[3]}, reinterpret_cast<u32x4_t*>(sdst));
-    __builtin_nontemporal_store(u32x4_t{spd[4], spd[5], spd[6], spd[7]},
-                                reinterpret_cast<u32x4_t*>(sdst + kFragBytes));
+    if constexpr (ROWS) {
+      // row-major: units 16 half .. 16 half + 15 of the lane's row (the
+      // words as rows_words left them), two 16-byte stores
+      *reinterpret_cast<u32x4_t*>(sdst) = u32x4_t{spd[0], spd[1], spd[4], spd[5]};
+      *reinterpret_cast<u32x4_t*>(sdst + 16) = u32x4_t{spd[2], spd[3], spd[6], spd[7]};
+    } else {
+      __builtin_nontemporal_store(u32x4_t{spd[0], spd[1], spd[2], spd[3]}, reinterpret_cast<u32x4_t*>(sdst));
+      __builtin_nontemporal_store(u32x4_t{spd[4], spd[5], spd[6], spd[7]},
+                                  reinterpret_cast<u32x4_t*>(sdst + kFragBytes));
+    }
   };
   if (ta < tb) {
     issue(ta, 0);
@@ -500,17 +513,36 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
       // alive in copies
 #pragma unroll
       for (int v = 0; v < 16; v += 2) spd[v >> 1] = pack_bf16(acc[0][v], acc[0][v + 1]);
-      if (p.s_out && u0 >= lo)
-        sdst = reinterpret_cast<char*>(p.s_out) + score_tile_off(p.g.ntiles, ttile, tile, wave) + lane * 16;
+      if constexpr (ROWS) {
+        // word k of lane (row, half) holds units 8 (k / 2) + 4 half + 2 (k %
+        // 2) + {0, 1} of the tile.  Swapping words k and 4 + k between the
+        // two lanes of a row (v_permlane32_swap: the upper half of the first
+        // operand with the lower half of the second) leaves lane half with
+        // units 16 half .. 16 half + 15 as words 0, 1, 4, 5, 2, 3, 6, 7.
+        // Every lane of the wave runs it (the stores below are per lane).
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const auto r = __builtin_amdgcn_permlane32_swap(spd[k], spd[4 + k], false, false);
+          spd[k] = r[0];
+          spd[4 + k] = r[1];
+        }
+        if (u0 >= lo && tt[0] < p.g.T)
+          sdst = reinterpret_cast<char*>(p.s_out) + (tt[0] * p.s_ld + u0 + 16 * half) * 2;
+      } else {
+        if (p.s_out && u0 >= lo)
+          sdst = reinterpret_cast<char*>(p.s_out) + score_tile_off(p.g.ntiles, ttile, tile, wave) + lane * 16;
+      }
     }
     // this tile's moments (v41:441-444): the packed bf16 scores (v41:503),
     // units outside the split excluded
+    if constexpr (MODE != kStatsRowsOnly) {
 #pragma unroll
-    for (int b = 0; b < TBW; ++b) {
-      uint32_t sp[8];
+      for (int b = 0; b < TBW; ++b) {
+        uint32_t sp[8];
 #pragma unroll
-      for (int v = 0; v < 16; v += 2) sp[v >> 1] = pack_bf16(acc[b][v], acc[b][v + 1]);
-      moment_tile<MODE>(ms[b], sp, u0, lo, hi, half);
+        for (int v = 0; v < 16; v += 2) sp[v >> 1] = pack_bf16(acc[b][v], acc[b][v + 1]);
+        moment_tile<MODE>(ms[b], sp, u0, lo, hi, half);
+      }
     }
     wait_vm0();
     __syncthreads();
@@ -518,8 +550,10 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
   if constexpr (STORE) {
     if (sdst) store_scores();
   }
+  if constexpr (MODE != kStatsRowsOnly) {
 #pragma unroll
-  for (int b = 0; b < TBW; ++b) moment_store<MODE>(ms[b], p.mom, split, p.g.T, tt[b], half);
+    for (int b = 0; b < TBW; ++b) moment_store<MODE>(ms[b], p.mom, split, p.g.T, tt[b], half);
+  }
 }
 
 // Three workgroups per CU where the registers allow it without spills (not
@@ -3071,6 +3105,54 @@ hipError_t pack_unit_major(const uint16_t* src, uint16_t* dst, int64_t N, int D,
   int64_t blocks = (rows + 255) / 256;
   if (blocks > 8192) blocks = 8192;
   hipLaunchKernelGGL(pack_w_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, src, dst, N, D, rows);
+  return hipGetLastError();
+}
+
+// Row-major bf16 GEMM on the moments kernel's tile loop: 128-row token tiles,
+// ceil(N / 32) unit tiles split over about two workgroups per CU.
+static Geometry rows_geometry(int64_t rows, int64_t n) {
+  Geometry g{};
+  g.T = rows;
+  g.N = n;
+  g.cs = n;
+  g.nc = 1;
+  g.ntiles = static_cast<int>((n + kUnitTile - 1) / kUnitTile);
+  g.TT_st = static_cast<int>((rows + kTokTile - 1) / kTokTile);
+  int spc = static_cast<int>((2 * kTargetBlocks + g.TT_st - 1) / g.TT_st);
+  spc = spc < 1 ? 1 : (spc > g.ntiles ? g.ntiles : spc);
+  g.spc_st = g.S_st = g.spc = g.S = spc;
+  g.TT = g.TT_st;
+  return g;
+}
+
+bool rows_gemm_supports(int64_t k) { return k == 384 || k == 128 || k == 64 || k == 32; }
+
+int rows_gemm_splits(int64_t rows, int64_t n) { return rows > 0 && n > 0 ? rows_geometry(rows, n).S_st : 1; }
+
+hipError_t rows_gemm(const uint16_t* a, int64_t rows, const uint16_t* b, int64_t n, int64_t k, uint16_t* out,
+                     int64_t ld, float* mom, hipStream_t s) {
+  if (rows <= 0 || n <= 0) return hipSuccess;
+  if (!rows_gemm_supports(k) || ld % 8 != 0 || ld < (n + kUnitTile - 1) / kUnitTile * kUnitTile)
+    return hipErrorInvalidValue;
+  StatsParams sp{};
+  sp.h = a;
+  sp.emb = b;
+  sp.mom = mom;
+  sp.g = rows_geometry(rows, n);
+  sp.s_out = out;
+  sp.s_ld = ld;
+  void (*fn)(StatsParams) = nullptr;
+  switch (k) {
+    case 384: fn = mom ? srw_stats_kernel<24, kStatsRows, 1> : srw_stats_kernel<24, kStatsRowsOnly, 1>; break;
+    case 128: fn = mom ? srw_stats_kernel<8, kStatsRows, 1> : srw_stats_kernel<8, kStatsRowsOnly, 1>; break;
+    case 64: fn = mom ? srw_stats_kernel<4, kStatsRows, 1> : srw_stats_kernel<4, kStatsRowsOnly, 1>; break;
+    default: fn = mom ? srw_stats_kernel<2, kStatsRows, 1> : srw_stats_kernel<2, kStatsRowsOnly, 1>; break;
+  }
+  const size_t smem = static_cast<size_t>(2 * (k / 16)) * kFragBytes;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     static_cast<int>(smem));
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(sp.g.TT_st * sp.g.S_st)), dim3(kThreads), smem, s, sp);
   return hipGetLastError();
 }
 

@@ -1465,7 +1465,6 @@ struct ElemParams {
   float* inten_part;      // [N64 / 64][Tv] sum intensity partials (E1)
   float* psum;            // [Tv64 / 64][N64] column sums of s (E1)
   float* pmax;            // [Tv64 / 64][N64] column maxima of the gate (E1)
-  float* DM;              // [Tv, N64] dm (E2)
   uint16_t* DXR;          // [T, N64] d(xr) per token (E2)
   uint16_t* DXRT;         // [N64, T64] (E2)
   float* dm_part;         // [N64 / 64][Tv] (E2)
@@ -1536,14 +1535,39 @@ __global__ __launch_bounds__(256) void bwd_fwd_elem_kernel(ElemParams p) {
   store_transposed(tile, kTile, p.PT, p.Tv64, et.n0, et.v0, p.N64);
 }
 
-// E2: the gate derivative (v41:506-518) from the stored scores, x.r and dP:
-// d(gate_bf) and d(xr) from the bf16 product, through act * intensity, the
-// cutoff / cap clamps and the den term to dm; d(xr) summed over the routes of
-// a token (the broadcast of x.r, v41:796-797) and stored in both layouts
+// The gate derivative of one element (v41:506-518) from its bf16 score s,
+// x.r and dP: d(gate_bf) and d(xr) from the bf16 product, then through act *
+// intensity, the cutoff / cap clamps and the den term dden to dm, the
+// cotangent of the margin m = s - tau - thr.  Written once, without
+// contraction, so that bwd_gate_elem_kernel's row sums of dm and
+// bwd_ds_elem_kernel's recomputed dm are the same values.
+struct GateGrad {
+  float dm, dx;
+};
+__device__ inline GateGrad gate_grad(float s, float x, float dp, float tau, float dden, const GateParams& gp,
+                                     float exp_scale, float sharp) {
+#pragma clang fp contract(off)
+  const float m = (s - tau) - gp.thr;
+  const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(m * exp_scale));
+  const float am = fmaxf(m - gp.cut, 0.0f);
+  const float it = gp.eps + fminf(am, gp.maxi);
+  const float gb = round_bf16(act * it);
+  const float dgb = round_bf16(dp * x);  // d(gate_bf): bf16 multiply transpose
+  const float dx = round_bf16(dp * gb);  // d(xr)
+  const float dit = dgb * act + dden;
+  const float dam = am < gp.maxi ? dit : 0.f;
+  const float dm = (m - gp.cut > 0.f ? dam : 0.f) + dgb * it * sharp * act * (1.0f - act);
+  return GateGrad{dm, dx};
+}
+
+// E2: the gate derivative from the stored scores, x.r and dP: per-row sums of
+// dm (the tau chain's input) and d(xr), summed over the routes of a token
+// (the broadcast of x.r, v41:796-797) and stored in both layouts.  dm itself
+// is not stored: the ds pass recomputes it from the same bf16 inputs (reading
+// three bf16 arrays costs less than writing and reading an fp32 one).
 __global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
   __shared__ uint16_t tile[kTile][kTile + 8];
   const ElemTile et = elem_tile();
-  const float thr = p.gp.thr, cut = p.gp.cut, eps = p.gp.eps, maxi = p.gp.maxi;
   const int64_t n = et.n0 + 8 * et.q;
   float dxs[2][8];
 #pragma unroll
@@ -1552,7 +1576,7 @@ __global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
     const int64_t v = et.v0 + r;
     const bool row_ok = v < p.Tv;
     const int64_t vl = row_ok ? v : p.Tv - 1;
-    float s[8], x[8], dp[8], dm[8];
+    float s[8], x[8], dp[8];
     load8_bf16(p.S + vl * p.N64 + n, s);
     load8_bf16(p.XR + (vl / p.routes) * p.N64 + n, x);
     load8_bf16(p.DP + vl * p.N64 + n, dp);
@@ -1561,23 +1585,9 @@ __global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const bool ok = row_ok && n + e < p.N;
-      const float m = (s[e] - tau) - thr;
-      const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(m * p.exp_scale));
-      const float am = fmaxf(m - cut, 0.0f);
-      const float it = eps + fminf(am, maxi);
-      const float gb = round_bf16(act * it);
-      const float dgb = round_bf16(dp[e] * x[e]);  // d(gate_bf): bf16 multiply transpose
-      const float dx = round_bf16(dp[e] * gb);     // d(xr)
-      const float dit = dgb * act + dden;
-      const float dam = am < maxi ? dit : 0.f;
-      const float d = (m - cut > 0.f ? dam : 0.f) + dgb * it * p.sharp * act * (1.0f - act);
-      dm[e] = ok ? d : 0.f;
-      dxs[rr][e] = ok ? dx : 0.f;
-      sdm += dm[e];
-    }
-    if (row_ok) {
-      *reinterpret_cast<float4*>(p.DM + v * p.N64 + n) = float4{dm[0], dm[1], dm[2], dm[3]};
-      *reinterpret_cast<float4*>(p.DM + v * p.N64 + n + 4) = float4{dm[4], dm[5], dm[6], dm[7]};
+      const GateGrad gg = gate_grad(s[e], x[e], dp[e], tau, dden, p.gp, p.exp_scale, p.sharp);
+      dxs[rr][e] = ok ? gg.dx : 0.f;
+      sdm += ok ? gg.dm : 0.f;
     }
     sdm = rowsum8(sdm);
     if (et.q == 0 && row_ok) p.dm_part[static_cast<int64_t>(blockIdx.x) * p.Tv + v] = sdm;
@@ -1607,7 +1617,10 @@ __global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
 
 struct DsParams {
   const uint16_t* S;    // [Tv, N64]
-  const float* DM;      // [Tv, N64]
+  const uint16_t* XR;   // [T, N64]
+  const uint16_t* DP;   // [Tv, N64]
+  const float* tau;     // [Tv]
+  const float* dden;    // [Tv]
   const float* alpha;   // [Tv]
   const float* beta;    // [Tv]
   const float* pn;      // [N64]
@@ -1617,11 +1630,15 @@ struct DsParams {
   uint16_t* DST;        // [N64, Tv64]
   float d_pen;
   int64_t Tv, N, N64, Tv64;
+  int routes;
+  GateParams gp;
+  float exp_scale, sharp;
 };
 
 // E3: ds = bf16(dm + alpha_v + beta_v s + (c0 + c1 pn[n] - d_pen [pn < 0] dead[n]) / Tv)
 // (the tau chain, v41:461-464, and the per-unit score_lb / dead-penalty
-// terms, v41:445-447, 543-552), zero past N; both layouts
+// terms, v41:445-447, 543-552), zero past N; both layouts.  dm as in E2
+// (gate_grad on the same bf16 inputs).
 __global__ __launch_bounds__(256) void bwd_ds_elem_kernel(DsParams p) {
   __shared__ uint16_t tile[kTile][kTile + 8];
   const ElemTile et = elem_tile();
@@ -1640,14 +1657,16 @@ __global__ __launch_bounds__(256) void bwd_ds_elem_kernel(DsParams p) {
     const int64_t v = et.v0 + r;
     const bool row_ok = v < p.Tv;
     const int64_t vl = row_ok ? v : p.Tv - 1;
-    float s[8], o[8];
+    float s[8], x[8], dp[8], o[8];
     load8_bf16(p.S + vl * p.N64 + n, s);
-    const float4 d0 = *reinterpret_cast<const float4*>(p.DM + vl * p.N64 + n);
-    const float4 d1 = *reinterpret_cast<const float4*>(p.DM + vl * p.N64 + n + 4);
-    const float dm[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-    const float a = p.alpha[vl], b = p.beta[vl];
+    load8_bf16(p.XR + (vl / p.routes) * p.N64 + n, x);
+    load8_bf16(p.DP + vl * p.N64 + n, dp);
+    const float a = p.alpha[vl], b = p.beta[vl], tau = p.tau[vl], dden = p.dden[vl];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = row_ok && n + e < p.N ? dm[e] + a + b * s[e] + unit[e] : 0.f;
+    for (int e = 0; e < 8; ++e) {
+      const float dm = gate_grad(s[e], x[e], dp[e], tau, dden, p.gp, p.exp_scale, p.sharp).dm;
+      o[e] = row_ok && n + e < p.N ? dm + a + b * s[e] + unit[e] : 0.f;
+    }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const uint32_t w = pack_bf16(o[2 * k], o[2 * k + 1]);
@@ -1855,10 +1874,11 @@ hipError_t bwd_gemm(const BGemm& g, const uint16_t* A, const uint16_t* B, int64_
 }
 
 struct BLayout {
-  size_t S, XR, DP, DM, DXR, DS, PT, DXRT, DST, ET, RT, HT, XT, DRAWT, DRAW;
+  size_t S, XR, DP, DXR, DS, PT, DXRT, DST, ET, RT, HT, XT, DRAWT, DRAW;
   size_t mom, inten_part, dm_part, tokv, psum, pmax, pn, dead, blk, coef, part, total;
   int64_t Tv, T64, Tv64, N64;
   int CT, RTv, RTt, NB, TS, nblk;
+  int S_st;  // moment partials per row
   BGemm g_dw, g_dh, g_dx, g_de, g_dr;
 };
 
@@ -1890,7 +1910,6 @@ BLayout blayout(const srw_desc_t& d) {
   l.S = take(vn);
   l.XR = take(tn);
   l.DP = take(vn);
-  l.DM = take(2 * vn);
   l.DXR = take(tn);
   l.DS = take(vn);
   l.PT = take(static_cast<size_t>(l.N64) * l.Tv64 * 2);
@@ -1902,7 +1921,8 @@ BLayout blayout(const srw_desc_t& d) {
   l.XT = take(static_cast<size_t>(D) * l.T64 * 2);
   l.DRAWT = take(static_cast<size_t>(D) * l.Tv64 * 2);
   l.DRAW = take(static_cast<size_t>(l.Tv) * D * 2);
-  l.mom = take(static_cast<size_t>(2 * l.CT) * l.Tv * 2 * 4);
+  l.S_st = rows_gemm_supports(dr) ? rows_gemm_splits(l.Tv, N) : 2 * l.CT;
+  l.mom = take(static_cast<size_t>(l.S_st) * l.Tv * 2 * 4);
   l.inten_part = take(static_cast<size_t>(l.NB) * l.Tv * 4);
   l.dm_part = take(static_cast<size_t>(l.NB) * l.Tv * 4);
   l.tokv = take(static_cast<size_t>(l.Tv) * 9 * 4);
@@ -1964,7 +1984,7 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   uint16_t *S = b16(l.S), *XR = b16(l.XR), *DP = b16(l.DP), *DXR = b16(l.DXR), *DS = b16(l.DS);
   uint16_t *PT = b16(l.PT), *DXRT = b16(l.DXRT), *DST = b16(l.DST), *ET = b16(l.ET), *RT = b16(l.RT);
   uint16_t *HT = b16(l.HT), *XT = b16(l.XT), *DRAWT = b16(l.DRAWT), *DRAW = b16(l.DRAW);
-  float *DM = f32(l.DM), *mom = f32(l.mom), *inten_part = f32(l.inten_part), *dm_part = f32(l.dm_part);
+  float *mom = f32(l.mom), *inten_part = f32(l.inten_part), *dm_part = f32(l.dm_part);
   float *tokv = f32(l.tokv), *psum = f32(l.psum), *pmax = f32(l.pmax), *pn = f32(l.pn), *dead = f32(l.dead);
   float *blk = f32(l.blk), *coef = f32(l.coef), *part = f32(l.part);
   float *mean = tokv, *var = tokv + Tv, *sdev = tokv + 2 * Tv, *tau = tokv + 3 * Tv, *dden = tokv + 4 * Tv;
@@ -1989,25 +2009,37 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   SRW_TRY(transpose(h, HT, Tv, l.Tv64, dr, st));
   SRW_TRY(transpose(x, XT, T, l.T64, D, st));
 
-  // forward recompute: scores (stored), moments, tau, x.r (stored)
-  TStatsParams sp{};
-  sp.h = h;
-  sp.emb = emb;
-  sp.S = S;
-  sp.mom = mom;
-  sp.Tv = Tv;
-  sp.N = N;
-  sp.N64 = N64;
-  sp.dr = dr;
-  sp.RT = l.RTv;
-  sp.CT = l.CT;
-  hipLaunchKernelGGL(tiled_stats_kernel, dim3(static_cast<unsigned>(8 * l.RTv * ((l.CT + 7) / 8))),
-                     dim3(kGThreads), kGemmLds, st, sp);
-  SRW_TRY(hipGetLastError());
+  // forward recompute: scores (stored), moments, tau, x.r (stored).  The
+  // three [rows, N64] products with K = d_route or d_model (scores, x.r and
+  // dP below) run on the moments kernel's tile loop where it takes that K
+  // (rows_gemm: 128-row tiles, about two workgroups per CU), else on the
+  // 256 x 256 tiles here.
+  if (rows_gemm_supports(dr)) {
+    SRW_TRY(rows_gemm(h, Tv, emb, N, dr, S, N64, mom, st));
+  } else {
+    TStatsParams sp{};
+    sp.h = h;
+    sp.emb = emb;
+    sp.S = S;
+    sp.mom = mom;
+    sp.Tv = Tv;
+    sp.N = N;
+    sp.N64 = N64;
+    sp.dr = dr;
+    sp.RT = l.RTv;
+    sp.CT = l.CT;
+    hipLaunchKernelGGL(tiled_stats_kernel, dim3(static_cast<unsigned>(8 * l.RTv * ((l.CT + 7) / 8))),
+                       dim3(kGThreads), kGemmLds, st, sp);
+    SRW_TRY(hipGetLastError());
+  }
   hipLaunchKernelGGL(bwd_token_stats_kernel, dim3(static_cast<unsigned>((Tv + 3) / 4)), dim3(256), 0, st, mom,
-                     2 * l.CT, Tv, N, a.in.tau_offset, mean, var, sdev, tau);
+                     l.S_st, Tv, N, a.in.tau_offset, mean, var, sdev, tau);
   SRW_TRY(hipGetLastError());
-  SRW_TRY(store_gemm(read, x, XR, T, T, 1, N, N64, D, st));
+  if (rows_gemm_supports(D)) {
+    SRW_TRY(rows_gemm(x, T, read, N, D, XR, N64, nullptr, st));
+  } else {
+    SRW_TRY(store_gemm(read, x, XR, T, T, 1, N, N64, D, st));
+  }
 
   // E1: gates, P^T, sum intensity, per-unit statistics
   ElemParams ep{};
@@ -2020,7 +2052,6 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   ep.inten_part = inten_part;
   ep.psum = psum;
   ep.pmax = pmax;
-  ep.DM = DM;
   ep.DXR = DXR;
   ep.DXRT = DXRT;
   ep.dm_part = dm_part;
@@ -2055,7 +2086,11 @@ hipError_t tiled_backward(const BackwardArgs& a) {
     SRW_TRY(hipGetLastError());
   }
   dominant_kernel_begin(st);
-  SRW_TRY(store_gemm(write, DRAW, DP, Tv, Tv, 1, N, N64, D, st));
+  if (rows_gemm_supports(D)) {
+    SRW_TRY(rows_gemm(DRAW, Tv, write, N, D, DP, N64, nullptr, st));
+  } else {
+    SRW_TRY(store_gemm(write, DRAW, DP, Tv, Tv, 1, N, N64, D, st));
+  }
   dominant_kernel_end(st);
   hipLaunchKernelGGL(bwd_gate_elem_kernel, grid_e, dim3(256), 0, st, ep);
   SRW_TRY(hipGetLastError());
@@ -2065,7 +2100,10 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   // E3: ds in both layouts
   DsParams dp{};
   dp.S = S;
-  dp.DM = DM;
+  dp.XR = XR;
+  dp.DP = DP;
+  dp.tau = tau;
+  dp.dden = dden;
   dp.alpha = alpha;
   dp.beta = beta;
   dp.pn = pn;
@@ -2078,6 +2116,10 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   dp.N = N;
   dp.N64 = N64;
   dp.Tv64 = l.Tv64;
+  dp.routes = R;
+  dp.gp = a.gp;
+  dp.exp_scale = exp_scale;
+  dp.sharp = d.sharpness;
   hipLaunchKernelGGL(bwd_ds_elem_kernel, grid_e, dim3(256), 0, st, dp);
   SRW_TRY(hipGetLastError());
 
