@@ -91,9 +91,20 @@ __device__ inline Opnd make_opnd(const uint16_t* p, int64_t ld, int64_t row0, in
 // they are needed), and k-step 3's MFMAs also cover the first fragment reads
 // of block kb + 1.  (Global->LDS loads interleaved with fragment reads make
 // the compiler wait for every LDS read, so they stay in k-step 3.)
-template <class Hook>
-__device__ inline void gemm_loop(f32x16_t (&acc)[4][4], const Opnd& A, const Opnd& B, int64_t k0, int nk, char* lds,
-                                 int wave, int lane, Hook&& hook) {
+// s_waitcnt immediate for vmcnt(n) (expcnt and lgkmcnt not waited on)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// NBF: B fragments per wave and k-step -- the B tile holds 64 NBF rows (256 or
+// 192), each wave 32 NBF of them, so the output tile is 256 x 64 NBF (192 when
+// the B side is 384 wide: no padded columns).
+template <int NBF, class Hook>
+__device__ inline void gemm_loop(f32x16_t (&acc)[4][NBF], const Opnd& A, const Opnd& B, int64_t k0, int nk,
+                                 char* lds, int wave, int lane, Hook&& hook) {
+  constexpr int NB = 64 * NBF;                 // B-tile rows
+  constexpr int NL = 8 + NB / 32;              // 16-byte loads per wave and k block
+  constexpr int NQ = 4 * NBF;                  // MFMAs per wave and k-step
+  constexpr int NF = 4 + NBF;                  // operand fragments per k-step
+  constexpr int STAGE = kOpBytes + NB * kGK * 2;
   const int wa = wave >> 1, wb = wave & 1;
   const int u = lane & 31, h = lane >> 5;
   int le[4];
@@ -107,24 +118,26 @@ __device__ inline void gemm_loop(f32x16_t (&acc)[4][4], const Opnd& A, const Opn
     else
       g2lds16(B.base + kbyte + B.off[q - 8], stage + kOpBytes + (q - 8) * kGroupBytes + wave * 1024);
   };
-  // fragment g of k-step m: g < 4 the A rows 128 wa + 32 g .., else the B rows 128 wb + 32 (g - 4) ..
+  // fragment g of k-step m: g < 4 the A rows 128 wa + 32 g .., else the B rows 32 NBF wb + 32 (g - 4) ..
   auto frag = [&](const char* stage, int g, int m) {
-    const int off = g < 4 ? (4 * wa + g) * kGroupBytes : kOpBytes + (4 * wb + g - 4) * kGroupBytes;
+    const int off = g < 4 ? (4 * wa + g) * kGroupBytes : kOpBytes + (NBF * wb + g - 4) * kGroupBytes;
     return *reinterpret_cast<const u32x4_t*>(stage + off + le[m]);
   };
+  // the order the next k-step uses its fragments: a0, b0 .. b(NBF-1), a1, a2, a3
+  auto order = [](int r) { return r == 0 ? 0 : (r <= NBF ? 3 + r : r - NBF); };
 #pragma unroll
-  for (int q = 0; q < 16; ++q) issue(q, 0, lds);
+  for (int q = 0; q < NL; ++q) issue(q, 0, lds);
 #pragma unroll
-  for (int q = 0; q < 16; ++q) issue(q, 1, lds + kStageBytes);
-  __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16): block 0 has landed, block 1 is in flight
+  for (int q = 0; q < NL; ++q) issue(q, 1, lds + STAGE);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(NL));  // block 0 has landed, block 1 is in flight
   barrier_lds();
   hook(0, lds);
-  u32x4_t f[2][8];
+  u32x4_t f[2][NF];
 #pragma unroll
-  for (int g = 0; g < 8; ++g) f[0][g] = frag(lds, g, 0);
+  for (int g = 0; g < NF; ++g) f[0][g] = frag(lds, g, 0);
   for (int kb = 0; kb < nk; ++kb) {
-    char* st = lds + (kb & 1) * kStageBytes;
-    char* nxt = lds + ((kb & 1) ^ 1) * kStageBytes;
+    char* st = lds + (kb & 1) * STAGE;
+    char* nxt = lds + ((kb & 1) ^ 1) * STAGE;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int cb = m & 1;
@@ -135,14 +148,20 @@ __device__ inline void gemm_loop(f32x16_t (&acc)[4][4], const Opnd& A, const Opn
         if (kb + 1 < nk) hook(kb + 1, nxt);
       }
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        acc[q >> 2][q & 3] = mfma(f[cb][q >> 2], f[cb][4 + (q & 3)], acc[q >> 2][q & 3]);
-        if ((q & 1) == 0) {  // read order a0 b0 b1 b2 b3 a1 a2 a3: the order the next k-step uses them
-          constexpr int kOrder[8] = {0, 4, 5, 6, 7, 1, 2, 3};
-          const int g = kOrder[q >> 1];
-          f[cb ^ 1][g] = m < 3 ? frag(st, g, m + 1) : frag(nxt, g, 0);
+      for (int q = 0; q < NQ; ++q) {
+        acc[q / NBF][q % NBF] = mfma(f[cb][q / NBF], f[cb][4 + q % NBF], acc[q / NBF][q % NBF]);
+        // fragment r of the next k-step is read at MFMA r NQ / NF (one per two MFMAs at NBF = 4)
+#pragma unroll
+        for (int r = 0; r < NF; ++r) {
+          if (r * NQ / NF == q) {
+            const int g = order(r);
+            f[cb ^ 1][g] = m < 3 ? frag(st, g, m + 1) : frag(nxt, g, 0);
+          }
         }
-        if (m == 3) issue(q, kb + 2, st);
+        if (m == 3) {
+#pragma unroll
+          for (int L = q * NL / NQ; L < (q + 1) * NL / NQ; ++L) issue(L, kb + 2, st);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -150,6 +169,9 @@ __device__ inline void gemm_loop(f32x16_t (&acc)[4][4], const Opnd& A, const Opn
   wait_vm0();
   __syncthreads();  // the trailing reloads have landed before LDS is reused
 }
+
+// LDS of a gemm_loop<NBF> workgroup: two stages of the A and B tiles
+constexpr int gemm_lds(int nbf) { return 2 * (kOpBytes + 64 * nbf * kGK * 2); }
 
 struct NoHook {
   __device__ void operator()(int, char*) const {}
@@ -851,6 +873,7 @@ struct TWriteParams {
   float* out_part;     // [S][Tv][D]
   int64_t Tv, N, N64, D, cs;
   int nc, spc, S, RT, DT;
+  int round_out;       // store bf16-rounded values (one split: out_part is the result)
 };
 
 // zero the units outside [lo, hi) of the P tile of one k block (first unit kbase)
@@ -868,6 +891,7 @@ __device__ inline void mask_units(char* tile, int64_t kbase, int64_t lo, int64_t
   }
 }
 
+template <int NBF>
 __global__ __launch_bounds__(kGThreads) void tiled_write_kernel(TWriteParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
@@ -885,14 +909,14 @@ __global__ __launch_bounds__(kGThreads) void tiled_write_kernel(TWriteParams p) 
   const int64_t lo = c * p.cs, hi = (c + 1) * p.cs < p.N ? (c + 1) * p.cs : p.N;
   const int64_t b_lo = lo / kGK, b_hi = (hi + kGK - 1) / kGK, nb = b_hi - b_lo;
   const int64_t kb0 = b_lo + nb * sub / p.spc, kb1 = b_lo + nb * (sub + 1) / p.spc;
-  const int64_t v0 = static_cast<int64_t>(rt) * kGRows, d0 = static_cast<int64_t>(dt) * kGRows;
+  const int64_t v0 = static_cast<int64_t>(rt) * kGRows, d0 = static_cast<int64_t>(dt) * (64 * NBF);
   const Opnd A = make_opnd(p.P, p.N64, v0, p.Tv, 1, wave, lane);
   const Opnd B = make_opnd(p.wt, p.N64, d0, p.D, 1, wave, lane);
-  f32x16_t acc[4][4];
+  f32x16_t acc[4][NBF];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+    for (int j = 0; j < NBF; ++j) acc[i][j] = f32x16_t{};
   auto hook = [&](int kb, char* stage) {
     const int64_t kbase = (kb0 + kb) * kGK;
     if (kbase < lo || kbase + kGK > hi) {  // a block shared with the neighbouring chunk
@@ -910,9 +934,9 @@ __global__ __launch_bounds__(kGThreads) void tiled_write_kernel(TWriteParams p) 
       const int64_t t = v0 + 128 * wa + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
       if (t >= p.Tv) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t d = d0 + 128 * wb + 32 * j + u;
-        if (d < p.D) dst[t * p.D + d] = acc[i][j][v];
+      for (int j = 0; j < NBF; ++j) {
+        const int64_t d = d0 + 32 * NBF * wb + 32 * j + u;
+        if (d < p.D) dst[t * p.D + d] = p.round_out ? round_bf16(acc[i][j][v]) : acc[i][j][v];
       }
     }
   }
@@ -1050,8 +1074,8 @@ TLayout tlayout(const srw_desc_t& d, const TGeo& g) {
   return l;
 }
 
-hipError_t set_lds(const void* fn) {
-  return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+hipError_t set_lds(const void* fn, int bytes = kGemmLds) {
+  return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 }
 
 }  // namespace
@@ -1179,7 +1203,7 @@ hipError_t tiled_forward(const LaunchArgs& a) {
   static_assert(kGemmLds <= 160 * 1024, "LDS per workgroup");
   for (const void* fn : {reinterpret_cast<const void*>(tiled_stats_kernel),
                          reinterpret_cast<const void*>(tiled_gate_kernel<false>),
-                         reinterpret_cast<const void*>(tiled_write_kernel)})
+                         reinterpret_cast<const void*>(tiled_write_kernel<4>)})
     if ((e = set_lds(fn)) != hipSuccess) return e;
 
   if (!(d.flags & SRW_FLAG_POOL_CACHED) && !tiled_sparse(d)) {  // (the sparse path gathers W's rows)
@@ -1250,7 +1274,7 @@ hipError_t tiled_forward(const LaunchArgs& a) {
   wp.RT = g.RT;
   wp.DT = g.DT;
   const unsigned grid_w = static_cast<unsigned>(8 * g.DT * ((static_cast<int64_t>(g.RT) * g.S + 7) / 8));
-  hipLaunchKernelGGL(tiled_write_kernel, dim3(grid_w), dim3(kGThreads), kGemmLds, a.stream, wp);
+  hipLaunchKernelGGL(tiled_write_kernel<4>, dim3(grid_w), dim3(kGThreads), kGemmLds, a.stream, wp);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 
   hipLaunchKernelGGL(tiled_tok_sum_kernel, dim3(static_cast<unsigned>((g.Tv + 63) / 64)), dim3(256), 0, a.stream,
@@ -1792,15 +1816,33 @@ __global__ __launch_bounds__(256) void bwd_sum_kernel(const float* __restrict__ 
 struct BGemm {
   int64_t M, Nc, K;  // out [M, Nc] = A [M, K] . B [Nc, K]^T
   int RT, DT, spc;
+  int nbf;           // tile width 64 nbf (tiled_write_kernel<nbf>)
 };
 
 BGemm bgemm(int64_t M, int64_t Nc, int64_t K) {
-  BGemm g{M, Nc, K, static_cast<int>((M + kGRows - 1) / kGRows), static_cast<int>((Nc + kGRows - 1) / kGRows), 1};
-  const int64_t blocks = (K + kGK - 1) / kGK;
-  // one wave of workgroups over the 256 CUs (fewer splits: less fp32 partial traffic;
-  // measured 131 us per Know-pool gradient GEMM against 144 with two waves)
-  int64_t spc = (256 + static_cast<int64_t>(g.RT) * g.DT - 1) / (static_cast<int64_t>(g.RT) * g.DT);
-  spc = spc < 1 ? 1 : (spc > blocks ? blocks : spc);
+  // output tiles 256 x 192 where that pads the Nc side less than 256 x 256
+  // (Nc = 384: two tiles either way, a quarter of the wider ones' MFMAs idle)
+  const int64_t p256 = (Nc + 255) / 256 * 256, p192 = (Nc + 191) / 192 * 192;
+  const int nbf = p192 < p256 ? 3 : 4;
+  BGemm g{M, Nc, K, static_cast<int>((M + kGRows - 1) / kGRows), static_cast<int>((Nc + 64 * nbf - 1) / (64 * nbf)),
+          1, nbf};
+  const int64_t blocks = (K + kGK - 1) / kGK, tiles = static_cast<int64_t>(g.RT) * g.DT;
+  // K splits: the fewest that minimise the busiest CU's k blocks (rounds of
+  // 256 workgroups x blocks per split) plus the fp32 partials' write and read
+  // back, priced at ~1.6 us per k block and ~5 TB/s.  One split writes the
+  // bf16-rounded result directly.  (Know-pool gradient GEMMs with K = T: 198
+  // tiles, where two splits take as many block rounds as one.)
+  double best = 0.0;
+  int64_t spc = 1;
+  for (int64_t c = 1; c <= 64 && c <= blocks; ++c) {
+    const int64_t rounds = (tiles * c + 255) / 256, per = (blocks + c - 1) / c;
+    const double cost = 1.6 * static_cast<double>(rounds * per) +
+                        (c > 1 ? 2.0 * c * M * Nc * 4 / 5.0e6 : 0.0);  // us
+    if (c == 1 || cost < best) {
+      best = cost;
+      spc = c;
+    }
+  }
   g.spc = static_cast<int>(spc);
   return g;
 }
@@ -1863,10 +1905,15 @@ hipError_t bwd_gemm(const BGemm& g, const uint16_t* A, const uint16_t* B, int64_
   wp.S = g.spc;
   wp.RT = g.RT;
   wp.DT = g.DT;
+  wp.round_out = g.spc == 1;
+  if (g.spc == 1) wp.out_part = out;  // the bf16-rounded result directly
   const unsigned grid = static_cast<unsigned>(8 * g.DT * ((static_cast<int64_t>(g.RT) * g.spc + 7) / 8));
-  hipLaunchKernelGGL(tiled_write_kernel, dim3(grid), dim3(kGThreads), kGemmLds, s, wp);
+  if (g.nbf == 3)
+    hipLaunchKernelGGL(tiled_write_kernel<3>, dim3(grid), dim3(kGThreads), gemm_lds(3), s, wp);
+  else
+    hipLaunchKernelGGL(tiled_write_kernel<4>, dim3(grid), dim3(kGThreads), kGemmLds, s, wp);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || g.spc == 1) return e;
   const int64_t n = g.M * g.Nc;
   hipLaunchKernelGGL(bwd_sum_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, part, g.spc, n,
                      out);
@@ -1999,8 +2046,9 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   hipError_t e;
   for (const void* fn : {reinterpret_cast<const void*>(tiled_stats_kernel),
                          reinterpret_cast<const void*>(tiled_store_kernel),
-                         reinterpret_cast<const void*>(tiled_write_kernel)})
+                         reinterpret_cast<const void*>(tiled_write_kernel<4>)})
     if ((e = set_lds(fn)) != hipSuccess) return e;
+  if ((e = set_lds(reinterpret_cast<const void*>(tiled_write_kernel<3>), gemm_lds(3))) != hipSuccess) return e;
 #define SRW_TRY(expr) \
   if ((e = (expr)) != hipSuccess) return e
   // operands of the K = units / K = rows contractions, unit- or row-contiguous
