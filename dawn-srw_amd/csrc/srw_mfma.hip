@@ -275,10 +275,11 @@ struct MomState {
 
 // Join one 32-unit tile (sp: the lane's 16 packed bf16 scores, v41:503, in
 // accumulator order) to the state; units outside [lo, hi) enter as zeros.
-template <int MODE>
+// FULL: the caller has checked that every unit of the tile is in [lo, hi).
+template <int MODE, bool FULL = false>
 __device__ __attribute__((always_inline)) inline void moment_tile(MomState& m, const uint32_t (&sp)[8], int64_t u0,
                                                                    int64_t lo, int64_t hi, int half) {
-  const bool full = u0 >= lo && u0 + kUnitTile <= hi;
+  const bool full = FULL || (u0 >= lo && u0 + kUnitTile <= hi);
   if constexpr (MODE == kStatsChan) {
     // this tile's units in the split, their sum and sum of squares about
     // their mean (both lane halves), joined to the running (count, mean, M2)
@@ -536,12 +537,19 @@ __device__ __attribute__((always_inline)) inline void stats_body(const StatsPara
     // this tile's moments (v41:441-444): the packed bf16 scores (v41:503),
     // units outside the split excluded
     if constexpr (MODE != kStatsRowsOnly) {
+      // a uniform branch between the whole tiles (all but a split's edge
+      // tiles) and the masked ones: as selects, the masking's 64-bit unit
+      // compares ran on every tile (~4.6 VALU instructions per MFMA)
+      const bool full = u0 >= lo && u0 + kUnitTile <= hi;
 #pragma unroll
       for (int b = 0; b < TBW; ++b) {
         uint32_t sp[8];
 #pragma unroll
         for (int v = 0; v < 16; v += 2) sp[v >> 1] = pack_bf16(acc[b][v], acc[b][v + 1]);
-        moment_tile<MODE>(ms[b], sp, u0, lo, hi, half);
+        if (full)
+          moment_tile<MODE, true>(ms[b], sp, u0, lo, hi, half);
+        else
+          moment_tile<MODE, false>(ms[b], sp, u0, lo, hi, half);
       }
     }
     wait_vm0();
