@@ -340,8 +340,10 @@ __device__ inline GateElem gate_elem(float s, float c_exp, float k_exp, float ta
 }
 
 // KEEP (the backward's recompute): P and x.r go to P_out / XR_out and the
-// stored scores stay.
-template <bool KEEP>
+// stored scores stay.  GOUT: every unit's fp32 gate also goes to G (a
+// variant of its own: the per-element stores and their addresses would
+// otherwise sit in every call's epilogue code).
+template <bool KEEP, bool GOUT = false>
 __global__ __launch_bounds__(kGThreads) void tiled_gate_kernel(TGateParams p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
@@ -408,9 +410,9 @@ __global__ __launch_bounds__(kGThreads) void tiled_gate_kernel(TGateParams p) {
             is += inten;
             bits = __builtin_amdgcn_alignbit(bits, sign, 31);  // bits << 1 | sign bit
             g2[e] = g;
-            if constexpr (!KEEP) {
+            if constexpr (GOUT) {
               const int64_t un = nb + 8 * ((v + e) >> 2) + ((v + e) & 3);
-              if (p.G && tok && un < p.N) p.G[t * p.N + un] = g;
+              if (tok && un < p.N) p.G[t * p.N + un] = g;
             }
           }
           const uint32_t gq = pack_bf16(g2[0], g2[1]);                              // gate_bf (v41:516)
@@ -1203,6 +1205,7 @@ hipError_t tiled_forward(const LaunchArgs& a) {
   static_assert(kGemmLds <= 160 * 1024, "LDS per workgroup");
   for (const void* fn : {reinterpret_cast<const void*>(tiled_stats_kernel),
                          reinterpret_cast<const void*>(tiled_gate_kernel<false>),
+                         reinterpret_cast<const void*>(tiled_gate_kernel<false, true>),
                          reinterpret_cast<const void*>(tiled_write_kernel<4>)})
     if ((e = set_lds(fn)) != hipSuccess) return e;
 
@@ -1255,7 +1258,10 @@ hipError_t tiled_forward(const LaunchArgs& a) {
   gp.gp = a.gp;
   gp.exp_scale = -d.sharpness * 1.4426950408889634f;
   dominant_kernel_begin(a.stream);
-  hipLaunchKernelGGL(tiled_gate_kernel<false>, dim3(grid_rc), dim3(kGThreads), kGemmLds, a.stream, gp);
+  if (gp.G)
+    hipLaunchKernelGGL((tiled_gate_kernel<false, true>), dim3(grid_rc), dim3(kGThreads), kGemmLds, a.stream, gp);
+  else
+    hipLaunchKernelGGL(tiled_gate_kernel<false>, dim3(grid_rc), dim3(kGThreads), kGemmLds, a.stream, gp);
   dominant_kernel_end(a.stream);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 
