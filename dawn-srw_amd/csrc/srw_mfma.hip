@@ -2773,6 +2773,9 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
         if (i < ntl) pf[i][j][b] = *reinterpret_cast<const u32x4_t*>(xl + ((i * TB + b) * 2 + j) * kFragBytes + lane * 16);
       }
   float* op = p.out_part + static_cast<int64_t>(split) * Tv * D;
+  // the lane's element (b, v) of column block c at lrow + (32 b + 8 (v / 4) +
+  // v % 4) D + 32 c: compile-time offsets from one per-lane base
+  float* lrow = op + (row0 + 4 * half) * D + 32 * wave * NDB + col;
 #pragma unroll
   for (int c = 0; c < NDB; ++c) {
     f32x16_t oacc[TB];
@@ -2793,14 +2796,14 @@ __device__ __attribute__((always_inline)) inline void decode_body(const MainPara
       for (int b = 0; b < TB; ++b)
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-          __builtin_nontemporal_store(oacc[b][v], &op[(row0 + 32 * b + unit_of_acc(v, half)) * D + 32 * (wave * NDB + c) + col]);
+          __builtin_nontemporal_store(oacc[b][v], lrow + (32 * b + 8 * (v >> 2) + (v & 3)) * D + 32 * c);
     } else {
 #pragma unroll
       for (int b = 0; b < TB; ++b)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int64_t t = row0 + 32 * b + unit_of_acc(v, half);
-          if (t < Tv) __builtin_nontemporal_store(oacc[b][v], &op[t * D + 32 * (wave * NDB + c) + col]);
+          if (t < Tv) __builtin_nontemporal_store(oacc[b][v], lrow + (32 * b + 8 * (v >> 2) + (v & 3)) * D + 32 * c);
         }
     }
   }
