@@ -893,15 +893,18 @@ __device__ inline void mask_units(char* tile, int64_t kbase, int64_t lo, int64_t
   }
 }
 
-template <int NBF>
-__global__ __launch_bounds__(kGThreads) void tiled_write_kernel(TWriteParams p) {
+// MAYROUND: p.round_out is honoured (the backward's products); without it
+// the kernel has no rounding code (the forward's write GEMM: its register
+// allocation spilled with the rounded form compiled in beside the plain one).
+template <int NBF, bool MAYROUND>
+__device__ __attribute__((always_inline)) inline void write_body(const TWriteParams& p, const int bid) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wa = wave >> 1, wb = wave & 1, u = lane & 31, h = lane >> 5;
   // workgroups of one (token tile, split) on one XCD, consecutive: their D
   // tiles share the P tile
-  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int x = bid & 7, k = bid >> 3;
   const int dt = k % p.DT;
   const int w = (k / p.DT) * 8 + x;
   if (w >= p.RT * p.S) return;
@@ -929,19 +932,47 @@ __global__ __launch_bounds__(kGThreads) void tiled_write_kernel(TWriteParams p) 
   gemm_loop(acc, A, B, kb0 * kGK, static_cast<int>(kb1 - kb0), lds, wave, lane, hook);
 
   float* dst = p.out_part + static_cast<int64_t>(split) * p.Tv * p.D;
+  // (a uniform branch: a select per element kept both forms of every value live)
+  auto store = [&](auto round_tag) {
+    constexpr bool RND = decltype(round_tag)::value;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int64_t t = v0 + 128 * wa + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
-      if (t >= p.Tv) continue;
+      for (int v = 0; v < 16; ++v) {
+        const int64_t t = v0 + 128 * wa + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (t >= p.Tv) continue;
 #pragma unroll
-      for (int j = 0; j < NBF; ++j) {
-        const int64_t d = d0 + 32 * NBF * wb + 32 * j + u;
-        if (d < p.D) dst[t * p.D + d] = p.round_out ? round_bf16(acc[i][j][v]) : acc[i][j][v];
+        for (int j = 0; j < NBF; ++j) {
+          const int64_t d = d0 + 32 * NBF * wb + 32 * j + u;
+          if (d < p.D) dst[t * p.D + d] = RND ? round_bf16(acc[i][j][v]) : acc[i][j][v];
+        }
       }
     }
-  }
+  };
+  if (MAYROUND && p.round_out)
+    store(std::true_type{});
+  else
+    store(std::false_type{});
+}
+template <int NBF, bool MAYROUND = false>
+__global__ __launch_bounds__(kGThreads) void tiled_write_kernel(TWriteParams p) {
+  write_body<NBF, MAYROUND>(p, blockIdx.x);
+}
+// Several independent products in one launch (the backward's five gradient
+// contractions): group i owns workgroups [start[i], start[i + 1]), each
+// range a multiple of 8 so that the workgroup -> XCD mapping is the
+// single-product one.
+constexpr int kWriteBatch = 5;
+struct TWriteBatch {
+  TWriteParams p[kWriteBatch];
+  int start[kWriteBatch + 1];
+  int n;
+};
+template <int NBF>
+__global__ __launch_bounds__(kGThreads) void tiled_write_batch_kernel(TWriteBatch b) {
+  int i = 0;
+  for (int k = 1; k < b.n; ++k) i += static_cast<int>(blockIdx.x) >= b.start[k] ? 1 : 0;
+  write_body<NBF, true>(b.p[i], static_cast<int>(blockIdx.x) - b.start[i]);
 }
 
 // per-token sums of the gate kernel's partials, in a fixed order:
@@ -1894,13 +1925,13 @@ hipError_t transpose(const uint16_t* src, uint16_t* dst, int64_t rows, int64_t r
 }
 
 // out [M, Nc] (fp32, bf16-rounded) = A [M, K] . B [Nc, K]^T, both with row
-// stride ld (elements), zero past K
-hipError_t bwd_gemm(const BGemm& g, const uint16_t* A, const uint16_t* B, int64_t ld, float* part, float* out,
-                    hipStream_t s) {
+// stride ld (elements), zero past K: the write kernel's parameters (one
+// split: the rounded result straight into out; else fp32 partials in part)
+TWriteParams bwd_params(const BGemm& g, const uint16_t* A, const uint16_t* B, int64_t ld, float* part, float* out) {
   TWriteParams wp{};
   wp.P = A;
   wp.wt = B;
-  wp.out_part = part;
+  wp.out_part = g.spc == 1 ? out : part;
   wp.Tv = g.M;
   wp.N = g.K;
   wp.N64 = ld;
@@ -1912,18 +1943,59 @@ hipError_t bwd_gemm(const BGemm& g, const uint16_t* A, const uint16_t* B, int64_
   wp.RT = g.RT;
   wp.DT = g.DT;
   wp.round_out = g.spc == 1;
-  if (g.spc == 1) wp.out_part = out;  // the bf16-rounded result directly
-  const unsigned grid = static_cast<unsigned>(8 * g.DT * ((static_cast<int64_t>(g.RT) * g.spc + 7) / 8));
-  if (g.nbf == 3)
-    hipLaunchKernelGGL(tiled_write_kernel<3>, dim3(grid), dim3(kGThreads), gemm_lds(3), s, wp);
-  else
-    hipLaunchKernelGGL(tiled_write_kernel<4>, dim3(grid), dim3(kGThreads), kGemmLds, s, wp);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || g.spc == 1) return e;
+  return wp;
+}
+unsigned bwd_grid(const BGemm& g) {
+  return static_cast<unsigned>(8 * g.DT * ((static_cast<int64_t>(g.RT) * g.spc + 7) / 8));
+}
+hipError_t bwd_sum(const BGemm& g, const float* part, float* out, hipStream_t s) {
+  if (g.spc == 1) return hipSuccess;
   const int64_t n = g.M * g.Nc;
   hipLaunchKernelGGL(bwd_sum_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, part, g.spc, n,
                      out);
   return hipGetLastError();
+}
+
+// The gradient contractions: one launch for all of them when their tiles
+// have one width (the products' workgroups then fill the CUs that one
+// product's last round leaves idle), else one launch each; split products'
+// partials (part[i], disjoint) summed after.
+hipError_t bwd_gemms(const BGemm* g, const uint16_t* const* A, const uint16_t* const* B, const int64_t* ld,
+                     float* const* part, float* const* out, int n, hipStream_t s) {
+  bool same = n <= kWriteBatch;
+  for (int i = 1; i < n; ++i) same = same && g[i].nbf == g[0].nbf;
+  if (same) {
+    TWriteBatch b{};
+    b.n = n;
+    b.start[0] = 0;
+    for (int i = 0; i < n; ++i) {
+      b.p[i] = bwd_params(g[i], A[i], B[i], ld[i], part[i], out[i]);
+      b.start[i + 1] = b.start[i] + static_cast<int>(bwd_grid(g[i]));
+    }
+    if (g[0].nbf == 3)
+      hipLaunchKernelGGL(tiled_write_batch_kernel<3>, dim3(static_cast<unsigned>(b.start[n])), dim3(kGThreads),
+                         gemm_lds(3), s, b);
+    else
+      hipLaunchKernelGGL(tiled_write_batch_kernel<4>, dim3(static_cast<unsigned>(b.start[n])), dim3(kGThreads),
+                         kGemmLds, s, b);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  } else {
+    for (int i = 0; i < n; ++i) {
+      const TWriteParams wp = bwd_params(g[i], A[i], B[i], ld[i], part[i], out[i]);
+      if (g[i].nbf == 3)
+        hipLaunchKernelGGL((tiled_write_kernel<3, true>), dim3(bwd_grid(g[i])), dim3(kGThreads), gemm_lds(3), s, wp);
+      else
+        hipLaunchKernelGGL((tiled_write_kernel<4, true>), dim3(bwd_grid(g[i])), dim3(kGThreads), kGemmLds, s, wp);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+  }
+  for (int i = 0; i < n; ++i) {
+    hipError_t e = bwd_sum(g[i], part[i], out[i], s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 struct BLayout {
@@ -1985,11 +2057,10 @@ BLayout blayout(const srw_desc_t& d) {
   l.dead = take(static_cast<size_t>(l.N64) * 4);
   l.blk = take(static_cast<size_t>(l.nblk) * 2 * 4);
   l.coef = take(4 * 4);
+  // one fp32 partial region per split product (they run in one launch)
   size_t part = 0;
-  for (const BGemm& g : {l.g_dw, l.g_dh, l.g_dx, l.g_de, l.g_dr}) {
-    const size_t b = static_cast<size_t>(g.spc) * g.M * g.Nc * 4;
-    part = b > part ? b : part;
-  }
+  for (const BGemm& g : {l.g_dw, l.g_dr, l.g_de, l.g_dx, l.g_dh})
+    if (g.spc > 1) part += al256(static_cast<int64_t>(g.spc) * g.M * g.Nc * 4);
   l.part = take(part);
   l.total = off;
   return l;
@@ -2054,7 +2125,10 @@ hipError_t tiled_backward(const BackwardArgs& a) {
                          reinterpret_cast<const void*>(tiled_store_kernel),
                          reinterpret_cast<const void*>(tiled_write_kernel<4>)})
     if ((e = set_lds(fn)) != hipSuccess) return e;
-  if ((e = set_lds(reinterpret_cast<const void*>(tiled_write_kernel<3>), gemm_lds(3))) != hipSuccess) return e;
+  if ((e = set_lds(reinterpret_cast<const void*>(tiled_write_kernel<3, true>), gemm_lds(3))) != hipSuccess) return e;
+  if ((e = set_lds(reinterpret_cast<const void*>(tiled_write_kernel<4, true>))) != hipSuccess) return e;
+  if ((e = set_lds(reinterpret_cast<const void*>(tiled_write_batch_kernel<3>), gemm_lds(3))) != hipSuccess) return e;
+  if ((e = set_lds(reinterpret_cast<const void*>(tiled_write_batch_kernel<4>))) != hipSuccess) return e;
 #define SRW_TRY(expr) \
   if ((e = (expr)) != hipSuccess) return e
   // operands of the K = units / K = rows contractions, unit- or row-contiguous
@@ -2179,11 +2253,20 @@ hipError_t tiled_backward(const BackwardArgs& a) {
 
   // the five gradient contractions: bf16 dots, fp32 accumulation
   SRW_TRY(transpose(DRAW, DRAWT, Tv, l.Tv64, D, st));
-  SRW_TRY(bwd_gemm(l.g_dw, PT, DRAWT, l.Tv64, part, a.g.dwrite, st));
-  SRW_TRY(bwd_gemm(l.g_dr, DXRT, XT, l.T64, part, a.g.dread, st));
-  SRW_TRY(bwd_gemm(l.g_de, DST, HT, l.Tv64, part, a.g.demb, st));
-  SRW_TRY(bwd_gemm(l.g_dx, DXR, RT, N64, part, a.g.dx, st));
-  SRW_TRY(bwd_gemm(l.g_dh, DS, ET, N64, part, a.g.dh, st));
+  {
+    const BGemm gs[5] = {l.g_dw, l.g_dr, l.g_de, l.g_dx, l.g_dh};
+    const uint16_t* As[5] = {PT, DXRT, DST, DXR, DS};
+    const uint16_t* Bs[5] = {DRAWT, XT, HT, RT, ET};
+    const int64_t lds_[5] = {l.Tv64, l.T64, l.Tv64, N64, N64};
+    float* outs[5] = {a.g.dwrite, a.g.dread, a.g.demb, a.g.dx, a.g.dh};
+    float* parts[5];
+    float* pp = part;
+    for (int i = 0; i < 5; ++i) {
+      parts[i] = pp;
+      if (gs[i].spc > 1) pp += al256(static_cast<int64_t>(gs[i].spc) * gs[i].M * gs[i].Nc * 4) / 4;
+    }
+    SRW_TRY(bwd_gemms(gs, As, Bs, lds_, parts, outs, 5, st));
+  }
 #undef SRW_TRY
   return hipSuccess;
 }
