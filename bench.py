@@ -628,6 +628,9 @@ def main() -> int:
     ap.add_argument("--tiled", action="store_true",
                     help="run the tiled-GEMM kernels (P materialised) where a fused kernel "
                          "exists too (they serve d_model > 384 anyway)")
+    ap.add_argument("--no-residuals", action="store_true",
+                    help="with --backward: no forward residuals (den, unit statistics); the "
+                         "backward recomputes them from the scores")
     ap.add_argument("--backward", action="store_true",
                     help="time the backward (srw_backward: the VJP of fused_gate_srw for the "
                          "training step) instead of the forward; one route, bf16")
@@ -753,8 +756,16 @@ def main() -> int:
         # cotangents of out (synthetic, seeded) and of score_lb / dead_penalty
         gen = torch.Generator().manual_seed(args.seed + 1)
         d_out = torch.randn(shape.T, 1, shape.D, generator=gen).to(dev)
+        den = unit_diag = None
+        if not args.no_residuals:
+            # the drop-in's training path: its forward (with diagnostics)
+            # hands the backward its den and unit statistics
+            fplan = pkg.SrwPlan(*plan.inputs[:6], stats=args.stats, chunk_size=cs, want_mask=False, diag=True)
+            fplan.launch(stream)
+            torch.cuda.synchronize()
+            den, unit_diag = fplan.den, fplan.unit_diag
         bplan = pkg.SrwBackwardPlan(x, h, plan.inputs[2], plan.inputs[3], plan.inputs[4],
-                                    plan.inputs[5], plan.out, d_out, 1e-2, 1e-2)
+                                    plan.inputs[5], plan.out, d_out, 1e-2, 1e-2, den=den, unit_diag=unit_diag)
         bplan.launch(stream)
         torch.cuda.synchronize()
         log(f"backward first call done, path={bplan.path}, workspace {bplan.ws_bytes / 2**30:.2f} GiB")
@@ -907,6 +918,7 @@ def main() -> int:
                    "d_route": dr, "n_units": N, "routes": R, "chunk": cs,
                    "stats": args.stats, "diag": args.diag, "pool_cached": args.pool_cached,
                    "tiled": args.tiled, "pass": "backward" if args.backward else "forward",
+                   "residuals": bool(args.backward and not args.no_residuals),
                    "graph": args.graph, "sparse_skip": args.sparse, "gate": args.gate,
                    "cold": args.cold,
                    "tau_offset": round(tau_value, 4),

@@ -19,7 +19,7 @@ import threading
 import torch  # noqa: F401  (must precede loading the HIP library)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libsrw_amd.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 MAX_BATCH = 4          # SRW_MAX_BATCH
 
 # srw_status_t
@@ -84,7 +84,8 @@ class SrwOutputs(ctypes.Structure):
 
 class SrwCotangents(ctypes.Structure):
     _fields_ = [("d_out", ctypes.c_void_p), ("out", ctypes.c_void_p),
-                ("d_score_lb", ctypes.c_float), ("d_dead_penalty", ctypes.c_float)]
+                ("d_score_lb", ctypes.c_float), ("d_dead_penalty", ctypes.c_float),
+                ("den", ctypes.c_void_p), ("unit_diag", ctypes.c_void_p)]
 
 
 class SrwGrads(ctypes.Structure):

@@ -363,6 +363,7 @@ srw_status_t srw_backward(const srw_desc_t* d, const srw_tensors_t* in, const sr
   }
   if (!in->x || !in->h || !in->emb || !in->tau_offset || !in->read || !in->write) return SRW_EINVAL;
   if (!cot->d_out || !cot->out) return SRW_EINVAL;
+  if (!cot->den != !cot->unit_diag) return SRW_EINVAL;  // the forward's residuals: both or neither
   if (!grads->dx || !grads->dh || !grads->demb || !grads->dtau_offset || !grads->dread || !grads->dwrite)
     return SRW_EINVAL;
   if (!isfinite(cot->d_score_lb) || !isfinite(cot->d_dead_penalty)) return SRW_EINVAL;

@@ -1603,7 +1603,7 @@ __global__ __launch_bounds__(256) void bwd_fwd_elem_kernel(ElemParams p) {
 // contraction, so that bwd_gate_elem_kernel's row sums of dm and
 // bwd_ds_elem_kernel's recomputed dm are the same values.
 struct GateGrad {
-  float dm, dx;
+  float dm, dx, gb;  // gb: the bf16 gate (v41:516)
 };
 __device__ inline GateGrad gate_grad(float s, float x, float dp, float tau, float dden, const GateParams& gp,
                                      float exp_scale, float sharp) {
@@ -1618,7 +1618,7 @@ __device__ inline GateGrad gate_grad(float s, float x, float dp, float tau, floa
   const float dit = dgb * act + dden;
   const float dam = am < gp.maxi ? dit : 0.f;
   const float dm = (m - gp.cut > 0.f ? dam : 0.f) + dgb * it * sharp * act * (1.0f - act);
-  return GateGrad{dm, dx};
+  return GateGrad{dm, dx, gb};
 }
 
 // E2: the gate derivative from the stored scores, x.r and dP: per-row sums of
@@ -1626,8 +1626,12 @@ __device__ inline GateGrad gate_grad(float s, float x, float dp, float tau, floa
 // (the broadcast of x.r, v41:796-797) and stored in both layouts.  dm itself
 // is not stored: the ds pass recomputes it from the same bf16 inputs (reading
 // three bf16 arrays costs less than writing and reading an fp32 one).
+// PT_OUT (the forward's den and unit statistics given, no E1 pass): also P^T
+// = bf16(gate_bf * xr)^T (v41:516-518) from the same gate.
+template <bool PT_OUT>
 __global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
   __shared__ uint16_t tile[kTile][kTile + 8];
+  __shared__ uint16_t ptile[PT_OUT ? kTile : 1][kTile + 8];
   const ElemTile et = elem_tile();
   const int64_t n = et.n0 + 8 * et.q;
   float dxs[2][8];
@@ -1642,13 +1646,22 @@ __global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
     load8_bf16(p.XR + (vl / p.routes) * p.N64 + n, x);
     load8_bf16(p.DP + vl * p.N64 + n, dp);
     const float tau = p.tau[vl], dden = p.dden[vl];
-    float sdm = 0.f;
+    float sdm = 0.f, pr[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const bool ok = row_ok && n + e < p.N;
       const GateGrad gg = gate_grad(s[e], x[e], dp[e], tau, dden, p.gp, p.exp_scale, p.sharp);
       dxs[rr][e] = ok ? gg.dx : 0.f;
       sdm += ok ? gg.dm : 0.f;
+      pr[e] = ok ? gg.gb * x[e] : 0.f;  // bf16 product, rounded by the packing below
+    }
+    if constexpr (PT_OUT) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t w = pack_bf16(pr[2 * k], pr[2 * k + 1]);
+        ptile[r][8 * et.q + 2 * k] = static_cast<uint16_t>(w);
+        ptile[r][8 * et.q + 2 * k + 1] = static_cast<uint16_t>(w >> 16);
+      }
     }
     sdm = rowsum8(sdm);
     if (et.q == 0 && row_ok) p.dm_part[static_cast<int64_t>(blockIdx.x) * p.Tv + v] = sdm;
@@ -1674,6 +1687,7 @@ __global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
   }
   __syncthreads();
   store_transposed(tile, nt, p.DXRT, p.T64, et.n0, t0, p.N64);
+  if constexpr (PT_OUT) store_transposed(ptile, kTile, p.PT, p.Tv64, et.n0, et.v0, p.N64);
 }
 
 struct DsParams {
@@ -1806,6 +1820,27 @@ __global__ __launch_bounds__(256) void bwd_unit_reduce_kernel(const float* __res
   if (n < N64) {
     pn[n] = m;
     dead[n] = ok && gmax < dead_thr ? 1.0f : 0.0f;
+  }
+  const float a = block_sum<256>(m, red);
+  const float b = block_sum<256>(m * m, red);
+  if (threadIdx.x == 0) {
+    blk[2 * blockIdx.x] = a;
+    blk[2 * blockIdx.x + 1] = b;
+  }
+}
+
+// The same from the forward's unit diagnostics (unit_diag[n][2] = sum of the
+// unit's scores over the rows, its max gate): pn, dead and the block sums.
+__global__ __launch_bounds__(256) void bwd_unit_from_diag_kernel(const float* __restrict__ ud, int64_t T, int64_t N,
+                                                                 int64_t N64, float dead_thr, float* __restrict__ pn,
+                                                                 float* __restrict__ dead, float* __restrict__ blk) {
+  __shared__ float red[4];
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const bool ok = n < N;
+  const float m = ok ? ud[n * SRW_UDIAG_COUNT + SRW_UDIAG_SCORE_SUM] / static_cast<float>(T) : 0.f;
+  if (n < N64) {
+    pn[n] = m;
+    dead[n] = ok && ud[n * SRW_UDIAG_COUNT + SRW_UDIAG_GATE_MAX] < dead_thr ? 1.0f : 0.0f;
   }
   const float a = block_sum<256>(m, red);
   const float b = block_sum<256>(m * m, red);
@@ -2193,20 +2228,31 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   ep.exp_scale = exp_scale;
   ep.sharp = d.sharpness;
   const dim3 grid_e(static_cast<unsigned>(l.NB), static_cast<unsigned>(l.TS));
-  hipLaunchKernelGGL(bwd_fwd_elem_kernel, grid_e, dim3(256), 0, st, ep);
-  SRW_TRY(hipGetLastError());
-  hipLaunchKernelGGL(bwd_rowsum_kernel, dim3(static_cast<unsigned>((Tv + 63) / 64)), dim3(256), 0, st, inten_part,
-                     l.NB, Tv, zsum);
-  SRW_TRY(hipGetLastError());
-  hipLaunchKernelGGL(bwd_unit_reduce_kernel, dim3(static_cast<unsigned>(l.nblk)), dim3(256), 0, st, psum, pmax, l.TS,
-                     Tv, N, N64, d.dead_threshold, pn, dead, blk);
-  SRW_TRY(hipGetLastError());
+  // the forward's den and unit statistics given: no E1 pass (P^T comes from
+  // the E2 pass's gates)
+  const bool res = a.cot.den && a.cot.unit_diag;
+  const float* zs = zsum;
+  if (res) {
+    zs = a.cot.den;  // den = max(sum intensity, 1): the den term's test sum > 1 reads the same on it
+    hipLaunchKernelGGL(bwd_unit_from_diag_kernel, dim3(static_cast<unsigned>(l.nblk)), dim3(256), 0, st,
+                       a.cot.unit_diag, Tv, N, N64, d.dead_threshold, pn, dead, blk);
+    SRW_TRY(hipGetLastError());
+  } else {
+    hipLaunchKernelGGL(bwd_fwd_elem_kernel, grid_e, dim3(256), 0, st, ep);
+    SRW_TRY(hipGetLastError());
+    hipLaunchKernelGGL(bwd_rowsum_kernel, dim3(static_cast<unsigned>((Tv + 63) / 64)), dim3(256), 0, st, inten_part,
+                       l.NB, Tv, zsum);
+    SRW_TRY(hipGetLastError());
+    hipLaunchKernelGGL(bwd_unit_reduce_kernel, dim3(static_cast<unsigned>(l.nblk)), dim3(256), 0, st, psum, pmax,
+                       l.TS, Tv, N, N64, d.dead_threshold, pn, dead, blk);
+    SRW_TRY(hipGetLastError());
+  }
   hipLaunchKernelGGL(bwd_unit_coef_kernel, dim3(1), dim3(256), 0, st, blk, l.nblk, N, a.cot.d_score_lb, coef);
   SRW_TRY(hipGetLastError());
 
   // cotangent of the chunk dots and the den term; dP; E2: the gate derivative
   hipLaunchKernelGGL(bwd_prep_kernel, dim3(static_cast<unsigned>(Tv)), dim3(256), 0, st, a.cot.d_out,
-                     static_cast<const uint16_t*>(a.cot.out), zsum, 1, d.scale, static_cast<int>(D), DRAW, dden,
+                     static_cast<const uint16_t*>(a.cot.out), zs, 1, d.scale, static_cast<int>(D), DRAW, dden,
                      dsc);
   SRW_TRY(hipGetLastError());
   if (a.g.dscale) {
@@ -2220,7 +2266,10 @@ hipError_t tiled_backward(const BackwardArgs& a) {
     SRW_TRY(store_gemm(write, DRAW, DP, Tv, Tv, 1, N, N64, D, st));
   }
   dominant_kernel_end(st);
-  hipLaunchKernelGGL(bwd_gate_elem_kernel, grid_e, dim3(256), 0, st, ep);
+  if (res)
+    hipLaunchKernelGGL(bwd_gate_elem_kernel<true>, grid_e, dim3(256), 0, st, ep);
+  else
+    hipLaunchKernelGGL(bwd_gate_elem_kernel<false>, grid_e, dim3(256), 0, st, ep);
   SRW_TRY(hipGetLastError());
   hipLaunchKernelGGL(bwd_token_kernel, dim3(static_cast<unsigned>((Tv + 3) / 4)), dim3(256), 0, st, dm_part, l.NB,
                      Tv, N, a.in.tau_offset, mean, var, sdev, a.g.dtau_offset, alpha, beta);

@@ -273,7 +273,7 @@ class SrwBackwardPlan:
 
     def __init__(self, x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: float = 0.0,
                  d_dead_penalty: float = 0.0, *, consts: GateConfig = GateConfig(),
-                 scale: float = 1.0):
+                 scale: float = 1.0, den=None, unit_diag=None):
         if x.dim() != 2:
             raise ValueError("x must be [T, D]")
         T, D = x.shape
@@ -298,6 +298,11 @@ class SrwBackwardPlan:
         _check_dev("write", write, dev, x.dtype, (N, D))
         _check_dev("out", out, dev, x.dtype, (T, R, D))
         _check_dev("d_out", d_out, dev, torch.float32, (T, R, D))
+        if (den is None) != (unit_diag is None):
+            raise ValueError("den and unit_diag (the forward's residuals) go together")
+        if den is not None:
+            _check_dev("den", den, dev, torch.float32, (T, R))
+            _check_dev("unit_diag", unit_diag, dev, torch.float32, (N, len(C.UDIAG)))
         desc = C.desc_init()
         desc.T, desc.d_model, desc.d_route, desc.n_units = T, D, dr, N
         desc.n_routes = R
@@ -316,12 +321,13 @@ class SrwBackwardPlan:
                           dscale=torch.empty((), **f32))
         self.ws_bytes = C.backward_workspace_size(desc)
         self.workspace = torch.empty(max(self.ws_bytes, 1), dtype=torch.uint8, device=dev)
-        self.inputs = (x, h, emb, tau_offset, read, write, out, d_out)
+        self.inputs = (x, h, emb, tau_offset, read, write, out, d_out, den, unit_diag)
         self.device = dev
         self._desc = desc
         self._tens = C.SrwTensors(_ptr(x), _ptr(x if h_is_x else h), _ptr(emb), _ptr(tau_offset),
                                   _ptr(read), _ptr(write))
-        self._cot = C.SrwCotangents(_ptr(d_out), _ptr(out), float(d_score_lb), float(d_dead_penalty))
+        self._cot = C.SrwCotangents(_ptr(d_out), _ptr(out), float(d_score_lb), float(d_dead_penalty),
+                                    _ptr(den), _ptr(unit_diag))
         self._g = C.SrwGrads(*(_ptr(self.grads[k]) for k in
                                ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite", "dscale")))
         self._lib = C.load_library()
@@ -343,7 +349,7 @@ class SrwBackwardPlan:
 
 def srw_backward(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: float = 0.0,
                  d_dead_penalty: float = 0.0, *, consts: GateConfig = GateConfig(),
-                 scale: float = 1.0, stream=None) -> dict:
+                 scale: float = 1.0, stream=None, den=None, unit_diag=None) -> dict:
     """Reverse-mode derivative of one srw_forward call (the VJP of
     fused_gate_srw that the reference's train_step takes with
     jax.value_and_grad, scripts/train_jax.py:548-726).
@@ -357,8 +363,12 @@ def srw_backward(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: flo
     [N, dr], dtau_offset [T, R], dread / dwrite [N, D] and dscale [] (of
     ``scale``, which multiplies out: the caller's *_scale, v41:1044-1053,
     1175); when ``h is x`` the total gradient of x is dx + dh[:, 0].
+    ``den`` [T, R] and ``unit_diag`` [N, 2] (both or neither): the same
+    forward call's den and unit diagnostics (a ``diag=True`` call, as the
+    drop-in's forward makes), which spare the backward its own pass over the
+    scores for them.
     """
     plan = SrwBackwardPlan(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb,
-                           d_dead_penalty, consts=consts, scale=scale)
+                           d_dead_penalty, consts=consts, scale=scale, den=den, unit_diag=unit_diag)
     plan.launch(stream)
     return plan.results()

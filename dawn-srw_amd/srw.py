@@ -157,7 +157,9 @@ class _FusedSrw(torch.autograd.Function):
         shape = (B, S, D) if routes == 1 else (B, S, 2, D)
         out = res["out"].reshape(shape).to(torch.float32)
         outs = (out,) + _diag_tuple(res, N, B, S, routes, consts.dead_threshold)
-        ctx.save_for_backward(xb, hb, eb, tau, rdb, wb, res["out"])
+        # the forward's den and unit statistics: the backward takes them
+        # instead of recomputing them from the scores
+        ctx.save_for_backward(xb, hb, eb, tau, rdb, wb, res["out"], res["den"], res["unit_diag"])
         ctx.meta = (routes, consts, tuple(t.shape for t in (x, h, emb, tau_offset, read, write)),
                     tuple(t.dtype for t in (x, h, emb, tau_offset, read, write)))
         ctx.mark_non_differentiable(*(outs[i] for i in _NO_GRAD))
@@ -172,7 +174,7 @@ class _FusedSrw(torch.autograd.Function):
                     f"the gradient through output {i} ({_NAMES[i]}) of the fused SRW layer is not "
                     "implemented; out, score_lb and dead_penalty are differentiable")
         routes, consts, shapes, dtypes = ctx.meta
-        xb, hb, eb, tau, rdb, wb, out_b = ctx.saved_tensors
+        xb, hb, eb, tau, rdb, wb, out_b, den, unit_diag = ctx.saved_tensors
         T, D = xb.shape
         d_out = grads[_OUT]
         if d_out is None:
@@ -181,7 +183,8 @@ class _FusedSrw(torch.autograd.Function):
             d_out = d_out.reshape(T, routes, D).to(torch.float32).contiguous()
         d_lb = 0.0 if grads[_SCORE_LB] is None else float(grads[_SCORE_LB])
         d_pen = 0.0 if grads[_DEAD_PENALTY] is None else float(grads[_DEAD_PENALTY])
-        g = srw_backward(xb, hb, eb, tau, rdb, wb, out_b, d_out, d_lb, d_pen, consts=consts)
+        g = srw_backward(xb, hb, eb, tau, rdb, wb, out_b, d_out, d_lb, d_pen, consts=consts,
+                         den=den.reshape(T, routes), unit_diag=unit_diag)
         res = [g[k] for k in ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite")]
         res = [r.reshape(sh).to(dt) for r, sh, dt in zip(res, shapes, dtypes)]
         return (*res, None, None, None)

@@ -64,7 +64,7 @@
 extern "C" {
 #endif
 
-#define SRW_AMD_ABI_VERSION 6
+#define SRW_AMD_ABI_VERSION 7
 
 typedef enum srw_status {
   SRW_OK = 0,
@@ -218,6 +218,15 @@ typedef struct srw_cotangents {
                               inputs (desc->dtype; required: the den term) */
   float d_score_lb;        /* cotangent of score_lb (v41:477-483) */
   float d_dead_penalty;    /* cotangent of dead_penalty (v41:543-552) */
+  /* Optional residuals of that forward call, both or neither: its den and
+   * its unit_diag (a call with SRW_FLAG_DIAG, as the drop-in's forward
+   * makes).  With them the backward takes den, each unit's mean score
+   * (score_lb) and max gate (the dead units) from the forward instead of
+   * recomputing them in a pass of its own over the scores (no counterpart
+   * in the reference, whose autodiff keeps its own residuals; values equal
+   * up to the forward's summation order). */
+  const float* den;        /* [T, n_routes] or NULL */
+  const float* unit_diag;  /* [N, SRW_UDIAG_COUNT] or NULL */
 } srw_cotangents_t;
 
 /* Gradients written by srw_backward, float32; all required but dscale.

@@ -69,6 +69,58 @@ def test_backward_matches_oracle_vjp(pkg, dev, case):
         assert err <= 2e-2, (k, err)
 
 
+@pytest.mark.parametrize("case", [CASES[0], CASES[1], CASES[4]], ids=lambda c: "T{}D{}dr{}N{}{}".format(
+    c[0], c[1], c[2], c[3], "x" if c[4] else ""))
+def test_backward_with_forward_residuals(pkg, dev, case):
+    """With the forward's den and unit diagnostics handed over (the drop-in's
+    training path) the backward skips its own pass over the scores for them:
+    every gradient still within the oracle bar, and within 1e-2 of the
+    backward that recomputes them (the two differ by the forward's summation
+    order of den and the unit score sums)."""
+    T, D, dr, N, hx, seed, tau = case
+    print(f"[gpu] backward with residuals {case}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, hx, seed, tau)
+    xb = inp["x"].to(BF)
+    hb = xb if hx else inp["h"][:, 0].to(BF)
+    eb, rb, wb = (inp[k].to(BF) for k in ("emb", "read", "write"))
+    g = torch.Generator().manual_seed(seed + 99)
+    d_out = torch.randn(T, D, generator=g)
+    d_lb, d_pen = 0.37, -0.81
+    ref = srw_vjp.fused_gate_srw_vjp(xb.float(), hb.float(), eb.float(), inp["tau_offset"], rb.float(),
+                                     wb.float(), d_out, d_lb, d_pen, max_chunk_size=max(N, 1))
+    x = xb.to(dev)
+    h = x if hx else hb[:, None].contiguous().to(dev)
+    args = (x, h, eb.to(dev), inp["tau_offset"].to(dev), rb.to(dev), wb.to(dev))
+    fwd = pkg.srw_forward(*args, want_mask=False, diag=True)
+    got = pkg.srw_backward(*args, fwd["out"], d_out[:, None].to(dev), d_lb, d_pen,
+                           den=fwd["den"], unit_diag=fwd["unit_diag"])
+    plain = pkg.srw_backward(*args, fwd["out"], d_out[:, None].to(dev), d_lb, d_pen)
+    torch.cuda.synchronize()
+    pairs = dict(dx=(got["dx"], plain["dx"]), dh=(got["dh"][:, 0], plain["dh"][:, 0]),
+                 demb=(got["demb"], plain["demb"]), dtau_offset=(got["dtau_offset"], plain["dtau_offset"]),
+                 dread=(got["dread"], plain["dread"]), dwrite=(got["dwrite"], plain["dwrite"]))
+    for k, (v, w) in pairs.items():
+        err = rel_fro(v.cpu(), ref[k].float())
+        same = rel_fro(v.cpu(), w.cpu())
+        print(f"  {k}: rel err {err:.3e}, against the recomputing backward {same:.3e}", flush=True)
+        assert torch.isfinite(v).all(), k
+        assert err <= 2e-2, (k, err)
+        assert same <= 1e-2, (k, same)
+
+
+def test_backward_residuals_both_or_neither(pkg, dev):
+    """den without unit_diag (or the reverse) is refused."""
+    T, D, N = 32, 128, 300
+    x = torch.randn(T, D, device=dev).to(BF)
+    emb = torch.randn(N, D, device=dev).to(BF)
+    rw = torch.randn(N, D, device=dev).to(BF)
+    tau = torch.full((T, 1), -0.5, device=dev)
+    out = torch.zeros(T, 1, D, dtype=BF, device=dev)
+    d_out = torch.zeros(T, 1, D, device=dev)
+    with pytest.raises(ValueError):
+        pkg.srw_backward(x, x, emb, tau, rw, rw, out, d_out, 0.0, 0.0, den=torch.ones(T, 1, device=dev))
+
+
 def test_backward_linear_in_cotangents(pkg, dev):
     """The VJP is linear in (d_out, d_lb, d_pen): grad(a + b) = grad(a) + grad(b)
     up to the bf16 rounding of each contraction."""
