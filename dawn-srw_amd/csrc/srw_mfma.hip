@@ -1148,11 +1148,12 @@ constexpr int kWsThreads = 512;
 
 // DG: training diagnostics -- per-token extras in tok_part (TPS = 12), per-unit
 // score sums and max margins per 32-row block into unit_part.  GL: the v4.0.1 GELU
-// gate (p.sstd; the row sums carry z+ where v4.1 has the intensity), without
-// diagnostics.
+// gate (p.sstd; the row sums carry z+ where v4.1 has the intensity); with DG
+// its diagnostics (v401:311-320): the max gate itself in TP_SMAX, the gate >
+// 0.5 / boundary / z-band counts, sum g log g, and per unit the max gate in
+// place of the max margin.
 template <int DB, int KH, bool HX, bool DG, bool GL = false>
 __device__ __attribute__((always_inline)) inline void main_ws_body(const MainParams& p, const int bid) {
-  static_assert(!(DG && GL), "the GELU gate has no diagnostics variant here");
   // With the GELU gate the producer gates (its registers have room for the
   // longer element chain; the consumer's are held by the write GEMM's
   // accumulators): it hands the consumer bf16(gate) where the scores go,
@@ -1247,7 +1248,7 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
     // the GELU gate's row: tau (bf16 for _srw_inference) and 1 / s_std
     const float gl_tau = GL ? (p.gl_raw_bf16 ? __uint_as_float(pack_bf16(0.0f, p.tau[tl])) : p.tau[tl]) : 0.f;
     const float gl_istd = GL ? 1.0f / p.sstd[tl] : 1.f;
-    float gl_gsum = 0.f;
+    float gl_gsum = 0.f, gl_gmax = 0.f, gl_glogg = 0.f;
     float smax = -INFINITY, isum = 0.f;
     uint32_t n_strong = 0, n_bound = 0, n_075 = 0, n_030 = 0, n_cap = 0, nact = 0;
     // Drain the x / h loads here: left pending into the tile loop, they make
@@ -1264,7 +1265,7 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
       if constexpr (DG) {
         if (it >= 1) {
           const int64_t pu0 = static_cast<int64_t>(ta + it - 1) * kUnitTile;
-          if (p.mask32 && half == 0 && t < p.g.T) {
+          if (!GL && p.mask32 && half == 0 && t < p.g.T) {  // (the GELU gate stores its mask words at once)
             uint32_t* dst = p.mask32 + t * p.mask_words32 + (ta + it - 1);
             const bool shared = (pu0 < lo) || (pu0 + kUnitTile > hi && hi < p.g.N);
             if (shared) atomicOr(dst, pend_m);
@@ -1321,6 +1322,28 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
           const int64_t u0 = static_cast<int64_t>(ta + it) * kUnitTile;
           const bool full = u0 >= lo && u0 + kUnitTile <= hi;
           uint32_t bits = 0;
+          [[maybe_unused]] const bool row_ok = t < p.g.T;
+          if constexpr (DG) {
+            // per unit of the tile the sum of scores over the wave's 32 rows
+            // (score_lb, v401:257-260), reduced before the gate loop so that
+            // its registers are free there
+            float su[16];
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const uint32_t pr = sx[4 * (v >> 2) + ((v & 3) >> 1)];
+              const float sv = (v & 1) ? hi_f32(pr) : lo_f32(pr);
+              bool ok = row_ok;
+              if (!full) {
+                const int64_t u = u0 + unit_of_acc(v, half);
+                ok = ok && u >= lo && u < hi;
+              }
+              su[v] = ok ? sv : 0.f;
+            }
+            reduce_scatter16(su, lane, [](float x, float y) { return x + y; });
+            pend_su = su[0];
+          }
+          // diagnostics: per unit the max gate over the wave's 32 rows
+          [[maybe_unused]] float gx[DG ? 16 : 1];
 #pragma unroll
           for (int q = 0; q < 8; ++q) {
             const int w = 4 * (q >> 1) + (q & 1);  // the word of elements 2q, 2q + 1
@@ -1331,9 +1354,10 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
               float zp;
               float g = gelu_gate(sv, gl_tau, gl_istd, zp, p.gl_raw_bf16 != 0);
               uint32_t sign = __float_as_uint(gl_tau - sv);
+              bool ok = true;
               if (!full) {
                 const int64_t u = u0 + unit_of_acc(2 * q + e, half);
-                const bool ok = u >= lo && u < hi;
+                ok = u >= lo && u < hi;
                 g = ok ? g : 0.f;
                 zp = ok ? zp : 0.f;
                 sign = ok ? sign : 0u;
@@ -1342,8 +1366,28 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
               isum += zp;
               bits = __builtin_amdgcn_alignbit(bits, sign, 31);  // bits << 1 | active
               g2[e] = g;
+              if constexpr (DG) {
+                // v401:311-318.  phi > 0.95 or phi < 0.05 <=> |z| > Phi^-1(0.95)
+                // (phi is increasing in z; z over every unit, passing or not);
+                // 0 < z < 0.75 <=> active and not z+ >= 0.75 (n_075 = active
+                // count - those, at the end; likewise 0.30); units outside the
+                // split have g = z+ = 0 and are excluded from the boundary
+                // count by ok
+                const float z = (sv - gl_tau) * gl_istd;
+                n_strong += g > 0.5f ? 1u : 0u;
+                n_bound += (ok && fabsf(z) > 1.6448536269514722f) ? 1u : 0u;
+                n_075 += zp >= 0.75f ? 1u : 0u;
+                n_030 += zp >= 0.30f ? 1u : 0u;
+                gl_gmax = fmaxf(gl_gmax, g);
+                gl_glogg = fmaf(g, __builtin_amdgcn_logf(g + 1e-8f), gl_glogg);  // log2; ln at the end
+                gx[2 * q + e] = row_ok ? g : 0.f;
+              }
             }
             sx[w] = pack_bf16(g2[0], g2[1]);  // gate_bf (v401:307)
+          }
+          if constexpr (DG) {
+            reduce_scatter16(gx, lane, [](float x, float y) { return fmaxf(x, y); });
+            pend_mx = gx[0];
           }
           const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
           uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
@@ -1357,7 +1401,7 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
             else *dst = m;
           }
         }
-        if constexpr (DG) {
+        if constexpr (DG && !GL) {
           // per-unit sum of scores and max of (score - tau) over this wave's 32
           // rows (v41:445-447, 543-552): butterfly over the lanes of each half
           const int64_t u0 = static_cast<int64_t>(ta + it) * kUnitTile;
@@ -1421,14 +1465,31 @@ __device__ __attribute__((always_inline)) inline void main_ws_body(const MainPar
       gl_gsum += __shfl_xor(gl_gsum, 32);
       isum += __shfl_xor(isum, 32);
       nact += __shfl_xor(nact, 32);
+      if constexpr (DG) {
+        gl_gmax = fmaxf(gl_gmax, __shfl_xor(gl_gmax, 32));
+        n_strong += __shfl_xor(n_strong, 32);
+        n_bound += __shfl_xor(n_bound, 32);
+        n_075 += __shfl_xor(n_075, 32);
+        n_030 += __shfl_xor(n_030, 32);
+        gl_glogg += __shfl_xor(gl_glogg, 32);
+      }
       if (half == 0 && t < p.g.T) {
         float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * TPS;
         tp[0] = gl_gsum;
         tp[1] = isum;  // sum of z+
         tp[2] = static_cast<float>(nact);
+        if constexpr (DG) {
+          tp[TP_SMAX] = gl_gmax;  // the max gate itself
+          tp[TP_STRONG] = static_cast<float>(n_strong);
+          tp[TP_BOUND] = static_cast<float>(n_bound);
+          tp[TP_075] = static_cast<float>(nact - n_075);  // 0 < z < 0.75
+          tp[TP_030] = static_cast<float>(nact - n_030);
+          tp[TP_CAP] = 0.f;
+          tp[TP_GLOGG] = gl_glogg * 0.69314718055994531f;  // log2 -> ln
+        }
       }
     }
-    if constexpr (DG) {
+    if constexpr (DG && !GL) {
       smax = fmaxf(smax, __shfl_xor(smax, 32));
       n_strong += __shfl_xor(n_strong, 32);
       n_bound += __shfl_xor(n_bound, 32);
@@ -2086,6 +2147,24 @@ __global__ __launch_bounds__(256) void srw_tau_batch_kernel(Batch<TauParams> b) 
 // eight independent loads in flight.
 // ---------------------------------------------------------------------------
 
+// The row's gate and intensity maxima for token_diag from its TP_SMAX
+// partials' max m.  v4.1: m is the max score, and gate and intensity are
+// non-decreasing in the score (v41:583, 536-537).  The v4.0.1 gate (den_gate):
+// m is the max gate itself (v401:321), and there is no intensity.
+__device__ __attribute__((always_inline)) inline void diag_maxima(const FinalParams& p, int64_t t, float m, float* td) {
+  if (p.den_gate) {
+    td[SRW_TDIAG_GATE_MAX] = m;
+    td[SRW_TDIAG_INT_MAX] = 0.f;
+    return;
+  }
+  const float tau_thr = p.tau[t] + p.gp.thr;
+  const float tau_cut = tau_thr + p.gp.cut;
+  const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(m, p.exp_scale, -tau_thr * p.exp_scale)));
+  const float imax = p.gp.eps + __builtin_amdgcn_fmed3f(m - tau_cut, 0.0f, p.gp.maxi);
+  td[SRW_TDIAG_GATE_MAX] = act * imax;
+  td[SRW_TDIAG_INT_MAX] = imax;
+}
+
 // NG: split groups per workgroup; VW: columns per thread (1, 2 or 4: 4-,
 // 8- or 16-byte loads; the widest that leaves two workgroups per CU).  One workgroup per (row, block of 256 / NG
 // x VW columns); thread (g, c) = (tid / CW, tid % CW) sums columns
@@ -2201,12 +2280,8 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
 #pragma unroll
     for (int k = 0; k < 6; ++k) c[k] = wave_sum(c[k]);
     if (tid == 0) {
-      const float tau_thr = p.tau[t] + p.gp.thr;
-      const float tau_cut = tau_thr + p.gp.cut;
-      const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(smax, p.exp_scale, -tau_thr * p.exp_scale)));
-      const float imax = p.gp.eps + __builtin_amdgcn_fmed3f(smax - tau_cut, 0.0f, p.gp.maxi);
       float* td = p.token_diag + t * SRW_TDIAG_COUNT;
-      td[SRW_TDIAG_GATE_MAX] = act * imax;
+      diag_maxima(p, t, smax, td);
       td[SRW_TDIAG_INT_SUM] = I;
       td[SRW_TDIAG_N_STRONG] = c[0];
       td[SRW_TDIAG_N_BOUNDARY] = c[1];
@@ -2214,7 +2289,6 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
       td[SRW_TDIAG_N_BAND030] = c[3];
       td[SRW_TDIAG_N_INT_CAP] = c[4];
       td[SRW_TDIAG_G_LOG_G] = c[5];
-      td[SRW_TDIAG_INT_MAX] = imax;
     }
   }
 }
@@ -2329,12 +2403,8 @@ __device__ __attribute__((always_inline)) inline void finalize_rows_body(const F
 #pragma unroll
     for (int k = 0; k < 6; ++k) c[k] = wave_sum(c[k]);
     if (lane == 0) {
-      const float tau_thr = p.tau[t] + p.gp.thr;
-      const float tau_cut = tau_thr + p.gp.cut;
-      const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(smax, p.exp_scale, -tau_thr * p.exp_scale)));
-      const float imax = p.gp.eps + __builtin_amdgcn_fmed3f(smax - tau_cut, 0.0f, p.gp.maxi);
       float* td = p.token_diag + t * SRW_TDIAG_COUNT;
-      td[SRW_TDIAG_GATE_MAX] = act * imax;
+      diag_maxima(p, t, smax, td);
       td[SRW_TDIAG_INT_SUM] = is;
       td[SRW_TDIAG_N_STRONG] = c[0];
       td[SRW_TDIAG_N_BOUNDARY] = c[1];
@@ -2342,7 +2412,6 @@ __device__ __attribute__((always_inline)) inline void finalize_rows_body(const F
       td[SRW_TDIAG_N_BAND030] = c[3];
       td[SRW_TDIAG_N_INT_CAP] = c[4];
       td[SRW_TDIAG_G_LOG_G] = c[5];
-      td[SRW_TDIAG_INT_MAX] = imax;
     }
   }
 }
@@ -2366,9 +2435,11 @@ __global__ __launch_bounds__(256) void srw_finalize_rows_batch_kernel(Batch<Fina
 // order, the slices combine in LDS in slice order: the result is the same on
 // every call (the atomics it replaces summed in arrival order).
 // ---------------------------------------------------------------------------
+// gate_direct: the partials carry the max gate itself (the v4.0.1 gate, whose
+// z scale differs per row), not the max margin.
 __global__ __launch_bounds__(256) void srw_unit_diag_kernel(const float2* __restrict__ part, int64_t rows, int64_t N,
                                                             float* __restrict__ unit_diag, GateParams gp,
-                                                            float exp_scale) {
+                                                            float exp_scale, int gate_direct) {
   __shared__ float2 red[4][64];
   const int ul = threadIdx.x & 63, slice = threadIdx.x >> 6;
   const int64_t u = static_cast<int64_t>(blockIdx.x) * 64 + ul;
@@ -2400,7 +2471,8 @@ __global__ __launch_bounds__(256) void srw_unit_diag_kernel(const float2* __rest
       m = fmaxf(m, red[q][ul].y);
     }
     unit_diag[u * SRW_UDIAG_COUNT + SRW_UDIAG_SCORE_SUM] = s;
-    unit_diag[u * SRW_UDIAG_COUNT + SRW_UDIAG_GATE_MAX] = m > -INFINITY ? gate_of_margin(m - gp.thr, gp, exp_scale) : 0.f;
+    unit_diag[u * SRW_UDIAG_COUNT + SRW_UDIAG_GATE_MAX] =
+        !(m > -INFINITY) ? 0.f : (gate_direct ? m : gate_of_margin(m - gp.thr, gp, exp_scale));
   }
 }
 
@@ -2854,6 +2926,9 @@ template <int DB, int KH, bool HX, bool WS>
 Kernels kernels_of(bool dg, bool gl = false) {
   if constexpr (WS) {
     constexpr int lds = (2 * (KH + 2 * DB) + 2 * 2 * DB + 16) * kFragBytes;  // 2 E/R, 2 W^T, S
+    if (dg && gl)
+      return Kernels{srw_stats_kernel<KH, kStatsDiag, 1>, srw_stats_kernel<KH, kStatsChan, 1>,
+                     srw_main_ws_kernel<DB, KH, HX, true, true>, kWsThreads, lds};
     if (dg)
       return Kernels{srw_stats_kernel<KH, kStatsDiag, 1>, srw_stats_kernel<KH, kStatsChan, 1>,
                      srw_main_ws_kernel<DB, KH, HX, true>, kWsThreads, lds};
@@ -2870,9 +2945,8 @@ Kernels kernels_of(bool dg, bool gl = false) {
 
 // Instantiated shapes (d_model, d_route); for d_route == d_model there is a
 // variant whose score operand is the x registers themselves (h aliases x).
-// gl: the v4.0.1 GELU gate (warp-specialised kernels, no diagnostics).
+// gl: the v4.0.1 GELU gate (warp-specialised kernels).
 bool pick(int64_t D, int64_t dr, bool hx, bool dg, Kernels* k, bool gl = false) {
-  if (dg && gl) return false;
   if (hx && D == dr) {
     if (D == 384) { *k = kernels_of<12, 24, true, true>(dg, gl); return true; }
     if (D == 128) { *k = kernels_of<4, 8, true, true>(dg, gl); return true; }
@@ -3172,7 +3246,7 @@ FinalParams final_params_of(const FinalizeArgs& f);
 
 bool mfma_supports(const srw_desc_t& d, bool h_is_x) {
   if (d.dtype != SRW_BF16) return false;
-  const bool gl = d.gate == SRW_GATE_GELU_V401;  // the GELU gate runs without diagnostics here
+  const bool gl = d.gate == SRW_GATE_GELU_V401;
   if (d.stats_mode != SRW_STATS_ONEPASS && d.stats_mode != SRW_STATS_CENTERED &&
       !(d.stats_mode == SRW_STATS_GRAM && gram_supports(d.d_route)))
     return false;
@@ -3363,7 +3437,8 @@ hipError_t mfma_forward(const LaunchArgs& a, const char** path_name) {
   if (unit_part) {
     const int64_t rows = (g.T + 31) / 32;
     hipLaunchKernelGGL(srw_unit_diag_kernel, dim3(static_cast<unsigned>((d.n_units + 63) / 64)), dim3(256), 0,
-                       a.stream, unit_part, rows, static_cast<int64_t>(d.n_units), unit_diag, a.gp, f.exp_scale);
+                       a.stream, unit_part, rows, static_cast<int64_t>(d.n_units), unit_diag, a.gp, f.exp_scale,
+                       gl ? 1 : 0);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return hipSuccess;

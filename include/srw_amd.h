@@ -172,8 +172,8 @@ enum {
   SRW_TDIAG_N_BAND075,    /* #0.05 < act < 0.95 (v4.0.1: #0 < z < 0.75) */
   SRW_TDIAG_N_BAND030,    /* #0.2 < act < 0.8 (v4.0.1: #0 < z < 0.30) */
   SRW_TDIAG_G_LOG_G,      /* sum_n gate * log(gate + 1e-8) */
-  SRW_TDIAG_INT_MAX,      /* max_n intensity */
-  SRW_TDIAG_N_INT_CAP,    /* #intensity >= eps + max_intensity - 1e-3 */
+  SRW_TDIAG_INT_MAX,      /* max_n intensity (v4.0.1: 0) */
+  SRW_TDIAG_N_INT_CAP,    /* #intensity >= eps + max_intensity - 1e-3 (v4.0.1: 0) */
   SRW_TDIAG_COUNT
 };
 

@@ -114,3 +114,135 @@ def test_gelu_v401_den_floor_and_no_pass(pkg, dev):
     assert bool((got["gate_sum"][:, 0] == 0).all()) and bool((got["den"][:, 0] == 1).all())
     assert bool((got["out"].float() == 0).all())
     assert int(got["n_active"].sum()) == 0
+
+
+# ---------------------------------------------------------------- v4.0.1 diagnostics
+#
+# SRW_FLAG_DIAG with the GELU gate (the training forward of v401:230-367, whose
+# fused function always returns its diagnostics) on the matrix cores
+# (srw_main_ws_kernel<..., DG, GL>) and on the generic kernels, against the
+# oracle's trace.  Counts are thresholds on z (phi > 0.95 or < 0.05 <=> |z| >
+# Phi^-1(0.95); gate > 0.5 <=> z > z* with z* Phi(z*) = 0.5; the z bands), so
+# an element may fall on the other side of an edge only when its z lies
+# within the z-shift of one bf16 score ulp plus the tau / s_std slack: the
+# count difference is bounded by the number of such elements (+ 2).
+
+V401_DIAG_CASES = [
+    # T, D, dr, N, h_is_x, max_chunk, seed
+    (256, 384, 384, 6000, True, 2500, 61),    # h aliases x, two reference chunks
+    (200, 384, 128, 1580, False, 12500, 62),  # the model's router width, ragged T
+    (130, 128, 64, 1000, False, 300, 63),     # four chunks, chunk edges inside tiles
+]
+
+
+def _z_star():
+    """z* with z* Phi(z*) = 0.5 (gate > 0.5 <=> z > z*), by bisection in float64."""
+    lo, hi = 0.0, 3.0
+    for _ in range(80):
+        mid = 0.5 * (lo + hi)
+        v = mid * 0.5 * (1.0 + torch.erf(torch.tensor(mid / 2 ** 0.5, dtype=torch.float64)))
+        lo, hi = (mid, hi) if float(v) < 0.5 else (lo, mid)
+    return 0.5 * (lo + hi)
+
+
+def _check_v401_diag(got, tr, sc, T, N, label):
+    """token_diag [T,1,14] / unit_diag [N,2] of one call against the oracle
+    trace (z, gate, tau, s_std) and the oracle's bf16 scores sc [T, N]."""
+    td = got["token_diag"][:, 0].double()
+    z = tr["z"].reshape(T, N).double()
+    gate = tr["gate"].reshape(T, N).double()
+    s_std = tr["s_std"].reshape(T).double()
+    names = ["s_mean", "s_std", "tau", "sum_s3", "sum_s4", "gate_max", "int_sum", "n_strong",
+             "n_boundary", "n_band075", "n_band030", "g_log_g", "int_max", "n_int_cap"]
+    col = {n: i for i, n in enumerate(names)}
+    assert torch.allclose(td[:, col["s_mean"]], tr["s_mean"].reshape(T).double(), rtol=1e-4, atol=1e-5)
+    assert torch.allclose(td[:, col["s_std"]], s_std, rtol=1e-4, atol=1e-5)
+    assert torch.allclose(td[:, col["tau"]], tr["tau"].reshape(T).double(), rtol=1e-4, atol=1e-5)
+    sc = sc.double()
+    sens = (3 * sc.abs() ** 2 * bf16_ulp(sc)).sum(dim=-1)
+    d3 = (td[:, col["sum_s3"]] - (sc ** 3).sum(-1)).abs()
+    assert (d3 <= 0.02 * sens + 1e-5 * (sc.abs() ** 3).sum(-1)).all(), label
+    assert torch.allclose(td[:, col["gate_max"]], gate.amax(-1), rtol=2e-3, atol=1e-6), label
+    assert torch.allclose(td[:, col["int_sum"]], z.clamp_min(0).sum(-1), rtol=2e-3, atol=1e-4), label
+    mag = (gate * torch.log(gate + 1e-8)).abs().sum(-1)
+    d = (td[:, col["g_log_g"]] - (gate * torch.log(gate + 1e-8)).sum(-1)).abs()
+    assert (d <= 1e-3 + 2e-3 * mag).all(), label
+    assert bool((td[:, col["int_max"]] == 0).all()) and bool((td[:, col["n_int_cap"]] == 0).all())
+    # counts, with the tie band in z
+    dz = (bf16_ulp(sc) + 1e-4 * s_std[:, None]) / s_std[:, None] + 1e-5
+    zs, z95 = _z_star(), 1.6448536269514722
+    preds = {
+        "n_strong": (z > zs, (zs,)),
+        "n_boundary": (z.abs() > z95, (z95, -z95)),
+        "n_band075": ((z > 0) & (z < 0.75), (0.0, 0.75)),
+        "n_band030": ((z > 0) & (z < 0.30), (0.0, 0.30)),
+    }
+    for n, (pred, edges) in preds.items():
+        band = sum(((z - c).abs() <= dz).sum(-1) for c in edges)
+        diff = (td[:, col[n]] - pred.sum(-1)).abs()
+        print(f"  {label} {n}: max |diff| {float(diff.max())}, max band {int(band.max())}", flush=True)
+        assert (diff <= band + 2).all(), (label, n)
+    # per-unit score sums: a score may round to the neighbouring bf16 value
+    # (the two sides sum its products in another order, ~1 in 10^3): bound the
+    # difference by four of the unit's largest score ulps plus 2% of its
+    # summed ulps (a missing or repeated 32-row block moves a sum by ~32 |s|)
+    ud = got["unit_diag"].double()
+    d = (ud[:, 0] - sc.sum(0)).abs()
+    ulp = bf16_ulp(sc)
+    bound = 4 * ulp.amax(0) + 0.02 * ulp.sum(0) + 1e-5 * sc.abs().sum(0)
+    print(f"  {label} unit score_sum: max |diff| {float(d.max()):.3e}, max diff/bound "
+          f"{float((d / bound).max()):.3f}", flush=True)
+    assert (d <= bound).all(), label
+    assert torch.allclose(ud[:, 1], gate.amax(0), rtol=2e-3, atol=1e-5), label
+
+
+@pytest.mark.parametrize("case", V401_DIAG_CASES, ids=lambda c: "T{}D{}dr{}N{}{}c{}".format(
+    c[0], c[1], c[2], c[3], "x" if c[4] else "", c[5]))
+def test_gelu_v401_diagnostics_match_oracle(pkg, dev, case):
+    T, D, dr, N, hx, max_chunk, seed = case
+    print(f"[gpu] gelu v401 diagnostics {case}", flush=True)
+    inp = _inputs(pkg, T, D, dr, N, hx, seed, 0.0)
+    inp["tau_offset"].uniform_(-0.6, 1.2, generator=torch.Generator().manual_seed(seed))
+    _, cs = srw_ref.chunk_plan(N, max_chunk)
+    fast = _gpu(pkg, dev, inp, chunk_size=cs, stats="onepass", want_mask=True, diag=True)
+    plain = _gpu(pkg, dev, inp, chunk_size=cs, stats="onepass", want_mask=True)
+    slow = _gpu(pkg, dev, inp, chunk_size=cs, stats="onepass", want_mask=True, diag=True, emulate=True)
+    assert fast["path"] == "mfma_bf16" and plain["path"] == "mfma_bf16" and slow["path"] == "generic"
+    # diagnostics leave the forward's results unchanged, bit for bit
+    for k in ("out", "gate_sum", "den", "n_active", "pass_mask"):
+        assert torch.equal(fast[k], plain[k]), k
+    x = inp["x"][None]
+    h = x if hx else inp["h"][:, 0][None]
+    ref, tr = srw_ref.fused_gate_srw_gelu_v401(x, h, inp["emb"], inp["tau_offset"][None], inp["read"],
+                                               inp["write"], max_chunk_size=max_chunk, return_trace=True)
+    _check_common(fast, ref[0], tr["z"], tr["s_std"], tr["tau"], tr["gate_sum"], tr["den"], T, N, D)
+    hh = (inp["x"] if hx else inp["h"][:, 0]).to(BF).float()
+    sc = (hh @ inp["emb"].to(BF).float().T).to(BF).float()       # bf16 scores (v401:251)
+    _check_v401_diag(fast, tr, sc, T, N, "mfma")
+    _check_v401_diag(slow, tr, sc, T, N, "generic")
+
+
+@pytest.mark.parametrize("hx", [False, True], ids=["router_h", "h_is_x"])
+def test_dropin_v401_16_tuple(pkg, dev, hx):
+    """make_sharded_srw_v401 (v401:194-369) against the oracle's 16-tuple."""
+    B, S, D, N = 2, 40, 128, 1200
+    dr = D if hx else 64
+    print(f"[gpu] drop-in v401 16-tuple B{B} S{S} D{D} dr{dr} N{N} hx={hx}", flush=True)
+    inp = _inputs(pkg, B * S, D, dr, N, hx, 71, 0.0)
+    inp["tau_offset"].uniform_(-0.5, 1.0, generator=torch.Generator().manual_seed(71))
+    x = inp["x"].reshape(B, S, D)
+    h = x if hx else inp["h"].reshape(B, S, dr)
+    tau = inp["tau_offset"].reshape(B, S, 1)
+    fn = pkg.make_sharded_srw_v401(None, max_chunk_size=500)
+    xd = x.to(dev)
+    got = fn(xd, xd if hx else h.to(dev), inp["emb"].to(dev), tau.to(dev), inp["read"].to(dev),
+             inp["write"].to(dev))
+    torch.cuda.synchronize()
+    ref = srw_ref.fused_gate_srw_gelu_v401(x, h, inp["emb"], tau, inp["read"], inp["write"],
+                                           max_chunk_size=500)
+    assert len(got) == 16
+    assert rel_fro(got[0].cpu(), ref[0]) <= REL_BF16
+    for i, name in enumerate(srw_ref.FUSED_V401_OUTPUT_NAMES[1:], start=1):
+        g, r = got[i].detach().cpu().float(), ref[i].float()
+        assert g.shape == r.shape, name
+        assert torch.allclose(g, r, rtol=2e-2, atol=2e-3), (name, g, r)
