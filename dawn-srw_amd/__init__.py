@@ -14,11 +14,12 @@ The directory name is not a Python identifier; load the package with
 from ._capi import SrwError, SrwLibraryError, load_library  # noqa: F401
 from .layer import GateConfig, SrwBackwardPlan, SrwBatchPlan, SrwPlan, srw_backward, srw_forward  # noqa: F401
 from .srw import (chunk_plan, make_sharded_srw, make_sharded_srw_paired, make_sharded_srw_v401,  # noqa: F401
-                  srw_inference, srw_inference_with_gates)
+                  make_sharded_srw_paired_v401, srw_inference, srw_inference_with_gates)
 from . import checkpoint, data, inputs, model  # noqa: F401
 from .model import DawnConfig, DawnModel, init_params  # noqa: F401
 
 __all__ = ["SrwError", "SrwLibraryError", "load_library", "GateConfig",
-           "SrwPlan", "SrwBatchPlan", "SrwBackwardPlan", "srw_forward", "srw_backward", "chunk_plan", "make_sharded_srw",
-           "make_sharded_srw_paired", "make_sharded_srw_v401", "srw_inference", "srw_inference_with_gates",
+           "SrwPlan", "SrwBatchPlan", "SrwBackwardPlan", "srw_forward", "srw_backward", "chunk_plan",
+           "make_sharded_srw", "make_sharded_srw_paired", "make_sharded_srw_v401",
+           "make_sharded_srw_paired_v401", "srw_inference", "srw_inference_with_gates",
            "inputs", "model", "checkpoint", "data", "DawnConfig", "DawnModel", "init_params"]

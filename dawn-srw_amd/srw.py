@@ -10,9 +10,10 @@ Reference (madst0614/DAWN-SRW, models/dawn_spatial_v41_exp.py):
   (h [B,S,2,dr], tau_offset [B,S,2,1], out [B,S,2,D]).
 * ``_srw_inference(x, h, emb_norm, tau_offset, w_read, w_write)``
   (:1713-1738) -> out (dtype-preserving, two-pass centred std).
-* The v4.0.1 ``make_sharded_srw(mesh, max_chunk_size=2048)``
-  (models/legacy/dawn_spatial_v401_exp.py:194-369, GELU gate) as
-  ``make_sharded_srw_v401`` -> 16-tuple (forward only).
+* The v4.0.1 ``make_sharded_srw(mesh, max_chunk_size=2048)`` and
+  ``make_sharded_srw_paired`` (models/legacy/dawn_spatial_v401_exp.py:
+  194-554, GELU gate) as ``make_sharded_srw_v401`` /
+  ``make_sharded_srw_paired_v401`` -> 16-tuple (forward only).
 
 The factories return functions with the same positional signature and the
 same 22-tuple order, so they slot into ``sharded_fns = (fused_single,
@@ -39,7 +40,7 @@ from .layer import GateConfig, srw_backward, srw_forward
 from . import _capi as C
 
 __all__ = ["make_sharded_srw", "make_sharded_srw_paired", "make_sharded_srw_v401",
-           "srw_inference", "chunk_plan", "GateConfig"]
+           "make_sharded_srw_paired_v401", "srw_inference", "chunk_plan", "GateConfig"]
 
 _TD = C.TDIAG_INDEX
 
@@ -225,57 +226,65 @@ def make_sharded_srw_paired(mesh=None, max_chunk_size=2048, dead_threshold=0.01,
                  activation_threshold, activation_cutoff, epsilon, max_intensity)
 
 
-def _diag_tuple_v401(res, N, B, S):
+def _diag_tuple_v401(res, N, B, S, R=1):
     """The v4.0.1 diagnostics (models/legacy/dawn_spatial_v401_exp.py:
-    343-367), one route: [T]- and [N]-sized kernel reductions -> the
-    reference's 15 values after out.  token_diag's INT_SUM column holds the
-    sum of z+ and its band / boundary / strong columns the v4.0.1 counts
-    (include/srw_amd.h)."""
-    td = res["token_diag"][:, 0]
-    g = res["gate_sum"][:, 0]                   # [T]
-    na = res["n_active"][:, 0].to(torch.float32)
-    col = lambda k: td[:, _TD[k]]               # noqa: E731
+    343-367 single, :525-553 paired): [T,R]- and [N]-sized kernel reductions
+    -> the reference's 15 values after out.  token_diag's INT_SUM column
+    holds the sum of z+ and its band / boundary / strong columns the v4.0.1
+    counts (include/srw_amd.h).  Per-token outputs keep the [B,S,1] shape,
+    averaged over the routes when R == 2 (:525-538); every scalar is over
+    the (token, route) rows."""
+    td = res["token_diag"]
+    g = res["gate_sum"]                         # [T,R]
+    na = res["n_active"].to(torch.float32)
+    col = lambda k: td[..., _TD[k]]             # noqa: E731
     s_mean, s_std, tau = col("s_mean"), col("s_std"), col("tau")
     n_tot = float(N)
-    bs1 = lambda v: v.reshape(B, S, 1)          # noqa: E731
-    # skewness from the raw third moment (v401:276-279)
+
+    def per_token(v):                           # [T,R] -> [B,S,1]
+        return v.mean(dim=1).reshape(B, S, 1) if R == 2 else v.reshape(B, S, 1)
+
+    # skewness from the raw third moment (v401:276-279, :455-458)
     cube_mean = col("sum_s3") / n_tot
     central_third = cube_mean - 3.0 * s_mean * (s_std ** 2) - s_mean ** 3
     skew = (central_third / (s_std ** 3 + 1e-8)).mean()
-    # score LB: variance of the per-unit mean score (v401:257-260, 281-289)
-    per_neuron = res["unit_diag"][:, 0] / float(B * S)
+    # score LB: variance of the per-unit mean score over every (token, route)
+    # row (v401:257-260, 281-289; :436)
+    per_neuron = res["unit_diag"][:, 0] / float(B * S * R)
     mean_score = per_neuron.sum() / n_tot
     var_score = (per_neuron ** 2).sum() / n_tot - mean_score ** 2
     score_lb = var_score / (mean_score ** 2 + var_score + 1e-2)
-    # gate entropy (v401:360-363)
+    # gate entropy (v401:360-363, :545-548)
     gse = g + 1e-8
     ent = -col("g_log_g") / gse + torch.log(gse)
     act_eps = na + 1e-8
-    return (bs1(na / n_tot), bs1(col("gate_max")), score_lb, s_std.mean(), g.mean(), na.mean(),
-            bs1(col("n_strong") / n_tot), bs1(col("n_boundary") / n_tot),
-            bs1(col("int_sum") / act_eps), tau.mean(),
+    return (per_token(na / n_tot), per_token(col("gate_max")), score_lb, s_std.mean(), g.mean(), na.mean(),
+            per_token(col("n_strong") / n_tot), per_token(col("n_boundary") / n_tot),
+            per_token(col("int_sum") / act_eps), tau.mean(),
             (col("n_band075") / act_eps).mean(), (col("n_band030") / act_eps).mean(),
             skew, na.std(correction=0), ent.mean())
 
 
 class _FusedSrwV401(torch.autograd.Function):
-    """The v4.0.1 fused_gate_srw (v401:230-367) as an autograd node whose
-    backward is not implemented (the VJP here covers the v4.1 gate)."""
+    """The v4.0.1 fused_gate_srw(_paired) (v401:230-367, :408-554) as an
+    autograd node whose backward is not implemented (the VJP here covers the
+    v4.1 gate)."""
 
     @staticmethod
-    def forward(ctx, x, h, emb, tau_offset, read, write, cs):
+    def forward(ctx, x, h, emb, tau_offset, read, write, routes, cs):
         B, S, D = x.shape
         N = emb.shape[0]
         bf = torch.bfloat16
         xb = x.reshape(B * S, D).to(bf).contiguous()                       # v401:238-242
-        hb = h.reshape(B * S, 1, h.shape[-1]).to(bf).contiguous()
-        tau = tau_offset.reshape(B * S, 1).to(torch.float32).contiguous()
+        hb = h.reshape(B * S, routes, h.shape[-1]).to(bf).contiguous()
+        tau = tau_offset.reshape(B * S, routes).to(torch.float32).contiguous()
         eb, rdb, wb = (t.to(bf).contiguous() for t in (emb, read, write))
-        h_call = xb if h is x else hb
+        h_call = xb if (h is x and routes == 1) else hb
         res = srw_forward(xb, h_call, eb, tau, rdb, wb, gate="gelu_v401", stats="onepass",
                           chunk_size=cs, diag=True, want_mask=False)
-        out = res["out"].reshape(B, S, D).to(torch.float32)
-        outs = (out,) + _diag_tuple_v401(res, N, B, S)
+        shape = (B, S, D) if routes == 1 else (B, S, 2, D)
+        out = res["out"].reshape(shape).to(torch.float32)
+        outs = (out,) + _diag_tuple_v401(res, N, B, S, routes)
         ctx.mark_non_differentiable(*outs[1:])
         return outs
 
@@ -285,22 +294,35 @@ class _FusedSrwV401(torch.autograd.Function):
                                   "implemented; srw_backward covers the v4.1 gate")
 
 
+def _make_v401(routes, mesh, max_chunk_size):
+    _check_mesh(mesh)
+
+    def fused(x, h, emb, tau_offset, read, write):
+        _, cs = chunk_plan(emb.shape[0], max_chunk_size)                  # v401:231-235
+        return _FusedSrwV401.apply(x, h, emb, tau_offset, read, write, routes, cs)
+
+    fused.__name__ = "fused_gate_srw" if routes == 1 else "fused_gate_srw_paired"
+    return fused
+
+
 def make_sharded_srw_v401(mesh=None, max_chunk_size=2048):
     """The v4.0.1 ``make_sharded_srw(mesh, max_chunk_size=2048)``
     (models/legacy/dawn_spatial_v401_exp.py:194-369): returns
     ``fused_gate_srw(x, h, emb, tau_offset, read, write)`` -> the 16-tuple
     (out, active_frac, gate_max, score_lb, score_std, gate_sum, active_n_mean,
     strong_frac, phi_binary_frac, z_mean_active, tau_abs_mean, z_lt_075_frac,
-    z_lt_030_frac, score_skew, active_per_token_std, gate_entropy).  One
-    route; inputs cast to bf16 (v401:238-242), one-pass statistics, R and W
-    rows forward-normalised per chunk (v401:300-301)."""
-    _check_mesh(mesh)
+    z_lt_030_frac, score_skew, active_per_token_std, gate_entropy).  Inputs
+    cast to bf16 (v401:238-242), one-pass statistics, R and W rows
+    forward-normalised per chunk (v401:300-301).  Forward only."""
+    return _make_v401(1, mesh, max_chunk_size)
 
-    def fused_gate_srw(x, h, emb, tau_offset, read, write):
-        _, cs = chunk_plan(emb.shape[0], max_chunk_size)                  # v401:231-235
-        return _FusedSrwV401.apply(x, h, emb, tau_offset, read, write, cs)
 
-    return fused_gate_srw
+def make_sharded_srw_paired_v401(mesh=None, max_chunk_size=2048):
+    """The v4.0.1 ``make_sharded_srw_paired(mesh, max_chunk_size=2048)``
+    (v401:372-554): h [B,S,2,dr], tau_offset [B,S,2,1] -> the 16-tuple with
+    out [B,S,2,D] and the per-token outputs averaged over the two routes;
+    x.R^T shared by both routes.  Forward only."""
+    return _make_v401(2, mesh, max_chunk_size)
 
 
 def srw_inference(x, h, emb_norm, tau_offset, w_read, w_write, *,

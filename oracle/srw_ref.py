@@ -31,6 +31,7 @@ __all__ = [
     "srw_inference", "srw_inference_with_gates",
     "fused_gate_srw", "fused_gate_srw_paired",
     "srw_inference_gelu_v401", "fused_gate_srw_gelu_v401",
+    "fused_gate_srw_gelu_v401_paired",
     "FUSED_OUTPUT_NAMES", "FUSED_V401_OUTPUT_NAMES",
 ]
 
@@ -555,6 +556,84 @@ def fused_gate_srw_gelu_v401(x, h, emb, tau_offset, read, write, *,
         out_f, act_n / N, gmax, st["score_lb"], s_std.mean(), wsum.mean(),
         act_n.mean(), strong / N, phi_bin / N, zsum / (act_n + 1e-8), tau.mean(),
         (z075 / (act_n + 1e-8)).mean(), (z030 / (act_n + 1e-8)).mean(),
+        st["score_skew"], act_n.std(correction=0), ent.mean(),
+    )
+    if not return_trace:
+        return res
+    return res, dict(s_mean=s_mean, s_std=s_std, tau=tau, den=den,
+                     gate_sum=wsum, n_active=act_n, raw_out=out,
+                     z=torch.cat(trace_z, dim=-1), gate=torch.cat(trace_gate, dim=-1),
+                     nc=nc, cs=cs)
+
+
+def fused_gate_srw_gelu_v401_paired(x, h, emb, tau_offset, read, write, *,
+                                    max_chunk_size: int = 2048, return_trace=False,
+                                    exact: bool = False):
+    """v4.0.1 ``fused_gate_srw_paired`` (v401:408-554), 1x1 mesh -> 16-tuple.
+
+    x [B,S,D], h [B,S,2,dr], tau_offset [B,S,2,1].  Statistics per (token,
+    route) row (v401:426-457); x @ R_norm^T once per chunk, shared by both
+    routes (v401:496-497); per-token outputs averaged over the route axis
+    (v401:532-541); every scalar over (B, S, 2), per-unit score means over
+    (B, S, 2) for score_lb (v401:436).  ``exact`` as in
+    ``fused_gate_srw_gelu_v401``.
+    """
+    N = emb.shape[0]
+    nc, cs = chunk_plan(N, max_chunk_size)                         # v401:409-413
+    B, S, D = x.shape
+    R = h.shape[2]
+    acc = F64 if exact else F32
+    if exact:
+        h_bf, x_bf, emb_bf, read_bf, write_bf = (t.to(F64) for t in (h, x, emb, read, write))
+        dot = lambda a, b: a @ b.T                                 # noqa: E731
+        rnd = lambda t: t                                          # noqa: E731
+    else:
+        h_bf, x_bf, emb_bf, read_bf, write_bf = _prepare(x, h, emb, read, write)  # v401:416-420
+        dot = lambda a, b: dot_bf16(a.to(BF16), b.to(BF16)).to(F32)  # noqa: E731
+        rnd = bf16_round
+    st = _pass1_stats(h_bf, emb_bf, nc, cs, N, route_axis=True, exact=exact)
+    s_mean, s_std = st["s_mean"], st["s_std"]                      # [B,S,2,1]
+    tau = s_mean + tau_offset.to(acc) * s_std                      # v401:453
+    z1 = torch.zeros(B, S, R, 1, dtype=acc)
+    out = torch.zeros(B, S, R, D, dtype=acc)
+    wsum, gmax = z1.clone(), torch.full((B, S, R, 1), -1e9, dtype=acc)
+    act_n, strong, phi_bin, zsum = z1.clone(), z1.clone(), z1.clone(), z1.clone()
+    z075, z030, glogg = z1.clone(), z1.clone(), z1.clone()
+    trace_z, trace_gate = [], []
+    for i in range(nc):                                            # v401:471-514
+        sl = slice(i * cs, (i + 1) * cs)
+        ec = emb_bf[sl]
+        rc = _norm_rows(read_bf[sl])                               # v401:479
+        wc = _norm_rows(write_bf[sl])                              # v401:480
+        scores = dot(h_bf, ec)                                     # v401:481 [B,S,2,cs]
+        raw = scores - tau                                         # v401:482
+        z, phi, gate = gate_gelu_v401(raw, s_std)                  # v401:483-485
+        gate_bf = rnd(gate)                                        # v401:486
+        xr = dot(x_bf, rc)                                         # v401:487 [B,S,cs], shared
+        prod = rnd(gate_bf * xr[:, :, None, :])                    # v401:488 bf16 multiply
+        out = out + dot(prod, wc.T.contiguous())                   # v401:488 bf16 dot, as f32
+        wsum = wsum + gate.sum(dim=-1, keepdim=True)               # v401:489
+        act_n = act_n + (gate > 0.0).to(acc).sum(dim=-1, keepdim=True)
+        strong = strong + (gate > 0.5).to(acc).sum(dim=-1, keepdim=True)
+        phi_bin = phi_bin + ((phi > 0.95) | (phi < 0.05)).to(acc).sum(dim=-1, keepdim=True)
+        zsum = zsum + torch.where(z > 0, z, torch.zeros((), dtype=acc)).sum(dim=-1, keepdim=True)
+        z075 = z075 + ((z > 0) & (z < 0.75)).to(acc).sum(dim=-1, keepdim=True)
+        z030 = z030 + ((z > 0) & (z < 0.30)).to(acc).sum(dim=-1, keepdim=True)
+        glogg = glogg + (gate * torch.log(gate + 1e-8)).sum(dim=-1, keepdim=True)  # v401:496-497
+        gmax = torch.maximum(gmax, gate.amax(dim=-1, keepdim=True))
+        if return_trace:
+            trace_z.append(z)
+            trace_gate.append(gate)
+    den = _v401_den(wsum, zsum)                                    # v401:521-522, per route
+    out_f = rnd(out / den)                                         # v401:523-524
+    act_eps = act_n + 1e-8
+    gate_sum_eps = wsum + 1e-8                                     # v401:546
+    ent = -glogg / gate_sum_eps + torch.log(gate_sum_eps)
+    res = (
+        out_f, _route_mean(act_n / N), _route_mean(gmax), st["score_lb"], s_std.mean(),
+        wsum.mean(), act_n.mean(), _route_mean(strong / N), _route_mean(phi_bin / N),
+        _route_mean(zsum / act_eps), tau.mean(),                   # v401:526-543
+        (z075 / act_eps).mean(), (z030 / act_eps).mean(),
         st["score_skew"], act_n.std(correction=0), ent.mean(),
     )
     if not return_trace:

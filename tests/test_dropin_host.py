@@ -77,3 +77,26 @@ def test_v401_16_tuple_assembly_matches_oracle(pkg):
         r_ = torch.as_tensor(r_, dtype=F64)
         assert g.shape == r_.shape, name
         assert torch.allclose(g, r_, rtol=1e-6, atol=1e-9), (name, g, r_)
+
+
+def test_v401_paired_16_tuple_assembly_matches_oracle(pkg):
+    """The two-route form (v401:525-553): per-token outputs averaged over
+    the routes, scalars over every (token, route) row."""
+    B, S, D, dr, N = 2, 5, 12, 8, 72
+    x, h, e, tau, r, w = _inputs(B, S, D, dr, N, seed=72)
+    g = torch.Generator().manual_seed(73)
+    h2 = torch.stack([h, torch.randn(B, S, dr, generator=g, dtype=F64)], dim=2)      # [B,S,2,dr]
+    tau2 = torch.stack([tau, tau - 0.3], dim=2)                                       # [B,S,2,1]
+    ref, tr = srw_ref.fused_gate_srw_gelu_v401_paired(x, h2, e, tau2, r, w, max_chunk_size=24,
+                                                      exact=True, return_trace=True)
+    T = B * S
+    cols = _kernel_columns({k: (v.reshape(2 * T, *v.shape[3:]) if torch.is_tensor(v) and v.dim() == 4 else v)
+                            for k, v in tr.items()}, h2.reshape(2 * T, 1, dr), e, 2 * T, 1, N)
+    res = dict(token_diag=cols["token_diag"].reshape(T, 2, 14), unit_diag=cols["unit_diag"],
+               gate_sum=cols["gate_sum"].reshape(T, 2), n_active=cols["n_active"].reshape(T, 2))
+    got = pkg.srw._diag_tuple_v401(res, N, B, S, 2)
+    for name, g_, r_ in zip(srw_ref.FUSED_V401_OUTPUT_NAMES[1:], got, ref[1:]):
+        g_ = torch.as_tensor(g_, dtype=F64)
+        r_ = torch.as_tensor(r_, dtype=F64)
+        assert g_.shape == r_.shape, name
+        assert torch.allclose(g_, r_, rtol=1e-6, atol=1e-9), (name, g_, r_)

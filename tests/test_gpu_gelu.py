@@ -246,3 +246,34 @@ def test_dropin_v401_16_tuple(pkg, dev, hx):
         g, r = got[i].detach().cpu().float(), ref[i].float()
         assert g.shape == r.shape, name
         assert torch.allclose(g, r, rtol=2e-2, atol=2e-3), (name, g, r)
+
+
+def test_dropin_v401_paired_16_tuple(pkg, dev):
+    """make_sharded_srw_paired_v401 (v401:372-554) against the oracle's paired
+    16-tuple; the call runs on the matrix cores (two routes, GELU gate,
+    diagnostics)."""
+    B, S, D, dr, N = 2, 40, 128, 64, 1200
+    print(f"[gpu] drop-in v401 paired 16-tuple B{B} S{S} D{D} dr{dr} N{N}", flush=True)
+    shape = pkg.inputs.PoolShape(T=B * S, D=D, N=N, dr=dr, routes=2, h_is_x=False)
+    inp = pkg.inputs.make_pool_inputs(shape, seed=81)
+    inp["tau_offset"].uniform_(-0.5, 1.0, generator=torch.Generator().manual_seed(81))
+    x = inp["x"].reshape(B, S, D)
+    h = inp["h"].reshape(B, S, 2, dr)
+    tau = inp["tau_offset"].reshape(B, S, 2, 1)
+    fn = pkg.make_sharded_srw_paired_v401(None, max_chunk_size=500)
+    got = fn(x.to(dev), h.to(dev), inp["emb"].to(dev), tau.to(dev), inp["read"].to(dev), inp["write"].to(dev))
+    torch.cuda.synchronize()
+    ref = srw_ref.fused_gate_srw_gelu_v401_paired(x, h, inp["emb"], tau, inp["read"], inp["write"],
+                                                  max_chunk_size=500)
+    assert len(got) == 16 and got[0].shape == (B, S, 2, D)
+    assert rel_fro(got[0].cpu(), ref[0]) <= REL_BF16
+    for i, name in enumerate(srw_ref.FUSED_V401_OUTPUT_NAMES[1:], start=1):
+        g, r = got[i].detach().cpu().float(), ref[i].float()
+        assert g.shape == r.shape, name
+        assert torch.allclose(g, r, rtol=2e-2, atol=2e-3), (name, g, r)
+    # the same call through srw_forward names its kernel family
+    _, cs = srw_ref.chunk_plan(N, 500)
+    res = pkg.srw_forward(inp["x"].to(BF).to(dev), inp["h"].to(BF).to(dev), inp["emb"].to(BF).to(dev),
+                          inp["tau_offset"].to(dev), inp["read"].to(BF).to(dev), inp["write"].to(BF).to(dev),
+                          gate="gelu_v401", stats="onepass", chunk_size=cs, diag=True, want_mask=False)
+    assert res["path"] == "mfma_bf16"

@@ -651,3 +651,66 @@ def test_gate_norm_floor():
     assert torch.equal(gnorm, gate / 1e-8)
     assert _gate_norm_matches_brute(gnorm, x, h, e, tau, r, w)
     assert not _gate_norm_matches_brute(gate / gate.sum(-1, keepdim=True), x, h, e, tau, r, w)
+
+
+# ---------------------------------------------------------------- v4.0.1 paired function
+#
+# fused_gate_srw_gelu_v401_paired (v401:408-554) against ONE single-route call
+# (fused_gate_srw_gelu_v401, pinned above against brute force, closed forms and
+# scipy) over the 2*B*S virtual rows (token t, route r) -> row (s, r) of a
+# [B, 2S] batch with x repeated per route, in exact arithmetic: every statistic
+# of the paired function is per (token, route) row over N (v401:426-457), so
+# that single call holds every row of it, and its reductions fix the paired
+# ones -- out route by route (den per route, v401:521-524); the active / gate
+# max / strong / boundary fractions and z_mean_active as route means
+# (v401:525-538); every scalar over (B, S, 2), score_lb from per-unit means
+# over (B, S, 2) (v401:436).
+
+_V401_PAIRED_ROUTE_MEAN = ("active_frac", "gate_max", "strong_frac", "boundary_frac", "z_mean_active")
+
+
+def _v401_paired_vs_single_mismatch(seed=23):
+    B, S, D, dr, N = 2, 6, 24, 16, 360
+    x, h, e, tau, r, w = _v401_inputs(seed, T=B * S, D=D, dr=dr, N=N, tau=0.1)
+    g = torch.Generator().manual_seed(seed + 1)
+    h2 = torch.stack([h, torch.randn(B * S, dr, generator=g, dtype=F64)], dim=1)   # [T, 2, dr]
+    tau2 = torch.stack([tau, tau + 0.4], dim=1)                                   # [T, 2, 1]
+    pr = srw_ref.fused_gate_srw_gelu_v401_paired(x.reshape(B, S, D), h2.reshape(B, S, 2, dr), e,
+                                                 tau2.reshape(B, S, 2, 1), r, w, max_chunk_size=90,
+                                                 exact=True)
+    xs = x.reshape(B, S, 1, D).expand(B, S, 2, D).reshape(B, 2 * S, D)
+    sg = srw_ref.fused_gate_srw_gelu_v401(xs, h2.reshape(B, 2 * S, dr), e, tau2.reshape(B, 2 * S, 1), r, w,
+                                          max_chunk_size=90, exact=True)
+    P = dict(zip(srw_ref.FUSED_V401_OUTPUT_NAMES, pr))
+    Q = dict(zip(srw_ref.FUSED_V401_OUTPUT_NAMES, sg))
+    bad = []
+    for name in srw_ref.FUSED_V401_OUTPUT_NAMES:
+        p, q = P[name], Q[name]
+        if name == "out":
+            q = q.reshape(B, S, 2, D)
+        elif name in _V401_PAIRED_ROUTE_MEAN:
+            q = q.reshape(B, S, 2, 1).mean(dim=2)
+        if p.shape != q.shape or not torch.allclose(p, q, rtol=1e-10, atol=1e-12):
+            bad.append(name)
+    return bad
+
+
+def test_v401_paired_equals_one_single_over_route_rows():
+    assert _v401_paired_vs_single_mismatch() == []
+
+
+V401_PAIRED_MUTATIONS = {
+    # per-unit score means per route (over (B, S) only) for score_lb
+    "score_lb_per_route": ("_unit_means", lambda s, axes: s.mean(dim=axes[:2]), "score_lb"),
+    # per-token fractions of route 0 instead of the route mean
+    "active_frac_unaveraged": ("_route_mean", lambda t: t[:, :, 0], "active_frac"),
+    # one den for both routes (the routes' gate sums added)
+    "den_over_routes": ("_v401_den", lambda g, zp: torch.clamp_min(g.sum(dim=-2, keepdim=True), 1.0), "out"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(V401_PAIRED_MUTATIONS))
+def test_planted_v401_paired_mistakes_are_caught(monkeypatch, name):
+    attr, fn, field = V401_PAIRED_MUTATIONS[name]
+    monkeypatch.setattr(srw_ref, attr, fn)
+    assert field in _v401_paired_vs_single_mismatch()
