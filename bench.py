@@ -125,12 +125,12 @@ def host_cpus() -> dict:
 
 
 def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: bool = False,
-                 f32_inference: bool = False) -> dict:
+                 f32_inference: bool = False, gate: str = "v41") -> dict:
     """The oracle's fused_gate_srw (bf16 emulation) -- or, with ``backward``,
-    its hand-written VJP; with ``f32_inference`` its fp32 srw_inference --
-    on a token sample of the same pool, timed on the host cores (test
-    infrastructure as the timed CPU restatement; never part of the GPU
-    path)."""
+    its hand-written VJP; with ``f32_inference`` its fp32 srw_inference;
+    with ``gate`` "gelu_v401" the v4.0.1 forms of these -- on a token sample
+    of the same pool, timed on the host cores (test infrastructure as the
+    timed CPU restatement; never part of the GPU path)."""
     import torch
     from oracle import srw_ref, srw_vjp
 
@@ -150,7 +150,21 @@ def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: b
     elif f32_inference and shape.routes == 1:
         what = "srw_inference fp32"
         h = x if shape.h_is_x else inp["h"][:T_s, 0]
-        fn = lambda: srw_ref.srw_inference(x, h, inp["emb"], tau, inp["read"], inp["write"])  # noqa: E731
+        ref_fn = srw_ref.srw_inference_gelu_v401 if gate == "gelu_v401" else srw_ref.srw_inference
+        if gate == "gelu_v401":
+            what = "srw_inference_gelu_v401 fp32"
+        fn = lambda: ref_fn(x, h, inp["emb"], tau, inp["read"], inp["write"])  # noqa: E731
+    elif gate == "gelu_v401":
+        what = "fused_gate_srw_gelu_v401" + ("_paired" if shape.routes == 2 else "")
+        if shape.routes == 1:
+            h = x if shape.h_is_x else inp["h"][:T_s, 0]
+            fn = lambda: srw_ref.fused_gate_srw_gelu_v401(  # noqa: E731
+                x[None], h[None], inp["emb"], tau[None], inp["read"], inp["write"], max_chunk_size=chunk)
+        else:
+            h = inp["h"][:T_s]
+            fn = lambda: srw_ref.fused_gate_srw_gelu_v401_paired(  # noqa: E731
+                x[None], h[None], inp["emb"], tau.reshape(1, T_s, 2, 1), inp["read"], inp["write"],
+                max_chunk_size=chunk)
     elif shape.routes == 1:
         h = x if shape.h_is_x else inp["h"][:T_s, 0]
         fn = lambda: srw_ref.fused_gate_srw(  # noqa: E731
@@ -687,6 +701,9 @@ def main() -> int:
     if args.dtype == "f32" and (args.workload in ("decode", "qkv", "model") or args.backward or args.tiled):
         print("bench.py: --dtype f32 times the single-pool forward", file=sys.stderr)
         return 2
+    if args.gate == "gelu_v401" and args.backward:
+        print("bench.py: the backward covers the v4.1 gate only", file=sys.stderr)
+        return 2
     if args.cold and (args.graph or args.workload in ("decode", "qkv", "model")):
         print("bench.py: --cold times single eager calls of one pool", file=sys.stderr)
         return 2
@@ -905,7 +922,7 @@ def main() -> int:
     if args.cpu_seconds > 0:
         torch.set_num_threads(min(os.cpu_count() or 1, CPU_THREADS_MAX))
         cpu = cpu_baseline(pkg, shape, inp, tau_value, max_chunk, args.cpu_seconds, args.backward,
-                           f32_inference=args.dtype == "f32" and args.stats == "centered")
+                           f32_inference=args.dtype == "f32" and args.stats == "centered", gate=args.gate)
 
     value = T / (step_ms * 1e-3)
     line = {
