@@ -139,7 +139,19 @@ def cpu_baseline(pkg, shape, inp, tau_value, chunk, budget_s: float, backward: b
     x = inp["x"][:T_s]
     tau = torch.full((T_s, shape.routes), tau_value)
     what = "fused_gate_srw"
-    if backward:
+    if backward and gate == "gelu_v401":
+        what = "fused_gate_srw_gelu_v401 VJP (torch autograd through oracle/srw_ref.py)"
+        bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+        h0 = x if shape.h_is_x else inp["h"][:T_s, 0]
+        d_out = torch.randn(T_s, shape.D, generator=torch.Generator().manual_seed(1))
+
+        def fn():
+            xl, el, rl, wl = (bf(t).requires_grad_(True) for t in (x, inp["emb"], inp["read"], inp["write"]))
+            hl = xl if shape.h_is_x else bf(h0).requires_grad_(True)
+            tl = tau.clone().requires_grad_(True)
+            res = srw_ref.fused_gate_srw_gelu_v401(xl[None], hl[None], el, tl[None], rl, wl, max_chunk_size=chunk)
+            ((res[0][0] * d_out).sum() + 1e-2 * res[3]).backward()
+    elif backward:
         what = "fused_gate_srw VJP (oracle/srw_vjp.py)"
         bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
         h = x if shape.h_is_x else inp["h"][:T_s, 0]
@@ -701,9 +713,6 @@ def main() -> int:
     if args.dtype == "f32" and (args.workload in ("decode", "qkv", "model") or args.backward or args.tiled):
         print("bench.py: --dtype f32 times the single-pool forward", file=sys.stderr)
         return 2
-    if args.gate == "gelu_v401" and args.backward:
-        print("bench.py: the backward covers the v4.1 gate only", file=sys.stderr)
-        return 2
     if args.cold and (args.graph or args.workload in ("decode", "qkv", "model")):
         print("bench.py: --cold times single eager calls of one pool", file=sys.stderr)
         return 2
@@ -777,12 +786,16 @@ def main() -> int:
         if not args.no_residuals:
             # the drop-in's training path: its forward (with diagnostics)
             # hands the backward its den and unit statistics
-            fplan = pkg.SrwPlan(*plan.inputs[:6], stats=args.stats, chunk_size=cs, want_mask=False, diag=True)
+            fplan = pkg.SrwPlan(*plan.inputs[:6], stats=args.stats, chunk_size=cs, want_mask=False, diag=True,
+                                gate=args.gate)
             fplan.launch(stream)
             torch.cuda.synchronize()
             den, unit_diag = fplan.den, fplan.unit_diag
+        # the v4.0.1 function has no dead_penalty (its cotangent stays 0)
+        d_pen = 0.0 if args.gate == "gelu_v401" else 1e-2
         bplan = pkg.SrwBackwardPlan(x, h, plan.inputs[2], plan.inputs[3], plan.inputs[4],
-                                    plan.inputs[5], plan.out, d_out, 1e-2, 1e-2, den=den, unit_diag=unit_diag)
+                                    plan.inputs[5], plan.out, d_out, 1e-2, d_pen, den=den, unit_diag=unit_diag,
+                                    gate=args.gate)
         bplan.launch(stream)
         torch.cuda.synchronize()
         log(f"backward first call done, path={bplan.path}, workspace {bplan.ws_bytes / 2**30:.2f} GiB")

@@ -367,6 +367,8 @@ srw_status_t srw_backward(const srw_desc_t* d, const srw_tensors_t* in, const sr
   if (!grads->dx || !grads->dh || !grads->demb || !grads->dtau_offset || !grads->dread || !grads->dwrite)
     return SRW_EINVAL;
   if (!isfinite(cot->d_score_lb) || !isfinite(cot->d_dead_penalty)) return SRW_EINVAL;
+  // the v4.0.1 fused function has no dead-unit penalty (v401:343-367)
+  if (d->gate == SRW_GATE_GELU_V401 && cot->d_dead_penalty != 0.0f) return SRW_EINVAL;
   const size_t need = align256(srw::tiled_backward_workspace_bytes(*d));
   if (!workspace || workspace_bytes < need) return SRW_EWORKSPACE;
   srw::BackwardArgs a{};

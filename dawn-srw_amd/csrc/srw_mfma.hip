@@ -783,31 +783,6 @@ struct TileDiag {
   }
 };
 
-// v4.0.1 GELU gate of a score s (v401:303-306): z = (s - tau) / s_std,
-// Phi(z) = 0.5 (1 + erf(z / sqrt 2)), gate = z Phi(z) for z > 0, else 0.
-// zpos = max(z, 0) (the row's z sum, v401:314); the unit passes <=> z > 0
-// <=> s > tau, the sign bit of tau - s.  inv_std = 1 / s_std of the row.
-// raw_bf16: s - tau rounded to bf16, as _srw_inference computes it in the
-// scores' dtype (v401:1451-1452; tau is then bf16 as well).
-// erf of the non-negative argument by Abramowitz & Stegun 7.1.26:
-// erf(x) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^(-x^2),
-// t = 1 / (1 + p x), |error| <= 1.5e-7 -- a few registers, where the
-// library erff spills the kernels' registers.
-__device__ inline float gelu_gate(float s, float tau, float inv_std, float& zpos, bool raw_bf16 = false) {
-  float raw = s - tau;
-  if (raw_bf16) raw = __uint_as_float(pack_bf16(0.0f, raw));  // the high half: bf16(raw)
-  const float z = raw * inv_std;
-  const float x = fmaxf(z, 0.0f) * 0.7071067811865476f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, x, 1.0f));
-  float q = fmaf(1.061405429f, t, -1.453152027f);
-  q = fmaf(q, t, 1.421413741f);
-  q = fmaf(q, t, -0.284496736f);
-  q = fmaf(q, t, 0.254829592f);
-  const float erf = 1.0f - q * t * __builtin_amdgcn_exp2f(-x * x * 1.4426950408889634f);
-  zpos = z > 0.0f ? z : 0.0f;
-  return z > 0.0f ? z * (0.5f * (1.0f + erf)) : 0.0f;
-}
-
 // Software pipeline over the split's 32-unit tiles.  Iteration i runs the
 // score/read GEMMs of tile i+1 interleaved (sched_group_barrier) with the gate
 // epilogue of tile i -- matrix-core and vector-ALU work of one wave overlap --

@@ -1529,6 +1529,8 @@ struct ElemParams {
   uint16_t* DXR;          // [T, N64] d(xr) per token (E2)
   uint16_t* DXRT;         // [N64, T64] (E2)
   float* dm_part;         // [N64 / 64][Tv] (E2)
+  float* dmz_part;        // [N64 / 64][Tv] sums of dm z (E2, the v4.0.1 gate)
+  const float* sdev;      // [Tv] s_std (the v4.0.1 gate's z scale)
   int64_t Tv, N, N64, Tv64, T64;
   int routes;
   GateParams gp;
@@ -1539,6 +1541,9 @@ struct ElemParams {
 // xr)^T (v41:516-518), per-row sum intensity partials (den, v41:527, 584),
 // per-unit column sums of s and maxima of the gate (score_lb / dead penalty,
 // v41:445, 543)
+// GL: the v4.0.1 gate (v401:303-310): the forward kernels' z Phi(z) and, for
+// den = max(sum gate, 1) (v401:340), per-row sums of the gate.
+template <bool GL>
 __global__ __launch_bounds__(256) void bwd_fwd_elem_kernel(ElemParams p) {
   __shared__ uint16_t tile[kTile][kTile + 8];
   __shared__ float cs[32][kTile + 1], cm[32][kTile + 1];
@@ -1557,13 +1562,21 @@ __global__ __launch_bounds__(256) void bwd_fwd_elem_kernel(ElemParams p) {
     load8_bf16(p.XR + (vl / p.routes) * p.N64 + n, x);
     const float tau_thr = p.tau[vl] + p.gp.thr;
     const float k_exp = -tau_thr * c_exp, tau_cut = tau_thr + p.gp.cut;
+    const float istd = GL ? 1.0f / p.sdev[vl] : 0.f;
     float isum = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const bool ok = row_ok && n + e < p.N;
-      const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(s[e], c_exp, k_exp)));
-      const float it = eps + __builtin_amdgcn_fmed3f(s[e] - tau_cut, 0.0f, maxi);
-      const float g = act * it;
+      float g, it;
+      if constexpr (GL) {
+        float zp;
+        g = gelu_gate(s[e], p.tau[vl], istd, zp);
+        it = g;  // the row sum is the gate sum
+      } else {
+        const float act = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fmaf(s[e], c_exp, k_exp)));
+        it = eps + __builtin_amdgcn_fmed3f(s[e] - tau_cut, 0.0f, maxi);
+        g = act * it;
+      }
       pr[e] = ok ? round_bf16(g) * x[e] : 0.f;  // bf16 product, rounded by the packing below
       isum += ok ? it : 0.f;
       colsum[e] += ok ? s[e] : 0.f;
@@ -1621,6 +1634,43 @@ __device__ inline GateGrad gate_grad(float s, float x, float dp, float tau, floa
   return GateGrad{dm, dx, gb};
 }
 
+// Phi(z) = 0.5 (1 + erf(z / sqrt 2)) for z >= 0, erf by Abramowitz & Stegun
+// 7.1.26 (the forward kernels' gelu_gate evaluates the same expression).
+__device__ inline float gelu_cdf_pos(float z) {
+  const float x = z * 0.7071067811865476f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, x, 1.0f));
+  float q = fmaf(1.061405429f, t, -1.453152027f);
+  q = fmaf(q, t, 1.421413741f);
+  q = fmaf(q, t, -0.284496736f);
+  q = fmaf(q, t, 0.254829592f);
+  return 0.5f * (1.0f + (1.0f - q * t * __builtin_amdgcn_exp2f(-x * x * 1.4426950408889634f)));
+}
+
+// The v4.0.1 gate's derivative of one element (v401:303-309): z = (s - tau) /
+// s_std, gate = z Phi(z) for z > 0 (the forward's gelu_gate, so that P and
+// the gates here are the forward's), d(gate_bf) and d(xr) from the bf16
+// product, the den term (den = max(sum gate, 1), v401:340: every gate's
+// cotangent gains dden), then dz = dgate (Phi(z) + z phi(z)) for z > 0, phi
+// the normal density.  dm: the cotangent of s - tau, dz / s_std; dmz = dm z
+// (the s_std chain: d s_std = -sum dm z).
+struct GateGradGl {
+  float dm, dmz, dx, gb;
+};
+__device__ inline GateGradGl gate_grad_gl(float s, float x, float dp, float tau, float istd, float dden) {
+#pragma clang fp contract(off)
+  float zp;
+  const float g = gelu_gate(s, tau, istd, zp);
+  const float z = (s - tau) * istd;
+  const float gb = round_bf16(g);
+  const float dgb = round_bf16(dp * x);  // d(gate_bf): bf16 multiply transpose
+  const float dx = round_bf16(dp * gb);  // d(xr)
+  const float dg = dgb + dden;
+  const float pdf = 0.3989422804014327f * __builtin_amdgcn_exp2f(-0.5f * z * z * 1.4426950408889634f);
+  const float dz = z > 0.f ? dg * (gelu_cdf_pos(z) + z * pdf) : 0.f;
+  const float dm = dz * istd;
+  return GateGradGl{dm, dm * z, dx, gb};
+}
+
 // E2: the gate derivative from the stored scores, x.r and dP: per-row sums of
 // dm (the tau chain's input) and d(xr), summed over the routes of a token
 // (the broadcast of x.r, v41:796-797) and stored in both layouts.  dm itself
@@ -1628,7 +1678,7 @@ __device__ inline GateGrad gate_grad(float s, float x, float dp, float tau, floa
 // three bf16 arrays costs less than writing and reading an fp32 one).
 // PT_OUT (the forward's den and unit statistics given, no E1 pass): also P^T
 // = bf16(gate_bf * xr)^T (v41:516-518) from the same gate.
-template <bool PT_OUT>
+template <bool PT_OUT, bool GL = false>
 __global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
   __shared__ uint16_t tile[kTile][kTile + 8];
   __shared__ uint16_t ptile[PT_OUT ? kTile : 1][kTile + 8];
@@ -1646,14 +1696,27 @@ __global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
     load8_bf16(p.XR + (vl / p.routes) * p.N64 + n, x);
     load8_bf16(p.DP + vl * p.N64 + n, dp);
     const float tau = p.tau[vl], dden = p.dden[vl];
-    float sdm = 0.f, pr[8];
+    const float istd = GL ? 1.0f / p.sdev[vl] : 0.f;
+    float sdm = 0.f, sdmz = 0.f, pr[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const bool ok = row_ok && n + e < p.N;
-      const GateGrad gg = gate_grad(s[e], x[e], dp[e], tau, dden, p.gp, p.exp_scale, p.sharp);
-      dxs[rr][e] = ok ? gg.dx : 0.f;
-      sdm += ok ? gg.dm : 0.f;
-      pr[e] = ok ? gg.gb * x[e] : 0.f;  // bf16 product, rounded by the packing below
+      float dm, dx, gb;
+      if constexpr (GL) {
+        const GateGradGl gg = gate_grad_gl(s[e], x[e], dp[e], tau, istd, dden);
+        dm = gg.dm;
+        dx = gg.dx;
+        gb = gg.gb;
+        sdmz += ok ? gg.dmz : 0.f;
+      } else {
+        const GateGrad gg = gate_grad(s[e], x[e], dp[e], tau, dden, p.gp, p.exp_scale, p.sharp);
+        dm = gg.dm;
+        dx = gg.dx;
+        gb = gg.gb;
+      }
+      dxs[rr][e] = ok ? dx : 0.f;
+      sdm += ok ? dm : 0.f;
+      pr[e] = ok ? gb * x[e] : 0.f;  // bf16 product, rounded by the packing below
     }
     if constexpr (PT_OUT) {
 #pragma unroll
@@ -1665,6 +1728,10 @@ __global__ __launch_bounds__(256) void bwd_gate_elem_kernel(ElemParams p) {
     }
     sdm = rowsum8(sdm);
     if (et.q == 0 && row_ok) p.dm_part[static_cast<int64_t>(blockIdx.x) * p.Tv + v] = sdm;
+    if constexpr (GL) {
+      sdmz = rowsum8(sdmz);
+      if (et.q == 0 && row_ok) p.dmz_part[static_cast<int64_t>(blockIdx.x) * p.Tv + v] = sdmz;
+    }
   }
   // d(xr) per token: one row per route (single) or the pair's sum (paired)
   const int nt = p.routes == 2 ? kTile / 2 : kTile;  // tokens in this tile
@@ -1703,6 +1770,7 @@ struct DsParams {
   const float* coef;    // {c0, c1}
   uint16_t* DS;         // [Tv, N64]
   uint16_t* DST;        // [N64, Tv64]
+  const float* sdev;    // [Tv] s_std (the v4.0.1 gate)
   float d_pen;
   int64_t Tv, N, N64, Tv64;
   int routes;
@@ -1714,6 +1782,7 @@ struct DsParams {
 // (the tau chain, v41:461-464, and the per-unit score_lb / dead-penalty
 // terms, v41:445-447, 543-552), zero past N; both layouts.  dm as in E2
 // (gate_grad on the same bf16 inputs).
+template <bool GL = false>
 __global__ __launch_bounds__(256) void bwd_ds_elem_kernel(DsParams p) {
   __shared__ uint16_t tile[kTile][kTile + 8];
   const ElemTile et = elem_tile();
@@ -1737,9 +1806,12 @@ __global__ __launch_bounds__(256) void bwd_ds_elem_kernel(DsParams p) {
     load8_bf16(p.XR + (vl / p.routes) * p.N64 + n, x);
     load8_bf16(p.DP + vl * p.N64 + n, dp);
     const float a = p.alpha[vl], b = p.beta[vl], tau = p.tau[vl], dden = p.dden[vl];
+    const float istd = GL ? 1.0f / p.sdev[vl] : 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float dm = gate_grad(s[e], x[e], dp[e], tau, dden, p.gp, p.exp_scale, p.sharp).dm;
+      float dm;
+      if constexpr (GL) dm = gate_grad_gl(s[e], x[e], dp[e], tau, istd, dden).dm;
+      else dm = gate_grad(s[e], x[e], dp[e], tau, dden, p.gp, p.exp_scale, p.sharp).dm;
       o[e] = row_ok && n + e < p.N ? dm + a + b * s[e] + unit[e] : 0.f;
     }
 #pragma unroll
@@ -1776,7 +1848,10 @@ __global__ __launch_bounds__(256) void bwd_rowsum_kernel(const float* __restrict
 // tau chain per token (v41:461-464): dtau = -sum_n dm; tau = mean + off * std,
 // std = sqrt(E[s^2] - mean^2) + 1e-8.  Writes d tau_offset and the affine
 // coefficients of the score gradient, ds = dm + alpha + beta * s (+ unit term)
-__global__ __launch_bounds__(256) void bwd_token_kernel(const float* __restrict__ dm_part, int S2, int64_t T,
+// dmz_part (the v4.0.1 gate, else null): sums of dm z, z = (s - tau) / s_std;
+// z's own dependence on s_std adds d s_std = -sum_n dm z (v401:304).
+__global__ __launch_bounds__(256) void bwd_token_kernel(const float* __restrict__ dm_part,
+                                                        const float* __restrict__ dmz_part, int S2, int64_t T,
                                                         int64_t N, const float* __restrict__ tau_off,
                                                         const float* __restrict__ mean, const float* __restrict__ var,
                                                         const float* __restrict__ sdev, float* __restrict__ dtau_off,
@@ -1784,14 +1859,18 @@ __global__ __launch_bounds__(256) void bwd_token_kernel(const float* __restrict_
   const int lane = threadIdx.x & 63;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  float a = 0.f;
-  for (int s = lane; s < S2; s += 64) a += dm_part[static_cast<int64_t>(s) * T + t];
+  float a = 0.f, c = 0.f;
+  for (int s = lane; s < S2; s += 64) {
+    a += dm_part[static_cast<int64_t>(s) * T + t];
+    if (dmz_part) c += dmz_part[static_cast<int64_t>(s) * T + t];
+  }
   a = wave_sum(a);
+  c = wave_sum(c);
   if (lane == 0) {
     const float fN = static_cast<float>(N);
     const float dtau = -a;
     dtau_off[t] = dtau * sdev[t];
-    const float dstd = dtau * tau_off[t];
+    const float dstd = dtau * tau_off[t] - c;
     const float dvar = dstd / (2.0f * sqrtf(var[t]));
     const float dmean = dtau - 2.0f * mean[t] * dvar;
     alpha[t] = dmean / fN;
@@ -1872,6 +1951,29 @@ __global__ __launch_bounds__(256) void bwd_unit_coef_kernel(const float* __restr
     coef[0] = d_lb * (-dvs * 2.0f * ms / fN + dms / fN);
     coef[1] = d_lb * dvs * 2.0f / fN;
   }
+}
+
+// The v4.0.1 forward normalisation r_hat = r / (||r|| + 1e-8) of the read
+// and write rows (v401:300-301), backwards, in place: grad holds d r_hat of
+// each row on entry and d r = d r_hat / c - r (r . d r_hat) / (c^2 ||r||)
+// (c = ||r|| + 1e-8) on exit.  One workgroup per row, fp32 from the bf16 rows.
+__global__ __launch_bounds__(256) void bwd_norm_rows_kernel(const uint16_t* __restrict__ rows, float* __restrict__ grad,
+                                                            int64_t D) {
+  __shared__ float red[4];
+  const int64_t n = blockIdx.x;
+  const uint16_t* r = rows + n * D;
+  float* g = grad + n * D;
+  float ss = 0.f, dot = 0.f;
+  for (int64_t i = threadIdx.x; i < D; i += 256) {
+    const float v = bf16_to_f32(r[i]);
+    ss += v * v;
+    dot += v * g[i];
+  }
+  ss = block_sum<256>(ss, red);
+  dot = block_sum<256>(dot, red);
+  const float nrm = sqrtf(ss), c = nrm + 1e-8f;
+  const float k = nrm > 0.f ? dot / (c * c * nrm) : 0.f;
+  for (int64_t i = threadIdx.x; i < D; i += 256) g[i] = g[i] / c - bf16_to_f32(r[i]) * k;
 }
 
 // out[i] = bf16(sum_s part[s][i]) widened to fp32: the reference's gradient
@@ -2034,8 +2136,8 @@ hipError_t bwd_gemms(const BGemm* g, const uint16_t* const* A, const uint16_t* c
 }
 
 struct BLayout {
-  size_t S, XR, DP, DXR, DS, PT, DXRT, DST, ET, RT, HT, XT, DRAWT, DRAW;
-  size_t mom, inten_part, dm_part, tokv, psum, pmax, pn, dead, blk, coef, part, total;
+  size_t S, XR, DP, DXR, DS, PT, DXRT, DST, ET, RT, HT, XT, DRAWT, DRAW, RN, WN;
+  size_t mom, inten_part, dm_part, dmz_part, tokv, psum, pmax, pn, dead, blk, coef, part, total;
   int64_t Tv, T64, Tv64, N64;
   int CT, RTv, RTt, NB, TS, nblk;
   int S_st;  // moment partials per row
@@ -2081,10 +2183,15 @@ BLayout blayout(const srw_desc_t& d) {
   l.XT = take(static_cast<size_t>(D) * l.T64 * 2);
   l.DRAWT = take(static_cast<size_t>(D) * l.Tv64 * 2);
   l.DRAW = take(static_cast<size_t>(l.Tv) * D * 2);
+  // the v4.0.1 gate: the forward-normalised read and write rows (v401:300-301)
+  const bool gl = d.gate == SRW_GATE_GELU_V401;
+  l.RN = take(gl ? static_cast<size_t>(N) * D * 2 : 0);
+  l.WN = take(gl ? static_cast<size_t>(N) * D * 2 : 0);
   l.S_st = rows_gemm_supports(dr) ? rows_gemm_splits(l.Tv, N) : 2 * l.CT;
   l.mom = take(static_cast<size_t>(l.S_st) * l.Tv * 2 * 4);
   l.inten_part = take(static_cast<size_t>(l.NB) * l.Tv * 4);
   l.dm_part = take(static_cast<size_t>(l.NB) * l.Tv * 4);
+  l.dmz_part = take(gl ? static_cast<size_t>(l.NB) * l.Tv * 4 : 0);
   l.tokv = take(static_cast<size_t>(l.Tv) * 9 * 4);
   l.psum = take(static_cast<size_t>(l.TS) * l.N64 * 4);
   l.pmax = take(static_cast<size_t>(l.TS) * l.N64 * 4);
@@ -2123,7 +2230,8 @@ hipError_t store_gemm(const uint16_t* A, const uint16_t* B, uint16_t* C, int64_t
 }  // namespace
 
 bool tiled_backward_supports(const srw_desc_t& d) {
-  if (d.dtype != SRW_BF16 || d.gate != SRW_GATE_V41 || d.stats_mode != SRW_STATS_ONEPASS) return false;
+  if (d.dtype != SRW_BF16 || d.stats_mode != SRW_STATS_ONEPASS) return false;
+  if (d.gate != SRW_GATE_V41 && d.gate != SRW_GATE_GELU_V401) return false;
   if (d.n_routes != 1 && d.n_routes != 2) return false;
   if (d.d_model % kNAlign != 0 || d.d_route % kNAlign != 0) return false;
   if (d.flags & (SRW_FLAG_EMULATE | SRW_FLAG_NO_FAST | SRW_FLAG_SPARSE_SKIP)) return false;
@@ -2149,6 +2257,8 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   float *mean = tokv, *var = tokv + Tv, *sdev = tokv + 2 * Tv, *tau = tokv + 3 * Tv, *dden = tokv + 4 * Tv;
   float *alpha = tokv + 5 * Tv, *beta = tokv + 6 * Tv, *zsum = tokv + 7 * Tv, *dsc = tokv + 8 * Tv;
   const auto* emb = static_cast<const uint16_t*>(a.in.emb);
+  const bool gl = d.gate == SRW_GATE_GELU_V401;
+  // the rows the products use: the v4.0.1 gate's forward-normalised ones
   const auto* read = static_cast<const uint16_t*>(a.in.read);
   const auto* write = static_cast<const uint16_t*>(a.in.write);
   const auto* x = static_cast<const uint16_t*>(a.in.x);
@@ -2166,6 +2276,12 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   if ((e = set_lds(reinterpret_cast<const void*>(tiled_write_batch_kernel<4>))) != hipSuccess) return e;
 #define SRW_TRY(expr) \
   if ((e = (expr)) != hipSuccess) return e
+  if (gl) {
+    SRW_TRY(normalize_rows_bf16(static_cast<const uint16_t*>(a.in.read), b16(l.RN), N, D, st));
+    SRW_TRY(normalize_rows_bf16(static_cast<const uint16_t*>(a.in.write), b16(l.WN), N, D, st));
+    read = b16(l.RN);
+    write = b16(l.WN);
+  }
   // operands of the K = units / K = rows contractions, unit- or row-contiguous
   SRW_TRY(transpose(emb, ET, N, N64, dr, st));
   SRW_TRY(transpose(read, RT, N, N64, D, st));
@@ -2218,6 +2334,8 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   ep.DXR = DXR;
   ep.DXRT = DXRT;
   ep.dm_part = dm_part;
+  ep.dmz_part = gl ? f32(l.dmz_part) : nullptr;
+  ep.sdev = sdev;
   ep.Tv = Tv;
   ep.N = N;
   ep.N64 = N64;
@@ -2233,12 +2351,13 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   const bool res = a.cot.den && a.cot.unit_diag;
   const float* zs = zsum;
   if (res) {
-    zs = a.cot.den;  // den = max(sum intensity, 1): the den term's test sum > 1 reads the same on it
+    zs = a.cot.den;  // den = max(sum intensity (v4.0.1: gate), 1): the den term's test sum > 1 reads the same on it
     hipLaunchKernelGGL(bwd_unit_from_diag_kernel, dim3(static_cast<unsigned>(l.nblk)), dim3(256), 0, st,
                        a.cot.unit_diag, Tv, N, N64, d.dead_threshold, pn, dead, blk);
     SRW_TRY(hipGetLastError());
   } else {
-    hipLaunchKernelGGL(bwd_fwd_elem_kernel, grid_e, dim3(256), 0, st, ep);
+    if (gl) hipLaunchKernelGGL(bwd_fwd_elem_kernel<true>, grid_e, dim3(256), 0, st, ep);
+    else hipLaunchKernelGGL(bwd_fwd_elem_kernel<false>, grid_e, dim3(256), 0, st, ep);
     SRW_TRY(hipGetLastError());
     hipLaunchKernelGGL(bwd_rowsum_kernel, dim3(static_cast<unsigned>((Tv + 63) / 64)), dim3(256), 0, st, inten_part,
                        l.NB, Tv, zsum);
@@ -2266,13 +2385,17 @@ hipError_t tiled_backward(const BackwardArgs& a) {
     SRW_TRY(store_gemm(write, DRAW, DP, Tv, Tv, 1, N, N64, D, st));
   }
   dominant_kernel_end(st);
-  if (res)
+  if (res && gl)
+    hipLaunchKernelGGL((bwd_gate_elem_kernel<true, true>), grid_e, dim3(256), 0, st, ep);
+  else if (res)
     hipLaunchKernelGGL(bwd_gate_elem_kernel<true>, grid_e, dim3(256), 0, st, ep);
+  else if (gl)
+    hipLaunchKernelGGL((bwd_gate_elem_kernel<false, true>), grid_e, dim3(256), 0, st, ep);
   else
     hipLaunchKernelGGL(bwd_gate_elem_kernel<false>, grid_e, dim3(256), 0, st, ep);
   SRW_TRY(hipGetLastError());
-  hipLaunchKernelGGL(bwd_token_kernel, dim3(static_cast<unsigned>((Tv + 3) / 4)), dim3(256), 0, st, dm_part, l.NB,
-                     Tv, N, a.in.tau_offset, mean, var, sdev, a.g.dtau_offset, alpha, beta);
+  hipLaunchKernelGGL(bwd_token_kernel, dim3(static_cast<unsigned>((Tv + 3) / 4)), dim3(256), 0, st, dm_part,
+                     ep.dmz_part, l.NB, Tv, N, a.in.tau_offset, mean, var, sdev, a.g.dtau_offset, alpha, beta);
   SRW_TRY(hipGetLastError());
   // E3: ds in both layouts
   DsParams dp{};
@@ -2288,6 +2411,7 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   dp.coef = coef;
   dp.DS = DS;
   dp.DST = DST;
+  dp.sdev = sdev;
   dp.d_pen = a.cot.d_dead_penalty;
   dp.Tv = Tv;
   dp.N = N;
@@ -2297,7 +2421,8 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   dp.gp = a.gp;
   dp.exp_scale = exp_scale;
   dp.sharp = d.sharpness;
-  hipLaunchKernelGGL(bwd_ds_elem_kernel, grid_e, dim3(256), 0, st, dp);
+  if (gl) hipLaunchKernelGGL(bwd_ds_elem_kernel<true>, grid_e, dim3(256), 0, st, dp);
+  else hipLaunchKernelGGL(bwd_ds_elem_kernel<false>, grid_e, dim3(256), 0, st, dp);
   SRW_TRY(hipGetLastError());
 
   // the five gradient contractions: bf16 dots, fp32 accumulation
@@ -2315,6 +2440,14 @@ hipError_t tiled_backward(const BackwardArgs& a) {
       if (gs[i].spc > 1) pp += al256(static_cast<int64_t>(gs[i].spc) * gs[i].M * gs[i].Nc * 4) / 4;
     }
     SRW_TRY(bwd_gemms(gs, As, Bs, lds_, parts, outs, 5, st));
+  }
+  if (gl) {  // d read / d write through the forward normalisation
+    hipLaunchKernelGGL(bwd_norm_rows_kernel, dim3(static_cast<unsigned>(N)), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(a.in.read), a.g.dread, D);
+    SRW_TRY(hipGetLastError());
+    hipLaunchKernelGGL(bwd_norm_rows_kernel, dim3(static_cast<unsigned>(N)), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(a.in.write), a.g.dwrite, D);
+    SRW_TRY(hipGetLastError());
   }
 #undef SRW_TRY
   return hipSuccess;

@@ -273,7 +273,9 @@ class SrwBackwardPlan:
 
     def __init__(self, x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: float = 0.0,
                  d_dead_penalty: float = 0.0, *, consts: GateConfig = GateConfig(),
-                 scale: float = 1.0, den=None, unit_diag=None):
+                 scale: float = 1.0, den=None, unit_diag=None, gate: str = "v41"):
+        if gate not in _GATES:
+            raise ValueError(f"gate must be one of {sorted(_GATES)}")
         if x.dim() != 2:
             raise ValueError("x must be [T, D]")
         T, D = x.shape
@@ -307,6 +309,7 @@ class SrwBackwardPlan:
         desc.T, desc.d_model, desc.d_route, desc.n_units = T, D, dr, N
         desc.n_routes = R
         desc.dtype = C.SRW_BF16
+        desc.gate = _GATES[gate]
         desc.sharpness = consts.sharpness
         desc.act_threshold = consts.activation_threshold
         desc.act_cutoff = consts.activation_cutoff
@@ -349,7 +352,7 @@ class SrwBackwardPlan:
 
 def srw_backward(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: float = 0.0,
                  d_dead_penalty: float = 0.0, *, consts: GateConfig = GateConfig(),
-                 scale: float = 1.0, stream=None, den=None, unit_diag=None) -> dict:
+                 scale: float = 1.0, stream=None, den=None, unit_diag=None, gate: str = "v41") -> dict:
     """Reverse-mode derivative of one srw_forward call (the VJP of
     fused_gate_srw that the reference's train_step takes with
     jax.value_and_grad, scripts/train_jax.py:548-726).
@@ -366,9 +369,12 @@ def srw_backward(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb: flo
     ``den`` [T, R] and ``unit_diag`` [N, 2] (both or neither): the same
     forward call's den and unit diagnostics (a ``diag=True`` call, as the
     drop-in's forward makes), which spare the backward its own pass over the
-    scores for them.
+    scores for them.  ``gate`` "gelu_v401": the VJP of the v4.0.1 fused
+    function (models/legacy/dawn_spatial_v401_exp.py:229-554), which has no
+    dead_penalty (``d_dead_penalty`` must be 0).
     """
     plan = SrwBackwardPlan(x, h, emb, tau_offset, read, write, out, d_out, d_score_lb,
-                           d_dead_penalty, consts=consts, scale=scale, den=den, unit_diag=unit_diag)
+                           d_dead_penalty, consts=consts, scale=scale, den=den, unit_diag=unit_diag,
+                           gate=gate)
     plan.launch(stream)
     return plan.results()

@@ -13,7 +13,7 @@ Reference (madst0614/DAWN-SRW, models/dawn_spatial_v41_exp.py):
 * The v4.0.1 ``make_sharded_srw(mesh, max_chunk_size=2048)`` and
   ``make_sharded_srw_paired`` (models/legacy/dawn_spatial_v401_exp.py:
   194-554, GELU gate) as ``make_sharded_srw_v401`` /
-  ``make_sharded_srw_paired_v401`` -> 16-tuple (forward only).
+  ``make_sharded_srw_paired_v401`` -> 16-tuple.
 
 The factories return functions with the same positional signature and the
 same 22-tuple order, so they slot into ``sharded_fns = (fused_single,
@@ -265,10 +265,20 @@ def _diag_tuple_v401(res, N, B, S, R=1):
             skew, na.std(correction=0), ent.mean())
 
 
+# Positions in the v4.0.1 16-tuple (v401:364-367).  Its callers' losses use
+# out and score_lb (lb_loss, v401:909, 978); outputs behind stop_gradient
+# (gate_max, tau_abs_mean, z_lt_*, score_skew, active_per_token_std,
+# gate_entropy, v401:276-279, 344-363) and the counts carry no gradient.
+_NO_GRAD_V401 = (1, 2, 6, 7, 8, 10, 11, 12, 13, 14, 15)
+_NAMES_V401 = _NAMES[:16]
+
+
 class _FusedSrwV401(torch.autograd.Function):
-    """The v4.0.1 fused_gate_srw(_paired) (v401:230-367, :408-554) as an
-    autograd node whose backward is not implemented (the VJP here covers the
-    v4.1 gate)."""
+    """The v4.0.1 fused_gate_srw(_paired) (v401:230-367, :408-554) as one
+    autograd node: the forward runs srw_forward (bf16, the GELU gate, one-pass
+    statistics, diagnostics), the backward srw_backward with the gate and the
+    cotangents of out and score_lb.  Differentiating score_std, the gate sum
+    or z_mean_active raises NotImplementedError."""
 
     @staticmethod
     def forward(ctx, x, h, emb, tau_offset, read, write, routes, cs):
@@ -285,13 +295,34 @@ class _FusedSrwV401(torch.autograd.Function):
         shape = (B, S, D) if routes == 1 else (B, S, 2, D)
         out = res["out"].reshape(shape).to(torch.float32)
         outs = (out,) + _diag_tuple_v401(res, N, B, S, routes)
-        ctx.mark_non_differentiable(*outs[1:])
+        ctx.save_for_backward(xb, hb, eb, tau, rdb, wb, res["out"], res["den"], res["unit_diag"])
+        ctx.meta = (routes, tuple(t.shape for t in (x, h, emb, tau_offset, read, write)),
+                    tuple(t.dtype for t in (x, h, emb, tau_offset, read, write)))
+        ctx.mark_non_differentiable(*(outs[i] for i in _NO_GRAD_V401))
+        ctx.set_materialize_grads(False)
         return outs
 
     @staticmethod
     def backward(ctx, *grads):
-        raise NotImplementedError("the backward of the v4.0.1 (GELU gate) fused SRW layer is not "
-                                  "implemented; srw_backward covers the v4.1 gate")
+        for i, g in enumerate(grads):
+            if g is not None and i not in (_OUT, _SCORE_LB) and i not in _NO_GRAD_V401:
+                raise NotImplementedError(
+                    f"the gradient through output {i} ({_NAMES_V401[i]}) of the v4.0.1 fused SRW layer "
+                    "is not implemented; out and score_lb are differentiable")
+        routes, shapes, dtypes = ctx.meta
+        xb, hb, eb, tau, rdb, wb, out_b, den, unit_diag = ctx.saved_tensors
+        T, D = xb.shape
+        d_out = grads[_OUT]
+        if d_out is None:
+            d_out = torch.zeros(T, routes, D, dtype=torch.float32, device=xb.device)
+        else:
+            d_out = d_out.reshape(T, routes, D).to(torch.float32).contiguous()
+        d_lb = 0.0 if grads[_SCORE_LB] is None else float(grads[_SCORE_LB])
+        g = srw_backward(xb, hb, eb, tau, rdb, wb, out_b, d_out, d_lb, 0.0, gate="gelu_v401",
+                         den=den.reshape(T, routes), unit_diag=unit_diag)
+        res = [g[k] for k in ("dx", "dh", "demb", "dtau_offset", "dread", "dwrite")]
+        res = [r.reshape(sh).to(dt) for r, sh, dt in zip(res, shapes, dtypes)]
+        return (*res, None, None)
 
 
 def _make_v401(routes, mesh, max_chunk_size):
@@ -313,7 +344,8 @@ def make_sharded_srw_v401(mesh=None, max_chunk_size=2048):
     strong_frac, phi_binary_frac, z_mean_active, tau_abs_mean, z_lt_075_frac,
     z_lt_030_frac, score_skew, active_per_token_std, gate_entropy).  Inputs
     cast to bf16 (v401:238-242), one-pass statistics, R and W rows
-    forward-normalised per chunk (v401:300-301).  Forward only."""
+    forward-normalised per chunk (v401:300-301); out and score_lb
+    backpropagate to the six inputs through ``srw_backward``."""
     return _make_v401(1, mesh, max_chunk_size)
 
 
@@ -321,7 +353,7 @@ def make_sharded_srw_paired_v401(mesh=None, max_chunk_size=2048):
     """The v4.0.1 ``make_sharded_srw_paired(mesh, max_chunk_size=2048)``
     (v401:372-554): h [B,S,2,dr], tau_offset [B,S,2,1] -> the 16-tuple with
     out [B,S,2,D] and the per-token outputs averaged over the two routes;
-    x.R^T shared by both routes.  Forward only."""
+    x.R^T shared by both routes; differentiable as the single form."""
     return _make_v401(2, mesh, max_chunk_size)
 
 

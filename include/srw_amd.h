@@ -31,7 +31,10 @@
  *          train_step (scripts/train_jax.py:548-726, through the sharded_fns
  *          tuple of :2324-2333): cotangents of out, score_lb and
  *          dead_penalty (the outputs the loss uses, :586-603) in, gradients of
- *          x, h, emb, tau_offset, read and write out
+ *          x, h, emb, tau_offset, read and write out; with gate =
+ *          SRW_GATE_GELU_V401 the VJP of the v4.0.1 fused function
+ *          (models/legacy/dawn_spatial_v401_exp.py:229-554: out and score_lb,
+ *          the lb_loss of its callers, :978)
  *   srw_forward, dtype = SRW_F32, SRW_STATS_ONEPASS
  *       -> no reference counterpart (an extension: the reference's
  *          fused_gate_srw casts every operand to bf16, v41:422-428); checked
@@ -310,9 +313,12 @@ srw_status_t srw_backward_workspace_size(const srw_desc_t* desc, size_t* bytes);
  * `stream`: recomputes the forward's scores, gates and products from the
  * inputs (as the reference's jax.checkpoint-ed scans do, v41:434, 489) and
  * writes the gradients of <d_out, out> + d_score_lb * score_lb +
- * d_dead_penalty * dead_penalty.  bf16, v4.1 gate, one route or the paired
- * routes (n_routes = 2, fused_gate_srw_paired), one-pass statistics, d_model
- * and d_route multiples of 64; anything else returns SRW_EUNSUPPORTED.  With
+ * d_dead_penalty * dead_penalty.  bf16, the v4.1 gate or the v4.0.1 GELU
+ * gate (whose function has no dead_penalty: d_dead_penalty must be 0, else
+ * SRW_EINVAL; read and write enter through the forward normalisation), one
+ * route or the paired routes (n_routes = 2, fused_gate_srw_paired),
+ * one-pass statistics, d_model and d_route multiples of 64; anything else
+ * returns SRW_EUNSUPPORTED.  With
  * T = 0 the gradients of emb, read, write (and dscale) are zero.  The cotangents of bf16 values are rounded to bf16 where
  * the reference's bf16 casts, dots and products transpose (the gradients are
  * bf16 dot outputs widened to float32). */

@@ -714,3 +714,32 @@ def test_planted_v401_paired_mistakes_are_caught(monkeypatch, name):
     attr, fn, field = V401_PAIRED_MUTATIONS[name]
     monkeypatch.setattr(srw_ref, attr, fn)
     assert field in _v401_paired_vs_single_mismatch()
+
+
+def test_v401_autograd_matches_finite_differences():
+    """The GPU backward of the v4.0.1 gate is checked against torch autograd
+    through fused_gate_srw_gelu_v401; in exact arithmetic that autograd
+    equals central finite differences of <d_out, out> + d_lb score_lb in
+    every input (x, h, emb, tau_offset, read, write)."""
+    T, D, dr, N = 10, 12, 8, 48
+    x, h, e, tau, r, w = _v401_inputs(31, T=T, D=D, dr=dr, N=N, tau=0.2)
+    g = torch.Generator().manual_seed(32)
+    d_out = torch.randn(T, D, generator=g, dtype=F64)
+
+    def loss(*a):
+        res = srw_ref.fused_gate_srw_gelu_v401(a[0][None], a[1][None], a[2], a[3][None], a[4], a[5],
+                                               max_chunk_size=16, exact=True)
+        return (res[0][0] * d_out).sum() + 0.37 * res[3]
+
+    inputs = [x, h, e, tau, r, w]
+    leaves = [t.clone().requires_grad_(True) for t in inputs]
+    loss(*leaves).backward()
+    eps = 1e-6
+    for i, t in enumerate(inputs):
+        for (a, b) in ((0, 0), (t.shape[0] // 2, t.shape[1] - 1), (t.shape[0] - 1, t.shape[1] // 2)):
+            p = [u.clone() for u in inputs]
+            m = [u.clone() for u in inputs]
+            p[i][a, b] += eps
+            m[i][a, b] -= eps
+            fd = float((loss(*p) - loss(*m)) / (2 * eps))
+            assert math.isclose(float(leaves[i].grad[a, b]), fd, rel_tol=1e-5, abs_tol=1e-8), (i, a, b)
