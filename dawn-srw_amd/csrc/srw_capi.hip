@@ -366,6 +366,12 @@ srw_status_t srw_backward(const srw_desc_t* d, const srw_tensors_t* in, const sr
   if (!cot->den != !cot->unit_diag) return SRW_EINVAL;  // the forward's residuals: both or neither
   if (!grads->dx || !grads->dh || !grads->demb || !grads->dtau_offset || !grads->dread || !grads->dwrite)
     return SRW_EINVAL;
+  // rows are read and written in 16-byte pieces
+  for (const void* p : {in->x, in->h, in->emb, in->read, in->write, cot->out, static_cast<const void*>(cot->d_out),
+                        static_cast<const void*>(grads->dx), static_cast<const void*>(grads->dh),
+                        static_cast<const void*>(grads->demb), static_cast<const void*>(grads->dread),
+                        static_cast<const void*>(grads->dwrite)})
+    if (reinterpret_cast<uintptr_t>(p) & 15) return SRW_EINVAL;
   if (!isfinite(cot->d_score_lb) || !isfinite(cot->d_dead_penalty)) return SRW_EINVAL;
   // the v4.0.1 fused function has no dead-unit penalty (v401:343-367)
   if (d->gate == SRW_GATE_GELU_V401 && cot->d_dead_penalty != 0.0f) return SRW_EINVAL;

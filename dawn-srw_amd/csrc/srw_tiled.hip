@@ -1849,28 +1849,46 @@ __global__ __launch_bounds__(256) void bwd_rowsum_kernel(const float* __restrict
 // std = sqrt(E[s^2] - mean^2) + 1e-8.  Writes d tau_offset and the affine
 // coefficients of the score gradient, ds = dm + alpha + beta * s (+ unit term)
 // dmz_part (the v4.0.1 gate, else null): sums of dm z, z = (s - tau) / s_std;
-// z's own dependence on s_std adds d s_std = -sum_n dm z (v401:304).
+// z's own dependence on s_std adds d s_std = -sum_n dm z (v401:304).  16 rows
+// per workgroup, 16 partial groups per row (a block's partials are
+// row-contiguous: 64-byte loads), combined in a fixed order.
+constexpr int kTokRows = 16, kTokGroups = 16;
 __global__ __launch_bounds__(256) void bwd_token_kernel(const float* __restrict__ dm_part,
                                                         const float* __restrict__ dmz_part, int S2, int64_t T,
                                                         int64_t N, const float* __restrict__ tau_off,
                                                         const float* __restrict__ mean, const float* __restrict__ var,
                                                         const float* __restrict__ sdev, float* __restrict__ dtau_off,
                                                         float* __restrict__ alpha, float* __restrict__ beta) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  float a = 0.f, c = 0.f;
-  for (int s = lane; s < S2; s += 64) {
-    a += dm_part[static_cast<int64_t>(s) * T + t];
-    if (dmz_part) c += dmz_part[static_cast<int64_t>(s) * T + t];
+  __shared__ float red[2][kTokGroups][kTokRows + 1];
+  const int c = threadIdx.x % kTokRows, grp = threadIdx.x / kTokRows;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kTokRows + c;
+  const int64_t tl = t < T ? t : T - 1;
+  float a[2] = {0.f, 0.f}, z[2] = {0.f, 0.f};
+  int b = grp;
+  for (; b + kTokGroups < S2; b += 2 * kTokGroups) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      a[k] += dm_part[static_cast<int64_t>(b + kTokGroups * k) * T + tl];
+      if (dmz_part) z[k] += dmz_part[static_cast<int64_t>(b + kTokGroups * k) * T + tl];
+    }
   }
-  a = wave_sum(a);
-  c = wave_sum(c);
-  if (lane == 0) {
+  for (; b < S2; b += kTokGroups) {
+    a[0] += dm_part[static_cast<int64_t>(b) * T + tl];
+    if (dmz_part) z[0] += dmz_part[static_cast<int64_t>(b) * T + tl];
+  }
+  red[0][grp][c] = a[0] + a[1];
+  red[1][grp][c] = z[0] + z[1];
+  __syncthreads();
+  if (grp == 0 && t < T) {
+    float sa = 0.f, sz = 0.f;
+    for (int q = 0; q < kTokGroups; ++q) {
+      sa += red[0][q][c];
+      sz += red[1][q][c];
+    }
     const float fN = static_cast<float>(N);
-    const float dtau = -a;
+    const float dtau = -sa;
     dtau_off[t] = dtau * sdev[t];
-    const float dstd = dtau * tau_off[t] - c;
+    const float dstd = dtau * tau_off[t] - sz;
     const float dvar = dstd / (2.0f * sqrtf(var[t]));
     const float dmean = dtau - 2.0f * mean[t] * dvar;
     alpha[t] = dmean / fN;
@@ -1956,24 +1974,56 @@ __global__ __launch_bounds__(256) void bwd_unit_coef_kernel(const float* __restr
 // The v4.0.1 forward normalisation r_hat = r / (||r|| + 1e-8) of the read
 // and write rows (v401:300-301), backwards, in place: grad holds d r_hat of
 // each row on entry and d r = d r_hat / c - r (r . d r_hat) / (c^2 ||r||)
-// (c = ||r|| + 1e-8) on exit.  One workgroup per row, fp32 from the bf16 rows.
+// (c = ||r|| + 1e-8) on exit.  One wave per row (four per workgroup), fp32
+// from the bf16 rows.
 __global__ __launch_bounds__(256) void bwd_norm_rows_kernel(const uint16_t* __restrict__ rows, float* __restrict__ grad,
-                                                            int64_t D) {
-  __shared__ float red[4];
-  const int64_t n = blockIdx.x;
-  const uint16_t* r = rows + n * D;
-  float* g = grad + n * D;
+                                                            int64_t N, int64_t D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;
+  // four adjacent elements per lane and step (8- and 16-byte accesses; D is a
+  // multiple of 64), rows of up to 1024 elements held between the two sweeps
+  const uint2* r = reinterpret_cast<const uint2*>(rows + n * D);
+  float4* g = reinterpret_cast<float4*>(grad + n * D);
+  const int64_t D4 = D / 4;
+  constexpr int kRegs = 4;
+  float4 rv[kRegs], gv[kRegs];
   float ss = 0.f, dot = 0.f;
-  for (int64_t i = threadIdx.x; i < D; i += 256) {
-    const float v = bf16_to_f32(r[i]);
-    ss += v * v;
-    dot += v * g[i];
+#pragma unroll
+  for (int j = 0; j < kRegs; ++j) {
+    const int64_t i = lane + 64 * j;
+    if (i < D4) {
+      const uint2 w = r[i];
+      rv[j] = make_float4(lo_f32(w.x), hi_f32(w.x), lo_f32(w.y), hi_f32(w.y));
+      gv[j] = g[i];
+      ss += rv[j].x * rv[j].x + rv[j].y * rv[j].y + rv[j].z * rv[j].z + rv[j].w * rv[j].w;
+      dot += rv[j].x * gv[j].x + rv[j].y * gv[j].y + rv[j].z * gv[j].z + rv[j].w * gv[j].w;
+    }
   }
-  ss = block_sum<256>(ss, red);
-  dot = block_sum<256>(dot, red);
+  for (int64_t i = lane + 64 * kRegs; i < D4; i += 64) {  // rows beyond 1024 elements
+    const uint2 w = r[i];
+    const float4 gg = g[i];
+    const float a = lo_f32(w.x), b = hi_f32(w.x), c = lo_f32(w.y), d = hi_f32(w.y);
+    ss += a * a + b * b + c * c + d * d;
+    dot += a * gg.x + b * gg.y + c * gg.z + d * gg.w;
+  }
+  ss = wave_sum(ss);
+  dot = wave_sum(dot);
   const float nrm = sqrtf(ss), c = nrm + 1e-8f;
   const float k = nrm > 0.f ? dot / (c * c * nrm) : 0.f;
-  for (int64_t i = threadIdx.x; i < D; i += 256) g[i] = g[i] / c - bf16_to_f32(r[i]) * k;
+#pragma unroll
+  for (int j = 0; j < kRegs; ++j) {
+    const int64_t i = lane + 64 * j;
+    if (i < D4)
+      g[i] = make_float4(gv[j].x / c - rv[j].x * k, gv[j].y / c - rv[j].y * k, gv[j].z / c - rv[j].z * k,
+                         gv[j].w / c - rv[j].w * k);
+  }
+  for (int64_t i = lane + 64 * kRegs; i < D4; i += 64) {
+    const uint2 w = r[i];
+    const float4 gg = g[i];
+    g[i] = make_float4(gg.x / c - lo_f32(w.x) * k, gg.y / c - hi_f32(w.x) * k, gg.z / c - lo_f32(w.y) * k,
+                       gg.w / c - hi_f32(w.y) * k);
+  }
 }
 
 // out[i] = bf16(sum_s part[s][i]) widened to fp32: the reference's gradient
@@ -2394,8 +2444,9 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   else
     hipLaunchKernelGGL(bwd_gate_elem_kernel<false>, grid_e, dim3(256), 0, st, ep);
   SRW_TRY(hipGetLastError());
-  hipLaunchKernelGGL(bwd_token_kernel, dim3(static_cast<unsigned>((Tv + 3) / 4)), dim3(256), 0, st, dm_part,
-                     ep.dmz_part, l.NB, Tv, N, a.in.tau_offset, mean, var, sdev, a.g.dtau_offset, alpha, beta);
+  hipLaunchKernelGGL(bwd_token_kernel, dim3(static_cast<unsigned>((Tv + kTokRows - 1) / kTokRows)), dim3(256), 0, st,
+                     dm_part, ep.dmz_part, l.NB, Tv, N, a.in.tau_offset, mean, var, sdev, a.g.dtau_offset, alpha,
+                     beta);
   SRW_TRY(hipGetLastError());
   // E3: ds in both layouts
   DsParams dp{};
@@ -2442,11 +2493,12 @@ hipError_t tiled_backward(const BackwardArgs& a) {
     SRW_TRY(bwd_gemms(gs, As, Bs, lds_, parts, outs, 5, st));
   }
   if (gl) {  // d read / d write through the forward normalisation
-    hipLaunchKernelGGL(bwd_norm_rows_kernel, dim3(static_cast<unsigned>(N)), dim3(256), 0, st,
-                       static_cast<const uint16_t*>(a.in.read), a.g.dread, D);
+    const dim3 grid_n(static_cast<unsigned>((N + 3) / 4));
+    hipLaunchKernelGGL(bwd_norm_rows_kernel, grid_n, dim3(256), 0, st, static_cast<const uint16_t*>(a.in.read),
+                       a.g.dread, N, D);
     SRW_TRY(hipGetLastError());
-    hipLaunchKernelGGL(bwd_norm_rows_kernel, dim3(static_cast<unsigned>(N)), dim3(256), 0, st,
-                       static_cast<const uint16_t*>(a.in.write), a.g.dwrite, D);
+    hipLaunchKernelGGL(bwd_norm_rows_kernel, grid_n, dim3(256), 0, st, static_cast<const uint16_t*>(a.in.write),
+                       a.g.dwrite, N, D);
     SRW_TRY(hipGetLastError());
   }
 #undef SRW_TRY

@@ -318,7 +318,8 @@ srw_status_t srw_backward_workspace_size(const srw_desc_t* desc, size_t* bytes);
  * SRW_EINVAL; read and write enter through the forward normalisation), one
  * route or the paired routes (n_routes = 2, fused_gate_srw_paired),
  * one-pass statistics, d_model and d_route multiples of 64; anything else
- * returns SRW_EUNSUPPORTED.  With
+ * returns SRW_EUNSUPPORTED.  Every tensor and gradient pointer 16-byte
+ * aligned (as device allocations are), else SRW_EINVAL.  With
  * T = 0 the gradients of emb, read, write (and dscale) are zero.  The cotangents of bf16 values are rounded to bf16 where
  * the reference's bf16 casts, dots and products transpose (the gradients are
  * bf16 dot outputs widened to float32). */
