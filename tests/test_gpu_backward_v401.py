@@ -30,6 +30,7 @@ CASES = [
     (200, 384, 128, 1580, False, 1, 2, 12500),   # router h, ragged T and N
     (130, 128, 64, 1000, False, 1, 3, 300),      # four chunks
     (96, 384, 128, 1580, False, 2, 4, 12500),    # paired routes
+    (64, 1024, 1024, 700, True, 1, 5, 12500),    # configs[4] widths: the products on the 256 x 256 tiles
 ]
 
 
