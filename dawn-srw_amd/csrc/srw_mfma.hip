@@ -676,21 +676,21 @@ __device__ __attribute__((always_inline)) inline void store_unit_part(const Main
 // half of the main kernels' DIAG work: per token the max score, act-band
 // counts as thresholds on the exp argument (act > 0.9 <=> arg < -log2 9;
 // 0.1 < act < 0.9 <=> |arg| < log2 9; 0.05 / 0.95: log2 19; 0.2 / 0.8: 2),
-// capped intensities (s >= tau + thr + cut + max_intensity - 1e-3), the
-// intensity sum and the pass bits (v41:503-534); per unit of the tile the
-// sum of scores and the max of s - tau over the wave's 32 rows (v41:445-447,
-// 543-552), by a butterfly over the lanes of each half, into unit_part.
-// sw: the lane's bf16 scores, element v (unit unit_of_acc(v, half) of its
-// token) in word v / 2, the low half for even v.  The tile's pass-mask words
-// and unit partials go to an LDS block (DiagLds) from which another wave
-// stores them: the storing wave need not wait for the stores to complete.
+// capped intensities (s >= tau + thr + cut + max_intensity - 1e-3)
+// (v41:519-534; the intensity sum and the pass bits come from the gate
+// epilogue, as without diagnostics); per unit of the tile the sum of scores
+// and the max of s - tau over the wave's 32 rows (v41:445-447, 543-552), by a
+// butterfly over the lanes of each half, into unit_part.  sw: the lane's bf16
+// scores, element v (unit unit_of_acc(v, half) of its token) in word v / 2,
+// the low half for even v.  The tile's unit partials go to an LDS block
+// (DiagLds) from which another wave stores them: the storing wave need not
+// wait for the stores to complete.
 struct DiagLds {
-  uint32_t mask[32];  // per token of the wave block: the tile's pass-mask word
   float2 unit[32];    // per unit of the tile: (sum of scores, max of s - tau) over the block's rows
 };
 struct TileDiag {
-  float smax = -INFINITY, isum = 0.f;
-  uint32_t n_strong = 0, n_bound = 0, n_075 = 0, n_030 = 0, n_cap = 0, nact = 0;
+  float smax = -INFINITY;
+  uint32_t n_strong = 0, n_bound = 0, n_075 = 0, n_030 = 0, n_cap = 0;
   // FAST: every unit of the tile in [lo, hi) and every row of the wave
   // block valid (the selects drop out)
   template <bool FAST>
@@ -703,7 +703,6 @@ struct TileDiag {
     const float tau_cut = tau_thr + p.gp.cut;
     const float cap_s = tau_cut + (p.gp.maxi - 1e-3f);
     const bool full = FAST || (u0 >= lo && u0 + kUnitTile <= hi);
-    uint32_t bits = 0;
     float su[16], mx[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -721,18 +720,6 @@ struct TileDiag {
       n_075 += (uok && aa < 4.247927513443585f) ? 1u : 0u;
       n_030 += (uok && aa < 2.0f) ? 1u : 0u;
       n_cap += (uok && sv >= cap_s) ? 1u : 0u;
-      // intensity sum and pass bits (v41:503-511, 528) as in the gate epilogue
-      const float inten = p.gp.eps + __builtin_amdgcn_fmed3f(sv - tau_cut, 0.0f, p.gp.maxi);
-      isum += uok ? inten : 0.f;
-      bits = __builtin_amdgcn_alignbit(bits, uok ? __float_as_uint(arg) : 0u, 31);
-    }
-    {
-      const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
-      uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
-      m <<= 4 * half;
-      nact += __builtin_popcount(m);
-      m |= __shfl_xor(m, 32);
-      if (half == 0) dl->mask[lane] = m;
     }
     reduce_scatter16(su, lane, [](float x, float y) { return x + y; });
     reduce_scatter16(mx, lane, [](float x, float y) { return fmaxf(x, y); });
@@ -741,21 +728,12 @@ struct TileDiag {
       dl->unit[unit_of_acc(k, half)] = make_float2(su[0], mx[0]);
     }
   }
-  // a block's mask words and unit partials of tile utile from LDS to global
-  // memory (lane l: token tw + l's mask word; lanes 0-31: unit u0 + l)
+  // a block's unit partials of tile utile from LDS to global memory (lanes
+  // 32-63: unit u0 + lane - 32)
   __device__ __attribute__((always_inline)) static void emit(const MainParams& p, const DiagLds* dl, int utile,
                                                              int lane, int64_t lo, int64_t hi, int64_t tw) {
     const int64_t u0 = static_cast<int64_t>(utile) * kUnitTile;
-    const int64_t t = tw + (lane & 31);
-    if (lane < 32) {
-      if (p.mask32 && t < p.g.T) {
-        const uint32_t m = dl->mask[lane];
-        uint32_t* dst = p.mask32 + t * p.mask_words32 + utile;
-        const bool shared = (u0 < lo) || (u0 + kUnitTile > hi && hi < p.g.N);
-        if (shared) atomicOr(dst, m);
-        else *dst = m;
-      }
-    } else {
+    if (lane >= 32) {
       const int64_t u = u0 + (lane - 32);
       if (p.unit_part && u >= lo && u < hi && tw < p.g.T) p.unit_part[(tw >> 5) * p.g.N + u] = dl->unit[lane - 32];
     }
@@ -768,11 +746,7 @@ struct TileDiag {
     n_075 += __shfl_xor(n_075, 32);
     n_030 += __shfl_xor(n_030, 32);
     n_cap += __shfl_xor(n_cap, 32);
-    isum += __shfl_xor(isum, 32);
-    nact += __shfl_xor(nact, 32);
     if (half == 0 && row_ok) {
-      tp[1] = isum;
-      tp[2] = static_cast<float>(nact);
       tp[TP_SMAX] = smax;
       tp[TP_STRONG] = static_cast<float>(n_strong);
       tp[TP_BOUND] = static_cast<float>(n_bound);
@@ -1868,12 +1842,9 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
             sign = ok ? sign : 0u;
           }
           gsum += g;
-          if constexpr (DG) {
-            glogg = fmaf(g, __builtin_amdgcn_logf(g + 1e-8f), glogg);  // sum gate log2 (gate + 1e-8)
-          } else {
-            isum += inten;
-            bits = __builtin_amdgcn_alignbit(bits, sign, 31);   // bits << 1 | active
-          }
+          if constexpr (DG) glogg = fmaf(g, __builtin_amdgcn_logf(g + 1e-8f), glogg);  // sum gate log2 (gate + 1e-8)
+          isum += inten;
+          bits = __builtin_amdgcn_alignbit(bits, sign, 31);   // bits << 1 | active
           g2[e] = g;
         }
         const uint32_t gq = pack_bf16(g2[0], g2[1]);             // gate_bf (v41:516)
@@ -1885,8 +1856,8 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
     // the producers load every tile (R, W^T, scores): a consumer's global
     // accesses are its mask words and partials, stores it need not wait for
     for (int it = 0; it <= n; ++it) {
-      // diagnostics: the producers' mask words and unit partials of tile
-      // ta + it - 2 (written in the previous iteration)
+      // diagnostics: the producers' unit partials of tile ta + it - 2
+      // (written in the previous iteration)
       if constexpr (DG)
         if (it >= 2) TileDiag::emit(p, d_blk + (it & 1) * 4, ta + it - 2, lane, lo, hi, tw);
       if (it > 0) {
@@ -1900,8 +1871,8 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
           bits = gate_tile(std::integral_constant<bool, true>{}, u0, pk, srp, xrp);
         else
           bits = gate_tile(std::integral_constant<bool, false>{}, u0, pk, srp, xrp);
-        // pass bitmask of the tile (the producers emit it with diagnostics)
-        if constexpr (!DG) {
+        // pass bitmask of the tile
+        {
           const uint32_t b = __builtin_bitreverse32(bits) >> 16;  // element v at bit v
           uint32_t m = (b & 0xFu) | ((b & 0xF0u) << 4) | ((b & 0xF00u) << 8) | ((b & 0xF000u) << 12);
           m <<= 4 * half;
@@ -1945,12 +1916,9 @@ __device__ __attribute__((always_inline)) inline void main_ss_body(const MainPar
     if (half == 0 && t < p.g.T) {
       float* tp = p.tok_part + (static_cast<int64_t>(split) * p.g.T + t) * TPS;
       tp[0] = gsum;
-      if constexpr (DG) {
-        tp[TP_GLOGG] = glogg * 0.69314718055994531f;  // log2 -> ln
-      } else {
-        tp[1] = isum;
-        tp[2] = static_cast<float>(nact);
-      }
+      tp[1] = isum;
+      tp[2] = static_cast<float>(nact);
+      if constexpr (DG) tp[TP_GLOGG] = glogg * 0.69314718055994531f;  // log2 -> ln
     }
     float* op = p.out_part + static_cast<int64_t>(split) * p.g.T * D;
     if (tw + 32 <= p.g.T) {
