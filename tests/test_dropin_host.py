@@ -100,3 +100,24 @@ def test_v401_paired_16_tuple_assembly_matches_oracle(pkg):
         r_ = torch.as_tensor(r_, dtype=F64)
         assert g_.shape == r_.shape, name
         assert torch.allclose(g_, r_, rtol=1e-6, atol=1e-9), (name, g_, r_)
+
+
+def test_v401_factories_refuse_a_larger_mesh(pkg):
+    """One GPU: a mesh with a data or model axis above 1 is refused, as for
+    the v4.1 factories."""
+    import pytest
+
+    class Mesh:
+        shape = {"data": 2, "model": 1}
+
+    for make in (pkg.make_sharded_srw_v401, pkg.make_sharded_srw_paired_v401):
+        with pytest.raises(NotImplementedError):
+            make(Mesh())
+        make(None)
+
+
+def test_backward_refuses_an_unknown_gate(pkg):
+    import pytest
+    t = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        pkg.srw_backward(t, t, t, torch.zeros(4, 1), t, t, t, torch.zeros(4, 1, 64), gate="relu")
