@@ -224,3 +224,24 @@ def test_mesh_larger_than_one_device_refused(pkg):
     with pytest.raises(NotImplementedError):
         pkg.make_sharded_srw(Mesh())
     pkg.make_sharded_srw(None)
+
+
+def test_v401_backward_workspace_holds_the_normalised_rows(C):
+    """srw_backward_workspace_size with the v4.0.1 gate: the v4.1 layout plus
+    the forward-normalised read and write rows (bf16, N x D each) and the
+    per-row sums of dm z ([N64 / 64][T] fp32)."""
+    al = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    T, D, dr, N = 16, 64, 64, 100
+    base = C.backward_workspace_size(_desc(C, T=T, d_model=D, d_route=dr, n_units=N))
+    gl = C.backward_workspace_size(_desc(C, T=T, d_model=D, d_route=dr, n_units=N, gate=C.SRW_GATE_GELU_V401))
+    N64 = (N + 63) // 64 * 64
+    assert gl == base + 2 * al(N * D * 2) + al(N64 // 64 * T * 4)
+    # the v4.0.1 function has no dead penalty: a cotangent for it is refused
+    # before any launch (no tensors are touched)
+    d = _desc(C, T=T, d_model=D, d_route=dr, n_units=N, gate=C.SRW_GATE_GELU_V401)
+    cot = C.SrwCotangents(256, 256, 0.0, 0.5, None, None)
+    t = C.SrwTensors(256, 256, 256, 256, 256, 256)
+    g = C.SrwGrads(256, 256, 256, 256, 256, 256, None)
+    st = C.load_library().srw_backward(ctypes.byref(d), ctypes.byref(t), ctypes.byref(cot), ctypes.byref(g),
+                                       None, 0, None)
+    assert st == C.SRW_EINVAL
