@@ -2126,6 +2126,25 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
   const int64_t t = bx;
   const int tid = threadIdx.x;
   const int g = tid / CW, c = tid % CW;
+  const int64_t stride = p.T * p.D;
+  const int d = (by * CW + c) * VW;
+  const bool dok = d < p.D;
+  const vec_t* col = reinterpret_cast<const vec_t*>(p.out_part + t * p.D + (dok ? d : 0));
+  const int64_t vstride = stride / VW;
+  // many splits per chunk (decode): when one round of eight loads per thread
+  // covers a chunk, the first chunk's loads go out before the per-token
+  // partials are reduced and each next chunk's before the current one is
+  // (the additions keep their order)
+  const bool one_round = NG > 1 && p.spc <= 8 * NG;
+  auto load_chunk = [&](int s0, vec_t (&v)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int s = s0 + g + NG * j;
+      v[j] = s < s0 + p.spc ? col[s * vstride] : vec_t{};
+    }
+  };
+  vec_t cur[8];
+  if (one_round) load_chunk(0, cur);
   float gs = 0.f, is = 0.f, na = 0.f;
   for (int s = tid; s < p.S_tok; s += 256) {
     const float* tp = p.tok_part + (static_cast<int64_t>(s) * p.T + t) * p.tps;
@@ -2146,11 +2165,6 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
   const float I = red[1][0] + red[1][1] + red[1][2] + red[1][3];
   const float NA = red[2][0] + red[2][1] + red[2][2] + red[2][3];
   const float den = fmaxf(p.den_gate ? G : I, 1.0f);          // v41:584, v401:340
-  const int64_t stride = p.T * p.D;
-  const int d = (by * CW + c) * VW;
-  const bool dok = d < p.D;
-  const vec_t* col = reinterpret_cast<const vec_t*>(p.out_part + t * p.D + (dok ? d : 0));
-  const int64_t vstride = stride / VW;
   vec_t raw = {};
   auto round_v = [](vec_t x) {
     vec_t r;
@@ -2172,14 +2186,23 @@ __device__ __attribute__((always_inline)) inline void finalize_body(const FinalP
   }
   for (int s0 = 0; s0 < p.S && !(NG == 1 && p.spc == 1); s0 += p.spc) {  // one reference chunk
     vec_t acc[8] = {};
-    // rounds of eight splits per thread, all eight loads in flight at once
-    // (predicated past the chunk's end)
-    for (int s = s0 + g; s < s0 + p.spc; s += 8 * NG) {
-      vec_t v[8];
+    if (one_round) {
+      vec_t nxt[8] = {};
+      if (s0 + p.spc < p.S) load_chunk(s0 + p.spc, nxt);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = s + NG * j < s0 + p.spc ? col[(s + NG * j) * vstride] : vec_t{};
+      for (int j = 0; j < 8; ++j) acc[j] += cur[j];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] += v[j];
+      for (int j = 0; j < 8; ++j) cur[j] = nxt[j];
+    } else {
+      // rounds of eight splits per thread, all eight loads in flight at once
+      // (predicated past the chunk's end)
+      for (int s = s0 + g; s < s0 + p.spc; s += 8 * NG) {
+        vec_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = s + NG * j < s0 + p.spc ? col[(s + NG * j) * vstride] : vec_t{};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += v[j];
+      }
     }
     const vec_t sum = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
     if constexpr (NG == 1) {
