@@ -713,6 +713,9 @@ def main() -> int:
     if args.dtype == "f32" and (args.workload in ("decode", "qkv", "model") or args.backward or args.tiled):
         print("bench.py: --dtype f32 times the single-pool forward", file=sys.stderr)
         return 2
+    if args.gate != "v41" and args.workload in ("decode", "qkv", "model"):
+        print("bench.py: --gate gelu_v401 times the single-pool calls", file=sys.stderr)
+        return 2
     if args.cold and (args.graph or args.workload in ("decode", "qkv", "model")):
         print("bench.py: --cold times single eager calls of one pool", file=sys.stderr)
         return 2
