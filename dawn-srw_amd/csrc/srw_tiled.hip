@@ -33,6 +33,7 @@
 // XOR-swizzled by row so the fragment reads are free of bank conflicts.
 
 #include <type_traits>
+#include <utility>
 
 #include "srw_internal.hpp"
 #include "srw_mfma_util.hpp"
@@ -2071,6 +2072,28 @@ BGemm bgemm(int64_t M, int64_t Nc, int64_t K) {
   return g;
 }
 
+// Products that run as one launch (the backward's five gradient products):
+// each product's K splits re-picked for the batch -- the fewest whose
+// workgroups carry no more k blocks than the batch's mean per CU (the
+// products' k blocks over 256 CUs, one workgroup per CU at a time).  With
+// the longest workgroups dispatched first (tiled_backward orders the batch
+// so), no CU's last workgroup then runs far past that mean, and fewer
+// splits write and read back fewer fp32 partials.  (Know pool, T = 4096: d x
+// and d h in two splits of 197 k blocks beside a mean of 247, where the
+// per-product model took eight.)
+void batch_splits(BGemm* const* gs, int n) {
+  int64_t total = 0;
+  for (int i = 0; i < n; ++i)
+    total += static_cast<int64_t>(gs[i]->RT) * gs[i]->DT * ((gs[i]->K + kGK - 1) / kGK);
+  const int64_t mean = (total + 255) / 256;
+  for (int i = 0; i < n; ++i) {
+    const int64_t blocks = (gs[i]->K + kGK - 1) / kGK;
+    int64_t c = 1;
+    while (c < 64 && c < blocks && (blocks + c - 1) / c > mean) ++c;
+    gs[i]->spc = static_cast<int>(c);
+  }
+}
+
 // bf16 src [rows, cols] -> dst [cols, rows_pad] (zero rows past `rows`), 64 x
 // 64 tiles, 16-byte loads along src rows and 16-byte stores along dst rows
 // (cols a multiple of 8)
@@ -2212,6 +2235,13 @@ BLayout blayout(const srw_desc_t& d) {
   l.g_dx = bgemm(T, D, N);
   l.g_de = bgemm(N, dr, l.Tv);
   l.g_dr = bgemm(N, D, T);
+  {
+    // one launch when the five share a tile width (bwd_gemms)
+    BGemm* const gs[5] = {&l.g_dw, &l.g_dr, &l.g_de, &l.g_dx, &l.g_dh};
+    bool one = 5 <= kWriteBatch;
+    for (int i = 1; i < 5; ++i) one = one && gs[i]->nbf == gs[0]->nbf;
+    if (one) batch_splits(gs, 5);
+  }
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t at = off;
@@ -2479,11 +2509,22 @@ hipError_t tiled_backward(const BackwardArgs& a) {
   // the five gradient contractions: bf16 dots, fp32 accumulation
   SRW_TRY(transpose(DRAW, DRAWT, Tv, l.Tv64, D, st));
   {
-    const BGemm gs[5] = {l.g_dw, l.g_dr, l.g_de, l.g_dx, l.g_dh};
+    BGemm gs[5] = {l.g_dw, l.g_dr, l.g_de, l.g_dx, l.g_dh};
     const uint16_t* As[5] = {PT, DXRT, DST, DXR, DS};
     const uint16_t* Bs[5] = {DRAWT, XT, HT, RT, ET};
-    const int64_t lds_[5] = {l.Tv64, l.T64, l.Tv64, N64, N64};
+    int64_t lds_[5] = {l.Tv64, l.T64, l.Tv64, N64, N64};
     float* outs[5] = {a.g.dwrite, a.g.dread, a.g.demb, a.g.dx, a.g.dh};
+    // the products with the longest workgroups (k blocks per split) first
+    // (stable insertion sort of the five)
+    auto wg_blocks = [](const BGemm& g) { return ((g.K + kGK - 1) / kGK + g.spc - 1) / g.spc; };
+    for (int i = 1; i < 5; ++i)
+      for (int j = i; j > 0 && wg_blocks(gs[j]) > wg_blocks(gs[j - 1]); --j) {
+        std::swap(gs[j], gs[j - 1]);
+        std::swap(As[j], As[j - 1]);
+        std::swap(Bs[j], Bs[j - 1]);
+        std::swap(lds_[j], lds_[j - 1]);
+        std::swap(outs[j], outs[j - 1]);
+      }
     float* parts[5];
     float* pp = part;
     for (int i = 0; i < 5; ++i) {
